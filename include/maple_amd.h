@@ -1,0 +1,173 @@
+/*
+ * maple_amd -- C ABI of the MI355X (gfx950) packed-ternary MoE decode kernels.
+ *
+ * Every entry point takes raw device pointers, int64 sizes/leading dimensions,
+ * dtype enums and a hipStream_t passed as void*.  Nothing here allocates,
+ * synchronises the device or the host, or keeps state between calls, so all
+ * calls are capturable in a HIP graph.  Outputs are written in the dtype the
+ * reference uses for them; inputs are never modified.
+ *
+ * Return value: MA_OK (0) or an MA_E* status; ma_last_error() then holds a
+ * message for the calling thread.  The Python host maps MA_EVALUE to
+ * ValueError, MA_ETYPE to TypeError and MA_ERUNTIME to RuntimeError, the
+ * exception types the reference raises for the same conditions.
+ *
+ * Layouts (reference src/maple_run/pack.py:17-20):
+ *   ternary   uint32 [N, K/16] (or [K/16, N] with packed_kn), 16 two-bit
+ *             codes per word, LSB first, value = code - 1.
+ *   rtn4      uint32 [N, K/8] (or [K/8, N] with packed_kn), 8 four-bit codes
+ *             per word, LSB first, value = q * scale[g] + bias[g].
+ * Rows of x / y are contiguous along K / N with leading dimension ld*.
+ */
+#ifndef MAPLE_AMD_H
+#define MAPLE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of float tensors. */
+enum { MA_F32 = 0, MA_BF16 = 1, MA_F16 = 2 };
+/* Status codes. */
+enum { MA_OK = 0, MA_EVALUE = 1, MA_ETYPE = 2, MA_ERUNTIME = 3 };
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int ma_version(void);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* ma_last_error(void);
+
+/*
+ * y[b, n] = alpha[n] * sum_k (code[n, k] - 1) * x_hat[b, k]
+ * with x_hat = x, or with rms_weight != NULL, x_hat = x * w_rms and the row
+ * scaled by rsqrt(mean(x^2) + rms_eps): the fused input RMSNorm.
+ * y has x's dtype.  Replaces ternary_gemv, src/maple_run/kernels/ternary_gemv.py:261-388.
+ */
+int ma_ternary_gemv(const void* x, int x_dtype, int64_t batch, int64_t ldx,
+                    const uint32_t* packed, int64_t n_out, int64_t nwords, int packed_kn,
+                    const void* row_alpha, int alpha_dtype,
+                    const void* rms_weight, int rms_dtype, float rms_eps,
+                    void* y, int64_t ldy, void* stream);
+
+/*
+ * Router: logits = x @ W^T (+ bias), softmax over the experts, the top_k
+ * largest probabilities in descending order (ties: lowest expert index) and
+ * their renormalised weights p / (sum p_top + 1e-20).
+ * ids int32 [tokens, top_k], weights float32 [tokens, top_k].
+ * workspace: at least ma_router_workspace_bytes(tokens, n_experts) bytes.
+ * Replaces router_topk, src/maple_run/kernels/router.py:141-217 (the bias is
+ * an optional addition; NULL is the reference behaviour).
+ */
+size_t ma_router_workspace_bytes(int64_t tokens, int64_t n_experts);
+int ma_router_topk(const void* x, int x_dtype, int64_t tokens, int64_t ldx,
+                   const void* gate_weight, int w_dtype, int64_t n_experts, int64_t k_in,
+                   const float* bias, int top_k,
+                   int32_t* ids, float* weights,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Dispatch of (token, slot) pairs p = token * top_k + slot to experts:
+ * counts[e], offsets[e] (exclusive scan, n_experts + 1 entries), pair_ids
+ * (pairs stably sorted by expert id, so every expert's list is ascending in
+ * token) and inverse[p] (position of pair p in pair_ids).  ids may be int32
+ * or int64 (ids_is_int64).  No reference counterpart: the reference grids over
+ * pairs directly (src/maple_run/kernels/ternary_expert.py:210,443).
+ */
+int ma_moe_dispatch(const void* ids, int ids_is_int64, int64_t n_pairs, int n_experts,
+                    int32_t* counts, int32_t* offsets, int32_t* pair_ids, int32_t* inverse,
+                    void* stream);
+
+/*
+ * y[s, n] = alpha[e, n] * sum_k (code[e, n, k] - 1) * x[s / x_div, k], e = ids[s].
+ * x_div = 1 for one x row per slot, top_k for one x row per token.
+ * packed: [E, N, K/16] (or [E, K/16, N] with packed_kn); alpha [E, N].
+ * Replaces ternary_expert_gemv, src/maple_run/kernels/ternary_expert.py:125-234.
+ */
+int ma_ternary_expert_gemv(const void* x, int x_dtype, int64_t ldx, int64_t x_div,
+                           const uint32_t* packed, int64_t n_experts, int64_t n_out,
+                           int64_t nwords, int packed_kn,
+                           const void* row_alpha, int alpha_dtype,
+                           const void* ids, int ids_is_int64, int64_t n_slots,
+                           void* y, int64_t ldy, void* stream);
+
+/*
+ * h[t, j, i] = clamp(up, -7, 7) * g * sigmoid(g), g = min(gate, 7), with
+ * up = alpha[e, i] * (T_e[i] . x[t]) and gate the same on row N + i
+ * (rows are [up; gate]), e = ids[t, j].  h has x's dtype, [tokens*top_k, N].
+ * Replaces ternary_expert_swiglu, src/maple_run/kernels/ternary_expert.py:403-468.
+ */
+int ma_ternary_expert_swiglu(const void* x, int x_dtype, int64_t ldx, int64_t tokens,
+                             int64_t top_k, const uint32_t* packed, int64_t n_experts,
+                             int64_t n_rows, int64_t nwords, int packed_kn,
+                             const void* row_alpha, int alpha_dtype,
+                             const void* ids, int ids_is_int64,
+                             void* h, int64_t ldh, void* stream);
+
+/*
+ * y[t, n] = sum_j w[t, j] * alpha[e, n] * (T_e[n] . x[t, j]) (+ residual[t, n])
+ * in float32 with a single rounding on store; x is [tokens, top_k, K]
+ * (row stride ldx per slot), y has x's dtype.
+ * Replaces ternary_expert_down_sum, src/maple_run/kernels/ternary_expert.py:471-556.
+ */
+int ma_ternary_expert_down_sum(const void* x, int x_dtype, int64_t ldx,
+                               const uint32_t* packed, int64_t n_experts, int64_t n_out,
+                               int64_t nwords, int packed_kn,
+                               const void* row_alpha, int alpha_dtype,
+                               const void* ids, int ids_is_int64, const float* topk_weight,
+                               const void* residual, int residual_dtype,
+                               int64_t tokens, int64_t top_k,
+                               void* y, int64_t ldy, void* stream);
+
+/*
+ * y[t, n] = sum_j w[t, j] * expert_out[t, j, n] (+ residual[t, n]), float32
+ * accumulate, stored in expert_out's dtype.
+ * Replaces moe_reduce_add, src/maple_run/kernels/fused_norm.py:164-202.
+ */
+int ma_moe_reduce_add(const void* expert_out, int eo_dtype, int64_t tokens, int64_t top_k,
+                      int64_t n, const float* topk_weight,
+                      const void* residual, int residual_dtype,
+                      void* y, void* stream);
+
+/*
+ * RMSNorm over rows of n: y = x * rsqrt(mean(x^2) + eps) * w, y in x's dtype.
+ * Replaces rms_norm, src/maple_run/kernels/fused_norm.py:105-125.
+ */
+int ma_rms_norm(const void* x, int x_dtype, int64_t rows, int64_t n,
+                const void* weight, int w_dtype, float eps, void* y, void* stream);
+
+/*
+ * residual = x + y; normed = rms_norm(residual) (computed from the float32
+ * sum); both in x's dtype.  Replaces add_rms_norm, fused_norm.py:128-161.
+ */
+int ma_add_rms_norm(const void* x, const void* y, int dtype, int64_t rows, int64_t n,
+                    const void* weight, int w_dtype, float eps,
+                    void* residual, void* normed, void* stream);
+
+/*
+ * y[b, n] = sum_g sum_{k in g} (q[n, k] * scale[n, g] + bias[n, g]) * x[b, k],
+ * float32 accumulate, y in x's dtype.  scales/biases are [N, K/group]
+ * (or [K/group, N] with packed_kn).
+ * Replaces rtn4_gemv, src/maple_run/kernels/rtn4.py:285-415.
+ */
+int ma_rtn4_gemv(const void* x, int x_dtype, int64_t batch, int64_t ldx,
+                 const uint32_t* packed, int64_t n_out, int64_t nwords, int packed_kn,
+                 const void* scales, int scales_dtype, const void* biases, int biases_dtype,
+                 int64_t group_size, void* y, int64_t ldy, void* stream);
+
+/*
+ * out[i, k] = q[ids[i], k] * scale[ids[i], g] + bias[ids[i], g] in float32.
+ * Replaces rtn4_embedding, src/maple_run/kernels/rtn4.py:27-47.
+ */
+int ma_rtn4_embedding(const void* ids, int ids_is_int64, int64_t n_ids,
+                      const uint32_t* packed, int64_t vocab, int64_t nwords,
+                      const void* scales, int scales_dtype, const void* biases, int biases_dtype,
+                      int64_t group_size, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAPLE_AMD_H */

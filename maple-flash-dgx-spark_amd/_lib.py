@@ -1,0 +1,98 @@
+"""ctypes binding of ``libmaple_amd.so`` (the C ABI in ``include/maple_amd.h``).
+
+The library is loaded after ``torch`` so that it binds to the HIP runtime torch
+already mapped (both carry the SONAME ``libamdhip64.so.7``).  There is no
+fallback: if the library is missing, every call raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libmaple_amd.so")
+
+F32, BF16, F16 = 0, 1, 2
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+_Z = ctypes.c_size_t
+
+# name -> argtypes (restype is int unless listed in _RESTYPES)
+_SIGNATURES = {
+    "ma_version": [],
+    "ma_last_error": [],
+    "ma_ternary_gemv": [_P, _I, _L, _L, _P, _L, _L, _I, _P, _I, _P, _I, _F, _P, _L, _P],
+    "ma_router_workspace_bytes": [_L, _L],
+    "ma_router_topk": [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _P, _P, _P, _Z, _P],
+    "ma_moe_dispatch": [_P, _I, _L, _I, _P, _P, _P, _P, _P],
+    "ma_ternary_expert_gemv": [_P, _I, _L, _L, _P, _L, _L, _L, _I, _P, _I, _P, _I, _L, _P, _L, _P],
+    "ma_ternary_expert_swiglu": [_P, _I, _L, _L, _L, _P, _L, _L, _L, _I, _P, _I, _P, _I, _P, _L, _P],
+    "ma_ternary_expert_down_sum": [_P, _I, _L, _P, _L, _L, _L, _I, _P, _I, _P, _I, _P, _P, _I,
+                                   _L, _L, _P, _L, _P],
+    "ma_moe_reduce_add": [_P, _I, _L, _L, _L, _P, _P, _I, _P, _P],
+    "ma_rms_norm": [_P, _I, _L, _L, _P, _I, _F, _P, _P],
+    "ma_add_rms_norm": [_P, _P, _I, _L, _L, _P, _I, _F, _P, _P, _P],
+    "ma_rtn4_gemv": [_P, _I, _L, _L, _P, _L, _L, _I, _P, _I, _P, _I, _L, _P, _L, _P],
+    "ma_rtn4_embedding": [_P, _I, _L, _P, _L, _L, _P, _I, _P, _I, _L, _P, _P],
+}
+_RESTYPES = {"ma_last_error": ctypes.c_char_p, "ma_router_workspace_bytes": _Z}
+
+_lib = None
+
+
+def declared_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def load() -> ctypes.CDLL:
+    """Load and declare the library once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"maple_amd HIP library not found at {LIB_PATH}; build it with "
+                "`python maple-flash-dgx-spark_amd/build.py` (there is no CPU fallback)."
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(lib, name, None)
+            if fn is None:
+                continue
+            fn.argtypes = argtypes
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        _lib = lib
+    return _lib
+
+
+def dtype_code(t: torch.Tensor, what: str) -> int:
+    code = _DTYPES.get(t.dtype)
+    if code is None:
+        raise TypeError(f"{what} must be float32, bfloat16 or float16; got {t.dtype}.")
+    return code
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+_ERRORS = {1: ValueError, 2: TypeError, 3: RuntimeError}
+
+
+def call(name: str, *args) -> int:
+    """Call ``name``; map a non-zero status to the reference's exception type."""
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        msg = lib.ma_last_error().decode(errors="replace")
+        raise _ERRORS.get(status, RuntimeError)(msg or f"{name} failed with status {status}")
+    return status

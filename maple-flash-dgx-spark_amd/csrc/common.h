@@ -1,0 +1,179 @@
+// Shared device/host helpers for the maple_amd HIP library (gfx950 only).
+//
+// Packed formats (reference src/maple_run/pack.py:17-20):
+//   ternary: 16 two-bit codes per uint32, LSB first, value = code - 1
+//   rtn4:    8 four-bit codes per uint32, LSB first, value = q * scale + bias
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/maple_amd.h"
+
+namespace ma {
+
+// ---------------------------------------------------------------------------
+// Error reporting: the last failure message of the calling host thread.
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+int fail(int status, const char* fmt, ...);
+int check_launch(const char* what);
+
+// ---------------------------------------------------------------------------
+// Scalar conversions.  bf16 is carried as raw uint16 bits.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even float -> bf16 (NaN stays a quiet NaN).  Branch-free.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t r = u + 0x7fffu + ((u >> 16) & 1u);
+  const uint32_t q = ((u & 0x7fffffffu) > 0x7f800000u) ? (u | 0x00400000u) : r;
+  return static_cast<uint16_t>(q >> 16);
+}
+
+// bf16 bits of a float known to be exactly representable in bf16.
+__device__ __forceinline__ uint32_t bf16_bits_exact(float f) { return __float_as_uint(f) >> 16; }
+
+// Typed scalar load with the dtype fixed at compile time (no branch, so the
+// load can be issued early and waited on only where it is used).
+template <int DT>
+__device__ __forceinline__ float ld_t(const void* p, int64_t i) {
+  if constexpr (DT == MA_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else if constexpr (DT == MA_F16) return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+  else return static_cast<const float*>(p)[i];
+}
+
+__device__ __forceinline__ float ld_f(const void* p, int dt, int64_t i) {
+  switch (dt) {
+    case MA_BF16: return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    case MA_F16: return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+    default: return static_cast<const float*>(p)[i];
+  }
+}
+
+__device__ __forceinline__ void st_f(void* p, int dt, int64_t i, float v) {
+  switch (dt) {
+    case MA_BF16: static_cast<uint16_t*>(p)[i] = f32_to_bf16(v); break;
+    case MA_F16: static_cast<_Float16*>(p)[i] = static_cast<_Float16>(v); break;
+    default: static_cast<float*>(p)[i] = v; break;
+  }
+}
+
+__device__ __forceinline__ int64_t ld_id(const void* p, int is64, int64_t i) {
+  return is64 ? static_cast<const int64_t*>(p)[i] : static_cast<const int32_t*>(p)[i];
+}
+
+// ---------------------------------------------------------------------------
+// Ternary expansion for v_dot2_f32_bf16.
+//
+// A 2-bit code c placed in mantissa bits [p, p+1] of bf16 1.0 (0x3F80) reads
+// as exactly 1 + c * 2^(p-7).  With p = 3 that is 1 + c/16, with p = 5 it is
+// 1 + c/4.  Pair j of a word holds codes j (low half) and j + 8 (high half);
+// one shift lines both up, one and/or builds the bf16x2 operand:
+//
+//   pair 0,1: w << 3     pair 2,3: w >> 1     pair 4,5: w >> 5     pair 6,7: w >> 9
+//   even pair: bits 3-4 (f = 16)               odd pair: bits 5-6 (f = 4)
+//
+// Dotting against x' = f * x (exact: a power-of-two scale) gives
+// sum (f + c) x, so sum (c - 1) x = acc - sum (f + 1) x, where the second sum
+// depends only on x and is formed once per lane.  Code 3 therefore reads as
+// +2, the reference semantics (kernels/ternary_gemv.py:126-128).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kOneBf16x2 = 0x3F803F80u;
+constexpr uint32_t kMaskP3 = 0x00180018u;
+constexpr uint32_t kMaskP5 = 0x00600060u;
+
+__device__ __forceinline__ float pair_scale(int j) { return (j & 1) ? 4.0f : 16.0f; }
+
+// (a & m) | o as one v_and_or_b32.  The operands are pinned to VGPRs: with
+// both constants as literals the compiler would split it into two VOP2 ops.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
+  return r;
+}
+
+// Loop-invariant constants of expand_word, held in registers by the caller.
+struct ExpandConsts {
+  uint32_t m3, m5, one;
+  __device__ __forceinline__ ExpandConsts() : m3(kMaskP3), m5(kMaskP5), one(kOneBf16x2) {}
+};
+
+// The 8 bf16x2 operands of one packed word.
+__device__ __forceinline__ void expand_word(uint32_t w, uint32_t e[8], const ExpandConsts& k) {
+  const uint32_t s0 = w << 3, s1 = w >> 1, s2 = w >> 5, s3 = w >> 9;
+  e[0] = and_or(s0, k.m3, k.one);
+  e[1] = and_or(s0, k.m5, k.one);
+  e[2] = and_or(s1, k.m3, k.one);
+  e[3] = and_or(s1, k.m5, k.one);
+  e[4] = and_or(s2, k.m3, k.one);
+  e[5] = and_or(s2, k.m5, k.one);
+  e[6] = and_or(s3, k.m3, k.one);
+  e[7] = and_or(s3, k.m5, k.one);
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// Pack two floats that are exactly representable in bf16 into a bf16x2 word.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return bf16_bits_exact(lo) | (bf16_bits_exact(hi) << 16);
+}
+
+// x' pairs for one word from 16 consecutive activations xs[0..15] (already
+// float): pair j = (f_j * xs[j], f_j * xs[j+8]).  Returns sum (f_j + 1) xs.
+// Only exact when xs are bf16 values (the fast path's input dtype).
+__device__ __forceinline__ float prep_word_pairs(const float xs[16], uint32_t xp[8]) {
+  float c = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float f = pair_scale(j);
+    xp[j] = pack_bf16x2(f * xs[j], f * xs[j + 8]);
+    c += (f + 1.0f) * (xs[j] + xs[j + 8]);
+  }
+  return c;
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level helpers (wave64).
+// ---------------------------------------------------------------------------
+// DPP / swizzle lane exchanges.  quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E;
+// row_ror:n = 0x120 + n rotates within each 16-lane row.  ds_swizzle in
+// bitmask mode reads lane ((j & 0x1F) ^ xor) within each 32-lane half.
+#define MA_DPP(v, ctrl) \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, false))
+#define MA_SWZ_XOR(v, x) \
+  __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, (v)), 0x1F | ((x) << 10)))
+
+// Sum over aligned groups of WIDTH lanes (WIDTH in {1,2,4,8,16,32,64}); every
+// lane of a group receives the group's total.
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (WIDTH >= 2) v += MA_DPP(v, 0xB1);
+  if constexpr (WIDTH >= 4) v += MA_DPP(v, 0x4E);
+  if constexpr (WIDTH == 8) v += MA_SWZ_XOR(v, 4);
+  if constexpr (WIDTH >= 16) {
+    v += MA_DPP(v, 0x124);
+    v += MA_DPP(v, 0x128);
+  }
+  if constexpr (WIDTH >= 32) v += MA_SWZ_XOR(v, 16);
+  if constexpr (WIDTH >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace ma

@@ -1,0 +1,375 @@
+// Indexed stacked-expert ternary kernels (gfx950).
+//
+// Semantics follow reference src/maple_run/kernels/ternary_expert.py:
+//   expert_gemv     :58-122   y[s] = alpha_e * (T_e . x_s), e = ids[s]
+//   expert_swiglu   :240-319  rows [up; gate]; clamp(up,+-7) * g * sigmoid(g), g = min(gate, 7)
+//   expert_down_sum :322-400  y[t] = sum_j w[t,j] * alpha_e (T_e . x[t,j]) (+ residual)
+// Fast kernels: bf16 activations, [E, N, K/16] codes, nwords = KW * LPR; each
+// one-wave workgroup handles U row-iterations of one slot (or token), with
+// every weight load of the wave issued before the activations are prepared.
+// Generic kernels: any dtype / layout, one wave per output row.
+#include "ternary_engine.h"
+
+namespace ma {
+
+constexpr float kMlpClamp = 7.0f;  // ternary_expert.py:237
+
+// Expert id of a slot, clamped into [0, n_exp): an id outside the stack would
+// otherwise address memory outside the weights (no host-side check is possible
+// without a device sync).
+__device__ __forceinline__ int64_t expert_id(const void* ids, int ids64, int64_t s, int64_t n_exp) {
+  const int64_t e = ld_id(ids, ids64, s);
+  return e < 0 ? 0 : (e >= n_exp ? n_exp - 1 : e);
+}
+
+__device__ __forceinline__ float swiglu(float up, float gate) {
+  up = fminf(fmaxf(up, -kMlpClamp), kMlpClamp);
+  gate = fminf(gate, kMlpClamp);
+  return up * (gate / (1.0f + expf(-gate)));
+}
+
+// ---------------------------------------------------------------------------
+// Fast SwiGLU: lanes of sub-group [0, PPI) compute up rows, [PPI, 2*PPI) the
+// matching gate rows; the gate value is fetched across the wave.
+// ---------------------------------------------------------------------------
+template <int KW, int LPR, int U, int ADT>
+__global__ __launch_bounds__(64) void k_swiglu_fast(
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t topk,
+    const uint32_t* __restrict__ w, int64_t n_half,
+    const void* __restrict__ alpha, const void* __restrict__ ids, int ids64, int64_t n_exp,
+    uint16_t* __restrict__ h, int64_t ldh) {
+  constexpr int NW = KW * LPR;
+  constexpr int RPI = 64 / LPR;
+  constexpr int PPI = RPI / 2;
+  const int lane = threadIdx.x & 63;
+  const int kl = lane % LPR, sub = lane / LPR;
+  const int half = sub / PPI, pi = sub % PPI;
+  const int64_t slot = blockIdx.y;
+  const int64_t e = expert_id(ids, ids64, slot, n_exp);
+  const uint32_t* we = w + e * (2 * n_half) * NW;
+  const int64_t a_off = e * (2 * n_half);
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * (PPI * U);
+
+  uint32_t wv[U][KW];
+  float a[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int64_t i = i0 + u * PPI + pi;
+    i = i < n_half ? i : n_half - 1;
+    const int64_t row = i + half * n_half;
+    load_words_v<KW>(we + row * NW + kl * KW, wv[u]);
+    a[u] = ld_t<ADT>(alpha, a_off + row);
+  }
+  XSlice<KW> xs;
+  xs.load(x + (slot / topk) * ldx, kl);
+  xs.finish();
+  const ExpandConsts kc;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const float v = group_sum<LPR>(slice_dot<KW>(wv[u], xs, kc) * a[u]);
+    const float g = __shfl(v, lane + PPI * LPR, 64);
+    const int64_t i = i0 + u * PPI + pi;
+    if (half == 0 && kl == 0 && i < n_half) h[slot * ldh + i] = f32_to_bf16(swiglu(v, g));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fast expert GEMV: rows i0 + u*RPI + sub of expert ids[slot].
+// ---------------------------------------------------------------------------
+template <int KW, int LPR, int U, int ADT>
+__global__ __launch_bounds__(64) void k_egemv_fast(
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t x_div,
+    const uint32_t* __restrict__ w, int64_t n_out,
+    const void* __restrict__ alpha, const void* __restrict__ ids, int ids64, int64_t n_exp,
+    uint16_t* __restrict__ y, int64_t ldy) {
+  constexpr int NW = KW * LPR;
+  constexpr int RPI = 64 / LPR;
+  const int lane = threadIdx.x & 63;
+  const int kl = lane % LPR, sub = lane / LPR;
+  const int64_t slot = blockIdx.y;
+  const int64_t e = expert_id(ids, ids64, slot, n_exp);
+  const uint32_t* we = w + e * n_out * NW;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * (RPI * U);
+  uint32_t wv[U][KW];
+  float a[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int64_t r = r0 + u * RPI + sub;
+    r = r < n_out ? r : n_out - 1;
+    load_words_v<KW>(we + r * NW + kl * KW, wv[u]);
+    a[u] = ld_t<ADT>(alpha, e * n_out + r);
+  }
+  XSlice<KW> xs;
+  xs.load(x + (slot / x_div) * ldx, kl);
+  xs.finish();
+  const ExpandConsts kc;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const float v = group_sum<LPR>(slice_dot<KW>(wv[u], xs, kc) * a[u]);
+    const int64_t r = r0 + u * RPI + sub;
+    if (kl == 0 && r < n_out) y[slot * ldy + r] = f32_to_bf16(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fast down projection + top-k weighted combine (+ residual), float32 until
+// the single store.  One token per grid row; the slots are walked in order.
+// ---------------------------------------------------------------------------
+template <int KW, int LPR, int U, int ADT>
+__global__ __launch_bounds__(64) void k_down_sum_fast(
+    const uint16_t* __restrict__ x, int64_t ldx,
+    const uint32_t* __restrict__ w, int64_t n_out,
+    const void* __restrict__ alpha, const void* __restrict__ ids, int ids64, int64_t n_exp,
+    const float* __restrict__ wts, const void* __restrict__ res, int res_dt,
+    int64_t topk, uint16_t* __restrict__ y, int64_t ldy) {
+  constexpr int NW = KW * LPR;
+  constexpr int RPI = 64 / LPR;
+  const int lane = threadIdx.x & 63;
+  const int kl = lane % LPR, sub = lane / LPR;
+  const int64_t t = blockIdx.y;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * (RPI * U);
+  int64_t rr[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t r = r0 + u * RPI + sub;
+    rr[u] = r < n_out ? r : n_out - 1;
+  }
+  float out[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) out[u] = 0.f;
+  const ExpandConsts kc;
+  for (int64_t j = 0; j < topk; ++j) {
+    const int64_t s = t * topk + j;
+    const int64_t e = expert_id(ids, ids64, s, n_exp);
+    const float wj = wts[s];
+    const uint32_t* we = w + e * n_out * NW;
+    uint32_t wv[U][KW];
+    float a[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      load_words_v<KW>(we + rr[u] * NW + kl * KW, wv[u]);
+      a[u] = ld_t<ADT>(alpha, e * n_out + rr[u]);
+    }
+    XSlice<KW> xs;
+    xs.load(x + s * ldx, kl);
+    xs.finish();
+#pragma unroll
+    for (int u = 0; u < U; ++u) out[u] += wj * group_sum<LPR>(slice_dot<KW>(wv[u], xs, kc) * a[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t r = r0 + u * RPI + sub;
+    if (kl == 0 && r < n_out) {
+      float v = out[u];
+      if (res) v += ld_f(res, res_dt, t * n_out + r);
+      y[t * ldy + r] = f32_to_bf16(v);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic kernels: one wave per (slot, row); any float dtype, either layout.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float row_dot_generic(const void* x, int x_dt, int64_t xoff,
+                                                 const uint32_t* w, int64_t e, int64_t row,
+                                                 int64_t n_rows, int64_t nwords, int kn,
+                                                 int lane) {
+  float acc = 0.f;
+  const uint32_t* we = w + e * n_rows * nwords;
+  for (int64_t wi = lane; wi < nwords; wi += 64) {
+    const uint32_t word = kn ? we[wi * n_rows + row] : we[row * nwords + wi];
+#pragma unroll 4
+    for (int i = 0; i < 16; ++i) {
+      const float v = static_cast<float>((word >> (2 * i)) & 3u) - 1.0f;
+      acc += v * ld_f(x, x_dt, xoff + wi * 16 + i);
+    }
+  }
+  return group_sum<64>(acc);
+}
+
+// mode 0: gemv, 1: swiglu (row = up row, gate row = row + n_half)
+__global__ __launch_bounds__(256) void k_expert_generic(
+    const void* __restrict__ x, int x_dt, int64_t ldx, int64_t x_div,
+    const uint32_t* __restrict__ w, int64_t n_rows, int64_t n_out, int64_t nwords, int kn,
+    const void* __restrict__ alpha, int a_dt, const void* __restrict__ ids, int ids64,
+    int64_t n_exp, int mode, void* __restrict__ y, int y_dt, int64_t ldy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= n_out) return;
+  const int64_t slot = blockIdx.y;
+  const int64_t e = expert_id(ids, ids64, slot, n_exp);
+  const int64_t xoff = (slot / x_div) * ldx;
+  const float v = row_dot_generic(x, x_dt, xoff, w, e, row, n_rows, nwords, kn, lane) *
+                  ld_f(alpha, a_dt, e * n_rows + row);
+  float out = v;
+  if (mode == 1) {
+    const int64_t grow = row + n_out;
+    const float g = row_dot_generic(x, x_dt, xoff, w, e, grow, n_rows, nwords, kn, lane) *
+                    ld_f(alpha, a_dt, e * n_rows + grow);
+    out = swiglu(v, g);
+  }
+  if (lane == 0) st_f(y, y_dt, slot * ldy + row, out);
+}
+
+__global__ __launch_bounds__(256) void k_down_sum_generic(
+    const void* __restrict__ x, int x_dt, int64_t ldx,
+    const uint32_t* __restrict__ w, int64_t n_out, int64_t nwords, int kn,
+    const void* __restrict__ alpha, int a_dt, const void* __restrict__ ids, int ids64,
+    int64_t n_exp, const float* __restrict__ wts, const void* __restrict__ res, int res_dt, int64_t topk,
+    void* __restrict__ y, int64_t ldy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= n_out) return;
+  const int64_t t = blockIdx.y;
+  float acc = 0.f;
+  for (int64_t j = 0; j < topk; ++j) {
+    const int64_t s = t * topk + j;
+    const int64_t e = expert_id(ids, ids64, s, n_exp);
+    const float v = row_dot_generic(x, x_dt, s * ldx, w, e, row, n_out, nwords, kn, lane);
+    acc += wts[s] * (v * ld_f(alpha, a_dt, e * n_out + row));
+  }
+  if (lane == 0) {
+    if (res) acc += ld_f(res, res_dt, t * n_out + row);
+    st_f(y, x_dt, t * ldy + row, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch.
+// ---------------------------------------------------------------------------
+#define MA_EXPERT_SHAPES(X) X(32, 4) X(32, 8) X(32, 2) X(32, 1) X(32, 3) X(32, 5) X(16, 3) X(16, 1) X(8, 1)
+
+static bool fast_shape(int64_t nwords, int& lpr, int& kw) {
+#define MA_PICK(L, K) \
+  if (nwords == (L) * (K)) { lpr = L; kw = K; return true; }
+  MA_EXPERT_SHAPES(MA_PICK)
+#undef MA_PICK
+  return false;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+static bool fast_ok(const void* x, int x_dt, int64_t ldx, const uint32_t* w, int64_t nwords,
+                    int kn, int a_dt, int& lpr, int& kw) {
+  if (x_dt != MA_BF16 || kn || (a_dt != MA_BF16 && a_dt != MA_F32)) return false;
+  if (!fast_shape(nwords, lpr, kw)) return false;
+  const uintptr_t wa = (kw % 4 == 0) ? 16 : (kw % 2 == 0) ? 8 : 4;
+  return aligned16(x) && (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(w) % wa) == 0;
+}
+
+}  // namespace ma
+
+using namespace ma;
+
+extern "C" int ma_ternary_expert_swiglu(const void* x, int x_dtype, int64_t ldx, int64_t tokens,
+                                        int64_t top_k, const uint32_t* packed,
+                                        int64_t n_experts, int64_t n_rows, int64_t nwords,
+                                        int packed_kn, const void* row_alpha, int alpha_dtype,
+                                        const void* ids, int ids_is_int64, void* h, int64_t ldh,
+                                        void* stream) {
+  if (tokens < 0 || top_k < 1 || n_rows < 0 || (n_rows % 2) || nwords < 1 || n_experts < 1)
+    return fail(MA_EVALUE, "ternary_expert_swiglu: bad sizes");
+  const int64_t slots = tokens * top_k, n_half = n_rows / 2;
+  if (slots == 0 || n_half == 0) return MA_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int lpr = 0, kw = 0;
+  if (fast_ok(x, x_dtype, ldx, packed, nwords, packed_kn, alpha_dtype, lpr, kw)) {
+    constexpr int U = 4;
+#define MA_LAUNCH(L, K)                                                                        \
+  if (lpr == L && kw == K) {                                                                   \
+    constexpr int PPI = (64 / L) / 2;                                                          \
+    dim3 grid(static_cast<unsigned>(cdiv(n_half, PPI * U)), static_cast<unsigned>(slots));    \
+    if (alpha_dtype == MA_BF16)                                                                \
+      hipLaunchKernelGGL((k_swiglu_fast<K, L, U, MA_BF16>), grid, dim3(64), 0, s,              \
+                         static_cast<const uint16_t*>(x), ldx, top_k, packed, n_half,          \
+                         row_alpha, ids, ids_is_int64, n_experts, static_cast<uint16_t*>(h), ldh);        \
+    else                                                                                       \
+      hipLaunchKernelGGL((k_swiglu_fast<K, L, U, MA_F32>), grid, dim3(64), 0, s,               \
+                         static_cast<const uint16_t*>(x), ldx, top_k, packed, n_half,          \
+                         row_alpha, ids, ids_is_int64, n_experts, static_cast<uint16_t*>(h), ldh);        \
+    return check_launch("ternary_expert_swiglu");                                             \
+  }
+    MA_EXPERT_SHAPES(MA_LAUNCH)
+#undef MA_LAUNCH
+  }
+  dim3 grid(static_cast<unsigned>(cdiv(n_half, 4)), static_cast<unsigned>(slots));
+  hipLaunchKernelGGL(k_expert_generic, grid, dim3(256), 0, s, x, x_dtype, ldx, top_k, packed,
+                     n_rows, n_half, nwords, packed_kn, row_alpha, alpha_dtype, ids,
+                     ids_is_int64, n_experts, 1, h, x_dtype, ldh);
+  return check_launch("ternary_expert_swiglu");
+}
+
+extern "C" int ma_ternary_expert_gemv(const void* x, int x_dtype, int64_t ldx, int64_t x_div,
+                                      const uint32_t* packed, int64_t n_experts, int64_t n_out,
+                                      int64_t nwords, int packed_kn, const void* row_alpha,
+                                      int alpha_dtype, const void* ids, int ids_is_int64,
+                                      int64_t n_slots, void* y, int64_t ldy, void* stream) {
+  if (n_slots < 0 || n_out < 0 || nwords < 1 || x_div < 1 || n_experts < 1)
+    return fail(MA_EVALUE, "ternary_expert_gemv: bad sizes");
+  if (n_slots == 0 || n_out == 0) return MA_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int lpr = 0, kw = 0;
+  if (fast_ok(x, x_dtype, ldx, packed, nwords, packed_kn, alpha_dtype, lpr, kw)) {
+    constexpr int U = 2;
+#define MA_LAUNCH(L, K)                                                                        \
+  if (lpr == L && kw == K) {                                                                   \
+    dim3 grid(static_cast<unsigned>(cdiv(n_out, (64 / L) * U)), static_cast<unsigned>(n_slots)); \
+    if (alpha_dtype == MA_BF16)                                                                \
+      hipLaunchKernelGGL((k_egemv_fast<K, L, U, MA_BF16>), grid, dim3(64), 0, s,               \
+                         static_cast<const uint16_t*>(x), ldx, x_div, packed, n_out,           \
+                         row_alpha, ids, ids_is_int64, n_experts, static_cast<uint16_t*>(y), ldy);        \
+    else                                                                                       \
+      hipLaunchKernelGGL((k_egemv_fast<K, L, U, MA_F32>), grid, dim3(64), 0, s,                \
+                         static_cast<const uint16_t*>(x), ldx, x_div, packed, n_out,           \
+                         row_alpha, ids, ids_is_int64, n_experts, static_cast<uint16_t*>(y), ldy);        \
+    return check_launch("ternary_expert_gemv");                                               \
+  }
+    MA_EXPERT_SHAPES(MA_LAUNCH)
+#undef MA_LAUNCH
+  }
+  dim3 grid(static_cast<unsigned>(cdiv(n_out, 4)), static_cast<unsigned>(n_slots));
+  hipLaunchKernelGGL(k_expert_generic, grid, dim3(256), 0, s, x, x_dtype, ldx, x_div, packed,
+                     n_out, n_out, nwords, packed_kn, row_alpha, alpha_dtype, ids,
+                     ids_is_int64, n_experts, 0, y, x_dtype, ldy);
+  return check_launch("ternary_expert_gemv");
+}
+
+extern "C" int ma_ternary_expert_down_sum(const void* x, int x_dtype, int64_t ldx,
+                                          const uint32_t* packed, int64_t n_experts,
+                                          int64_t n_out, int64_t nwords, int packed_kn,
+                                          const void* row_alpha, int alpha_dtype,
+                                          const void* ids, int ids_is_int64,
+                                          const float* topk_weight, const void* residual,
+                                          int residual_dtype, int64_t tokens, int64_t top_k,
+                                          void* y, int64_t ldy, void* stream) {
+  if (tokens < 0 || top_k < 1 || n_out < 0 || nwords < 1 || n_experts < 1)
+    return fail(MA_EVALUE, "ternary_expert_down_sum: bad sizes");
+  if (tokens == 0 || n_out == 0) return MA_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int lpr = 0, kw = 0;
+  if (fast_ok(x, x_dtype, ldx, packed, nwords, packed_kn, alpha_dtype, lpr, kw)) {
+    constexpr int U = 2;
+#define MA_LAUNCH(L, K)                                                                        \
+  if (lpr == L && kw == K) {                                                                   \
+    dim3 grid(static_cast<unsigned>(cdiv(n_out, (64 / L) * U)), static_cast<unsigned>(tokens)); \
+    if (alpha_dtype == MA_BF16)                                                                \
+      hipLaunchKernelGGL((k_down_sum_fast<K, L, U, MA_BF16>), grid, dim3(64), 0, s,            \
+                         static_cast<const uint16_t*>(x), ldx, packed, n_out, row_alpha, ids,  \
+                         ids_is_int64, n_experts, topk_weight, residual, residual_dtype, top_k,           \
+                         static_cast<uint16_t*>(y), ldy);                                      \
+    else                                                                                       \
+      hipLaunchKernelGGL((k_down_sum_fast<K, L, U, MA_F32>), grid, dim3(64), 0, s,             \
+                         static_cast<const uint16_t*>(x), ldx, packed, n_out, row_alpha, ids,  \
+                         ids_is_int64, n_experts, topk_weight, residual, residual_dtype, top_k,           \
+                         static_cast<uint16_t*>(y), ldy);                                      \
+    return check_launch("ternary_expert_down_sum");                                           \
+  }
+    MA_EXPERT_SHAPES(MA_LAUNCH)
+#undef MA_LAUNCH
+  }
+  dim3 grid(static_cast<unsigned>(cdiv(n_out, 4)), static_cast<unsigned>(tokens));
+  hipLaunchKernelGGL(k_down_sum_generic, grid, dim3(256), 0, s, x, x_dtype, ldx, packed, n_out,
+                     nwords, packed_kn, row_alpha, alpha_dtype, ids, ids_is_int64, n_experts, topk_weight,
+                     residual, residual_dtype, top_k, y, ldy);
+  return check_launch("ternary_expert_down_sum");
+}

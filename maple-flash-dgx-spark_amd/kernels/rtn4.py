@@ -1,0 +1,107 @@
+"""4-bit RTN embedding lookup and GEMV (lm_head / embeddings).
+
+Drop-ins for reference ``src/maple_run/kernels/rtn4.py``: ``rtn4_embedding``
+(:27-47) and ``rtn4_gemv`` (:285-415).  Dequant is ``code * scale + bias`` per
+group, 8 LSB-first codes per uint32.  Unlike the reference, every batch size
+works with group 64 and 128 (the reference rejects group 128 above batch 16,
+``rtn4.py:79-81,349-353``).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+_CODES_PER_WORD = 8
+HEAD_GROUP_SIZE = 64
+
+
+def rtn4_embedding(
+    input_ids: torch.Tensor,
+    packed_weight: torch.Tensor,
+    scales: torch.Tensor,
+    biases: torch.Tensor,
+    group_size: int = HEAD_GROUP_SIZE,
+) -> torch.Tensor:
+    """Gather packed rows for ``input_ids`` and dequant those rows only (float32)."""
+    if packed_weight.dtype != torch.uint32:
+        raise TypeError(f"packed_weight must be uint32 codes, got {packed_weight.dtype}.")
+    if not input_ids.is_cuda or not packed_weight.is_cuda:
+        raise RuntimeError("rtn4_embedding requires CUDA tensors.")
+    vocab, nwords = packed_weight.shape
+    k = nwords * _CODES_PER_WORD
+    ids = input_ids.reshape(-1)
+    if ids.dtype not in (torch.int32, torch.int64):
+        ids = ids.to(torch.int64)
+    ids = ids.contiguous()
+    out = torch.empty(ids.numel(), k, device=packed_weight.device, dtype=torch.float32)
+    sc, bs = scales.contiguous(), biases.contiguous()
+    _lib.call(
+        "ma_rtn4_embedding",
+        _lib.ptr(ids), int(ids.dtype == torch.int64), ids.numel(),
+        _lib.ptr(packed_weight.contiguous()), vocab, nwords,
+        _lib.ptr(sc), _lib.dtype_code(sc, "scales"), _lib.ptr(bs), _lib.dtype_code(bs, "biases"),
+        int(group_size), _lib.ptr(out), _lib.stream_of(packed_weight),
+    )
+    return out.reshape(*input_ids.shape, k)
+
+
+def rtn4_gemv(
+    x: torch.Tensor,
+    packed_weight: torch.Tensor,
+    scales: torch.Tensor,
+    biases: torch.Tensor,
+    group_size: int = HEAD_GROUP_SIZE,
+    *,
+    packed_kn: bool = False,
+) -> torch.Tensor:
+    """Decode GEMV ``y = x @ W`` with 4-bit packed ``W`` (affine RTN)."""
+    if packed_weight.dtype != torch.uint32:
+        raise TypeError(
+            f"packed_weight must be uint32 codes, got {packed_weight.dtype}; "
+            "refusing to run a dense-weight path."
+        )
+    if packed_weight.ndim != 2:
+        raise ValueError(
+            f"packed_weight must be 2-D [N, K/8] or [K/8, N]; got shape "
+            f"{tuple(packed_weight.shape)}."
+        )
+    if not x.is_cuda or not packed_weight.is_cuda:
+        raise RuntimeError("rtn4_gemv requires CUDA tensors.")
+    if packed_kn:
+        nwords, n_out = packed_weight.shape
+        n_groups = nwords * _CODES_PER_WORD // group_size
+        if tuple(scales.shape) != (n_groups, n_out) or tuple(biases.shape) != (n_groups, n_out):
+            raise ValueError(
+                f"packed_kn scales/biases expected {(n_groups, n_out)}, "
+                f"got {tuple(scales.shape)} and {tuple(biases.shape)}."
+            )
+    else:
+        n_out, nwords = packed_weight.shape
+        n_groups = nwords * _CODES_PER_WORD // group_size
+        if tuple(scales.shape) != (n_out, n_groups) or tuple(biases.shape) != (n_out, n_groups):
+            raise ValueError(
+                f"scales/biases expected {(n_out, n_groups)}, got {tuple(scales.shape)} "
+                f"and {tuple(biases.shape)}."
+            )
+    k_in = nwords * _CODES_PER_WORD
+    if x.shape[-1] != k_in:
+        raise ValueError(f"x last dim {x.shape[-1]} != packed K ({k_in}).")
+    if k_in % group_size:
+        raise ValueError(f"K={k_in} is not a whole number of RTN groups (group_size={group_size}).")
+    leading = x.shape[:-1]
+    batch = int(x.numel() // k_in)
+    x_mat = x.reshape(batch, k_in)
+    if x_mat.stride(-1) != 1:
+        x_mat = x_mat.contiguous()
+    y = torch.empty(batch, n_out, device=x.device, dtype=x.dtype)
+    pw, sc, bs = packed_weight.contiguous(), scales.contiguous(), biases.contiguous()
+    _lib.call(
+        "ma_rtn4_gemv",
+        _lib.ptr(x_mat), _lib.dtype_code(x_mat, "x"), batch, x_mat.stride(0) if batch else k_in,
+        _lib.ptr(pw), n_out, nwords, int(bool(packed_kn)),
+        _lib.ptr(sc), _lib.dtype_code(sc, "scales"), _lib.ptr(bs), _lib.dtype_code(bs, "biases"),
+        int(group_size), _lib.ptr(y), n_out, _lib.stream_of(x),
+    )
+    return y.reshape(*leading, n_out)

@@ -1,0 +1,61 @@
+"""The C ABI: the built library loads and exports every declared symbol (CPU).
+
+No compute call is made here (no GPU); the GPU tests call through the same
+entry points.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from maple_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "maple_amd.h"
+
+
+def declared_in_header() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(ma_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_path():
+    names = declared_in_header()
+    for must in ("ma_ternary_gemv", "ma_router_topk", "ma_moe_dispatch", "ma_ternary_expert_swiglu",
+                 "ma_ternary_expert_gemv", "ma_ternary_expert_down_sum", "ma_moe_reduce_add",
+                 "ma_rtn4_gemv", "ma_rtn4_embedding", "ma_rms_norm", "ma_add_rms_norm"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in declared_in_header() if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_binding_covers_header():
+    assert set(declared_in_header()) <= set(_lib.declared_symbols())
+
+
+def test_version_and_error_string():
+    lib = _lib.load()
+    assert lib.ma_version() >= 100
+    assert isinstance(lib.ma_last_error(), bytes)
+
+
+def test_size_errors_map_without_a_gpu():
+    """Bad sizes are rejected on the host before any launch: status -> ValueError."""
+    with pytest.raises(ValueError, match="bad sizes"):
+        _lib.call("ma_ternary_gemv", None, 1, -1, 16, None, 4, 1, 0, None, 0, None, 0, 1e-6,
+                  None, 4, None)
+    with pytest.raises(ValueError, match="top_k"):
+        _lib.call("ma_router_topk", None, 1, 1, 16, None, 1, 4, 16, None, 5, None, None, None, 0, None)
+    with pytest.raises(ValueError, match="n_experts"):
+        _lib.call("ma_moe_dispatch", None, 0, 8, 0, None, None, None, None, None)
+    with pytest.raises(ValueError, match="groups"):
+        _lib.call("ma_rtn4_gemv", None, 1, 1, 96, None, 4, 12, 0, None, 1, None, 1, 64, None, 4, None)

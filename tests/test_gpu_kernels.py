@@ -1,0 +1,298 @@
+"""HIP kernels vs the CPU oracle on seeded inputs (needs the GPU).
+
+Tolerances: bf16 outputs within one bf16 ulp (2^-8 relative) plus 1e-3 of the
+output scale of the float64 oracle evaluated on the same bf16 inputs, and max
+relative error <= 1e-2; float32 outputs rtol/atol 1e-4 (the reference's own
+float32 tolerance, tests/test_ternary_gemv.py:91).  Integer outputs (unpacked
+values, top-k ids away from float ties, dispatch lists) are compared exactly.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import assert_bf16_close, assert_f32_close, np_f, np_u32, tie_safe_rows
+from maple_amd import synthetic
+from maple_amd.kernels import (
+    add_rms_norm,
+    moe_dispatch,
+    moe_reduce_add,
+    rms_norm,
+    router_topk,
+    rtn4_embedding,
+    rtn4_gemv,
+    ternary_expert_down_sum,
+    ternary_expert_gemv,
+    ternary_expert_swiglu,
+    ternary_gemv,
+)
+from oracle import kernels as ok
+from oracle import pack
+
+pytestmark = pytest.mark.gpu
+
+
+def _u32(a: np.ndarray, dev) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(dev).view(torch.uint32)
+
+
+# ---------------------------------------------------------------- ternary GEMV
+def test_gemv_reference_kat(dev):
+    """tests/test_ternary_gemv.py:114-132: LSB-first codes, code 2 -> +a, code 0 -> -a."""
+    codes = np.ones((2, 128), np.uint32)
+    codes[0, 0] = 2
+    codes[1, 1] = 0
+    w = _u32(pack.pack_2bit(codes), dev)
+    alpha = torch.tensor([0.5, 1.25], device=dev)
+    x = torch.arange(128, device=dev, dtype=torch.float32)
+    y = ternary_gemv(x, w, alpha)
+    assert_f32_close(np_f(y), [0.0, -1.25], rtol=0, atol=1e-6)
+    yb = ternary_gemv(x.bfloat16(), w, alpha)  # bf16 fast path: same answer
+    assert_f32_close(np_f(yb), [0.0, -1.25], rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("n_out,k_in", [(1536, 2048), (2560, 2048), (2048, 768), (96, 128), (64, 256),
+                                        (33, 512), (40, 4096), (17, 2560)])
+def test_gemv_bf16_batch1_vs_oracle(dev, n_out, k_in):
+    w = synthetic.ternary_packed((n_out, k_in), 11, dev)
+    alpha = synthetic.uniform_bf16((n_out,), 0.01, 0.05, 12, dev)
+    x = synthetic.randn_bf16((1, k_in), 13, dev)
+    y = ternary_gemv(x, w, alpha)
+    assert y.shape == (1, n_out) and y.dtype == torch.bfloat16
+    ref = ok.ternary_gemv(np_f(x), np_u32(w), np_f(alpha))
+    assert_bf16_close(np_f(y), ref, what=f"gemv {n_out}x{k_in}")
+
+
+def test_gemv_code3_is_plus_two(dev):
+    """Code 3 (never produced by ternarize) reads as +2 (ternary_gemv.py:126-128)."""
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 4, (64, 2048), dtype=np.uint32)
+    w = _u32(pack.pack_2bit(codes), dev)
+    alpha = torch.rand(64, device=dev) + 0.5
+    x = synthetic.randn_bf16((1, 2048), 3, dev)
+    ref = ok.ternary_gemv(np_f(x), pack.pack_2bit(codes), np_f(alpha))
+    assert_bf16_close(np_f(ternary_gemv(x, w, alpha)), ref, what="code3 bf16")
+    assert_f32_close(np_f(ternary_gemv(x.float(), w, alpha)), ref, rtol=1e-4, atol=1e-3, what="code3 f32")
+
+
+@pytest.mark.parametrize("batch", [2, 3, 4, 8, 17, 32])
+def test_gemv_bf16_batched_vs_oracle(dev, batch):
+    w = synthetic.ternary_packed((512, 2048), 21, dev)
+    alpha = synthetic.uniform_bf16((512,), 0.01, 0.05, 22, dev)
+    x = synthetic.randn_bf16((batch, 2048), 23, dev)
+    y = ternary_gemv(x, w, alpha)
+    assert_bf16_close(np_f(y), ok.ternary_gemv(np_f(x), np_u32(w), np_f(alpha)), what=f"B={batch}")
+    rows = torch.cat([ternary_gemv(x[i:i + 1], w, alpha) for i in range(batch)])
+    torch.testing.assert_close(y, rows, rtol=8e-3, atol=8e-3)
+
+
+@pytest.mark.parametrize("batch", [1, 2, 8, 32])
+def test_gemv_fused_rms_vs_oracle(dev, batch):
+    w = synthetic.ternary_packed((2560, 2048), 31, dev)
+    alpha = synthetic.uniform_bf16((2560,), 0.01, 0.05, 32, dev)
+    x = synthetic.randn_bf16((batch, 2048), 33, dev)
+    rms_w = torch.rand(2048, device=dev) + 0.5
+    y = ternary_gemv(x, w, alpha, rms_weight=rms_w, rms_eps=1e-6)
+    ref = ok.ternary_gemv(np_f(x), np_u32(w), np_f(alpha), rms_weight=np_f(rms_w), rms_eps=1e-6)
+    assert_bf16_close(np_f(y), ref, what=f"rms B={batch}")
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_gemv_fp32_activations_and_packed_kn(dev, batch):
+    rng = np.random.default_rng(7)
+    wf = rng.standard_normal((96, 256)).astype(np.float32)
+    packed, alpha = pack.ternarize(wf)
+    w = _u32(packed, dev)
+    a = torch.from_numpy(alpha).to(dev)
+    x = torch.from_numpy(rng.standard_normal((batch, 256)).astype(np.float32)).to(dev)
+    ref = ok.ternary_gemv(np_f(x), packed, alpha)
+    assert_f32_close(np_f(ternary_gemv(x, w, a)), ref, what="fp32 nk")
+    w_kn = _u32(np.ascontiguousarray(packed.T), dev)
+    assert_f32_close(np_f(ternary_gemv(x, w_kn, a, packed_kn=True)), ref, what="fp32 kn")
+    xb = x.bfloat16()
+    refb = ok.ternary_gemv(np_f(xb), packed, alpha)
+    assert_bf16_close(np_f(ternary_gemv(xb, w_kn, a, packed_kn=True)), refb, what="bf16 kn")
+
+
+def test_gemv_1d_x_and_empty_batch(dev):
+    w = synthetic.ternary_packed((48, 128), 41, dev)
+    alpha = torch.rand(48, device=dev)
+    x = synthetic.randn_bf16((128,), 42, dev)
+    y = ternary_gemv(x, w, alpha)
+    assert y.shape == (48,)
+    assert_bf16_close(np_f(y), ok.ternary_gemv(np_f(x), np_u32(w), np_f(alpha)), what="1d")
+    assert ternary_gemv(x[None][:0], w, alpha).shape == (0, 48)
+
+
+def test_gemv_rejects_non_uint32(dev):
+    with pytest.raises(TypeError, match="uint32"):
+        ternary_gemv(torch.randn(128, device=dev), torch.randn(16, 8, device=dev).bfloat16(),
+                     torch.ones(16, device=dev))
+
+
+# ---------------------------------------------------------------- router
+@pytest.mark.parametrize("tokens,n_exp,top_k", [(1, 64, 8), (32, 64, 8), (128, 64, 8), (2048, 64, 8),
+                                                (3, 4, 2), (5, 256, 8)])
+def test_router_vs_oracle(dev, tokens, n_exp, top_k):
+    gw = synthetic.randn_bf16((n_exp, 2048), 51, dev, std=0.02)
+    x = synthetic.randn_bf16((tokens, 2048), 52, dev)
+    ids, wts = router_topk(x, gw, top_k)
+    assert ids.dtype == torch.int32 and wts.dtype == torch.float32
+    rid, rw, probs = ok.router_topk(np_f(x), np_f(gw), top_k)
+    safe = tie_safe_rows(probs, top_k)
+    assert safe.mean() > 0.98, f"too many near-ties ({(~safe).sum()})"
+    np.testing.assert_array_equal(ids.cpu().numpy()[safe], rid[safe])
+    np.testing.assert_allclose(wts.cpu().numpy()[safe], rw[safe], rtol=1e-4, atol=1e-6)
+
+
+def test_router_ties_and_bias(dev):
+    gw = torch.zeros(6, 64, device=dev, dtype=torch.bfloat16)
+    gw[4, 0] = gw[2, 0] = 1.0
+    x = torch.zeros(1, 64, device=dev, dtype=torch.bfloat16)
+    x[0, 0] = 1.0
+    ids, wts = router_topk(x, gw, 4)
+    assert ids[0].tolist() == [2, 4, 0, 1]
+    bias = torch.tensor([0, 0, 0, 0, 0, 5.0], device=dev)
+    ids, _ = router_topk(x, gw, 2, bias=bias)
+    assert ids[0].tolist() == [5, 2]
+
+
+# ---------------------------------------------------------------- dispatch
+@pytest.mark.parametrize("tokens,top_k,n_exp", [(1, 8, 64), (32, 8, 64), (128, 8, 64), (2048, 8, 64),
+                                                (7, 3, 5), (0, 8, 64), (1000, 8, 256)])
+def test_dispatch_bit_exact(dev, tokens, top_k, n_exp):
+    g = torch.Generator(device=dev).manual_seed(tokens * 7 + n_exp)
+    ids = torch.randint(0, n_exp, (tokens, top_k), generator=g, device=dev, dtype=torch.int32)
+    d = moe_dispatch(ids, n_exp)
+    c, o, p, inv = ok.dispatch(ids.cpu().numpy(), n_exp)
+    np.testing.assert_array_equal(d.counts.cpu().numpy(), c)
+    np.testing.assert_array_equal(d.offsets.cpu().numpy(), o)
+    np.testing.assert_array_equal(d.pair_ids.cpu().numpy(), p)
+    np.testing.assert_array_equal(d.inverse.cpu().numpy(), inv)
+
+
+def test_dispatch_skewed_int64(dev):
+    """All pairs on one expert plus a few singletons, int64 ids."""
+    ids = torch.full((300, 8), 17, device=dev, dtype=torch.int64)
+    ids[5, 3] = 0
+    ids[299, 7] = 63
+    d = moe_dispatch(ids, 64)
+    c, o, p, inv = ok.dispatch(ids.cpu().numpy(), 64)
+    np.testing.assert_array_equal(d.pair_ids.cpu().numpy(), p)
+    np.testing.assert_array_equal(d.offsets.cpu().numpy(), o)
+
+
+# ---------------------------------------------------------------- experts
+def _experts(dev, n_exp=8, hidden=2048, inter=768, seed=0):
+    return synthetic.make_moe_layer(hidden=hidden, n_experts=n_exp, inter=inter, seed=seed, device=dev)
+
+
+@pytest.mark.parametrize("tokens,top_k", [(1, 8), (3, 2), (32, 8)])
+def test_expert_swiglu_vs_oracle(dev, tokens, top_k):
+    L = _experts(dev)
+    x = synthetic.randn_bf16((tokens, 2048), 61, dev)
+    g = torch.Generator(device=dev).manual_seed(62)
+    ids = torch.stack([torch.randperm(8, generator=g, device=dev)[:top_k] for _ in range(tokens)]).int()
+    h = ternary_expert_swiglu(x, L.up_gate_packed, L.up_gate_alpha, ids)
+    assert h.shape == (tokens, top_k, 768) and h.dtype == torch.bfloat16
+    ref = ok.ternary_expert_swiglu(np_f(x), np_u32(L.up_gate_packed), np_f(L.up_gate_alpha), ids.cpu().numpy())
+    assert_bf16_close(np_f(h), ref, what="swiglu")
+
+
+@pytest.mark.parametrize("per_slot", [True, False])
+def test_expert_gemv_vs_oracle(dev, per_slot):
+    L = _experts(dev)
+    ids = torch.tensor([[0, 3], [5, 5], [7, 1]], device=dev, dtype=torch.int32)
+    k = 768
+    x = synthetic.randn_bf16((3, 2, k) if per_slot else (3, k), 71, dev)
+    y = ternary_expert_gemv(x, L.down_packed, L.down_alpha, ids)
+    ref = ok.ternary_expert_gemv(np_f(x), np_u32(L.down_packed), np_f(L.down_alpha), ids.cpu().numpy())
+    assert_bf16_close(np_f(y), ref, what="expert gemv")
+
+
+def test_expert_kernels_fp32_generic_path(dev):
+    """fp32 activations take the generic kernels; reference tolerance 1e-4."""
+    rng = np.random.default_rng(3)
+    n_exp, hidden, inter = 4, 128, 128
+    up, up_a = pack.ternarize(rng.standard_normal((n_exp, inter, hidden)).astype(np.float32))
+    gt, gt_a = pack.ternarize(rng.standard_normal((n_exp, inter, hidden)).astype(np.float32))
+    dn, dn_a = pack.ternarize(rng.standard_normal((n_exp, hidden, inter)).astype(np.float32))
+    ug = np.concatenate([up, gt], axis=1)
+    ug_a = np.concatenate([up_a, gt_a], axis=1)
+    x = rng.standard_normal((3, hidden)).astype(np.float32)
+    ids = np.array([[0, 3], [1, 1], [2, 0]], np.int32)
+    w = np.array([[0.6, 0.4], [0.5, 0.5], [0.2, 0.8]], np.float32)
+    res = rng.standard_normal((3, hidden)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    h = ternary_expert_swiglu(t(x), _u32(ug, dev), t(ug_a), t(ids))
+    href = ok.ternary_expert_swiglu(x, ug, ug_a, ids)
+    assert_f32_close(np_f(h), href, what="swiglu fp32")
+    y = ternary_expert_down_sum(h, _u32(dn, dev), t(dn_a), t(ids), t(w), residual=t(res))
+    assert_f32_close(np_f(y), ok.ternary_expert_down_sum(np_f(h), dn, dn_a, ids, w, residual=res),
+                     what="down_sum fp32")
+    eo = ternary_expert_gemv(h, _u32(dn, dev), t(dn_a), t(ids))
+    assert_f32_close(np_f(moe_reduce_add(eo, t(w), t(res))), ok.moe_reduce_add(np_f(eo), w, res),
+                     what="reduce fp32")
+
+
+@pytest.mark.parametrize("tokens", [1, 4])
+def test_expert_down_sum_vs_oracle(dev, tokens):
+    L = _experts(dev)
+    top_k = 8
+    g = torch.Generator(device=dev).manual_seed(81)
+    ids = torch.stack([torch.randperm(8, generator=g, device=dev) for _ in range(tokens)]).int()
+    w = torch.softmax(torch.randn(tokens, top_k, device=dev, generator=g), -1)
+    h = synthetic.randn_bf16((tokens, top_k, 768), 82, dev)
+    res = synthetic.randn_bf16((tokens, 2048), 83, dev)
+    y = ternary_expert_down_sum(h, L.down_packed, L.down_alpha, ids, w, residual=res)
+    ref = ok.ternary_expert_down_sum(np_f(h), np_u32(L.down_packed), np_f(L.down_alpha), ids.cpu().numpy(),
+                                     np_f(w), residual=np_f(res))
+    assert_bf16_close(np_f(y), ref, what="down_sum")
+
+
+def test_expert_ids_out_of_range_are_clamped_not_faulting(dev):
+    L = _experts(dev, n_exp=4, hidden=256, inter=128)
+    x = synthetic.randn_bf16((1, 256), 5, dev)
+    bad = torch.tensor([[9, -1]], device=dev, dtype=torch.int32)
+    good = torch.tensor([[3, 0]], device=dev, dtype=torch.int32)
+    torch.testing.assert_close(ternary_expert_swiglu(x, L.up_gate_packed, L.up_gate_alpha, bad),
+                               ternary_expert_swiglu(x, L.up_gate_packed, L.up_gate_alpha, good))
+
+
+# ---------------------------------------------------------------- RTN4 / norms
+@pytest.mark.parametrize("batch,group", [(1, 128), (1, 64), (2, 128), (4, 64), (32, 128)])
+def test_rtn4_gemv_vs_oracle(dev, batch, group):
+    w, sc, bs = synthetic.rtn4_table(4096, 2048, group, 91, dev)
+    x = synthetic.randn_bf16((batch, 2048), 92, dev)
+    y = rtn4_gemv(x, w, sc, bs, group_size=group)
+    ref = ok.rtn4_gemv(np_f(x), np_u32(w), np_f(sc), np_f(bs), group_size=group)
+    assert_bf16_close(np_f(y), ref, what=f"rtn4 B={batch} g={group}")
+
+
+def test_rtn4_reference_fixture_fp32_and_kn(dev):
+    rng = np.random.default_rng(1)
+    wf = rng.standard_normal((64, 256)).astype(np.float32)
+    packed, scales, biases = pack.quantize_rtn(wf)
+    x = rng.standard_normal((2, 256)).astype(np.float32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    ref = ok.rtn4_gemv(x, packed, scales, biases)
+    assert_f32_close(np_f(rtn4_gemv(t(x), _u32(packed, dev), t(scales), t(biases))), ref, what="rtn4 fp32")
+    y_kn = rtn4_gemv(t(x), _u32(np.ascontiguousarray(packed.T), dev), t(scales.T), t(biases.T), packed_kn=True)
+    assert_f32_close(np_f(y_kn), ref, what="rtn4 kn")
+    ids = torch.tensor([[3, 7, 0], [1, 1, 63]], device=dev)
+    emb = rtn4_embedding(ids, _u32(packed, dev), t(scales), t(biases))
+    assert_f32_close(np_f(emb), ok.rtn4_embedding(ids.cpu().numpy(), packed, scales, biases),
+                     rtol=1e-6, atol=1e-6, what="embedding")
+
+
+def test_norms_vs_oracle(dev):
+    x = synthetic.randn_bf16((3, 2048), 101, dev)
+    y = synthetic.randn_bf16((3, 2048), 102, dev)
+    w = torch.rand(2048, device=dev) + 0.5
+    assert_bf16_close(np_f(rms_norm(x, w)), ok.rms_norm(np_f(x), np_f(w)), what="rms_norm")
+    res, nrm = add_rms_norm(x, y, w)
+    s, n = ok.add_rms_norm(np_f(x), np_f(y), np_f(w))
+    assert_bf16_close(np_f(res), s, what="residual")
+    assert_bf16_close(np_f(nrm), n, what="normed")
