@@ -1,0 +1,226 @@
+"""Benchmark: packed-ternary MoE FFN layer, decode batch 1, on one MI355X.
+
+Workload: one synthetic MoE FFN layer (hidden 2048, 64 experts, SwiGLU
+intermediate 768, top-8 routing) at decode batch 1, run through the HIP
+kernels (router top-k, fused up+gate SwiGLU, down projection + weighted
+combine).  ``--layers`` distinct layers (default 24, ~1.8 GB of packed
+weights, several times the 256 MB Infinity Cache) are captured in one HIP
+graph and replayed, so every layer's weights come from HBM.
+
+A step is one graph replay: ``--layers`` MoE-layer decodes, each on its own
+cold layer.  ``value`` is the whole-layer algorithmic HBM throughput:
+(selected experts' packed codes + scales, the router weight, x in and y out)
+per layer, times layers and steps, over the timed wall time.
+
+``roofline`` covers the dominant kernel (the SwiGLU expert kernel, which
+streams 2/3 of the bytes): algorithmic bytes per launch over its average
+launch period, timed with HIP events on the stream it runs on over a graph of
+back-to-back launches on the same cold layers (the period includes the
+dispatch gap between dependent kernels, so it is an upper bound on the
+kernel's own duration).  ``traffic`` is read from the rocprofv3 counter
+summary under profiles/ when present.
+
+``cpu_baseline`` times the CPU oracle path (NumPy unpack -> dequantise ->
+float32 matmul over the 8 selected experts, the reference's own test
+oracle) on a bounded sample of the same workload on this host's cores.
+
+    python bench.py [--steps 20] [--warmup 3] [--layers 24] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "decode tok/s (bs1, bs32); packed-ternary MoE layer HBM GB/s vs 8 TB/s peak"
+HBM_PEAK_GBS = 8000.0
+HIDDEN, EXPERTS, INTER, TOPK = 2048, 64, 768, 8
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def layer_bytes() -> dict:
+    codes = (2 * INTER * HIDDEN + HIDDEN * INTER) // 4
+    alpha = (2 * INTER + HIDDEN) * 2
+    expert = codes + alpha
+    router = EXPERTS * HIDDEN * 2
+    act = HIDDEN * 2 * 2
+    swiglu = TOPK * (2 * INTER * HIDDEN // 4 + 2 * INTER * 2) + HIDDEN * 2 + TOPK * INTER * 2
+    return {"expert": expert, "selected": TOPK * expert, "layer": TOPK * expert + router + act,
+            "swiglu_launch": swiglu}
+
+
+def graph_of(fn):
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def read_traffic(kernel: str):
+    """HBM bytes per launch from profiles/<kernel>_traffic.md, if measured."""
+    p = ROOT / "profiles" / f"{kernel}_traffic.md"
+    if not p.exists():
+        return None
+    m = re.search(r"hbm_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(seconds: float = 12.0) -> dict:
+    import numpy as np
+
+    from oracle import kernels as ok
+    from oracle import pack
+
+    cores = len(os.sched_getaffinity(0))
+    rng = np.random.default_rng(0)
+    ug = pack.pack_2bit(rng.integers(0, 3, (EXPERTS, 2 * INTER, HIDDEN), dtype=np.uint32))
+    ua = rng.uniform(0.01, 0.05, (EXPERTS, 2 * INTER)).astype(np.float32)
+    dn = pack.pack_2bit(rng.integers(0, 3, (EXPERTS, HIDDEN, INTER), dtype=np.uint32))
+    da = rng.uniform(0.01, 0.05, (EXPERTS, HIDDEN)).astype(np.float32)
+    gw = (rng.standard_normal((EXPERTS, HIDDEN)) * 0.02).astype(np.float32)
+    xs = rng.standard_normal((64, 1, HIDDEN)).astype(np.float32)
+    for i in range(3):
+        ok.moe_layer_cpu_fp32(xs[i], gw, ug, ua, dn, da, TOPK)
+    times = []
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while len(times) < 20 or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        ok.moe_layer_cpu_fp32(xs[i % 64], gw, ug, ua, dn, da, TOPK)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    med = float(np.median(times))
+    return {
+        "value": round(layer_bytes()["layer"] / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{len(times)} MoE-layer decodes (bs1, H2048 E64 I768 top-8), median "
+                  f"{med * 1e3:.1f} ms; NumPy unpack + float32 matmul per selected expert, "
+                  f"BLAS threads = {cores}, os.cpu_count() = {os.cpu_count()}",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=24)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from maple_amd import synthetic
+    from maple_amd.kernels import router_topk, ternary_expert_swiglu
+    from maple_amd.moe import moe_block
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    nb = layer_bytes()
+    L = args.layers
+    log(f"building {L} cold MoE layers ...")
+    layers = [synthetic.make_moe_layer(HIDDEN, EXPERTS, INTER, seed=i, device=dev) for i in range(L)]
+    x = synthetic.randn_bf16((1, HIDDEN), 12345, dev)
+    torch.cuda.synchronize()
+
+    # Whole-layer timing: L layer decodes per graph replay.
+    g = graph_of(lambda: [moe_block(x, layers[i], TOPK) for i in range(L)])
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(True), torch.cuda.Event(True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    value = nb["layer"] * L / (ms * 1e-3) / 1e9
+    log(f"MoE layer bs1: {ms * 1e3 / L:.2f} us/layer, {value:.1f} GB/s (wall {wall:.3f} s)")
+
+    # Dominant kernel: SwiGLU expert kernel over the same cold layers.
+    ids = [router_topk(x, layers[i].gate_weight, TOPK)[0] for i in range(L)]
+    gk = graph_of(lambda: [ternary_expert_swiglu(x, layers[i].up_gate_packed,
+                                                 layers[i].up_gate_alpha, ids[i]) for i in range(L)])
+    for _ in range(args.warmup):
+        gk.replay()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    k0, k1 = torch.cuda.Event(True), torch.cuda.Event(True)
+    k0.record(s)
+    for _ in range(args.steps):
+        gk.replay()
+    k1.record(s)
+    torch.cuda.synchronize()
+    per_launch = k0.elapsed_time(k1) / (args.steps * L) * 1e-3
+    achieved = nb["swiglu_launch"] / per_launch / 1e9
+    log(f"swiglu kernel: {per_launch * 1e6:.2f} us/launch, {achieved:.1f} GB/s")
+
+    from maple_amd.kernels.router import router_wait_timed_out
+
+    if router_wait_timed_out(dev):
+        log("router reported a timed-out wait: results invalid")
+        return 1
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "moe_ffn_layer_decode_bs1", "hidden": HIDDEN, "experts": EXPERTS,
+                   "intermediate": INTER, "top_k": TOPK, "tokens": 1, "cold_layers": L,
+                   "bytes_per_layer": nb["layer"], "us_per_layer": round(ms * 1e3 / L, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic("swiglu_bs1"), "kernel": "k_swiglu_fast",
+                     "bytes_per_launch": nb["swiglu_launch"],
+                     "us_per_launch": round(per_launch * 1e6, 3)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        log("timing the CPU baseline ...")
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -31,6 +31,9 @@ FLAGS = [
     "-fPIC",
     "-ffp-contract=fast",
     "-munsafe-fp-atomics",
+    # Kernel arguments arrive preloaded in SGPRs (saves a dependent load at
+    # the head of every kernel; decode kernels are latency-bound).
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     # Keep the compiler from forming packed-FP32 instructions.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}",

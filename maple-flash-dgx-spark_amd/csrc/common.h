@@ -169,10 +169,23 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  v = fmaxf(v, MA_DPP(v, 0xB1));
+  v = fmaxf(v, MA_DPP(v, 0x4E));
+  v = fmaxf(v, MA_DPP(v, 0x124));
+  v = fmaxf(v, MA_DPP(v, 0x128));
+  v = fmaxf(v, MA_SWZ_XOR(v, 16));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
 }
+
+// Value of lane `src` (a compile-time or wave-uniform index) in every lane.
+__device__ __forceinline__ float lane_bcast(float v, int src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
+}
+
+// Nothing may be scheduled across this point: keeps every load issued above
+// it ahead of the arithmetic below (the scheduler otherwise sinks loads next
+// to their first use to save registers, serialising their latencies).
+#define MA_ISSUE_FENCE() __builtin_amdgcn_sched_barrier(0)
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

@@ -22,6 +22,11 @@ __device__ __forceinline__ int64_t expert_id(const void* ids, int ids64, int64_t
   return e < 0 ? 0 : (e >= n_exp ? n_exp - 1 : e);
 }
 
+// The fast kernels take int32 ids only (one scalar load, no dtype branch).
+__device__ __forceinline__ int64_t clamp_id(int32_t e, int64_t n_exp) {
+  return e < 0 ? 0 : (e >= n_exp ? n_exp - 1 : e);
+}
+
 __device__ __forceinline__ float swiglu(float up, float gate) {
   up = fminf(fmaxf(up, -kMlpClamp), kMlpClamp);
   gate = fminf(gate, kMlpClamp);
@@ -29,44 +34,92 @@ __device__ __forceinline__ float swiglu(float up, float gate) {
 }
 
 // ---------------------------------------------------------------------------
-// Fast SwiGLU: lanes of sub-group [0, PPI) compute up rows, [PPI, 2*PPI) the
+// x' staging in LDS: one workgroup prepares the pairs of one bf16 activation
+// row once (thread t -> word t), so its waves do not each reload and
+// re-convert x.  xs[w][j] = pair j of word w, cw[w] = sum (f_j + 1) x over w.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void stage_row(const uint16_t* __restrict__ row, int64_t nwords,
+                                          uint32_t (*xs)[8], float* cw) {
+  for (int64_t wi = threadIdx.x; wi < nwords; wi += blockDim.x) {
+    const uint4 a = reinterpret_cast<const uint4*>(row + wi * 16)[0];
+    const uint4 b = reinterpret_cast<const uint4*>(row + wi * 16)[1];
+    const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      v[2 * q] = __uint_as_float(u[q] << 16);
+      v[2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
+    }
+    uint32_t pr[8];
+    cw[wi] = prep_word_pairs(v, pr);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xs[wi][j] = pr[j];
+  }
+}
+
+template <int KW>
+__device__ __forceinline__ void slice_from_lds(const uint32_t (*xs)[8], const float* cw, int kl,
+                                               XSlice<KW>& out) {
+  out.c = 0.f;
+#pragma unroll
+  for (int i = 0; i < KW; ++i) {
+    const int w = kl * KW + i;
+    const uint4 lo = *reinterpret_cast<const uint4*>(&xs[w][0]);
+    const uint4 hi = *reinterpret_cast<const uint4*>(&xs[w][4]);
+    out.xp[i][0] = lo.x; out.xp[i][1] = lo.y; out.xp[i][2] = lo.z; out.xp[i][3] = lo.w;
+    out.xp[i][4] = hi.x; out.xp[i][5] = hi.y; out.xp[i][6] = hi.z; out.xp[i][7] = hi.w;
+    out.c += cw[w];
+  }
+}
+
+constexpr int kMaxStageWords = 256;  // K <= 4096 for the LDS-staged kernels
+
+// ---------------------------------------------------------------------------
+// Fast SwiGLU: the waves of a workgroup share the staged x of one token.  In a
+// wave, lanes of sub-group [0, PPI) compute up rows and [PPI, 2*PPI) the
 // matching gate rows; the gate value is fetched across the wave.
 // ---------------------------------------------------------------------------
+constexpr int kSwigluWaves = 8;
+
 template <int KW, int LPR, int U, int ADT>
-__global__ __launch_bounds__(64) void k_swiglu_fast(
+__global__ __launch_bounds__(64 * kSwigluWaves) void k_swiglu_fast(
     const uint16_t* __restrict__ x, int64_t ldx, int64_t topk,
     const uint32_t* __restrict__ w, int64_t n_half,
-    const void* __restrict__ alpha, const void* __restrict__ ids, int ids64, int64_t n_exp,
+    const void* __restrict__ alpha, const int32_t* __restrict__ ids, int64_t n_exp,
     uint16_t* __restrict__ h, int64_t ldh) {
   constexpr int NW = KW * LPR;
   constexpr int RPI = 64 / LPR;
   constexpr int PPI = RPI / 2;
-  const int lane = threadIdx.x & 63;
+  __shared__ __align__(16) uint32_t xs[NW][8];
+  __shared__ float cw[NW];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int kl = lane % LPR, sub = lane / LPR;
   const int half = sub / PPI, pi = sub % PPI;
   const int64_t slot = blockIdx.y;
-  const int64_t e = expert_id(ids, ids64, slot, n_exp);
+  const int64_t e = clamp_id(ids[slot], n_exp);
   const uint32_t* we = w + e * (2 * n_half) * NW;
   const int64_t a_off = e * (2 * n_half);
-  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * (PPI * U);
+  const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kSwigluWaves + wv) * (PPI * U);
 
-  uint32_t wv[U][KW];
+  uint32_t wv_[U][KW];
   float a[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     int64_t i = i0 + u * PPI + pi;
     i = i < n_half ? i : n_half - 1;
     const int64_t row = i + half * n_half;
-    load_words_v<KW>(we + row * NW + kl * KW, wv[u]);
+    load_words_v<KW>(we + row * NW + kl * KW, wv_[u]);
     a[u] = ld_t<ADT>(alpha, a_off + row);
   }
-  XSlice<KW> xs;
-  xs.load(x + (slot / topk) * ldx, kl);
-  xs.finish();
+  MA_ISSUE_FENCE();
+  stage_row(x + (slot / topk) * ldx, NW, xs, cw);
+  __syncthreads();
+  XSlice<KW> xsl;
+  slice_from_lds<KW>(xs, cw, kl, xsl);
   const ExpandConsts kc;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const float v = group_sum<LPR>(slice_dot<KW>(wv[u], xs, kc) * a[u]);
+    const float v = group_sum<LPR>(slice_dot<KW>(wv_[u], xsl, kc) * a[u]);
     const float g = __shfl(v, lane + PPI * LPR, 64);
     const int64_t i = i0 + u * PPI + pi;
     if (half == 0 && kl == 0 && i < n_half) h[slot * ldh + i] = f32_to_bf16(swiglu(v, g));
@@ -80,14 +133,14 @@ template <int KW, int LPR, int U, int ADT>
 __global__ __launch_bounds__(64) void k_egemv_fast(
     const uint16_t* __restrict__ x, int64_t ldx, int64_t x_div,
     const uint32_t* __restrict__ w, int64_t n_out,
-    const void* __restrict__ alpha, const void* __restrict__ ids, int ids64, int64_t n_exp,
+    const void* __restrict__ alpha, const int32_t* __restrict__ ids, int64_t n_exp,
     uint16_t* __restrict__ y, int64_t ldy) {
   constexpr int NW = KW * LPR;
   constexpr int RPI = 64 / LPR;
   const int lane = threadIdx.x & 63;
   const int kl = lane % LPR, sub = lane / LPR;
   const int64_t slot = blockIdx.y;
-  const int64_t e = expert_id(ids, ids64, slot, n_exp);
+  const int64_t e = clamp_id(ids[slot], n_exp);
   const uint32_t* we = w + e * n_out * NW;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * (RPI * U);
   uint32_t wv[U][KW];
@@ -101,6 +154,7 @@ __global__ __launch_bounds__(64) void k_egemv_fast(
   }
   XSlice<KW> xs;
   xs.load(x + (slot / x_div) * ldx, kl);
+  MA_ISSUE_FENCE();
   xs.finish();
   const ExpandConsts kc;
 #pragma unroll
@@ -113,57 +167,73 @@ __global__ __launch_bounds__(64) void k_egemv_fast(
 
 // ---------------------------------------------------------------------------
 // Fast down projection + top-k weighted combine (+ residual), float32 until
-// the single store.  One token per grid row; the slots are walked in order.
+// the single store.  A workgroup owns RPI output rows of one token; its 4
+// waves split the TK slots (wave w takes slots w, w + 4, ...), every lane
+// loads its own K slice of each slot's activations and weights up front, and
+// the waves' partial sums meet in LDS.
 // ---------------------------------------------------------------------------
-template <int KW, int LPR, int U, int ADT>
-__global__ __launch_bounds__(64) void k_down_sum_fast(
+constexpr int kDownWaves = 8;
+
+template <int KW, int LPR, int TK, int U, int ADT>
+__global__ __launch_bounds__(64 * kDownWaves) void k_down_sum_fast(
     const uint16_t* __restrict__ x, int64_t ldx,
     const uint32_t* __restrict__ w, int64_t n_out,
-    const void* __restrict__ alpha, const void* __restrict__ ids, int ids64, int64_t n_exp,
+    const void* __restrict__ alpha, const int32_t* __restrict__ ids, int64_t n_exp,
     const float* __restrict__ wts, const void* __restrict__ res, int res_dt,
-    int64_t topk, uint16_t* __restrict__ y, int64_t ldy) {
+    uint16_t* __restrict__ y, int64_t ldy) {
   constexpr int NW = KW * LPR;
   constexpr int RPI = 64 / LPR;
+  constexpr int SPW = TK >= kDownWaves ? TK / kDownWaves : 1;  // slots per wave
+  constexpr int RPB = RPI * U;                                  // rows per workgroup
+  __shared__ float part[kDownWaves][RPB];
   const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kl = lane % LPR, sub = lane / LPR;
   const int64_t t = blockIdx.y;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * (RPI * U);
-  int64_t rr[U];
+  const int64_t rbase = static_cast<int64_t>(blockIdx.x) * RPB;
+  uint32_t wd[SPW][U][KW];
+  float a[SPW][U], wj[SPW];
+  XSlice<KW> xs[SPW];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t r = r0 + u * RPI + sub;
-    rr[u] = r < n_out ? r : n_out - 1;
-  }
-  float out[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) out[u] = 0.f;
-  const ExpandConsts kc;
-  for (int64_t j = 0; j < topk; ++j) {
-    const int64_t s = t * topk + j;
-    const int64_t e = expert_id(ids, ids64, s, n_exp);
-    const float wj = wts[s];
-    const uint32_t* we = w + e * n_out * NW;
-    uint32_t wv[U][KW];
-    float a[U];
+  for (int q = 0; q < SPW; ++q) {
+    const int j = wv + kDownWaves * q;
+    const int jj = j < TK ? j : 0;  // idle waves (TK < waves) read slot 0 and add nothing
+    const int64_t e = clamp_id(ids[t * TK + jj], n_exp);
+    wj[q] = j < TK ? wts[t * TK + jj] : 0.f;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      load_words_v<KW>(we + rr[u] * NW + kl * KW, wv[u]);
-      a[u] = ld_t<ADT>(alpha, e * n_out + rr[u]);
+      int64_t r = rbase + u * RPI + sub;
+      r = r < n_out ? r : n_out - 1;
+      load_words_v<KW>(w + (e * n_out + r) * NW + kl * KW, wd[q][u]);
+      a[q][u] = ld_t<ADT>(alpha, e * n_out + r);
     }
-    XSlice<KW> xs;
-    xs.load(x + s * ldx, kl);
-    xs.finish();
+    xs[q].load(x + (t * TK + jj) * ldx, kl);
+  }
+  const int64_t ro = rbase + threadIdx.x;
+  float resv = 0.f;
+  if (res && threadIdx.x < RPB && ro < n_out) resv = ld_f(res, res_dt, t * n_out + ro);
+  MA_ISSUE_FENCE();
+  const ExpandConsts kc;
+  float acc[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) out[u] += wj * group_sum<LPR>(slice_dot<KW>(wv[u], xs, kc) * a[u]);
+  for (int u = 0; u < U; ++u) acc[u] = 0.f;
+#pragma unroll
+  for (int q = 0; q < SPW; ++q) {
+    xs[q].finish();
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[u] += slice_dot<KW>(wd[q][u], xs[q], kc) * (wj[q] * a[q][u]);
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int64_t r = r0 + u * RPI + sub;
-    if (kl == 0 && r < n_out) {
-      float v = out[u];
-      if (res) v += ld_f(res, res_dt, t * n_out + r);
-      y[t * ldy + r] = f32_to_bf16(v);
-    }
+    const float v = group_sum<LPR>(acc[u]);
+    if (kl == 0) part[wv][u * RPI + sub] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < RPB && ro < n_out) {
+    float v = resv;
+#pragma unroll
+    for (int ww = 0; ww < kDownWaves; ++ww) v += part[ww][threadIdx.x];
+    y[t * ldy + ro] = f32_to_bf16(v);
   }
 }
 
@@ -238,6 +308,8 @@ __global__ __launch_bounds__(256) void k_down_sum_generic(
 // Host dispatch.
 // ---------------------------------------------------------------------------
 #define MA_EXPERT_SHAPES(X) X(32, 4) X(32, 8) X(32, 2) X(32, 1) X(32, 3) X(32, 5) X(16, 3) X(16, 1) X(8, 1)
+// down projections: K = intermediate size (768 -> 48 words; 512 -> 32; 128 -> 8)
+#define MA_DOWN_SHAPES(X) X(16, 3) X(32, 1) X(16, 1) X(8, 1) X(32, 2)
 
 static bool fast_shape(int64_t nwords, int& lpr, int& kw) {
 #define MA_PICK(L, K) \
@@ -250,8 +322,8 @@ static bool fast_shape(int64_t nwords, int& lpr, int& kw) {
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 static bool fast_ok(const void* x, int x_dt, int64_t ldx, const uint32_t* w, int64_t nwords,
-                    int kn, int a_dt, int& lpr, int& kw) {
-  if (x_dt != MA_BF16 || kn || (a_dt != MA_BF16 && a_dt != MA_F32)) return false;
+                    int kn, int a_dt, int ids64, int& lpr, int& kw) {
+  if (x_dt != MA_BF16 || kn || ids64 || (a_dt != MA_BF16 && a_dt != MA_F32)) return false;
   if (!fast_shape(nwords, lpr, kw)) return false;
   const uintptr_t wa = (kw % 4 == 0) ? 16 : (kw % 2 == 0) ? 8 : 4;
   return aligned16(x) && (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(w) % wa) == 0;
@@ -273,20 +345,22 @@ extern "C" int ma_ternary_expert_swiglu(const void* x, int x_dtype, int64_t ldx,
   if (slots == 0 || n_half == 0) return MA_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   int lpr = 0, kw = 0;
-  if (fast_ok(x, x_dtype, ldx, packed, nwords, packed_kn, alpha_dtype, lpr, kw)) {
-    constexpr int U = 4;
+  if (fast_ok(x, x_dtype, ldx, packed, nwords, packed_kn, alpha_dtype, ids_is_int64, lpr, kw) &&
+      nwords <= kMaxStageWords) {
+    constexpr int U = 3;
 #define MA_LAUNCH(L, K)                                                                        \
   if (lpr == L && kw == K) {                                                                   \
     constexpr int PPI = (64 / L) / 2;                                                          \
-    dim3 grid(static_cast<unsigned>(cdiv(n_half, PPI * U)), static_cast<unsigned>(slots));    \
+    dim3 grid(static_cast<unsigned>(cdiv(n_half, kSwigluWaves * PPI * U)),                     \
+              static_cast<unsigned>(slots));                                                   \
     if (alpha_dtype == MA_BF16)                                                                \
-      hipLaunchKernelGGL((k_swiglu_fast<K, L, U, MA_BF16>), grid, dim3(64), 0, s,              \
+      hipLaunchKernelGGL((k_swiglu_fast<K, L, U, MA_BF16>), grid, dim3(64 * kSwigluWaves), 0, s, \
                          static_cast<const uint16_t*>(x), ldx, top_k, packed, n_half,          \
-                         row_alpha, ids, ids_is_int64, n_experts, static_cast<uint16_t*>(h), ldh);        \
+                         row_alpha, static_cast<const int32_t*>(ids), n_experts, static_cast<uint16_t*>(h), ldh);        \
     else                                                                                       \
-      hipLaunchKernelGGL((k_swiglu_fast<K, L, U, MA_F32>), grid, dim3(64), 0, s,               \
+      hipLaunchKernelGGL((k_swiglu_fast<K, L, U, MA_F32>), grid, dim3(64 * kSwigluWaves), 0, s, \
                          static_cast<const uint16_t*>(x), ldx, top_k, packed, n_half,          \
-                         row_alpha, ids, ids_is_int64, n_experts, static_cast<uint16_t*>(h), ldh);        \
+                         row_alpha, static_cast<const int32_t*>(ids), n_experts, static_cast<uint16_t*>(h), ldh);        \
     return check_launch("ternary_expert_swiglu");                                             \
   }
     MA_EXPERT_SHAPES(MA_LAUNCH)
@@ -309,7 +383,7 @@ extern "C" int ma_ternary_expert_gemv(const void* x, int x_dtype, int64_t ldx, i
   if (n_slots == 0 || n_out == 0) return MA_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   int lpr = 0, kw = 0;
-  if (fast_ok(x, x_dtype, ldx, packed, nwords, packed_kn, alpha_dtype, lpr, kw)) {
+  if (fast_ok(x, x_dtype, ldx, packed, nwords, packed_kn, alpha_dtype, ids_is_int64, lpr, kw)) {
     constexpr int U = 2;
 #define MA_LAUNCH(L, K)                                                                        \
   if (lpr == L && kw == K) {                                                                   \
@@ -317,11 +391,11 @@ extern "C" int ma_ternary_expert_gemv(const void* x, int x_dtype, int64_t ldx, i
     if (alpha_dtype == MA_BF16)                                                                \
       hipLaunchKernelGGL((k_egemv_fast<K, L, U, MA_BF16>), grid, dim3(64), 0, s,               \
                          static_cast<const uint16_t*>(x), ldx, x_div, packed, n_out,           \
-                         row_alpha, ids, ids_is_int64, n_experts, static_cast<uint16_t*>(y), ldy);        \
+                         row_alpha, static_cast<const int32_t*>(ids), n_experts, static_cast<uint16_t*>(y), ldy);        \
     else                                                                                       \
       hipLaunchKernelGGL((k_egemv_fast<K, L, U, MA_F32>), grid, dim3(64), 0, s,                \
                          static_cast<const uint16_t*>(x), ldx, x_div, packed, n_out,           \
-                         row_alpha, ids, ids_is_int64, n_experts, static_cast<uint16_t*>(y), ldy);        \
+                         row_alpha, static_cast<const int32_t*>(ids), n_experts, static_cast<uint16_t*>(y), ldy);        \
     return check_launch("ternary_expert_gemv");                                               \
   }
     MA_EXPERT_SHAPES(MA_LAUNCH)
@@ -347,25 +421,29 @@ extern "C" int ma_ternary_expert_down_sum(const void* x, int x_dtype, int64_t ld
   if (tokens == 0 || n_out == 0) return MA_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   int lpr = 0, kw = 0;
-  if (fast_ok(x, x_dtype, ldx, packed, nwords, packed_kn, alpha_dtype, lpr, kw)) {
-    constexpr int U = 2;
-#define MA_LAUNCH(L, K)                                                                        \
-  if (lpr == L && kw == K) {                                                                   \
+  const bool tk_ok = top_k == 8 || top_k == 4 || top_k == 2 || top_k == 1;
+  if (tk_ok && fast_ok(x, x_dtype, ldx, packed, nwords, packed_kn, alpha_dtype, ids_is_int64, lpr, kw)) {
+#define MA_LAUNCH_TK(L, K, TK)                                                                 \
+  if (lpr == L && kw == K && top_k == TK) {                                                    \
+    constexpr int U = 2;                                                                       \
     dim3 grid(static_cast<unsigned>(cdiv(n_out, (64 / L) * U)), static_cast<unsigned>(tokens)); \
+    const auto* xb = static_cast<const uint16_t*>(x);                                          \
+    const auto* ib = static_cast<const int32_t*>(ids);                                         \
+    auto* yb = static_cast<uint16_t*>(y);                                                      \
     if (alpha_dtype == MA_BF16)                                                                \
-      hipLaunchKernelGGL((k_down_sum_fast<K, L, U, MA_BF16>), grid, dim3(64), 0, s,            \
-                         static_cast<const uint16_t*>(x), ldx, packed, n_out, row_alpha, ids,  \
-                         ids_is_int64, n_experts, topk_weight, residual, residual_dtype, top_k,           \
-                         static_cast<uint16_t*>(y), ldy);                                      \
+      hipLaunchKernelGGL((k_down_sum_fast<K, L, TK, U, MA_BF16>), grid, dim3(64 * kDownWaves), 0, s, xb, ldx, \
+                         packed, n_out, row_alpha, ib, n_experts, topk_weight, residual,       \
+                         residual_dtype, yb, ldy);                                             \
     else                                                                                       \
-      hipLaunchKernelGGL((k_down_sum_fast<K, L, U, MA_F32>), grid, dim3(64), 0, s,             \
-                         static_cast<const uint16_t*>(x), ldx, packed, n_out, row_alpha, ids,  \
-                         ids_is_int64, n_experts, topk_weight, residual, residual_dtype, top_k,           \
-                         static_cast<uint16_t*>(y), ldy);                                      \
+      hipLaunchKernelGGL((k_down_sum_fast<K, L, TK, U, MA_F32>), grid, dim3(64 * kDownWaves), 0, s, xb, ldx, \
+                         packed, n_out, row_alpha, ib, n_experts, topk_weight, residual,       \
+                         residual_dtype, yb, ldy);                                             \
     return check_launch("ternary_expert_down_sum");                                           \
   }
-    MA_EXPERT_SHAPES(MA_LAUNCH)
+#define MA_LAUNCH(L, K) MA_LAUNCH_TK(L, K, 8) MA_LAUNCH_TK(L, K, 4) MA_LAUNCH_TK(L, K, 2) MA_LAUNCH_TK(L, K, 1)
+    MA_DOWN_SHAPES(MA_LAUNCH)
 #undef MA_LAUNCH
+#undef MA_LAUNCH_TK
   }
   dim3 grid(static_cast<unsigned>(cdiv(n_out, 4)), static_cast<unsigned>(tokens));
   hipLaunchKernelGGL(k_down_sum_generic, grid, dim3(256), 0, s, x, x_dtype, ldx, packed, n_out,

@@ -3,14 +3,149 @@
 // Semantics of reference src/maple_run/kernels/router.py:39-126: float32
 // logits (+ this build's optional bias), p = exp(l - max) / sum, k passes of
 // argmax with the winner masked out (descending; ties to the lowest index),
-// w_j = p_j / (sum p_top + 1e-20).
+// w_j = p_j / (sum p_top + 1e-20).  Products are bf16 x bf16 summed by
+// v_dot2_f32_bf16: exact products, float32 accumulation.
 //
-// Two launches like the reference: one wave per (token, expert) logit with
-// bf16 x bf16 products summed by v_dot2_f32_bf16 (exact products, float32
-// accumulation), then one wave per token for softmax and top-k.
+// Decode (tokens <= kFusedMaxTokens, bf16): ONE launch.  Workgroup (e, t)
+// computes logit e of token t and publishes it as a 64-bit (value, tag = 1)
+// word; workgroup (0, t) waits for the E tagged words of its token, clears
+// them back to 0 and runs softmax + top-k.  The workspace therefore starts
+// and ends every call all-zero (it must be zero-filled once when allocated),
+// no atomic read-modify-write is used, and calls sharing a workspace must not
+// overlap.  The wait is bounded (about 0.2 s): on timeout the kernel records
+// an error in the workspace instead of hanging.
+//
+// Otherwise: two launches, like the reference (logits kernel, then top-k).
 #include "common.h"
 
 namespace ma {
+
+constexpr int kRouterMaxPerLane = 16;  // up to 1024 experts
+constexpr int64_t kFusedMaxTokens = 16;
+constexpr int64_t kFusedMaxExperts = 256;
+
+// Workspace layout of the fused path (uint32 words):
+//   [1]      error flag (1 = a wait timed out)
+//   [64 ...] tagged logits, uint64 [tokens][E]: (1 << 32) | float bits
+constexpr size_t kWsHeader = 64 * sizeof(uint32_t);
+
+__device__ __forceinline__ float router_dot(const uint16_t* __restrict__ x,
+                                            const uint16_t* __restrict__ w, int64_t k_in,
+                                            int tid, int nthreads) {
+  const uint4* xp = reinterpret_cast<const uint4*>(x);
+  const uint4* wp = reinterpret_cast<const uint4*>(w);
+  const int64_t n8 = k_in / 8;
+  float a0 = 0.f, a1 = 0.f;
+  for (int64_t i = tid; i < n8; i += nthreads) {
+    const uint4 a = xp[i], b = wp[i];
+    a0 = dot2(a.x, b.x, a0);
+    a1 = dot2(a.y, b.y, a1);
+    a0 = dot2(a.z, b.z, a0);
+    a1 = dot2(a.w, b.w, a1);
+  }
+  return a0 + a1;
+}
+
+// Softmax over the wave-held logits p[i] (expert lane + 64 i), then top-k by
+// rank: the rank of an expert is the number of experts with a larger
+// probability, or an equal one at a lower index, so rank order is the
+// reference's descending order with ties to the lowest index.  Ranks come
+// from v_readlane broadcasts (no LDS round trips).  One full wave runs this.
+template <int PER>
+__device__ __forceinline__ void softmax_topk(float (&p)[PER], int64_t n_exp, int top_k,
+                                             int32_t* __restrict__ ids,
+                                             float* __restrict__ wts) {
+  const int lane = threadIdx.x & 63;
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) m = fmaxf(m, p[i]);
+  m = wave_max(m);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t e = lane + 64 * i;
+    p[i] = e < n_exp ? expf(p[i] - m) : 0.f;
+    sum += p[i];
+  }
+  sum = group_sum<64>(sum);
+  const float inv_sum = 1.0f / sum;
+  int rank[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t e = lane + 64 * i;
+    p[i] = e < n_exp ? p[i] * inv_sum : -INFINITY;
+    rank[i] = 0;
+  }
+#pragma unroll
+  for (int im = 0; im < PER; ++im) {
+    for (int src = 0; src < 64; ++src) {
+      const float q = lane_bcast(p[im], src);
+      const int em = src + 64 * im;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int e = lane + 64 * i;
+        rank[i] += (q > p[i]) || (q == p[i] && em < e);
+      }
+    }
+  }
+  float sel = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) sel += rank[i] < top_k ? p[i] : 0.f;
+  const float inv_total = 1.0f / (group_sum<64>(sel) + 1e-20f);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    if (e < n_exp && rank[i] < top_k) {
+      ids[rank[i]] = e;
+      wts[rank[i]] = p[i] * inv_total;
+    }
+  }
+}
+
+template <int PER>
+__global__ __launch_bounds__(256) void k_router_fused(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
+    int64_t n_exp, int64_t k_in, const float* __restrict__ bias, int top_k,
+    int32_t* __restrict__ ids, float* __restrict__ wts, uint32_t* __restrict__ ws) {
+  __shared__ float red[4];
+  const int64_t e = blockIdx.x, t = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  uint64_t* tagged = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(ws) + kWsHeader);
+
+  float s = router_dot(x + t * ldx, w + e * k_in, k_in, tid, 256);
+  s = group_sum<64>(s);
+  if (lane == 0) red[wv] = s;
+  __syncthreads();
+  if (tid == 0) {
+    const float logit = (red[0] + red[1]) + (red[2] + red[3]) + (bias ? bias[e] : 0.f);
+    const uint64_t word = (1ull << 32) | __float_as_uint(logit);
+    __hip_atomic_store(&tagged[t * n_exp + e], word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (e != 0 || wv != 0) return;
+
+  // Workgroup (0, t), wave 0: gather the E tagged logits of token t.
+  float p[PER];
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  bool timed_out = false;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t ee = lane + 64 * i;
+    p[i] = -INFINITY;
+    if (ee < n_exp) {
+      uint64_t v = __hip_atomic_load(&tagged[t * n_exp + ee], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      while ((v >> 32) != 1ull && !timed_out) {
+        __builtin_amdgcn_s_sleep(2);
+        v = __hip_atomic_load(&tagged[t * n_exp + ee], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > 20000000ull;  // 0.2 s at 100 MHz
+      }
+      p[i] = __uint_as_float(static_cast<uint32_t>(v));
+      __hip_atomic_store(&tagged[t * n_exp + ee], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (__ballot(timed_out) && lane == 0)
+    __hip_atomic_store(&ws[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  softmax_topk<PER>(p, n_exp, top_k, ids + t * top_k, wts + t * top_k);
+}
 
 __global__ __launch_bounds__(256) void k_router_logits(
     const void* __restrict__ x, int x_dt, int64_t ldx, const void* __restrict__ w, int w_dt,
@@ -20,100 +155,39 @@ __global__ __launch_bounds__(256) void k_router_logits(
   const int64_t e = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int64_t t = blockIdx.y;
   if (e >= n_exp) return;  // uniform per wave
-  float a0 = 0.f, a1 = 0.f;
+  float a = 0.f;
   if (fast) {
-    const uint4* xp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + t * ldx);
-    const uint4* wp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(w) + e * k_in);
-    const int64_t n8 = k_in / 8;
-#pragma unroll 4
-    for (int64_t i = lane; i < n8; i += 64) {
-      const uint4 a = xp[i], b = wp[i];
-      a0 = dot2(a.x, b.x, a0);
-      a1 = dot2(a.y, b.y, a1);
-      a0 = dot2(a.z, b.z, a0);
-      a1 = dot2(a.w, b.w, a1);
-    }
+    a = router_dot(static_cast<const uint16_t*>(x) + t * ldx,
+                   static_cast<const uint16_t*>(w) + e * k_in, k_in, lane, 64);
   } else {
     for (int64_t k = lane; k < k_in; k += 64)
-      a0 += ld_f(x, x_dt, t * ldx + k) * ld_f(w, w_dt, e * k_in + k);
+      a += ld_f(x, x_dt, t * ldx + k) * ld_f(w, w_dt, e * k_in + k);
   }
-  const float s = group_sum<64>(a0 + a1);
+  const float s = group_sum<64>(a);
   if (lane == 0) logits[t * n_exp + e] = s + (bias ? bias[e] : 0.f);
 }
 
-// Wave arg-max of (value, index): larger value wins, ties to the lower index.
-__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float ov = __shfl_xor(v, off, 64);
-    const int oi = __shfl_xor(idx, off, 64);
-    if (ov > v || (ov == v && oi < idx)) {
-      v = ov;
-      idx = oi;
-    }
-  }
-}
-
-constexpr int kRouterMaxPerLane = 16;  // up to 1024 experts
-
+template <int PER>
 __global__ __launch_bounds__(64) void k_router_topk(const float* __restrict__ logits,
                                                     int64_t n_exp, int top_k,
                                                     int32_t* __restrict__ ids,
                                                     float* __restrict__ wts) {
   const int lane = threadIdx.x;
   const int64_t t = blockIdx.x;
-  const float* l = logits + t * n_exp;
-  float p[kRouterMaxPerLane];
-  float m = -INFINITY;
+  float p[PER];
 #pragma unroll
-  for (int i = 0; i < kRouterMaxPerLane; ++i) {
+  for (int i = 0; i < PER; ++i) {
     const int64_t e = lane + 64 * i;
-    p[i] = e < n_exp ? l[e] : -INFINITY;
-    m = fmaxf(m, p[i]);
+    p[i] = e < n_exp ? logits[t * n_exp + e] : -INFINITY;
   }
-  m = wave_max(m);
-  float sum = 0.f;
-#pragma unroll
-  for (int i = 0; i < kRouterMaxPerLane; ++i) {
-    const int64_t e = lane + 64 * i;
-    p[i] = e < n_exp ? expf(p[i] - m) : 0.f;
-    sum += p[i];
-  }
-  sum = group_sum<64>(sum);
-  const float inv_sum = 1.0f / sum;
-#pragma unroll
-  for (int i = 0; i < kRouterMaxPerLane; ++i) {
-    const int64_t e = lane + 64 * i;
-    p[i] = e < n_exp ? p[i] * inv_sum : -INFINITY;
-  }
-  float total = 0.f;
-  float mine = 0.f;  // lane j < top_k keeps the j-th pick
-  int mine_id = 0;
-  for (int j = 0; j < top_k; ++j) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < kRouterMaxPerLane; ++i) {
-      const int e = lane + 64 * i;
-      if (p[i] > bv) {
-        bv = p[i];
-        bi = e;
-      }
-    }
-    wave_argmax(bv, bi);
-    total += bv;
-    if (lane == j) {
-      mine = bv;
-      mine_id = bi;
-    }
-#pragma unroll
-    for (int i = 0; i < kRouterMaxPerLane; ++i)
-      if (lane + 64 * i == bi) p[i] = -INFINITY;
-  }
-  if (lane < top_k) {
-    ids[t * top_k + lane] = mine_id;
-    wts[t * top_k + lane] = mine * (1.0f / (total + 1e-20f));
-  }
+  softmax_topk<PER>(p, n_exp, top_k, ids + t * top_k, wts + t * top_k);
+}
+
+static bool fused_ok(int x_dtype, int w_dtype, int64_t tokens, int64_t n_exp, int64_t k_in,
+                     int64_t ldx, const void* x, const void* w) {
+  return x_dtype == MA_BF16 && w_dtype == MA_BF16 && tokens <= kFusedMaxTokens &&
+         n_exp <= kFusedMaxExperts && (k_in % 8) == 0 && (ldx % 8) == 0 &&
+         ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15u) == 0;
 }
 
 }  // namespace ma
@@ -121,7 +195,12 @@ __global__ __launch_bounds__(64) void k_router_topk(const float* __restrict__ lo
 using namespace ma;
 
 extern "C" size_t ma_router_workspace_bytes(int64_t tokens, int64_t n_experts) {
-  return static_cast<size_t>(tokens > 0 ? tokens : 0) * static_cast<size_t>(n_experts > 0 ? n_experts : 0) * sizeof(float);
+  const size_t t = static_cast<size_t>(tokens > 0 ? tokens : 0);
+  const size_t e = static_cast<size_t>(n_experts > 0 ? n_experts : 0);
+  // The fused path's tagged region comes first (it must stay zero between
+  // calls); the two-pass path's float32 logits follow it.
+  const size_t fused = kWsHeader + kFusedMaxTokens * kFusedMaxExperts * sizeof(uint64_t);
+  return fused + t * e * sizeof(float);
 }
 
 extern "C" int ma_router_topk(const void* x, int x_dtype, int64_t tokens, int64_t ldx,
@@ -137,16 +216,37 @@ extern "C" int ma_router_topk(const void* x, int x_dtype, int64_t tokens, int64_
   if (n_experts > 64 * kRouterMaxPerLane)
     return fail(MA_EVALUE, "router_topk supports at most %d experts", 64 * kRouterMaxPerLane);
   if (tokens == 0) return MA_OK;
-  if (workspace_bytes < ma_router_workspace_bytes(tokens, n_experts))
+  if (!workspace || workspace_bytes < ma_router_workspace_bytes(tokens, n_experts))
     return fail(MA_EVALUE, "router_topk: workspace too small");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  float* logits = static_cast<float*>(workspace);
+  if (fused_ok(x_dtype, w_dtype, tokens, n_experts, k_in, ldx, x, gate_weight)) {
+    dim3 grid(static_cast<unsigned>(n_experts), static_cast<unsigned>(tokens));
+    const auto* xb = static_cast<const uint16_t*>(x);
+    const auto* wb = static_cast<const uint16_t*>(gate_weight);
+    auto* wsp = static_cast<uint32_t*>(workspace);
+    if (n_experts <= 64)
+      hipLaunchKernelGGL(k_router_fused<1>, grid, dim3(256), 0, s, xb, ldx, wb, n_experts, k_in,
+                         bias, top_k, ids, weights, wsp);
+    else
+      hipLaunchKernelGGL(k_router_fused<4>, grid, dim3(256), 0, s, xb, ldx, wb, n_experts, k_in,
+                         bias, top_k, ids, weights, wsp);
+    return check_launch("router_topk");
+  }
+  float* logits = reinterpret_cast<float*>(static_cast<char*>(workspace) + kWsHeader +
+                                           kFusedMaxTokens * kFusedMaxExperts * sizeof(uint64_t));
   const int fast = x_dtype == MA_BF16 && w_dtype == MA_BF16 && (k_in % 8) == 0 &&
-                   (ldx % 8) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gate_weight)) & 15u) == 0;
+                   (ldx % 8) == 0 &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gate_weight)) & 15u) == 0;
   dim3 g1(static_cast<unsigned>(cdiv(n_experts, 4)), static_cast<unsigned>(tokens));
   hipLaunchKernelGGL(k_router_logits, g1, dim3(256), 0, s, x, x_dtype, ldx, gate_weight, w_dtype,
                      n_experts, k_in, bias, logits, fast);
-  hipLaunchKernelGGL(k_router_topk, dim3(static_cast<unsigned>(tokens)), dim3(64), 0, s, logits,
-                     n_experts, top_k, ids, weights);
+  const dim3 gt(static_cast<unsigned>(tokens));
+  if (n_experts <= 64)
+    hipLaunchKernelGGL(k_router_topk<1>, gt, dim3(64), 0, s, logits, n_experts, top_k, ids, weights);
+  else if (n_experts <= 256)
+    hipLaunchKernelGGL(k_router_topk<4>, gt, dim3(64), 0, s, logits, n_experts, top_k, ids, weights);
+  else
+    hipLaunchKernelGGL(k_router_topk<kRouterMaxPerLane>, gt, dim3(64), 0, s, logits, n_experts,
+                       top_k, ids, weights);
   return check_launch("router_topk");
 }

@@ -68,6 +68,7 @@ __global__ __launch_bounds__(64) void k_rtn4_fast(
     for (int i = 0; i < KW; ++i)
       xr[bt][i] = reinterpret_cast<const uint4*>(x + b * ldx + static_cast<int64_t>(kl * KW + i) * 8)[0];
   }
+  MA_ISSUE_FENCE();
   uint32_t xp[BT][KW][4];
   float xsum[BT];
 #pragma unroll

@@ -105,6 +105,7 @@ __global__ __launch_bounds__(64) void k_tgemv_fast(
 #pragma unroll
       for (int q = 0; q < 16; ++q) rmsv[i][q] = rms_w[static_cast<int64_t>(kl * KW + i) * 16 + q];
   }
+  MA_ISSUE_FENCE();
 
 #pragma unroll
   for (int bt = 0; bt < BT; ++bt) {

@@ -26,9 +26,10 @@ def _expert_nk(packed_weight: torch.Tensor, packed_kn: bool) -> tuple[int, int, 
 
 
 def _ids_arg(ids: torch.Tensor) -> tuple[torch.Tensor, int]:
-    if ids.dtype not in (torch.int32, torch.int64):
+    # The kernels' fast paths read int32 ids (the router's output dtype).
+    if ids.dtype != torch.int32:
         ids = ids.to(torch.int32)
-    return ids.contiguous(), int(ids.dtype == torch.int64)
+    return ids.contiguous(), 0
 
 
 def _rows(t: torch.Tensor, k: int) -> torch.Tensor:

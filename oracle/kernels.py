@@ -25,7 +25,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .pack import dequantize_rtn, ternary_values, unpack_4bit
+from .pack import dequantize_rtn, ternary_values, unpack_2bit, unpack_4bit
 
 MLP_CLAMP = 7.0  # ternary_expert.py:237, model.py:35
 
@@ -248,3 +248,34 @@ def add_rms_norm(x, y, weight, eps=1e-6):
     """``s = x + y``; returns ``(s, rms_norm(s))`` (``fused_norm.py:31-56``)."""
     s = np.asarray(x, np.float64) + np.asarray(y, np.float64)
     return s, rms_norm(s, weight, eps)
+
+
+def moe_layer_cpu_fp32(x, gate_weight, up_gate_packed, up_gate_alpha, down_packed, down_alpha, top_k):
+    """The reference's CPU oracle path for one MoE layer, float32 throughout:
+    router ``linear -> softmax -> topk -> renorm`` (``tests/test_model.py:225-229``),
+    then for every selected expert NumPy ``unpack_2bit`` -> ``(code - 1) * alpha``
+    -> matmul (``tests/test_ternary_gemv.py:24-25,83-86``; the loop of
+    ``tests/test_model.py:230-241``).  The unpack is part of every call.
+    Used as the CPU baseline; returns ``[T, H]`` float32.
+    """
+    x = np.asarray(x, np.float32).reshape(-1, np.shape(gate_weight)[1])
+    logits = x @ np.asarray(gate_weight, np.float32).T
+    logits -= logits.max(axis=1, keepdims=True)
+    p = np.exp(logits)
+    p /= p.sum(axis=1, keepdims=True)
+    ids = np.argsort(-p, axis=1, kind="stable")[:, :top_k]
+    top = np.take_along_axis(p, ids, axis=1)
+    wts = top / (top.sum(axis=1, keepdims=True) + np.float32(1e-20))
+    inter = np.shape(up_gate_packed)[1] // 2
+    y = np.zeros_like(x)
+    for t in range(x.shape[0]):
+        for j in range(top_k):
+            e = int(ids[t, j])
+            wug = (unpack_2bit(up_gate_packed[e]).astype(np.float32) - 1.0) * np.asarray(up_gate_alpha[e], np.float32)[:, None]
+            ug = wug @ x[t]
+            up = np.clip(ug[:inter], -MLP_CLAMP, MLP_CLAMP)
+            gate = np.minimum(ug[inter:], MLP_CLAMP)
+            h = up * gate / (1.0 + np.exp(-gate))
+            wd = (unpack_2bit(down_packed[e]).astype(np.float32) - 1.0) * np.asarray(down_alpha[e], np.float32)[:, None]
+            y[t] += wts[t, j] * (wd @ h)
+    return y
