@@ -84,6 +84,72 @@ def read_traffic(kernel: str):
     return float(m.group(1)) if m else None
 
 
+def time_graph(g, steps: int, warmup: int) -> float:
+    """Seconds per replay of graph ``g`` (HIP events on the current stream)."""
+    import torch
+
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(True), torch.cuda.Event(True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / steps
+
+
+def extra_workloads(layers, dev, steps: int) -> dict:
+    """The other configurations: one GEMV, Zipf-routed batches, a prefill chunk."""
+    import torch
+
+    from maple_amd import synthetic
+    from maple_amd.kernels import router_topk, ternary_gemv
+    from maple_amd.moe import moe_block
+
+    out = {}
+    # Single packed ternary GEMV, 1536 x 2048, batch 1, 1024 distinct cold copies.
+    n, k, reps = 1536, 2048, 1024
+    base = synthetic.ternary_packed((8, n, k), 77, dev)
+    ws = [base[i % 8].clone() for i in range(reps)]
+    alpha = synthetic.uniform_bf16((n,), 0.01, 0.05, 78, dev)
+    xg = synthetic.randn_bf16((1, k), 79, dev)
+    g = graph_of(lambda: [ternary_gemv(xg, ws[i], alpha) for i in range(reps)])
+    t = time_graph(g, 3, 1) / reps
+    nbytes = n * k // 4 + n * 2 + k * 2 + n * 2
+    out["gemv_1536x2048_bs1"] = {"us_per_call": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1)}
+    del ws, base, g
+    # Zipf(1.1)-routed MoE layers at 32 and 128 tokens.
+    bias = synthetic.zipf_router_bias(EXPERTS, 1.1, 1.0, seed=3).to(dev)
+    zl = [synthetic.MoELayer(l.gate_weight, l.up_gate_packed, l.up_gate_alpha, l.down_packed,
+                             l.down_alpha, bias) for l in layers]
+    for tokens in (32, 128):
+        x = synthetic.randn_bf16((tokens, HIDDEN), 1000 + tokens, dev)
+        touched = 0
+        for l in zl:
+            ids, _ = router_topk(x, l.gate_weight, TOPK, bias=l.router_bias)
+            touched += int(torch.unique(ids).numel())
+        nbytes = touched * layer_bytes()["expert"] + len(zl) * (EXPERTS * HIDDEN * 2 + tokens * HIDDEN * 4)
+        g = graph_of(lambda: [moe_block(x, l, TOPK) for l in zl])
+        t = time_graph(g, max(steps // 2, 3), 2)
+        out[f"moe_layer_zipf_T{tokens}"] = {
+            "us_per_layer": round(t * 1e6 / len(zl), 2), "GB/s": round(nbytes / t / 1e9, 1),
+            "experts_touched_per_layer": round(touched / len(zl), 1),
+            "tokens_per_s": round(tokens * len(zl) / t, 0)}
+        del g
+    # Prefill chunk: 2048 tokens through one MoE layer (grouped MFMA path).
+    tokens = 2048
+    x = synthetic.randn_bf16((tokens, HIDDEN), 2048, dev)
+    pl = zl[:4]
+    g = graph_of(lambda: [moe_block(x, l, TOPK) for l in pl])
+    t = time_graph(g, 5, 2) / len(pl)
+    flops = tokens * TOPK * (3 * 2 * INTER * HIDDEN)
+    out["moe_prefill_T2048"] = {"us_per_layer": round(t * 1e6, 1), "TFLOP/s": round(flops / t / 1e12, 1),
+                                "mfma_frac_of_2500": round(flops / t / 2.5e15, 4)}
+    return out
+
+
 def cpu_baseline(seconds: float = 12.0) -> dict:
     import numpy as np
 
@@ -127,6 +193,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -214,7 +281,12 @@ def main() -> int:
                      "bytes_per_launch": nb["swiglu_launch"],
                      "us_per_launch": round(per_launch * 1e6, 3)},
         "cpu_baseline": None,
+        "extra": None,
     }
+    if not args.no_extra:
+        log("timing the other workloads ...")
+        out["extra"] = extra_workloads(layers, dev, args.steps)
+        log(json.dumps(out["extra"]))
     if not args.no_cpu:
         log("timing the CPU baseline ...")
         out["cpu_baseline"] = cpu_baseline()

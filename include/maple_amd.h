@@ -166,6 +166,30 @@ int ma_rtn4_embedding(const void* ids, int ids_is_int64, int64_t n_ids,
                       const void* scales, int scales_dtype, const void* biases, int biases_dtype,
                       int64_t group_size, float* out, void* stream);
 
+/*
+ * Grouped MoE FFN after dispatch (batched decode and prefill), on MFMA:
+ * per expert, h = SwiGLU(up/gate GEMM) over its pairs (rounded to bf16 as the
+ * reference stores it), out = down GEMM per pair (rounded to bf16), then
+ * y[t] = sum_j w[t, j] * out[pair(t, j)] (+ residual) in float32, stored bf16.
+ * offsets / pair_ids / inverse are ma_moe_dispatch's outputs.  x is bf16
+ * [tokens, hidden]; hidden and inter must be multiples of 256; row_alpha bf16
+ * or float32.  h_out (optional, bf16 [tokens*top_k, inter], row stride ldh)
+ * receives h in slot order; y (optional) is bf16 [tokens, hidden].
+ * workspace: ma_grouped_workspace_bytes(tokens * top_k, inter, hidden).
+ * Replaces MapleSparseMoeBlock's SwiGLU -> down -> moe_reduce_add chain
+ * (src/maple_run/model.py:468-473) for token counts where experts see many
+ * tokens; the reference instead runs one program per (token, slot).
+ */
+size_t ma_grouped_workspace_bytes(int64_t n_pairs, int64_t inter, int64_t hidden);
+int ma_moe_grouped(const void* x, int64_t ldx, int64_t tokens, int64_t top_k,
+                   const uint32_t* up_gate, const void* up_gate_alpha,
+                   const uint32_t* down, const void* down_alpha, int alpha_dtype,
+                   int64_t n_experts, int64_t hidden, int64_t inter,
+                   const int32_t* offsets, const int32_t* pair_ids, const int32_t* inverse,
+                   const float* topk_weight, const void* residual, int residual_dtype,
+                   void* h_out, int64_t ldh, void* y,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,8 +40,12 @@ _SIGNATURES = {
     "ma_add_rms_norm": [_P, _P, _I, _L, _L, _P, _I, _F, _P, _P, _P],
     "ma_rtn4_gemv": [_P, _I, _L, _L, _P, _L, _L, _I, _P, _I, _P, _I, _L, _P, _L, _P],
     "ma_rtn4_embedding": [_P, _I, _L, _P, _L, _L, _P, _I, _P, _I, _L, _P, _P],
+    "ma_grouped_workspace_bytes": [_L, _L, _L],
+    "ma_moe_grouped": [_P, _L, _L, _L, _P, _P, _P, _P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _I,
+                       _P, _L, _P, _P, _Z, _P],
 }
-_RESTYPES = {"ma_last_error": ctypes.c_char_p, "ma_router_workspace_bytes": _Z}
+_RESTYPES = {"ma_last_error": ctypes.c_char_p, "ma_router_workspace_bytes": _Z,
+             "ma_grouped_workspace_bytes": _Z}
 
 _lib = None
 

@@ -141,6 +141,15 @@ __device__ __forceinline__ float prep_word_pairs(const float xs[16], uint32_t xp
   return c;
 }
 
+// SwiGLU of the reference's expert MLP (kernels/ternary_expert.py:314-318):
+// clamp(up, -7, 7) * g * sigmoid(g) with g = min(gate, 7).
+constexpr float kMlpClamp = 7.0f;
+__device__ __forceinline__ float swiglu_act(float up, float gate) {
+  up = fminf(fmaxf(up, -kMlpClamp), kMlpClamp);
+  gate = fminf(gate, kMlpClamp);
+  return up * (gate / (1.0f + expf(-gate)));
+}
+
 // ---------------------------------------------------------------------------
 // Wave-level helpers (wave64).
 // ---------------------------------------------------------------------------

@@ -12,7 +12,6 @@
 
 namespace ma {
 
-constexpr float kMlpClamp = 7.0f;  // ternary_expert.py:237
 
 // Expert id of a slot, clamped into [0, n_exp): an id outside the stack would
 // otherwise address memory outside the weights (no host-side check is possible
@@ -27,11 +26,6 @@ __device__ __forceinline__ int64_t clamp_id(int32_t e, int64_t n_exp) {
   return e < 0 ? 0 : (e >= n_exp ? n_exp - 1 : e);
 }
 
-__device__ __forceinline__ float swiglu(float up, float gate) {
-  up = fminf(fmaxf(up, -kMlpClamp), kMlpClamp);
-  gate = fminf(gate, kMlpClamp);
-  return up * (gate / (1.0f + expf(-gate)));
-}
 
 // ---------------------------------------------------------------------------
 // x' staging in LDS: one workgroup prepares the pairs of one bf16 activation
@@ -122,7 +116,7 @@ __global__ __launch_bounds__(64 * kSwigluWaves) void k_swiglu_fast(
     const float v = group_sum<LPR>(slice_dot<KW>(wv_[u], xsl, kc) * a[u]);
     const float g = __shfl(v, lane + PPI * LPR, 64);
     const int64_t i = i0 + u * PPI + pi;
-    if (half == 0 && kl == 0 && i < n_half) h[slot * ldh + i] = f32_to_bf16(swiglu(v, g));
+    if (half == 0 && kl == 0 && i < n_half) h[slot * ldh + i] = f32_to_bf16(swiglu_act(v, g));
   }
 }
 
@@ -276,7 +270,7 @@ __global__ __launch_bounds__(256) void k_expert_generic(
     const int64_t grow = row + n_out;
     const float g = row_dot_generic(x, x_dt, xoff, w, e, grow, n_rows, nwords, kn, lane) *
                     ld_f(alpha, a_dt, e * n_rows + grow);
-    out = swiglu(v, g);
+    out = swiglu_act(v, g);
   }
   if (lane == 0) st_f(y, y_dt, slot * ldy + row, out);
 }

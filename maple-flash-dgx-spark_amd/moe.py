@@ -1,21 +1,69 @@
 """The MoE FFN block on the HIP kernels (reference ``src/maple_run/model.py:448-474``).
 
 ``MapleSparseMoeBlock`` keeps the reference composition and call signature:
-router -> fused up+gate SwiGLU -> down -> top-k combine (+ residual), with no
-host sync and no per-expert Python loop.  The down projection and the combine
-run as one launch (``ternary_expert_down_sum``), which skips the reference's
-bf16 rounding of each slot's down output before the combine
-(``model.py:470-473``); the result stays within bf16 tolerance of the
-reference composition.
+router -> up+gate SwiGLU -> down -> top-k combine (+ residual), with no host
+sync and no per-expert Python loop.  Two execution plans, chosen by the token
+count alone (never by routing, which stays on the device):
+
+* decode (``tokens < GROUPED_MIN_TOKENS``): per-slot kernels, as the
+  reference does -- fused SwiGLU, then the down projection and the combine in
+  one launch (``ternary_expert_down_sum``).  That skips the reference's bf16
+  rounding of each slot's down output before the combine
+  (``model.py:470-473``); the result stays within bf16 tolerance of it.
+* batched decode / prefill: dispatch the (token, slot) pairs into per-expert
+  lists and run grouped MFMA GEMMs (``ma_moe_grouped``), so each selected
+  expert's weights are read once per tile of its tokens instead of once per
+  pair.  Rounding points match the reference (bf16 h, bf16 per-slot output,
+  float32 combine).
 """
 
 from __future__ import annotations
 
 import torch
 
+from . import _lib
+from .kernels.dispatch import moe_dispatch
 from .kernels.router import router_topk
 from .kernels.ternary_expert import ternary_expert_down_sum, ternary_expert_swiglu
 from .synthetic import MoELayer
+
+GROUPED_MIN_TOKENS = 4
+
+
+def moe_grouped(x: torch.Tensor, layer: MoELayer, ids: torch.Tensor, wts: torch.Tensor,
+                residual: torch.Tensor | None = None, *, return_h: bool = False):
+    """Dispatch + grouped MFMA SwiGLU/down + combine for ``x [T, H]`` (bf16).
+
+    Returns ``y [T, H]`` (bf16), and with ``return_h`` also ``h [T, k, I]``.
+    """
+    tokens, hidden = x.shape
+    top_k = int(ids.shape[-1])
+    inter = layer.inter
+    d = moe_dispatch(ids, layer.n_experts)
+    n_pairs = tokens * top_k
+    nbytes = int(_lib.load().ma_grouped_workspace_bytes(n_pairs, inter, hidden))
+    ws = torch.empty(nbytes, device=x.device, dtype=torch.uint8)
+    y = torch.empty(tokens, hidden, device=x.device, dtype=torch.bfloat16)
+    h = torch.empty(n_pairs, inter, device=x.device, dtype=torch.bfloat16) if return_h else None
+    res = None if residual is None else residual.reshape(tokens, hidden).contiguous()
+    xc = x.contiguous()
+    w = wts.reshape(-1).float().contiguous()
+    alpha_dt = _lib.dtype_code(layer.up_gate_alpha, "row_alpha")
+    if _lib.dtype_code(layer.down_alpha, "row_alpha") != alpha_dt:
+        raise TypeError("up_gate and down row_alpha must share a dtype")
+    _lib.call(
+        "ma_moe_grouped",
+        _lib.ptr(xc), xc.stride(0), tokens, top_k,
+        _lib.ptr(layer.up_gate_packed), _lib.ptr(layer.up_gate_alpha),
+        _lib.ptr(layer.down_packed), _lib.ptr(layer.down_alpha), alpha_dt,
+        layer.n_experts, hidden, inter,
+        _lib.ptr(d.offsets), _lib.ptr(d.pair_ids), _lib.ptr(d.inverse), _lib.ptr(w),
+        _lib.ptr(res), _lib.dtype_code(res, "residual") if res is not None else 0,
+        _lib.ptr(h), inter, _lib.ptr(y), _lib.ptr(ws), ws.numel(), _lib.stream_of(x),
+    )
+    if return_h:
+        return y, h.reshape(tokens, top_k, inter)
+    return y
 
 
 def moe_block(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tensor | None = None):
@@ -23,9 +71,13 @@ def moe_block(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
     hidden = x.shape[-1]
     xf = x.reshape(-1, hidden)
     ids, wts = router_topk(xf, layer.gate_weight, top_k, bias=layer.router_bias)
-    h = ternary_expert_swiglu(xf, layer.up_gate_packed, layer.up_gate_alpha, ids)
     res = None if residual is None else residual.reshape(-1, hidden)
-    y = ternary_expert_down_sum(h, layer.down_packed, layer.down_alpha, ids, wts, residual=res)
+    if xf.shape[0] >= GROUPED_MIN_TOKENS and xf.dtype == torch.bfloat16 \
+            and hidden % 256 == 0 and layer.inter % 256 == 0:
+        y = moe_grouped(xf, layer, ids, wts, res)
+    else:
+        h = ternary_expert_swiglu(xf, layer.up_gate_packed, layer.up_gate_alpha, ids)
+        y = ternary_expert_down_sum(h, layer.down_packed, layer.down_alpha, ids, wts, residual=res)
     return y.reshape(x.shape), ids, wts
 
 
@@ -41,12 +93,10 @@ class MapleSparseMoeBlock:
         self.moe_intermediate = moe_intermediate
         self.router_bias = router_bias
 
+    def _layer(self) -> MoELayer:
+        return MoELayer(self.gate_weight, self.up_gate.packed_weight, self.up_gate.row_alpha,
+                        self.down.packed_weight, self.down.row_alpha, self.router_bias)
+
     def __call__(self, hidden_states: torch.Tensor, residual: torch.Tensor | None = None):
-        shape = hidden_states.shape
-        hidden = shape[-1]
-        x = hidden_states.reshape(-1, hidden)
-        topk_idx, topk_weight = router_topk(x, self.gate_weight, self.top_k, bias=self.router_bias)
-        hidden_e = self.up_gate.swiglu(x, topk_idx)
-        res = None if residual is None else residual.reshape(-1, hidden)
-        y = self.down.down_sum(hidden_e, topk_idx, topk_weight, residual=res)
-        return y.view(shape)
+        y, _, _ = moe_block(hidden_states, self._layer(), self.top_k, residual)
+        return y

@@ -279,3 +279,17 @@ def moe_layer_cpu_fp32(x, gate_weight, up_gate_packed, up_gate_alpha, down_packe
             wd = (unpack_2bit(down_packed[e]).astype(np.float32) - 1.0) * np.asarray(down_alpha[e], np.float32)[:, None]
             y[t] += wts[t, j] * (wd @ h)
     return y
+
+
+def moe_experts(x, ids, wts, up_gate_packed, up_gate_alpha, down_packed, down_alpha,
+                residual=None, *, round_bf16=True):
+    """Expert half of ``model.py:468-473`` for a given routing: SwiGLU, per-slot
+    down projection and the weighted combine, with the reference's bf16
+    rounding of ``h`` and of each slot's down output.  Returns ``(y, h)``."""
+    h = ternary_expert_swiglu(x, up_gate_packed, up_gate_alpha, ids)
+    if round_bf16:
+        h = bf16_round(h).astype(np.float64)
+    eo = ternary_expert_gemv(h, down_packed, down_alpha, ids)
+    if round_bf16:
+        eo = bf16_round(eo).astype(np.float64)
+    return moe_reduce_add(eo, wts, residual), h

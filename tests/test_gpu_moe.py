@@ -1,0 +1,119 @@
+"""MoE FFN layer on the HIP kernels vs the CPU oracle (needs the GPU).
+
+Shapes are the synthetic workloads: hidden 2048, 64 experts, intermediate
+768, top-8; decode batch 1 (per-slot kernels) and 32 / 128 tokens with
+Zipf(1.1)-skewed routing plus a 2048-token prefill chunk (dispatch + grouped
+MFMA kernels).  Routing is checked against the oracle's (ids exact on rows
+without float near-ties); the expert outputs against the oracle evaluated on
+the kernel's own routing, with the reference's bf16 rounding points; the
+dispatch lists exactly.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import assert_bf16_close, np_f, np_u32, tie_safe_rows
+from maple_amd import synthetic
+from maple_amd.kernels import moe_dispatch, router_topk
+from maple_amd.moe import GROUPED_MIN_TOKENS, moe_block, moe_grouped
+from oracle import kernels as ok
+
+pytestmark = pytest.mark.gpu
+
+H, E, I, K = 2048, 64, 768, 8
+
+
+@pytest.fixture(scope="module")
+def layer(dev):
+    return synthetic.make_moe_layer(H, E, I, seed=7, device=dev)
+
+
+def _oracle_inputs(L):
+    return (np_u32(L.up_gate_packed), np_f(L.up_gate_alpha), np_u32(L.down_packed), np_f(L.down_alpha))
+
+
+def _check_routing(x, L, ids, wts, k=K):
+    rid, rw, probs = ok.router_topk(np_f(x), np_f(L.gate_weight), k,
+                                    bias=None if L.router_bias is None else np_f(L.router_bias))
+    safe = tie_safe_rows(probs, k)
+    assert safe.mean() > 0.98
+    np.testing.assert_array_equal(ids.cpu().numpy()[safe], rid[safe])
+    np.testing.assert_allclose(wts.cpu().numpy()[safe], rw[safe], rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("tokens", [1, 2])
+def test_moe_block_decode_vs_oracle(dev, layer, tokens):
+    x = synthetic.randn_bf16((tokens, H), 100 + tokens, dev)
+    res = synthetic.randn_bf16((tokens, H), 200 + tokens, dev)
+    y, ids, wts = moe_block(x, layer, K, residual=res)
+    torch.cuda.synchronize()
+    _check_routing(x, layer, ids, wts)
+    ref, _ = ok.moe_experts(np_f(x), ids.cpu().numpy(), wts.cpu().numpy(), *_oracle_inputs(layer),
+                            residual=np_f(res))
+    assert_bf16_close(np_f(y), ref, what=f"moe bs{tokens}")
+
+
+@pytest.mark.parametrize("tokens", [32, 128, 2048])
+def test_moe_grouped_zipf_vs_oracle(dev, layer, tokens):
+    assert tokens >= GROUPED_MIN_TOKENS
+    L = synthetic.MoELayer(layer.gate_weight, layer.up_gate_packed, layer.up_gate_alpha,
+                           layer.down_packed, layer.down_alpha,
+                           synthetic.zipf_router_bias(E, 1.1, 1.0, seed=3).to(dev))
+    x = synthetic.randn_bf16((tokens, H), 300 + tokens, dev)
+    ids, wts = router_topk(x, L.gate_weight, K, bias=L.router_bias)
+    y, h = moe_grouped(x, L, ids, wts, return_h=True)
+    torch.cuda.synchronize()
+    _check_routing(x, L, ids, wts)
+    idn, wn = ids.cpu().numpy(), wts.cpu().numpy()
+    counts = np.bincount(idn.reshape(-1), minlength=E)
+    assert counts.max() >= min(tokens, 8 * tokens // E)  # the skew is real
+    d = moe_dispatch(ids, E)
+    c, o, p, inv = ok.dispatch(idn, E)
+    np.testing.assert_array_equal(d.pair_ids.cpu().numpy(), p)
+    np.testing.assert_array_equal(d.offsets.cpu().numpy(), o)
+    np.testing.assert_array_equal(d.inverse.cpu().numpy(), inv)
+    ref, href = ok.moe_experts(np_f(x), idn, wn, *_oracle_inputs(L))
+    assert_bf16_close(np_f(h), href, what=f"h T={tokens}")
+    # y passes two bf16 rounding points (h and each slot's down output, as in
+    # the reference), so an element may differ by sum_j w_j * ulp(out_j):
+    # about one bf16 ulp of the output scale, whatever |y| itself is.
+    assert_bf16_close(np_f(y), ref, atol_frac=2.0 ** -7, what=f"y T={tokens}")
+
+
+def test_moe_block_grouped_matches_per_slot(dev, layer):
+    """The two plans agree on the same routing (bf16 tolerance)."""
+    x = synthetic.randn_bf16((16, H), 400, dev)
+    res = synthetic.randn_bf16((16, H), 401, dev)
+    ids, wts = router_topk(x, layer.gate_weight, K)
+    yg = moe_grouped(x, layer, ids, wts, res)
+    from maple_amd.kernels import ternary_expert_down_sum, ternary_expert_swiglu
+
+    hs = ternary_expert_swiglu(x, layer.up_gate_packed, layer.up_gate_alpha, ids)
+    ys = ternary_expert_down_sum(hs, layer.down_packed, layer.down_alpha, ids, wts, residual=res)
+    assert_bf16_close(np_f(yg), np_f(ys), rtol=2 ** -7, atol_frac=2e-3, what="grouped vs per-slot")
+
+
+def test_moe_block_graph_replays_match_eager(dev, layer):
+    """Captured once, replayed three times with eager work in between."""
+    x = synthetic.randn_bf16((1, H), 500, dev)
+    y_eager, _, _ = moe_block(x, layer, K)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        moe_block(x, layer, K)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y_g, _, _ = moe_block(x, layer, K)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(y_g, y_eager, rtol=0, atol=0)
+        moe_block(x, layer, K)  # eager work between replays
+        torch.cuda.synchronize()
+    from maple_amd.kernels.router import router_wait_timed_out
+
+    assert not router_wait_timed_out(dev)
