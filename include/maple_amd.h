@@ -190,6 +190,39 @@ int ma_moe_grouped(const void* x, int64_t ldx, int64_t tokens, int64_t top_k,
                    void* h_out, int64_t ldh, void* y,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Decode (q_len = 1) QK RMSNorm + partial RoPE + KV write.  qkv bf16
+ * [batch, (n_heads + 2 n_kv_heads) * head_dim] (row stride ldq); per head
+ * x * rsqrt(mean(x^2) + eps) * w (q_norm_w / k_norm_w float32 [head_dim]),
+ * rotate-half RoPE on the first rotary_dim dims with cos/sin from float32
+ * tables [n_pos, rotary_dim] at position seqlen[b], rounded to bf16 like the
+ * reference's table gather; K/V stored at seqlen[b] of the bf16 caches
+ * [batch, n_kv_heads, max_len, head_dim]; q_out bf16 [batch, n_heads, head_dim].
+ * head_dim must be 64.  Replaces apply_qkv_decode,
+ * src/maple_run/kernels/decode_attn.py:362-439 (which takes the gathered
+ * per-row cos/sin instead of the table).
+ */
+int ma_qk_norm_rope_store(const void* qkv, int64_t ldq, int64_t batch, int n_heads,
+                          int n_kv_heads, int head_dim, const float* q_norm_w,
+                          const float* k_norm_w, const float* cos_table, const float* sin_table,
+                          int64_t n_pos, int rotary_dim, int use_rope, float eps,
+                          const int64_t* seqlen, void* k_cache, void* v_cache, int64_t max_len,
+                          void* q_out, void* stream);
+
+/*
+ * Decode GQA attention: out[b, h] = softmax(q[b, h] . K^T * scale) V over
+ * positions [start, min(seqlen[b] + 1, max_len)) of the caches, start =
+ * kv_len - window when window > 0.  bf16 in/out, float32 accumulation,
+ * split over the sequence with a log-sum-exp merge.  head_dim must be 64.
+ * workspace: ma_gqa_workspace_bytes(batch, n_kv_heads, max_len).
+ * Replaces decode_gqa_attn, src/maple_run/kernels/decode_attn.py:470-592.
+ */
+size_t ma_gqa_workspace_bytes(int64_t batch, int n_kv_heads, int64_t max_len);
+int ma_decode_gqa_attn(const void* q, int64_t batch, int n_heads, int n_kv_heads, int head_dim,
+                       const void* k_cache, const void* v_cache, const int64_t* seqlen,
+                       int64_t max_len, int64_t window, float scale, void* out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,7 +1,21 @@
 """HIP kernels of the hot path, exported under the reference's names
-(``src/maple_run/kernels/__init__.py:5-39``), plus ``moe_dispatch``."""
+(``src/maple_run/kernels/__init__.py:5-39``), plus ``moe_dispatch``.
+
+Importing this package does not load the HIP library; the first kernel call
+does (and raises if it has not been built).  The functions are bound eagerly
+so that ``ternary_gemv`` names the function even after its submodule of the
+same name has been imported.
+"""
 
 from __future__ import annotations
+
+from .decode_attn import apply_qkv_decode, decode_gqa_attn
+from .dispatch import moe_dispatch
+from .fused_norm import add_rms_norm, moe_reduce_add, rms_norm
+from .router import router_topk
+from .rtn4 import rtn4_embedding, rtn4_gemv
+from .ternary_expert import ternary_expert_down_sum, ternary_expert_gemv, ternary_expert_swiglu
+from .ternary_gemv import ternary_gemv
 
 __all__ = [
     "ternary_gemv",
@@ -15,31 +29,6 @@ __all__ = [
     "rms_norm",
     "add_rms_norm",
     "moe_reduce_add",
+    "apply_qkv_decode",
+    "decode_gqa_attn",
 ]
-
-_WHERE = {
-    "ternary_gemv": "ternary_gemv",
-    "ternary_expert_gemv": "ternary_expert",
-    "ternary_expert_swiglu": "ternary_expert",
-    "ternary_expert_down_sum": "ternary_expert",
-    "router_topk": "router",
-    "moe_dispatch": "dispatch",
-    "rtn4_gemv": "rtn4",
-    "rtn4_embedding": "rtn4",
-    "rms_norm": "fused_norm",
-    "add_rms_norm": "fused_norm",
-    "moe_reduce_add": "fused_norm",
-}
-
-
-def __getattr__(name: str):
-    mod = _WHERE.get(name)
-    if mod is None:
-        raise AttributeError(f"module {__name__!r} has no attribute {name}")
-    import importlib
-
-    fn = getattr(importlib.import_module(f"{__name__}.{mod}"), name)
-    # Importing a submodule binds its name on this package; a function that
-    # shares its module's name (ternary_gemv) must win.
-    globals()[name] = fn
-    return fn

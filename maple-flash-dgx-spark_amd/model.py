@@ -1,0 +1,187 @@
+"""Synthetic packed decoder on the HIP kernels (decode path of reference
+``src/maple_run/model.py``: ``MapleDecoderLayer`` :477-506,
+``MapleForCausalLM.forward`` :848-886, ``KVCache`` :116-310).
+
+One decode step, per layer:
+  qkv   = ternary_gemv(hidden, W_qkv, rms_weight=input_ln)     (fused RMSNorm)
+  q     = apply_qkv_decode(qkv, ...)    QK-norm + RoPE, K/V written at seqlen
+  attn  = decode_gqa_attn(q, K, V, seqlen)
+  o     = ternary_gemv(attn, W_o)
+  hidden, mlp_in = add_rms_norm(hidden, o, post_ln)
+  hidden = moe_block(mlp_in, residual=hidden)
+then seqlen += 1, final rms_norm, RTN4 lm_head, greedy argmax.
+
+Weights are random with the synthetic distributions (``synthetic.py``): every
+projection packed ternary, norm weights 1, the lm_head and embedding 4-bit RTN
+with group 128 and zero-centred dequantised values, RoPE on every layer over
+half the head (rotary_dim 32, theta 1e4), full attention (no window).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from . import synthetic
+from .kernels.decode_attn import apply_qkv_decode, decode_gqa_attn
+from .kernels.fused_norm import add_rms_norm, rms_norm
+from .kernels.rtn4 import rtn4_embedding, rtn4_gemv
+from .kernels.ternary_gemv import ternary_gemv
+from .moe import moe_block
+
+
+@dataclass
+class DecoderConfig:
+    hidden: int = 2048
+    layers: int = 24
+    heads: int = 32
+    kv_heads: int = 4
+    head_dim: int = 64
+    experts: int = 64
+    inter: int = 768
+    top_k: int = 8
+    vocab: int = 151936
+    rtn_group: int = 128
+    rope_theta: float = 10000.0
+    partial_rotary: float = 0.5
+    eps: float = 1e-6
+    lm_scale: tuple = (0.003, 0.006)
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+    @property
+    def rotary_dim(self) -> int:
+        return int(self.head_dim * self.partial_rotary)
+
+
+@dataclass
+class DecoderLayerWeights:
+    qkv: torch.Tensor
+    qkv_alpha: torch.Tensor
+    o: torch.Tensor
+    o_alpha: torch.Tensor
+    input_ln: torch.Tensor
+    post_ln: torch.Tensor
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+    moe: synthetic.MoELayer
+
+
+def rope_tables(max_len: int, rotary_dim: int, theta: float, device):
+    """float32 cos/sin ``[max_len, rotary_dim]`` built like ``model.py:66-92``
+    (``inv_freq = theta^(-2i/rot)``, ``emb = cat(freqs, freqs)``)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, rotary_dim, 2, device=device, dtype=torch.float32) / rotary_dim))
+    t = torch.arange(max_len, device=device, dtype=torch.float32)
+    freqs = torch.outer(t, inv_freq)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().contiguous(), emb.sin().contiguous()
+
+
+@dataclass
+class KVCache:
+    """Preallocated bf16 K/V per layer ``[B, n_kv, max_len, D]`` and one write
+    position per row (``model.py:116-143``)."""
+
+    k: list
+    v: list
+    seqlen: torch.Tensor
+    max_len: int
+    attn_ws: torch.Tensor = field(default=None)
+
+
+class SyntheticDecoder:
+    def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 4096 + 128):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.max_len = max_len
+        c, dev, s = cfg, self.device, seed * 1000
+        ones = lambda n: torch.ones(n, device=dev, dtype=torch.float32)
+        self.layers = []
+        for i in range(c.layers):
+            qkv, qkv_a = synthetic.ternary_linear(c.qkv_rows, c.hidden, s + 10 * i + 1, dev)
+            o, o_a = synthetic.ternary_linear(c.hidden, c.heads * c.head_dim, s + 10 * i + 2, dev)
+            moe = synthetic.make_moe_layer(c.hidden, c.experts, c.inter, seed=s + 10 * i + 3, device=dev)
+            self.layers.append(DecoderLayerWeights(qkv, qkv_a, o, o_a, ones(c.hidden), ones(c.hidden),
+                                                   ones(c.head_dim), ones(c.head_dim), moe))
+        lo, hi = c.lm_scale
+        self.lm_head = synthetic.rtn4_table(c.vocab, c.hidden, c.rtn_group, s + 901, dev, lo, hi)
+        self.embed = synthetic.rtn4_table(c.vocab, c.hidden, c.rtn_group, s + 902, dev, lo, hi)
+        self.final_norm = ones(c.hidden)
+        self.cos, self.sin = rope_tables(max_len, c.rotary_dim, c.rope_theta, dev)
+
+    def make_cache(self, batch: int, prefill_len: int, seed: int = 0) -> KVCache:
+        """Cache rows filled with seeded N(0, 1) bf16 K/V for ``prefill_len``
+        positions; decoding then writes at ``prefill_len``."""
+        c = self.cfg
+        shape = (batch, c.kv_heads, self.max_len, c.head_dim)
+        ks, vs = [], []
+        for i in range(c.layers):
+            k = synthetic.randn_bf16(shape, 50_000 + seed * 97 + 2 * i, self.device)
+            v = synthetic.randn_bf16(shape, 50_001 + seed * 97 + 2 * i, self.device)
+            k[:, :, prefill_len:] = 0
+            v[:, :, prefill_len:] = 0
+            ks.append(k)
+            vs.append(v)
+        seqlen = torch.full((batch,), prefill_len, device=self.device, dtype=torch.int64)
+        from . import _lib
+
+        nbytes = int(_lib.load().ma_gqa_workspace_bytes(batch, c.kv_heads, self.max_len))
+        ws = torch.empty(nbytes, device=self.device, dtype=torch.uint8)
+        return KVCache(ks, vs, seqlen, self.max_len, ws)
+
+    def layer_step(self, i: int, hidden: torch.Tensor, cache: KVCache, routing=None) -> torch.Tensor:
+        c, L = self.cfg, self.layers[i]
+        bsz = hidden.shape[0]
+        qkv = ternary_gemv(hidden, L.qkv, L.qkv_alpha, rms_weight=L.input_ln, rms_eps=c.eps)
+        q = apply_qkv_decode(qkv, L.q_norm, L.k_norm, self.cos, self.sin, cache.k[i], cache.v[i],
+                             cache.seqlen, num_heads=c.heads, num_kv_heads=c.kv_heads,
+                             head_dim=c.head_dim, rotary_dim=c.rotary_dim, eps=c.eps)
+        attn = decode_gqa_attn(q, cache.k[i], cache.v[i], cache.seqlen, scale=c.head_dim ** -0.5,
+                               workspace=cache.attn_ws)
+        o = ternary_gemv(attn.reshape(bsz, -1), L.o, L.o_alpha)
+        hidden, mlp_in = add_rms_norm(hidden, o, L.post_ln, c.eps)
+        y, ids, _ = moe_block(mlp_in, L.moe, c.top_k, residual=hidden)
+        if routing is not None:
+            routing.append(ids)
+        return y
+
+    def forward(self, input_ids: torch.Tensor, cache: KVCache, routing: list | None = None) -> torch.Tensor:
+        """One decode step for ``input_ids [B]``; returns bf16 logits ``[B, vocab]``.
+        ``routing``, if a list, receives each layer's expert ids."""
+        hidden = self.embed_tokens(input_ids)
+        for i in range(self.cfg.layers):
+            hidden = self.layer_step(i, hidden, cache, routing)
+        cache.seqlen.add_(1)
+        return self.head(hidden)
+
+    def embed_tokens(self, input_ids: torch.Tensor) -> torch.Tensor:
+        w, sc, bs = self.embed
+        return rtn4_embedding(input_ids, w, sc, bs, group_size=self.cfg.rtn_group).to(torch.bfloat16)
+
+    def head(self, hidden: torch.Tensor) -> torch.Tensor:
+        """Final RMSNorm and the RTN4 lm_head: bf16 logits ``[B, vocab]``."""
+        hidden = rms_norm(hidden, self.final_norm, self.cfg.eps)
+        w, sc, bs = self.lm_head
+        return rtn4_gemv(hidden, w, sc, bs, group_size=self.cfg.rtn_group)
+
+    def greedy_step(self, ids: torch.Tensor, cache: KVCache) -> torch.Tensor:
+        """forward + argmax, writing the next ids back into ``ids`` (graph-safe)."""
+        logits = self.forward(ids, cache)
+        ids.copy_(torch.argmax(logits, dim=-1))
+        return logits
+
+    def decode_bytes(self, batch: int, kv_len: int) -> int:
+        """Algorithmic HBM bytes of one decode step (weights touched once, the
+        KV read for every row; experts counted as 8 selected per token at most
+        the 64 that exist)."""
+        c = self.cfg
+        lay = (c.qkv_rows + c.hidden) * c.hidden // 4 + (c.qkv_rows + c.hidden) * 2
+        router = c.experts * c.hidden * 2
+        expert = (3 * c.inter * c.hidden) // 4 + (2 * c.inter + c.hidden) * 2
+        experts = min(c.experts, c.top_k * batch) * expert
+        kv = batch * 2 * c.kv_heads * kv_len * c.head_dim * 2
+        head = c.vocab * c.hidden // 2 + 2 * c.vocab * (c.hidden // c.rtn_group) * 2
+        return c.layers * (lay + router + experts + kv) + head

@@ -1,0 +1,217 @@
+"""Decode attention and the synthetic decoder vs the CPU oracle (needs the GPU).
+
+Attention: QK-norm + RoPE + KV write and split GQA at ragged lengths up to
+4096 (the reference's ragged set, tests/test_fused_decode.py:245, plus 4096).
+Decoder: a reduced model over several teacher-forced steps at batch 1 and 3,
+graph replays equal to eager, and one step of the full 24-layer synthetic
+decoder (hidden 2048, 32/4 heads, 64 experts, vocab 151936) at batch 1.
+Logits: cosine >= 0.9999 and max error <= 1e-2 of the logit scale; greedy ids
+equal where the top-2 logits of the oracle are separated.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import assert_bf16_close, np_f, np_u32
+from maple_amd import synthetic
+from maple_amd.kernels import apply_qkv_decode, decode_gqa_attn
+from maple_amd.model import DecoderConfig, SyntheticDecoder
+from oracle import decoder as od
+
+pytestmark = pytest.mark.gpu
+
+
+def test_qk_norm_rope_store_vs_oracle(dev):
+    nq, nkv, d, max_len, rot = 32, 4, 64, 4224, 32
+    seqlen = torch.tensor([0, 100, 4095], device=dev)
+    qkv = synthetic.randn_bf16((3, (nq + 2 * nkv) * d), 1, dev)
+    kc = synthetic.randn_bf16((3, nkv, max_len, d), 2, dev)
+    vc = synthetic.randn_bf16((3, nkv, max_len, d), 3, dev)
+    k0, v0 = kc.clone(), vc.clone()
+    qw = torch.rand(d, device=dev) + 0.5
+    kw = torch.rand(d, device=dev) + 0.5
+    cos, sin = od.rope_tables(max_len, rot, 1e4)
+    q = apply_qkv_decode(qkv, qw, kw, torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev),
+                         kc, vc, seqlen, num_heads=nq, num_kv_heads=nkv, head_dim=d, rotary_dim=rot)
+    x = np_f(qkv)
+    for b, pos in enumerate(seqlen.tolist()):
+        cs, sn = od.bf(cos[pos]), od.bf(sin[pos])
+        ref_q = np.stack([od.head_norm_rope(x[b, h * d:(h + 1) * d], np_f(qw), cs, sn, rot, 1e-6)
+                          for h in range(nq)])
+        assert_bf16_close(np_f(q[b, :, 0]), ref_q, what=f"q row {b}")
+        for kh in range(nkv):
+            o0, o1 = (nq + kh) * d, (nq + nkv + kh) * d
+            ref_k = od.head_norm_rope(x[b, o0:o0 + d], np_f(kw), cs, sn, rot, 1e-6)
+            assert_bf16_close(np_f(kc[b, kh, pos]), ref_k, what=f"k row {b}")
+            np.testing.assert_array_equal(np_f(vc[b, kh, pos]), x[b, o1:o1 + d])
+        mask = torch.ones(max_len, dtype=torch.bool, device=dev)
+        mask[pos] = False
+        assert torch.equal(kc[b][:, mask], k0[b][:, mask]) and torch.equal(vc[b][:, mask], v0[b][:, mask])
+
+
+@pytest.mark.parametrize("window", [None, 512])
+def test_gqa_ragged_vs_oracle(dev, window):
+    nq, nkv, d, max_len = 32, 4, 64, 4096
+    lens = [1, 63, 64, 65, 300, 511, 1000, 4096]
+    seqlen = torch.tensor([n - 1 for n in lens], device=dev)
+    q = synthetic.randn_bf16((len(lens), nq, 1, d), 11, dev)
+    kc = synthetic.randn_bf16((len(lens), nkv, max_len, d), 12, dev)
+    vc = synthetic.randn_bf16((len(lens), nkv, max_len, d), 13, dev)
+    out = decode_gqa_attn(q, kc, vc, seqlen, scale=d ** -0.5, window=window)
+    for b, n in enumerate(lens):
+        ref = od.gqa(np_f(q[b, :, 0]), np_f(kc[b]), np_f(vc[b]), n, d ** -0.5, window)
+        assert_bf16_close(np_f(out[b, :, 0]), ref, atol_frac=2e-3, what=f"len {n}")
+    # a row alone gives the same bits as in the batch
+    solo = decode_gqa_attn(q[6:7], kc[6:7], vc[6:7], seqlen[6:7], scale=d ** -0.5, window=window)
+    assert torch.equal(solo, out[6:7])
+
+
+def _to_np(model: SyntheticDecoder) -> dict:
+    c = model.cfg
+    layers = []
+    for L in model.layers:
+        layers.append(dict(
+            qkv=np_u32(L.qkv), qkv_alpha=np_f(L.qkv_alpha), o=np_u32(L.o), o_alpha=np_f(L.o_alpha),
+            input_ln=np_f(L.input_ln), post_ln=np_f(L.post_ln), q_norm=np_f(L.q_norm),
+            k_norm=np_f(L.k_norm),
+            moe=dict(gate_weight=np_f(L.moe.gate_weight), up_gate_packed=np_u32(L.moe.up_gate_packed),
+                     up_gate_alpha=np_f(L.moe.up_gate_alpha), down_packed=np_u32(L.moe.down_packed),
+                     down_alpha=np_f(L.moe.down_alpha))))
+    cfg = dict(hidden=c.hidden, heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim,
+               rotary_dim=c.rotary_dim, eps=c.eps, rtn_group=c.rtn_group, top_k=c.top_k)
+    w, s, b = model.embed
+    lw, ls, lb = model.lm_head
+    return dict(cfg=cfg, layers=layers, embed=(np_u32(w), np_f(s), np_f(b)),
+                lm_head=(np_u32(lw), np_f(ls), np_f(lb)), final_norm=np_f(model.final_norm),
+                cos=np_f(model.cos), sin=np_f(model.sin))
+
+
+def _cache_np(cache) -> dict:
+    return dict(k=[np_f(k) for k in cache.k], v=[np_f(v) for v in cache.v],
+                seqlen=cache.seqlen.cpu().numpy().copy())
+
+
+def _check_logits(logits, ref, what):
+    y = np_f(logits)
+    for b in range(y.shape[0]):
+        cos = float(np.dot(y[b], ref[b]) / (np.linalg.norm(y[b]) * np.linalg.norm(ref[b])))
+        assert cos >= 0.9999, f"{what} row {b}: cosine {cos:.6f}"
+        err = np.abs(y[b] - ref[b]).max() / np.abs(ref[b]).max()
+        assert err <= 1e-2, f"{what} row {b}: max rel err {err:.3g}"
+        top2 = np.sort(ref[b])[-2:]
+        if top2[1] - top2[0] > 4 * 2 ** -8 * abs(top2[1]):
+            assert int(np.argmax(y[b])) == int(np.argmax(ref[b])), f"{what} row {b}: greedy id"
+
+
+SMALL = DecoderConfig(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=64, experts=8, inter=256,
+                      top_k=2, vocab=1024, rtn_group=128, lm_scale=(0.01, 0.02))
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_small_decoder_steps_vs_oracle(dev, batch):
+    model = SyntheticDecoder(SMALL, dev, seed=5, max_len=128)
+    cache = model.make_cache(batch, prefill_len=37, seed=1)
+    m = _to_np(model)
+    cnp = _cache_np(cache)
+    ids = torch.randint(0, SMALL.vocab, (batch,), device=dev, generator=torch.Generator(device=dev).manual_seed(3))
+    for step in range(3):
+        logits = model.forward(ids, cache)
+        ref, _ = od.decoder_step(m, cnp, ids.cpu().numpy())
+        _check_logits(logits, ref, f"step {step}")
+        ids = torch.argmax(logits, dim=-1)  # teacher-forced: both continue from the device ids
+    np.testing.assert_array_equal(cache.seqlen.cpu().numpy(), cnp["seqlen"])
+
+
+def test_decoder_graph_replays_match_eager(dev):
+    model = SyntheticDecoder(SMALL, dev, seed=6, max_len=128)
+    ids0 = torch.tensor([5, 900], device=dev)
+    c_e = model.make_cache(2, prefill_len=20, seed=2)
+    ids_e = ids0.clone()
+    eager = [model.greedy_step(ids_e, c_e).clone() for _ in range(4)]
+    c_g = model.make_cache(2, prefill_len=20, seed=2)
+    ids_g = ids0.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # warm-up step, then rewind the cache position
+        model.greedy_step(ids_g, c_g)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    c_g.seqlen.fill_(20)
+    ids_g.copy_(ids0)
+    c_g2 = model.make_cache(2, prefill_len=20, seed=2)
+    for i in range(SMALL.layers):
+        c_g.k[i].copy_(c_g2.k[i])
+        c_g.v[i].copy_(c_g2.v[i])
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        lg = model.greedy_step(ids_g, c_g)
+    c_g.seqlen.fill_(20)
+    ids_g.copy_(ids0)
+    for i in range(SMALL.layers):
+        c_g.k[i].copy_(c_g2.k[i])
+        c_g.v[i].copy_(c_g2.v[i])
+    for step in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(lg, eager[step]), f"replay {step}"
+        torch.zeros(1, device=dev).add_(1)  # eager work between replays
+
+
+def _cos(a, b):
+    a, b = np.ravel(a), np.ravel(b)
+    return float(np.dot(a, b) / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def test_full_decoder_one_step_vs_oracle(dev):
+    """Full 24-layer model, one step at batch 1 over a 4096-token cache.
+
+    Layer by layer, each device layer's output is compared with the oracle's
+    layer on the same (device) input: cosine >= 0.9999 and max error <= 1e-2;
+    the expert ids equal the oracle's own top-k where the k-th and (k+1)-th
+    probabilities differ by more than 1e-3 (the two layers see inputs that
+    differ by rounding, about 2e-3 in a router logit).  The logits from the device's final hidden
+    state meet the logits bar.  End to end, with no teacher forcing, the
+    logits cosine is held to >= 0.99: this random 24-layer network amplifies
+    rounding, and the oracle itself, given half-an-ulp relative noise at each
+    RMSNorm output and the same routing, reaches only cosine 0.998.
+    """
+    model = SyntheticDecoder(DecoderConfig(), dev, seed=0, max_len=4096 + 64)
+    c = model.cfg
+    cache = model.make_cache(1, prefill_len=4096, seed=0)
+    m = _to_np(model)
+    cnp = _cache_np(cache)
+    e2e = _cache_np(cache)
+    oc = dict(m["cfg"], cos=m["cos"], sin=m["sin"])
+    ids = torch.tensor([12345], device=dev)
+    h = model.embed_tokens(ids)
+    h_ref = od.bf(od.ok.rtn4_embedding(ids.cpu().numpy(), *m["embed"], group_size=c.rtn_group))
+    np.testing.assert_array_equal(np_f(h), h_ref)
+    h_e2e = h_ref
+    dev_ids = []
+    for i in range(c.layers):
+        routing = []
+        out = model.layer_step(i, h, cache, routing)
+        rid = routing[0].cpu().numpy()
+        dev_ids.append(rid)
+        ref, (own, probs) = od.decoder_layer(m["layers"][i], oc, np_f(h), cnp, i, router_ids=rid)
+        y = np_f(out)
+        assert _cos(y, ref) >= 0.9999, f"layer {i}: cosine {_cos(y, ref):.6f}"
+        assert np.abs(y - ref).max() <= 1e-2 * np.abs(ref).max(), f"layer {i}: max err"
+        p = np.sort(probs.reshape(-1))[::-1]
+        if p[c.top_k - 1] - p[c.top_k] > 1e-3:
+            np.testing.assert_array_equal(np.sort(rid, -1), np.sort(own, -1), err_msg=f"layer {i} ids")
+        h_e2e, _ = od.decoder_layer(m["layers"][i], oc, h_e2e, e2e, i, router_ids=rid)
+        h = out
+    cache.seqlen.add_(1)
+    logits = model.head(h)
+    torch.cuda.synchronize()
+    _check_logits(logits, od.final_logits(m, np_f(h)), "full decoder head")
+    ref_e2e = od.final_logits(m, h_e2e)
+    cos = _cos(np_f(logits), ref_e2e)
+    assert cos >= 0.99, f"end-to-end cosine {cos:.6f}"
+    # forward() gives the same bits as the layer-by-layer calls
+    cache2 = model.make_cache(1, prefill_len=4096, seed=0)
+    assert torch.equal(model.forward(ids, cache2), logits)
