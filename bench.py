@@ -3,9 +3,10 @@
 Workload: one synthetic MoE FFN layer (hidden 2048, 64 experts, SwiGLU
 intermediate 768, top-8 routing) at decode batch 1, run through the HIP
 kernels (router top-k, fused up+gate SwiGLU, down projection + weighted
-combine).  ``--layers`` distinct layers (default 24, ~1.8 GB of packed
-weights, several times the 256 MB Infinity Cache) are captured in one HIP
-graph and replayed, so every layer's weights come from HBM.
+combine).  ``--layers`` distinct layers (default 96: 7.3 GB of packed
+weights, of which the 8 selected experts per layer are 0.91 GB, 3.6 times the
+256 MB Infinity Cache) are captured in one HIP graph and replayed in a cycle,
+so every layer's weights come from HBM.
 
 A step is one graph replay: ``--layers`` MoE-layer decodes, each on its own
 cold layer.  ``value`` is the whole-layer algorithmic HBM throughput:
@@ -24,7 +25,9 @@ summary under profiles/ when present.
 float32 matmul over the 8 selected experts, the reference's own test
 oracle) on a bounded sample of the same workload on this host's cores.
 
-    python bench.py [--steps 20] [--warmup 3] [--layers 24] [--no-cpu]
+    python bench.py [--steps 20] [--warmup 3] [--layers 96] [--no-cpu]
+                    [--no-decoder] [--no-extra]
+    python bench.py --counters-pass   # SwiGLU graph + a 256 MiB copy, for rocprofv3 --pmc
 """
 
 from __future__ import annotations
@@ -150,6 +153,40 @@ def extra_workloads(layers, dev, steps: int) -> dict:
     return out
 
 
+def decoder_tokens_per_s(dev, batch: int, steps: int, warmup: int) -> dict:
+    """Greedy decode of the full synthetic decoder (24 layers, hidden 2048,
+    32/4 heads of 64, 64 experts top-8, RTN4 lm_head over 151936 tokens) at
+    ``batch`` rows over a 4096-token KV cache, one HIP graph replay per step
+    (the whole step captured).  Each replay appends one position per row."""
+    import torch
+
+    from maple_amd.model import DecoderConfig, SyntheticDecoder
+
+    cfg = DecoderConfig()
+    model = SyntheticDecoder(cfg, dev, seed=0, max_len=4096 + steps + warmup + 8)
+    cache = model.make_cache(batch, prefill_len=4096, seed=0)
+    gen = torch.Generator(device=dev).manual_seed(batch)
+    ids = torch.randint(0, cfg.vocab, (batch,), device=dev, generator=gen)
+    g = graph_of(lambda: model.greedy_step(ids, cache))
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(True), torch.cuda.Event(True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / steps
+    nbytes = model.decode_bytes(batch, 4096 + warmup + steps // 2)
+    out = {"tokens_per_s": round(batch / t, 1), "ms_per_step": round(t * 1e3, 4),
+           "kv_len": 4096, "algorithmic_GB/s": round(nbytes / t / 1e9, 1),
+           "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+    del g, cache, model
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(seconds: float = 12.0) -> dict:
     import numpy as np
 
@@ -191,9 +228,12 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--layers", type=int, default=24)
+    ap.add_argument("--layers", type=int, default=96)
+    ap.add_argument("--counters-pass", action="store_true",
+                    help="only replay the SwiGLU graph and a plain 256 MiB copy (for counters)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-decoder", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -258,6 +298,16 @@ def main() -> int:
     if router_wait_timed_out(dev):
         log("router reported a timed-out wait: results invalid")
         return 1
+    if args.counters_pass:
+        # Calibration copy: 256 MiB read + 256 MiB written per launch.
+        a = torch.empty(128 << 20, device=dev, dtype=torch.bfloat16).fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(4):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"counters_pass": True, "swiglu_launches": (args.steps + args.warmup + 1) * L,
+                          "copy_bytes": a.numel() * 2}), flush=True)
+        return 0
 
     out = {
         "metric": METRIC,
@@ -281,8 +331,15 @@ def main() -> int:
                      "bytes_per_launch": nb["swiglu_launch"],
                      "us_per_launch": round(per_launch * 1e6, 3)},
         "cpu_baseline": None,
+        "decode": None,
         "extra": None,
     }
+    if not args.no_decoder:
+        out["decode"] = {}
+        for bsz in (1, 32):
+            log(f"timing the full decoder at batch {bsz} ...")
+            out["decode"][f"bs{bsz}"] = decoder_tokens_per_s(dev, bsz, max(args.steps, 10), args.warmup)
+            log(json.dumps(out["decode"][f"bs{bsz}"]))
     if not args.no_extra:
         log("timing the other workloads ...")
         out["extra"] = extra_workloads(layers, dev, args.steps)

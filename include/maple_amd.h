@@ -193,35 +193,59 @@ int ma_moe_grouped(const void* x, int64_t ldx, int64_t tokens, int64_t top_k,
 /*
  * Decode (q_len = 1) QK RMSNorm + partial RoPE + KV write.  qkv bf16
  * [batch, (n_heads + 2 n_kv_heads) * head_dim] (row stride ldq); per head
- * x * rsqrt(mean(x^2) + eps) * w (q_norm_w / k_norm_w float32 [head_dim]),
- * rotate-half RoPE on the first rotary_dim dims with cos/sin from float32
- * tables [n_pos, rotary_dim] at position seqlen[b], rounded to bf16 like the
- * reference's table gather; K/V stored at seqlen[b] of the bf16 caches
- * [batch, n_kv_heads, max_len, head_dim]; q_out bf16 [batch, n_heads, head_dim].
- * head_dim must be 64.  Replaces apply_qkv_decode,
- * src/maple_run/kernels/decode_attn.py:362-439 (which takes the gathered
- * per-row cos/sin instead of the table).
+ * x * rsqrt(mean(x^2) + eps) * w (q_norm_w / k_norm_w [head_dim] of w_dtype),
+ * rotate-half RoPE on the first rotary_dim dims.  cos/sin (cs_dtype, row
+ * stride ld_cs): n_pos == 0 -> row b holds batch row b's values (the
+ * reference's gathered [B, rotary_dim] form); n_pos > 0 -> a table of n_pos
+ * rows indexed by seqlen[b] (clamped).  Values are rounded to bf16 before use.
+ * K/V are stored at position seqlen[b] (clamped to [0, max_len)) of cache row
+ * row_map[b] (b when row_map is NULL; clamped to [0, cache_rows)) of the bf16
+ * caches [cache_rows, n_kv_heads, max_len, head_dim]; q_out bf16
+ * [batch, n_heads, head_dim].  head_dim must be 64.
+ * Replaces apply_qkv_decode, src/maple_run/kernels/decode_attn.py:362-439.
  */
 int ma_qk_norm_rope_store(const void* qkv, int64_t ldq, int64_t batch, int n_heads,
-                          int n_kv_heads, int head_dim, const float* q_norm_w,
-                          const float* k_norm_w, const float* cos_table, const float* sin_table,
-                          int64_t n_pos, int rotary_dim, int use_rope, float eps,
-                          const int64_t* seqlen, void* k_cache, void* v_cache, int64_t max_len,
-                          void* q_out, void* stream);
+                          int n_kv_heads, int head_dim, const void* q_norm_w,
+                          const void* k_norm_w, int w_dtype, const void* cos, const void* sin,
+                          int cs_dtype, int64_t ld_cs, int64_t n_pos, int rotary_dim,
+                          int use_rope, float eps, const int64_t* seqlen,
+                          const int64_t* row_map, void* k_cache, void* v_cache,
+                          int64_t cache_rows, int64_t max_len, void* q_out, void* stream);
 
 /*
  * Decode GQA attention: out[b, h] = softmax(q[b, h] . K^T * scale) V over
- * positions [start, min(seqlen[b] + 1, max_len)) of the caches, start =
- * kv_len - window when window > 0.  bf16 in/out, float32 accumulation,
- * split over the sequence with a log-sum-exp merge.  head_dim must be 64.
- * workspace: ma_gqa_workspace_bytes(batch, n_kv_heads, max_len).
- * Replaces decode_gqa_attn, src/maple_run/kernels/decode_attn.py:470-592.
+ * positions [start, min(seqlen[b] + 1, max_len)) of cache row row_map[b] (b
+ * when NULL), start = kv_len - window when window > 0.  q / out bf16
+ * [batch, n_heads, head_dim], float32 accumulation, P rounded to bf16, split
+ * over the sequence (128 positions per split) and merged in the same launch.
+ * workspace: ma_gqa_workspace_bytes(batch, n_kv_heads, max_len) bytes,
+ * 16-byte aligned; its first bytes are per-(row, KV head) tickets that must
+ * be zero before the first call (each call leaves them zero).  Calls that
+ * share a workspace must not overlap.  head_dim must be 64.
+ * Replaces decode_gqa_attn, src/maple_run/kernels/decode_attn.py:470-592
+ * (which merges the splits in a second kernel, :317-359).
  */
 size_t ma_gqa_workspace_bytes(int64_t batch, int n_kv_heads, int64_t max_len);
 int ma_decode_gqa_attn(const void* q, int64_t batch, int n_heads, int n_kv_heads, int head_dim,
-                       const void* k_cache, const void* v_cache, const int64_t* seqlen,
-                       int64_t max_len, int64_t window, float scale, void* out,
-                       void* workspace, size_t workspace_bytes, void* stream);
+                       const void* k_cache, const void* v_cache, int64_t cache_rows,
+                       int64_t max_len, const int64_t* seqlen, const int64_t* row_map,
+                       int64_t window, float scale, void* out, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/*
+ * ma_qk_norm_rope_store followed by ma_decode_gqa_attn in one launch (same
+ * arguments and results; q is not written out).  The decode step of the
+ * reference's MapleAttention, src/maple_run/model.py:368-414, which runs the
+ * RoPE gather, apply_qkv_decode and decode_gqa_attn as separate launches.
+ */
+int ma_decode_attn_fused(const void* qkv, int64_t ldq, int64_t batch, int n_heads,
+                         int n_kv_heads, int head_dim, const void* q_norm_w,
+                         const void* k_norm_w, int w_dtype, const void* cos, const void* sin,
+                         int cs_dtype, int64_t ld_cs, int64_t n_pos, int rotary_dim,
+                         int use_rope, float eps, const int64_t* seqlen, const int64_t* row_map,
+                         void* k_cache, void* v_cache, int64_t cache_rows, int64_t max_len,
+                         int64_t window, float scale, void* out, void* workspace,
+                         size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -41,10 +41,12 @@ _SIGNATURES = {
     "ma_rtn4_gemv": [_P, _I, _L, _L, _P, _L, _L, _I, _P, _I, _P, _I, _L, _P, _L, _P],
     "ma_rtn4_embedding": [_P, _I, _L, _P, _L, _L, _P, _I, _P, _I, _L, _P, _P],
     "ma_grouped_workspace_bytes": [_L, _L, _L],
-    "ma_qk_norm_rope_store": [_P, _L, _L, _I, _I, _I, _P, _P, _P, _P, _L, _I, _I, _F, _P, _P, _P,
-                              _L, _P, _P],
+    "ma_qk_norm_rope_store": [_P, _L, _L, _I, _I, _I, _P, _P, _I, _P, _P, _I, _L, _L, _I, _I, _F,
+                              _P, _P, _P, _P, _L, _L, _P, _P],
     "ma_gqa_workspace_bytes": [_L, _I, _L],
-    "ma_decode_gqa_attn": [_P, _L, _I, _I, _I, _P, _P, _P, _L, _L, _F, _P, _P, _Z, _P],
+    "ma_decode_gqa_attn": [_P, _L, _I, _I, _I, _P, _P, _L, _L, _P, _P, _L, _F, _P, _P, _Z, _P],
+    "ma_decode_attn_fused": [_P, _L, _L, _I, _I, _I, _P, _P, _I, _P, _P, _I, _L, _L, _I, _I, _F,
+                             _P, _P, _P, _P, _L, _L, _L, _F, _P, _P, _Z, _P],
     "ma_moe_grouped": [_P, _L, _L, _L, _P, _P, _P, _P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _I,
                        _P, _L, _P, _P, _Z, _P],
 }

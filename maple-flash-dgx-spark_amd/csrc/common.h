@@ -127,6 +127,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return bf16_bits_exact(lo) | (bf16_bits_exact(hi) << 16);
 }
 
+// Round two floats to bf16 (nearest even) and pack them, lo in the low half.
+__device__ __forceinline__ uint32_t pack_bf16x2_rn(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
 // x' pairs for one word from 16 consecutive activations xs[0..15] (already
 // float): pair j = (f_j * xs[j], f_j * xs[j+8]).  Returns sum (f_j + 1) xs.
 // Only exact when xs are bf16 values (the fast path's input dtype).
@@ -196,6 +201,6 @@ __device__ __forceinline__ float lane_bcast(float v, int src) {
 // to their first use to save registers, serialising their latencies).
 #define MA_ISSUE_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace ma

@@ -9,7 +9,7 @@ same name has been imported.
 
 from __future__ import annotations
 
-from .decode_attn import apply_qkv_decode, decode_gqa_attn
+from .decode_attn import apply_qkv_decode, decode_attention, decode_gqa_attn, gqa_workspace
 from .dispatch import moe_dispatch
 from .fused_norm import add_rms_norm, moe_reduce_add, rms_norm
 from .router import router_topk
@@ -31,4 +31,6 @@ __all__ = [
     "moe_reduce_add",
     "apply_qkv_decode",
     "decode_gqa_attn",
+    "decode_attention",
+    "gqa_workspace",
 ]

@@ -4,8 +4,8 @@
 
 One decode step, per layer:
   qkv   = ternary_gemv(hidden, W_qkv, rms_weight=input_ln)     (fused RMSNorm)
-  q     = apply_qkv_decode(qkv, ...)    QK-norm + RoPE, K/V written at seqlen
-  attn  = decode_gqa_attn(q, K, V, seqlen)
+  attn  = decode_attention(qkv, ...)    QK-norm + RoPE, K/V written at seqlen,
+                                        GQA over the cache (one launch)
   o     = ternary_gemv(attn, W_o)
   hidden, mlp_in = add_rms_norm(hidden, o, post_ln)
   hidden = moe_block(mlp_in, residual=hidden)
@@ -24,7 +24,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import synthetic
-from .kernels.decode_attn import apply_qkv_decode, decode_gqa_attn
+from .kernels.decode_attn import decode_attention, gqa_workspace
 from .kernels.fused_norm import add_rms_norm, rms_norm
 from .kernels.rtn4 import rtn4_embedding, rtn4_gemv
 from .kernels.ternary_gemv import ternary_gemv
@@ -82,8 +82,9 @@ def rope_tables(max_len: int, rotary_dim: int, theta: float, device):
 
 @dataclass
 class KVCache:
-    """Preallocated bf16 K/V per layer ``[B, n_kv, max_len, D]`` and one write
-    position per row (``model.py:116-143``)."""
+    """Preallocated bf16 K/V per layer ``[B, n_kv, max_len, D]``, one write
+    position per row (``model.py:116-143``) and the attention workspace
+    (zeroed once; the kernels leave its tickets zero)."""
 
     k: list
     v: list
@@ -126,21 +127,17 @@ class SyntheticDecoder:
             ks.append(k)
             vs.append(v)
         seqlen = torch.full((batch,), prefill_len, device=self.device, dtype=torch.int64)
-        from . import _lib
-
-        nbytes = int(_lib.load().ma_gqa_workspace_bytes(batch, c.kv_heads, self.max_len))
-        ws = torch.empty(nbytes, device=self.device, dtype=torch.uint8)
+        ws = gqa_workspace(batch, c.kv_heads, self.max_len, self.device)
         return KVCache(ks, vs, seqlen, self.max_len, ws)
 
     def layer_step(self, i: int, hidden: torch.Tensor, cache: KVCache, routing=None) -> torch.Tensor:
         c, L = self.cfg, self.layers[i]
         bsz = hidden.shape[0]
         qkv = ternary_gemv(hidden, L.qkv, L.qkv_alpha, rms_weight=L.input_ln, rms_eps=c.eps)
-        q = apply_qkv_decode(qkv, L.q_norm, L.k_norm, self.cos, self.sin, cache.k[i], cache.v[i],
-                             cache.seqlen, num_heads=c.heads, num_kv_heads=c.kv_heads,
-                             head_dim=c.head_dim, rotary_dim=c.rotary_dim, eps=c.eps)
-        attn = decode_gqa_attn(q, cache.k[i], cache.v[i], cache.seqlen, scale=c.head_dim ** -0.5,
-                               workspace=cache.attn_ws)
+        attn = decode_attention(qkv, L.q_norm, L.k_norm, self.cos, self.sin, cache.k[i], cache.v[i],
+                                cache.seqlen, cache.attn_ws, num_heads=c.heads,
+                                num_kv_heads=c.kv_heads, head_dim=c.head_dim,
+                                rotary_dim=c.rotary_dim, eps=c.eps, scale=c.head_dim ** -0.5)
         o = ternary_gemv(attn.reshape(bsz, -1), L.o, L.o_alpha)
         hidden, mlp_in = add_rms_norm(hidden, o, L.post_ln, c.eps)
         y, ids, _ = moe_block(mlp_in, L.moe, c.top_k, residual=hidden)

@@ -17,39 +17,53 @@ import torch
 
 from _helpers import assert_bf16_close, np_f, np_u32
 from maple_amd import synthetic
-from maple_amd.kernels import apply_qkv_decode, decode_gqa_attn
+from maple_amd.kernels import apply_qkv_decode, decode_attention, decode_gqa_attn, gqa_workspace
 from maple_amd.model import DecoderConfig, SyntheticDecoder
 from oracle import decoder as od
 
 pytestmark = pytest.mark.gpu
 
 
-def test_qk_norm_rope_store_vs_oracle(dev):
+def _rope_rows(table, seqlen, dev):
+    """The reference's gather: float32 table rows at seqlen, cast to bf16."""
+    return torch.from_numpy(table).to(dev)[seqlen.clamp(0, table.shape[0] - 1)].to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("mapped", [False, True])
+def test_qk_norm_rope_store_vs_oracle(dev, mapped):
     nq, nkv, d, max_len, rot = 32, 4, 64, 4224, 32
     seqlen = torch.tensor([0, 100, 4095], device=dev)
+    rows = 5 if mapped else 3
+    row_map = torch.tensor([4, 0, 2], device=dev) if mapped else None
+    crow = row_map.tolist() if mapped else [0, 1, 2]
     qkv = synthetic.randn_bf16((3, (nq + 2 * nkv) * d), 1, dev)
-    kc = synthetic.randn_bf16((3, nkv, max_len, d), 2, dev)
-    vc = synthetic.randn_bf16((3, nkv, max_len, d), 3, dev)
+    kc = synthetic.randn_bf16((rows, nkv, max_len, d), 2, dev)
+    vc = synthetic.randn_bf16((rows, nkv, max_len, d), 3, dev)
     k0, v0 = kc.clone(), vc.clone()
     qw = torch.rand(d, device=dev) + 0.5
     kw = torch.rand(d, device=dev) + 0.5
     cos, sin = od.rope_tables(max_len, rot, 1e4)
-    q = apply_qkv_decode(qkv, qw, kw, torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev),
-                         kc, vc, seqlen, num_heads=nq, num_kv_heads=nkv, head_dim=d, rotary_dim=rot)
+    q = apply_qkv_decode(qkv, qw, kw, _rope_rows(cos, seqlen, dev), _rope_rows(sin, seqlen, dev),
+                         kc, vc, seqlen, row_map=row_map, num_heads=nq, num_kv_heads=nkv,
+                         head_dim=d, rotary_dim=rot, use_rope=True, use_qk_norm=True, eps=1e-6)
     x = np_f(qkv)
+    touched = torch.zeros(rows, max_len, dtype=torch.bool, device=dev)
     for b, pos in enumerate(seqlen.tolist()):
         cs, sn = od.bf(cos[pos]), od.bf(sin[pos])
         ref_q = np.stack([od.head_norm_rope(x[b, h * d:(h + 1) * d], np_f(qw), cs, sn, rot, 1e-6)
                           for h in range(nq)])
         assert_bf16_close(np_f(q[b, :, 0]), ref_q, what=f"q row {b}")
+        r = crow[b]
         for kh in range(nkv):
             o0, o1 = (nq + kh) * d, (nq + nkv + kh) * d
             ref_k = od.head_norm_rope(x[b, o0:o0 + d], np_f(kw), cs, sn, rot, 1e-6)
-            assert_bf16_close(np_f(kc[b, kh, pos]), ref_k, what=f"k row {b}")
-            np.testing.assert_array_equal(np_f(vc[b, kh, pos]), x[b, o1:o1 + d])
-        mask = torch.ones(max_len, dtype=torch.bool, device=dev)
-        mask[pos] = False
-        assert torch.equal(kc[b][:, mask], k0[b][:, mask]) and torch.equal(vc[b][:, mask], v0[b][:, mask])
+            assert_bf16_close(np_f(kc[r, kh, pos]), ref_k, what=f"k row {b}")
+            np.testing.assert_array_equal(np_f(vc[r, kh, pos]), x[b, o1:o1 + d])
+        touched[r, pos] = True
+    untouched = ~touched
+    for r in range(rows):
+        assert torch.equal(kc[r][:, untouched[r]], k0[r][:, untouched[r]])
+        assert torch.equal(vc[r][:, untouched[r]], v0[r][:, untouched[r]])
 
 
 @pytest.mark.parametrize("window", [None, 512])
@@ -67,6 +81,52 @@ def test_gqa_ragged_vs_oracle(dev, window):
     # a row alone gives the same bits as in the batch
     solo = decode_gqa_attn(q[6:7], kc[6:7], vc[6:7], seqlen[6:7], scale=d ** -0.5, window=window)
     assert torch.equal(solo, out[6:7])
+
+
+@pytest.mark.parametrize("window", [None, 300])
+def test_fused_attention_equals_two_step(dev, window):
+    """decode_attention gives the bits of apply_qkv_decode + decode_gqa_attn
+    (q, the written K/V and the output), for ragged rows through a row map,
+    and leaves the workspace tickets at zero."""
+    nq, nkv, d, max_len, rot = 32, 4, 64, 1100, 32
+    seqlen = torch.tensor([0, 127, 128, 700, 1099], device=dev)
+    row_map = torch.tensor([3, 5, 0, 1, 4], device=dev)
+    qkv = synthetic.randn_bf16((5, (nq + 2 * nkv) * d), 21, dev)
+    kc = synthetic.randn_bf16((6, nkv, max_len, d), 22, dev)
+    vc = synthetic.randn_bf16((6, nkv, max_len, d), 23, dev)
+    qw = (torch.rand(d, device=dev) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(d, device=dev) + 0.5).to(torch.bfloat16)
+    cos, sin = od.rope_tables(max_len, rot, 1e4)
+    kc2, vc2 = kc.clone(), vc.clone()
+    q = apply_qkv_decode(qkv, qw, kw, _rope_rows(cos, seqlen, dev), _rope_rows(sin, seqlen, dev),
+                         kc, vc, seqlen, row_map=row_map, num_heads=nq, num_kv_heads=nkv,
+                         head_dim=d, rotary_dim=rot, use_rope=True, use_qk_norm=True, eps=1e-6)
+    ref = decode_gqa_attn(q, kc, vc, seqlen, row_map=row_map, scale=d ** -0.5, window=window)
+    ws = gqa_workspace(5, nkv, max_len, dev)
+    for _ in range(2):
+        out = decode_attention(qkv, qw, kw, torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev),
+                               kc2, vc2, seqlen, ws, row_map=row_map, num_heads=nq, num_kv_heads=nkv,
+                               head_dim=d, rotary_dim=rot, eps=1e-6, scale=d ** -0.5, window=window)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        assert torch.equal(kc2, kc) and torch.equal(vc2, vc)
+        assert int(ws[:5 * nkv * 4].count_nonzero()) == 0, "tickets not reset"
+    # and the output matches the oracle on the written cache
+    for b, n in enumerate((seqlen + 1).tolist()):
+        r = int(row_map[b])
+        o = od.gqa(np_f(q[b, :, 0]), np_f(kc[r]), np_f(vc[r]), n, d ** -0.5, window)
+        assert_bf16_close(np_f(out[b, :, 0]), o, atol_frac=2e-3, what=f"row {b}")
+
+
+def test_attention_rejects_bad_shapes(dev):
+    q = torch.zeros(2, 32, 1, 128, device=dev, dtype=torch.bfloat16)
+    kc = torch.zeros(2, 4, 64, 128, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        decode_gqa_attn(q, kc, kc, torch.zeros(2, device=dev, dtype=torch.int64), scale=1.0, window=None)
+    q = torch.zeros(2, 34, 1, 64, device=dev, dtype=torch.bfloat16)
+    kc = torch.zeros(2, 4, 64, 64, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        decode_gqa_attn(q, kc, kc, torch.zeros(2, device=dev, dtype=torch.int64), scale=1.0, window=None)
 
 
 def _to_np(model: SyntheticDecoder) -> dict:
