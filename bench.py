@@ -79,8 +79,8 @@ def graph_of(fn):
 
 
 def read_traffic(kernel: str):
-    """HBM bytes per launch from profiles/<kernel>_traffic.md, if measured."""
-    p = ROOT / "profiles" / f"{kernel}_traffic.md"
+    """HBM bytes per launch from profiles/<kernel>_traffic.txt, if measured."""
+    p = ROOT / "profiles" / f"{kernel}_traffic.txt"
     if not p.exists():
         return None
     m = re.search(r"hbm_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
@@ -223,6 +223,41 @@ def cpu_baseline(seconds: float = 12.0) -> dict:
     }
 
 
+def counters_pass(dev, n_layers: int) -> int:
+    """Workload for rocprofv3 --pmc passes (FETCH_SIZE / WRITE_SIZE per
+    dispatch): the SwiGLU expert kernel over ``n_layers`` cold layers, twice,
+    then a plain 256 MiB device copy four times to calibrate the counter
+    against a known byte count.  Traffic does not depend on the weight values,
+    so the layers are left uninitialised and the 8 experts of layer l are fixed
+    (8l .. 8l+7 mod 64): no random-number kernels run under the profiler."""
+    import torch
+
+    from maple_amd.kernels import ternary_expert_swiglu
+
+    kw = HIDDEN // 16
+    ug = [torch.empty(EXPERTS, 2 * INTER, kw, device=dev, dtype=torch.int32).view(torch.uint32)
+          for _ in range(n_layers)]
+    ua = [torch.empty(EXPERTS, 2 * INTER, device=dev, dtype=torch.bfloat16) for _ in range(n_layers)]
+    ids = [torch.tensor([[(8 * l + j) % EXPERTS for j in range(TOPK)]], dtype=torch.int32).to(dev)
+           for l in range(n_layers)]
+    x = torch.ones(1, HIDDEN, dtype=torch.bfloat16).to(dev)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        for l in range(n_layers):
+            ternary_expert_swiglu(x, ug[l], ua[l], ids[l])
+    torch.cuda.synchronize()
+    a = torch.empty(128 << 20, device=dev, dtype=torch.bfloat16)
+    b = torch.empty_like(a)
+    for _ in range(4):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"counters_pass": True, "swiglu_launches": 2 * n_layers,
+                      "swiglu_bytes_per_launch": layer_bytes()["swiglu_launch"],
+                      "copy_bytes_read": a.numel() * 2, "copy_bytes_written": a.numel() * 2}),
+          flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -253,6 +288,8 @@ def main() -> int:
     torch.cuda.set_device(dev)
     nb = layer_bytes()
     L = args.layers
+    if args.counters_pass:
+        return counters_pass(dev, L)
     log(f"building {L} cold MoE layers ...")
     layers = [synthetic.make_moe_layer(HIDDEN, EXPERTS, INTER, seed=i, device=dev) for i in range(L)]
     x = synthetic.randn_bf16((1, HIDDEN), 12345, dev)
@@ -298,17 +335,6 @@ def main() -> int:
     if router_wait_timed_out(dev):
         log("router reported a timed-out wait: results invalid")
         return 1
-    if args.counters_pass:
-        # Calibration copy: 256 MiB read + 256 MiB written per launch.
-        a = torch.empty(128 << 20, device=dev, dtype=torch.bfloat16).fill_(1)
-        b = torch.empty_like(a)
-        for _ in range(4):
-            b.copy_(a)
-        torch.cuda.synchronize()
-        print(json.dumps({"counters_pass": True, "swiglu_launches": (args.steps + args.warmup + 1) * L,
-                          "copy_bytes": a.numel() * 2}), flush=True)
-        return 0
-
     out = {
         "metric": METRIC,
         "value": round(value, 2),
