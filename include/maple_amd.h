@@ -191,6 +191,39 @@ int ma_moe_grouped(const void* x, int64_t ldx, int64_t tokens, int64_t top_k,
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * One token through the whole MoE layer in ONE launch (decode batch 1):
+ * router (x @ gate_weight^T + bias, softmax, top-k, renormalise), expert
+ * SwiGLU (h in bf16), down projections and the weighted combine, + residual;
+ * y bf16 [hidden], topk_ids int32 [top_k], topk_weight float32 [top_k].
+ * With x_add != NULL the block first computes s = x + x_add (float32) and runs
+ * on bf16(rms_norm(s) * norm_weight) with residual bf16(s) (the decoder's
+ * post-attention add + RMSNorm); otherwise residual may be NULL.  bf16 x,
+ * gate weight and row scales.  Built shapes (hidden, inter, top_k): (2048,
+ * 768, 8) and (256, 128, 2); experts <= 256; other shapes return MA_EVALUE
+ * (use the per-kernel entry points).  workspace:
+ * ma_moe_fused_workspace_bytes(...) bytes, zero-filled before its first use
+ * and never cleared again (the kernel keeps a monotonic counter there);
+ * calls sharing a workspace must not overlap.  A cross-workgroup
+ * wait that exceeds about 0.2 s sets the word read by ma_moe_fused_timed_out
+ * instead of hanging.  Replaces MapleSparseMoeBlock.__call__ at T = 1,
+ * src/maple_run/model.py:448-474 (router_topk, ternary_expert_swiglu,
+ * ternary_expert_gemv, moe_reduce_add: four launches there), optionally with
+ * add_rms_norm, src/maple_run/kernels/fused_norm.py:128-161.
+ */
+size_t ma_moe_fused_workspace_bytes(int64_t n_experts, int64_t hidden, int64_t inter,
+                                    int64_t top_k);
+int ma_moe_fused(const void* x, const void* x_add, const void* norm_weight, int norm_dtype,
+                 float eps, const void* residual, const void* gate_weight,
+                 const float* router_bias, int64_t n_experts, int64_t hidden, int64_t inter,
+                 int64_t top_k, const uint32_t* up_gate, const void* up_gate_alpha,
+                 const uint32_t* down, const void* down_alpha, void* y, int32_t* topk_ids,
+                 float* topk_weight, void* workspace, size_t workspace_bytes, void* stream);
+/* *out = 1 if any ma_moe_fused call on this workspace timed out waiting
+ * (synchronises the stream).  No reference counterpart: the reference has no
+ * cross-workgroup wait. */
+int ma_moe_fused_timed_out(const void* workspace, int* out, void* stream);
+
+/*
  * Decode (q_len = 1) QK RMSNorm + partial RoPE + KV write.  qkv bf16
  * [batch, (n_heads + 2 n_kv_heads) * head_dim] (row stride ldq); per head
  * x * rsqrt(mean(x^2) + eps) * w (q_norm_w / k_norm_w [head_dim] of w_dtype),

@@ -47,11 +47,16 @@ _SIGNATURES = {
     "ma_decode_gqa_attn": [_P, _L, _I, _I, _I, _P, _P, _L, _L, _P, _P, _L, _F, _P, _P, _Z, _P],
     "ma_decode_attn_fused": [_P, _L, _L, _I, _I, _I, _P, _P, _I, _P, _P, _I, _L, _L, _I, _I, _F,
                              _P, _P, _P, _P, _L, _L, _L, _F, _P, _P, _Z, _P],
+    "ma_moe_fused_workspace_bytes": [_L, _L, _L, _L],
+    "ma_moe_fused": [_P, _P, _P, _I, _F, _P, _P, _P, _L, _L, _L, _L, _P, _P, _P, _P, _P, _P, _P, _P,
+                     _Z, _P],
+    "ma_moe_fused_timed_out": [_P, _P, _P],
     "ma_moe_grouped": [_P, _L, _L, _L, _P, _P, _P, _P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _I,
                        _P, _L, _P, _P, _Z, _P],
 }
 _RESTYPES = {"ma_last_error": ctypes.c_char_p, "ma_router_workspace_bytes": _Z,
-             "ma_grouped_workspace_bytes": _Z, "ma_gqa_workspace_bytes": _Z}
+             "ma_grouped_workspace_bytes": _Z, "ma_gqa_workspace_bytes": _Z,
+             "ma_moe_fused_workspace_bytes": _Z}
 
 _lib = None
 

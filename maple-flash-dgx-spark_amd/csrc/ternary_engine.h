@@ -83,4 +83,49 @@ __device__ __forceinline__ float slice_dot(const uint32_t wv[KW], const XSlice<K
   return (a0 + a1) - xs.c;
 }
 
+// The fast kernels take int32 ids only (one scalar load, no dtype branch).
+__device__ __forceinline__ int64_t clamp_id(int32_t e, int64_t n_exp) {
+  return e < 0 ? 0 : (e >= n_exp ? n_exp - 1 : e);
+}
+
+
+// ---------------------------------------------------------------------------
+// x' staging in LDS: one workgroup prepares the pairs of one bf16 activation
+// row once (thread t -> word t), so its waves do not each reload and
+// re-convert x.  xs[w][j] = pair j of word w, cw[w] = sum (f_j + 1) x over w.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void stage_row(const uint16_t* __restrict__ row, int64_t nwords,
+                                          uint32_t (*xs)[8], float* cw) {
+  for (int64_t wi = threadIdx.x; wi < nwords; wi += blockDim.x) {
+    const uint4 a = reinterpret_cast<const uint4*>(row + wi * 16)[0];
+    const uint4 b = reinterpret_cast<const uint4*>(row + wi * 16)[1];
+    const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      v[2 * q] = __uint_as_float(u[q] << 16);
+      v[2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
+    }
+    uint32_t pr[8];
+    cw[wi] = prep_word_pairs(v, pr);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xs[wi][j] = pr[j];
+  }
+}
+
+template <int KW>
+__device__ __forceinline__ void slice_from_lds(const uint32_t (*xs)[8], const float* cw, int kl,
+                                               XSlice<KW>& out) {
+  out.c = 0.f;
+#pragma unroll
+  for (int i = 0; i < KW; ++i) {
+    const int w = kl * KW + i;
+    const uint4 lo = *reinterpret_cast<const uint4*>(&xs[w][0]);
+    const uint4 hi = *reinterpret_cast<const uint4*>(&xs[w][4]);
+    out.xp[i][0] = lo.x; out.xp[i][1] = lo.y; out.xp[i][2] = lo.z; out.xp[i][3] = lo.w;
+    out.xp[i][4] = hi.x; out.xp[i][5] = hi.y; out.xp[i][6] = hi.z; out.xp[i][7] = hi.w;
+    out.c += cw[w];
+  }
+}
+
 }  // namespace ma

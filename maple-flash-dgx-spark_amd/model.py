@@ -9,6 +9,8 @@ One decode step, per layer:
   o     = ternary_gemv(attn, W_o)
   hidden, mlp_in = add_rms_norm(hidden, o, post_ln)
   hidden = moe_block(mlp_in, residual=hidden)
+  (with fused_moe=True at batch 1, when built for the shape, the last two
+  lines are one launch: moe_fused(hidden, add=o, norm_weight=post_ln))
 then seqlen += 1, final rms_norm, RTN4 lm_head, greedy argmax.
 
 Weights are random with the synthetic distributions (``synthetic.py``): every
@@ -28,7 +30,7 @@ from .kernels.decode_attn import decode_attention, gqa_workspace
 from .kernels.fused_norm import add_rms_norm, rms_norm
 from .kernels.rtn4 import rtn4_embedding, rtn4_gemv
 from .kernels.ternary_gemv import ternary_gemv
-from .moe import moe_block
+from .moe import fused_supported, moe_block, moe_fused
 
 
 @dataclass
@@ -94,8 +96,10 @@ class KVCache:
 
 
 class SyntheticDecoder:
-    def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 4096 + 128):
+    def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 4096 + 128,
+                 fused_moe: bool = False):
         self.cfg = cfg
+        self.fused_moe = fused_moe
         self.device = torch.device(device)
         self.max_len = max_len
         c, dev, s = cfg, self.device, seed * 1000
@@ -139,8 +143,12 @@ class SyntheticDecoder:
                                 num_kv_heads=c.kv_heads, head_dim=c.head_dim,
                                 rotary_dim=c.rotary_dim, eps=c.eps, scale=c.head_dim ** -0.5)
         o = ternary_gemv(attn.reshape(bsz, -1), L.o, L.o_alpha)
-        hidden, mlp_in = add_rms_norm(hidden, o, L.post_ln, c.eps)
-        y, ids, _ = moe_block(mlp_in, L.moe, c.top_k, residual=hidden)
+        if bsz == 1 and self.fused_moe and fused_supported(L.moe, c.top_k, hidden):
+            # add + RMSNorm + router + experts + combine in one launch
+            y, ids, _ = moe_fused(hidden, L.moe, c.top_k, add=o, norm_weight=L.post_ln, eps=c.eps)
+        else:
+            hidden, mlp_in = add_rms_norm(hidden, o, L.post_ln, c.eps)
+            y, ids, _ = moe_block(mlp_in, L.moe, c.top_k, residual=hidden)
         if routing is not None:
             routing.append(ids)
         return y

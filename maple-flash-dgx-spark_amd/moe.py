@@ -5,6 +5,12 @@ router -> up+gate SwiGLU -> down -> top-k combine (+ residual), with no host
 sync and no per-expert Python loop.  Two execution plans, chosen by the token
 count alone (never by routing, which stays on the device):
 
+* ``plan="fused"`` (one token, shapes built into ``ma_moe_fused``): router,
+  SwiGLU, down and combine (optionally with the add + RMSNorm ahead of the
+  block) in one persistent launch.  Measured slower than the per-slot chain
+  (23 us against 14.3 us per layer at hidden 2048 / 64 experts): its phases
+  are a longer chain of dependent memory round trips than three launches
+  are, so "auto" does not pick it.
 * decode (``tokens < GROUPED_MIN_TOKENS``): per-slot kernels, as the
   reference does -- fused SwiGLU, then the down projection and the combine in
   one launch (``ternary_expert_down_sum``).  That skips the reference's bf16
@@ -28,6 +34,78 @@ from .kernels.ternary_expert import ternary_expert_down_sum, ternary_expert_swig
 from .synthetic import MoELayer
 
 GROUPED_MIN_TOKENS = 4
+
+# One zero-filled workspace per device for the one-launch layer kernel: calls
+# hand data between workgroups through it, tagged by a generation counter the
+# kernel advances, so it is never cleared again.  Calls on one device must not
+# overlap (decode runs from one stream).
+_FUSED_WS: dict[int, torch.Tensor] = {}
+
+
+def _fused_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _FUSED_WS.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 16), device=device, dtype=torch.uint8)
+        _FUSED_WS[idx] = ws
+    return ws
+
+
+def fused_supported(layer: MoELayer, top_k: int, x: torch.Tensor) -> bool:
+    """True if ``ma_moe_fused`` is built for this layer's shape and dtypes."""
+    if x.dtype != torch.bfloat16 or layer.gate_weight.dtype != torch.bfloat16:
+        return False
+    if layer.up_gate_alpha.dtype != torch.bfloat16 or layer.down_alpha.dtype != torch.bfloat16:
+        return False
+    return int(_lib.load().ma_moe_fused_workspace_bytes(layer.n_experts, layer.hidden, layer.inter,
+                                                        top_k)) > 0
+
+
+def moe_fused_timed_out(device: torch.device | int = 0) -> bool:
+    """True if a one-launch MoE call on ``device`` ever timed out waiting for
+    another workgroup (the kernel records it instead of hanging).  Syncs."""
+    idx = device if isinstance(device, int) else (device.index or 0)
+    ws = _FUSED_WS.get(idx)
+    return bool(ws is not None and int(ws[8:12].view(torch.int32).item()) != 0)
+
+
+def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tensor | None = None,
+              *, add: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None,
+              eps: float = 1e-6):
+    """One token through the whole MoE layer in one launch.
+
+    Plain: ``y = x_res + sum_j w_j down_j(swiglu_j(x))`` with ``x_res =
+    residual`` (or none).  With ``add``/``norm_weight`` (the decoder's
+    post-attention add + RMSNorm, ``fused_norm.py:128-161``): ``s = x + add``,
+    the block runs on ``rms_norm(s) * norm_weight`` and adds ``bf16(s)``.
+    Returns ``(y [1, H], ids int32 [1, k], weights float32 [1, k])``.
+    """
+    hidden = x.shape[-1]
+    xf = x.reshape(1, hidden).contiguous()
+    ad = None if add is None else add.reshape(1, hidden).contiguous()
+    if ad is not None and norm_weight is None:
+        raise ValueError("moe_fused: add needs norm_weight")
+    res = None if residual is None or ad is not None else residual.reshape(1, hidden).contiguous()
+    nbytes = int(_lib.load().ma_moe_fused_workspace_bytes(layer.n_experts, hidden, layer.inter, top_k))
+    if nbytes == 0:
+        raise ValueError(f"moe_fused: shape (hidden {hidden}, inter {layer.inter}, top_k {top_k}) "
+                         "is not built into the one-launch kernel")
+    ws = _fused_workspace(x.device, nbytes)
+    y = torch.empty(1, hidden, device=x.device, dtype=torch.bfloat16)
+    ids = torch.empty(1, top_k, device=x.device, dtype=torch.int32)
+    wts = torch.empty(1, top_k, device=x.device, dtype=torch.float32)
+    nw = None if norm_weight is None else norm_weight.reshape(-1).contiguous()
+    bias = None if layer.router_bias is None else layer.router_bias.float().contiguous()
+    _lib.call(
+        "ma_moe_fused",
+        _lib.ptr(xf), _lib.ptr(ad), _lib.ptr(nw),
+        _lib.dtype_code(nw, "norm_weight") if nw is not None else 0, float(eps), _lib.ptr(res),
+        _lib.ptr(layer.gate_weight), _lib.ptr(bias), layer.n_experts, hidden, layer.inter, top_k,
+        _lib.ptr(layer.up_gate_packed), _lib.ptr(layer.up_gate_alpha), _lib.ptr(layer.down_packed),
+        _lib.ptr(layer.down_alpha), _lib.ptr(y), _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(ws),
+        ws.numel(), _lib.stream_of(x),
+    )
+    return y, ids, wts
 
 
 def moe_grouped(x: torch.Tensor, layer: MoELayer, ids: torch.Tensor, wts: torch.Tensor,
@@ -66,13 +144,20 @@ def moe_grouped(x: torch.Tensor, layer: MoELayer, ids: torch.Tensor, wts: torch.
     return y
 
 
-def moe_block(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tensor | None = None):
-    """One MoE layer on ``x [..., H]``; returns ``(y, ids, weights)``."""
+def moe_block(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tensor | None = None,
+              *, plan: str = "auto"):
+    """One MoE layer on ``x [..., H]``; returns ``(y, ids, weights)``.
+
+    ``plan``: "auto" (grouped MFMA from GROUPED_MIN_TOKENS tokens, per-slot
+    kernels below), or "per_slot" / "grouped" / "fused" to force one."""
     hidden = x.shape[-1]
     xf = x.reshape(-1, hidden)
+    if plan == "fused":
+        y, ids, wts = moe_fused(xf, layer, top_k, residual)
+        return y.reshape(x.shape), ids, wts
     ids, wts = router_topk(xf, layer.gate_weight, top_k, bias=layer.router_bias)
     res = None if residual is None else residual.reshape(-1, hidden)
-    if xf.shape[0] >= GROUPED_MIN_TOKENS and xf.dtype == torch.bfloat16 \
+    if plan == "grouped" or plan == "auto" and xf.shape[0] >= GROUPED_MIN_TOKENS and xf.dtype == torch.bfloat16 \
             and hidden % 256 == 0 and layer.inter % 256 == 0:
         y = moe_grouped(xf, layer, ids, wts, res)
     else:

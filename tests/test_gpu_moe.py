@@ -53,7 +53,9 @@ def test_moe_block_decode_vs_oracle(dev, layer, tokens):
     _check_routing(x, layer, ids, wts)
     ref, _ = ok.moe_experts(np_f(x), ids.cpu().numpy(), wts.cpu().numpy(), *_oracle_inputs(layer),
                             residual=np_f(res))
-    assert_bf16_close(np_f(y), ref, what=f"moe bs{tokens}")
+    # two bf16 rounding points (h; each slot's down output in the oracle and
+    # the one-launch kernel): the grouped path's 2^-7 absolute tolerance
+    assert_bf16_close(np_f(y), ref, atol_frac=2.0 ** -7, what=f"moe bs{tokens}")
 
 
 @pytest.mark.parametrize("tokens", [32, 128, 2048])

@@ -1,0 +1,132 @@
+"""One-launch MoE layer (``ma_moe_fused``) vs the CPU oracle (needs the GPU).
+
+Decode batch 1 at the synthetic shapes: hidden 2048, 64 experts,
+intermediate 768, top-8 (plain, with residual, with a Zipf router bias, and
+with the decoder's add + RMSNorm in front), and the small smoke shape (hidden
+256, 8 experts, intermediate 128, top-2).  Routing is checked against the
+oracle's own top-k (ids exact where the k-th and (k+1)-th probabilities are
+separated), y against the oracle on the kernel's routing.  y passes two bf16
+rounding points (h, and each slot's down output, as the reference stores
+them), so an input near a rounding boundary can land one bf16 ulp of that
+intermediate away: y's absolute tolerance is 2^-7 of its scale (as for the
+grouped path), the relative bound 1e-2 as everywhere.  Many consecutive
+calls on one workspace (each call tags its data with a new generation), graph
+replays equal to eager calls, and no cross-workgroup wait ever timing out.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import assert_bf16_close, np_f, np_u32, tie_safe_rows
+from maple_amd import synthetic
+from maple_amd.moe import moe_block, moe_fused, moe_fused_timed_out
+from oracle import kernels as ok
+
+pytestmark = pytest.mark.gpu
+
+
+Y_ATOL = 2.0 ** -7
+
+
+def _oracle(x, L, ids, wts, k, residual=None):
+    rid, rw, probs = ok.router_topk(x, np_f(L.gate_weight), k,
+                                    bias=None if L.router_bias is None else np_f(L.router_bias))
+    safe = tie_safe_rows(probs, k)
+    idn, wn = ids.cpu().numpy(), wts.cpu().numpy()
+    np.testing.assert_array_equal(idn[safe], rid[safe])
+    np.testing.assert_allclose(wn[safe], rw[safe], rtol=1e-4, atol=1e-6)
+    y, _ = ok.moe_experts(x, idn, wn, np_u32(L.up_gate_packed), np_f(L.up_gate_alpha),
+                          np_u32(L.down_packed), np_f(L.down_alpha), residual=residual)
+    return y
+
+
+@pytest.fixture(scope="module")
+def layers(dev):
+    return [synthetic.make_moe_layer(2048, 64, 768, seed=40 + i, device=dev) for i in range(3)]
+
+
+@pytest.mark.parametrize("with_res", [False, True])
+def test_fused_plain_vs_oracle(dev, layers, with_res):
+    for step in range(4):  # consecutive calls over different layers
+        L = layers[step % len(layers)]
+        x = synthetic.randn_bf16((1, 2048), 500 + step, dev)
+        res = synthetic.randn_bf16((1, 2048), 600 + step, dev) if with_res else None
+        y, ids, wts = moe_fused(x, L, 8, res)
+        torch.cuda.synchronize()
+        ref = _oracle(np_f(x), L, ids, wts, 8, None if res is None else np_f(res))
+        assert_bf16_close(np_f(y), ref, atol_frac=Y_ATOL, what=f"fused step {step}")
+    assert not moe_fused_timed_out(dev)
+
+
+def test_fused_zipf_bias_vs_oracle(dev, layers):
+    L0 = layers[0]
+    L = synthetic.MoELayer(L0.gate_weight, L0.up_gate_packed, L0.up_gate_alpha, L0.down_packed,
+                           L0.down_alpha, synthetic.zipf_router_bias(64, 1.1, 1.0, seed=3).to(dev))
+    for step in range(3):
+        x = synthetic.randn_bf16((1, 2048), 700 + step, dev)
+        y, ids, wts = moe_block(x, L, 8, plan="fused")
+        torch.cuda.synchronize()
+        assert_bf16_close(np_f(y), _oracle(np_f(x), L, ids, wts, 8), atol_frac=Y_ATOL, what=f"zipf step {step}")
+
+
+def test_fused_add_norm_vs_oracle(dev, layers):
+    L = layers[1]
+    a = synthetic.randn_bf16((1, 2048), 801, dev)
+    b = synthetic.randn_bf16((1, 2048), 802, dev, std=0.5)
+    w = torch.rand(2048, device=dev) + 0.5
+    y, ids, wts = moe_fused(a, L, 8, add=b, norm_weight=w, eps=1e-6)
+    torch.cuda.synchronize()
+    s = np_f(a) + np_f(b)
+    res = ok.bf16_round(s).astype(np.float64)
+    x = ok.bf16_round(ok.rms_norm(s, np_f(w), 1e-6)).astype(np.float64)
+    assert_bf16_close(np_f(y), _oracle(x, L, ids, wts, 8, res), atol_frac=Y_ATOL, what="add+norm")
+
+
+def test_fused_small_shape_vs_oracle(dev):
+    L = synthetic.make_moe_layer(256, 8, 128, seed=9, device=dev)
+    for step in range(3):
+        x = synthetic.randn_bf16((1, 256), 900 + step, dev)
+        y, ids, wts = moe_fused(x, L, 2)
+        torch.cuda.synchronize()
+        assert_bf16_close(np_f(y), _oracle(np_f(x), L, ids, wts, 2), atol_frac=Y_ATOL, what=f"small {step}")
+
+
+def test_fused_agrees_with_per_slot_plan(dev, layers):
+    L = layers[2]
+    x = synthetic.randn_bf16((1, 2048), 1001, dev)
+    y1, i1, w1 = moe_block(x, L, 8, plan="fused")
+    y2, i2, w2 = moe_block(x, L, 8, plan="per_slot")
+    torch.cuda.synchronize()
+    assert torch.equal(i1, i2)
+    torch.testing.assert_close(w1, w2, rtol=1e-6, atol=1e-7)
+    assert_bf16_close(np_f(y1), np_f(y2), atol_frac=Y_ATOL, what="fused vs per-slot")
+
+
+def test_fused_graph_replays_match_eager(dev, layers):
+    xs = [synthetic.randn_bf16((1, 2048), 1100 + i, dev) for i in range(6)]
+    eager = [moe_fused(xs[i], layers[i % 3], 8)[0].clone() for i in range(6)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        [moe_fused(xs[i], layers[i % 3], 8) for i in range(6)]
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = [moe_fused(xs[i], layers[i % 3], 8)[0] for i in range(6)]
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for i in range(6):
+            assert torch.equal(outs[i], eager[i]), f"replay {rep} layer {i}"
+        torch.zeros(1, device=dev).add_(1)  # eager work between replays
+    assert not moe_fused_timed_out(dev)
+
+
+def test_fused_rejects_unbuilt_shape(dev):
+    L = synthetic.make_moe_layer(512, 8, 256, seed=1, device=dev)
+    with pytest.raises(ValueError):
+        moe_fused(synthetic.randn_bf16((1, 512), 1, dev), L, 2)
