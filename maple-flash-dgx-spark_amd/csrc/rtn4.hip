@@ -203,6 +203,11 @@ static bool rtn4_fast_launch(const void* x, int64_t batch, int64_t ldx, const ui
 
 using namespace ma;
 
+// Batched MFMA path (dense_mfma.hip) for batch >= 5.
+int launch_rtn4_mfma(const uint16_t* x, int64_t batch, int64_t ldx, const uint32_t* w,
+                     int64_t n_out, int64_t nwords, int64_t group, const void* scales,
+                     const void* biases, int s_dt, uint16_t* y, int64_t ldy, hipStream_t s);
+
 extern "C" int ma_rtn4_gemv(const void* x, int x_dtype, int64_t batch, int64_t ldx,
                             const uint32_t* packed, int64_t n_out, int64_t nwords, int packed_kn,
                             const void* scales, int scales_dtype, const void* biases,
@@ -217,6 +222,11 @@ extern "C" int ma_rtn4_gemv(const void* x, int x_dtype, int64_t batch, int64_t l
   const bool fast = x_dtype == MA_BF16 && !packed_kn && scales_dtype == biases_dtype &&
                     (scales_dtype == MA_BF16 || scales_dtype == MA_F32) && (ldx % 8) == 0 &&
                     ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(packed)) & 15u) == 0;
+  if (fast && batch >= 5 && (group_size == 64 || group_size == 128) && nwords % 16 == 0 &&
+      (reinterpret_cast<uintptr_t>(y) & 15u) == 0)
+    return launch_rtn4_mfma(static_cast<const uint16_t*>(x), batch, ldx, packed, n_out, nwords,
+                            group_size, scales, biases, scales_dtype, static_cast<uint16_t*>(y),
+                            ldy, s);
   if (fast) {
     bool done;
     if (batch >= 4)

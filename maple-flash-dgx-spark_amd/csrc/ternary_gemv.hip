@@ -95,6 +95,23 @@ void tgemv_generic(const void* x, int x_dtype, int64_t batch, int64_t ldx, const
 
 }  // namespace ma
 
+// Batched MFMA path (dense_mfma.hip), batch >= kMfmaMinBatch.
+int launch_tgemm_mfma(const uint16_t* x, int64_t batch, int64_t ldx, const uint32_t* w,
+                      int64_t n_out, int64_t nwords, const void* alpha, int alpha_dt,
+                      const void* rms_w, int rms_dt, float rms_eps, uint16_t* y, int64_t ldy,
+                      hipStream_t s);
+constexpr int64_t kMfmaMinBatch = 5;
+
+static bool mfma_ok(const void* x, int x_dtype, int64_t batch, int64_t ldx, const uint32_t* packed,
+                    int64_t nwords, int packed_kn, int alpha_dtype, const void* rms_weight,
+                    int rms_dtype, const void* y) {
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  return batch >= kMfmaMinBatch && x_dtype == MA_BF16 && !packed_kn && nwords % 16 == 0 &&
+         (alpha_dtype == MA_BF16 || alpha_dtype == MA_F32) &&
+         (!rms_weight || rms_dtype == MA_F32 || rms_dtype == MA_BF16 || rms_dtype == MA_F16) &&
+         a16(x) && ldx % 8 == 0 && a16(packed) && a16(y);
+}
+
 extern "C" int ma_ternary_gemv(const void* x, int x_dtype, int64_t batch, int64_t ldx,
                                const uint32_t* packed, int64_t n_out, int64_t nwords,
                                int packed_kn, const void* row_alpha, int alpha_dtype,
@@ -109,6 +126,11 @@ extern "C" int ma_ternary_gemv(const void* x, int x_dtype, int64_t batch, int64_
   if (ldx < nwords * 16 || ldy < n_out)
     return fail(MA_EVALUE, "ternary_gemv: leading dimension too small");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (mfma_ok(x, x_dtype, batch, ldx, packed, nwords, packed_kn, alpha_dtype, rms_weight,
+              rms_dtype, y))
+    return launch_tgemm_mfma(static_cast<const uint16_t*>(x), batch, ldx, packed, n_out, nwords,
+                             row_alpha, alpha_dtype, rms_weight, rms_dtype, rms_eps,
+                             static_cast<uint16_t*>(y), ldy, s);
   if (!tgemv_fast(x, x_dtype, batch, ldx, packed, n_out, nwords, packed_kn, row_alpha,
                   alpha_dtype, rms_weight, rms_dtype, rms_eps, y, ldy, s))
     tgemv_generic(x, x_dtype, batch, ldx, packed, n_out, nwords, packed_kn, row_alpha,

@@ -261,6 +261,31 @@ def test_expert_ids_out_of_range_are_clamped_not_faulting(dev):
                                ternary_expert_swiglu(x, L.up_gate_packed, L.up_gate_alpha, good))
 
 
+@pytest.mark.parametrize("batch,n_out,k_in", [(5, 2560, 2048), (16, 200, 256), (33, 2048, 2048),
+                                                (64, 130, 512)])
+def test_gemv_mfma_batched_vs_oracle(dev, batch, n_out, k_in):
+    """Batch >= 5 runs the MFMA GEMM: partial row tiles, more than one token
+    tile, and batched == per-row (reference tests/test_ternary_gemv.py:227-247)."""
+    w = synthetic.ternary_packed((n_out, k_in), 41 + batch, dev)
+    alpha = synthetic.uniform_bf16((n_out,), 0.01, 0.05, 42, dev)
+    x = synthetic.randn_bf16((batch, k_in), 43, dev)
+    y = ternary_gemv(x, w, alpha)
+    assert_bf16_close(np_f(y), ok.ternary_gemv(np_f(x), np_u32(w), np_f(alpha)), what=f"mfma B={batch}")
+    rows = torch.cat([ternary_gemv(x[i:i + 1], w, alpha) for i in range(batch)])
+    torch.testing.assert_close(y, rows, rtol=8e-3, atol=8e-3)
+
+
+@pytest.mark.parametrize("batch", [6, 48])
+def test_gemv_mfma_fused_rms_vs_oracle(dev, batch):
+    w = synthetic.ternary_packed((2560, 2048), 51, dev)
+    alpha = synthetic.uniform_bf16((2560,), 0.01, 0.05, 52, dev).float()
+    x = synthetic.randn_bf16((batch, 2048), 53, dev)
+    rms_w = (torch.rand(2048, device=dev) + 0.5).to(torch.bfloat16)
+    y = ternary_gemv(x, w, alpha, rms_weight=rms_w, rms_eps=1e-6)
+    ref = ok.ternary_gemv(np_f(x), np_u32(w), np_f(alpha), rms_weight=np_f(rms_w), rms_eps=1e-6)
+    assert_bf16_close(np_f(y), ref, what=f"mfma rms B={batch}")
+
+
 # ---------------------------------------------------------------- RTN4 / norms
 @pytest.mark.parametrize("batch,group", [(1, 128), (1, 64), (2, 128), (4, 64), (32, 128)])
 def test_rtn4_gemv_vs_oracle(dev, batch, group):
@@ -269,6 +294,21 @@ def test_rtn4_gemv_vs_oracle(dev, batch, group):
     y = rtn4_gemv(x, w, sc, bs, group_size=group)
     ref = ok.rtn4_gemv(np_f(x), np_u32(w), np_f(sc), np_f(bs), group_size=group)
     assert_bf16_close(np_f(y), ref, what=f"rtn4 B={batch} g={group}")
+
+
+@pytest.mark.parametrize("batch,group,n_out", [(5, 64, 4000), (16, 128, 4096), (32, 64, 1000),
+                                               (40, 128, 4096)])
+def test_rtn4_mfma_batched_vs_oracle(dev, batch, group, n_out):
+    """Batch >= 5 runs the MFMA RTN4 GEMM (both group sizes, partial row
+    tiles, several token tiles); batched == per-row within 8e-3
+    (reference tests/test_rtn4.py:151-169)."""
+    w, sc, bs = synthetic.rtn4_table(n_out, 2048, group, 93 + batch, dev)
+    x = synthetic.randn_bf16((batch, 2048), 94, dev)
+    y = rtn4_gemv(x, w, sc, bs, group_size=group)
+    ref = ok.rtn4_gemv(np_f(x), np_u32(w), np_f(sc), np_f(bs), group_size=group)
+    assert_bf16_close(np_f(y), ref, what=f"rtn4 mfma B={batch} g={group}")
+    rows = torch.cat([rtn4_gemv(x[i:i + 1], w, sc, bs, group_size=group) for i in range(batch)])
+    torch.testing.assert_close(y, rows, rtol=8e-3, atol=8e-3)
 
 
 def test_rtn4_reference_fixture_fp32_and_kn(dev):
