@@ -26,12 +26,10 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// Round-to-nearest-even float -> bf16 (NaN stays a quiet NaN).  Branch-free.
+// Round-to-nearest-even float -> bf16 (NaN stays a NaN): gfx950's
+// v_cvt_pk_bf16_f32, one instruction.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t r = u + 0x7fffu + ((u >> 16) & 1u);
-  const uint32_t q = ((u & 0x7fffffffu) > 0x7f800000u) ? (u | 0x00400000u) : r;
-  return static_cast<uint16_t>(q >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 // bf16 bits of a float known to be exactly representable in bf16.
@@ -129,7 +127,9 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 // Round two floats to bf16 (nearest even) and pack them, lo in the low half.
 __device__ __forceinline__ uint32_t pack_bf16x2_rn(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+  const bf16x2v_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // x' pairs for one word from 16 consecutive activations xs[0..15] (already

@@ -5,8 +5,9 @@
 // lm_head (_rtn4_gemm_kernel, src/maple_run/kernels/rtn4.py:170-282, in the
 // factored per-group form s_g (q.x)_g + b_g sum_g x of :197-208).
 //
-// y[t, n] for a tile of 128 rows (4 waves x 2 blocks of 16) and 16*NB tokens,
-// K walked in chunks of 16 words.  v_mfma_f32_16x16x32_bf16 layouts (checked
+// y[t, n] for a tile of rows (4 waves x MB blocks of 16; the ternary GEMM uses
+// MB = 1, the RTN4 one MB = 2) and 16*NB tokens, K walked in chunks of 16
+// words with the next chunk's weights and activations loaded ahead.  v_mfma_f32_16x16x32_bf16 layouts (checked
 // on the device): A lane l holds row l%16, k 8(l/16)..+8; B col l%16, k
 // 8(l/16)..+8; C col l%16, rows 4(l/16)..+4.
 //
@@ -36,20 +37,49 @@ constexpr uint32_t kMaskQ4d = 0x00780078u;
 // Ternary: y = alpha (.) (T x_hat) [* rsqrt(mean(x^2) + eps) with RMS], where
 // x_hat = x * w_rms split as hi + lo bf16 when RMS.
 // ---------------------------------------------------------------------------
-template <int NB, bool RMS, int ADT>
+// 16 weights of the input RMSNorm (float32 or bf16) for K positions 16 wd ..
+__device__ __forceinline__ void load_rms16(const void* p, int rdt, int64_t wd, float out[16]) {
+  if (rdt == MA_F32) {
+    const uint4* q = reinterpret_cast<const uint4*>(static_cast<const float*>(p) + wd * 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 v = q[i];
+      out[4 * i] = __uint_as_float(v.x);
+      out[4 * i + 1] = __uint_as_float(v.y);
+      out[4 * i + 2] = __uint_as_float(v.z);
+      out[4 * i + 3] = __uint_as_float(v.w);
+    }
+  } else {
+    const uint4* q = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + wd * 16);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint4 v = q[i];
+      const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        out[8 * i + 2 * j] = __uint_as_float(u[j] << 16);
+        out[8 * i + 2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
+      }
+    }
+  }
+}
+
+template <int NB, int MB, bool RMS, int ADT>
 __global__ __launch_bounds__(256) void k_tgemm_mfma(
     const uint16_t* __restrict__ x, int64_t batch, int64_t ldx, const uint32_t* __restrict__ w,
     int64_t n_out, int64_t nwords, const void* __restrict__ alpha,
     const void* __restrict__ rms_w, int rms_dt, float rms_eps, uint16_t* __restrict__ y,
     int64_t ldy) {
-  constexpr int NT = 16 * NB, MB = 2, NV = RMS ? 2 : 1;
-  __shared__ __align__(16) uint32_t xs[NV][NT][kDenseChunk][8];
+  constexpr int NT = 16 * NB, NV = RMS ? 2 : 1, ROWS = 64 * MB;
+  // x' pairs, word-major: a B fragment read by 16 lanes (16 tokens) is one
+  // contiguous 256-byte run, so the reads are free of bank conflicts.
+  __shared__ __align__(16) uint32_t xs[NV][kDenseChunk][2][NT][4];
   __shared__ float cst[NT], ssq[NT];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g = lane >> 4;
   const int64_t t0 = static_cast<int64_t>(blockIdx.y) * NT;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kDenseRows + 32 * wv;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * ROWS + 16 * MB * wv;
   if (tid < NT) {
     cst[tid] = 0.f;
     ssq[tid] = 0.f;
@@ -67,42 +97,41 @@ __global__ __launch_bounds__(256) void k_tgemm_mfma(
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
   const ExpandConsts kc;
-  uint4 wq[MB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) wq[mb] = *reinterpret_cast<const uint4*>(rowp[mb]);
-  __syncthreads();
-  for (int64_t c0 = 0; c0 < nwords; c0 += kDenseChunk) {
-    // Stage x' for this chunk: NT tokens x 16 words, NB items per thread.
-    uint4 xa[NB], xb[NB];
+  // x (and RMS weight) loads of chunk c0 for this thread's staging items.
+  auto load_x = [&](int64_t c0, uint4 (&xa)[NB], uint4 (&xb)[NB]) {
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
-      const int col = item >> 4, wd = item & 15;
+      const int col = item % NT, wd = item / NT;
       int64_t t = t0 + col;
       t = t < batch ? t : batch - 1;
       const uint4* src = reinterpret_cast<const uint4*>(x + t * ldx + (c0 + wd) * 16);
       xa[it] = src[0];
       xb[it] = src[1];
     }
+  };
+  uint4 wq[MB], xa[NB], xb[NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) wq[mb] = *reinterpret_cast<const uint4*>(rowp[mb]);
+  load_x(0, xa, xb);
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < nwords; c0 += kDenseChunk) {
     float wr[RMS ? NB : 1][16];
     if constexpr (RMS) {
 #pragma unroll
-      for (int it = 0; it < NB; ++it) {
-        const int wd = (tid + 256 * it) & 15;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) wr[it][q] = ld_f(rms_w, rms_dt, (c0 + wd) * 16 + q);
-      }
+      for (int it = 0; it < NB; ++it) load_rms16(rms_w, rms_dt, c0 + (tid + 256 * it) / NT, wr[it]);
     }
-    // Next chunk's weights, in flight during this chunk's MFMAs.
-    uint4 wn[MB];
+    // Next chunk's weights and x, in flight during this chunk's work.
     const int64_t cn = c0 + kDenseChunk < nwords ? c0 + kDenseChunk : c0;
+    uint4 wn[MB], xan[NB], xbn[NB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) wn[mb] = *reinterpret_cast<const uint4*>(rowp[mb] + cn);
+    load_x(cn, xan, xbn);
     MA_ISSUE_FENCE();
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
-      const int col = item >> 4, wd = item & 15;
+      const int col = item % NT, wd = item / NT;
       const bool valid = t0 + col < batch;
       const uint32_t u[8] = {xa[it].x, xa[it].y, xa[it].z, xa[it].w,
                              xb[it].x, xb[it].y, xb[it].z, xb[it].w};
@@ -124,16 +153,16 @@ __global__ __launch_bounds__(256) void k_tgemm_mfma(
           lo[q] = bf16_to_f32(f32_to_bf16(xh - hi[q]));
         }
         c = prep_word_pairs(hi, pr);
-        *reinterpret_cast<uint4*>(&xs[0][col][wd][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-        *reinterpret_cast<uint4*>(&xs[0][col][wd][4]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+        *reinterpret_cast<uint4*>(&xs[0][wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+        *reinterpret_cast<uint4*>(&xs[0][wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
         c += prep_word_pairs(lo, pr);
-        *reinterpret_cast<uint4*>(&xs[NV - 1][col][wd][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-        *reinterpret_cast<uint4*>(&xs[NV - 1][col][wd][4]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+        *reinterpret_cast<uint4*>(&xs[NV - 1][wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+        *reinterpret_cast<uint4*>(&xs[NV - 1][wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
         atomicAdd(&ssq[col], ss);
       } else {
         c = prep_word_pairs(v, pr);
-        *reinterpret_cast<uint4*>(&xs[0][col][wd][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-        *reinterpret_cast<uint4*>(&xs[0][col][wd][4]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+        *reinterpret_cast<uint4*>(&xs[0][wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+        *reinterpret_cast<uint4*>(&xs[0][wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
       }
       atomicAdd(&cst[col], c);
     }
@@ -155,7 +184,7 @@ __global__ __launch_bounds__(256) void k_tgemm_mfma(
         for (int vv = 0; vv < NV; ++vv)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
-            const uint4 b = *reinterpret_cast<const uint4*>(&xs[vv][nb * 16 + r16][4 * g + q][4 * hf]);
+            const uint4 b = *reinterpret_cast<const uint4*>(&xs[vv][4 * g + q][hf][nb * 16 + r16][0]);
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) acc[mb][nb] = mfma16(a[mb][hf], b, acc[mb][nb]);
           }
@@ -163,6 +192,11 @@ __global__ __launch_bounds__(256) void k_tgemm_mfma(
     __syncthreads();
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) wq[mb] = wn[mb];
+#pragma unroll
+    for (int it = 0; it < NB; ++it) {
+      xa[it] = xan[it];
+      xb[it] = xbn[it];
+    }
   }
   // Epilogue: lane holds token col r16 of block nb, rows 4g .. 4g+3 of block mb.
   const int64_t kin = nwords * 16;
@@ -210,7 +244,7 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
   constexpr int NT = 16 * NB, MB = 2;
   constexpr int GPC = kDenseChunk / GW;  // groups per chunk
   constexpr int SPG = GW / 4;            // k-slices per group
-  __shared__ __align__(16) uint32_t xs[NT][kDenseChunk][4];
+  __shared__ __align__(16) uint32_t xs[kDenseChunk][NT][4];  // word-major (see above)
   __shared__ float xg[NT][GPC];
   __shared__ float sb[2][kDenseRows][GPC];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -244,7 +278,7 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
-      const int col = item >> 4, wd = item & 15;
+      const int col = item % NT, wd = item / NT;
       int64_t t = t0 + col;
       t = t < batch ? t : batch - 1;
       xr[it] = reinterpret_cast<const uint4*>(x + t * ldx + (c0 + wd) * 8)[0];
@@ -276,7 +310,7 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
-      const int col = item >> 4, wd = item & 15;
+      const int col = item % NT, wd = item / NT;
       const bool valid = t0 + col < batch;
       const uint32_t u4[4] = {xr[it].x, xr[it].y, xr[it].z, xr[it].w};
       float xv[8];
@@ -292,7 +326,7 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
         pr[j] = pack_bf16x2(16.f * xv[j], 16.f * xv[j + 4]);
         sx += xv[j] + xv[j + 4];
       }
-      *reinterpret_cast<uint4*>(&xs[col][wd][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+      *reinterpret_cast<uint4*>(&xs[wd][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
       atomicAdd(&xg[col][wd / GW], sx);
     }
     __syncthreads();
@@ -307,7 +341,7 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
       }
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const uint4 b = *reinterpret_cast<const uint4*>(&xs[nb * 16 + r16][4 * s + g][0]);
+        const uint4 b = *reinterpret_cast<const uint4*>(&xs[4 * s + g][nb * 16 + r16][0]);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[mb][nb] = mfma16(a[mb], b, acc[mb][nb]);
       }
@@ -367,9 +401,11 @@ int launch_tgemm_mfma(const uint16_t* x, int64_t batch, int64_t ldx, const uint3
                       hipStream_t s) {
   const int nb = batch <= 16 ? 1 : 2;
   const int64_t nt = 16 * nb;
-  dim3 grid(static_cast<unsigned>(cdiv(n_out, kDenseRows)), static_cast<unsigned>(cdiv(batch, nt)));
-#define MA_TG(NB, RMS, ADT)                                                                   \
-  hipLaunchKernelGGL((k_tgemm_mfma<NB, RMS, ADT>), grid, dim3(256), 0, s, x, batch, ldx, w, \
+  // 64-row tiles (one 16-row block per wave): more workgroups for the
+  // decoder's 2048-2560-row projections.
+  dim3 grid(static_cast<unsigned>(cdiv(n_out, 64)), static_cast<unsigned>(cdiv(batch, nt)));
+#define MA_TG(NB, RMS, ADT)                                                                      \
+  hipLaunchKernelGGL((k_tgemm_mfma<NB, 1, RMS, ADT>), grid, dim3(256), 0, s, x, batch, ldx, w, \
                      n_out, nwords, alpha, rms_w, rms_dt, rms_eps, y, ldy)
 #define MA_TG_A(NB, RMS) \
   if (alpha_dt == MA_F32) MA_TG(NB, RMS, MA_F32); else MA_TG(NB, RMS, MA_BF16);

@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256) void k_grouped_swiglu(
     const int32_t* __restrict__ pair_ids, int n_exp,
     uint16_t* __restrict__ hp, uint16_t* __restrict__ h, int64_t ldh) {
   constexpr int NT = 16 * NB;
-  __shared__ __align__(16) uint32_t xs[NT][kChunkWords][8];
+  __shared__ __align__(16) uint32_t xs[kChunkWords][2][NT][4];  // word-major: conflict-free B reads
   __shared__ float cst[NT];
   __shared__ int32_t tok[NT], pid[NT];
   int e, pos0, np;
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void k_grouped_swiglu(
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
-      const int col = item >> 4, wd = item & 15;
+      const int col = item % NT, wd = item / NT;
       const int t = tok[col];
       const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t < 0 ? 0 : t) * ldx + (c0 + wd) * 16);
       xa[it] = src[0];
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(256) void k_grouped_swiglu(
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
-      const int col = item >> 4, wd = item & 15;
+      const int col = item % NT, wd = item / NT;
       uint32_t pr[8];
       float c = 0.f;
       if (tok[col] >= 0) {
@@ -168,8 +168,8 @@ __global__ __launch_bounds__(256) void k_grouped_swiglu(
 #pragma unroll
         for (int j = 0; j < 8; ++j) pr[j] = 0u;
       }
-      *reinterpret_cast<uint4*>(&xs[col][wd][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-      *reinterpret_cast<uint4*>(&xs[col][wd][4]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+      *reinterpret_cast<uint4*>(&xs[wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+      *reinterpret_cast<uint4*>(&xs[wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
       atomicAdd(&cst[col], c);
     }
     __syncthreads();
@@ -188,7 +188,7 @@ __global__ __launch_bounds__(256) void k_grouped_swiglu(
       for (int hf = 0; hf < 2; ++hf) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-          const uint4 b = *reinterpret_cast<const uint4*>(&xs[nb * 16 + r16][4 * g + q][4 * hf]);
+          const uint4 b = *reinterpret_cast<const uint4*>(&xs[4 * g + q][hf][nb * 16 + r16][0]);
 #pragma unroll
           for (int mb = 0; mb < 4; ++mb) acc[mb][nb] = mfma_bf16(a[mb][hf], b, acc[mb][nb]);
         }
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256) void k_grouped_down(
     int64_t nwk, const void* __restrict__ alpha, const int32_t* __restrict__ offsets,
     int n_exp, uint16_t* __restrict__ out) {
   constexpr int NT = 16 * NB;
-  __shared__ __align__(16) uint32_t xs[NT][kChunkWords][8];
+  __shared__ __align__(16) uint32_t xs[kChunkWords][2][NT][4];  // word-major: conflict-free B reads
   __shared__ float cst[NT];
   int e, pos0, np;
   if (!decode_tile(offsets, n_exp, blockIdx.y, NT, e, pos0, np)) return;
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(256) void k_grouped_down(
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
-      const int col = item >> 4, wd = item & 15;
+      const int col = item % NT, wd = item / NT;
       const int64_t prow = pos0 + (col < np ? col : 0);
       const uint4* src = reinterpret_cast<const uint4*>(hp + (prow * nwk + c0 + wd) * 8);
       ha[it] = src[0];
@@ -275,14 +275,14 @@ __global__ __launch_bounds__(256) void k_grouped_down(
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
-      const int col = item >> 4, wd = item & 15;
+      const int col = item % NT, wd = item / NT;
       uint32_t pr[8] = {ha[it].x, ha[it].y, ha[it].z, ha[it].w, hb[it].x, hb[it].y, hb[it].z, hb[it].w};
       if (col >= np) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) pr[j] = 0u;
       }
-      *reinterpret_cast<uint4*>(&xs[col][wd][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-      *reinterpret_cast<uint4*>(&xs[col][wd][4]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+      *reinterpret_cast<uint4*>(&xs[wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+      *reinterpret_cast<uint4*>(&xs[wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
       atomicAdd(&cst[col], pairs_cst(pr));
     }
     __syncthreads();
@@ -301,7 +301,7 @@ __global__ __launch_bounds__(256) void k_grouped_down(
       for (int hf = 0; hf < 2; ++hf) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-          const uint4 b = *reinterpret_cast<const uint4*>(&xs[nb * 16 + r16][4 * g + q][4 * hf]);
+          const uint4 b = *reinterpret_cast<const uint4*>(&xs[4 * g + q][hf][nb * 16 + r16][0]);
 #pragma unroll
           for (int mb = 0; mb < 4; ++mb) acc[mb][nb] = mfma_bf16(a[mb][hf], b, acc[mb][nb]);
         }

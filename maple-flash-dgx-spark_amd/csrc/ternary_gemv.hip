@@ -108,8 +108,8 @@ static bool mfma_ok(const void* x, int x_dtype, int64_t batch, int64_t ldx, cons
   auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   return batch >= kMfmaMinBatch && x_dtype == MA_BF16 && !packed_kn && nwords % 16 == 0 &&
          (alpha_dtype == MA_BF16 || alpha_dtype == MA_F32) &&
-         (!rms_weight || rms_dtype == MA_F32 || rms_dtype == MA_BF16 || rms_dtype == MA_F16) &&
-         a16(x) && ldx % 8 == 0 && a16(packed) && a16(y);
+         (!rms_weight || rms_dtype == MA_F32 || rms_dtype == MA_BF16) &&
+         a16(x) && ldx % 8 == 0 && a16(packed) && a16(y) && (!rms_weight || a16(rms_weight));
 }
 
 extern "C" int ma_ternary_gemv(const void* x, int x_dtype, int64_t batch, int64_t ldx,
