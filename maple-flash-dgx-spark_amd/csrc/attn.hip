@@ -21,10 +21,11 @@
 namespace ma {
 
 constexpr int kHeadDim = 64;                // head_dim of the synthetic decoder
-constexpr int kSplit = 128;                 // positions per workgroup = threads
+constexpr int kSplit = 128;                 // positions per chunk
+constexpr int kAttnThreads = 256;           // 4 waves, 32 positions of a chunk each
 constexpr int kMaxGroup = 16;               // query heads per KV head
-constexpr int kWRow = kHeadDim + 4;         // LDS row of interleaved V pairs in
-                                            // words, padded: rows 4 banks apart
+constexpr int kVtRow = kSplit / 2 + 4;      // LDS row (one dim) of V position
+                                            // pairs in words, padded
 constexpr size_t kCounterAlign = 256;
 constexpr int kCombineChunk = 12;           // splits whose partials load together
 constexpr int kTargetGroups = 1024;         // workgroups an attention launch aims for
@@ -113,55 +114,55 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope_store(
     k_cache[((crow * nkv + (hs - nq)) * max_len + pos) * kHeadDim + d] = yb;
 }
 
-// Loads of the K and V rows of position t (clamped to hi - 1 when dead).
-__device__ __forceinline__ void load_kv_rows(const uint16_t* __restrict__ k_cache,
-                                             const uint16_t* __restrict__ v_cache, int64_t row,
-                                             uint4 kr[8], uint4 vr[8]) {
-  const uint4* kp = reinterpret_cast<const uint4*>(k_cache + row * kHeadDim);
-  const uint4* vp = reinterpret_cast<const uint4*>(v_cache + row * kHeadDim);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    vr[i] = vp[i];
-    kr[i] = kp[i];
-  }
+typedef __bf16 bf16x8a_t __attribute__((ext_vector_type(8)));
+typedef float f32x4a_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4a_t mfma_att(uint4 a, uint4 b, f32x4a_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8a_t, a),
+                                                 __builtin_bit_cast(bf16x8a_t, b), c, 0, 0, 0);
 }
 
-// One workgroup (128 threads, 2 waves) per (split, KV head, row); a split
+__device__ __forceinline__ uint32_t sel32(bool c, uint32_t a, uint32_t b) { return c ? a : b; }
+
+// One workgroup (256 threads, 4 waves) per (split, KV head, row); a split
 // walks chunks of 128 positions (the grid holds about kTargetGroups
-// workgroups; rows x KV heads x splits), thread t on position lo + t:
-//   q:     FUSED normalises + ropes the group's q heads from the qkv row; the
-//          split holding position seqlen[b] also makes the new K/V (used in
-//          place of what it read, stored to the cache at the end).
-//          Otherwise q is read.
-//   chunk: V rows of positions 2m, 2m+1 (lanes t, t^1) are interleaved into
-//          LDS as bf16 pairs W[m][d] = (v_2m[d], v_2m+1[d]); scores q.k *
-//          scale (dot2 over dim pairs) -> LDS; the next chunk's K/V loads
-//          are issued; online softmax per head (running max and sum, P
-//          rounded to bf16); P.V by thread (head, 4 dims) with one dot2 per
-//          position pair, the accumulator rescaled by exp(m_old - m_new).
-//   end:   one split: normalise and store.  Several: write (acc, m, l)
-//          partials with device-coherent stores; the last split of the (row,
-//          KV head) to take a ticket merges them and resets the ticket.
+// workgroups), wave w owning positions 32w .. 32w+31 of each chunk.  On
+// v_mfma_f32_16x16x32_bf16 (A lane l: row l%16, k 8(l/16)..+8; B: col l%16,
+// k 8(l/16)..+8; C: col l%16, rows 4(l/16)..+4):
+//   S^T = K Q^T: A = K rows loaded straight from the cache (16 positions x
+//     32 dims), B = q (16 head slots; slots >= group are zero), so lane l
+//     ends with head l%16's scores for positions 4(l/16)..+4 of each block;
+//   online softmax per head over the chunk (running max and sum, P rounded
+//     to bf16 as the reference does before P.V);
+//   O += P V: the lane's own 8 P values are its A fragment (k order:
+//     positions 4g..4g+3 of block 0 then of block 1), and B takes V in the
+//     same order from LDS, where V is stored transposed in position pairs
+//     (vt[d][m] = (v_2m[d], v_2m+1[d]), built with one DPP exchange).
+//   FUSED: the group's q heads are RMS-normalised + roped from the qkv row;
+//     the split holding position seqlen[b] builds the new K/V, uses them in
+//     place of what it read and stores them to the cache at the end.
+// One split: normalise and store.  Several: (acc, m, l) partials with
+// device-coherent stores; the last split of the (row, KV head) to take a
+// ticket merges them and resets the ticket.
 template <bool FUSED>
-__global__ __launch_bounds__(kSplit) void k_decode_attn(
+__global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     const uint16_t* __restrict__ src, int64_t ldq, const void* __restrict__ qn_w,
     const void* __restrict__ kn_w, int w_dt, RopeSrc rope, float eps,
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, int64_t cache_rows,
     int64_t max_len, const int64_t* __restrict__ seqlen, const int64_t* __restrict__ row_map,
     int nq, int nkv, int64_t window, float scale, int max_splits, uint32_t* __restrict__ tickets,
     float* __restrict__ part_acc, float* __restrict__ part_ml, uint16_t* __restrict__ out) {
-  __shared__ __align__(16) uint32_t qs[kMaxGroup][kHeadDim / 2];
-  __shared__ __align__(16) uint32_t vw[kSplit / 2][kWRow];
-  __shared__ __align__(16) float sc[kMaxGroup][kSplit];
-  __shared__ __align__(16) uint16_t pb[kMaxGroup][kSplit];
-  __shared__ __align__(16) uint32_t kvnew[2][kHeadDim / 2];
+  __shared__ __align__(16) uint16_t qs[kMaxGroup][kHeadDim];
+  __shared__ __align__(16) uint32_t vt[kHeadDim][kVtRow];
+  __shared__ __align__(16) uint16_t kvnew[2][kHeadDim];
+  __shared__ float wm[4][kMaxGroup], wl[4][kMaxGroup];
   __shared__ float hm[kMaxGroup], hl[kMaxGroup], hr[kMaxGroup];
   __shared__ int s_last;
   const int sp = blockIdx.x, kvh = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
-  // wave index, made visibly wave-uniform so that branches on it stay scalar
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
   const int group = nq / nkv;
   const int64_t pos = clamp64(seqlen[b], 0, max_len - 1);
   const int64_t kv_len = pos + 1;
@@ -176,188 +177,213 @@ __global__ __launch_bounds__(kSplit) void k_decode_attn(
   const int64_t base = (crow * nkv + kvh) * max_len;
   const bool owns_pos = FUSED && sp == n_spl - 1;
 
-  // First chunk's K/V rows: the longest latency.
-  uint4 kr[8], vr[8];
-  {
-    const int64_t lo = start + static_cast<int64_t>(c_beg) * kSplit;
+  // K fragments: positions 32 wv + 16 pb + r16, dims 8 g + 32 ks.
+  // V rows: position 32 wv + (lane >> 1), dims 32 (lane & 1) .. +32.
+  auto load_chunk = [&](int c, uint4 (&kf)[2][2], uint4 (&vr)[4]) {
+    const int64_t lo = start + static_cast<int64_t>(c) * kSplit;
     const int64_t hi = lo + kSplit < kv_len ? lo + kSplit : kv_len;
-    const int64_t t = lo + tid;
-    load_kv_rows(k_cache, v_cache, base + (t < hi ? t : hi - 1), kr, vr);
-  }
-  uint16_t new_kv = 0;  // FUSED owner split: this wave's new K (wave 0) or V (wave 1)
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {
+      int64_t t = lo + 32 * wv + 16 * pb + r16;
+      t = t < hi ? t : hi - 1;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        kf[pb][ks] = *reinterpret_cast<const uint4*>(k_cache + (base + t) * kHeadDim + 8 * g + 32 * ks);
+    }
+    int64_t tv = lo + 32 * wv + (lane >> 1);
+    tv = tv < hi ? tv : hi - 1;
+    const uint4* vp = reinterpret_cast<const uint4*>(v_cache + (base + tv) * kHeadDim + 32 * (lane & 1));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vr[i] = vp[i];
+  };
+  uint4 kf[2][2], vr[4];
+  load_chunk(c_beg, kf, vr);
+
+  uint16_t new_kv = 0;  // FUSED owner split: the new K (wave 0) or V (wave 1) element
   if constexpr (FUSED) {
     // Every load of the prologue is issued before any of them is used.
     const uint16_t* row = src + b * ldq;
-    uint16_t xq[kMaxGroup / 2];
+    uint16_t xq[kMaxGroup / 4];
 #pragma unroll
-    for (int i = 0; i < kMaxGroup / 2; ++i) {
-      const int hh = wv + 2 * i;
+    for (int i = 0; i < kMaxGroup / 4; ++i) {
+      const int hh = wv + 4 * i;
       xq[i] = hh < group ? row[(kvh * group + hh) * kHeadDim + lane] : uint16_t(0);
     }
-    const uint16_t xkv = owns_pos ? row[(nq + kvh + (wv ? nkv : 0)) * kHeadDim + lane] : uint16_t(0);
+    const uint16_t xkv =
+        owns_pos && wv < 2 ? row[(nq + kvh + (wv ? nkv : 0)) * kHeadDim + lane] : uint16_t(0);
     const float wq = ld_f(qn_w, w_dt, lane);
     const float wk = ld_f(kn_w, w_dt, lane);
     const float2 cs = rope_coeffs(rope, b, pos);
 #pragma unroll
-    for (int i = 0; i < kMaxGroup / 2; ++i) {
-      const int hh = wv + 2 * i;
-      if (hh < group) {
-        const float y = norm_rope_lane(bf16_to_f32(xq[i]), wq, cs, rope, eps);
-        reinterpret_cast<uint16_t*>(qs[hh])[lane] = f32_to_bf16(y);
-      }
+    for (int i = 0; i < kMaxGroup / 4; ++i) {
+      const int hh = wv + 4 * i;
+      if (hh < kMaxGroup)
+        qs[hh][lane] = hh < group ? f32_to_bf16(norm_rope_lane(bf16_to_f32(xq[i]), wq, cs, rope, eps))
+                                  : uint16_t(0);
     }
-    if (owns_pos) {
+    if (owns_pos && wv < 2) {
       new_kv = xkv;  // wave 1: V is stored as is
       if (wv == 0) new_kv = f32_to_bf16(norm_rope_lane(bf16_to_f32(xkv), wk, cs, rope, eps));
-      reinterpret_cast<uint16_t*>(kvnew[wv])[lane] = new_kv;
+      kvnew[wv][lane] = new_kv;
     }
   } else {
-    const uint32_t* qsrc = reinterpret_cast<const uint32_t*>(src + (b * nq + kvh * group) * kHeadDim);
-    for (int i = tid; i < group * (kHeadDim / 2); i += kSplit)
-      qs[i / (kHeadDim / 2)][i % (kHeadDim / 2)] = qsrc[i];
+    const uint16_t* qsrc = src + (b * nq + kvh * group) * kHeadDim;
+    for (int i = tid; i < kMaxGroup * kHeadDim; i += kAttnThreads) {
+      const int hh = i / kHeadDim;
+      qs[hh][i % kHeadDim] = hh < group ? qsrc[i] : uint16_t(0);
+    }
   }
-  if (tid < group) {
+  if (tid < kMaxGroup) {
     hm[tid] = -INFINITY;
     hl[tid] = 0.f;
   }
   __syncthreads();
+  uint4 qf[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) qf[ks] = *reinterpret_cast<const uint4*>(&qs[r16][8 * g + 32 * ks]);
 
-  float o[kMaxGroup / 8][4] = {};  // thread items: (head, 4 dims), up to 2 per thread
+  f32x4a_t oacc[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) oacc[nb] = f32x4a_t{0.f, 0.f, 0.f, 0.f};
   for (int c = c_beg; c < c_end; ++c) {
     const int64_t lo = start + static_cast<int64_t>(c) * kSplit;
     const int64_t hi = lo + kSplit < kv_len ? lo + kSplit : kv_len;
-    const int64_t t = lo + tid;
-    const bool live = t < hi;
-    if constexpr (FUSED) {  // the position written by this launch: use the new K/V
-      const bool use_new = owns_pos && t == pos;
+    if constexpr (FUSED) {  // the position written by this launch: the new K/V
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {  // selects, so that kr/vr stay in registers
-        const uint4 nk = *reinterpret_cast<const uint4*>(&kvnew[0][4 * i]);
-        const uint4 nv = *reinterpret_cast<const uint4*>(&kvnew[1][4 * i]);
-        kr[i].x = use_new ? nk.x : kr[i].x;
-        kr[i].y = use_new ? nk.y : kr[i].y;
-        kr[i].z = use_new ? nk.z : kr[i].z;
-        kr[i].w = use_new ? nk.w : kr[i].w;
-        vr[i].x = use_new ? nv.x : vr[i].x;
-        vr[i].y = use_new ? nv.y : vr[i].y;
-        vr[i].z = use_new ? nv.z : vr[i].z;
-        vr[i].w = use_new ? nv.w : vr[i].w;
+      for (int pb = 0; pb < 2; ++pb) {
+        const bool nk = owns_pos && lo + 32 * wv + 16 * pb + r16 == pos;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const uint4 v = *reinterpret_cast<const uint4*>(&kvnew[0][8 * g + 32 * ks]);
+          kf[pb][ks] = make_uint4(sel32(nk, v.x, kf[pb][ks].x), sel32(nk, v.y, kf[pb][ks].y),
+                                  sel32(nk, v.z, kf[pb][ks].z), sel32(nk, v.w, kf[pb][ks].w));
+        }
+      }
+      const bool nv = owns_pos && lo + 32 * wv + (lane >> 1) == pos;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 v = *reinterpret_cast<const uint4*>(&kvnew[1][32 * (lane & 1) + 8 * i]);
+        vr[i] = make_uint4(sel32(nv, v.x, vr[i].x), sel32(nv, v.y, vr[i].y), sel32(nv, v.z, vr[i].z),
+                           sel32(nv, v.w, vr[i].w));
       }
     }
-    // Interleave V with the neighbouring position: the even lane of a pair
-    // builds dims 0..31, the odd lane dims 32..63.
+    // V^T in position pairs: lanes l and l ^ 2 hold positions 2m and 2m + 1
+    // of the same 32 dims; the even one builds the half's dims 0..15, the
+    // odd one dims 16..31.
     {
-      uint32_t v[32];
+      uint32_t v[16];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 4; ++i) {
         v[4 * i] = vr[i].x;
         v[4 * i + 1] = vr[i].y;
         v[4 * i + 2] = vr[i].z;
         v[4 * i + 3] = vr[i].w;
       }
-      const bool odd = tid & 1;
-      uint32_t w[32];
+      const bool odd = (lane >> 1) & 1;
+      const int d0 = 32 * (lane & 1) + (odd ? 16 : 0);
+      const int m = 16 * wv + (lane >> 2);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint32_t mine = odd ? v[16 + j] : v[j];
-        const uint32_t send = odd ? v[j] : v[16 + j];
-        const uint32_t other = __builtin_amdgcn_update_dpp(0, send, 0xB1, 0xF, 0xF, false);
-        const uint32_t e = odd ? other : mine, od = odd ? mine : other;  // positions 2m, 2m+1
-        w[2 * j] = (e & 0xffffu) | (od << 16);
-        w[2 * j + 1] = (e >> 16) | (od & 0xffff0000u);
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t mine = odd ? v[8 + j] : v[j];
+        const uint32_t send = odd ? v[j] : v[8 + j];
+        const uint32_t other = __builtin_amdgcn_update_dpp(0, send, 0x4E, 0xF, 0xF, false);
+        const uint32_t e = odd ? other : mine, o = odd ? mine : other;
+        vt[d0 + 2 * j][m] = (e & 0xffffu) | (o << 16);
+        vt[d0 + 2 * j + 1][m] = (e >> 16) | (o & 0xffff0000u);
       }
-      uint32_t* dst = &vw[tid >> 1][odd ? kHeadDim / 2 : 0];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        *reinterpret_cast<uint4*>(dst + 4 * i) =
-            make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
     }
-    for (int hh = 0; hh < group; ++hh) {
-      float a0 = 0.f, a1 = 0.f;
+    // Scores and this wave's per-head maximum.
+    float s[2][4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint4 qq = *reinterpret_cast<const uint4*>(&qs[hh][4 * i]);
-        a0 = dot2(kr[i].x, qq.x, a0);
-        a1 = dot2(kr[i].y, qq.y, a1);
-        a0 = dot2(kr[i].z, qq.z, a0);
-        a1 = dot2(kr[i].w, qq.w, a1);
+    for (int pb = 0; pb < 2; ++pb) {
+      f32x4a_t acc = mfma_att(kf[pb][0], qf[0], f32x4a_t{0.f, 0.f, 0.f, 0.f});
+      acc = mfma_att(kf[pb][1], qf[1], acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        s[pb][i] = lo + 32 * wv + 16 * pb + 4 * g + i < hi ? acc[i] * scale : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (g == 0) wm[wv][r16] = mx;
+    __syncthreads();
+    if (c + 1 < c_end) load_chunk(c + 1, kf, vr);  // in flight during softmax and P.V
+    const float m_old = hm[r16];
+    const float m_new = fmaxf(m_old, fmaxf(fmaxf(wm[0][r16], wm[1][r16]), fmaxf(wm[2][r16], wm[3][r16])));
+    float p[2][4], ls = 0.f;
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[pb][i] = s[pb][i] == -INFINITY ? 0.f : expf(s[pb][i] - m_new);
+        ls += p[pb][i];
       }
-      sc[hh][tid] = live ? (a0 + a1) * scale : -INFINITY;
+    ls += __shfl_xor(ls, 16, 64);
+    ls += __shfl_xor(ls, 32, 64);
+    if (g == 0) wl[wv][r16] = ls;
+    // P in bf16 as the A fragment: k = positions 4g..4g+3 of block 0, then of block 1.
+    const uint4 pa = make_uint4(pack_bf16x2_rn(p[0][0], p[0][1]), pack_bf16x2_rn(p[0][2], p[0][3]),
+                                pack_bf16x2_rn(p[1][0], p[1][1]), pack_bf16x2_rn(p[1][2], p[1][3]));
+    __syncthreads();
+    if (tid < kMaxGroup) {
+      const float mo = hm[tid];
+      const float mn = fmaxf(mo, fmaxf(fmaxf(wm[0][tid], wm[1][tid]), fmaxf(wm[2][tid], wm[3][tid])));
+      const float r = expf(mo - mn);  // 0 on the first chunk
+      hl[tid] = hl[tid] * r + ((wl[0][tid] + wl[1][tid]) + (wl[2][tid] + wl[3][tid]));
+      hm[tid] = mn;
+      hr[tid] = r;
     }
     __syncthreads();
-    if (c + 1 < c_end) {  // next chunk's rows, in flight during softmax and P.V
-      const int64_t lo2 = lo + kSplit;
-      const int64_t hi2 = lo2 + kSplit < kv_len ? lo2 + kSplit : kv_len;
-      const int64_t t2 = lo2 + tid;
-      load_kv_rows(k_cache, v_cache, base + (t2 < hi2 ? t2 : hi2 - 1), kr, vr);
-    }
-    // Online softmax: wave w takes heads w, w + 2, ...; lane owns positions
-    // lane and lane + 64.  Position lo is always live, so the max is finite.
-    for (int hh = wv; hh < group; hh += 2) {
-      const float v0 = sc[hh][lane], v1 = sc[hh][lane + 64];
-      const float m_old = hm[hh];
-      const float m = fmaxf(m_old, wave_max(fmaxf(v0, v1)));
-      const float p0 = v0 == -INFINITY ? 0.f : expf(v0 - m);
-      const float p1 = v1 == -INFINITY ? 0.f : expf(v1 - m);
-      const float l = group_sum<64>(p0 + p1);
-      pb[hh][lane] = f32_to_bf16(p0);  // P in bf16 for P.V
-      pb[hh][lane + 64] = f32_to_bf16(p1);
-      if (lane == 0) {
-        const float r = expf(m_old - m);  // 0 on the first chunk
-        hm[hh] = m;
-        hl[hh] = hl[hh] * r + l;
-        hr[hh] = r;
-      }
-    }
-    __syncthreads();
-    // P.V: thread (head hh, dims 4dq..4dq+3), one dot2 per position pair.
-    // Dead positions have P = 0 and a finite (duplicated) V row.
-    const int npairs = (static_cast<int>(hi - lo) + 1) >> 1;
+    float rr[4];
 #pragma unroll
-    for (int k = 0; k < kMaxGroup / 8; ++k) {
-      const int item = tid + kSplit * k;
-      if (item < group * 16) {
-        const int hh = item >> 4, dq = item & 15;
-        const uint32_t* pw = reinterpret_cast<const uint32_t*>(pb[hh]);
-        const float r = hr[hh];
-        float o0 = o[k][0] * r, o1 = o[k][1] * r, o2 = o[k][2] * r, o3 = o[k][3] * r;
-#pragma unroll 4
-        for (int m = 0; m < npairs; ++m) {
-          const uint32_t pp = pw[m];
-          const uint4 vv = *reinterpret_cast<const uint4*>(&vw[m][4 * dq]);
-          o0 = dot2(vv.x, pp, o0);
-          o1 = dot2(vv.y, pp, o1);
-          o2 = dot2(vv.z, pp, o2);
-          o3 = dot2(vv.w, pp, o3);
-        }
-        o[k][0] = o0;
-        o[k][1] = o1;
-        o[k][2] = o2;
-        o[k][3] = o3;
-      }
+    for (int i = 0; i < 4; ++i) rr[i] = hr[4 * g + i];
+    const int mp = 16 * wv + 2 * g;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int d = 16 * nb + r16;
+      const uint2 b0 = *reinterpret_cast<const uint2*>(&vt[d][mp]);
+      const uint2 b1 = *reinterpret_cast<const uint2*>(&vt[d][mp + 8]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) oacc[nb][i] *= rr[i];
+      oacc[nb] = mfma_att(pa, make_uint4(b0.x, b0.y, b1.x, b1.y), oacc[nb]);
     }
-    __syncthreads();  // vw / sc / pb are rewritten by the next chunk
+    __syncthreads();  // vt / wm / wl are rewritten by the next chunk
   }
-  // The new K/V go to the cache last: a store to the cache ahead of the reads
-  // of kr makes the compiler keep kr in scratch memory.
-  if (owns_pos) (wv == 0 ? k_cache : v_cache)[(base + pos) * kHeadDim + lane] = new_kv;
-  const int64_t pidx = (b * nkv + kvh) * max_splits + sp;
+  // The new K/V go to the cache last (after every read of the cache).
+  if (owns_pos && wv < 2) (wv == 0 ? k_cache : v_cache)[(base + pos) * kHeadDim + lane] = new_kv;
+  // Sum the waves' P.V (same running max, so a plain sum) in a fixed order,
+  // through LDS that V no longer needs.
+  static_assert(sizeof(vt) >= 4 * kMaxGroup * kHeadDim * sizeof(float), "reduction buffer");
+  float (*ow)[kMaxGroup][kHeadDim] = reinterpret_cast<float (*)[kMaxGroup][kHeadDim]>(&vt[0][0]);
 #pragma unroll
-  for (int k = 0; k < kMaxGroup / 8; ++k) {
-    const int item = tid + kSplit * k;
-    if (item < group * 16) {
-      const int hh = item >> 4, dq = item & 15;
-      if (n_spl == 1) {
-        const float inv = 1.f / hl[hh];
-        uint2 r;
-        r.x = pack_bf16x2_rn(o[k][0] * inv, o[k][1] * inv);
-        r.y = pack_bf16x2_rn(o[k][2] * inv, o[k][3] * inv);
-        *reinterpret_cast<uint2*>(out + (b * nq + kvh * group + hh) * kHeadDim + 4 * dq) = r;
-      } else {
-        float* pa = part_acc + (pidx * kMaxGroup + hh) * kHeadDim + 4 * dq;
-        st_coherent2(pa, o[k][0], o[k][1]);
-        st_coherent2(pa + 2, o[k][2], o[k][3]);
-      }
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (4 * g + i < group) ow[wv][4 * g + i][16 * nb + r16] = oacc[nb][i];
+  __syncthreads();
+  const int64_t pidx = (b * nkv + kvh) * max_splits + sp;
+  for (int item = tid; item < group * 16; item += kAttnThreads) {
+    const int hh = item >> 4, dq = item & 15;
+    float4 o = *reinterpret_cast<const float4*>(&ow[0][hh][4 * dq]);
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const float4 q = *reinterpret_cast<const float4*>(&ow[w][hh][4 * dq]);
+      o.x += q.x;
+      o.y += q.y;
+      o.z += q.z;
+      o.w += q.w;
+    }
+    if (n_spl == 1) {
+      const float inv = 1.f / hl[hh];
+      uint2 r;
+      r.x = pack_bf16x2_rn(o.x * inv, o.y * inv);
+      r.y = pack_bf16x2_rn(o.z * inv, o.w * inv);
+      *reinterpret_cast<uint2*>(out + (b * nq + kvh * group + hh) * kHeadDim + 4 * dq) = r;
+    } else {
+      float* pa2 = part_acc + (pidx * kMaxGroup + hh) * kHeadDim + 4 * dq;
+      st_coherent2(pa2, o.x, o.y);
+      st_coherent2(pa2 + 2, o.z, o.w);
     }
   }
   if (n_spl == 1) return;
@@ -374,7 +400,7 @@ __global__ __launch_bounds__(kSplit) void k_decode_attn(
   if (!s_last) return;
   // Merge: one pass with a running max, kCombineChunk splits' loads at a time.
   const int64_t p0 = (b * nkv + kvh) * max_splits;
-  for (int item = tid; item < group * 16; item += kSplit) {
+  for (int item = tid; item < group * 16; item += kAttnThreads) {
     const int hh = item >> 4, dq = item & 15;
     float mx = -INFINITY, den = 0.f, n0 = 0.f, n1 = 0.f, n2 = 0.f, n3 = 0.f;
     for (int s0 = 0; s0 < n_spl; s0 += kCombineChunk) {
@@ -509,9 +535,9 @@ static int launch_attn(bool fused, const void* src, int64_t ldq, const void* qn_
       seqlen, row_map, nq, nkv, window, scale, static_cast<int>(max_splits), tickets, acc, ml, \
       static_cast<uint16_t*>(out)
   if (fused)
-    hipLaunchKernelGGL(k_decode_attn<true>, grid, dim3(kSplit), 0, s, MA_ATTN_ARGS);
+    hipLaunchKernelGGL(k_decode_attn<true>, grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
   else
-    hipLaunchKernelGGL(k_decode_attn<false>, grid, dim3(kSplit), 0, s, MA_ATTN_ARGS);
+    hipLaunchKernelGGL(k_decode_attn<false>, grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
 #undef MA_ATTN_ARGS
   return check_launch(what);
 }
