@@ -280,6 +280,15 @@ int ma_decode_attn_fused(const void* qkv, int64_t ldq, int64_t batch, int n_head
                          int64_t window, float scale, void* out, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/*
+ * Greedy choice: out[r] = argmax over the n values of row r (bf16 or float32,
+ * row stride ldx), the lowest index on ties; out int64
+ * [rows].  Replaces torch.argmax(logits, dim=-1) of the greedy step,
+ * src/maple_run/generate.py:146-148.
+ */
+int ma_argmax_rows(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t ldx,
+                   int64_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

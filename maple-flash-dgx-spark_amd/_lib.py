@@ -51,6 +51,7 @@ _SIGNATURES = {
     "ma_moe_fused": [_P, _P, _P, _I, _F, _P, _P, _P, _L, _L, _L, _L, _P, _P, _P, _P, _P, _P, _P, _P,
                      _Z, _P],
     "ma_moe_fused_timed_out": [_P, _P, _P],
+    "ma_argmax_rows": [_P, _I, _L, _L, _L, _P, _P],
     "ma_moe_grouped": [_P, _L, _L, _L, _P, _P, _P, _P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _I,
                        _P, _L, _P, _P, _Z, _P],
 }

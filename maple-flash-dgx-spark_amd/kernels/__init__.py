@@ -12,6 +12,7 @@ from __future__ import annotations
 from .decode_attn import apply_qkv_decode, decode_attention, decode_gqa_attn, gqa_workspace
 from .dispatch import moe_dispatch
 from .fused_norm import add_rms_norm, moe_reduce_add, rms_norm
+from .greedy import greedy_argmax
 from .router import router_topk
 from .rtn4 import rtn4_embedding, rtn4_gemv
 from .ternary_expert import ternary_expert_down_sum, ternary_expert_gemv, ternary_expert_swiglu
@@ -33,4 +34,5 @@ __all__ = [
     "decode_gqa_attn",
     "decode_attention",
     "gqa_workspace",
+    "greedy_argmax",
 ]

@@ -28,6 +28,7 @@ import torch
 from . import synthetic
 from .kernels.decode_attn import decode_attention, gqa_workspace
 from .kernels.fused_norm import add_rms_norm, rms_norm
+from .kernels.greedy import greedy_argmax
 from .kernels.rtn4 import rtn4_embedding, rtn4_gemv
 from .kernels.ternary_gemv import ternary_gemv
 from .moe import fused_supported, moe_block, moe_fused
@@ -175,7 +176,7 @@ class SyntheticDecoder:
     def greedy_step(self, ids: torch.Tensor, cache: KVCache) -> torch.Tensor:
         """forward + argmax, writing the next ids back into ``ids`` (graph-safe)."""
         logits = self.forward(ids, cache)
-        ids.copy_(torch.argmax(logits, dim=-1))
+        greedy_argmax(logits, out=ids)
         return logits
 
     def decode_bytes(self, batch: int, kv_len: int) -> int:

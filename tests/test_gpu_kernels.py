@@ -336,3 +336,23 @@ def test_norms_vs_oracle(dev):
     s, n = ok.add_rms_norm(np_f(x), np_f(y), np_f(w))
     assert_bf16_close(np_f(res), s, what="residual")
     assert_bf16_close(np_f(nrm), n, what="normed")
+
+
+# ---------------------------------------------------------------- greedy argmax
+@pytest.mark.parametrize("rows,n,dtype", [(1, 151936, torch.bfloat16), (32, 151936, torch.bfloat16),
+                                          (3, 1001, torch.float32), (5, 7, torch.bfloat16)])
+def test_greedy_argmax_matches_torch(dev, rows, n, dtype):
+    from maple_amd.kernels import greedy_argmax
+
+    g = torch.Generator(device=dev).manual_seed(rows * 7 + n)
+    x = torch.randn(rows, n, generator=g, device=dev).to(dtype)
+    # plant ties: the row maximum also at a later and at an earlier position
+    m = x.float().amax(dim=1)
+    x[0, n - 1] = m[0].to(dtype)
+    if n > 2:
+        x[rows - 1, 1] = (m[rows - 1] + 1).to(dtype)
+        x[rows - 1, n - 2] = (m[rows - 1] + 1).to(dtype)
+    got = greedy_argmax(x)
+    torch.testing.assert_close(got, torch.argmax(x.float(), dim=-1), rtol=0, atol=0)
+    out = torch.empty(rows, dtype=torch.int64, device=dev)
+    assert greedy_argmax(x, out=out) is out and torch.equal(out, got)
