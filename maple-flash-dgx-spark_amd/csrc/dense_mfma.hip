@@ -127,7 +127,8 @@ __global__ __launch_bounds__(256) void k_tgemm_mfma(
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) wn[mb] = *reinterpret_cast<const uint4*>(rowp[mb] + cn);
     load_x(cn, xan, xbn);
-    MA_ISSUE_FENCE();
+    // (no sched_barrier here: with loads into loop-carried registers just
+    // above, it produced wrong MFMA operands on this compiler)
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
@@ -299,7 +300,8 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int s = 0; s < 4; ++s) wn[mb][s] = rowp[mb][cn + 4 * s];
-    MA_ISSUE_FENCE();
+    // (no sched_barrier here: with loads into loop-carried registers just
+    // above, it produced wrong MFMA operands on this compiler)
     if (tid < NT * GPC) xg[tid / GPC][tid % GPC] = 0.f;
     {
       const int which = tid >> 7, rr = tid & 127;

@@ -140,12 +140,11 @@ __global__ __launch_bounds__(256) void k_grouped_swiglu(
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const ExpandConsts kc;
   __syncthreads();
-  for (int64_t c0 = 0; c0 < nwords; c0 += kChunkWords) {
-    uint4 wq[4];
+  // Weights and x of chunk c0 (x' staging items: NT columns x 16 words, NB
+  // per thread); the next chunk's are in flight during this chunk's work.
+  auto load_chunk = [&](int64_t c0, uint4 (&wq)[4], uint4 (&xa)[NB], uint4 (&xb)[NB]) {
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) wq[mb] = *reinterpret_cast<const uint4*>(rowp[mb] + c0);
-    // Stage x' for this chunk: NT columns x 16 words, NB items per thread.
-    uint4 xa[NB], xb[NB];
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
@@ -155,7 +154,14 @@ __global__ __launch_bounds__(256) void k_grouped_swiglu(
       xa[it] = src[0];
       xb[it] = src[1];
     }
-    MA_ISSUE_FENCE();
+  };
+  uint4 wq[4], xa[NB], xb[NB];
+  load_chunk(0, wq, xa, xb);
+  for (int64_t c0 = 0; c0 < nwords; c0 += kChunkWords) {
+    uint4 wn[4], xan[NB], xbn[NB];
+    load_chunk(c0 + kChunkWords < nwords ? c0 + kChunkWords : c0, wn, xan, xbn);
+    // (no sched_barrier here: with loads into loop-carried registers just
+    // above, it produced wrong MFMA operands on this compiler)
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
@@ -195,6 +201,13 @@ __global__ __launch_bounds__(256) void k_grouped_swiglu(
       }
     }
     __syncthreads();
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) wq[mb] = wn[mb];
+#pragma unroll
+    for (int it = 0; it < NB; ++it) {
+      xa[it] = xan[it];
+      xb[it] = xbn[it];
+    }
   }
   // Epilogue: rows i0 + 16 mb + 4 g + r (up: mb 0,1; gate: mb 2,3 -> same rows).
   const int64_t nwh = n_half / 16;
@@ -257,11 +270,9 @@ __global__ __launch_bounds__(256) void k_grouped_down(
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const ExpandConsts kc;
   __syncthreads();
-  for (int64_t c0 = 0; c0 < nwk; c0 += kChunkWords) {
-    uint4 wq[4];
+  auto load_chunk = [&](int64_t c0, uint4 (&wq)[4], uint4 (&ha)[NB], uint4 (&hb)[NB]) {
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) wq[mb] = *reinterpret_cast<const uint4*>(rowp[mb] + c0);
-    uint4 ha[NB], hb[NB];
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
@@ -271,7 +282,14 @@ __global__ __launch_bounds__(256) void k_grouped_down(
       ha[it] = src[0];
       hb[it] = src[1];
     }
-    MA_ISSUE_FENCE();
+  };
+  uint4 wq[4], ha[NB], hb[NB];
+  load_chunk(0, wq, ha, hb);
+  for (int64_t c0 = 0; c0 < nwk; c0 += kChunkWords) {
+    uint4 wn[4], han[NB], hbn[NB];
+    load_chunk(c0 + kChunkWords < nwk ? c0 + kChunkWords : c0, wn, han, hbn);
+    // (no sched_barrier here: with loads into loop-carried registers just
+    // above, it produced wrong MFMA operands on this compiler)
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int item = tid + 256 * it;
@@ -308,6 +326,13 @@ __global__ __launch_bounds__(256) void k_grouped_down(
       }
     }
     __syncthreads();
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) wq[mb] = wn[mb];
+#pragma unroll
+    for (int it = 0; it < NB; ++it) {
+      ha[it] = han[it];
+      hb[it] = hbn[it];
+    }
   }
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
