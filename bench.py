@@ -28,6 +28,7 @@ oracle) on a bounded sample of the same workload on this host's cores.
     python bench.py [--steps 20] [--warmup 3] [--layers 96] [--no-cpu]
                     [--no-decoder] [--no-extra]
     python bench.py --counters-pass   # SwiGLU graph + a 256 MiB copy, for rocprofv3 --pmc
+    python bench.py --decode-batch 32 # only the full decoder at one batch size
 """
 
 from __future__ import annotations
@@ -269,6 +270,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-decoder", action="store_true")
+    ap.add_argument("--decode-batch", type=int, default=0,
+                    help="only time the full decoder at this batch (for profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -290,6 +293,10 @@ def main() -> int:
     L = args.layers
     if args.counters_pass:
         return counters_pass(dev, L)
+    if args.decode_batch > 0:
+        res = decoder_tokens_per_s(dev, args.decode_batch, max(args.steps, 10), args.warmup)
+        print(json.dumps({"decode": {f"bs{args.decode_batch}": res}}), flush=True)
+        return 0
     log(f"building {L} cold MoE layers ...")
     layers = [synthetic.make_moe_layer(HIDDEN, EXPERTS, INTER, seed=i, device=dev) for i in range(L)]
     x = synthetic.randn_bf16((1, HIDDEN), 12345, dev)

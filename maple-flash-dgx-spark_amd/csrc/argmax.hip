@@ -44,7 +44,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_rows(const void* __re
   const int64_t nvec = vec ? n / PER : 0;  // rows not 16-byte aligned: scalar loop only
   const uint4* p = reinterpret_cast<const uint4*>(static_cast<const char*>(x) +
                                                   row * ldx * (DT == MA_BF16 ? 2 : 4));
-  constexpr int U = 4;
+  constexpr int U = 20;  // 1024 x 20 x 16 B = 320 KB in flight: one round for a 151936-token bf16 row
   for (int64_t v0 = tid; v0 < nvec; v0 += static_cast<int64_t>(kArgmaxThreads) * U) {
     uint4 q[U];
 #pragma unroll

@@ -28,7 +28,7 @@ constexpr int kVtRow = kSplit / 2 + 4;      // LDS row (one dim) of V position
                                             // pairs in words, padded
 constexpr size_t kCounterAlign = 256;
 constexpr int kCombineChunk = 12;           // splits whose partials load together
-constexpr int kTargetGroups = 1024;         // workgroups an attention launch aims for
+constexpr int kTargetGroups = 512;          // workgroups an attention launch aims for (swept: 512 best at batch 32)
 
 // Device-coherent (agent-scope) 8-byte store / load of two floats: visible to
 // workgroups on every XCD once the store has completed, without a fence.
