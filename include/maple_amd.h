@@ -202,8 +202,10 @@ int ma_moe_grouped(const void* x, int64_t ldx, int64_t tokens, int64_t top_k,
  * 768, 8) and (256, 128, 2); experts <= 256; other shapes return MA_EVALUE
  * (use the per-kernel entry points).  workspace:
  * ma_moe_fused_workspace_bytes(...) bytes, zero-filled before its first use
- * and never cleared again (the kernel keeps a monotonic counter there);
- * calls sharing a workspace must not overlap.  A cross-workgroup
+ * and never cleared again (the kernel keeps a call counter there and tags
+ * the data it hands between workgroups with it); calls sharing a workspace
+ * must not overlap.
+ * A cross-workgroup
  * wait that exceeds about 0.2 s sets the word read by ma_moe_fused_timed_out
  * instead of hanging.  Replaces MapleSparseMoeBlock.__call__ at T = 1,
  * src/maple_run/model.py:448-474 (router_topk, ternary_expert_swiglu,

@@ -9,20 +9,23 @@
 // of it (kernels/fused_norm.py:31-56): s = a + b in float32, residual =
 // bf16(s), x = bf16(s * rsqrt(mean(s^2) + eps) * w).
 //
-// A persistent grid of G workgroups (all resident) runs four phases; the one
-// hand-off between workgroups goes through the workspace with
-// device-coherent stores and a monotonic counter (no grid barrier, nothing to
-// clear between calls):
-//   1. every workgroup stages x (after the optional add + RMSNorm);
-//   2. every workgroup computes all E router logits itself (the router is
-//      small and L2-resident) and the softmax + top-k;
-//   3. it issues its down-projection weight loads (known once the ids are),
-//      computes its slice of the 8 x I SwiGLU outputs, publishes them and
-//      counts itself in;
-//   4. it waits until all G have, stages h and finishes its rows of y.
-// The last workgroup to finish (a ticket) advances the counter base.  Every
-// wait is bounded (about 0.2 s); on timeout the workspace error word is set
-// and the kernel finishes with wrong values instead of hanging.
+// A persistent grid of G workgroups (all resident) runs four phases with two
+// hand-offs between workgroups, both through device-coherent memory and with
+// nothing to clear between calls:
+//   1. every workgroup stages x (after the optional add + RMSNorm); workgroup
+//      e < E also computes router logit e and publishes it tagged with the
+//      call's number;
+//   2. every workgroup polls the E tagged logits until all are this call's,
+//      and runs softmax + top-k itself;
+//   3. it issues its SwiGLU and down-projection weight loads (known once the
+//      ids are), computes its slice of the 8 x I SwiGLU outputs, publishes it;
+//   grid barrier (a two-level arrival tree, per-group release flags);
+//   4. it stages h and finishes its rows of y.
+// (Polling all of h directly instead of the barrier measured slower: every
+// workgroup re-reading 12+ KB while the last outputs land loads the same
+// coherent path the producers are writing through.)
+// Every wait is bounded (about 0.2 s); on timeout the workspace error word is
+// set and the kernel finishes with wrong values instead of hanging.
 #include "ternary_engine.h"
 #include "topk.h"
 
@@ -31,12 +34,24 @@ namespace ma {
 constexpr int kFusedWaves = 4;
 constexpr uint64_t kFusedSpin = 20000000ull;  // 0.2 s of the 100 MHz realtime counter
 
-// Workspace layout (uint32 words, then bytes):
-//   [1] end ticket   [2] error   [3] h-done counter (+1 per workgroup per call)
-//   [4] the counter's value when this call started (advanced by G by the
-//       last workgroup out, so the goal is base + G whatever the grid size)
-//   [256 bytes ...)  h, bf16 [TK * I]
-constexpr size_t kMoeWsHeader = 256;
+constexpr int kBarGroups = 16;  // sub-counters (and release flags) of the h barrier
+constexpr int kLine = 64;       // uint32 words in a 256-byte line
+
+// Workspace layout (256-byte lines of uint32 words; every counter and flag has
+// a line of its own so that arrivals and polls on different ones do not meet):
+//   line 0, word 2     error (1 = a wait timed out)
+//   lines 1 .. 16, 17  h barrier: sub-counters, top counter
+//   lines 18 .. 33     release flags, all holding the number of calls made
+//                      on this workspace
+//   [16 KB, 48 KB)     router logits: one tagged 64-bit word (tag << 32 |
+//                      float bits) per expert every 128 bytes, E <= 256
+//   [48 KB ...)        h, bf16 [TK * I]
+constexpr int kSubB = 1, kTopB = kSubB + kBarGroups, kFlags = kTopB + 1;
+constexpr size_t kLogitOff = 16384;
+constexpr int kLogitStride = 16;  // uint64 words between logits
+constexpr size_t kMoeWsHeader = 49152;
+static_assert(kFlags + kBarGroups <= static_cast<int>(kLogitOff / 256), "workspace lines");
+static_assert(kLogitOff + 256 * kLogitStride * 8 <= kMoeWsHeader, "workspace logits");
 
 __device__ __forceinline__ uint32_t ld_coh32(const uint32_t* p) {
   return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -50,8 +65,43 @@ __device__ __forceinline__ void st_coh32(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ void st_coh64(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
 __device__ __forceinline__ void st_coh16(uint16_t* p, uint16_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Grid barrier, run by all 64 lanes of wave 0 of every workgroup once its
+// global stores (and its read of the release flag, f_old) have completed.
+// Workgroup wg arrives on sub-counter wg % kBarGroups; the last arriver there
+// clears it and arrives on the top counter; the last arriver on top clears
+// that and writes f_old + 1 to all kBarGroups flags (one lane each), so the
+// flags always hold equal values and nothing needs clearing afterwards.  The
+// others poll their group's flag until it leaves f_old.  (One atomic per
+// workgroup on a single counter would serialise all G of them at one
+// address.)  Needs G >= kBarGroups, every workgroup resident.  Returns true
+// (on all lanes) if the wait timed out.
+__device__ bool grid_barrier(uint32_t* sub, uint32_t* top, uint32_t* flags, uint32_t f_old, int G,
+                             int wg, int lane, uint64_t t0) {
+  const int g = wg % kBarGroups;
+  int release = 0;
+  if (lane == 0) {
+    const uint32_t n_g = static_cast<uint32_t>((G - g + kBarGroups - 1) / kBarGroups);
+    if (atomicAdd(&sub[kLine * g], 1u) == n_g - 1) {
+      st_coh32(&sub[kLine * g], 0u);
+      if (atomicAdd(top, 1u) == static_cast<uint32_t>(kBarGroups - 1)) {
+        st_coh32(top, 0u);
+        release = 1;
+      }
+    }
+  }
+  if (__shfl(release, 0, 64) && lane < kBarGroups) st_coh32(&flags[kLine * lane], f_old + 1u);
+  int timed_out = 0;
+  if (lane == 0)
+    while (ld_coh32(&flags[kLine * g]) == f_old && !timed_out) {
+      __builtin_amdgcn_s_sleep(2);
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kFusedSpin;
+    }
+  return __shfl(timed_out, 0, 64) != 0;
 }
 
 // Shapes: H = 16 * KWH * LPRH (SwiGLU rows split over LPRH lanes), I = 16 *
@@ -69,45 +119,62 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   constexpr int NWH = KWH * LPRH, H = 16 * NWH;
   constexpr int NWI = KWI * LPRI, I = 16 * NWI;
   constexpr int RPIH = 64 / LPRH, PPI = RPIH / 2;      // SwiGLU: up/gate pairs per wave pass
-  constexpr int UNITS_WG = kFusedWaves * US * PPI;     // h outputs per workgroup
+  constexpr int OPW = US * PPI;                        // SwiGLU outputs per wave
   constexpr int RPID = 64 / LPRI;                      // down rows per wave pass
   constexpr int RPB = RPID * UD;                       // y rows per workgroup
   constexpr int SPW = TK >= kFusedWaves ? TK / kFusedWaves : 1;
   static_assert(TK % kFusedWaves == 0 || TK < kFusedWaves, "top-k split over waves");
-  static_assert(H % 8 == 0 && H / 8 <= 64 * kFusedWaves * 4, "router staging");
 
   __shared__ __align__(16) uint32_t xs[NWH][8];
   __shared__ float cw[NWH];
-  __shared__ __align__(16) uint16_t xr[H];         // bf16 x for the router
   __shared__ __align__(16) uint32_t hs[TK][NWI][8];
   __shared__ float hc[TK][NWI];
-  __shared__ float s_logit[64 * PER];
-  __shared__ int32_t s_ids[TK];
-  __shared__ float s_wts[TK];
-  __shared__ float red[kFusedWaves];
+  __shared__ float s_p[64 * PER];
+  __shared__ int s_rank[kFusedWaves][64 * PER];
+  __shared__ int32_t s_ids[kFusedWaves][TK];  // one copy per wave
+  __shared__ float s_wts[kFusedWaves][TK];
+  __shared__ float red[kFusedWaves], red2[kFusedWaves];
   __shared__ float part[kFusedWaves][RPB];
-  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, wg = blockIdx.x;
-  // h-done counter value at the start of this call (written only by the
-  // previous call's last workgroup, so every workgroup reads the same value)
-  const uint32_t base = ld_coh32(&ws[4]);
-  uint16_t* hbuf = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(ws) + kMoeWsHeader);
+  uint32_t* const flags = ws + kLine * kFlags;
+  uint64_t* const logits = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(ws) + kLogitOff);
+  uint16_t* const hbuf = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(ws) + kMoeWsHeader);
+  // Calls made on this workspace so far (the h barrier moves the flags to f0
+  // + 1 only once every workgroup has arrived, so every workgroup reads f0);
+  // this call's logits carry the tag f0 + 1.
+  const uint32_t f0 = ld_coh32(&flags[kLine * (wg % kBarGroups)]);
+  const uint64_t tag = static_cast<uint64_t>(f0 + 1u) << 32;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   bool timed_out = false;
+  const bool router_wg = wg < n_exp;  // workgroup e < E computes router logit e
 
-  // ---- 1. x (optionally add + RMSNorm), staged as raw bf16 and as x' pairs
+  // The residual of this workgroup's y rows, loaded now and used at the end
+  // (pointers that are always valid, so no branch makes the load wait here).
+  const int ro = wg * RPB + tid;
+  const int roc = ro < H ? ro : H - 1;
+  const uint16_t* const res_a = xb ? xa : (residual ? residual : xa);
+  const uint16_t* const res_b = xb ? xb : xa;
+  const uint32_t ra = res_a[roc], rb = res_b[roc];
+
+  // ---- 1. x (optionally add + RMSNorm) staged as x' pairs; workgroup e also
+  // takes the dot product with router row e (loaded alongside x)
+  float dot = 0.f;
   {
     // thread t owns words t, t + 256, ... (16 values each)
     constexpr int WPT = (NWH + 255) / 256;
     float v[WPT][16];
+    uint4 gr[WPT][2];
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
       const int w = tid + 256 * i;
       const int wc = w < NWH ? w : NWH - 1;
+      const uint4* gp = reinterpret_cast<const uint4*>(gate_w + static_cast<int64_t>(router_wg ? wg : 0) * H + wc * 16);
+      gr[i][0] = gp[0];
+      gr[i][1] = gp[1];
       const uint4 a0 = reinterpret_cast<const uint4*>(xa + wc * 16)[0];
       const uint4 a1 = reinterpret_cast<const uint4*>(xa + wc * 16)[1];
       const uint32_t u[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
@@ -153,87 +220,149 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
         cw[w] = prep_word_pairs(v[i], pr);
 #pragma unroll
         for (int j = 0; j < 8; ++j) xs[w][j] = pr[j];
-        uint4 r0, r1;
-        r0.x = pack_bf16x2(v[i][0], v[i][1]);   r0.y = pack_bf16x2(v[i][2], v[i][3]);
-        r0.z = pack_bf16x2(v[i][4], v[i][5]);   r0.w = pack_bf16x2(v[i][6], v[i][7]);
-        r1.x = pack_bf16x2(v[i][8], v[i][9]);   r1.y = pack_bf16x2(v[i][10], v[i][11]);
-        r1.z = pack_bf16x2(v[i][12], v[i][13]); r1.w = pack_bf16x2(v[i][14], v[i][15]);
-        reinterpret_cast<uint4*>(xr + w * 16)[0] = r0;
-        reinterpret_cast<uint4*>(xr + w * 16)[1] = r1;
+        // the bf16 x words themselves, against the router row
+        const uint32_t g[8] = {gr[i][0].x, gr[i][0].y, gr[i][0].z, gr[i][0].w,
+                               gr[i][1].x, gr[i][1].y, gr[i][1].z, gr[i][1].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dot = dot2(pack_bf16x2(v[i][2 * j], v[i][2 * j + 1]), g[j], dot);
       }
     }
   }
+  if (router_wg) {
+    const float s = group_sum<64>(dot);
+    if (lane == 0) red2[wv] = s;
+  }
   __syncthreads();
+  if (router_wg && tid == 0) {
+    float l = red2[0];
+#pragma unroll
+    for (int w = 1; w < kFusedWaves; ++w) l += red2[w];
+    st_coh64(&logits[kLogitStride * wg], tag | __float_as_uint(l + (bias ? bias[wg] : 0.f)));
+  }
 
-  // ---- 2. router: every workgroup computes all E logits itself (the router
-  // weights are L2-resident after the first workgroup of an XCD reads them),
-  // so no workgroup waits for another to learn the expert ids.  Wave w takes
-  // experts w, w + 4, ...; lane l holds x[32 l, 32 l + 32) for H = 2048.
-  {
-    constexpr int XU = H / 8 / 64;  // uint4 of x (and of a router row) per lane
-    static_assert(H % 512 == 0 || H == 256, "router lane split");
-    constexpr int XUL = XU > 0 ? XU : 1;
-    uint4 xl[XUL];
-#pragma unroll
-    for (int i = 0; i < XUL; ++i) {
-      const int idx = lane * XUL + i;
-      xl[i] = idx < H / 8 ? reinterpret_cast<const uint4*>(xr)[idx] : make_uint4(0, 0, 0, 0);
-    }
-    constexpr int EB = 4;  // experts per batch of loads
-    for (int e0 = wv * EB; e0 < n_exp; e0 += kFusedWaves * EB) {
-      uint4 wr[EB][XUL];
-#pragma unroll
-      for (int b = 0; b < EB; ++b) {
-        const int e = e0 + b < n_exp ? e0 + b : n_exp - 1;
-        const uint4* wp = reinterpret_cast<const uint4*>(gate_w + static_cast<int64_t>(e) * H);
-#pragma unroll
-        for (int i = 0; i < XUL; ++i) {
-          const int idx = lane * XUL + i;
-          wr[b][i] = idx < H / 8 ? wp[idx] : make_uint4(0, 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int b = 0; b < EB; ++b) {
-        float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-        for (int i = 0; i < XUL; ++i) {
-          a0 = dot2(xl[i].x, wr[b][i].x, a0);
-          a1 = dot2(xl[i].y, wr[b][i].y, a1);
-          a0 = dot2(xl[i].z, wr[b][i].z, a0);
-          a1 = dot2(xl[i].w, wr[b][i].w, a1);
-        }
-        const float sum = group_sum<64>(a0 + a1);
-        if (lane == 0 && e0 + b < n_exp) s_logit[e0 + b] = sum + (bias ? bias[e0 + b] : 0.f);
-      }
-    }
-  }
-  __syncthreads();
+  // ---- 2. softmax + top-k in every workgroup (router semantics of reference
+  // kernels/router.py:78-126), once wave 0 has seen all E logits of this call
+  // (each lane polls its tagged logit words until they carry this call's tag).
+  // The rank of an expert (experts with a larger probability, or an equal one
+  // at a lower index) is counted by all four waves over a quarter of the
+  // experts each; then every wave finds, per slot s, the expert of rank s by
+  // a ballot, so each wave holds the routing without further hand-offs.
   if (wv == 0) {
     float p[PER];
+    bool have[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      have[i] = lane + 64 * i >= n_exp;
+      p[i] = -INFINITY;
+    }
+    for (;;) {
+      bool done = true;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        if (!have[i]) {
+          const uint64_t v = ld_coh64(&logits[kLogitStride * (lane + 64 * i)]);
+          have[i] = (v & 0xffffffff00000000ull) == tag;
+          p[i] = __uint_as_float(static_cast<uint32_t>(v));
+          done = done && have[i];
+        }
+      }
+      if (__all(done) || timed_out) break;
+      __builtin_amdgcn_s_sleep(2);
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kFusedSpin;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) m = fmaxf(m, p[i]);
+    m = wave_max(m);
+    float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int e = lane + 64 * i;
-      p[i] = e < n_exp ? s_logit[e] : -INFINITY;
+      p[i] = e < n_exp ? expf(p[i] - m) : 0.f;
+      sum += p[i];
     }
-    softmax_topk<PER>(p, n_exp, TK, s_ids, s_wts);
+    const float inv_sum = 1.0f / group_sum<64>(sum);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = lane + 64 * i;
+      s_p[e] = e < n_exp ? p[i] * inv_sum : -INFINITY;
+    }
   }
   __syncthreads();
-  if (wg == 0 && tid < TK) {
-    ids_out[tid] = s_ids[tid];
-    wts_out[tid] = s_wts[tid];
+  {
+    constexpr int NJ = 64 * PER / kFusedWaves;  // experts each wave compares against
+    float p[PER];
+    int rank[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      p[i] = s_p[lane + 64 * i];
+      rank[i] = 0;
+    }
+    const int j0 = wv * NJ;
+#pragma unroll
+    for (int jj = 0; jj < NJ; jj += 4) {
+      const float4 q4 = *reinterpret_cast<const float4*>(&s_p[j0 + jj]);  // same address in every lane
+      const float q[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int j = j0 + jj + t;
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+          rank[i] += (q[t] > p[i]) || (q[t] == p[i] && j < lane + 64 * i);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) s_rank[wv][lane + 64 * i] = rank[i];
+  }
+  __syncthreads();
+  {
+    float p[PER], sel = 0.f;
+    int rank[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = lane + 64 * i;
+      p[i] = s_p[e];
+      rank[i] = s_rank[0][e];
+#pragma unroll
+      for (int w = 1; w < kFusedWaves; ++w) rank[i] += s_rank[w][e];
+      sel += rank[i] < TK ? p[i] : 0.f;  // invalid experts (p = -inf) rank behind every valid one
+    }
+    const float inv_total = 1.0f / (group_sum<64>(sel) + 1e-20f);
+#pragma unroll
+    for (int s = 0; s < TK; ++s) {
+      int e_s = 0;
+      float p_s = 0.f;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const uint64_t hit = __ballot(rank[i] == s);
+        if (hit) {
+          const int l = __builtin_ctzll(hit);
+          e_s = l + 64 * i;
+          p_s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[i]), l));
+        }
+      }
+      // every lane writes the same values, so each lane's later reads follow its own writes
+      s_ids[wv][s] = e_s;
+      s_wts[wv][s] = p_s * inv_total;
+    }
+  }
+  if (wg == 0 && wv == 0 && lane < TK) {
+    ids_out[lane] = s_ids[0][lane];
+    wts_out[lane] = s_wts[0][lane];
   }
 
-  // ---- 3. weights: SwiGLU rows of this workgroup's h outputs, then the down
-  // rows of its y rows (every load issued before any arithmetic)
+  // ---- 3. weights: SwiGLU rows of this wave's h outputs, then the down rows
+  // of this workgroup's y rows (every load issued before any arithmetic)
   const int klh = lane % LPRH, subh = lane / LPRH, half = subh / PPI, pi = subh % PPI;
+  const int o0 = (wg * kFusedWaves + wv) * OPW;  // this wave's first SwiGLU output
   uint32_t wu[US][KWH];
   float au[US];
 #pragma unroll
   for (int u = 0; u < US; ++u) {
-    int ug_i = (wg * kFusedWaves + wv) * (US * PPI) + u * PPI + pi;
+    int ug_i = o0 + u * PPI + pi;
     ug_i = ug_i < TK * I ? ug_i : TK * I - 1;
     const int s = ug_i / I, j = ug_i % I;
-    const int64_t e = clamp_id(s_ids[s], n_exp);
+    const int64_t e = clamp_id(s_ids[wv][s], n_exp);
     const int64_t row = e * (2 * I) + j + half * I;
     load_words_v<KWH>(ug + row * NWH + klh * KWH, wu[u]);
     au[u] = bf16_to_f32(ug_alpha[row]);
@@ -246,8 +375,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   for (int q = 0; q < SPW; ++q) {
     const int js = wv + kFusedWaves * q;
     const int jj = js < TK ? js : 0;  // idle waves (TK < waves) read slot 0 and add nothing
-    const int64_t e = clamp_id(s_ids[jj], n_exp);
-    wj[q] = js < TK ? s_wts[jj] : 0.f;
+    const int64_t e = clamp_id(s_ids[wv][jj], n_exp);
+    wj[q] = js < TK ? s_wts[wv][jj] : 0.f;
 #pragma unroll
     for (int u = 0; u < UD; ++u) {
       int r = rbase + u * RPID + subd;
@@ -256,17 +385,9 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
       ad[q][u] = bf16_to_f32(dn_alpha[e * H + r]);
     }
   }
-  float resv = 0.f;
-  const int ro = rbase + tid;
-  if (tid < RPB && ro < H) {
-    if (xb)
-      resv = bf16_to_f32(f32_to_bf16(bf16_to_f32(xa[ro]) + bf16_to_f32(xb[ro])));
-    else if (residual)
-      resv = bf16_to_f32(residual[ro]);
-  }
   MA_ISSUE_FENCE();
 
-  // SwiGLU outputs of this workgroup
+  // SwiGLU outputs of this wave
   {
     XSlice<KWH> xsl;
     slice_from_lds<KWH>(xs, cw, klh, xsl);
@@ -275,43 +396,46 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     for (int u = 0; u < US; ++u) {
       const float v = group_sum<LPRH>(slice_dot<KWH>(wu[u], xsl, kc) * au[u]);
       const float g = __shfl(v, lane + PPI * LPRH, 64);
-      const int ug_i = (wg * kFusedWaves + wv) * (US * PPI) + u * PPI + pi;
+      const int ug_i = o0 + u * PPI + pi;
       if (half == 0 && klh == 0 && ug_i < TK * I) st_coh16(&hbuf[ug_i], f32_to_bf16(swiglu_act(v, g)));
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // this workgroup's h stores have completed
   __syncthreads();
-  // ---- 4. count this workgroup in, wait until all G are (one lane polls a
-  // single monotonic counter: it reads base + G once this call's h is out)
-  if (tid == 0) {
-    atomicAdd(&ws[3], 1u);
-    const uint32_t goal = base + static_cast<uint32_t>(G);
-    while (static_cast<int32_t>(ld_coh32(&ws[3]) - goal) < 0 && !timed_out) {
-      __builtin_amdgcn_s_sleep(2);
-      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kFusedSpin;
-    }
-  }
+  // ---- 4. barrier (all of h out), stage h, finish this workgroup's rows of y
+  if (wv == 0) timed_out = grid_barrier(ws + kLine * kSubB, ws + kLine * kTopB, flags, f0, G, wg, lane, t0) || timed_out;
   __syncthreads();
-  for (int wi = tid; wi < TK * NWI; wi += 256) {
-    const int s = wi / NWI, w = wi % NWI;
-    const uint64_t* src = reinterpret_cast<const uint64_t*>(hbuf + s * I + w * 16);
-    uint32_t u[8];
+  {
+    constexpr int HIT = (TK * NWI + 255) / 256;  // h words per thread, all loads issued first
+    uint64_t d[HIT][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint64_t d = ld_coh64(src + q);
-      u[2 * q] = static_cast<uint32_t>(d);
-      u[2 * q + 1] = static_cast<uint32_t>(d >> 32);
+    for (int it = 0; it < HIT; ++it) {
+      const int wi = tid + 256 * it;
+      const int wc = wi < TK * NWI ? wi : TK * NWI - 1;
+      const uint64_t* src = reinterpret_cast<const uint64_t*>(hbuf + (wc / NWI) * I + (wc % NWI) * 16);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) d[it][q] = ld_coh64(src + q);
     }
-    float vv[16];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      vv[2 * q] = __uint_as_float(u[q] << 16);
-      vv[2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
+    for (int it = 0; it < HIT; ++it) {
+      const int wi = tid + 256 * it;
+      if (wi < TK * NWI) {
+        const int s = wi / NWI, w = wi % NWI;
+        float vv[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = static_cast<uint32_t>(d[it][q]), hi = static_cast<uint32_t>(d[it][q] >> 32);
+          vv[4 * q] = __uint_as_float(lo << 16);
+          vv[4 * q + 1] = __uint_as_float(lo & 0xffff0000u);
+          vv[4 * q + 2] = __uint_as_float(hi << 16);
+          vv[4 * q + 3] = __uint_as_float(hi & 0xffff0000u);
+        }
+        uint32_t pr[8];
+        hc[s][w] = prep_word_pairs(vv, pr);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hs[s][w][j] = pr[j];
+      }
     }
-    uint32_t pr[8];
-    hc[s][w] = prep_word_pairs(vv, pr);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) hs[s][w][j] = pr[j];
   }
   __syncthreads();
 
@@ -341,37 +465,32 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   }
   __syncthreads();
   if (tid < RPB && ro < H) {
-    float v = resv;
+    float v = xb ? bf16_to_f32(f32_to_bf16(__uint_as_float(ra << 16) + __uint_as_float(rb << 16)))
+                 : residual ? __uint_as_float(ra << 16) : 0.f;
 #pragma unroll
     for (int ww = 0; ww < kFusedWaves; ++ww) v += part[ww][tid];
     y[ro] = f32_to_bf16(v);
   }
   if (__ballot(timed_out) && lane == 0) st_coh32(&ws[2], 1u);
-
-  // ---- the last workgroup out advances the counter base
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) s_last = atomicAdd(&ws[1], 1u) == static_cast<uint32_t>(G - 1);
-  __syncthreads();
-  if (s_last && tid == 0) {
-    st_coh32(&ws[1], 0u);
-    st_coh32(&ws[4], base + static_cast<uint32_t>(G));
-  }
 }
 
 }  // namespace ma
+
+
 
 using namespace ma;
 
 namespace {
 
-// Supported (hidden, intermediate, top_k) shapes and their grid.
+// Supported (hidden, intermediate, top_k) shapes and their grid (at least
+// kBarGroups workgroups, and at least one per expert).
 struct FusedShape {
   int hidden, inter, top_k, grid;
 };
 // (2048, 768, 8): SwiGLU 24 outputs and down 8 rows per workgroup -> 256 groups.
 // (256, 128, 2): SwiGLU 16 outputs, down 8 rows per workgroup -> 32 groups.
 constexpr FusedShape kShapes[] = {{2048, 768, 8, 256}, {256, 128, 2, 32}};
+static_assert(kShapes[0].grid >= kBarGroups && kShapes[1].grid >= kBarGroups, "barrier groups");
 
 const FusedShape* find_shape(int64_t hidden, int64_t inter, int64_t top_k) {
   for (const auto& s : kShapes)
@@ -405,7 +524,7 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
     return fail(MA_EVALUE, "moe_fused: shape (hidden %lld, inter %lld, top_k %lld) not built",
                 static_cast<long long>(hidden), static_cast<long long>(inter),
                 static_cast<long long>(top_k));
-  if (n_experts < top_k || n_experts > 256 || n_experts > static_cast<int64_t>(s->grid) * 64)
+  if (n_experts < top_k || n_experts > 256 || n_experts > static_cast<int64_t>(s->grid))
     return fail(MA_EVALUE, "moe_fused: %lld experts unsupported", static_cast<long long>(n_experts));
   if (x_add && !norm_weight) return fail(MA_EVALUE, "moe_fused: add without norm weight");
   if (norm_weight && norm_dtype != MA_F32 && norm_dtype != MA_BF16)

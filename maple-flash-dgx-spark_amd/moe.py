@@ -35,19 +35,20 @@ from .synthetic import MoELayer
 
 GROUPED_MIN_TOKENS = 4
 
-# One zero-filled workspace per device for the one-launch layer kernel: calls
-# hand data between workgroups through it, tagged by a generation counter the
-# kernel advances, so it is never cleared again.  Calls on one device must not
-# overlap (decode runs from one stream).
-_FUSED_WS: dict[int, torch.Tensor] = {}
+# One zero-filled workspace per device and built shape for the one-launch
+# layer kernel: its workgroups hand data to each other through it, tagged with
+# per-workgroup call counters the kernel keeps there, so it is never cleared
+# again.  Calls on one device must not overlap (decode runs from one stream).
+_FUSED_WS: dict[tuple, torch.Tensor] = {}
 
 
-def _fused_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+def _fused_workspace(device: torch.device, shape: tuple, nbytes: int) -> torch.Tensor:
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    ws = _FUSED_WS.get(idx)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 16), device=device, dtype=torch.uint8)
-        _FUSED_WS[idx] = ws
+    key = (idx,) + shape
+    ws = _FUSED_WS.get(key)
+    if ws is None:
+        ws = torch.zeros(nbytes, device=device, dtype=torch.uint8)
+        _FUSED_WS[key] = ws
     return ws
 
 
@@ -65,8 +66,8 @@ def moe_fused_timed_out(device: torch.device | int = 0) -> bool:
     """True if a one-launch MoE call on ``device`` ever timed out waiting for
     another workgroup (the kernel records it instead of hanging).  Syncs."""
     idx = device if isinstance(device, int) else (device.index or 0)
-    ws = _FUSED_WS.get(idx)
-    return bool(ws is not None and int(ws[8:12].view(torch.int32).item()) != 0)
+    return any(int(ws[8:12].view(torch.int32).item()) != 0
+               for key, ws in _FUSED_WS.items() if key[0] == idx)
 
 
 def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tensor | None = None,
@@ -90,7 +91,7 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
     if nbytes == 0:
         raise ValueError(f"moe_fused: shape (hidden {hidden}, inter {layer.inter}, top_k {top_k}) "
                          "is not built into the one-launch kernel")
-    ws = _fused_workspace(x.device, nbytes)
+    ws = _fused_workspace(x.device, (hidden, layer.inter, top_k), nbytes)
     y = torch.empty(1, hidden, device=x.device, dtype=torch.bfloat16)
     ids = torch.empty(1, top_k, device=x.device, dtype=torch.int32)
     wts = torch.empty(1, top_k, device=x.device, dtype=torch.float32)
