@@ -2,8 +2,9 @@
 
 Workload: one synthetic MoE FFN layer (hidden 2048, 64 experts, SwiGLU
 intermediate 768, top-8 routing) at decode batch 1, run through the HIP
-kernels (router top-k, fused up+gate SwiGLU, down projection + weighted
-combine).  ``--layers`` distinct layers (default 96: 7.3 GB of packed
+one-launch MoE kernel (router top-k, up+gate SwiGLU, down projections and the
+weighted combine in one persistent launch; the three-launch per-slot chain is
+timed beside it).  ``--layers`` distinct layers (default 96: 7.3 GB of packed
 weights, of which the 8 selected experts per layer are 0.91 GB, 3.6 times the
 256 MB Infinity Cache) are captured in one HIP graph and replayed in a cycle,
 so every layer's weights come from HBM.
@@ -13,13 +14,13 @@ cold layer.  ``value`` is the whole-layer algorithmic HBM throughput:
 (selected experts' packed codes + scales, the router weight, x in and y out)
 per layer, times layers and steps, over the timed wall time.
 
-``roofline`` covers the dominant kernel (the SwiGLU expert kernel, which
-streams 2/3 of the bytes): algorithmic bytes per launch over its average
-launch period, timed with HIP events on the stream it runs on over a graph of
-back-to-back launches on the same cold layers (the period includes the
-dispatch gap between dependent kernels, so it is an upper bound on the
-kernel's own duration).  ``traffic`` is read from the rocprofv3 counter
-summary under profiles/ when present.
+``roofline`` covers the dominant kernel, which is the whole layer here
+(``k_moe_fused``): algorithmic bytes per launch over its average launch
+period, timed with HIP events on the stream it runs on over the graph of
+back-to-back launches on the cold layers (the period includes the dispatch
+gap between dependent kernels, so it is an upper bound on the kernel's own
+duration).  ``traffic`` is read from the rocprofv3 counter summary under
+profiles/ when present.
 
 ``cpu_baseline`` times the CPU oracle path (NumPy unpack -> dequantise ->
 float32 matmul over the 8 selected experts, the reference's own test
@@ -27,7 +28,7 @@ oracle) on a bounded sample of the same workload on this host's cores.
 
     python bench.py [--steps 20] [--warmup 3] [--layers 96] [--no-cpu]
                     [--no-decoder] [--no-extra]
-    python bench.py --counters-pass   # SwiGLU graph + a 256 MiB copy, for rocprofv3 --pmc
+    python bench.py --counters-pass   # MoE layer graph + a 256 MiB copy, for rocprofv3 --pmc
     python bench.py --decode-batch 32 # only the full decoder at one batch size
 """
 
@@ -59,9 +60,7 @@ def layer_bytes() -> dict:
     expert = codes + alpha
     router = EXPERTS * HIDDEN * 2
     act = HIDDEN * 2 * 2
-    swiglu = TOPK * (2 * INTER * HIDDEN // 4 + 2 * INTER * 2) + HIDDEN * 2 + TOPK * INTER * 2
-    return {"expert": expert, "selected": TOPK * expert, "layer": TOPK * expert + router + act,
-            "swiglu_launch": swiglu}
+    return {"expert": expert, "selected": TOPK * expert, "layer": TOPK * expert + router + act}
 
 
 def graph_of(fn):
@@ -226,34 +225,41 @@ def cpu_baseline(seconds: float = 12.0) -> dict:
 
 def counters_pass(dev, n_layers: int) -> int:
     """Workload for rocprofv3 --pmc passes (FETCH_SIZE / WRITE_SIZE per
-    dispatch): the SwiGLU expert kernel over ``n_layers`` cold layers, twice,
-    then a plain 256 MiB device copy four times to calibrate the counter
-    against a known byte count.  Traffic does not depend on the weight values,
-    so the layers are left uninitialised and the 8 experts of layer l are fixed
-    (8l .. 8l+7 mod 64): no random-number kernels run under the profiler."""
+    dispatch): the one-launch MoE layer kernel over ``n_layers`` cold layers,
+    twice, then a plain 256 MiB device copy four times to calibrate the
+    counter against a known byte count.  Traffic does not depend on the weight
+    values, so the expert weights are left uninitialised; the router rows are
+    set (by fill kernels, no random numbers under the profiler) so that layer
+    l selects 8 distinct experts, 8l + 56 .. 8l + 63 mod 64."""
     import torch
 
-    from maple_amd.kernels import ternary_expert_swiglu
+    from maple_amd import synthetic
+    from maple_amd.moe import moe_block
 
     kw = HIDDEN // 16
-    ug = [torch.empty(EXPERTS, 2 * INTER, kw, device=dev, dtype=torch.int32).view(torch.uint32)
-          for _ in range(n_layers)]
-    ua = [torch.empty(EXPERTS, 2 * INTER, device=dev, dtype=torch.bfloat16) for _ in range(n_layers)]
-    ids = [torch.tensor([[(8 * l + j) % EXPERTS for j in range(TOPK)]], dtype=torch.int32).to(dev)
-           for l in range(n_layers)]
+    layers = []
+    e = torch.arange(EXPERTS, device=dev, dtype=torch.float32)
+    for l in range(n_layers):
+        rank = torch.remainder(e - 8 * l, EXPERTS)  # logit of expert e with x = ones: rank / 64
+        gate = (rank / (EXPERTS * HIDDEN))[:, None].expand(EXPERTS, HIDDEN).to(torch.bfloat16).contiguous()
+        ug = torch.empty(EXPERTS, 2 * INTER, kw, device=dev, dtype=torch.int32).view(torch.uint32)
+        ua = torch.empty(EXPERTS, 2 * INTER, device=dev, dtype=torch.bfloat16)
+        dn = torch.empty(EXPERTS, HIDDEN, INTER // 16, device=dev, dtype=torch.int32).view(torch.uint32)
+        da = torch.empty(EXPERTS, HIDDEN, device=dev, dtype=torch.bfloat16)
+        layers.append(synthetic.MoELayer(gate, ug, ua, dn, da, None))
     x = torch.ones(1, HIDDEN, dtype=torch.bfloat16).to(dev)
     torch.cuda.synchronize()
     for _ in range(2):
         for l in range(n_layers):
-            ternary_expert_swiglu(x, ug[l], ua[l], ids[l])
+            moe_block(x, layers[l], TOPK, plan="fused")
     torch.cuda.synchronize()
     a = torch.empty(128 << 20, device=dev, dtype=torch.bfloat16)
     b = torch.empty_like(a)
     for _ in range(4):
         b.copy_(a)
     torch.cuda.synchronize()
-    print(json.dumps({"counters_pass": True, "swiglu_launches": 2 * n_layers,
-                      "swiglu_bytes_per_launch": layer_bytes()["swiglu_launch"],
+    print(json.dumps({"counters_pass": True, "moe_fused_launches": 2 * n_layers,
+                      "layer_bytes_per_launch": layer_bytes()["layer"],
                       "copy_bytes_read": a.numel() * 2, "copy_bytes_written": a.numel() * 2}),
           flush=True)
     return 0
@@ -266,7 +272,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=96)
     ap.add_argument("--counters-pass", action="store_true",
-                    help="only replay the SwiGLU graph and a plain 256 MiB copy (for counters)")
+                    help="only run the MoE layer kernel and a plain 256 MiB copy (for counters)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-decoder", action="store_true")
@@ -284,7 +290,6 @@ def main() -> int:
 
     __graft_entry__.load_package()
     from maple_amd import synthetic
-    from maple_amd.kernels import router_topk, ternary_expert_swiglu
     from maple_amd.moe import moe_block
 
     dev = torch.device("cuda:0")
@@ -302,45 +307,38 @@ def main() -> int:
     x = synthetic.randn_bf16((1, HIDDEN), 12345, dev)
     torch.cuda.synchronize()
 
-    # Whole-layer timing: L layer decodes per graph replay.
+    # Whole-layer timing: L layer decodes per graph replay (one launch each).
     g = graph_of(lambda: [moe_block(x, layers[i], TOPK) for i in range(L)])
     for _ in range(args.warmup):
         g.replay()
     torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(True), torch.cuda.Event(True)
     t0 = time.perf_counter()
-    e0.record()
+    e0.record(s)
     for _ in range(args.steps):
         g.replay()
-    e1.record()
+    e1.record(s)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
     value = nb["layer"] * L / (ms * 1e-3) / 1e9
+    per_launch = ms * 1e-3 / L  # the whole layer is one k_moe_fused launch
+    achieved = nb["layer"] / per_launch / 1e9
     log(f"MoE layer bs1: {ms * 1e3 / L:.2f} us/layer, {value:.1f} GB/s (wall {wall:.3f} s)")
+    del g
+    from maple_amd.moe import moe_fused_timed_out
 
-    # Dominant kernel: SwiGLU expert kernel over the same cold layers.
-    ids = [router_topk(x, layers[i].gate_weight, TOPK)[0] for i in range(L)]
-    gk = graph_of(lambda: [ternary_expert_swiglu(x, layers[i].up_gate_packed,
-                                                 layers[i].up_gate_alpha, ids[i]) for i in range(L)])
-    for _ in range(args.warmup):
-        gk.replay()
-    torch.cuda.synchronize()
-    s = torch.cuda.current_stream()
-    k0, k1 = torch.cuda.Event(True), torch.cuda.Event(True)
-    k0.record(s)
-    for _ in range(args.steps):
-        gk.replay()
-    k1.record(s)
-    torch.cuda.synchronize()
-    per_launch = k0.elapsed_time(k1) / (args.steps * L) * 1e-3
-    achieved = nb["swiglu_launch"] / per_launch / 1e9
-    log(f"swiglu kernel: {per_launch * 1e6:.2f} us/launch, {achieved:.1f} GB/s")
+    # The three-launch chain (router, SwiGLU, down + combine) on the same layers.
+    gc = graph_of(lambda: [moe_block(x, layers[i], TOPK, plan="per_slot") for i in range(L)])
+    chain = time_graph(gc, args.steps, args.warmup) / L
+    del gc
+    log(f"per-slot chain: {chain * 1e6:.2f} us/layer")
 
     from maple_amd.kernels.router import router_wait_timed_out
 
-    if router_wait_timed_out(dev):
-        log("router reported a timed-out wait: results invalid")
+    if router_wait_timed_out(dev) or moe_fused_timed_out(dev):
+        log("a kernel reported a timed-out cross-workgroup wait: results invalid")
         return 1
     out = {
         "metric": METRIC,
@@ -357,11 +355,12 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "moe_ffn_layer_decode_bs1", "hidden": HIDDEN, "experts": EXPERTS,
                    "intermediate": INTER, "top_k": TOPK, "tokens": 1, "cold_layers": L,
-                   "bytes_per_layer": nb["layer"], "us_per_layer": round(ms * 1e3 / L, 3)},
+                   "bytes_per_layer": nb["layer"], "us_per_layer": round(ms * 1e3 / L, 3),
+                   "per_slot_chain_us_per_layer": round(chain * 1e6, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic("swiglu_bs1"), "kernel": "k_swiglu_fast",
-                     "bytes_per_launch": nb["swiglu_launch"],
+                     "traffic": read_traffic("moe_fused_bs1"), "kernel": "k_moe_fused",
+                     "bytes_per_launch": nb["layer"],
                      "us_per_launch": round(per_launch * 1e6, 3)},
         "cpu_baseline": None,
         "decode": None,

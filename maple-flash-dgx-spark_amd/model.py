@@ -9,8 +9,9 @@ One decode step, per layer:
   o     = ternary_gemv(attn, W_o)
   hidden, mlp_in = add_rms_norm(hidden, o, post_ln)
   hidden = moe_block(mlp_in, residual=hidden)
-  (with fused_moe=True at batch 1, when built for the shape, the last two
-  lines are one launch: moe_fused(hidden, add=o, norm_weight=post_ln))
+  (at batch 1, when the one-launch MoE kernel is built for the shape and
+  fused_moe is left True, the last two lines are one launch:
+  moe_fused(hidden, add=o, norm_weight=post_ln))
 then seqlen += 1, final rms_norm, RTN4 lm_head, greedy argmax.
 
 Weights are random with the synthetic distributions (``synthetic.py``): every
@@ -98,7 +99,7 @@ class KVCache:
 
 class SyntheticDecoder:
     def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 4096 + 128,
-                 fused_moe: bool = False):
+                 fused_moe: bool = True):
         self.cfg = cfg
         self.fused_moe = fused_moe
         self.device = torch.device(device)

@@ -2,20 +2,21 @@
 
 ``MapleSparseMoeBlock`` keeps the reference composition and call signature:
 router -> up+gate SwiGLU -> down -> top-k combine (+ residual), with no host
-sync and no per-expert Python loop.  Two execution plans, chosen by the token
-count alone (never by routing, which stays on the device):
+sync and no per-expert Python loop.  Three execution plans, chosen by the
+token count and the shape alone (never by routing, which stays on the
+device):
 
-* ``plan="fused"`` (one token, shapes built into ``ma_moe_fused``): router,
+* one token, shapes built into ``ma_moe_fused`` (``plan="fused"``): router,
   SwiGLU, down and combine (optionally with the add + RMSNorm ahead of the
-  block) in one persistent launch.  Measured slower than the per-slot chain
-  (23 us against 14.3 us per layer at hidden 2048 / 64 experts): its phases
-  are a longer chain of dependent memory round trips than three launches
-  are, so "auto" does not pick it.
-* decode (``tokens < GROUPED_MIN_TOKENS``): per-slot kernels, as the
-  reference does -- fused SwiGLU, then the down projection and the combine in
-  one launch (``ternary_expert_down_sum``).  That skips the reference's bf16
-  rounding of each slot's down output before the combine
-  (``model.py:470-473``); the result stays within bf16 tolerance of it.
+  block) in one persistent launch; 12.0 us per layer at hidden 2048 / 64
+  experts / top-8 against 14.2 us for the per-slot chain.  Rounding points
+  match the reference (bf16 h, bf16 per-slot output, float32 combine).
+* other decode (``tokens < GROUPED_MIN_TOKENS``, ``plan="per_slot"``):
+  per-slot kernels, as the reference does -- fused SwiGLU, then the down
+  projection and the combine in one launch (``ternary_expert_down_sum``).
+  That skips the reference's bf16 rounding of each slot's down output before
+  the combine (``model.py:470-473``); the result stays within bf16 tolerance
+  of it.
 * batched decode / prefill: dispatch the (token, slot) pairs into per-expert
   lists and run grouped MFMA GEMMs (``ma_moe_grouped``), so each selected
   expert's weights are read once per tile of its tokens instead of once per
@@ -149,10 +150,13 @@ def moe_block(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
               *, plan: str = "auto"):
     """One MoE layer on ``x [..., H]``; returns ``(y, ids, weights)``.
 
-    ``plan``: "auto" (grouped MFMA from GROUPED_MIN_TOKENS tokens, per-slot
-    kernels below), or "per_slot" / "grouped" / "fused" to force one."""
+    ``plan``: "auto" (the one-launch kernel for one token where it is built,
+    grouped MFMA from GROUPED_MIN_TOKENS tokens, per-slot kernels otherwise),
+    or "per_slot" / "grouped" / "fused" to force one."""
     hidden = x.shape[-1]
     xf = x.reshape(-1, hidden)
+    if plan == "auto" and xf.shape[0] == 1 and fused_supported(layer, top_k, xf):
+        plan = "fused"
     if plan == "fused":
         y, ids, wts = moe_fused(xf, layer, top_k, residual)
         return y.reshape(x.shape), ids, wts
