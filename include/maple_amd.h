@@ -252,11 +252,14 @@ int ma_qk_norm_rope_store(const void* qkv, int64_t ldq, int64_t batch, int n_hea
  * positions [start, min(seqlen[b] + 1, max_len)) of cache row row_map[b] (b
  * when NULL), start = kv_len - window when window > 0.  q / out bf16
  * [batch, n_heads, head_dim], float32 accumulation, P rounded to bf16, split
- * over the sequence (128 positions per split) and merged in the same launch.
+ * over the sequence (128 positions per split) and merged in the same launch
+ * (the splits of a (row, KV head) meet at a barrier, then each merges a slice).
  * workspace: ma_gqa_workspace_bytes(batch, n_kv_heads, max_len) bytes,
- * 16-byte aligned; its first bytes are per-(row, KV head) tickets that must
- * be zero before the first call (each call leaves them zero).  Calls that
- * share a workspace must not overlap.  head_dim must be 64.
+ * 16-byte aligned, zero-filled before the first call: it starts with a sync
+ * area of 256-byte lines (line 0, int32 word 2: set to 1 if a barrier wait
+ * ever exceeded about 0.2 s; then per (row, KV head) an arrival-counter line,
+ * which each call leaves at zero, and a generation line).  Calls that share a
+ * workspace must not overlap.  head_dim must be 64.
  * Replaces decode_gqa_attn, src/maple_run/kernels/decode_attn.py:470-592
  * (which merges the splits in a second kernel, :317-359).
  */

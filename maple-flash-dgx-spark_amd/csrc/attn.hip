@@ -1,8 +1,9 @@
 // Decode attention for q_len = 1 (gfx950): QK RMSNorm + partial RoPE + KV
-// write, and split-sequence GQA whose partials are merged by the last split
-// to finish (a ticket per (row, KV head)), so one launch does the whole
-// attention.  A fused entry point also does the QK-norm/RoPE/KV write inside
-// the same launch.
+// write, and split-sequence GQA whose partials are merged in the same launch:
+// the splits of a (row, KV head) meet at a barrier of their own, then each
+// merges a slice of the output, so one launch does the whole attention.  A
+// fused entry point also does the QK-norm/RoPE/KV write inside the same
+// launch.
 //
 // Semantics of reference src/maple_run/kernels/decode_attn.py:
 //   apply_qkv_decode (:16-62, :65-163, :362-439): per head x * rsqrt(mean(x^2)
@@ -26,23 +27,38 @@ constexpr int kAttnThreads = 256;           // 4 waves, 32 positions of a chunk 
 constexpr int kMaxGroup = 16;               // query heads per KV head
 constexpr int kVtRow = kSplit / 2 + 4;      // LDS row (one dim) of V position
                                             // pairs in words, padded
-constexpr size_t kCounterAlign = 256;
-constexpr int kCombineChunk = 12;           // splits whose partials load together
+constexpr int kCombineChunk = 4;            // splits whose partials one merge lane loads together
+constexpr int kSyncLine = 64;               // uint32 words per 256-byte line of the sync area
+constexpr uint64_t kAttnSpin = 20000000ull; // 0.2 s of the 100 MHz realtime counter
 constexpr int kTargetGroups = 512;          // workgroups an attention launch aims for (swept: 512 best at batch 32)
 
-// Device-coherent (agent-scope) 8-byte store / load of two floats: visible to
-// workgroups on every XCD once the store has completed, without a fence.
-__device__ __forceinline__ void st_coherent2(float* p, float a, float b) {
-  const uint64_t v = static_cast<uint64_t>(__float_as_uint(a)) |
-                     (static_cast<uint64_t>(__float_as_uint(b)) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float2 ld_coherent2(const float* p) {
-  const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return make_float2(__uint_as_float(static_cast<uint32_t>(v)),
-                     __uint_as_float(static_cast<uint32_t>(v >> 32)));
-}
+// Device-coherent 8- and 16-byte access to the split partials through a
+// buffer resource: the sc1 cache policy (the bit agent-scope atomic loads and
+// stores carry on this GPU) sends each access to the coherent level, so a
+// store is visible to workgroups on every XCD once it has completed, without
+// a fence, and one 16-byte access replaces two 8-byte atomics (the merge is
+// bound by the number of coherent requests one CU issues).  Offsets are
+// bytes; the hardware range check drops accesses past num_bytes.
+constexpr int kCoherentPolicy = 16;  // sc1
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+struct CoherentBuf {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ CoherentBuf(const void* p, uint32_t num_bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, num_bytes, 0x00020000)) {}
+  __device__ float2 ld2(uint32_t off) const {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCoherentPolicy));
+  }
+  __device__ float4 ld4(uint32_t off) const {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoherentPolicy));
+  }
+  __device__ void st2(uint32_t off, float2 v) const {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, off, 0, kCoherentPolicy);
+  }
+  __device__ void st4(uint32_t off, float4 v) const {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, off, 0, kCoherentPolicy);
+  }
+};
 
 struct RopeSrc {
   const void* cos;
@@ -142,28 +158,40 @@ __device__ __forceinline__ uint32_t sel32(bool c, uint32_t a, uint32_t b) { retu
 //     the split holding position seqlen[b] builds the new K/V, uses them in
 //     place of what it read and stores them to the cache at the end.
 // One split: normalise and store.  Several: (acc, m, l) partials with
-// device-coherent stores; the last split of the (row, KV head) to take a
-// ticket merges them and resets the ticket.
+// device-coherent stores, a barrier among the splits of the (row, KV head)
+// (an arrival counter and a generation word, each on its own line of the
+// sync area: the last to arrive clears the counter and advances the
+// generation the others poll), then split s merges output items [s * ipw,
+// (s + 1) * ipw): every split reads a small slice of the partials instead of
+// one split reading them all.  The splits of a pair are consecutive in
+// dispatch order and far fewer than the GPU holds at once, so they are all
+// resident; the wait is bounded (about 0.2 s) and records a timeout in word 2
+// of the sync area instead of hanging.
 template <bool FUSED>
 __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     const uint16_t* __restrict__ src, int64_t ldq, const void* __restrict__ qn_w,
     const void* __restrict__ kn_w, int w_dt, RopeSrc rope, float eps,
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, int64_t cache_rows,
     int64_t max_len, const int64_t* __restrict__ seqlen, const int64_t* __restrict__ row_map,
-    int nq, int nkv, int64_t window, float scale, int max_splits, uint32_t* __restrict__ tickets,
+    int nq, int nkv, int64_t window, float scale, int max_splits, uint32_t* __restrict__ sync,
     float* __restrict__ part_acc, float* __restrict__ part_ml, uint16_t* __restrict__ out) {
   __shared__ __align__(16) uint16_t qs[kMaxGroup][kHeadDim];
   __shared__ __align__(16) uint32_t vt[kHeadDim][kVtRow];
   __shared__ __align__(16) uint16_t kvnew[2][kHeadDim];
   __shared__ float wm[4][kMaxGroup], wl[4][kMaxGroup];
   __shared__ float hm[kMaxGroup], hl[kMaxGroup], hr[kMaxGroup];
-  __shared__ int s_last;
   const int sp = blockIdx.x, kvh = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g = lane >> 4;
   const int group = nq / nkv;
+  // This pair's barrier words; the generation is read before this split can
+  // arrive, so it is the value the last arriver will advance.
+  uint32_t* const arrive = sync + kSyncLine * (1 + 2 * (b * nkv + kvh));
+  uint32_t* const gen = arrive + kSyncLine;
+  const uint32_t g0 = wv == 0 ? __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   const int64_t pos = clamp64(seqlen[b], 0, max_len - 1);
   const int64_t kv_len = pos + 1;
   const int64_t start = (window > 0 && kv_len > window) ? kv_len - window : 0;
@@ -363,6 +391,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       if (4 * g + i < group) ow[wv][4 * g + i][16 * nb + r16] = oacc[nb][i];
   __syncthreads();
   const int64_t pidx = (b * nkv + kvh) * max_splits + sp;
+  const int64_t n_part = static_cast<int64_t>(gridDim.z) * nkv * max_splits * kMaxGroup;
+  const CoherentBuf acc_buf(part_acc, static_cast<uint32_t>(n_part * kHeadDim * 4));
+  const CoherentBuf ml_buf(part_ml, static_cast<uint32_t>(n_part * 8));
   for (int item = tid; item < group * 16; item += kAttnThreads) {
     const int hh = item >> 4, dq = item & 15;
     float4 o = *reinterpret_cast<const float4*>(&ow[0][hh][4 * dq]);
@@ -381,64 +412,105 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       r.y = pack_bf16x2_rn(o.z * inv, o.w * inv);
       *reinterpret_cast<uint2*>(out + (b * nq + kvh * group + hh) * kHeadDim + 4 * dq) = r;
     } else {
-      float* pa2 = part_acc + (pidx * kMaxGroup + hh) * kHeadDim + 4 * dq;
-      st_coherent2(pa2, o.x, o.y);
-      st_coherent2(pa2 + 2, o.z, o.w);
+      acc_buf.st4(static_cast<uint32_t>(((pidx * kMaxGroup + hh) * kHeadDim + 4 * dq) * 4), o);
     }
   }
   if (n_spl == 1) return;
-  if (tid < group) st_coherent2(part_ml + (pidx * kMaxGroup + tid) * 2, hm[tid], hl[tid]);
-  // The partials were written with device-coherent stores; wait until they
-  // have all completed, then take a ticket.  (No device-scope fence: on this
-  // GPU that writes back the whole L2, which thousands of splits cannot
-  // afford.)
+  if (tid < group) ml_buf.st2(static_cast<uint32_t>((pidx * kMaxGroup + tid) * 8), make_float2(hm[tid], hl[tid]));
+  // Barrier among the n_spl splits of this (row, KV head), once this split's
+  // partials have completed (no device-scope fence: on this GPU that writes
+  // back the whole L2).
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  uint32_t* ticket = tickets + b * nkv + kvh;
-  if (tid == 0) s_last = atomicAdd(ticket, 1u) == static_cast<uint32_t>(n_spl - 1);
+  if (tid == 0) {
+    if (atomicAdd(arrive, 1u) == static_cast<uint32_t>(n_spl - 1)) {
+      __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gen, g0 + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      bool timed_out = false;
+      while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g0 && !timed_out) {
+        __builtin_amdgcn_s_sleep(1);
+        timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kAttnSpin;
+      }
+      if (timed_out) __hip_atomic_store(sync + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
   __syncthreads();
-  if (!s_last) return;
-  // Merge: one pass with a running max, kCombineChunk splits' loads at a time.
+  // Merge this split's slice.  Item (head, 4 dims) is shared by TPI adjacent
+  // lanes (the power of two >= n_spl, at most a wave); lane j folds splits j,
+  // j + TPI, ... (kCombineChunk per round, loads issued together) into a
+  // running (max, sum, acc) state, and the TPI states combine through lane
+  // exchanges in a fixed order.
   const int64_t p0 = (b * nkv + kvh) * max_splits;
-  for (int item = tid; item < group * 16; item += kAttnThreads) {
-    const int hh = item >> 4, dq = item & 15;
+  const int n_items = group * 16;
+  const int ipw = (n_items + n_spl - 1) / n_spl;
+  const int it_lo = sp * ipw, it_hi = it_lo + ipw < n_items ? it_lo + ipw : n_items;
+  int tpi = 1;
+  while (tpi < n_spl && tpi < 64) tpi *= 2;
+  for (int ib = it_lo; ib < it_hi; ib += kAttnThreads / tpi) {
+    const int item = ib + tid / tpi, j = tid % tpi;
+    const bool live = item < it_hi;
+    const int hh = live ? item >> 4 : 0, dq = item & 15;
     float mx = -INFINITY, den = 0.f, n0 = 0.f, n1 = 0.f, n2 = 0.f, n3 = 0.f;
-    for (int s0 = 0; s0 < n_spl; s0 += kCombineChunk) {
-      float2 ml[kCombineChunk], a01[kCombineChunk], a23[kCombineChunk];
+    for (int s0 = 0; s0 < n_spl; s0 += kCombineChunk * tpi) {  // uniform over the wave
+      float2 ml[kCombineChunk];
+      float4 ac[kCombineChunk];
 #pragma unroll
-      for (int u = 0; u < kCombineChunk; ++u) {
-        const int s = s0 + u < n_spl ? s0 + u : n_spl - 1;
-        const int64_t q = (p0 + s) * kMaxGroup + hh;
-        ml[u] = ld_coherent2(part_ml + q * 2);
-        a01[u] = ld_coherent2(part_acc + q * kHeadDim + 4 * dq);
-        a23[u] = ld_coherent2(part_acc + q * kHeadDim + 4 * dq + 2);
+      for (int u = 0; u < kCombineChunk; ++u) {  // absent splits load nothing
+        const int s = s0 + u * tpi + j;
+        ml[u] = make_float2(-INFINITY, 0.f);
+        ac[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (s < n_spl) {
+          const uint32_t q = static_cast<uint32_t>((p0 + s) * kMaxGroup + hh);
+          ml[u] = ml_buf.ld2(q * 8);
+          ac[u] = acc_buf.ld4((q * kHeadDim + 4 * dq) * 4);
+        }
       }
       MA_ISSUE_FENCE();
 #pragma unroll
-      for (int u = 0; u < kCombineChunk; ++u) {  // no early exit: arrays stay in registers
-        const bool ok = s0 + u < n_spl;  // u = 0 always is, so mx is finite after it
-        const float m = ok ? ml[u].x : -INFINITY;
-        const float mn = fmaxf(mx, m);
-        const float r = expf(mx - mn), w = ok ? expf(m - mn) : 0.f;
-        den = den * r + w * ml[u].y;
-        n0 = n0 * r + w * a01[u].x;
-        n1 = n1 * r + w * a01[u].y;
-        n2 = n2 * r + w * a23[u].x;
-        n3 = n3 * r + w * a23[u].y;
-        mx = mn;
+      for (int u = 0; u < kCombineChunk; ++u) {
+        if (s0 + u * tpi < n_spl) {  // uniform: some lane of every item has this split
+          const bool ok = s0 + u * tpi + j < n_spl;
+          const float m = ok ? ml[u].x : -INFINITY;
+          const float mn = fmaxf(mx, m);
+          const float r = mx == -INFINITY ? 0.f : expf(mx - mn);
+          const float w = ok ? expf(m - mn) : 0.f;
+          den = den * r + w * ml[u].y;
+          n0 = n0 * r + w * ac[u].x;
+          n1 = n1 * r + w * ac[u].y;
+          n2 = n2 * r + w * ac[u].z;
+          n3 = n3 * r + w * ac[u].w;
+          mx = mn;
+        }
       }
     }
-    uint2 r;
-    r.x = pack_bf16x2_rn(n0 / den, n1 / den);
-    r.y = pack_bf16x2_rn(n2 / den, n3 / den);
-    *reinterpret_cast<uint2*>(out + (b * nq + kvh * group + hh) * kHeadDim + 4 * dq) = r;
+    for (int off = 1; off < tpi; off <<= 1) {  // lanes without splits hold mx = -inf
+      const float mo = __shfl_xor(mx, off, 64), dn = __shfl_xor(den, off, 64);
+      const float o0 = __shfl_xor(n0, off, 64), o1 = __shfl_xor(n1, off, 64);
+      const float o2 = __shfl_xor(n2, off, 64), o3 = __shfl_xor(n3, off, 64);
+      const float mn = fmaxf(mx, mo);
+      const float r = mx == -INFINITY ? 0.f : expf(mx - mn);
+      const float ro = mo == -INFINITY ? 0.f : expf(mo - mn);
+      den = den * r + dn * ro;
+      n0 = n0 * r + o0 * ro;
+      n1 = n1 * r + o1 * ro;
+      n2 = n2 * r + o2 * ro;
+      n3 = n3 * r + o3 * ro;
+      mx = mn;
+    }
+    if (live && j == 0) {
+      uint2 r;
+      r.x = pack_bf16x2_rn(n0 / den, n1 / den);
+      r.y = pack_bf16x2_rn(n2 / den, n3 / den);
+      *reinterpret_cast<uint2*>(out + (b * nq + kvh * group + hh) * kHeadDim + 4 * dq) = r;
+    }
   }
-  if (tid == 0) atomicExch(ticket, 0u);
 }
 
-size_t ticket_bytes(int64_t batch, int nkv) {
-  const size_t n = static_cast<size_t>(batch) * nkv * sizeof(uint32_t);
-  return (n + kCounterAlign - 1) / kCounterAlign * kCounterAlign;
+// Sync area: line 0 (word 2: timeout), then per (row, KV head) an arrival
+// counter line and a generation line.
+size_t sync_bytes(int64_t batch, int nkv) {
+  return (1 + 2 * static_cast<size_t>(batch) * nkv) * kSyncLine * sizeof(uint32_t);
 }
 
 int64_t max_splits_for(int64_t max_len) { return cdiv(max_len, kSplit); }
@@ -504,7 +576,7 @@ extern "C" int ma_qk_norm_rope_store(const void* qkv, int64_t ldq, int64_t batch
 extern "C" size_t ma_gqa_workspace_bytes(int64_t batch, int n_kv_heads, int64_t max_len) {
   if (batch < 0 || n_kv_heads < 1 || max_len < 1) return 0;
   const size_t parts = static_cast<size_t>(batch) * n_kv_heads * max_splits_for(max_len) * kMaxGroup;
-  return ticket_bytes(batch, n_kv_heads) + parts * (kHeadDim + 2) * sizeof(float);
+  return sync_bytes(batch, n_kv_heads) + parts * (kHeadDim + 2) * sizeof(float);
 }
 
 // Shared launch of k_decode_attn for the two entry points below.
@@ -520,19 +592,21 @@ static int launch_attn(bool fused, const void* src, int64_t ldq, const void* qn_
       (!fused && !aligned16(src)))
     return fail(MA_EVALUE, "%s: buffers must be 16-byte aligned", what);
   const int64_t max_splits = max_splits_for(max_len);
+  if (batch * nkv * max_splits * kMaxGroup * kHeadDim * 4 >= (int64_t{1} << 32))
+    return fail(MA_EVALUE, "%s: batch x kv heads x max_len too large for one launch", what);
   const int64_t span = window > 0 && window < max_len ? window : max_len;
   const int64_t pairs = batch * nkv;
   int64_t grid_splits = cdiv(kTargetGroups, pairs);
   if (grid_splits > cdiv(span, kSplit)) grid_splits = cdiv(span, kSplit);
-  auto* tickets = static_cast<uint32_t*>(workspace);
-  float* acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + ticket_bytes(batch, nkv));
+  auto* sync = static_cast<uint32_t*>(workspace);
+  float* acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + sync_bytes(batch, nkv));
   float* ml = acc + static_cast<size_t>(batch) * nkv * max_splits * kMaxGroup * kHeadDim;
   dim3 grid(static_cast<unsigned>(grid_splits), static_cast<unsigned>(nkv),
             static_cast<unsigned>(batch));
 #define MA_ATTN_ARGS                                                                            \
   static_cast<const uint16_t*>(src), ldq, qn_w, kn_w, w_dt, rope, eps,                          \
       static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), cache_rows, max_len,    \
-      seqlen, row_map, nq, nkv, window, scale, static_cast<int>(max_splits), tickets, acc, ml, \
+      seqlen, row_map, nq, nkv, window, scale, static_cast<int>(max_splits), sync, acc, ml,   \
       static_cast<uint16_t*>(out)
   if (fused)
     hipLaunchKernelGGL(k_decode_attn<true>, grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);

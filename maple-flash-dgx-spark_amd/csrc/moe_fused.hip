@@ -165,13 +165,35 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   {
     // thread t owns words t, t + 256, ... (16 values each)
     constexpr int WPT = (NWH + 255) / 256;
-    float v[WPT][16];
+    float v[WPT][16], nw[WPT][16];
     uint4 gr[WPT][2];
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
       const int w = tid + 256 * i;
       const int wc = w < NWH ? w : NWH - 1;
+      if (xb) {  // the norm weights, loaded with x
+        if (norm_dt == MA_F32) {
+          const float4* np = reinterpret_cast<const float4*>(static_cast<const float*>(norm_w) + wc * 16);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float4 f = np[q];
+            nw[i][4 * q] = f.x;
+            nw[i][4 * q + 1] = f.y;
+            nw[i][4 * q + 2] = f.z;
+            nw[i][4 * q + 3] = f.w;
+          }
+        } else {
+          const uint4* np = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(norm_w) + wc * 16);
+          const uint4 n0 = np[0], n1 = np[1];
+          const uint32_t u[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            nw[i][2 * q] = __uint_as_float(u[q] << 16);
+            nw[i][2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
+          }
+        }
+      }
       const uint4* gp = reinterpret_cast<const uint4*>(gate_w + static_cast<int64_t>(router_wg ? wg : 0) * H + wc * 16);
       gr[i][0] = gp[0];
       gr[i][1] = gp[1];
@@ -205,11 +227,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
       const float rstd = rsqrtf((red[0] + red[1] + red[2] + red[3]) / static_cast<float>(H) + eps);
 #pragma unroll
       for (int i = 0; i < WPT; ++i) {
-        const int w = tid + 256 * i;
-        const int wc = w < NWH ? w : NWH - 1;
 #pragma unroll
-        for (int q = 0; q < 16; ++q)
-          v[i][q] = bf16_to_f32(f32_to_bf16(v[i][q] * rstd * ld_f(norm_w, norm_dt, wc * 16 + q)));
+        for (int q = 0; q < 16; ++q) v[i][q] = bf16_to_f32(f32_to_bf16(v[i][q] * rstd * nw[i][q]));
       }
     }
 #pragma unroll
@@ -532,8 +551,9 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
   if (!workspace || workspace_bytes < ws_bytes(n_experts, s->grid, inter, top_k))
     return fail(MA_EVALUE, "moe_fused: workspace too small");
   auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  if (!a16(x) || (x_add && !a16(x_add)) || !a16(gate_weight) || !a16(up_gate) || !a16(workspace))
-    return fail(MA_EVALUE, "moe_fused: x, x_add, weights and workspace must be 16-byte aligned");
+  if (!a16(x) || (x_add && (!a16(x_add) || !a16(norm_weight))) || !a16(gate_weight) ||
+      !a16(up_gate) || !a16(workspace))
+    return fail(MA_EVALUE, "moe_fused: x, x_add, norm weight, weights and workspace must be 16-byte aligned");
   const int per = n_experts <= 64 ? 1 : 4;
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define MA_FUSED_ARGS                                                                            \

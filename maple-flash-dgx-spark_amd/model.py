@@ -88,7 +88,7 @@ def rope_tables(max_len: int, rotary_dim: int, theta: float, device):
 class KVCache:
     """Preallocated bf16 K/V per layer ``[B, n_kv, max_len, D]``, one write
     position per row (``model.py:116-143``) and the attention workspace
-    (zeroed once; the kernels leave its tickets zero)."""
+    (zeroed once; the kernels leave its barrier counters zero)."""
 
     k: list
     v: list

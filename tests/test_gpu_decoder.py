@@ -87,7 +87,8 @@ def test_gqa_ragged_vs_oracle(dev, window):
 def test_fused_attention_equals_two_step(dev, window):
     """decode_attention gives the bits of apply_qkv_decode + decode_gqa_attn
     (q, the written K/V and the output), for ragged rows through a row map,
-    and leaves the workspace tickets at zero."""
+    leaves the per-(row, KV head) arrival counters of the split barrier at zero
+    and records no timed-out wait."""
     nq, nkv, d, max_len, rot = 32, 4, 64, 1100, 32
     seqlen = torch.tensor([0, 127, 128, 700, 1099], device=dev)
     row_map = torch.tensor([3, 5, 0, 1, 4], device=dev)
@@ -110,7 +111,9 @@ def test_fused_attention_equals_two_step(dev, window):
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
         assert torch.equal(kc2, kc) and torch.equal(vc2, vc)
-        assert int(ws[:5 * nkv * 4].count_nonzero()) == 0, "tickets not reset"
+        sync = ws[:256 * (1 + 2 * 5 * nkv)].view(torch.int32)
+        assert int(sync[2]) == 0, "a split barrier wait timed out"
+        assert int(sync[64::128][:5 * nkv].count_nonzero()) == 0, "arrival counters not reset"
     # and the output matches the oracle on the written cache
     for b, n in enumerate((seqlen + 1).tolist()):
         r = int(row_map[b])
