@@ -225,11 +225,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     for (int i = 0; i < 4; ++i) vr[i] = vp[i];
   };
   uint4 kf[2][2], vr[4];
-  load_chunk(c_beg, kf, vr);
-
   uint16_t new_kv = 0;  // FUSED owner split: the new K (wave 0) or V (wave 1) element
   if constexpr (FUSED) {
-    // Every load of the prologue is issued before any of them is used.
+    // Every load of the prologue is issued before any of them is used, and
+    // before the first chunk's (memory counters complete in issue order, so
+    // q would otherwise wait for the K/V chunk).
     const uint16_t* row = src + b * ldq;
     uint16_t xq[kMaxGroup / 4];
 #pragma unroll
@@ -242,6 +242,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     const float wq = ld_f(qn_w, w_dt, lane);
     const float wk = ld_f(kn_w, w_dt, lane);
     const float2 cs = rope_coeffs(rope, b, pos);
+    load_chunk(c_beg, kf, vr);
 #pragma unroll
     for (int i = 0; i < kMaxGroup / 4; ++i) {
       const int hh = wv + 4 * i;
@@ -256,9 +257,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     }
   } else {
     const uint16_t* qsrc = src + (b * nq + kvh * group) * kHeadDim;
-    for (int i = tid; i < kMaxGroup * kHeadDim; i += kAttnThreads) {
-      const int hh = i / kHeadDim;
-      qs[hh][i % kHeadDim] = hh < group ? qsrc[i] : uint16_t(0);
+    uint16_t xq[kMaxGroup * kHeadDim / kAttnThreads];
+#pragma unroll
+    for (int k = 0; k < kMaxGroup * kHeadDim / kAttnThreads; ++k) {
+      const int i = tid + kAttnThreads * k;
+      xq[k] = i / kHeadDim < group ? qsrc[i] : uint16_t(0);
+    }
+    load_chunk(c_beg, kf, vr);
+#pragma unroll
+    for (int k = 0; k < kMaxGroup * kHeadDim / kAttnThreads; ++k) {
+      const int i = tid + kAttnThreads * k;
+      qs[i / kHeadDim][i % kHeadDim] = xq[k];
     }
   }
   if (tid < kMaxGroup) {
