@@ -211,6 +211,13 @@ int ma_moe_grouped(const void* x, int64_t ldx, int64_t tokens, int64_t top_k,
  * src/maple_run/model.py:448-474 (router_topk, ternary_expert_swiglu,
  * ternary_expert_gemv, moe_reduce_add: four launches there), optionally with
  * add_rms_norm, src/maple_run/kernels/fused_norm.py:128-161.
+ * With next_w != NULL the same launch also computes the next layer's input
+ * projection from y: next_out bf16 [next_rows] = ternary_gemv(y, next_w
+ * [next_rows, hidden/16], next_alpha (f32/bf16), rms_weight = next_rms
+ * float32 [hidden], next_eps) -- the bits ma_ternary_gemv gives (reference
+ * src/maple_run/kernels/ternary_gemv.py:110-146, the QKV projection of
+ * MapleAttention, model.py:368-414); y, next_w and next_rms 16-byte aligned,
+ * next_rows <= 4096 at hidden 2048.
  */
 size_t ma_moe_fused_workspace_bytes(int64_t n_experts, int64_t hidden, int64_t inter,
                                     int64_t top_k);
@@ -219,7 +226,10 @@ int ma_moe_fused(const void* x, const void* x_add, const void* norm_weight, int 
                  const float* router_bias, int64_t n_experts, int64_t hidden, int64_t inter,
                  int64_t top_k, const uint32_t* up_gate, const void* up_gate_alpha,
                  const uint32_t* down, const void* down_alpha, void* y, int32_t* topk_ids,
-                 float* topk_weight, void* workspace, size_t workspace_bytes, void* stream);
+                 float* topk_weight, void* workspace, size_t workspace_bytes,
+                 const uint32_t* next_w, const void* next_alpha, int next_alpha_dtype,
+                 const float* next_rms, float next_eps, int64_t next_rows, void* next_out,
+                 void* stream);
 /* *out = 1 if any ma_moe_fused call on this workspace timed out waiting
  * (synchronises the stream).  No reference counterpart: the reference has no
  * cross-workgroup wait. */

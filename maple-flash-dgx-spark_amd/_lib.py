@@ -49,7 +49,7 @@ _SIGNATURES = {
                              _P, _P, _P, _P, _L, _L, _L, _F, _P, _P, _Z, _P],
     "ma_moe_fused_workspace_bytes": [_L, _L, _L, _L],
     "ma_moe_fused": [_P, _P, _P, _I, _F, _P, _P, _P, _L, _L, _L, _L, _P, _P, _P, _P, _P, _P, _P, _P,
-                     _Z, _P],
+                     _Z, _P, _P, _I, _P, _F, _L, _P, _P],
     "ma_moe_fused_timed_out": [_P, _P, _P],
     "ma_argmax_rows": [_P, _I, _L, _L, _L, _P, _P],
     "ma_moe_grouped": [_P, _L, _L, _L, _P, _P, _P, _P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _I,

@@ -27,6 +27,7 @@
 // Every wait is bounded (about 0.2 s); on timeout the workspace error word is
 // set and the kernel finishes with wrong values instead of hanging.
 #include "ternary_engine.h"
+#include "tgemv_fast.h"
 #include "topk.h"
 
 namespace ma {
@@ -41,16 +42,19 @@ constexpr int kLine = 64;       // uint32 words in a 256-byte line
 // a line of its own so that arrivals and polls on different ones do not meet):
 //   line 0, word 2     error (1 = a wait timed out)
 //   lines 1 .. 16, 17  h barrier: sub-counters, top counter
-//   lines 18 .. 33     release flags, all holding the number of calls made
-//                      on this workspace
+//   lines 18 .. 33     release flags, all holding the number of barriers
+//                      passed on this workspace
+//   lines 34 .. 49, 50 y barrier (calls with a next projection): sub-counters,
+//                      top counter
 //   [16 KB, 48 KB)     router logits: one tagged 64-bit word (tag << 32 |
 //                      float bits) per expert every 128 bytes, E <= 256
 //   [48 KB ...)        h, bf16 [TK * I]
 constexpr int kSubB = 1, kTopB = kSubB + kBarGroups, kFlags = kTopB + 1;
+constexpr int kSubC = kFlags + kBarGroups, kTopC = kSubC + kBarGroups;
 constexpr size_t kLogitOff = 16384;
 constexpr int kLogitStride = 16;  // uint64 words between logits
 constexpr size_t kMoeWsHeader = 49152;
-static_assert(kFlags + kBarGroups <= static_cast<int>(kLogitOff / 256), "workspace lines");
+static_assert(kTopC < static_cast<int>(kLogitOff / 256), "workspace lines");
 static_assert(kLogitOff + 256 * kLogitStride * 8 <= kMoeWsHeader, "workspace logits");
 
 __device__ __forceinline__ uint32_t ld_coh32(const uint32_t* p) {
@@ -115,7 +119,9 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     const uint32_t* __restrict__ ug, const uint16_t* __restrict__ ug_alpha,
     const uint32_t* __restrict__ dn, const uint16_t* __restrict__ dn_alpha,
     uint16_t* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ wts_out,
-    uint32_t* __restrict__ ws) {
+    uint32_t* __restrict__ ws, const uint32_t* __restrict__ nx_w, const void* __restrict__ nx_alpha,
+    int nx_alpha_dt, const float* __restrict__ nx_rms, float nx_eps, int nx_rows,
+    uint16_t* __restrict__ nx_out) {
   constexpr int NWH = KWH * LPRH, H = 16 * NWH;
   constexpr int NWI = KWI * LPRI, I = 16 * NWI;
   constexpr int RPIH = 64 / LPRH, PPI = RPIH / 2;      // SwiGLU: up/gate pairs per wave pass
@@ -135,6 +141,13 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   __shared__ float s_wts[kFusedWaves][TK];
   __shared__ float red[kFusedWaves], red2[kFusedWaves];
   __shared__ float part[kFusedWaves][RPB];
+  // next projection: y, and its RMS-folded x' pairs (hi and lo words, and the
+  // value each pair carries) for every word of y, laid out so that the LPRH
+  // lanes sharing a row read consecutive entries: word w = LPRH-lane l's
+  // KWH-th word i sits at column i * LPRH + l
+  __shared__ __align__(16) uint4 ys4[KWH * 2][LPRH];  // 8 bf16 of y per entry
+  __shared__ __align__(16) uint32_t pxh[8][NWH], pxl[8][NWH];
+  __shared__ __align__(16) float prr[8][NWH];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -404,6 +417,23 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
       ad[q][u] = bf16_to_f32(dn_alpha[e * H + r]);
     }
   }
+  // Next projection (optional): this workgroup's rows, issued after the
+  // expert loads so that waiting for those never waits for these.  Lanes
+  // split a row as the standalone GEMV does (LPRH lanes of KWH words), RPIH
+  // rows per wave pass, NXP passes.
+  constexpr int NXP = 2;
+  const int nx_rq = nx_w ? (nx_rows + G - 1) / G : 0;
+  uint32_t nxw[NXP][KWH];
+  float nxa[NXP];
+  if (nx_w) {
+#pragma unroll
+    for (int p = 0; p < NXP; ++p) {
+      int r = wg * nx_rq + p * kFusedWaves * RPIH + wv * RPIH + subh;
+      r = r < nx_rows ? r : nx_rows - 1;
+      load_words_v<KWH>(nx_w + static_cast<int64_t>(r) * NWH + klh * KWH, nxw[p]);
+      nxa[p] = ld_f(nx_alpha, nx_alpha_dt, r);
+    }
+  }
   MA_ISSUE_FENCE();
 
   // SwiGLU outputs of this wave
@@ -488,7 +518,115 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
                  : residual ? __uint_as_float(ra << 16) : 0.f;
 #pragma unroll
     for (int ww = 0; ww < kFusedWaves; ++ww) v += part[ww][tid];
-    y[ro] = f32_to_bf16(v);
+    if (nx_w)
+      st_coh16(&y[ro], f32_to_bf16(v));  // read back by every workgroup below
+    else
+      y[ro] = f32_to_bf16(v);
+  }
+
+  // ---- 5. next projection (optional): nx_out = ternary_gemv(y, nx_w, nx_alpha,
+  // rms_weight = nx_rms) -- reference kernels/ternary_gemv.py:110-146 -- once
+  // every workgroup's rows of y are out, with the standalone fast GEMV's
+  // per-lane arithmetic in the same order (so the same bits).
+  if (nx_w) {
+    __builtin_amdgcn_s_waitcnt(0);  // this workgroup's y stores have completed
+    __syncthreads();
+    if (wv == 0)
+      timed_out = grid_barrier(ws + kLine * kSubC, ws + kLine * kTopC, flags, f0 + 1u, G, wg, lane, t0) ||
+                  timed_out;
+    __syncthreads();  // every wave waits for the barrier before reading y
+    {  // y (device-coherent) into LDS, and its x' pairs: thread t builds pairs
+       // j0 .. j0 + 3 of word t / 2 (j0 = 4 (t & 1)), each from values j and
+       // j + 8 of the word times their RMS weights
+      constexpr int PIT = (NWH * 2 + 255) / 256;
+      uint64_t y0[PIT], y1[PIT], ya[PIT], yb[PIT], wa[PIT][2], wb[PIT][2];
+#pragma unroll
+      for (int k = 0; k < PIT; ++k) {
+        const int t = tid + 256 * k < NWH * 2 ? tid + 256 * k : NWH * 2 - 1;
+        const int w = t >> 1, j0 = 4 * (t & 1);
+        const uint64_t* yp = reinterpret_cast<const uint64_t*>(y + w * 16 + 8 * (t & 1));
+        y0[k] = ld_coh64(yp);  // values 8 (t & 1) .. + 8 of word w, raw
+        y1[k] = ld_coh64(yp + 1);
+        ya[k] = ld_coh64(reinterpret_cast<const uint64_t*>(y + w * 16 + j0));
+        yb[k] = ld_coh64(reinterpret_cast<const uint64_t*>(y + w * 16 + j0 + 8));
+        wa[k][0] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0)[0];
+        wa[k][1] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0)[1];
+        wb[k][0] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0 + 8)[0];
+        wb[k][1] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0 + 8)[1];
+      }
+#pragma unroll
+      for (int k = 0; k < PIT; ++k) {
+        const int t = tid + 256 * k;
+        if (t < NWH * 2) {
+          const int w = t >> 1, j0 = 4 * (t & 1);
+          const int col = (w % KWH) * LPRH + w / KWH;
+          ys4[(w % KWH) * 2 + (t & 1)][w / KWH] =
+              make_uint4(static_cast<uint32_t>(y0[k]), static_cast<uint32_t>(y0[k] >> 32),
+                         static_cast<uint32_t>(y1[k]), static_cast<uint32_t>(y1[k] >> 32));
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int j = j0 + jj;
+            const uint32_t ua = static_cast<uint32_t>(ya[k] >> (16 * jj)) & 0xffffu;
+            const uint32_t ub = static_cast<uint32_t>(yb[k] >> (16 * jj)) & 0xffffu;
+            const float ra_w = __uint_as_float(static_cast<uint32_t>(wa[k][jj >> 1] >> (32 * (jj & 1))));
+            const float rb_w = __uint_as_float(static_cast<uint32_t>(wb[k][jj >> 1] >> (32 * (jj & 1))));
+            const float xa = __uint_as_float(ua << 16) * ra_w, xb2 = __uint_as_float(ub << 16) * rb_w;
+            const float f = pair_scale(j);
+            uint16_t ha, la, hb, lb;
+            const float r0 = split_hi_lo(f * xa, ha, la);
+            const float r1 = split_hi_lo(f * xb2, hb, lb);
+            pxh[j][col] = static_cast<uint32_t>(ha) | (static_cast<uint32_t>(hb) << 16);
+            pxl[j][col] = static_cast<uint32_t>(la) | (static_cast<uint32_t>(lb) << 16);
+            prr[j][col] = r0 + r1;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    // This lane's slice, in the standalone GEMV's order: sum of squares of
+    // the raw values, then the pairs' correction term.
+    uint32_t xh[KWH][8], xl[KWH][8];
+    float c = 0.f, ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < KWH; ++i) {
+      const uint4 a0 = ys4[i * 2][klh];
+      const uint4 a1 = ys4[i * 2 + 1][klh];
+      const uint32_t u[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float v0 = __uint_as_float(u[q] << 16), v1 = __uint_as_float(u[q] & 0xffff0000u);
+        ss += v0 * v0;
+        ss += v1 * v1;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        xh[i][j] = pxh[j][i * LPRH + klh];
+        xl[i][j] = pxl[j][i * LPRH + klh];
+        const float f = pair_scale(j);
+        c += ((f + 1.0f) / f) * prr[j][i * LPRH + klh];
+      }
+    }
+    ss = group_sum<LPRH>(ss);
+    const float rstd = rsqrtf(ss / static_cast<float>(NWH * 16) + nx_eps);
+    const ExpandConsts kc;
+#pragma unroll
+    for (int p = 0; p < NXP; ++p) {
+      float acc[2] = {0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < KWH; ++i) {
+        uint32_t e[8];
+        expand_word(nxw[p][i], e, kc);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          acc[j & 1] = dot2(e[j], xh[i][j], acc[j & 1]);
+          acc[j & 1] = dot2(e[j], xl[i][j], acc[j & 1]);
+        }
+      }
+      const float d = group_sum<LPRH>(((acc[0] + acc[1]) - c) * (nxa[p] * rstd));
+      const int rl = p * kFusedWaves * RPIH + wv * RPIH + subh;
+      const int r = wg * nx_rq + rl;
+      if (klh == 0 && rl < nx_rq && r < nx_rows) nx_out[r] = f32_to_bf16(d);
+    }
   }
   if (__ballot(timed_out) && lane == 0) st_coh32(&ws[2], 1u);
 }
@@ -537,7 +675,9 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
                             const uint32_t* up_gate, const void* up_gate_alpha,
                             const uint32_t* down, const void* down_alpha, void* y,
                             int32_t* topk_ids, float* topk_weight, void* workspace,
-                            size_t workspace_bytes, void* stream) {
+                            size_t workspace_bytes, const uint32_t* next_w,
+                            const void* next_alpha, int next_alpha_dtype, const float* next_rms,
+                            float next_eps, int64_t next_rows, void* next_out, void* stream) {
   const FusedShape* s = find_shape(hidden, inter, top_k);
   if (!s)
     return fail(MA_EVALUE, "moe_fused: shape (hidden %lld, inter %lld, top_k %lld) not built",
@@ -554,6 +694,16 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
   if (!a16(x) || (x_add && (!a16(x_add) || !a16(norm_weight))) || !a16(gate_weight) ||
       !a16(up_gate) || !a16(workspace))
     return fail(MA_EVALUE, "moe_fused: x, x_add, norm weight, weights and workspace must be 16-byte aligned");
+  if (next_w) {
+    const int64_t max_rows = static_cast<int64_t>(s->grid) * 2 * 4 * (hidden == 2048 ? 2 : 4);
+    if (!next_alpha || !next_rms || !next_out || next_rows < 1 || next_rows > max_rows)
+      return fail(MA_EVALUE, "moe_fused: next projection needs alpha, rms weight, output and 1..%lld rows",
+                  static_cast<long long>(max_rows));
+    if (next_alpha_dtype != MA_F32 && next_alpha_dtype != MA_BF16)
+      return fail(MA_ETYPE, "moe_fused: next projection alpha dtype %d", next_alpha_dtype);
+    if (!a16(next_w) || !a16(next_rms) || !a16(y))
+      return fail(MA_EVALUE, "moe_fused: next projection weights, rms weight and y must be 16-byte aligned");
+  }
   const int per = n_experts <= 64 ? 1 : 4;
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define MA_FUSED_ARGS                                                                            \
@@ -561,7 +711,9 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
       eps, static_cast<const uint16_t*>(residual), static_cast<const uint16_t*>(gate_weight),    \
       router_bias, static_cast<int>(n_experts), up_gate,                                         \
       static_cast<const uint16_t*>(up_gate_alpha), down, static_cast<const uint16_t*>(down_alpha), \
-      static_cast<uint16_t*>(y), topk_ids, topk_weight, static_cast<uint32_t*>(workspace)
+      static_cast<uint16_t*>(y), topk_ids, topk_weight, static_cast<uint32_t*>(workspace),       \
+      next_w, next_alpha, next_alpha_dtype, next_rms, next_eps, static_cast<int>(next_rows),      \
+      static_cast<uint16_t*>(next_out)
   if (hidden == 2048) {
     if (per == 1)
       hipLaunchKernelGGL((k_moe_fused<4, 32, 6, 3, 16, 2, 8, 1>), dim3(s->grid), dim3(256), 0, st, MA_FUSED_ARGS);

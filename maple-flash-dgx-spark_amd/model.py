@@ -11,7 +11,9 @@ One decode step, per layer:
   hidden = moe_block(mlp_in, residual=hidden)
   (at batch 1, when the one-launch MoE kernel is built for the shape and
   fused_moe is left True, the last two lines are one launch:
-  moe_fused(hidden, add=o, norm_weight=post_ln))
+  moe_fused(hidden, add=o, norm_weight=post_ln), which in forward() also
+  computes the next layer's qkv line from its output, so only layer 0 runs
+  the standalone QKV projection)
 then seqlen += 1, final rms_norm, RTN4 lm_head, greedy argmax.
 
 Weights are random with the synthetic distributions (``synthetic.py``): every
@@ -136,31 +138,52 @@ class SyntheticDecoder:
         ws = gqa_workspace(batch, c.kv_heads, self.max_len, self.device)
         return KVCache(ks, vs, seqlen, self.max_len, ws)
 
-    def layer_step(self, i: int, hidden: torch.Tensor, cache: KVCache, routing=None) -> torch.Tensor:
+    def _layer(self, i: int, hidden: torch.Tensor, cache: KVCache, routing=None,
+               qkv: torch.Tensor | None = None, fuse_next: bool = True):
+        """Layer ``i``; returns ``(y, next_qkv)``.  ``qkv``: this layer's input
+        projection if an earlier launch already computed it.  ``next_qkv`` is
+        layer ``i + 1``'s projection when the one-launch MoE kernel computed it
+        from ``y`` (batch 1, ``fuse_next``), else None."""
         c, L = self.cfg, self.layers[i]
         bsz = hidden.shape[0]
-        qkv = ternary_gemv(hidden, L.qkv, L.qkv_alpha, rms_weight=L.input_ln, rms_eps=c.eps)
+        if qkv is None:
+            qkv = ternary_gemv(hidden, L.qkv, L.qkv_alpha, rms_weight=L.input_ln, rms_eps=c.eps)
         attn = decode_attention(qkv, L.q_norm, L.k_norm, self.cos, self.sin, cache.k[i], cache.v[i],
                                 cache.seqlen, cache.attn_ws, num_heads=c.heads,
                                 num_kv_heads=c.kv_heads, head_dim=c.head_dim,
                                 rotary_dim=c.rotary_dim, eps=c.eps, scale=c.head_dim ** -0.5)
         o = ternary_gemv(attn.reshape(bsz, -1), L.o, L.o_alpha)
+        next_qkv = None
         if bsz == 1 and self.fused_moe and fused_supported(L.moe, c.top_k, hidden):
-            # add + RMSNorm + router + experts + combine in one launch
-            y, ids, _ = moe_fused(hidden, L.moe, c.top_k, add=o, norm_weight=L.post_ln, eps=c.eps)
+            # add + RMSNorm + router + experts + combine (+ the next layer's
+            # RMS-folded QKV projection) in one launch
+            nl = None
+            if fuse_next and i + 1 < c.layers:
+                n = self.layers[i + 1]
+                nl = (n.qkv, n.qkv_alpha, n.input_ln, c.eps)
+            out = moe_fused(hidden, L.moe, c.top_k, add=o, norm_weight=L.post_ln, eps=c.eps,
+                            next_linear=nl)
+            y, ids = out[0], out[1]
+            if nl is not None:
+                next_qkv = out[3]
         else:
             hidden, mlp_in = add_rms_norm(hidden, o, L.post_ln, c.eps)
             y, ids, _ = moe_block(mlp_in, L.moe, c.top_k, residual=hidden)
         if routing is not None:
             routing.append(ids)
-        return y
+        return y, next_qkv
+
+    def layer_step(self, i: int, hidden: torch.Tensor, cache: KVCache, routing=None) -> torch.Tensor:
+        """Layer ``i`` on its own (its QKV projection computed here)."""
+        return self._layer(i, hidden, cache, routing, fuse_next=False)[0]
 
     def forward(self, input_ids: torch.Tensor, cache: KVCache, routing: list | None = None) -> torch.Tensor:
         """One decode step for ``input_ids [B]``; returns bf16 logits ``[B, vocab]``.
         ``routing``, if a list, receives each layer's expert ids."""
         hidden = self.embed_tokens(input_ids)
+        qkv = None
         for i in range(self.cfg.layers):
-            hidden = self.layer_step(i, hidden, cache, routing)
+            hidden, qkv = self._layer(i, hidden, cache, routing, qkv)
         cache.seqlen.add_(1)
         return self.head(hidden)
 

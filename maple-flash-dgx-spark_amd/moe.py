@@ -73,7 +73,7 @@ def moe_fused_timed_out(device: torch.device | int = 0) -> bool:
 
 def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tensor | None = None,
               *, add: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None,
-              eps: float = 1e-6):
+              eps: float = 1e-6, next_linear: tuple | None = None):
     """One token through the whole MoE layer in one launch.
 
     Plain: ``y = x_res + sum_j w_j down_j(swiglu_j(x))`` with ``x_res =
@@ -81,6 +81,11 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
     post-attention add + RMSNorm, ``fused_norm.py:128-161``): ``s = x + add``,
     the block runs on ``rms_norm(s) * norm_weight`` and adds ``bf16(s)``.
     Returns ``(y [1, H], ids int32 [1, k], weights float32 [1, k])``.
+
+    ``next_linear = (packed [N, H/16] uint32, alpha [N], rms_weight float32
+    [H], rms_eps)``: the same launch also computes the next layer's input
+    projection ``ternary_gemv(y, packed, alpha, rms_weight=..., rms_eps=...)``
+    (the same bits) and returns it as a fourth output ``[1, N]``.
     """
     hidden = x.shape[-1]
     xf = x.reshape(1, hidden).contiguous()
@@ -98,6 +103,17 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
     wts = torch.empty(1, top_k, device=x.device, dtype=torch.float32)
     nw = None if norm_weight is None else norm_weight.reshape(-1).contiguous()
     bias = None if layer.router_bias is None else layer.router_bias.float().contiguous()
+    nx_w = nx_a = nx_r = nx_out = None
+    nx_eps, nx_rows = 0.0, 0
+    if next_linear is not None:
+        nx_w, nx_a, nx_r, nx_eps = next_linear
+        if nx_w.dtype != torch.uint32:
+            raise TypeError("next_linear packed weight must be torch.uint32")
+        if nx_w.shape[1] * 16 != hidden or nx_r.numel() != hidden or nx_r.dtype != torch.float32:
+            raise ValueError("next_linear must be ([N, hidden/16] uint32, alpha [N], float32 rms [hidden], eps)")
+        nx_rows = int(nx_w.shape[0])
+        nx_a, nx_r = nx_a.contiguous(), nx_r.contiguous()
+        nx_out = torch.empty(1, nx_rows, device=x.device, dtype=torch.bfloat16)
     _lib.call(
         "ma_moe_fused",
         _lib.ptr(xf), _lib.ptr(ad), _lib.ptr(nw),
@@ -105,8 +121,12 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
         _lib.ptr(layer.gate_weight), _lib.ptr(bias), layer.n_experts, hidden, layer.inter, top_k,
         _lib.ptr(layer.up_gate_packed), _lib.ptr(layer.up_gate_alpha), _lib.ptr(layer.down_packed),
         _lib.ptr(layer.down_alpha), _lib.ptr(y), _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(ws),
-        ws.numel(), _lib.stream_of(x),
+        ws.numel(), _lib.ptr(nx_w), _lib.ptr(nx_a),
+        _lib.dtype_code(nx_a, "row_alpha") if nx_a is not None else 0, _lib.ptr(nx_r),
+        float(nx_eps), nx_rows, _lib.ptr(nx_out), _lib.stream_of(x),
     )
+    if next_linear is not None:
+        return y, ids, wts, nx_out
     return y, ids, wts
 
 

@@ -22,6 +22,7 @@ import torch
 
 from _helpers import assert_bf16_close, np_f, np_u32, tie_safe_rows
 from maple_amd import synthetic
+from maple_amd.kernels import ternary_gemv
 from maple_amd.moe import moe_block, moe_fused, moe_fused_timed_out
 from oracle import kernels as ok
 
@@ -121,6 +122,68 @@ def test_fused_graph_replays_match_eager(dev, layers):
         g.replay()
         torch.cuda.synchronize()
         for i in range(6):
+            assert torch.equal(outs[i], eager[i]), f"replay {rep} layer {i}"
+        torch.zeros(1, device=dev).add_(1)  # eager work between replays
+    assert not moe_fused_timed_out(dev)
+
+
+def _next_linear(n_out, hidden, seed, dev):
+    packed, alpha = synthetic.ternary_linear(n_out, hidden, seed, dev)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    rms = torch.rand(hidden, device=dev, generator=g) + 0.5
+    return packed, alpha, rms, 1e-6
+
+
+@pytest.mark.parametrize("with_add", [False, True])
+def test_fused_next_projection_equals_gemv(dev, layers, with_add):
+    """The next layer's RMS-folded projection computed in the same launch
+    gives the bits of ternary_gemv on the launch's own y (2560 rows, the
+    synthetic decoder's QKV), over consecutive calls."""
+    nl = _next_linear(2560, 2048, 77, dev)
+    for step in range(3):
+        L = layers[step % len(layers)]
+        x = synthetic.randn_bf16((1, 2048), 1200 + step, dev)
+        kw = {}
+        if with_add:
+            kw = dict(add=synthetic.randn_bf16((1, 2048), 1300 + step, dev, std=0.5),
+                      norm_weight=torch.rand(2048, device=dev) + 0.5)
+        y, ids, wts, q = moe_fused(x, L, 8, next_linear=nl, **kw)
+        y0, _, _ = moe_fused(x, L, 8, **kw)
+        ref = ternary_gemv(y, nl[0], nl[1], rms_weight=nl[2], rms_eps=nl[3])
+        torch.cuda.synchronize()
+        assert torch.equal(y, y0), f"y changed by the tail, step {step}"
+        assert torch.equal(q, ref), f"next projection, step {step}"
+    assert not moe_fused_timed_out(dev)
+
+
+def test_fused_next_projection_small_shape(dev):
+    L = synthetic.make_moe_layer(256, 8, 128, seed=19, device=dev)
+    nl = _next_linear(512, 256, 78, dev)
+    for step in range(2):
+        x = synthetic.randn_bf16((1, 256), 1400 + step, dev)
+        y, _, _, q = moe_fused(x, L, 2, next_linear=nl)
+        ref = ternary_gemv(y, nl[0], nl[1], rms_weight=nl[2], rms_eps=nl[3])
+        torch.cuda.synchronize()
+        assert torch.equal(q, ref), f"small next projection, step {step}"
+
+
+def test_fused_next_projection_graph_replays(dev, layers):
+    nl = _next_linear(2560, 2048, 79, dev)
+    xs = [synthetic.randn_bf16((1, 2048), 1500 + i, dev) for i in range(3)]
+    eager = [moe_fused(xs[i], layers[i], 8, next_linear=nl)[3].clone() for i in range(3)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        [moe_fused(xs[i], layers[i], 8, next_linear=nl) for i in range(3)]
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = [moe_fused(xs[i], layers[i], 8, next_linear=nl)[3] for i in range(3)]
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for i in range(3):
             assert torch.equal(outs[i], eager[i]), f"replay {rep} layer {i}"
         torch.zeros(1, device=dev).add_(1)  # eager work between replays
     assert not moe_fused_timed_out(dev)
