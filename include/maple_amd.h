@@ -268,8 +268,9 @@ int ma_qk_norm_rope_store(const void* qkv, int64_t ldq, int64_t batch, int n_hea
  * 16-byte aligned, zero-filled before the first call: it starts with a sync
  * area of 256-byte lines (line 0, int32 word 2: set to 1 if a barrier wait
  * ever exceeded about 0.2 s; then per (row, KV head) an arrival-counter line,
- * which each call leaves at zero, and a generation line).  Calls that share a
- * workspace must not overlap.  head_dim must be 64.
+ * which each call leaves at zero, and a generation line; then 33 lines of a
+ * grid barrier for the fused entry point's O projection).  Calls that share
+ * a workspace must not overlap.  head_dim must be 64.
  * Replaces decode_gqa_attn, src/maple_run/kernels/decode_attn.py:470-592
  * (which merges the splits in a second kernel, :317-359).
  */
@@ -285,6 +286,12 @@ int ma_decode_gqa_attn(const void* q, int64_t batch, int n_heads, int n_kv_heads
  * arguments and results; q is not written out).  The decode step of the
  * reference's MapleAttention, src/maple_run/model.py:368-414, which runs the
  * RoPE gather, apply_qkv_decode and decode_gqa_attn as separate launches.
+ * With o_w != NULL (batch 1, n_heads * head_dim = 2048) the same launch also
+ * computes the output projection o_proj of that attention:
+ * o_out bf16 [o_rows] = ternary_gemv(out, o_w [o_rows, 128], o_alpha
+ * (f32/bf16)) -- the bits ma_ternary_gemv gives (reference
+ * src/maple_run/kernels/ternary_gemv.py:261-388); o_w 16-byte aligned,
+ * o_rows <= 16 x the launch's workgroups (2112 for a 4224-position cache).
  */
 int ma_decode_attn_fused(const void* qkv, int64_t ldq, int64_t batch, int n_heads,
                          int n_kv_heads, int head_dim, const void* q_norm_w,
@@ -293,7 +300,13 @@ int ma_decode_attn_fused(const void* qkv, int64_t ldq, int64_t batch, int n_head
                          int use_rope, float eps, const int64_t* seqlen, const int64_t* row_map,
                          void* k_cache, void* v_cache, int64_t cache_rows, int64_t max_len,
                          int64_t window, float scale, void* out, void* workspace,
-                         size_t workspace_bytes, void* stream);
+                         size_t workspace_bytes, const uint32_t* o_w, const void* o_alpha,
+                         int o_alpha_dtype, int64_t o_rows, void* o_out, void* stream);
+/* 1 if ma_decode_attn_fused can compute an O projection of o_rows rows in the
+ * launch for these sizes, else 0.  No reference counterpart (a capability
+ * query for the fused output projection above). */
+int ma_decode_attn_o_supported(int64_t batch, int n_heads, int n_kv_heads, int head_dim,
+                               int64_t max_len, int64_t window, int64_t o_rows);
 
 /*
  * Greedy choice: out[r] = argmax over the n values of row r (bf16 or float32,

@@ -17,7 +17,8 @@
 //     splits merged with exp(m_s - max) weights.
 // Positions are clamped to [0, max_len) and mapped rows to [0, cache_rows), so
 // nothing is written or read outside the cache.
-#include "common.h"
+#include "grid_sync.h"
+#include "tgemv_fast.h"
 
 namespace ma {
 
@@ -28,6 +29,8 @@ constexpr int kMaxGroup = 16;               // query heads per KV head
 constexpr int kVtRow = kSplit / 2 + 4;      // LDS row (one dim) of V position
                                             // pairs in words, padded
 constexpr int kCombineChunk = 4;            // splits whose partials one merge lane loads together
+constexpr int kOWords = 4;                  // O projection: words of K per lane (K = 32 x 4 x 16 = 2048)
+constexpr int kOPass = 2;                   // O projection: row passes (8 rows each) per workgroup
 constexpr int kSyncLine = 64;               // uint32 words per 256-byte line of the sync area
 constexpr uint64_t kAttnSpin = 20000000ull; // 0.2 s of the 100 MHz realtime counter
 constexpr int kTargetGroups = 512;          // workgroups an attention launch aims for (swept: 512 best at batch 32)
@@ -59,6 +62,15 @@ struct CoherentBuf {
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, off, 0, kCoherentPolicy);
   }
 };
+
+// Attention output store: 4 bf16 values; device-coherent when other
+// workgroups of the launch read them back (the O projection below).
+__device__ __forceinline__ void store_out(uint16_t* p, uint2 r, bool coherent) {
+  if (coherent)
+    st_coh64(reinterpret_cast<uint64_t*>(p), (static_cast<uint64_t>(r.y) << 32) | r.x);
+  else
+    *reinterpret_cast<uint2*>(p) = r;
+}
 
 struct RopeSrc {
   const void* cos;
@@ -174,12 +186,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, int64_t cache_rows,
     int64_t max_len, const int64_t* __restrict__ seqlen, const int64_t* __restrict__ row_map,
     int nq, int nkv, int64_t window, float scale, int max_splits, uint32_t* __restrict__ sync,
-    float* __restrict__ part_acc, float* __restrict__ part_ml, uint16_t* __restrict__ out) {
+    float* __restrict__ part_acc, float* __restrict__ part_ml, uint16_t* __restrict__ out,
+    const uint32_t* __restrict__ o_w, const void* __restrict__ o_alpha, int o_alpha_dt, int o_rows,
+    uint16_t* __restrict__ o_out) {
   __shared__ __align__(16) uint16_t qs[kMaxGroup][kHeadDim];
   __shared__ __align__(16) uint32_t vt[kHeadDim][kVtRow];
   __shared__ __align__(16) uint16_t kvnew[2][kHeadDim];
   __shared__ float wm[4][kMaxGroup], wl[4][kMaxGroup];
   __shared__ float hm[kMaxGroup], hl[kMaxGroup], hr[kMaxGroup];
+  __shared__ __align__(16) uint4 os4[kOWords * 2][32];  // O projection input
   const int sp = blockIdx.x, kvh = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -192,13 +207,38 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   uint32_t* const gen = arrive + kSyncLine;
   const uint32_t g0 = wv == 0 ? __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  // O projection in the same launch (batch 1): a barrier over every workgroup
+  // of the launch on the sync area's last 33 lines, then each workgroup
+  // computes its rows of o from the whole attention output.
+  uint32_t* const gsub = sync + kSyncLine * (1 + 2 * gridDim.z * nkv);
+  uint32_t* const gtop = gsub + kSyncLine * kBarGroups;
+  uint32_t* const gflags = gtop + kSyncLine;
+  const int wgl = (static_cast<int>(b) * static_cast<int>(gridDim.y) + kvh) * static_cast<int>(gridDim.x) + sp;
+  const int n_wg = static_cast<int>(gridDim.x * gridDim.y * gridDim.z);
+  const uint32_t f0o = o_w && wv == 0 ? ld_coh32(&gflags[kSyncLine * (wgl % kBarGroups)]) : 0u;
+  // This workgroup's O rows (as the standalone GEMV splits them: 32 lanes of
+  // kOWords words per row, 2 rows per wave pass, kOPass passes), loaded once
+  // the K/V chunks are in, so that they do not compete with them.
+  const int o_rq = o_w ? (o_rows + n_wg - 1) / n_wg : 0;
+  const int okl = lane & 31, osub = lane >> 5;
+  uint32_t ow_w[kOPass][kOWords];
+  float ow_a[kOPass];
+  auto o_prefetch = [&]() {
+#pragma unroll
+    for (int p = 0; p < kOPass; ++p) {
+      int r = wgl * o_rq + p * 8 + wv * 2 + osub;
+      r = r < o_rows ? r : o_rows - 1;
+      load_words<kOWords>(o_w + static_cast<int64_t>(r) * (32 * kOWords) + okl * kOWords, ow_w[p]);
+      ow_a[p] = ld_f(o_alpha, o_alpha_dt, r);
+    }
+  };
   const int64_t pos = clamp64(seqlen[b], 0, max_len - 1);
   const int64_t kv_len = pos + 1;
   const int64_t start = (window > 0 && kv_len > window) ? kv_len - window : 0;
   const int n_chunks = static_cast<int>(cdiv(kv_len - start, kSplit));
   const int cps = static_cast<int>(cdiv(n_chunks, gridDim.x));  // chunks per split
   const int n_spl = static_cast<int>(cdiv(n_chunks, cps));
-  if (sp >= n_spl) return;
+  auto attend = [&]() {
   const int c_beg = sp * cps;
   const int c_end = c_beg + cps < n_chunks ? c_beg + cps : n_chunks;
   const int64_t crow = row_map ? clamp64(row_map[b], 0, cache_rows - 1) : b;
@@ -387,6 +427,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     }
     __syncthreads();  // vt / wm / wl are rewritten by the next chunk
   }
+  if (o_w) o_prefetch();  // after the K/V stream, in flight through the merge and the barrier
   // The new K/V go to the cache last (after every read of the cache).
   if (owns_pos && wv < 2) (wv == 0 ? k_cache : v_cache)[(base + pos) * kHeadDim + lane] = new_kv;
   // Sum the waves' P.V (same running max, so a plain sum) in a fixed order,
@@ -419,7 +460,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       uint2 r;
       r.x = pack_bf16x2_rn(o.x * inv, o.y * inv);
       r.y = pack_bf16x2_rn(o.z * inv, o.w * inv);
-      *reinterpret_cast<uint2*>(out + (b * nq + kvh * group + hh) * kHeadDim + 4 * dq) = r;
+      store_out(out + (b * nq + kvh * group + hh) * kHeadDim + 4 * dq, r, o_w != nullptr);
     } else {
       acc_buf.st4(static_cast<uint32_t>(((pidx * kMaxGroup + hh) * kHeadDim + 4 * dq) * 4), o);
     }
@@ -511,15 +552,74 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       uint2 r;
       r.x = pack_bf16x2_rn(n0 / den, n1 / den);
       r.y = pack_bf16x2_rn(n2 / den, n3 / den);
-      *reinterpret_cast<uint2*>(out + (b * nq + kvh * group + hh) * kHeadDim + 4 * dq) = r;
+      store_out(out + (b * nq + kvh * group + hh) * kHeadDim + 4 * dq, r, o_w != nullptr);
     }
   }
+  };
+  if (sp < n_spl)
+    attend();
+  else if (o_w)
+    o_prefetch();
+  if (!o_w) return;
+
+  // O projection: o_out = ternary_gemv(attention output, o_w, o_alpha) --
+  // reference kernels/ternary_gemv.py (the o_proj of MapleAttention,
+  // model.py:368-414) -- with the standalone fast GEMV's per-lane arithmetic
+  // in the same order (so the same bits), once every workgroup's slice of
+  // the attention output is out.
+  __builtin_amdgcn_s_waitcnt(0);  // this workgroup's output stores have completed
+  __syncthreads();
+  bool o_timed_out = false;
+  if (wv == 0) o_timed_out = grid_barrier(gsub, gtop, gflags, f0o, n_wg, wgl, lane, t0);
+  __syncthreads();
+  {  // entry (i, half, l) of os4 = values 8 half .. + 8 of word l * kOWords + i
+    const int w = tid >> 1, half = tid & 1;
+    const uint64_t* p = reinterpret_cast<const uint64_t*>(out + static_cast<int64_t>(b) * nq * kHeadDim +
+                                                          w * 16 + 8 * half);
+    const uint64_t v0 = ld_coh64(p), v1 = ld_coh64(p + 1);
+    os4[(w % kOWords) * 2 + half][w / kOWords] =
+        make_uint4(static_cast<uint32_t>(v0), static_cast<uint32_t>(v0 >> 32),
+                   static_cast<uint32_t>(v1), static_cast<uint32_t>(v1 >> 32));
+  }
+  __syncthreads();
+  uint32_t xh[kOWords][8];
+  float c = 0.f;
+#pragma unroll
+  for (int i = 0; i < kOWords; ++i) {
+    const uint4 a0 = os4[i * 2][okl], a1 = os4[i * 2 + 1][okl];
+    const uint32_t u[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    float xs[16];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      xs[2 * q] = __uint_as_float(u[q] << 16);
+      xs[2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
+    }
+    c += prep_word_pairs(xs, xh[i]);
+  }
+  const ExpandConsts kc;
+#pragma unroll
+  for (int p = 0; p < kOPass; ++p) {
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < kOWords; ++i) {
+      uint32_t e[8];
+      expand_word(ow_w[p][i], e, kc);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j & 1] = dot2(e[j], xh[i][j], acc[j & 1]);
+    }
+    const float d = group_sum<32>(((acc[0] + acc[1]) - c) * ow_a[p]);
+    const int rl = p * 8 + wv * 2 + osub;
+    const int r = wgl * o_rq + rl;
+    if (okl == 0 && rl < o_rq && r < o_rows) o_out[r] = f32_to_bf16(d);
+  }
+  if (o_timed_out && tid == 0) st_coh32(sync + 2, 1u);
 }
 
 // Sync area: line 0 (word 2: timeout), then per (row, KV head) an arrival
-// counter line and a generation line.
+// counter line and a generation line, then the O projection's grid barrier
+// (16 sub-counter lines, a top counter line, 16 release-flag lines).
 size_t sync_bytes(int64_t batch, int nkv) {
-  return (1 + 2 * static_cast<size_t>(batch) * nkv) * kSyncLine * sizeof(uint32_t);
+  return (1 + 2 * static_cast<size_t>(batch) * nkv + 2 * kBarGroups + 1) * kSyncLine * sizeof(uint32_t);
 }
 
 int64_t max_splits_for(int64_t max_len) { return cdiv(max_len, kSplit); }
@@ -588,13 +688,32 @@ extern "C" size_t ma_gqa_workspace_bytes(int64_t batch, int n_kv_heads, int64_t 
   return sync_bytes(batch, n_kv_heads) + parts * (kHeadDim + 2) * sizeof(float);
 }
 
+// Workgroups of one attention launch.
+static int64_t attn_grid_splits(int64_t batch, int nkv, int64_t max_len, int64_t window) {
+  const int64_t span = window > 0 && window < max_len ? window : max_len;
+  int64_t grid_splits = cdiv(kTargetGroups, batch * nkv);
+  if (grid_splits > cdiv(span, kSplit)) grid_splits = cdiv(span, kSplit);
+  return grid_splits;
+}
+
+extern "C" int ma_decode_attn_o_supported(int64_t batch, int n_heads, int n_kv_heads, int head_dim,
+                                          int64_t max_len, int64_t window, int64_t o_rows) {
+  if (batch != 1 || n_kv_heads < 1 || max_len < 1 ||
+      static_cast<int64_t>(n_heads) * head_dim != 32 * kOWords * 16)
+    return 0;
+  const int64_t n_wg = attn_grid_splits(batch, n_kv_heads, max_len, window) * n_kv_heads;
+  return n_wg >= kBarGroups && o_rows >= 1 && o_rows <= n_wg * 8 * kOPass;
+}
+
 // Shared launch of k_decode_attn for the two entry points below.
 static int launch_attn(bool fused, const void* src, int64_t ldq, const void* qn_w,
                        const void* kn_w, int w_dt, const RopeSrc& rope, float eps,
                        void* k_cache, void* v_cache, int64_t cache_rows, int64_t max_len,
                        const int64_t* seqlen, const int64_t* row_map, int64_t batch, int nq,
                        int nkv, int64_t window, float scale, void* out, void* workspace,
-                       size_t workspace_bytes, hipStream_t s, const char* what) {
+                       size_t workspace_bytes, const uint32_t* o_w, const void* o_alpha,
+                       int o_alpha_dt, int64_t o_rows, void* o_out, hipStream_t s,
+                       const char* what) {
   if (!workspace || workspace_bytes < ma_gqa_workspace_bytes(batch, nkv, max_len))
     return fail(MA_EVALUE, "%s: workspace too small", what);
   if (!aligned16(workspace) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out) ||
@@ -603,20 +722,31 @@ static int launch_attn(bool fused, const void* src, int64_t ldq, const void* qn_
   const int64_t max_splits = max_splits_for(max_len);
   if (batch * nkv * max_splits * kMaxGroup * kHeadDim * 4 >= (int64_t{1} << 32))
     return fail(MA_EVALUE, "%s: batch x kv heads x max_len too large for one launch", what);
-  const int64_t span = window > 0 && window < max_len ? window : max_len;
-  const int64_t pairs = batch * nkv;
-  int64_t grid_splits = cdiv(kTargetGroups, pairs);
-  if (grid_splits > cdiv(span, kSplit)) grid_splits = cdiv(span, kSplit);
+  const int64_t grid_splits = attn_grid_splits(batch, nkv, max_len, window);
   auto* sync = static_cast<uint32_t*>(workspace);
   float* acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + sync_bytes(batch, nkv));
   float* ml = acc + static_cast<size_t>(batch) * nkv * max_splits * kMaxGroup * kHeadDim;
   dim3 grid(static_cast<unsigned>(grid_splits), static_cast<unsigned>(nkv),
             static_cast<unsigned>(batch));
+  if (o_w) {
+    const int64_t n_wg = grid_splits * nkv * batch;
+    if (batch != 1 || static_cast<int64_t>(nq) * kHeadDim != 32 * kOWords * 16)
+      return fail(MA_EVALUE, "%s: the O projection in the launch needs batch 1 and n_heads x head_dim = %d",
+                  what, 32 * kOWords * 16);
+    if (n_wg < kBarGroups || o_rows < 1 || o_rows > n_wg * 8 * kOPass)
+      return fail(MA_EVALUE, "%s: O projection of %lld rows over %lld workgroups unsupported", what,
+                  static_cast<long long>(o_rows), static_cast<long long>(n_wg));
+    if (!o_alpha || !o_out || !aligned16(o_w))
+      return fail(MA_EVALUE, "%s: O projection needs 16-byte aligned weights, alpha and output", what);
+    if (o_alpha_dt != MA_F32 && o_alpha_dt != MA_BF16)
+      return fail(MA_ETYPE, "%s: O projection alpha dtype %d", what, o_alpha_dt);
+  }
 #define MA_ATTN_ARGS                                                                            \
   static_cast<const uint16_t*>(src), ldq, qn_w, kn_w, w_dt, rope, eps,                          \
       static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), cache_rows, max_len,    \
       seqlen, row_map, nq, nkv, window, scale, static_cast<int>(max_splits), sync, acc, ml,   \
-      static_cast<uint16_t*>(out)
+      static_cast<uint16_t*>(out), o_w, o_alpha, o_alpha_dt, static_cast<int>(o_rows),         \
+      static_cast<uint16_t*>(o_out)
   if (fused)
     hipLaunchKernelGGL(k_decode_attn<true>, grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
   else
@@ -638,7 +768,8 @@ extern "C" int ma_decode_gqa_attn(const void* q, int64_t batch, int n_heads, int
   return launch_attn(false, q, 0, nullptr, nullptr, MA_F32, none, 0.f,
                      const_cast<void*>(k_cache), const_cast<void*>(v_cache), cache_rows, max_len,
                      seqlen, row_map, batch, n_heads, n_kv_heads, window, scale, out, workspace,
-                     workspace_bytes, static_cast<hipStream_t>(stream), what);
+                     workspace_bytes, nullptr, nullptr, 0, 0, nullptr,
+                     static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int ma_decode_attn_fused(const void* qkv, int64_t ldq, int64_t batch, int n_heads,
@@ -649,7 +780,9 @@ extern "C" int ma_decode_attn_fused(const void* qkv, int64_t ldq, int64_t batch,
                                     const int64_t* seqlen, const int64_t* row_map, void* k_cache,
                                     void* v_cache, int64_t cache_rows, int64_t max_len,
                                     int64_t window, float scale, void* out, void* workspace,
-                                    size_t workspace_bytes, void* stream) {
+                                    size_t workspace_bytes, const uint32_t* o_w,
+                                    const void* o_alpha, int o_alpha_dtype, int64_t o_rows,
+                                    void* o_out, void* stream) {
   const char* what = "decode_attn_fused";
   if (int rc = check_heads(batch, n_heads, n_kv_heads, head_dim, max_len, cache_rows, row_map, what))
     return rc;
@@ -662,5 +795,6 @@ extern "C" int ma_decode_attn_fused(const void* qkv, int64_t ldq, int64_t batch,
   if (batch == 0) return MA_OK;
   return launch_attn(true, qkv, ldq, q_norm_w, k_norm_w, w_dtype, rope, eps, k_cache, v_cache,
                      cache_rows, max_len, seqlen, row_map, batch, n_heads, n_kv_heads, window,
-                     scale, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream), what);
+                     scale, out, workspace, workspace_bytes, o_w, o_alpha, o_alpha_dtype, o_rows,
+                     o_out, static_cast<hipStream_t>(stream), what);
 }

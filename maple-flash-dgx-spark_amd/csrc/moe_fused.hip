@@ -26,6 +26,7 @@
 // coherent path the producers are writing through.)
 // Every wait is bounded (about 0.2 s); on timeout the workspace error word is
 // set and the kernel finishes with wrong values instead of hanging.
+#include "grid_sync.h"
 #include "ternary_engine.h"
 #include "tgemv_fast.h"
 #include "topk.h"
@@ -33,10 +34,7 @@
 namespace ma {
 
 constexpr int kFusedWaves = 4;
-constexpr uint64_t kFusedSpin = 20000000ull;  // 0.2 s of the 100 MHz realtime counter
 
-constexpr int kBarGroups = 16;  // sub-counters (and release flags) of the h barrier
-constexpr int kLine = 64;       // uint32 words in a 256-byte line
 
 // Workspace layout (256-byte lines of uint32 words; every counter and flag has
 // a line of its own so that arrivals and polls on different ones do not meet):
@@ -56,57 +54,6 @@ constexpr int kLogitStride = 16;  // uint64 words between logits
 constexpr size_t kMoeWsHeader = 49152;
 static_assert(kTopC < static_cast<int>(kLogitOff / 256), "workspace lines");
 static_assert(kLogitOff + 256 * kLogitStride * 8 <= kMoeWsHeader, "workspace logits");
-
-__device__ __forceinline__ uint32_t ld_coh32(const uint32_t* p) {
-  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_coh64(const uint64_t* p) {
-  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coh32(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coh64(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void st_coh16(uint16_t* p, uint16_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Grid barrier, run by all 64 lanes of wave 0 of every workgroup once its
-// global stores (and its read of the release flag, f_old) have completed.
-// Workgroup wg arrives on sub-counter wg % kBarGroups; the last arriver there
-// clears it and arrives on the top counter; the last arriver on top clears
-// that and writes f_old + 1 to all kBarGroups flags (one lane each), so the
-// flags always hold equal values and nothing needs clearing afterwards.  The
-// others poll their group's flag until it leaves f_old.  (One atomic per
-// workgroup on a single counter would serialise all G of them at one
-// address.)  Needs G >= kBarGroups, every workgroup resident.  Returns true
-// (on all lanes) if the wait timed out.
-__device__ bool grid_barrier(uint32_t* sub, uint32_t* top, uint32_t* flags, uint32_t f_old, int G,
-                             int wg, int lane, uint64_t t0) {
-  const int g = wg % kBarGroups;
-  int release = 0;
-  if (lane == 0) {
-    const uint32_t n_g = static_cast<uint32_t>((G - g + kBarGroups - 1) / kBarGroups);
-    if (atomicAdd(&sub[kLine * g], 1u) == n_g - 1) {
-      st_coh32(&sub[kLine * g], 0u);
-      if (atomicAdd(top, 1u) == static_cast<uint32_t>(kBarGroups - 1)) {
-        st_coh32(top, 0u);
-        release = 1;
-      }
-    }
-  }
-  if (__shfl(release, 0, 64) && lane < kBarGroups) st_coh32(&flags[kLine * lane], f_old + 1u);
-  int timed_out = 0;
-  if (lane == 0)
-    while (ld_coh32(&flags[kLine * g]) == f_old && !timed_out) {
-      __builtin_amdgcn_s_sleep(2);
-      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kFusedSpin;
-    }
-  return __shfl(timed_out, 0, 64) != 0;
-}
 
 // Shapes: H = 16 * KWH * LPRH (SwiGLU rows split over LPRH lanes), I = 16 *
 // KWI * LPRI (down rows over LPRI lanes), US SwiGLU iterations and UD down
@@ -300,7 +247,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
       }
       if (__all(done) || timed_out) break;
       __builtin_amdgcn_s_sleep(2);
-      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kFusedSpin;
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
     }
     float m = -INFINITY;
 #pragma unroll

@@ -45,6 +45,14 @@ def _norm_weights(q_weight, k_weight):
     return q_weight.reshape(-1).contiguous(), k_weight.reshape(-1).contiguous()
 
 
+def o_projection_supported(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                           max_len: int, window: int | None, o_rows: int) -> bool:
+    """True if ``decode_attention(..., o_linear=...)`` can compute an output
+    projection of ``o_rows`` rows in its launch for these sizes."""
+    return bool(_lib.load().ma_decode_attn_o_supported(batch, num_heads, num_kv_heads, head_dim,
+                                                         max_len, int(window or 0), o_rows))
+
+
 def gqa_workspace(batch: int, num_kv_heads: int, max_len: int, device) -> torch.Tensor:
     """Zeroed workspace for ``decode_gqa_attn`` / ``decode_attention``; keep
     one per cache so decode allocates nothing inside a graph."""
@@ -159,10 +167,16 @@ def decode_attention(
     eps: float = 1e-6,
     scale: float,
     window: int | None = None,
-) -> torch.Tensor:
+    o_linear: tuple | None = None,
+):
     """``apply_qkv_decode`` + ``decode_gqa_attn`` in one launch, with the RoPE
     rows read from the float32 tables ``[n_pos, rotary_dim]`` at ``seqlen[b]``.
-    Returns the attention output ``[B, H, 1, D]`` bf16."""
+    Returns the attention output ``[B, H, 1, D]`` bf16.
+
+    ``o_linear = (packed [N, H*D/16] uint32, alpha [N])`` (batch 1, H*D = 2048):
+    the same launch also computes the output projection
+    ``ternary_gemv(out.reshape(1, -1), packed, alpha)`` (the same bits) and the
+    call returns ``(out, o [1, N])``."""
     if qkv.ndim != 2 or qkv.stride(1) != 1 or qkv.dtype != torch.bfloat16:
         raise ValueError("decode_attention expects a row-contiguous bf16 qkv [B, qkv].")
     bsz = qkv.shape[0]
@@ -173,6 +187,17 @@ def decode_attention(
     out = torch.empty(bsz, num_heads, 1, head_dim, device=qkv.device, dtype=qkv.dtype)
     qw, kw = _norm_weights(q_weight, k_weight)
     sl, rm = _i64(seqlen), _i64(row_map)
+    o_w = o_a = o = None
+    o_rows = 0
+    if o_linear is not None:
+        o_w, o_a = o_linear
+        if o_w.dtype != torch.uint32:
+            raise TypeError("o_linear packed weight must be torch.uint32")
+        if o_w.ndim != 2 or o_w.shape[1] * 16 != num_heads * head_dim:
+            raise ValueError("o_linear packed weight must be [N, num_heads * head_dim / 16]")
+        o_rows = int(o_w.shape[0])
+        o_a = o_a.contiguous()
+        o = torch.empty(bsz, o_rows, device=qkv.device, dtype=qkv.dtype)
     _lib.call(
         "ma_decode_attn_fused",
         _lib.ptr(qkv), qkv.stride(0), bsz, num_heads, num_kv_heads, head_dim,
@@ -180,6 +205,10 @@ def decode_attention(
         _lib.dtype_code(cos_table, "cos_table"), cos_table.stride(0), int(cos_table.shape[0]), int(rotary_dim),
         int(bool(use_rope)), float(eps), _lib.ptr(sl), _lib.ptr(rm),
         _lib.ptr(k_cache), _lib.ptr(v_cache), int(k_cache.shape[0]), max_len, int(window or 0),
-        float(scale), _lib.ptr(out), _lib.ptr(workspace), workspace.numel(), _lib.stream_of(qkv),
+        float(scale), _lib.ptr(out), _lib.ptr(workspace), workspace.numel(),
+        _lib.ptr(o_w), _lib.ptr(o_a), _lib.dtype_code(o_a, "row_alpha") if o_a is not None else 0,
+        o_rows, _lib.ptr(o), _lib.stream_of(qkv),
     )
+    if o_linear is not None:
+        return out, o
     return out

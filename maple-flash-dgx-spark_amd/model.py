@@ -29,7 +29,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import synthetic
-from .kernels.decode_attn import decode_attention, gqa_workspace
+from .kernels.decode_attn import decode_attention, gqa_workspace, o_projection_supported
 from .kernels.fused_norm import add_rms_norm, rms_norm
 from .kernels.greedy import greedy_argmax
 from .kernels.rtn4 import rtn4_embedding, rtn4_gemv
@@ -101,9 +101,10 @@ class KVCache:
 
 class SyntheticDecoder:
     def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 4096 + 128,
-                 fused_moe: bool = True):
+                 fused_moe: bool = True, fused_o: bool = False):
         self.cfg = cfg
         self.fused_moe = fused_moe
+        self.fused_o = fused_o
         self.device = torch.device(device)
         self.max_len = max_len
         c, dev, s = cfg, self.device, seed * 1000
@@ -148,11 +149,19 @@ class SyntheticDecoder:
         bsz = hidden.shape[0]
         if qkv is None:
             qkv = ternary_gemv(hidden, L.qkv, L.qkv_alpha, rms_weight=L.input_ln, rms_eps=c.eps)
-        attn = decode_attention(qkv, L.q_norm, L.k_norm, self.cos, self.sin, cache.k[i], cache.v[i],
-                                cache.seqlen, cache.attn_ws, num_heads=c.heads,
-                                num_kv_heads=c.kv_heads, head_dim=c.head_dim,
-                                rotary_dim=c.rotary_dim, eps=c.eps, scale=c.head_dim ** -0.5)
-        o = ternary_gemv(attn.reshape(bsz, -1), L.o, L.o_alpha)
+        akw = dict(num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim,
+                   rotary_dim=c.rotary_dim, eps=c.eps, scale=c.head_dim ** -0.5)
+        if bsz == 1 and self.fused_o and o_projection_supported(1, c.heads, c.kv_heads, c.head_dim,
+                                                                cache.max_len, None, c.hidden):
+            # attention and its output projection in one launch (measured: no
+            # faster than two launches at 4096 positions -- the grid barrier
+            # and the tail cost what the second launch does -- so off by default)
+            _, o = decode_attention(qkv, L.q_norm, L.k_norm, self.cos, self.sin, cache.k[i], cache.v[i],
+                                    cache.seqlen, cache.attn_ws, o_linear=(L.o, L.o_alpha), **akw)
+        else:
+            attn = decode_attention(qkv, L.q_norm, L.k_norm, self.cos, self.sin, cache.k[i], cache.v[i],
+                                    cache.seqlen, cache.attn_ws, **akw)
+            o = ternary_gemv(attn.reshape(bsz, -1), L.o, L.o_alpha)
         next_qkv = None
         if bsz == 1 and self.fused_moe and fused_supported(L.moe, c.top_k, hidden):
             # add + RMSNorm + router + experts + combine (+ the next layer's

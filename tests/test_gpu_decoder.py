@@ -17,7 +17,8 @@ import torch
 
 from _helpers import assert_bf16_close, np_f, np_u32
 from maple_amd import synthetic
-from maple_amd.kernels import apply_qkv_decode, decode_attention, decode_gqa_attn, gqa_workspace
+from maple_amd.kernels import apply_qkv_decode, decode_attention, decode_gqa_attn, gqa_workspace, ternary_gemv
+from maple_amd.kernels.decode_attn import o_projection_supported
 from maple_amd.model import DecoderConfig, SyntheticDecoder
 from oracle import decoder as od
 
@@ -119,6 +120,34 @@ def test_fused_attention_equals_two_step(dev, window):
         r = int(row_map[b])
         o = od.gqa(np_f(q[b, :, 0]), np_f(kc[r]), np_f(vc[r]), n, d ** -0.5, window)
         assert_bf16_close(np_f(out[b, :, 0]), o, atol_frac=2e-3, what=f"row {b}")
+
+
+@pytest.mark.parametrize("seqlen", [0, 130, 2000, 4100])
+def test_fused_attention_o_projection_equals_gemv(dev, seqlen):
+    """decode_attention(..., o_linear=...) at batch 1 returns the plain call's
+    attention output and, from the same launch, the bits of ternary_gemv on
+    it (the 2048 x 2048 o_proj), over consecutive calls on one workspace,
+    with no timed-out wait recorded."""
+    nq, nkv, d, max_len, rot = 32, 4, 64, 4224, 32
+    qkv = synthetic.randn_bf16((1, (nq + 2 * nkv) * d), 31 + seqlen, dev)
+    kc = synthetic.randn_bf16((1, nkv, max_len, d), 32, dev)
+    vc = synthetic.randn_bf16((1, nkv, max_len, d), 33, dev)
+    w = torch.ones(d, device=dev)
+    cos, sin = (torch.from_numpy(t).to(dev) for t in od.rope_tables(max_len, rot, 1e4))
+    sl = torch.tensor([seqlen], device=dev)
+    wo, ao = synthetic.ternary_linear(2048, 2048, 34, dev)
+    assert o_projection_supported(1, nq, nkv, d, max_len, None, 2048)
+    kw = dict(num_heads=nq, num_kv_heads=nkv, head_dim=d, rotary_dim=rot, eps=1e-6, scale=d ** -0.5)
+    kc2, vc2 = kc.clone(), vc.clone()
+    ref = decode_attention(qkv, w, w, cos, sin, kc, vc, sl, gqa_workspace(1, nkv, max_len, dev), **kw)
+    ws = gqa_workspace(1, nkv, max_len, dev)
+    for _ in range(3):
+        out, o = decode_attention(qkv, w, w, cos, sin, kc2, vc2, sl, ws, o_linear=(wo, ao), **kw)
+        o_ref = ternary_gemv(out.reshape(1, -1), wo, ao)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        assert torch.equal(o, o_ref)
+    assert int(ws[8:12].view(torch.int32).item()) == 0, "a barrier wait timed out"
 
 
 def test_attention_rejects_bad_shapes(dev):
