@@ -67,4 +67,35 @@ __device__ inline bool grid_barrier(uint32_t* sub, uint32_t* top, uint32_t* flag
   return __shfl(timed_out, 0, 64) != 0;
 }
 
+// Device-coherent 8- and 16-byte access through a buffer resource: the sc1 cache policy (the bit agent-scope atomic loads and
+// stores carry on this GPU) sends each access to the coherent level, so a
+// store is visible to workgroups on every XCD once it has completed, without
+// a fence, and one 16-byte access replaces two 8-byte atomics (reading
+// data just written elsewhere is bound by the number of coherent requests
+// one CU issues).  Offsets are bytes; the hardware range check drops
+// accesses past num_bytes.
+constexpr int kCoherentPolicy = 16;  // sc1
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+struct CoherentBuf {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ CoherentBuf(const void* p, uint32_t num_bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, num_bytes, 0x00020000)) {}
+  __device__ float2 ld2(uint32_t off) const {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCoherentPolicy));
+  }
+  __device__ uint4 ld4u(uint32_t off) const {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoherentPolicy));
+  }
+  __device__ float4 ld4(uint32_t off) const {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoherentPolicy));
+  }
+  __device__ void st2(uint32_t off, float2 v) const {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, off, 0, kCoherentPolicy);
+  }
+  __device__ void st4(uint32_t off, float4 v) const {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, off, 0, kCoherentPolicy);
+  }
+};
+
 }  // namespace ma

@@ -403,14 +403,18 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   __syncthreads();
   {
     constexpr int HIT = (TK * NWI + 255) / 256;  // h words per thread, all loads issued first
+    const CoherentBuf hcb(hbuf, TK * I * 2);
     uint64_t d[HIT][4];
 #pragma unroll
     for (int it = 0; it < HIT; ++it) {
       const int wi = tid + 256 * it;
       const int wc = wi < TK * NWI ? wi : TK * NWI - 1;
-      const uint64_t* src = reinterpret_cast<const uint64_t*>(hbuf + (wc / NWI) * I + (wc % NWI) * 16);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) d[it][q] = ld_coh64(src + q);
+      const uint32_t off = static_cast<uint32_t>(((wc / NWI) * I + (wc % NWI) * 16) * 2);
+      const uint4 q0 = hcb.ld4u(off), q1 = hcb.ld4u(off + 16);
+      d[it][0] = (static_cast<uint64_t>(q0.y) << 32) | q0.x;
+      d[it][1] = (static_cast<uint64_t>(q0.w) << 32) | q0.z;
+      d[it][2] = (static_cast<uint64_t>(q1.y) << 32) | q1.x;
+      d[it][3] = (static_cast<uint64_t>(q1.w) << 32) | q1.z;
     }
 #pragma unroll
     for (int it = 0; it < HIT; ++it) {
