@@ -31,6 +31,7 @@ __device__ __forceinline__ f32x4d_t mfma16(uint4 a, uint4 b, f32x4d_t c) {
 
 constexpr int kDenseChunk = 16;  // words of K per step
 constexpr int kDenseRows = 128;  // rows per workgroup (4 waves x 2 x 16)
+constexpr int kRmsMaxK = 8192;   // K of the RMS-folded ternary GEMM, at most
 constexpr uint32_t kMaskQ4d = 0x00780078u;
 
 // ---------------------------------------------------------------------------
@@ -75,6 +76,8 @@ __global__ __launch_bounds__(256) void k_tgemm_mfma(
   // contiguous 256-byte run, so the reads are free of bank conflicts.
   __shared__ __align__(16) uint32_t xs[NV][kDenseChunk][2][NT][4];
   __shared__ float cst[NT], ssq[NT];
+  // RMS weights of all of K, staged once (kRmsMaxK positions at most)
+  __shared__ __align__(16) float rws[RMS ? kRmsMaxK : 1];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g = lane >> 4;
@@ -114,13 +117,22 @@ __global__ __launch_bounds__(256) void k_tgemm_mfma(
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) wq[mb] = *reinterpret_cast<const uint4*>(rowp[mb]);
   load_x(0, xa, xb);
+  if constexpr (RMS) {
+    for (int64_t wd = tid; wd < nwords; wd += 256) {
+      float r[16];
+      load_rms16(rms_w, rms_dt, wd, r);
+#pragma unroll
+      for (int q = 0; q < 16; ++q) rws[wd * 16 + q] = r[q];
+    }
+  }
+  // A thread stages the same token column in every chunk, so its share of the
+  // token's correction (and squares) accumulates in registers; one reduction
+  // over the column's threads at the end.
+  float c_acc[NB], ss_acc[NB];
+#pragma unroll
+  for (int it = 0; it < NB; ++it) c_acc[it] = ss_acc[it] = 0.f;
   __syncthreads();
   for (int64_t c0 = 0; c0 < nwords; c0 += kDenseChunk) {
-    float wr[RMS ? NB : 1][16];
-    if constexpr (RMS) {
-#pragma unroll
-      for (int it = 0; it < NB; ++it) load_rms16(rms_w, rms_dt, c0 + (tid + 256 * it) / NT, wr[it]);
-    }
     // Next chunk's weights and x, in flight during this chunk's work.
     const int64_t cn = c0 + kDenseChunk < nwords ? c0 + kDenseChunk : c0;
     uint4 wn[MB], xan[NB], xbn[NB];
@@ -149,7 +161,7 @@ __global__ __launch_bounds__(256) void k_tgemm_mfma(
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
           ss += v[q] * v[q];
-          const float xh = v[q] * wr[it][q];
+          const float xh = v[q] * rws[(c0 + wd) * 16 + q];
           hi[q] = bf16_to_f32(f32_to_bf16(xh));
           lo[q] = bf16_to_f32(f32_to_bf16(xh - hi[q]));
         }
@@ -159,13 +171,13 @@ __global__ __launch_bounds__(256) void k_tgemm_mfma(
         c += prep_word_pairs(lo, pr);
         *reinterpret_cast<uint4*>(&xs[NV - 1][wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
         *reinterpret_cast<uint4*>(&xs[NV - 1][wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
-        atomicAdd(&ssq[col], ss);
+        ss_acc[it] += ss;
       } else {
         c = prep_word_pairs(v, pr);
         *reinterpret_cast<uint4*>(&xs[0][wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
         *reinterpret_cast<uint4*>(&xs[0][wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
       }
-      atomicAdd(&cst[col], c);
+      c_acc[it] += c;
     }
     __syncthreads();
 #pragma unroll
@@ -198,6 +210,28 @@ __global__ __launch_bounds__(256) void k_tgemm_mfma(
       xa[it] = xan[it];
       xb[it] = xbn[it];
     }
+  }
+  {  // the columns' correction and squares, summed over their threads in a fixed order
+    __shared__ float red_c[256], red_s[256];
+    float cs = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int it = 0; it < NB; ++it) {  // every item of this thread is column tid % NT
+      cs += c_acc[it];
+      s2 += ss_acc[it];
+    }
+    red_c[tid] = cs;
+    red_s[tid] = s2;
+    __syncthreads();
+    if (tid < NT) {
+      float a = 0.f, b = 0.f;
+      for (int k = 0; k < 256 / NT; ++k) {
+        a += red_c[tid + NT * k];
+        b += red_s[tid + NT * k];
+      }
+      cst[tid] = a;
+      ssq[tid] = b;
+    }
+    __syncthreads();
   }
   // Epilogue: lane holds token col r16 of block nb, rows 4g .. 4g+3 of block mb.
   const int64_t kin = nwords * 16;

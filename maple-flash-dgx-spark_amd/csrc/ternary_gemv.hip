@@ -108,7 +108,7 @@ static bool mfma_ok(const void* x, int x_dtype, int64_t batch, int64_t ldx, cons
   auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   return batch >= kMfmaMinBatch && x_dtype == MA_BF16 && !packed_kn && nwords % 16 == 0 &&
          (alpha_dtype == MA_BF16 || alpha_dtype == MA_F32) &&
-         (!rms_weight || rms_dtype == MA_F32 || rms_dtype == MA_BF16) &&
+         (!rms_weight || ((rms_dtype == MA_F32 || rms_dtype == MA_BF16) && nwords * 16 <= 8192)) &&
          a16(x) && ldx % 8 == 0 && a16(packed) && a16(y) && (!rms_weight || a16(rms_weight));
 }
 
