@@ -53,6 +53,27 @@ int ma_ternary_gemv(const void* x, int x_dtype, int64_t batch, int64_t ldx,
                     void* y, int64_t ldy, void* stream);
 
 /*
+ * ma_ternary_gemv with a caller-supplied workspace.  With the fused RMSNorm
+ * (rms_weight != NULL) and 17 tokens or more, every token's GEMM operands
+ * (the x' pairs of the hi and lo halves of x * w_rms, the correction and the
+ * RMS scale) are built once into the workspace by a first launch and the MFMA
+ * GEMM reads them from there.  workspace: 256-byte aligned, at least
+ * ma_ternary_gemv_workspace_bytes(batch, nwords, rms_weight != NULL) bytes;
+ * that query returns 0 where no workspace is used (no RMSNorm, batch < 17,
+ * nwords % 16 != 0), and then -- as for any input the GEMM does not take --
+ * the call is ma_ternary_gemv's and workspace may be NULL.  Same values as
+ * ma_ternary_gemv up to float32 summation order.  Replaces ternary_gemv,
+ * src/maple_run/kernels/ternary_gemv.py:261-388 (its batched path :156-258).
+ */
+size_t ma_ternary_gemv_workspace_bytes(int64_t batch, int64_t nwords, int rms);
+int ma_ternary_gemv_ws(const void* x, int x_dtype, int64_t batch, int64_t ldx,
+                       const uint32_t* packed, int64_t n_out, int64_t nwords, int packed_kn,
+                       const void* row_alpha, int alpha_dtype,
+                       const void* rms_weight, int rms_dtype, float rms_eps,
+                       void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/*
  * Router: logits = x @ W^T (+ bias), softmax over the experts, the top_k
  * largest probabilities in descending order (ties: lowest expert index) and
  * their renormalised weights p / (sum p_top + 1e-20).

@@ -28,6 +28,8 @@ _SIGNATURES = {
     "ma_version": [],
     "ma_last_error": [],
     "ma_ternary_gemv": [_P, _I, _L, _L, _P, _L, _L, _I, _P, _I, _P, _I, _F, _P, _L, _P],
+    "ma_ternary_gemv_workspace_bytes": [_L, _L, _I],
+    "ma_ternary_gemv_ws": [_P, _I, _L, _L, _P, _L, _L, _I, _P, _I, _P, _I, _F, _P, _L, _P, _Z, _P],
     "ma_router_workspace_bytes": [_L, _L],
     "ma_router_topk": [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _P, _P, _P, _Z, _P],
     "ma_moe_dispatch": [_P, _I, _L, _I, _P, _P, _P, _P, _P],
@@ -57,6 +59,7 @@ _SIGNATURES = {
                        _P, _L, _P, _P, _Z, _P],
 }
 _RESTYPES = {"ma_last_error": ctypes.c_char_p, "ma_router_workspace_bytes": _Z,
+             "ma_ternary_gemv_workspace_bytes": _Z,
              "ma_grouped_workspace_bytes": _Z, "ma_gqa_workspace_bytes": _Z,
              "ma_moe_fused_workspace_bytes": _Z}
 

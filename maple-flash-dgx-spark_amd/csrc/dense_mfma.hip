@@ -5,33 +5,68 @@
 // lm_head (_rtn4_gemm_kernel, src/maple_run/kernels/rtn4.py:170-282, in the
 // factored per-group form s_g (q.x)_g + b_g sum_g x of :197-208).
 //
-// y[t, n] for a tile of rows (4 waves x MB blocks of 16; the ternary GEMM uses
-// MB = 1, the RTN4 one MB = 2) and 16*NB tokens, K walked in chunks of 16
-// words with the next chunk's weights and activations loaded ahead.  v_mfma_f32_16x16x32_bf16 layouts (checked
-// on the device): A lane l holds row l%16, k 8(l/16)..+8; B col l%16, k
-// 8(l/16)..+8; C col l%16, rows 4(l/16)..+4.
+// v_mfma_f32_16x16x32_bf16 layouts (checked on the device): A lane l holds row
+// l%16, k 8(l/16)..+8; B col l%16, k 8(l/16)..+8; C col l%16, rows 4(l/16)..+4.
 //
 // Ternary: a lane expands one 16-code word into 8 bf16x2 dwords of 1 + c/f
-// (expand_word) = two MFMA k-slices; B holds the matching x' = f x pairs from
-// LDS, so C accumulates sum (f + c) x and y = alpha (C - sum (f + 1) x).
+// (expand_word) = two MFMA k-slices; B holds the matching x' = f x pairs, so C
+// accumulates sum (f + c) x and y = alpha (C - sum (f + 1) x).  A workgroup
+// takes 16 rows and 16 (or 32) tokens with K split over its 8 waves, one
+// 16-word chunk per wave at K = 2048, and the partial tiles are added in wave
+// order; decode projections have few rows, and a K walk per workgroup left
+// most of the chip idle.  With the RMSNorm folded in, from 17 tokens the x'
+// operands are built once per token by a first launch into a workspace.
 // RTN4: a word's 8 codes expand to 4 dwords of 1 + q/16 = one k-slice against
-// x' = 16 x pairs; after each RTN group C is folded into the output as
-// s_g (C - 16 X_g) + b_g X_g (X_g = sum of x over the group) and cleared.
+// x' = 16 x pairs staged in LDS; after each RTN group C is folded into the
+// output as s_g (C - 16 X_g) + b_g X_g (X_g = sum of x over the group) and
+// cleared.
 #include "common.h"
 
 namespace ma {
 
 typedef __bf16 bf16x8d_t __attribute__((ext_vector_type(8)));
 typedef float f32x4d_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x4d_t mfma16(uint4 a, uint4 b, f32x4d_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8d_t, a),
                                                  __builtin_bit_cast(bf16x8d_t, b), c, 0, 0, 0);
 }
 
+__device__ __forceinline__ f32x4d_t mfma16v(u32x4v_t a, u32x4v_t b, f32x4d_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8d_t, a),
+                                                 __builtin_bit_cast(bf16x8d_t, b), c, 0, 0, 0);
+}
+
+// Operand discipline of the K-split GEMMs: a step's A and B operands are all
+// built before its MFMAs issue and are kept live (empty asm uses that also
+// read the accumulators, so they sit after the MFMAs' results) until the
+// step's MFMAs are done.  No register an MFMA reads is then reused for another
+// value -- VALU result, load or MFMA result -- while that MFMA may still be
+// reading it.  When the compiler was left free to reuse those registers (an
+// MFMA result in its own B registers, a following instruction's result in the
+// previous MFMA's operands), this instruction gave wrong sums on gfx950.
+template <int NA>
+__device__ __forceinline__ void keep_b(const u32x4v_t& b, const f32x4d_t (&acc)[NA]) {
+  asm volatile("" ::"v"(b), "v"(acc[0]), "v"(acc[NA - 1]));
+}
+template <typename T, int M, int NA>
+__device__ __forceinline__ void keep_b(const T (&b)[M], const f32x4d_t (&acc)[NA]) {
+#pragma unroll
+  for (int i = 0; i < M; ++i) keep_b(b[i], acc);
+}
+
+template <int N, int M, typename T, int NA>
+__device__ __forceinline__ void keep_operands(const u32x4v_t (&av)[N][2], const T (&bv)[M],
+                                              const f32x4d_t (&acc)[NA]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    asm volatile("" ::"v"(av[i][0]), "v"(av[i][1]), "v"(acc[0]), "v"(acc[NA - 1]));
+  keep_b(bv, acc);
+}
+
 constexpr int kDenseChunk = 16;  // words of K per step
 constexpr int kDenseRows = 128;  // rows per workgroup (4 waves x 2 x 16)
-constexpr int kRmsMaxK = 8192;   // K of the RMS-folded ternary GEMM, at most
 constexpr uint32_t kMaskQ4d = 0x00780078u;
 
 // ---------------------------------------------------------------------------
@@ -65,203 +100,351 @@ __device__ __forceinline__ void load_rms16(const void* p, int rdt, int64_t wd, f
   }
 }
 
-template <int NB, int MB, bool RMS, int ADT>
-__global__ __launch_bounds__(256) void k_tgemm_mfma(
-    const uint16_t* __restrict__ x, int64_t batch, int64_t ldx, const uint32_t* __restrict__ w,
-    int64_t n_out, int64_t nwords, const void* __restrict__ alpha,
-    const void* __restrict__ rms_w, int rms_dt, float rms_eps, uint16_t* __restrict__ y,
-    int64_t ldy) {
-  constexpr int NT = 16 * NB, NV = RMS ? 2 : 1, ROWS = 64 * MB;
-  // x' pairs, word-major: a B fragment read by 16 lanes (16 tokens) is one
-  // contiguous 256-byte run, so the reads are free of bank conflicts.
-  __shared__ __align__(16) uint32_t xs[NV][kDenseChunk][2][NT][4];
-  __shared__ float cst[NT], ssq[NT];
-  // RMS weights of all of K, staged once (kRmsMaxK positions at most)
-  __shared__ __align__(16) float rws[RMS ? kRmsMaxK : 1];
+// ---------------------------------------------------------------------------
+// Two-launch form of the RMS-folded ternary GEMM.  k_xprep builds, once per
+// token, what the GEMM's B operands are made of -- the x' pairs of the hi and
+// lo bf16 halves of x * w_rms, the token's correction sum (f + 1) x and its
+// scale rsqrt(mean(x^2) + eps) -- in the GEMM's layout, so that k_tgemm_xpk
+// reads them instead of every row tile rebuilding them from x:
+//   xp [tile][v][word][half][NT] uint4 (v: hi, lo);  xc [tile * NT + col] = (c, scale)
+// Tokens past the batch are zero.  Per word the arithmetic is the one-launch
+// GEMM's; the per-token sums add up in another order.
+// ---------------------------------------------------------------------------
+constexpr int kXpTile = 32;  // tokens per tile of the two-launch form
+
+__global__ __launch_bounds__(128) void k_xprep(const uint16_t* __restrict__ x, int64_t batch,
+                                               int64_t ldx, int64_t nwords,
+                                               const void* __restrict__ rms_w, int rms_dt,
+                                               float rms_eps, int nt, uint4* __restrict__ xp,
+                                               float2* __restrict__ xc) {
+  __shared__ float red_c[128], red_s[128];
+  const int64_t t = blockIdx.x;
+  const int64_t tile = t / nt, col = t % nt;
+  const int tid = threadIdx.x;
+  const bool valid = t < batch;
+  float c = 0.f, ss = 0.f;
+  for (int64_t wd = tid; wd < nwords; wd += 128) {
+    float v[16];
+    if (valid) {
+      const uint4* src = reinterpret_cast<const uint4*>(x + t * ldx + wd * 16);
+      const uint4 a = src[0], b = src[1];
+      const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        v[2 * q] = __uint_as_float(u[q] << 16);
+        v[2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) v[q] = 0.f;
+    }
+    float r[16], hi[16], lo[16];
+    load_rms16(rms_w, rms_dt, wd, r);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      ss += v[q] * v[q];
+      const float xh = v[q] * r[q];
+      hi[q] = bf16_to_f32(f32_to_bf16(xh));
+      lo[q] = bf16_to_f32(f32_to_bf16(xh - hi[q]));
+    }
+    uint32_t pr[8];
+    uint4* dst = xp + ((tile * 2 * nwords + wd) * 2) * nt + col;  // v = hi, half 0
+    const int64_t vstride = nwords * 2 * nt;
+    c += prep_word_pairs(hi, pr);
+    dst[0] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+    dst[nt] = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+    c += prep_word_pairs(lo, pr);
+    dst[vstride] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+    dst[vstride + nt] = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+  }
+  red_c[tid] = c;
+  red_s[tid] = ss;
+  __syncthreads();
+  if (tid == 0) {  // fixed order
+    float a = 0.f, b = 0.f;
+    for (int i = 0; i < 128; ++i) {
+      a += red_c[i];
+      b += red_s[i];
+    }
+    xc[t] = make_float2(a, rsqrtf(b / static_cast<float>(nwords * 16) + rms_eps));
+  }
+}
+
+// K split over the waves of a workgroup: 16 rows x NT = 16 NB tokens per
+// workgroup, wave w takes chunks w, w + KW, ... and reads its B operands
+// straight from xp (each fragment is one 256-byte run per 16 lanes); the KW
+// partial tiles are summed in wave order through LDS before the epilogue.
+template <int NB, int NV, int ADT, int KW>
+__global__ __launch_bounds__(64 * KW) void k_tgemm_xpk(const uint4* __restrict__ xp,
+                                                       const float2* __restrict__ xc,
+                                                       int64_t batch, const uint32_t* __restrict__ w,
+                                                       int64_t n_out, int64_t nwords,
+                                                       const void* __restrict__ alpha,
+                                                       uint16_t* __restrict__ y, int64_t ldy) {
+  constexpr int NT = 16 * NB;
+  constexpr int NBF = 4 * 2 * NV * NB;  // B fragments per lane per chunk
+  __shared__ float red[KW][NB][4][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g = lane >> 4;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * NT;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * ROWS + 16 * MB * wv;
-  if (tid < NT) {
-    cst[tid] = 0.f;
-    ssq[tid] = 0.f;
-  }
-  const uint32_t* rowp[MB];
+  const int64_t tile = blockIdx.y;
+  const int64_t t0 = tile * NT;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 16;
+  int64_t r = row0 + r16;
+  r = r < n_out ? r : n_out - 1;
+  const uint32_t* rowp = w + r * nwords + 4 * g;
+  const u32x4v_t* tb = reinterpret_cast<const u32x4v_t*>(xp) + tile * NV * nwords * 2 * NT;
+  f32x4d_t acc[NB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    int64_t r = row0 + 16 * mb + r16;
-    r = r < n_out ? r : n_out - 1;
-    rowp[mb] = w + r * nwords + 4 * g;
-  }
-  f32x4d_t acc[MB][NB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
   const ExpandConsts kc;
-  // x (and RMS weight) loads of chunk c0 for this thread's staging items.
-  auto load_x = [&](int64_t c0, uint4 (&xa)[NB], uint4 (&xb)[NB]) {
+  for (int64_t c0 = 16 * wv; c0 < nwords; c0 += 16 * KW) {
+    const uint4 wq = *reinterpret_cast<const uint4*>(rowp + c0);
+    u32x4v_t bf[NBF];  // [q][hf][vv][nb]
 #pragma unroll
-    for (int it = 0; it < NB; ++it) {
-      const int item = tid + 256 * it;
-      const int col = item % NT, wd = item / NT;
-      int64_t t = t0 + col;
-      t = t < batch ? t : batch - 1;
-      const uint4* src = reinterpret_cast<const uint4*>(x + t * ldx + (c0 + wd) * 16);
-      xa[it] = src[0];
-      xb[it] = src[1];
-    }
-  };
-  uint4 wq[MB], xa[NB], xb[NB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) wq[mb] = *reinterpret_cast<const uint4*>(rowp[mb]);
-  load_x(0, xa, xb);
-  if constexpr (RMS) {
-    for (int64_t wd = tid; wd < nwords; wd += 256) {
-      float r[16];
-      load_rms16(rms_w, rms_dt, wd, r);
-#pragma unroll
-      for (int q = 0; q < 16; ++q) rws[wd * 16 + q] = r[q];
-    }
-  }
-  // A thread stages the same token column in every chunk, so its share of the
-  // token's correction (and squares) accumulates in registers; one reduction
-  // over the column's threads at the end.
-  float c_acc[NB], ss_acc[NB];
-#pragma unroll
-  for (int it = 0; it < NB; ++it) c_acc[it] = ss_acc[it] = 0.f;
-  __syncthreads();
-  for (int64_t c0 = 0; c0 < nwords; c0 += kDenseChunk) {
-    // Next chunk's weights and x, in flight during this chunk's work.
-    const int64_t cn = c0 + kDenseChunk < nwords ? c0 + kDenseChunk : c0;
-    uint4 wn[MB], xan[NB], xbn[NB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) wn[mb] = *reinterpret_cast<const uint4*>(rowp[mb] + cn);
-    load_x(cn, xan, xbn);
-    // (no sched_barrier here: with loads into loop-carried registers just
-    // above, it produced wrong MFMA operands on this compiler)
-#pragma unroll
-    for (int it = 0; it < NB; ++it) {
-      const int item = tid + 256 * it;
-      const int col = item % NT, wd = item / NT;
-      const bool valid = t0 + col < batch;
-      const uint32_t u[8] = {xa[it].x, xa[it].y, xa[it].z, xa[it].w,
-                             xb[it].x, xb[it].y, xb[it].z, xb[it].w};
-      float v[16];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        v[2 * q] = valid ? __uint_as_float(u[q] << 16) : 0.f;
-        v[2 * q + 1] = valid ? __uint_as_float(u[q] & 0xffff0000u) : 0.f;
-      }
-      uint32_t pr[8];
-      float c;
-      if constexpr (RMS) {
-        float ss = 0.f, hi[16], lo[16];
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          ss += v[q] * v[q];
-          const float xh = v[q] * rws[(c0 + wd) * 16 + q];
-          hi[q] = bf16_to_f32(f32_to_bf16(xh));
-          lo[q] = bf16_to_f32(f32_to_bf16(xh - hi[q]));
-        }
-        c = prep_word_pairs(hi, pr);
-        *reinterpret_cast<uint4*>(&xs[0][wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-        *reinterpret_cast<uint4*>(&xs[0][wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
-        c += prep_word_pairs(lo, pr);
-        *reinterpret_cast<uint4*>(&xs[NV - 1][wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-        *reinterpret_cast<uint4*>(&xs[NV - 1][wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
-        ss_acc[it] += ss;
-      } else {
-        c = prep_word_pairs(v, pr);
-        *reinterpret_cast<uint4*>(&xs[0][wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-        *reinterpret_cast<uint4*>(&xs[0][wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
-      }
-      c_acc[it] += c;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {  // word q of the lane's 4 -> k-slices 2q, 2q+1
-      uint4 a[MB][2];
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const uint32_t wsel = q == 0 ? wq[mb].x : q == 1 ? wq[mb].y : q == 2 ? wq[mb].z : wq[mb].w;
-        uint32_t ex[8];
-        expand_word(wsel, ex, kc);
-        a[mb][0] = make_uint4(ex[0], ex[1], ex[2], ex[3]);
-        a[mb][1] = make_uint4(ex[4], ex[5], ex[6], ex[7]);
-      }
+    for (int q = 0; q < 4; ++q)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
         for (int vv = 0; vv < NV; ++vv)
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) {
-            const uint4 b = *reinterpret_cast<const uint4*>(&xs[vv][4 * g + q][hf][nb * 16 + r16][0]);
+          for (int nb = 0; nb < NB; ++nb)
+            bf[((q * 2 + hf) * NV + vv) * NB + nb] =
+                tb[((vv * nwords + c0 + 4 * g + q) * 2 + hf) * NT + nb * 16 + r16];
+    // every load of the chunk in flight before the first MFMA (one round trip)
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4v_t av[4][2];  // A operands of the lane's 4 words, all built before the MFMAs
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) acc[mb][nb] = mfma16(a[mb][hf], b, acc[mb][nb]);
-          }
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t wsel = q == 0 ? wq.x : q == 1 ? wq.y : q == 2 ? wq.z : wq.w;
+      uint32_t ex[8];
+      expand_word(wsel, ex, kc);
+      av[q][0] = u32x4v_t{ex[0], ex[1], ex[2], ex[3]};
+      av[q][1] = u32x4v_t{ex[4], ex[5], ex[6], ex[7]};
     }
-    __syncthreads();
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) wq[mb] = wn[mb];
+    for (int q = 0; q < 4; ++q)
 #pragma unroll
-    for (int it = 0; it < NB; ++it) {
-      xa[it] = xan[it];
-      xb[it] = xbn[it];
-    }
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int vv = 0; vv < NV; ++vv)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            acc[nb] = mfma16v(av[q][hf], bf[((q * 2 + hf) * NV + vv) * NB + nb], acc[nb]);
+    keep_operands(av, bf, acc);
   }
-  {  // the columns' correction and squares, summed over their threads in a fixed order
-    __shared__ float red_c[256], red_s[256];
-    float cs = 0.f, s2 = 0.f;
 #pragma unroll
-    for (int it = 0; it < NB; ++it) {  // every item of this thread is column tid % NT
-      cs += c_acc[it];
-      s2 += ss_acc[it];
-    }
-    red_c[tid] = cs;
-    red_s[tid] = s2;
-    __syncthreads();
-    if (tid < NT) {
-      float a = 0.f, b = 0.f;
-      for (int k = 0; k < 256 / NT; ++k) {
-        a += red_c[tid + NT * k];
-        b += red_s[tid + NT * k];
-      }
-      cst[tid] = a;
-      ssq[tid] = b;
-    }
-    __syncthreads();
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wv][nb][i][lane] = acc[nb][i];
+  __syncthreads();
+  // Thread e < 4 NT: token col e % NT, rows 4 (e / NT) .. +3 of the tile.
+  const int e = tid;
+  if (e >= 4 * NT) return;
+  const int col = e % NT, rq = e / NT;
+  const int64_t t = t0 + col;
+  if (t >= batch) return;
+  const int nb = col / 16, ln = (col % 16) + 16 * rq;  // acc lane holding rows 4 rq ..
+  const float2 cs = xc[t];
+  const int64_t n0 = row0 + 4 * rq;
+  float o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < KW; ++k) s += red[k][nb][i][ln];
+    const int64_t n = n0 + i < n_out ? n0 + i : n_out - 1;
+    o[i] = ld_t<ADT>(alpha, n) * (s - cs.x) * cs.y;
   }
-  // Epilogue: lane holds token col r16 of block nb, rows 4g .. 4g+3 of block mb.
-  const int64_t kin = nwords * 16;
+  if (n0 + 3 < n_out && (ldy % 4) == 0) {
+    uint2 rr;
+    rr.x = pack_bf16x2_rn(o[0], o[1]);
+    rr.y = pack_bf16x2_rn(o[2], o[3]);
+    *reinterpret_cast<uint2*>(y + t * ldy + n0) = rr;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (n0 + i < n_out) y[t * ldy + n0 + i] = f32_to_bf16(o[i]);
+  }
+}
+
+// One-launch K-split form: 16 rows x NT = 16 NB tokens per workgroup, wave w
+// takes chunks w, w + KW, ...  A lane's B fragments are the x' pairs of words
+// 4g + q of its own token column, so it builds them from x in registers (no
+// LDS staging, no workspace), with that word's correction and squares; the
+// KW partial tiles and the per-token sums are added in a fixed order through
+// LDS.  RDT: -1 without the RMSNorm, else the dtype of w_rms.
+template <int NB, int RDT, int ADT, int KW>
+__global__ __launch_bounds__(64 * KW) void k_tgemm_ks(
+    const uint16_t* __restrict__ x, int64_t batch, int64_t ldx, const uint32_t* __restrict__ w,
+    int64_t n_out, int64_t nwords, const void* __restrict__ alpha, const void* __restrict__ rms_w,
+    float rms_eps, uint16_t* __restrict__ y, int64_t ldy) {
+  constexpr int NT = 16 * NB;
+  constexpr bool RMS = RDT >= 0;
+  constexpr int NV = RMS ? 2 : 1;
+  __shared__ float red[KW][NB][4][64];
+  __shared__ float red_c[KW][4][NT], red_s[KW][4][NT];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * NT;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 16;
+  int64_t r = row0 + r16;
+  r = r < n_out ? r : n_out - 1;
+  const uint32_t* rowp = w + r * nwords + 4 * g;
+  const uint16_t* xrow[NB];
+  bool valid[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    const int col = nb * 16 + r16;
-    const int64_t t = t0 + col;
-    if (t >= batch) continue;
-    const float cc = cst[col];
-    const float scale = RMS ? rsqrtf(ssq[col] / static_cast<float>(kin) + rms_eps) : 1.f;
+    const int64_t t = t0 + nb * 16 + r16;
+    valid[nb] = t < batch;
+    xrow[nb] = x + (valid[nb] ? t : batch - 1) * ldx + 64 * g;  // word 4g of chunk 0
+  }
+  f32x4d_t acc[NB];
+  float cp[NB], sp[NB];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int64_t n0 = row0 + 16 * mb + 4 * g;
-      float o[4];
+  for (int nb = 0; nb < NB; ++nb) {
+    acc[nb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+    cp[nb] = sp[nb] = 0.f;
+  }
+  const ExpandConsts kc;
+  constexpr int RV = RDT == MA_F32 ? 16 : 8;  // uint4 of w_rms per lane per chunk
+  for (int64_t c0 = 16 * wv; c0 < nwords; c0 += 16 * KW) {
+    const uint4 wq = *reinterpret_cast<const uint4*>(rowp + c0);
+    u32x4v_t xv[4][NB][2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t n = n0 + i < n_out ? n0 + i : n_out - 1;
-        o[i] = ld_t<ADT>(alpha, n) * (acc[mb][nb][i] - cc) * scale;
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const u32x4v_t* src = reinterpret_cast<const u32x4v_t*>(xrow[nb] + (c0 + q) * 16);
+        xv[q][nb][0] = src[0];
+        xv[q][nb][1] = src[1];
       }
-      if (n0 + 3 < n_out && (ldy % 4) == 0) {
-        uint2 r;
-        r.x = pack_bf16x2_rn(o[0], o[1]);
-        r.y = pack_bf16x2_rn(o[2], o[3]);
-        *reinterpret_cast<uint2*>(y + t * ldy + n0) = r;
-      } else {
+    u32x4v_t rv[RMS ? RV : 1];
+    if constexpr (RMS) {
+      const u32x4v_t* src = reinterpret_cast<const u32x4v_t*>(
+          static_cast<const char*>(rms_w) + (c0 + 4 * g) * 16 * (RDT == MA_F32 ? 4 : 2));
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (n0 + i < n_out) y[t * ldy + n0 + i] = f32_to_bf16(o[i]);
-      }
+      for (int i = 0; i < RV; ++i) rv[i] = src[i];
     }
+    // every load of the chunk in flight before the first use (one round trip)
+    __builtin_amdgcn_sched_barrier(0);
+    // Two words per step: their A and B operands are all built (VALU) before
+    // the step's MFMAs issue, and stay live until the MFMAs' results exist, so
+    // no operand register is rewritten while an MFMA may still read it.
+#pragma unroll
+    for (int qh = 0; qh < 4; qh += 2) {
+      u32x4v_t av[2][2];             // [word][half]
+      u32x4v_t bv[2][NB][NV][2];     // [word][token block][hi/lo][half]
+#pragma unroll
+      for (int qi = 0; qi < 2; ++qi) {
+        const int q = qh + qi;
+        const uint32_t wsel = q == 0 ? wq.x : q == 1 ? wq.y : q == 2 ? wq.z : wq.w;
+        uint32_t ex[8];
+        expand_word(wsel, ex, kc);
+        av[qi][0] = u32x4v_t{ex[0], ex[1], ex[2], ex[3]};
+        av[qi][1] = u32x4v_t{ex[4], ex[5], ex[6], ex[7]};
+        float rr[16];
+        if constexpr (RMS) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            if constexpr (RDT == MA_F32) {
+              rr[j] = __uint_as_float(rv[4 * q + j / 4][j % 4]);
+            } else {
+              const uint32_t u = rv[2 * q + j / 8][(j % 8) / 2];
+              rr[j] = __uint_as_float((j & 1) ? (u & 0xffff0000u) : (u << 16));
+            }
+          }
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          float v[16];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const uint32_t u = xv[q][nb][j / 4][j % 4];
+            v[2 * j] = valid[nb] ? __uint_as_float(u << 16) : 0.f;
+            v[2 * j + 1] = valid[nb] ? __uint_as_float(u & 0xffff0000u) : 0.f;
+          }
+          uint32_t pr[8];
+          if constexpr (RMS) {
+            float hi[16], lo[16], ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              ss += v[j] * v[j];
+              const float xh = v[j] * rr[j];
+              hi[j] = bf16_to_f32(f32_to_bf16(xh));
+              lo[j] = bf16_to_f32(f32_to_bf16(xh - hi[j]));
+            }
+            sp[nb] += ss;
+            float c = prep_word_pairs(hi, pr);
+            bv[qi][nb][0][0] = u32x4v_t{pr[0], pr[1], pr[2], pr[3]};
+            bv[qi][nb][0][1] = u32x4v_t{pr[4], pr[5], pr[6], pr[7]};
+            c += prep_word_pairs(lo, pr);
+            bv[qi][nb][NV - 1][0] = u32x4v_t{pr[0], pr[1], pr[2], pr[3]};
+            bv[qi][nb][NV - 1][1] = u32x4v_t{pr[4], pr[5], pr[6], pr[7]};
+            cp[nb] += c;
+          } else {
+            cp[nb] += prep_word_pairs(v, pr);
+            bv[qi][nb][0][0] = u32x4v_t{pr[0], pr[1], pr[2], pr[3]};
+            bv[qi][nb][0][1] = u32x4v_t{pr[4], pr[5], pr[6], pr[7]};
+          }
+        }
+      }
+#pragma unroll
+      for (int qi = 0; qi < 2; ++qi)
+#pragma unroll
+        for (int vv = 0; vv < NV; ++vv)
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+              acc[nb] = mfma16v(av[qi][hf], bv[qi][nb][vv][hf], acc[nb]);
+      keep_operands(av, bv, acc);
+    }
+  }
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wv][nb][i][lane] = acc[nb][i];
+    red_c[wv][g][nb * 16 + r16] = cp[nb];  // this lane's (g, token) share
+    red_s[wv][g][nb * 16 + r16] = sp[nb];
+  }
+  __syncthreads();
+  // Thread e < 4 NT: token col e % NT, rows 4 (e / NT) .. +3 of the tile.
+  const int e = tid;
+  if (e >= 4 * NT) return;
+  const int col = e % NT, rq = e / NT;
+  const int64_t t = t0 + col;
+  if (t >= batch) return;
+  const int nb = col / 16, ln = (col % 16) + 16 * rq;  // acc lane holding rows 4 rq ..
+  float cc = 0.f, ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < KW; ++k)
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg) {
+      cc += red_c[k][gg][col];
+      ss += red_s[k][gg][col];
+    }
+  const float scale = RMS ? rsqrtf(ss / static_cast<float>(nwords * 16) + rms_eps) : 1.f;
+  const int64_t n0 = row0 + 4 * rq;
+  float o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < KW; ++k) s += red[k][nb][i][ln];
+    const int64_t n = n0 + i < n_out ? n0 + i : n_out - 1;
+    o[i] = ld_t<ADT>(alpha, n) * (s - cc) * scale;
+  }
+  if (n0 + 3 < n_out && (ldy % 4) == 0) {
+    uint2 rr;
+    rr.x = pack_bf16x2_rn(o[0], o[1]);
+    rr.y = pack_bf16x2_rn(o[2], o[3]);
+    *reinterpret_cast<uint2*>(y + t * ldy + n0) = rr;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (n0 + i < n_out) y[t * ldy + n0 + i] = f32_to_bf16(o[i]);
   }
 }
 
@@ -429,26 +612,52 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
 
 using namespace ma;
 
+// Workspace of the two-launch ternary GEMM (x' operands of every token tile,
+// then (c, scale) per token).
+// Workspace of the two-launch RMS-folded ternary GEMM: the x' operands (hi and
+// lo halves) of every 32-token tile, then (c, scale) per token.
+size_t tgemm_xp_bytes(int64_t batch, int64_t nwords) {
+  const int64_t tiles = cdiv(batch, kXpTile);
+  return static_cast<size_t>(tiles * 2 * nwords * 2 * kXpTile) * 16 +
+         static_cast<size_t>(tiles * kXpTile) * 8;
+}
+
 // Launchers used by ternary_gemv.hip / rtn4.hip for batch >= 5 (bf16 x,
 // [N, K/16] or [N, K/8] codes, nwords % 16 == 0, 16-byte aligned rows).
+// Two-launch form: RMS-folded only (rms_w != NULL), workspace of
+// tgemm_xp_bytes(batch, nwords) bytes, 256-byte aligned.
+int launch_tgemm_xp(const uint16_t* x, int64_t batch, int64_t ldx, const uint32_t* w,
+                    int64_t n_out, int64_t nwords, const void* alpha, int alpha_dt,
+                    const void* rms_w, int rms_dt, float rms_eps, uint16_t* y, int64_t ldy,
+                    void* workspace, hipStream_t s) {
+  const int64_t tiles = cdiv(batch, kXpTile);
+  uint4* xp = static_cast<uint4*>(workspace);
+  float2* xc = reinterpret_cast<float2*>(xp + tiles * 2 * nwords * 2 * kXpTile);
+  hipLaunchKernelGGL(k_xprep, dim3(static_cast<unsigned>(tiles * kXpTile)), dim3(128), 0, s, x,
+                     batch, ldx, nwords, rms_w, rms_dt, rms_eps, kXpTile, xp, xc);
+  dim3 grid(static_cast<unsigned>(cdiv(n_out, 16)), static_cast<unsigned>(tiles));
+  if (alpha_dt == MA_F32)
+    hipLaunchKernelGGL((k_tgemm_xpk<kXpTile / 16, 2, MA_F32, 8>), grid, dim3(512), 0, s, xp, xc,
+                       batch, w, n_out, nwords, alpha, y, ldy);
+  else
+    hipLaunchKernelGGL((k_tgemm_xpk<kXpTile / 16, 2, MA_BF16, 8>), grid, dim3(512), 0, s, xp, xc,
+                       batch, w, n_out, nwords, alpha, y, ldy);
+  return check_launch("ternary_gemv (mfma, two launches)");
+}
+
+// One-launch form: 16-token tiles (the kernel's VGPR use at 32 tokens halves
+// the workgroups a CU holds; 16-token tiles were as fast or faster).
 int launch_tgemm_mfma(const uint16_t* x, int64_t batch, int64_t ldx, const uint32_t* w,
                       int64_t n_out, int64_t nwords, const void* alpha, int alpha_dt,
                       const void* rms_w, int rms_dt, float rms_eps, uint16_t* y, int64_t ldy,
                       hipStream_t s) {
-  const int nb = batch <= 16 ? 1 : 2;
-  const int64_t nt = 16 * nb;
-  // 64-row tiles (one 16-row block per wave): more workgroups for the
-  // decoder's 2048-2560-row projections.
-  dim3 grid(static_cast<unsigned>(cdiv(n_out, 64)), static_cast<unsigned>(cdiv(batch, nt)));
-#define MA_TG(NB, RMS, ADT)                                                                      \
-  hipLaunchKernelGGL((k_tgemm_mfma<NB, 1, RMS, ADT>), grid, dim3(256), 0, s, x, batch, ldx, w, \
-                     n_out, nwords, alpha, rms_w, rms_dt, rms_eps, y, ldy)
-#define MA_TG_A(NB, RMS) \
-  if (alpha_dt == MA_F32) MA_TG(NB, RMS, MA_F32); else MA_TG(NB, RMS, MA_BF16);
-#define MA_TG_R(NB) \
-  if (rms_w) { MA_TG_A(NB, true) } else { MA_TG_A(NB, false) }
-  if (nb == 1) { MA_TG_R(1) } else { MA_TG_R(2) }
-#undef MA_TG_R
+  dim3 grid(static_cast<unsigned>(cdiv(n_out, 16)), static_cast<unsigned>(cdiv(batch, 16)));
+#define MA_TG(RDT, ADT)                                                                        \
+  hipLaunchKernelGGL((k_tgemm_ks<1, RDT, ADT, 8>), grid, dim3(512), 0, s, x, batch, ldx, w, \
+                     n_out, nwords, alpha, rms_w, rms_eps, y, ldy)
+#define MA_TG_A(RDT) \
+  if (alpha_dt == MA_F32) MA_TG(RDT, MA_F32); else MA_TG(RDT, MA_BF16);
+  if (!rms_w) { MA_TG_A(-1) } else if (rms_dt == MA_F32) { MA_TG_A(MA_F32) } else { MA_TG_A(MA_BF16) }
 #undef MA_TG_A
 #undef MA_TG
   return check_launch("ternary_gemv (mfma)");

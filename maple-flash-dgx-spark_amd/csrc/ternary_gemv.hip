@@ -100,7 +100,15 @@ int launch_tgemm_mfma(const uint16_t* x, int64_t batch, int64_t ldx, const uint3
                       int64_t n_out, int64_t nwords, const void* alpha, int alpha_dt,
                       const void* rms_w, int rms_dt, float rms_eps, uint16_t* y, int64_t ldy,
                       hipStream_t s);
+// Two-launch MFMA path (RMS-folded; x' operands built once per token into a
+// workspace), taken by ma_ternary_gemv_ws from kXpMinBatch tokens.
+size_t tgemm_xp_bytes(int64_t batch, int64_t nwords);
+int launch_tgemm_xp(const uint16_t* x, int64_t batch, int64_t ldx, const uint32_t* w,
+                    int64_t n_out, int64_t nwords, const void* alpha, int alpha_dt,
+                    const void* rms_w, int rms_dt, float rms_eps, uint16_t* y, int64_t ldy,
+                    void* workspace, hipStream_t s);
 constexpr int64_t kMfmaMinBatch = 5;
+constexpr int64_t kXpMinBatch = 17;
 
 static bool mfma_ok(const void* x, int x_dtype, int64_t batch, int64_t ldx, const uint32_t* packed,
                     int64_t nwords, int packed_kn, int alpha_dtype, const void* rms_weight,
@@ -108,8 +116,8 @@ static bool mfma_ok(const void* x, int x_dtype, int64_t batch, int64_t ldx, cons
   auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   return batch >= kMfmaMinBatch && x_dtype == MA_BF16 && !packed_kn && nwords % 16 == 0 &&
          (alpha_dtype == MA_BF16 || alpha_dtype == MA_F32) &&
-         (!rms_weight || ((rms_dtype == MA_F32 || rms_dtype == MA_BF16) && nwords * 16 <= 8192)) &&
-         a16(x) && ldx % 8 == 0 && a16(packed) && a16(y) && (!rms_weight || a16(rms_weight));
+         (!rms_weight || rms_dtype == MA_F32 || rms_dtype == MA_BF16) && a16(x) && ldx % 8 == 0 &&
+         a16(packed) && a16(y) && (!rms_weight || a16(rms_weight));
 }
 
 extern "C" int ma_ternary_gemv(const void* x, int x_dtype, int64_t batch, int64_t ldx,
@@ -136,4 +144,38 @@ extern "C" int ma_ternary_gemv(const void* x, int x_dtype, int64_t batch, int64_
     tgemv_generic(x, x_dtype, batch, ldx, packed, n_out, nwords, packed_kn, row_alpha,
                   alpha_dtype, rms_weight, rms_dtype, rms_eps, y, ldy, s);
   return check_launch("ternary_gemv");
+}
+
+extern "C" size_t ma_ternary_gemv_workspace_bytes(int64_t batch, int64_t nwords, int rms) {
+  if (!rms || batch < kXpMinBatch || nwords < 1 || nwords % 16 != 0) return 0;
+  return tgemm_xp_bytes(batch, nwords);
+}
+
+extern "C" int ma_ternary_gemv_ws(const void* x, int x_dtype, int64_t batch, int64_t ldx,
+                                  const uint32_t* packed, int64_t n_out, int64_t nwords,
+                                  int packed_kn, const void* row_alpha, int alpha_dtype,
+                                  const void* rms_weight, int rms_dtype, float rms_eps, void* y,
+                                  int64_t ldy, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  using namespace ma;
+  if (batch < 0 || n_out < 0 || nwords < 1)
+    return fail(MA_EVALUE, "ternary_gemv: bad sizes batch=%lld n=%lld nwords=%lld",
+                (long long)batch, (long long)n_out, (long long)nwords);
+  if (batch == 0 || n_out == 0) return MA_OK;
+  if (!x || !packed || !row_alpha || !y) return fail(MA_EVALUE, "ternary_gemv: null pointer");
+  if (ldx < nwords * 16 || ldy < n_out)
+    return fail(MA_EVALUE, "ternary_gemv: leading dimension too small");
+  if (!rms_weight || batch < kXpMinBatch ||
+      !mfma_ok(x, x_dtype, batch, ldx, packed, nwords, packed_kn, alpha_dtype, rms_weight,
+               rms_dtype, y))
+    return ma_ternary_gemv(x, x_dtype, batch, ldx, packed, n_out, nwords, packed_kn, row_alpha,
+                           alpha_dtype, rms_weight, rms_dtype, rms_eps, y, ldy, stream);
+  const size_t need = tgemm_xp_bytes(batch, nwords);
+  if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255))
+    return fail(MA_EVALUE,
+                "ternary_gemv: workspace of %zu bytes (256-byte aligned) needed, got %zu at %p",
+                need, workspace_bytes, workspace);
+  return launch_tgemm_xp(static_cast<const uint16_t*>(x), batch, ldx, packed, n_out, nwords,
+                         row_alpha, alpha_dtype, rms_weight, rms_dtype, rms_eps,
+                         static_cast<uint16_t*>(y), ldy, workspace, static_cast<hipStream_t>(stream));
 }

@@ -1,8 +1,10 @@
 """Packed ternary GEMV ``y = x @ W`` with ``W`` kept as packed uint32 codes.
 
 Drop-in for reference ``src/maple_run/kernels/ternary_gemv.py:261-388``: same
-signature, argument meaning, output shape/dtype and exceptions.  The work is a
-single launch of ``ma_ternary_gemv`` (HIP, gfx950) on the current stream.
+signature, argument meaning, output shape/dtype and exceptions.  The work is
+``ma_ternary_gemv`` (one launch) or, for the RMS-folded form at 17 tokens and
+more, ``ma_ternary_gemv_ws`` (operand build + GEMM), HIP on gfx950, on the
+current stream.
 """
 
 from __future__ import annotations
@@ -77,13 +79,21 @@ def ternary_gemv(
         rms_w = rms_w.contiguous()
     pw = packed_weight.contiguous()
     alpha = alpha.contiguous()
-    _lib.call(
-        "ma_ternary_gemv",
+    args = (
         _lib.ptr(x_mat), _lib.dtype_code(x_mat, "x"), batch, x_mat.stride(0) if batch else k_in,
         _lib.ptr(pw), n_out, nwords, int(bool(packed_kn)),
         _lib.ptr(alpha), _lib.dtype_code(alpha, "row_alpha"),
         _lib.ptr(rms_w), _lib.dtype_code(rms_w, "rms_weight") if rms_w is not None else 0,
         float(rms_eps),
-        _lib.ptr(y), n_out, _lib.stream_of(x),
+        _lib.ptr(y), n_out,
     )
+    # With the RMSNorm folded in, from 17 tokens the MFMA GEMM's two-launch form
+    # builds each token's operands once into a workspace (the query says 0 where
+    # no workspace is used).
+    ws_bytes = _lib.load().ma_ternary_gemv_workspace_bytes(batch, nwords, int(rms_w is not None))
+    if ws_bytes:
+        ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+        _lib.call("ma_ternary_gemv_ws", *args, _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
+    else:
+        _lib.call("ma_ternary_gemv", *args, _lib.stream_of(x))
     return y.reshape(*leading, n_out)

@@ -286,6 +286,73 @@ def test_gemv_mfma_fused_rms_vs_oracle(dev, batch):
     assert_bf16_close(np_f(y), ref, what=f"mfma rms B={batch}")
 
 
+def _gemv_c(entry, x, w, alpha, rms_w=None, ws=None):
+    """Call ma_ternary_gemv / ma_ternary_gemv_ws directly on [B, K] x."""
+    from maple_amd import _lib
+    batch, k_in = x.shape
+    n_out, nwords = w.shape
+    y = torch.empty(batch, n_out, device=x.device, dtype=torch.bfloat16)
+    args = [_lib.ptr(x), _lib.BF16, batch, k_in, _lib.ptr(w), n_out, nwords, 0,
+            _lib.ptr(alpha), _lib.dtype_code(alpha, "alpha"), _lib.ptr(rms_w),
+            _lib.dtype_code(rms_w, "rms") if rms_w is not None else 0, 1e-6, _lib.ptr(y), n_out]
+    if entry == "ma_ternary_gemv_ws":
+        args += [_lib.ptr(ws), ws.numel() if ws is not None else 0]
+    _lib.call(entry, *args, _lib.stream_of(x))
+    return y
+
+
+@pytest.mark.parametrize("rms", [None, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("batch,n_out", [(5, 2560), (16, 130), (17, 2048), (32, 2560), (48, 700)])
+def test_gemv_mfma_one_and_two_launch_vs_oracle(dev, batch, n_out, rms):
+    """The one-launch K-split GEMM against the oracle, and the workspace entry
+    point (the two-launch form with the RMSNorm from 17 tokens, else the same
+    one launch) against it: same per-word arithmetic, only the float32 sums of
+    the per-token correction and squares add up in another order."""
+    from maple_amd import _lib
+    w = synthetic.ternary_packed((n_out, 2048), 61 + batch, dev)
+    alpha = synthetic.uniform_bf16((n_out,), 0.01, 0.05, 62, dev)
+    x = synthetic.randn_bf16((batch, 2048), 63, dev)
+    rms_w = None if rms is None else (torch.rand(2048, device=dev) + 0.5).to(rms)
+    nbytes = _lib.load().ma_ternary_gemv_workspace_bytes(batch, 128, int(rms is not None))
+    assert (nbytes > 0) == (rms is not None and batch >= 17)
+    ws = torch.full((max(nbytes, 256),), 0xAB, device=dev, dtype=torch.uint8)  # stale bytes
+    y1 = _gemv_c("ma_ternary_gemv", x, w, alpha, rms_w)
+    ref = ok.ternary_gemv(np_f(x), np_u32(w), np_f(alpha),
+                          rms_weight=None if rms_w is None else np_f(rms_w), rms_eps=1e-6)
+    assert_bf16_close(np_f(y1), ref, what=f"one-launch B={batch} rms={rms}")
+    y2 = _gemv_c("ma_ternary_gemv_ws", x, w, alpha, rms_w, ws)
+    torch.testing.assert_close(y2.float(), y1.float(), rtol=8e-3, atol=8e-3)
+    assert_bf16_close(np_f(y2), ref, what=f"workspace entry B={batch} rms={rms}")
+    assert torch.equal(y1, _gemv_c("ma_ternary_gemv", x, w, alpha, rms_w))  # deterministic
+    assert torch.equal(y2, _gemv_c("ma_ternary_gemv_ws", x, w, alpha, rms_w, ws))
+
+
+@pytest.mark.parametrize("batch", [8, 24])
+def test_gemv_mfma_rms_large_k(dev, batch):
+    """K = 12288 with the fused RMSNorm (no K limit on either form)."""
+    w = synthetic.ternary_packed((384, 12288), 71, dev)
+    alpha = synthetic.uniform_bf16((384,), 0.01, 0.05, 72, dev)
+    x = synthetic.randn_bf16((batch, 12288), 73, dev)
+    rms_w = (torch.rand(12288, device=dev) + 0.5).to(torch.bfloat16)
+    y = ternary_gemv(x, w, alpha, rms_weight=rms_w, rms_eps=1e-6)
+    ref = ok.ternary_gemv(np_f(x), np_u32(w), np_f(alpha), rms_weight=np_f(rms_w), rms_eps=1e-6)
+    assert_bf16_close(np_f(y), ref, what=f"rms K=12288 B={batch}")
+
+
+def test_gemv_two_launch_small_workspace_raises(dev):
+    from maple_amd import _lib
+    w = synthetic.ternary_packed((256, 2048), 81, dev)
+    alpha = synthetic.uniform_bf16((256,), 0.01, 0.05, 82, dev)
+    x = synthetic.randn_bf16((20, 2048), 83, dev)
+    rms_w = torch.rand(2048, device=dev) + 0.5
+    nbytes = _lib.load().ma_ternary_gemv_workspace_bytes(20, 128, 1)
+    ws = torch.empty(nbytes - 256, device=dev, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="workspace"):
+        _gemv_c("ma_ternary_gemv_ws", x, w, alpha, rms_w, ws)
+    with pytest.raises(ValueError, match="workspace"):
+        _gemv_c("ma_ternary_gemv_ws", x, w, alpha, rms_w, None)
+
+
 # ---------------------------------------------------------------- RTN4 / norms
 @pytest.mark.parametrize("batch,group", [(1, 128), (1, 64), (2, 128), (4, 64), (32, 128)])
 def test_rtn4_gemv_vs_oracle(dev, batch, group):
