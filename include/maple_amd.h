@@ -188,6 +188,30 @@ int ma_rtn4_embedding(const void* ids, int ids_is_int64, int64_t n_ids,
                       int64_t group_size, float* out, void* stream);
 
 /*
+ * Batched MoE routing in ONE launch: h = x + x_add (bf16; skipped when x_add
+ * is NULL, then h is x), xn = RMSNorm(h) * norm_weight (bf16), the router
+ * (logits = xn @ gate_weight^T + router_bias, softmax, top_k ids / weights)
+ * and the dispatch lists (counts, offsets, pair_ids, inverse as
+ * ma_moe_dispatch gives them).  Same values, bit for bit, as ma_add_rms_norm
+ * (or ma_rms_norm), ma_router_topk and ma_moe_dispatch run one after another
+ * at these sizes.  tokens <= 1024, hidden % 8 == 0 and <= 4096, n_experts <=
+ * 256; bf16 rows, 16-byte aligned.  workspace: 256-byte aligned, at least
+ * ma_moe_route_workspace_bytes(tokens, n_experts) bytes, zero-filled once
+ * when allocated (the kernel leaves it zero; word 64 becomes non-zero if a
+ * wait ever timed out); calls sharing a workspace must not overlap.
+ * Composes add_rms_norm (src/maple_run/kernels/fused_norm.py:31-56) and
+ * router_topk (src/maple_run/kernels/router.py:141-217) with the dispatch.
+ */
+size_t ma_moe_route_workspace_bytes(int64_t tokens, int64_t n_experts);
+int ma_moe_route(const void* x, const void* x_add, int64_t tokens, int64_t hidden,
+                 const void* norm_weight, int norm_dtype, float eps,
+                 const void* gate_weight, const float* router_bias,
+                 int64_t n_experts, int top_k, void* h_out, void* xn_out,
+                 int32_t* topk_ids, float* topk_weight, int32_t* counts,
+                 int32_t* offsets, int32_t* pair_ids, int32_t* inverse,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Grouped MoE FFN after dispatch (batched decode and prefill), on MFMA:
  * per expert, h = SwiGLU(up/gate GEMM) over its pairs (rounded to bf16 as the
  * reference stores it), out = down GEMM per pair (rounded to bf16), then

@@ -196,6 +196,17 @@ __device__ __forceinline__ float lane_bcast(float v, int src) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
 }
 
+// Block-wide sum over 256 threads; every thread gets the total.
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = group_sum<64>(v);
+  const int wv = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wv] = v;
+  __syncthreads();
+  const float t = red[0] + red[1] + red[2] + red[3];
+  __syncthreads();
+  return t;
+}
+
 // Nothing may be scheduled across this point: keeps every load issued above
 // it ahead of the arithmetic below (the scheduler otherwise sinks loads next
 // to their first use to save registers, serialising their latencies).

@@ -8,17 +8,6 @@
 
 namespace ma {
 
-// Block-wide sum over 256 threads; every thread gets the total.
-__device__ __forceinline__ float block_sum256(float v, float* red) {
-  v = group_sum<64>(v);
-  const int wv = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[wv] = v;
-  __syncthreads();
-  const float t = red[0] + red[1] + red[2] + red[3];
-  __syncthreads();
-  return t;
-}
-
 __global__ __launch_bounds__(256) void k_rms_norm(const void* __restrict__ x, int x_dt,
                                                   int64_t n, const void* __restrict__ w,
                                                   int w_dt, float eps, void* __restrict__ y) {

@@ -11,7 +11,9 @@ namespace ma {
 // probability, or an equal one at a lower index, so rank order is the
 // reference's descending order with ties to the lowest index.  Ranks come
 // from v_readlane broadcasts (no LDS round trips).  One full wave runs this.
-template <int PER>
+// COH: ids and weights are stored with the device-coherent policy (read by
+// another workgroup of the same launch).
+template <int PER, bool COH = false>
 __device__ __forceinline__ void softmax_topk(float (&p)[PER], int64_t n_exp, int top_k,
                                              int32_t* __restrict__ ids,
                                              float* __restrict__ wts) {
@@ -56,8 +58,14 @@ __device__ __forceinline__ void softmax_topk(float (&p)[PER], int64_t n_exp, int
   for (int i = 0; i < PER; ++i) {
     const int e = lane + 64 * i;
     if (e < n_exp && rank[i] < top_k) {
-      ids[rank[i]] = e;
-      wts[rank[i]] = p[i] * inv_total;
+      if constexpr (COH) {
+        __hip_atomic_store(&ids[rank[i]], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&wts[rank[i]], p[i] * inv_total, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        ids[rank[i]] = e;
+        wts[rank[i]] = p[i] * inv_total;
+      }
     }
   }
 }

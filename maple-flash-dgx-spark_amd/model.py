@@ -30,11 +30,11 @@ import torch
 
 from . import synthetic
 from .kernels.decode_attn import decode_attention, gqa_workspace, o_projection_supported
-from .kernels.fused_norm import add_rms_norm, rms_norm
+from .kernels.fused_norm import rms_norm
 from .kernels.greedy import greedy_argmax
 from .kernels.rtn4 import rtn4_embedding, rtn4_gemv
 from .kernels.ternary_gemv import ternary_gemv
-from .moe import fused_supported, moe_block, moe_fused
+from .moe import fused_supported, moe_fused, moe_layer
 
 
 @dataclass
@@ -176,8 +176,9 @@ class SyntheticDecoder:
             if nl is not None:
                 next_qkv = out[3]
         else:
-            hidden, mlp_in = add_rms_norm(hidden, o, L.post_ln, c.eps)
-            y, ids, _ = moe_block(mlp_in, L.moe, c.top_k, residual=hidden)
+            # add + RMSNorm + router + dispatch in one launch from 4 tokens,
+            # then the grouped experts
+            y, ids = moe_layer(hidden, L.moe, c.top_k, L.post_ln, c.eps, add=o.reshape(hidden.shape))
         if routing is not None:
             routing.append(ids)
         return y, next_qkv

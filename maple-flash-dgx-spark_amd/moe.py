@@ -130,16 +130,78 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
     return y, ids, wts
 
 
+ROUTE_MAX_TOKENS = 1024
+_ROUTE_WS: dict[tuple, torch.Tensor] = {}
+
+
+def route_supported(layer: MoELayer, top_k: int, x: torch.Tensor) -> bool:
+    """True if ``ma_moe_route`` takes these sizes and dtypes."""
+    tokens, hidden = x.reshape(-1, x.shape[-1]).shape
+    return (x.dtype == torch.bfloat16 and layer.gate_weight.dtype == torch.bfloat16
+            and 1 <= tokens <= ROUTE_MAX_TOKENS and hidden % 8 == 0 and hidden <= 4096
+            and layer.n_experts <= 256 and 1 <= top_k <= layer.n_experts)
+
+
+def route_timed_out(device: torch.device | int = 0) -> bool:
+    """True if a routing launch on ``device`` ever timed out waiting for
+    another workgroup (recorded in word 64 of its workspace).  Syncs."""
+    idx = device if isinstance(device, int) else (device.index or 0)
+    return any(int(ws[256:260].view(torch.int32).item()) != 0
+               for key, ws in _ROUTE_WS.items() if key[0] == idx)
+
+
+def moe_route(x: torch.Tensor, layer: MoELayer, top_k: int, norm_weight: torch.Tensor,
+              eps: float, add: torch.Tensor | None = None):
+    """Residual add + RMSNorm + router + dispatch in one launch for ``x [T, H]``.
+
+    Returns ``(h, xn, ids, weights, dispatch)``: ``h = x + add`` (``x`` itself
+    when ``add`` is None), ``xn = rms_norm(h) * norm_weight``, the router's
+    int32 ids / float32 weights ``[T, top_k]`` and the :class:`Dispatch` lists.
+    Equal, bit for bit, to add_rms_norm + router_topk + moe_dispatch."""
+    from .kernels.dispatch import Dispatch
+    tokens, hidden = x.shape
+    dev = x.device
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    nbytes = int(_lib.load().ma_moe_route_workspace_bytes(ROUTE_MAX_TOKENS, layer.n_experts))
+    key = (idx, layer.n_experts)
+    ws = _ROUTE_WS.get(key)
+    if ws is None:
+        ws = torch.zeros(nbytes, device=dev, dtype=torch.uint8)
+        _ROUTE_WS[key] = ws
+    xc = x.contiguous()
+    ac = None if add is None else add.reshape(tokens, hidden).contiguous()
+    h = torch.empty_like(xc) if ac is not None else xc
+    xn = torch.empty_like(xc)
+    ids = torch.empty(tokens, top_k, device=dev, dtype=torch.int32)
+    wts = torch.empty(tokens, top_k, device=dev, dtype=torch.float32)
+    n_exp = layer.n_experts
+    counts = torch.empty(n_exp, device=dev, dtype=torch.int32)
+    offsets = torch.empty(n_exp + 1, device=dev, dtype=torch.int32)
+    pair_ids = torch.empty(tokens * top_k, device=dev, dtype=torch.int32)
+    inverse = torch.empty(tokens * top_k, device=dev, dtype=torch.int32)
+    nwc = norm_weight.contiguous()
+    _lib.call(
+        "ma_moe_route",
+        _lib.ptr(xc), _lib.ptr(ac), tokens, hidden, _lib.ptr(nwc), _lib.dtype_code(nwc, "norm_weight"),
+        float(eps), _lib.ptr(layer.gate_weight), _lib.ptr(layer.router_bias), n_exp, int(top_k),
+        _lib.ptr(h) if ac is not None else None, _lib.ptr(xn), _lib.ptr(ids), _lib.ptr(wts),
+        _lib.ptr(counts), _lib.ptr(offsets), _lib.ptr(pair_ids), _lib.ptr(inverse),
+        _lib.ptr(ws), ws.numel(), _lib.stream_of(xc),
+    )
+    return h, xn, ids, wts, Dispatch(counts, offsets, pair_ids, inverse)
+
+
 def moe_grouped(x: torch.Tensor, layer: MoELayer, ids: torch.Tensor, wts: torch.Tensor,
-                residual: torch.Tensor | None = None, *, return_h: bool = False):
+                residual: torch.Tensor | None = None, *, return_h: bool = False, dispatch=None):
     """Dispatch + grouped MFMA SwiGLU/down + combine for ``x [T, H]`` (bf16).
 
+    ``dispatch``: the lists for ``ids`` if already built (``moe_route``).
     Returns ``y [T, H]`` (bf16), and with ``return_h`` also ``h [T, k, I]``.
     """
     tokens, hidden = x.shape
     top_k = int(ids.shape[-1])
     inter = layer.inter
-    d = moe_dispatch(ids, layer.n_experts)
+    d = dispatch if dispatch is not None else moe_dispatch(ids, layer.n_experts)
     n_pairs = tokens * top_k
     nbytes = int(_lib.load().ma_grouped_workspace_bytes(n_pairs, inter, hidden))
     ws = torch.empty(nbytes, device=x.device, dtype=torch.uint8)
@@ -189,6 +251,26 @@ def moe_block(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
         h = ternary_expert_swiglu(xf, layer.up_gate_packed, layer.up_gate_alpha, ids)
         y = ternary_expert_down_sum(h, layer.down_packed, layer.down_alpha, ids, wts, residual=res)
     return y.reshape(x.shape), ids, wts
+
+
+def moe_layer(hidden: torch.Tensor, layer: MoELayer, top_k: int, norm_weight: torch.Tensor,
+              eps: float, add: torch.Tensor | None = None):
+    """Post-attention half of a decoder layer for ``hidden [T, H]``:
+    ``h = hidden + add``, ``y = h + MoE(rms_norm(h) * norm_weight)``.
+    Returns ``(y, ids)``.  From GROUPED_MIN_TOKENS tokens the add, norm, router
+    and dispatch are one launch (``moe_route``) ahead of the grouped experts."""
+    from .kernels.fused_norm import add_rms_norm, rms_norm
+    tokens = hidden.shape[0]
+    if (tokens >= GROUPED_MIN_TOKENS and route_supported(layer, top_k, hidden)
+            and hidden.shape[-1] % 256 == 0 and layer.inter % 256 == 0):
+        h, xn, ids, wts, d = moe_route(hidden, layer, top_k, norm_weight, eps, add=add)
+        return moe_grouped(xn, layer, ids, wts, h, dispatch=d), ids
+    if add is not None:
+        h, xn = add_rms_norm(hidden, add, norm_weight, eps)
+    else:
+        h, xn = hidden, rms_norm(hidden, norm_weight, eps)
+    y, ids, _ = moe_block(xn, layer, top_k, residual=h)
+    return y, ids
 
 
 class MapleSparseMoeBlock:

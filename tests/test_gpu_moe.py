@@ -119,3 +119,50 @@ def test_moe_block_graph_replays_match_eager(dev, layer):
     from maple_amd.kernels.router import router_wait_timed_out
 
     assert not router_wait_timed_out(dev)
+
+
+# ---------------------------------------------------------------- one-launch routing
+@pytest.mark.parametrize("tokens,n_exp,hidden,with_add,nw_dtype,with_bias", [
+    (4, 64, 2048, True, torch.float32, False),
+    (32, 64, 2048, True, torch.bfloat16, True),
+    (33, 64, 2048, False, torch.float32, False),
+    (128, 256, 2048, True, torch.float32, True),
+    (5, 20, 4096, True, torch.bfloat16, False),
+    (1024, 64, 2048, True, torch.float32, False),
+])
+def test_moe_route_equals_separate_launches(dev, tokens, n_exp, hidden, with_add, nw_dtype, with_bias):
+    """ma_moe_route gives, bit for bit, add_rms_norm (or rms_norm) +
+    router_topk + moe_dispatch (router weights to float32 rounding where
+    router_topk's one-launch form runs); its routing matches the oracle's; the
+    workspace is left all-zero; called twice in a row (the ticket counter and
+    the tagged logits are reused)."""
+    from maple_amd.kernels import add_rms_norm, rms_norm
+    from maple_amd.moe import moe_route, route_timed_out, _ROUTE_WS
+    L = synthetic.make_moe_layer(hidden, n_exp, 256, seed=9, device=dev)
+    if with_bias:
+        L.router_bias = synthetic.zipf_router_bias(n_exp).to(dev)
+    k = min(K, n_exp)
+    x = synthetic.randn_bf16((tokens, hidden), 300 + tokens, dev)
+    add = synthetic.randn_bf16((tokens, hidden), 400 + tokens, dev) if with_add else None
+    nw = (torch.rand(hidden, device=dev) + 0.5).to(nw_dtype)
+    for call in range(2):
+        h, xn, ids, wts, d = moe_route(x, L, k, nw, 1e-6, add=add)
+        if with_add:
+            h_ref, xn_ref = add_rms_norm(x, add, nw, 1e-6)
+        else:
+            h_ref, xn_ref = x, rms_norm(x, nw, 1e-6)
+        ids_ref, wts_ref = router_topk(xn_ref, L.gate_weight, k, bias=L.router_bias)
+        d_ref = moe_dispatch(ids_ref, n_exp)
+        torch.cuda.synchronize()
+        assert torch.equal(h, h_ref) and torch.equal(xn, xn_ref), f"norm (call {call})"
+        assert torch.equal(ids, ids_ref), f"router ids (call {call})"
+        if tokens > 16:  # router_topk's two-launch form: the same float32 sums
+            assert torch.equal(wts, wts_ref), f"router weights (call {call})"
+        else:  # its one-launch form adds each logit's products in another order
+            torch.testing.assert_close(wts, wts_ref, rtol=1e-5, atol=1e-7)
+        for a, b in zip(d, d_ref):
+            assert torch.equal(a, b), f"dispatch (call {call})"
+    assert not route_timed_out(dev)
+    assert all(int(ws.count_nonzero()) == 0 for ws in _ROUTE_WS.values())
+    if tokens <= 128:
+        _check_routing(xn, L, ids, wts, k)
