@@ -189,7 +189,9 @@ int ma_rtn4_embedding(const void* ids, int ids_is_int64, int64_t n_ids,
 
 /*
  * Batched MoE routing in ONE launch: h = x + x_add (bf16; skipped when x_add
- * is NULL, then h is x), xn = RMSNorm(h) * norm_weight (bf16), the router
+ * is NULL, then h is x), xn = RMSNorm(h) * norm_weight (bf16) -- with xn_pairs
+ * / xn_corr (optional, both or neither; hidden % 16 == 0) also xn in the x'
+ * pair form ma_moe_grouped reads and each token's correction -- the router
  * (logits = xn @ gate_weight^T + router_bias, softmax, top_k ids / weights)
  * and the dispatch lists (counts, offsets, pair_ids, inverse as
  * ma_moe_dispatch gives them).  Same values, bit for bit, as ma_add_rms_norm
@@ -207,6 +209,7 @@ int ma_moe_route(const void* x, const void* x_add, int64_t tokens, int64_t hidde
                  const void* norm_weight, int norm_dtype, float eps,
                  const void* gate_weight, const float* router_bias,
                  int64_t n_experts, int top_k, void* h_out, void* xn_out,
+                 uint32_t* xn_pairs, float* xn_corr,
                  int32_t* topk_ids, float* topk_weight, int32_t* counts,
                  int32_t* offsets, int32_t* pair_ids, int32_t* inverse,
                  void* workspace, size_t workspace_bytes, void* stream);
@@ -221,12 +224,17 @@ int ma_moe_route(const void* x, const void* x_add, int64_t tokens, int64_t hidde
  * or float32.  h_out (optional, bf16 [tokens*top_k, inter], row stride ldh)
  * receives h in slot order; y (optional) is bf16 [tokens, hidden].
  * workspace: ma_grouped_workspace_bytes(tokens * top_k, inter, hidden).
+ * x_pairs / x_corr (optional, both or neither): x as ma_moe_route writes it
+ * in x' pair form (uint32 [tokens, hidden / 2]) with each token's correction
+ * (float32 [tokens]); decode batches then read the operands from there
+ * instead of building them from x (x is still passed).
  * Replaces MapleSparseMoeBlock's SwiGLU -> down -> moe_reduce_add chain
  * (src/maple_run/model.py:468-473) for token counts where experts see many
  * tokens; the reference instead runs one program per (token, slot).
  */
 size_t ma_grouped_workspace_bytes(int64_t n_pairs, int64_t inter, int64_t hidden);
-int ma_moe_grouped(const void* x, int64_t ldx, int64_t tokens, int64_t top_k,
+int ma_moe_grouped(const void* x, int64_t ldx, const uint32_t* x_pairs, const float* x_corr,
+                   int64_t tokens, int64_t top_k,
                    const uint32_t* up_gate, const void* up_gate_alpha,
                    const uint32_t* down, const void* down_alpha, int alpha_dtype,
                    int64_t n_experts, int64_t hidden, int64_t inter,

@@ -56,10 +56,10 @@ _SIGNATURES = {
     "ma_moe_fused_timed_out": [_P, _P, _P],
     "ma_moe_route_workspace_bytes": [_L, _L],
     "ma_moe_route": [_P, _P, _L, _L, _P, _I, _F, _P, _P, _L, _I, _P, _P, _P, _P, _P, _P, _P, _P,
-                     _P, _Z, _P],
+                     _P, _P, _P, _Z, _P],
     "ma_argmax_rows": [_P, _I, _L, _L, _L, _P, _P],
-    "ma_moe_grouped": [_P, _L, _L, _L, _P, _P, _P, _P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _I,
-                       _P, _L, _P, _P, _Z, _P],
+    "ma_moe_grouped": [_P, _L, _P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _L, _L, _P, _P, _P, _P, _P,
+                       _I, _P, _L, _P, _P, _Z, _P],
 }
 _RESTYPES = {"ma_last_error": ctypes.c_char_p, "ma_router_workspace_bytes": _Z,
              "ma_ternary_gemv_workspace_bytes": _Z,

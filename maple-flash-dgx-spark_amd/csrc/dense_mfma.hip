@@ -20,50 +20,9 @@
 // x' = 16 x pairs staged in LDS; after each RTN group C is folded into the
 // output as s_g (C - 16 X_g) + b_g X_g (X_g = sum of x over the group) and
 // cleared.
-#include "common.h"
+#include "mfma.h"
 
 namespace ma {
-
-typedef __bf16 bf16x8d_t __attribute__((ext_vector_type(8)));
-typedef float f32x4d_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ f32x4d_t mfma16(uint4 a, uint4 b, f32x4d_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8d_t, a),
-                                                 __builtin_bit_cast(bf16x8d_t, b), c, 0, 0, 0);
-}
-
-__device__ __forceinline__ f32x4d_t mfma16v(u32x4v_t a, u32x4v_t b, f32x4d_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8d_t, a),
-                                                 __builtin_bit_cast(bf16x8d_t, b), c, 0, 0, 0);
-}
-
-// Operand discipline of the K-split GEMMs: a step's A and B operands are all
-// built before its MFMAs issue and are kept live (empty asm uses that also
-// read the accumulators, so they sit after the MFMAs' results) until the
-// step's MFMAs are done.  No register an MFMA reads is then reused for another
-// value -- VALU result, load or MFMA result -- while that MFMA may still be
-// reading it.  When the compiler was left free to reuse those registers (an
-// MFMA result in its own B registers, a following instruction's result in the
-// previous MFMA's operands), this instruction gave wrong sums on gfx950.
-template <int NA>
-__device__ __forceinline__ void keep_b(const u32x4v_t& b, const f32x4d_t (&acc)[NA]) {
-  asm volatile("" ::"v"(b), "v"(acc[0]), "v"(acc[NA - 1]));
-}
-template <typename T, int M, int NA>
-__device__ __forceinline__ void keep_b(const T (&b)[M], const f32x4d_t (&acc)[NA]) {
-#pragma unroll
-  for (int i = 0; i < M; ++i) keep_b(b[i], acc);
-}
-
-template <int N, int M, typename T, int NA>
-__device__ __forceinline__ void keep_operands(const u32x4v_t (&av)[N][2], const T (&bv)[M],
-                                              const f32x4d_t (&acc)[NA]) {
-#pragma unroll
-  for (int i = 0; i < N; ++i)
-    asm volatile("" ::"v"(av[i][0]), "v"(av[i][1]), "v"(acc[0]), "v"(acc[NA - 1]));
-  keep_b(bv, acc);
-}
 
 constexpr int kDenseChunk = 16;  // words of K per step
 constexpr int kDenseRows = 128;  // rows per workgroup (4 waves x 2 x 16)
@@ -222,6 +181,7 @@ __global__ __launch_bounds__(64 * KW) void k_tgemm_xpk(const uint4* __restrict__
       av[q][0] = u32x4v_t{ex[0], ex[1], ex[2], ex[3]};
       av[q][1] = u32x4v_t{ex[4], ex[5], ex[6], ex[7]};
     }
+    mfma_block_begin();
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -230,7 +190,8 @@ __global__ __launch_bounds__(64 * KW) void k_tgemm_xpk(const uint4* __restrict__
         for (int vv = 0; vv < NV; ++vv)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb)
-            acc[nb] = mfma16v(av[q][hf], bf[((q * 2 + hf) * NV + vv) * NB + nb], acc[nb]);
+            mfma_acc(acc[nb], av[q][hf], bf[((q * 2 + hf) * NV + vv) * NB + nb]);
+    mfma_block_end();
     keep_operands(av, bf, acc);
   }
 #pragma unroll
@@ -391,6 +352,12 @@ __global__ __launch_bounds__(64 * KW) void k_tgemm_ks(
         }
       }
 #pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        pin(cp[nb]);
+        pin(sp[nb]);
+      }
+      mfma_block_begin();
+#pragma unroll
       for (int qi = 0; qi < 2; ++qi)
 #pragma unroll
         for (int vv = 0; vv < NV; ++vv)
@@ -398,7 +365,8 @@ __global__ __launch_bounds__(64 * KW) void k_tgemm_ks(
           for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
-              acc[nb] = mfma16v(av[qi][hf], bv[qi][nb][vv][hf], acc[nb]);
+              mfma_acc(acc[nb], av[qi][hf], bv[qi][nb][vv][hf]);
+      mfma_block_end();
       keep_operands(av, bv, acc);
     }
   }

@@ -25,7 +25,7 @@
 // pair's down output rounded to bf16 (ternary_expert.py:208); a gather
 // kernel then forms y[t] = sum_j w[t,j] out[pair(t,j)] (+ residual) in
 // float32 (fused_norm.py:83-96).
-#include "common.h"
+#include "mfma.h"
 
 namespace ma {
 
@@ -351,6 +351,501 @@ __global__ __launch_bounds__(256) void k_grouped_down(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode form (few pairs per expert): 16-pair tiles, K split over the KW waves
+// of a workgroup, each wave's operands loaded and built in registers (no LDS
+// staging) and the partial tiles added in wave order through LDS; with a
+// handful of tokens per expert, a K walk per workgroup left the chip idle.
+// Same per-word arithmetic as the kernels above; every sum has a fixed order.
+// ---------------------------------------------------------------------------
+
+// SwiGLU stage: a workgroup takes 16 MBH intermediate rows (MBH 16-row blocks
+// of up rows and the matching gate rows) of one 16-pair tile; wave w takes the
+// 16-word chunks w, w + KW, ... of K.  PAIRS: the activations arrive as x'
+// pairs with their per-token correction (x_pairs, x_corr: built once per
+// token upstream) and are loaded as B operands directly; otherwise each lane
+// builds its B operands from x.
+template <int MBH, int ADT, int KW, bool PAIRS>
+__global__ __launch_bounds__(64 * KW) void k_grouped_swiglu_ks(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint32_t* __restrict__ x_pairs,
+    const float* __restrict__ x_corr, int64_t topk,
+    const uint32_t* __restrict__ w, int64_t n_half, int64_t nwords,
+    const void* __restrict__ alpha, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ pair_ids, int n_exp,
+    uint16_t* __restrict__ hp, uint16_t* __restrict__ h, int64_t ldh) {
+  constexpr int MB = 2 * MBH;  // row blocks: up 0 .. MBH-1, gate MBH .. MB-1
+  static_assert(KW >= MBH, "the epilogue takes 64 threads per up block");
+  __shared__ float red[KW][MB][4][64];
+  __shared__ float red_c[KW][4][16];
+  int e, pos0, np;
+  if (!decode_tile(offsets, n_exp, blockIdx.y, 16, e, pos0, np)) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * 16 * MBH;
+  const uint32_t* we = w + static_cast<int64_t>(e) * (2 * n_half) * nwords;
+  const uint32_t* rowp[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    int64_t i = i0 + 16 * (mb % MBH) + r16;
+    i = i < n_half ? i : n_half - 1;
+    rowp[mb] = we + (i + (mb / MBH) * n_half) * nwords + 4 * g;
+  }
+  // this lane's B column: pair pos0 + r16 (token row of x), zero past np
+  const bool valid = r16 < np;
+  const int64_t tok = valid ? pair_ids[pos0 + r16] / topk : 0;
+  const uint16_t* xrow = x + tok * ldx + 64 * g;
+  const uint32_t* prow = x_pairs + (tok * nwords + 4 * g) * 8;
+  f32x4d_t acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+  float cp = 0.f;
+  const ExpandConsts kc;
+  for (int64_t c0 = 16 * wv; c0 < nwords; c0 += 16 * KW) {
+    u32x4v_t wq[MB], xv[4][2];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) wq[mb] = *reinterpret_cast<const u32x4v_t*>(rowp[mb] + c0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4v_t* src = PAIRS ? reinterpret_cast<const u32x4v_t*>(prow + (c0 + q) * 8)
+                                  : reinterpret_cast<const u32x4v_t*>(xrow + (c0 + q) * 16);
+      xv[q][0] = src[0];
+      xv[q][1] = src[1];
+    }
+    MA_ISSUE_FENCE();  // every load of the chunk in flight before the first use
+#pragma unroll
+    for (int qh = 0; qh < 4; qh += 2) {  // two words per step (operand registers)
+      u32x4v_t av[2][MB][2], bv[2][2];
+#pragma unroll
+      for (int qi = 0; qi < 2; ++qi) {
+        const int q = qh + qi;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          uint32_t ex[8];
+          expand_word(wq[mb][q], ex, kc);
+          av[qi][mb][0] = u32x4v_t{ex[0], ex[1], ex[2], ex[3]};
+          av[qi][mb][1] = u32x4v_t{ex[4], ex[5], ex[6], ex[7]};
+        }
+        if constexpr (PAIRS) {
+          bv[qi][0] = valid ? xv[q][0] : u32x4v_t{0u, 0u, 0u, 0u};
+          bv[qi][1] = valid ? xv[q][1] : u32x4v_t{0u, 0u, 0u, 0u};
+        } else {
+          uint32_t pr[8];
+          const float c = x16_to_pairs(make_uint4(xv[q][0].x, xv[q][0].y, xv[q][0].z, xv[q][0].w),
+                                       make_uint4(xv[q][1].x, xv[q][1].y, xv[q][1].z, xv[q][1].w), pr);
+          cp += valid ? c : 0.f;
+          bv[qi][0] = valid ? u32x4v_t{pr[0], pr[1], pr[2], pr[3]} : u32x4v_t{0u, 0u, 0u, 0u};
+          bv[qi][1] = valid ? u32x4v_t{pr[4], pr[5], pr[6], pr[7]} : u32x4v_t{0u, 0u, 0u, 0u};
+        }
+      }
+      pin(cp);
+      mfma_block_begin();
+#pragma unroll
+      for (int qi = 0; qi < 2; ++qi)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) mfma_acc(acc[mb], av[qi][mb][hf], bv[qi][hf]);
+      mfma_block_end();
+      keep_b(av, acc);
+      keep_b(bv, acc);
+    }
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wv][mb][r][lane] = acc[mb][r];
+  if constexpr (!PAIRS) red_c[wv][g][r16] = cp;
+  __syncthreads();
+  // Thread t < 64 MBH: pair column col = t % 16, rows 4 rq .. +3 of up block mbu.
+  if (tid >= 64 * MBH) return;
+  const int col = tid & 15, rq = (tid >> 4) & 3, mbu = tid >> 6;
+  if (col >= np) return;
+  const int pid = pair_ids[pos0 + col];
+  float c = 0.f;
+  if constexpr (PAIRS) {
+    c = x_corr[pid / topk];
+  } else {
+#pragma unroll
+    for (int k = 0; k < KW; ++k)
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg) c += red_c[k][gg][col];
+  }
+  const int ln = col + 16 * rq;
+  const int64_t nwh = n_half / 16;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t i = i0 + 16 * mbu + 4 * rq + r;
+    if (i >= n_half) continue;
+    float su = 0.f, sg = 0.f;
+#pragma unroll
+    for (int k = 0; k < KW; ++k) {
+      su += red[k][mbu][r][ln];
+      sg += red[k][mbu + MBH][r][ln];
+    }
+    const float au = ld_t<ADT>(alpha, static_cast<int64_t>(e) * 2 * n_half + i);
+    const float ag = ld_t<ADT>(alpha, static_cast<int64_t>(e) * 2 * n_half + n_half + i);
+    const uint16_t hb = f32_to_bf16(swiglu_act(au * (su - c), ag * (sg - c)));
+    if (hp) {
+      const int pos = static_cast<int>(i & 15), j = pos & 7, hh = pos >> 3;
+      const float hv = bf16_to_f32(hb) * pair_scale(j);  // exact: power-of-two scale
+      hp[((static_cast<int64_t>(pos0 + col) * nwh + (i >> 4)) * 8 + j) * 2 + hh] =
+          static_cast<uint16_t>(bf16_bits_exact(hv));
+    }
+    if (h) h[static_cast<int64_t>(pid) * ldh + i] = hb;
+  }
+}
+
+// Down stage: a workgroup takes 16 MB output rows of one 16-pair tile; wave w
+// takes the 4 QW-word chunks w, w + KW, ... of K (QW words per lane), reading
+// h's x' pairs straight from the pair-format buffer.
+template <int MB, int ADT, int KW, int QW>
+__global__ __launch_bounds__(64 * KW) void k_grouped_down_ks(
+    const uint32_t* __restrict__ hp, const uint32_t* __restrict__ w, int64_t n_out,
+    int64_t nwk, const void* __restrict__ alpha, const int32_t* __restrict__ offsets,
+    int n_exp, uint16_t* __restrict__ out) {
+  constexpr int CW = 4 * QW;  // words per chunk
+  static_assert(KW >= MB, "the epilogue takes 64 threads per row block");
+  __shared__ float red[KW][MB][4][64];
+  __shared__ float red_c[KW][4][16];
+  int e, pos0, np;
+  if (!decode_tile(offsets, n_exp, blockIdx.y, 16, e, pos0, np)) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16 * MB;
+  const uint32_t* we = w + static_cast<int64_t>(e) * n_out * nwk;
+  const uint32_t* rowp[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    int64_t n = n0 + 16 * mb + r16;
+    n = n < n_out ? n : n_out - 1;
+    rowp[mb] = we + n * nwk + QW * g;
+  }
+  const bool valid = r16 < np;
+  const uint32_t* hrow = hp + static_cast<int64_t>(pos0 + (valid ? r16 : 0)) * nwk * 8 + QW * g * 8;
+  f32x4d_t acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+  float cp = 0.f;
+  const ExpandConsts kc;
+  for (int64_t c0 = CW * wv; c0 < nwk; c0 += CW * KW) {
+    uint32_t wq[MB][QW];
+    u32x4v_t bv[QW][2];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      if constexpr (QW == 2) {
+        const uint2 v2 = *reinterpret_cast<const uint2*>(rowp[mb] + c0);
+        wq[mb][0] = v2.x;
+        wq[mb][1] = v2.y;
+      } else {
+#pragma unroll
+        for (int q = 0; q < QW; ++q) wq[mb][q] = rowp[mb][c0 + q];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < QW; ++q) {
+      const u32x4v_t* src = reinterpret_cast<const u32x4v_t*>(hrow + (c0 + q) * 8);
+      bv[q][0] = src[0];
+      bv[q][1] = src[1];
+    }
+    MA_ISSUE_FENCE();  // every load of the chunk in flight before the first use
+#pragma unroll
+    for (int q = 0; q < QW; ++q) {  // one word per step (operand registers)
+      u32x4v_t av[MB][2];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        uint32_t ex[8];
+        expand_word(wq[mb][q], ex, kc);
+        av[mb][0] = u32x4v_t{ex[0], ex[1], ex[2], ex[3]};
+        av[mb][1] = u32x4v_t{ex[4], ex[5], ex[6], ex[7]};
+      }
+      if (!valid) bv[q][0] = bv[q][1] = u32x4v_t{0u, 0u, 0u, 0u};
+      const uint32_t pr[8] = {bv[q][0].x, bv[q][0].y, bv[q][0].z, bv[q][0].w,
+                              bv[q][1].x, bv[q][1].y, bv[q][1].z, bv[q][1].w};
+      cp += pairs_cst(pr);
+      pin(cp);
+      mfma_block_begin();
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) mfma_acc(acc[mb], av[mb][hf], bv[q][hf]);
+      mfma_block_end();
+      keep_b(av, acc);
+      keep_b(bv[q], acc);
+    }
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wv][mb][r][lane] = acc[mb][r];
+  red_c[wv][g][r16] = cp;
+  __syncthreads();
+  // Thread t < 64 MB: pair column col = t % 16, rows 4 rq .. +3 of block mb.
+  if (tid >= 64 * MB) return;
+  const int col = tid & 15, rq = (tid >> 4) & 3, mb = tid >> 6;
+  if (col >= np) return;
+  float c = 0.f;
+#pragma unroll
+  for (int k = 0; k < KW; ++k)
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg) c += red_c[k][gg][col];
+  const int ln = col + 16 * rq;
+  const int64_t nb0 = n0 + 16 * mb + 4 * rq;
+  float o[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < KW; ++k) s += red[k][mb][r][ln];
+    const int64_t n = nb0 + r < n_out ? nb0 + r : n_out - 1;
+    o[r] = ld_t<ADT>(alpha, static_cast<int64_t>(e) * n_out + n) * (s - c);
+  }
+  uint16_t* orow = out + static_cast<int64_t>(pos0 + col) * n_out;
+  if (nb0 + 3 < n_out) {
+    uint2 rr;
+    rr.x = pack_bf16x2_rn(o[0], o[1]);
+    rr.y = pack_bf16x2_rn(o[2], o[3]);
+    *reinterpret_cast<uint2*>(orow + nb0) = rr;
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (nb0 + r < n_out) orow[nb0 + r] = f32_to_bf16(o[r]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode form, tile-resident: a workgroup stages its 16-pair tile's B operands
+// for all of K in LDS once (one sync), then each wave takes whole 16-row
+// blocks over all of K: a block's weights for the full K are loaded up front
+// (8 words per lane at K = 2048 ... per chunk of 16 words one uint4), so a
+// wave keeps all its weight bytes in flight at once and needs no cross-wave
+// reduction.  Same per-word arithmetic as the kernels above; each output is
+// one MFMA chain (fixed order).
+// ---------------------------------------------------------------------------
+constexpr int kErWaves = 8;
+// K of the tile-resident forms, in 256-code chunks (instantiated for the
+// synthetic model's hidden 2048 and intermediate 768; other sizes take the
+// K-split forms).
+constexpr int kErChunksUp = 8, kErChunksDown = 3;
+
+// SwiGLU: BPW up blocks (and the matching gate blocks) per wave; x' pairs of
+// the tile's tokens (x_pairs [T, K / 2] uint32, x_corr [T]) staged in LDS.
+template <int BPW, int ADT, int NCH>
+__global__ __launch_bounds__(64 * kErWaves) void k_grouped_swiglu_er(
+    const uint32_t* __restrict__ x_pairs, const float* __restrict__ x_corr, int64_t topk,
+    const uint32_t* __restrict__ w, int64_t n_half, const void* __restrict__ alpha,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ pair_ids, int n_exp,
+    uint16_t* __restrict__ hp, uint16_t* __restrict__ h, int64_t ldh) {
+  constexpr int NW = 16 * NCH;  // words of K
+  __shared__ u32x4v_t xs[NW][2][16];
+  __shared__ int32_t s_pid[16], s_tok[16];
+  __shared__ float s_c[16];
+  int e, pos0, np;
+  if (!decode_tile(offsets, n_exp, blockIdx.y, 16, e, pos0, np)) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t nblk = n_half / 16;
+  const int64_t b0 = (static_cast<int64_t>(blockIdx.x) * kErWaves + wv) * BPW;  // first up block
+  const uint32_t* we = w + static_cast<int64_t>(e) * (2 * n_half) * NW;
+  // weights of this wave's blocks for all of K, issued first
+  u32x4v_t wq[2 * BPW][NCH];
+#pragma unroll
+  for (int j = 0; j < 2 * BPW; ++j) {
+    int64_t blk = b0 + (j % BPW);
+    blk = blk < nblk ? blk : nblk - 1;
+    const uint32_t* rp = we + ((j / BPW) * n_half + blk * 16 + r16) * NW + 4 * g;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) wq[j][c] = *reinterpret_cast<const u32x4v_t*>(rp + 16 * c);
+  }
+  if (tid < 16) {
+    const int p = tid < np ? pair_ids[pos0 + tid] : -1;
+    s_pid[tid] = p;
+    s_tok[tid] = p >= 0 ? static_cast<int>(p / topk) : -1;
+  }
+  __syncthreads();
+  if (tid < 16) s_c[tid] = s_tok[tid] >= 0 ? x_corr[s_tok[tid]] : 0.f;
+  // stage the tile's x' pairs: item = (col, word, half), 16-byte loads, all
+  // issued before the first LDS store
+  constexpr int kItems = 16 * NW * 2, kPer = (kItems + 64 * kErWaves - 1) / (64 * kErWaves);
+  u32x4v_t sv[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int it = tid + 64 * kErWaves * k;
+    const int col = (it < kItems ? it : 0) / (NW * 2), rem = it % (NW * 2);
+    const int tk = s_tok[col];
+    sv[k] = u32x4v_t{0u, 0u, 0u, 0u};
+    if (it < kItems && tk >= 0)
+      sv[k] = *reinterpret_cast<const u32x4v_t*>(x_pairs + static_cast<int64_t>(tk) * (NW * 8) + rem * 4);
+  }
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int it = tid + 64 * kErWaves * k;
+    if (it < kItems) xs[(it % (NW * 2)) >> 1][it & 1][it / (NW * 2)] = sv[k];
+  }
+  __syncthreads();
+  f32x4d_t acc[2 * BPW];
+#pragma unroll
+  for (int j = 0; j < 2 * BPW; ++j) acc[j] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+  const ExpandConsts kc;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {  // one word per step (operand registers)
+      u32x4v_t av[2 * BPW][2], bv[2];
+#pragma unroll
+      for (int j = 0; j < 2 * BPW; ++j) {
+        uint32_t ex[8];
+        expand_word(wq[j][c][q], ex, kc);
+        av[j][0] = u32x4v_t{ex[0], ex[1], ex[2], ex[3]};
+        av[j][1] = u32x4v_t{ex[4], ex[5], ex[6], ex[7]};
+      }
+      bv[0] = xs[16 * c + 4 * g + q][0][r16];
+      bv[1] = xs[16 * c + 4 * g + q][1][r16];
+      mfma_block_begin();
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int j = 0; j < 2 * BPW; ++j) mfma_acc(acc[j], av[j][hf], bv[hf]);
+      mfma_block_end();
+      keep_b(av, acc);
+      keep_b(bv, acc);
+    }
+  }
+  // Epilogue: lane holds pair column r16, rows 4 g .. +3 of each block.
+  if (r16 >= np) return;
+  const float cc = s_c[r16];
+  const int pid = s_pid[r16];
+  const int64_t nwh = n_half / 16;
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) {
+    const int64_t blk = b0 + j;
+    if (blk >= nblk) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t i = blk * 16 + 4 * g + r;
+      const float au = ld_t<ADT>(alpha, static_cast<int64_t>(e) * 2 * n_half + i);
+      const float ag = ld_t<ADT>(alpha, static_cast<int64_t>(e) * 2 * n_half + n_half + i);
+      const uint16_t hb = f32_to_bf16(swiglu_act(au * (acc[j][r] - cc), ag * (acc[BPW + j][r] - cc)));
+      if (hp) {
+        const int pos = static_cast<int>(i & 15), jj = pos & 7, hh = pos >> 3;
+        const float hv = bf16_to_f32(hb) * pair_scale(jj);  // exact: power-of-two scale
+        hp[((static_cast<int64_t>(pos0 + r16) * nwh + (i >> 4)) * 8 + jj) * 2 + hh] =
+            static_cast<uint16_t>(bf16_bits_exact(hv));
+      }
+      if (h) h[static_cast<int64_t>(pid) * ldh + i] = hb;
+    }
+  }
+}
+
+// Down: BPW output blocks per wave; h's x' pairs of the tile (hp rows pos0 ..)
+// staged in LDS with each pair's correction.
+template <int BPW, int ADT, int NCH>
+__global__ __launch_bounds__(64 * kErWaves) void k_grouped_down_er(
+    const uint32_t* __restrict__ hp, const uint32_t* __restrict__ w, int64_t n_out,
+    const void* __restrict__ alpha, const int32_t* __restrict__ offsets, int n_exp,
+    uint16_t* __restrict__ out) {
+  constexpr int NW = 16 * NCH;  // words of K
+  __shared__ u32x4v_t xs[NW][2][16];
+  __shared__ float s_cw[16][NW];
+  __shared__ float s_c[16];
+  int e, pos0, np;
+  if (!decode_tile(offsets, n_exp, blockIdx.y, 16, e, pos0, np)) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t nblk = n_out / 16;
+  const int64_t b0 = (static_cast<int64_t>(blockIdx.x) * kErWaves + wv) * BPW;
+  const uint32_t* we = w + static_cast<int64_t>(e) * n_out * NW;
+  u32x4v_t wq[BPW][NCH];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) {
+    int64_t blk = b0 + j;
+    blk = blk < nblk ? blk : nblk - 1;
+    const uint32_t* rp = we + (blk * 16 + r16) * NW + 4 * g;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) wq[j][c] = *reinterpret_cast<const u32x4v_t*>(rp + 16 * c);
+  }
+  // stage: item = (col, word): both halves of the word and its correction,
+  // all loads issued before the first LDS store
+  constexpr int kItems = 16 * NW, kPer = (kItems + 64 * kErWaves - 1) / (64 * kErWaves);
+  u32x4v_t sv[kPer][2];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int it = tid + 64 * kErWaves * k;
+    const int col = it / NW, wd = it % NW;
+    sv[k][0] = sv[k][1] = u32x4v_t{0u, 0u, 0u, 0u};
+    if (it < kItems && col < np) {
+      const u32x4v_t* src = reinterpret_cast<const u32x4v_t*>(hp + (static_cast<int64_t>(pos0 + col) * NW + wd) * 8);
+      sv[k][0] = src[0];
+      sv[k][1] = src[1];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int it = tid + 64 * kErWaves * k;
+    if (it >= kItems) continue;
+    const int col = it / NW, wd = it % NW;
+    xs[wd][0][col] = sv[k][0];
+    xs[wd][1][col] = sv[k][1];
+    const uint32_t pr[8] = {sv[k][0].x, sv[k][0].y, sv[k][0].z, sv[k][0].w,
+                            sv[k][1].x, sv[k][1].y, sv[k][1].z, sv[k][1].w};
+    s_cw[col][wd] = pairs_cst(pr);
+  }
+  __syncthreads();
+  if (tid < 16) {  // fixed order
+    float c = 0.f;
+    for (int wd = 0; wd < NW; ++wd) c += s_cw[tid][wd];
+    s_c[tid] = c;
+  }
+  f32x4d_t acc[BPW];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) acc[j] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+  const ExpandConsts kc;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      u32x4v_t av[BPW][2], bv[2];
+#pragma unroll
+      for (int j = 0; j < BPW; ++j) {
+        uint32_t ex[8];
+        expand_word(wq[j][c][q], ex, kc);
+        av[j][0] = u32x4v_t{ex[0], ex[1], ex[2], ex[3]};
+        av[j][1] = u32x4v_t{ex[4], ex[5], ex[6], ex[7]};
+      }
+      bv[0] = xs[16 * c + 4 * g + q][0][r16];
+      bv[1] = xs[16 * c + 4 * g + q][1][r16];
+      mfma_block_begin();
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int j = 0; j < BPW; ++j) mfma_acc(acc[j], av[j][hf], bv[hf]);
+      mfma_block_end();
+      keep_b(av, acc);
+      keep_b(bv, acc);
+    }
+  }
+  __syncthreads();  // s_c
+  if (r16 >= np) return;
+  const float cc = s_c[r16];
+  uint16_t* orow = out + static_cast<int64_t>(pos0 + r16) * n_out;
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) {
+    const int64_t blk = b0 + j;
+    if (blk >= nblk) continue;
+    const int64_t n0 = blk * 16 + 4 * g;
+    float o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = ld_t<ADT>(alpha, static_cast<int64_t>(e) * n_out + n0 + r) * (acc[j][r] - cc);
+    uint2 rr;
+    rr.x = pack_bf16x2_rn(o[0], o[1]);
+    rr.y = pack_bf16x2_rn(o[2], o[3]);
+    *reinterpret_cast<uint2*>(orow + n0) = rr;
+  }
+}
+
 // y[t, n] = sum_j w[t, j] * out[inverse[t*k + j], n] (+ residual), float32 sum.
 __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ out,
                                                  const int32_t* __restrict__ inverse,
@@ -379,6 +874,10 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ ou
 
 using namespace ma;
 
+// Up to this many pairs per expert on average (decode batches) the K-split
+// kernels run; above it (prefill) the LDS-staged tiles of up to 64 pairs.
+constexpr int64_t kKsMaxPairsPerExpert = 16;
+
 static int grouped_nb(int64_t n_pairs, int64_t n_exp) {
   const int64_t per = n_pairs / (n_exp > 0 ? n_exp : 1);
   return per >= 48 ? 4 : (per >= 24 ? 2 : 1);
@@ -389,7 +888,8 @@ extern "C" size_t ma_grouped_workspace_bytes(int64_t n_pairs, int64_t inter, int
   return static_cast<size_t>(n_pairs) * (inter + hidden) * 2 + 256;
 }
 
-extern "C" int ma_moe_grouped(const void* x, int64_t ldx, int64_t tokens, int64_t top_k,
+extern "C" int ma_moe_grouped(const void* x, int64_t ldx, const uint32_t* x_pairs,
+                              const float* x_corr, int64_t tokens, int64_t top_k,
                               const uint32_t* up_gate, const void* up_gate_alpha,
                               const uint32_t* down, const void* down_alpha, int alpha_dtype,
                               int64_t n_experts, int64_t hidden, int64_t inter,
@@ -413,14 +913,46 @@ extern "C" int ma_moe_grouped(const void* x, int64_t ldx, int64_t tokens, int64_
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint16_t* hp = static_cast<uint16_t*>(workspace);
   uint16_t* out = hp + n_pairs * inter;
+  const int ne = static_cast<int>(n_experts);
+  const auto* xb = static_cast<const uint16_t*>(x);
+  auto* hb = static_cast<uint16_t*>(h_out);
+  if (n_pairs <= kKsMaxPairsPerExpert * n_experts) {
+    // decode: 16-pair tiles, K split over the waves of a workgroup
+    const unsigned max_tiles = static_cast<unsigned>(n_pairs / 16 + n_experts);
+    dim3 g1(static_cast<unsigned>(cdiv(inter, 32)), max_tiles);
+    dim3 g2(static_cast<unsigned>(cdiv(hidden, 64)), max_tiles);
+    // tile-resident forms: 16 rows (up + gate) / 32 rows per wave
+    dim3 ge1(static_cast<unsigned>(cdiv(inter, 16 * kErWaves)), max_tiles);
+    dim3 ge2(static_cast<unsigned>(cdiv(hidden, 32 * kErWaves)), max_tiles);
+#define MA_GROUPED_KS(ADT)                                                                       \
+  if (x_pairs && hidden == 16 * 16 * kErChunksUp)                                                \
+    hipLaunchKernelGGL((k_grouped_swiglu_er<1, ADT, kErChunksUp>), ge1, dim3(64 * kErWaves), 0,  \
+                       s, x_pairs, x_corr, top_k, up_gate, inter, up_gate_alpha, offsets,        \
+                       pair_ids, ne, hp, hb, ldh);                                               \
+  else if (x_pairs)                                                                              \
+    hipLaunchKernelGGL((k_grouped_swiglu_ks<2, ADT, 8, true>), g1, dim3(512), 0, s, xb, ldx,     \
+                       x_pairs, x_corr, top_k, up_gate, inter, hidden / 16, up_gate_alpha,      \
+                       offsets, pair_ids, ne, hp, hb, ldh);                                      \
+  else                                                                                           \
+    hipLaunchKernelGGL((k_grouped_swiglu_ks<2, ADT, 8, false>), g1, dim3(512), 0, s, xb, ldx,    \
+                       x_pairs, x_corr, top_k, up_gate, inter, hidden / 16, up_gate_alpha,      \
+                       offsets, pair_ids, ne, hp, hb, ldh);                                      \
+  if (inter == 16 * 16 * kErChunksDown)                                                          \
+    hipLaunchKernelGGL((k_grouped_down_er<2, ADT, kErChunksDown>), ge2, dim3(64 * kErWaves), 0,  \
+                       s, reinterpret_cast<const uint32_t*>(hp), down, hidden, down_alpha,       \
+                       offsets, ne, out);                                                        \
+  else                                                                                           \
+    hipLaunchKernelGGL((k_grouped_down_ks<4, ADT, 8, 2>), g2, dim3(512), 0, s,                   \
+                       reinterpret_cast<const uint32_t*>(hp), down, hidden, inter / 16,          \
+                       down_alpha, offsets, ne, out);
+    if (alpha_dtype == MA_BF16) { MA_GROUPED_KS(MA_BF16) } else { MA_GROUPED_KS(MA_F32) }
+#undef MA_GROUPED_KS
+  } else {
   const int nb = grouped_nb(n_pairs, n_experts);
   const int nt = 16 * nb;
   const unsigned max_tiles = static_cast<unsigned>(n_pairs / nt + n_experts);
-  const int ne = static_cast<int>(n_experts);
   dim3 g1(static_cast<unsigned>(cdiv(inter, 128)), max_tiles);
   dim3 g2(static_cast<unsigned>(cdiv(hidden, 256)), max_tiles);
-  const auto* xb = static_cast<const uint16_t*>(x);
-  auto* hb = static_cast<uint16_t*>(h_out);
 #define MA_GROUPED(NB, ADT)                                                                      \
   hipLaunchKernelGGL((k_grouped_swiglu<NB, ADT>), g1, dim3(256), 0, s, xb, ldx, top_k, up_gate,  \
                      inter, hidden / 16, up_gate_alpha, offsets, pair_ids, ne, hp, hb, ldh);     \
@@ -433,6 +965,7 @@ extern "C" int ma_moe_grouped(const void* x, int64_t ldx, int64_t tokens, int64_
     if (nb == 4) { MA_GROUPED(4, MA_F32) } else if (nb == 2) { MA_GROUPED(2, MA_F32) } else { MA_GROUPED(1, MA_F32) }
   }
 #undef MA_GROUPED
+  }
   if (y) {
     dim3 g3(static_cast<unsigned>(cdiv(hidden, 512)), static_cast<unsigned>(tokens));
     hipLaunchKernelGGL(k_combine, g3, dim3(256), 0, s, out, inverse, topk_weight, top_k, hidden,

@@ -41,9 +41,10 @@ __global__ __launch_bounds__(256) void k_moe_route(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ add, int64_t hidden,
     const void* __restrict__ nw, float eps, const uint16_t* __restrict__ gate,
     const float* __restrict__ bias, int64_t n_exp, int top_k, int64_t tokens, int bits,
-    uint16_t* __restrict__ h_out, uint16_t* __restrict__ xn_out, int32_t* __restrict__ ids,
-    float* __restrict__ wts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ pair_ids, int32_t* __restrict__ inverse, uint32_t* __restrict__ ws) {
+    uint16_t* __restrict__ h_out, uint16_t* __restrict__ xn_out, uint32_t* __restrict__ xn_pairs,
+    float* __restrict__ xn_corr, int32_t* __restrict__ ids, float* __restrict__ wts,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ pair_ids,
+    int32_t* __restrict__ inverse, uint32_t* __restrict__ ws) {
   __shared__ float red[4];
   __shared__ uint4 xs[256 * CH];  // xn of token t, packed bf16
   __shared__ int32_t base[4][kRouteMaxExperts];
@@ -97,10 +98,11 @@ __global__ __launch_bounds__(256) void k_moe_route(
     }
   }
   const float rstd = rsqrtf(block_sum256(ss, red) / static_cast<float>(hidden) + eps);
+  const bool pairs = eb == 0 && xn_pairs != nullptr;
+  float cpart = 0.f;  // sum (f + 1) xn over this thread's elements (pairs only)
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int ch = tid + 256 * c;
-    if (ch >= nch) continue;
     uint4 o, r;
     uint32_t* ow = reinterpret_cast<uint32_t*>(&o);
     uint32_t* rw = reinterpret_cast<uint32_t*>(&r);
@@ -110,11 +112,46 @@ __global__ __launch_bounds__(256) void k_moe_route(
                              v[c][2 * k + 1] * rstd * wgt[c][2 * k + 1]);
       if constexpr (ADD) rw[k] = pack_bf16x2_rn(v[c][2 * k], v[c][2 * k + 1]);
     }
+    if (pairs) {
+      // x' pairs of word ch / 2: pair j = (f_j xn_j, f_j xn_{j+8}); this
+      // thread holds elements 8 (ch & 1) .. +7 of the word, its partner
+      // (lane ^ 1) the other half.
+      uint32_t hv[4];  // f_j xn_j as bf16 bits, two per dword (exact)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float x0 = __uint_as_float(ow[k] << 16), x1 = __uint_as_float(ow[k] & 0xffff0000u);
+        const float f0 = pair_scale(2 * k), f1 = pair_scale(2 * k + 1);
+        hv[k] = pack_bf16x2(f0 * x0, f1 * x1);
+        if (ch < nch) cpart += (f0 + 1.0f) * x0 + (f1 + 1.0f) * x1;
+      }
+      uint32_t ov[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ov[k] = __shfl_xor(hv[k], 1, 64);
+      if ((ch & 1) == 0 && ch < nch) {
+        uint4 p0, p1;  // dword j: lo = own f_j xn_j, hi = partner's
+        p0.x = (hv[0] & 0xffffu) | (ov[0] << 16);
+        p0.y = (hv[0] >> 16) | (ov[0] & 0xffff0000u);
+        p0.z = (hv[1] & 0xffffu) | (ov[1] << 16);
+        p0.w = (hv[1] >> 16) | (ov[1] & 0xffff0000u);
+        p1.x = (hv[2] & 0xffffu) | (ov[2] << 16);
+        p1.y = (hv[2] >> 16) | (ov[2] & 0xffff0000u);
+        p1.z = (hv[3] & 0xffffu) | (ov[3] << 16);
+        p1.w = (hv[3] >> 16) | (ov[3] & 0xffff0000u);
+        uint4* dst = reinterpret_cast<uint4*>(xn_pairs + t * (hidden / 2) + (ch >> 1) * 8);
+        dst[0] = p0;
+        dst[1] = p1;
+      }
+    }
+    if (ch >= nch) continue;
     xs[ch] = o;
     if (eb == 0) {
       reinterpret_cast<uint4*>(xn_out + t * hidden)[ch] = o;
       if constexpr (ADD) reinterpret_cast<uint4*>(h_out + t * hidden)[ch] = r;
     }
+  }
+  if (pairs) {  // uniform per workgroup
+    const float csum = block_sum256(cpart, red);
+    if (tid == 0) xn_corr[t] = csum;
   }
   __syncthreads();
 
@@ -194,6 +231,7 @@ extern "C" int ma_moe_route(const void* x, const void* x_add, int64_t tokens, in
                             const void* norm_weight, int norm_dtype, float eps,
                             const void* gate_weight, const float* router_bias,
                             int64_t n_experts, int top_k, void* h_out, void* xn_out,
+                            uint32_t* xn_pairs, float* xn_corr,
                             int32_t* topk_ids, float* topk_weight, int32_t* counts,
                             int32_t* offsets, int32_t* pair_ids, int32_t* inverse,
                             void* workspace, size_t workspace_bytes, void* stream) {
@@ -209,8 +247,10 @@ extern "C" int ma_moe_route(const void* x, const void* x_add, int64_t tokens, in
     return fail(MA_ETYPE, "moe_route: norm weight must be float32 or bfloat16");
   if (tokens == 0) return MA_OK;
   if (!x || !norm_weight || !gate_weight || !xn_out || !topk_ids || !topk_weight || !counts ||
-      !offsets || !pair_ids || !inverse || (x_add && !h_out))
+      !offsets || !pair_ids || !inverse || (x_add && !h_out) || (!xn_pairs != !xn_corr))
     return fail(MA_EVALUE, "moe_route: null pointer");
+  if (xn_pairs && (hidden % 16 || (reinterpret_cast<uintptr_t>(xn_pairs) & 15)))
+    return fail(MA_EVALUE, "moe_route: x' pairs need hidden %% 16 == 0 and 16-byte alignment");
   auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (!a16(x) || !a16(gate_weight) || !a16(xn_out) || (x_add && (!a16(x_add) || !a16(h_out))))
     return fail(MA_EVALUE, "moe_route: rows must be 16-byte aligned");
@@ -232,7 +272,8 @@ extern "C" int ma_moe_route(const void* x, const void* x_add, int64_t tokens, in
 #define MA_RT(CH, WDT, PER, ADD)                                                                \
   hipLaunchKernelGGL((k_moe_route<CH, WDT, PER, ADD>), grid, dim3(256), 0, s, xb, ab, hidden, \
                      norm_weight, eps, gb, router_bias, n_experts, top_k, tokens, bits, hb, nb, \
-                     topk_ids, topk_weight, counts, offsets, pair_ids, inverse, wsp)
+                     xn_pairs, xn_corr, topk_ids, topk_weight, counts, offsets, pair_ids, inverse, \
+                     wsp)
 #define MA_RT_A(CH, WDT, PER) \
   if (x_add) { MA_RT(CH, WDT, PER, true); } else { MA_RT(CH, WDT, PER, false); }
 #define MA_RT_P(CH, WDT) \

@@ -151,13 +151,15 @@ def route_timed_out(device: torch.device | int = 0) -> bool:
 
 
 def moe_route(x: torch.Tensor, layer: MoELayer, top_k: int, norm_weight: torch.Tensor,
-              eps: float, add: torch.Tensor | None = None):
+              eps: float, add: torch.Tensor | None = None, *, pairs: bool = False):
     """Residual add + RMSNorm + router + dispatch in one launch for ``x [T, H]``.
 
     Returns ``(h, xn, ids, weights, dispatch)``: ``h = x + add`` (``x`` itself
     when ``add`` is None), ``xn = rms_norm(h) * norm_weight``, the router's
     int32 ids / float32 weights ``[T, top_k]`` and the :class:`Dispatch` lists.
-    Equal, bit for bit, to add_rms_norm + router_topk + moe_dispatch."""
+    Equal, bit for bit, to add_rms_norm + router_topk + moe_dispatch.  With
+    ``pairs``, a sixth item ``(xn_pairs, xn_corr)``: xn in the x' pair form the
+    grouped experts read, and each token's correction."""
     from .kernels.dispatch import Dispatch
     tokens, hidden = x.shape
     dev = x.device
@@ -180,22 +182,30 @@ def moe_route(x: torch.Tensor, layer: MoELayer, top_k: int, norm_weight: torch.T
     pair_ids = torch.empty(tokens * top_k, device=dev, dtype=torch.int32)
     inverse = torch.empty(tokens * top_k, device=dev, dtype=torch.int32)
     nwc = norm_weight.contiguous()
+    xp = torch.empty(tokens, hidden // 2, device=dev, dtype=torch.uint32) if pairs else None
+    xcorr = torch.empty(tokens, device=dev, dtype=torch.float32) if pairs else None
     _lib.call(
         "ma_moe_route",
         _lib.ptr(xc), _lib.ptr(ac), tokens, hidden, _lib.ptr(nwc), _lib.dtype_code(nwc, "norm_weight"),
         float(eps), _lib.ptr(layer.gate_weight), _lib.ptr(layer.router_bias), n_exp, int(top_k),
-        _lib.ptr(h) if ac is not None else None, _lib.ptr(xn), _lib.ptr(ids), _lib.ptr(wts),
+        _lib.ptr(h) if ac is not None else None, _lib.ptr(xn), _lib.ptr(xp), _lib.ptr(xcorr),
+        _lib.ptr(ids), _lib.ptr(wts),
         _lib.ptr(counts), _lib.ptr(offsets), _lib.ptr(pair_ids), _lib.ptr(inverse),
         _lib.ptr(ws), ws.numel(), _lib.stream_of(xc),
     )
-    return h, xn, ids, wts, Dispatch(counts, offsets, pair_ids, inverse)
+    d = Dispatch(counts, offsets, pair_ids, inverse)
+    if pairs:
+        return h, xn, ids, wts, d, (xp, xcorr)
+    return h, xn, ids, wts, d
 
 
 def moe_grouped(x: torch.Tensor, layer: MoELayer, ids: torch.Tensor, wts: torch.Tensor,
-                residual: torch.Tensor | None = None, *, return_h: bool = False, dispatch=None):
+                residual: torch.Tensor | None = None, *, return_h: bool = False, dispatch=None,
+                x_pairs=None):
     """Dispatch + grouped MFMA SwiGLU/down + combine for ``x [T, H]`` (bf16).
 
-    ``dispatch``: the lists for ``ids`` if already built (``moe_route``).
+    ``dispatch``: the lists for ``ids`` if already built (``moe_route``);
+    ``x_pairs``: ``(xn_pairs, xn_corr)`` of ``x`` from ``moe_route(pairs=True)``.
     Returns ``y [T, H]`` (bf16), and with ``return_h`` also ``h [T, k, I]``.
     """
     tokens, hidden = x.shape
@@ -215,7 +225,8 @@ def moe_grouped(x: torch.Tensor, layer: MoELayer, ids: torch.Tensor, wts: torch.
         raise TypeError("up_gate and down row_alpha must share a dtype")
     _lib.call(
         "ma_moe_grouped",
-        _lib.ptr(xc), xc.stride(0), tokens, top_k,
+        _lib.ptr(xc), xc.stride(0), _lib.ptr(x_pairs[0] if x_pairs else None),
+        _lib.ptr(x_pairs[1] if x_pairs else None), tokens, top_k,
         _lib.ptr(layer.up_gate_packed), _lib.ptr(layer.up_gate_alpha),
         _lib.ptr(layer.down_packed), _lib.ptr(layer.down_alpha), alpha_dt,
         layer.n_experts, hidden, inter,
@@ -263,8 +274,9 @@ def moe_layer(hidden: torch.Tensor, layer: MoELayer, top_k: int, norm_weight: to
     tokens = hidden.shape[0]
     if (tokens >= GROUPED_MIN_TOKENS and route_supported(layer, top_k, hidden)
             and hidden.shape[-1] % 256 == 0 and layer.inter % 256 == 0):
-        h, xn, ids, wts, d = moe_route(hidden, layer, top_k, norm_weight, eps, add=add)
-        return moe_grouped(xn, layer, ids, wts, h, dispatch=d), ids
+        h, xn, ids, wts, d, xp = moe_route(hidden, layer, top_k, norm_weight, eps, add=add,
+                                           pairs=True)
+        return moe_grouped(xn, layer, ids, wts, h, dispatch=d, x_pairs=xp), ids
     if add is not None:
         h, xn = add_rms_norm(hidden, add, norm_weight, eps)
     else:

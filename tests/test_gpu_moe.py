@@ -85,6 +85,31 @@ def test_moe_grouped_zipf_vs_oracle(dev, layer, tokens):
     assert_bf16_close(np_f(y), ref, atol_frac=2.0 ** -7, what=f"y T={tokens}")
 
 
+@pytest.mark.parametrize("tokens", [8, 32, 128])
+def test_moe_layer_routed_pairs_vs_oracle(dev, layer, tokens):
+    """The decoder's batched MoE half: one routing launch that also writes xn
+    as x' pairs, then the tile-resident expert kernels reading those pairs
+    (hidden 2048, intermediate 768), against the oracle on the same routing."""
+    from maple_amd.moe import moe_layer
+    L = synthetic.MoELayer(layer.gate_weight, layer.up_gate_packed, layer.up_gate_alpha,
+                           layer.down_packed, layer.down_alpha,
+                           synthetic.zipf_router_bias(E, 1.1, 1.0, seed=3).to(dev))
+    x = synthetic.randn_bf16((tokens, H), 600 + tokens, dev)
+    add = synthetic.randn_bf16((tokens, H), 700 + tokens, dev)
+    nw = synthetic.uniform_bf16((H,), 0.5, 1.5, 800, dev)
+    y, ids = moe_layer(x, L, K, nw, 1e-6, add=add)
+    from maple_amd.kernels import add_rms_norm
+    h, xn = add_rms_norm(x, add, nw, 1e-6)
+    ids2, wts = router_topk(xn, L.gate_weight, K, bias=L.router_bias)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ids2)
+    idn, wn = ids.cpu().numpy(), wts.cpu().numpy()
+    ref, _ = ok.moe_experts(np_f(xn), idn, wn, *_oracle_inputs(L), residual=np_f(h))
+    assert_bf16_close(np_f(y), ref, atol_frac=2.0 ** -7, what=f"routed y T={tokens}")
+    y2, _ = moe_layer(x, L, K, nw, 1e-6, add=add)
+    assert torch.equal(y, y2)  # deterministic
+
+
 def test_moe_block_grouped_matches_per_slot(dev, layer):
     """The two plans agree on the same routing (bf16 tolerance)."""
     x = synthetic.randn_bf16((16, H), 400, dev)
