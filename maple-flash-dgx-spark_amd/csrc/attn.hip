@@ -166,7 +166,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   __shared__ __align__(16) uint32_t vt[kHeadDim][kVtRow];
   __shared__ __align__(16) uint16_t kvnew[2][kHeadDim];
   __shared__ float wm[4][kMaxGroup], wl[4][kMaxGroup];
-  __shared__ float hm[kMaxGroup], hl[kMaxGroup], hr[kMaxGroup];
+  __shared__ float hm[kMaxGroup], hl[kMaxGroup];
   __shared__ __align__(16) uint4 os4[kOWords * 2][32];  // O projection input
   const int sp = blockIdx.x, kvh = blockIdx.y;
   const int64_t b = blockIdx.z;
@@ -283,15 +283,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       qs[i / kHeadDim][i % kHeadDim] = xq[k];
     }
   }
-  if (tid < kMaxGroup) {
-    hm[tid] = -INFINITY;
-    hl[tid] = 0.f;
-  }
   __syncthreads();
   uint4 qf[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) qf[ks] = *reinterpret_cast<const uint4*>(&qs[r16][8 * g + 32 * ks]);
 
+  // Each wave keeps its own running softmax state over its 32 positions of
+  // every chunk (head r16's max and sum, in the 4 lanes holding that head), so
+  // a chunk needs no workgroup barrier; the waves' states are combined once,
+  // after the last chunk.  V^T of a chunk sits in the wave's own columns of
+  // vt (positions 32 wv .. +31), which only that wave writes and reads.
+  float mrun = -INFINITY, lrun = 0.f;
   f32x4a_t oacc[4];
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) oacc[nb] = f32x4a_t{0.f, 0.f, 0.f, 0.f};
@@ -352,15 +354,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       for (int i = 0; i < 4; ++i)
         s[pb][i] = lo + 32 * wv + 16 * pb + 4 * g + i < hi ? acc[i] * scale : -INFINITY;
     }
+    if (c + 1 < c_end) load_chunk(c + 1, kf, vr);  // in flight during softmax and P.V
     float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    if (g == 0) wm[wv][r16] = mx;
-    __syncthreads();
-    if (c + 1 < c_end) load_chunk(c + 1, kf, vr);  // in flight during softmax and P.V
-    const float m_old = hm[r16];
-    const float m_new = fmaxf(m_old, fmaxf(fmaxf(wm[0][r16], wm[1][r16]), fmaxf(wm[2][r16], wm[3][r16])));
+    const float m_new = fmaxf(mrun, mx);
+    const float r = m_new == -INFINITY ? 1.f : expf(mrun - m_new);  // 0 on the first valid chunk
     float p[2][4], ls = 0.f;
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb)
@@ -371,23 +371,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       }
     ls += __shfl_xor(ls, 16, 64);
     ls += __shfl_xor(ls, 32, 64);
-    if (g == 0) wl[wv][r16] = ls;
+    lrun = lrun * r + ls;
+    mrun = m_new;
     // P in bf16 as the A fragment: k = positions 4g..4g+3 of block 0, then of block 1.
     const uint4 pa = make_uint4(pack_bf16x2_rn(p[0][0], p[0][1]), pack_bf16x2_rn(p[0][2], p[0][3]),
                                 pack_bf16x2_rn(p[1][0], p[1][1]), pack_bf16x2_rn(p[1][2], p[1][3]));
-    __syncthreads();
-    if (tid < kMaxGroup) {
-      const float mo = hm[tid];
-      const float mn = fmaxf(mo, fmaxf(fmaxf(wm[0][tid], wm[1][tid]), fmaxf(wm[2][tid], wm[3][tid])));
-      const float r = expf(mo - mn);  // 0 on the first chunk
-      hl[tid] = hl[tid] * r + ((wl[0][tid] + wl[1][tid]) + (wl[2][tid] + wl[3][tid]));
-      hm[tid] = mn;
-      hr[tid] = r;
-    }
-    __syncthreads();
+    // rescale of head 4g + i: held by lane 4g + i
     float rr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rr[i] = hr[4 * g + i];
+    for (int i = 0; i < 4; ++i) rr[i] = __shfl(r, 4 * g + i, 64);
     const int mp = 16 * wv + 2 * g;
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
@@ -398,20 +390,38 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       for (int i = 0; i < 4; ++i) oacc[nb][i] *= rr[i];
       oacc[nb] = mfma_att(pa, make_uint4(b0.x, b0.y, b1.x, b1.y), oacc[nb]);
     }
-    __syncthreads();  // vt / wm / wl are rewritten by the next chunk
-  }
+    }
   if (o_w) o_prefetch();  // after the K/V stream, in flight through the merge and the barrier
   // The new K/V go to the cache last (after every read of the cache).
   if (owns_pos && wv < 2) (wv == 0 ? k_cache : v_cache)[(base + pos) * kHeadDim + lane] = new_kv;
-  // Sum the waves' P.V (same running max, so a plain sum) in a fixed order,
-  // through LDS that V no longer needs.
+  // Combine the waves' states in a fixed order, through LDS that V no longer
+  // needs: head h's max M = max_w m_w, sum = sum_w l_w exp(m_w - M), output
+  // sum_w acc_w exp(m_w - M).
   static_assert(sizeof(vt) >= 4 * kMaxGroup * kHeadDim * sizeof(float), "reduction buffer");
   float (*ow)[kMaxGroup][kHeadDim] = reinterpret_cast<float (*)[kMaxGroup][kHeadDim]>(&vt[0][0]);
+  __syncthreads();  // every wave's last P.V has read its vt columns
+  if (g == 0) {
+    wm[wv][r16] = mrun;
+    wl[wv][r16] = lrun;
+  }
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (4 * g + i < group) ow[wv][4 * g + i][16 * nb + r16] = oacc[nb][i];
+  __syncthreads();
+  if (tid < kMaxGroup) {
+    const float M = fmaxf(fmaxf(wm[0][tid], wm[1][tid]), fmaxf(wm[2][tid], wm[3][tid]));
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float sc = wm[w][tid] == -INFINITY ? 0.f : expf(wm[w][tid] - M);
+      L += wl[w][tid] * sc;
+      wm[w][tid] = sc;  // from here on: wave w's scale for head tid
+    }
+    hm[tid] = M;
+    hl[tid] = L;
+  }
   __syncthreads();
   const int64_t pidx = (b * nkv + kvh) * max_splits + sp;
   const int64_t n_part = static_cast<int64_t>(gridDim.z) * nkv * max_splits * kMaxGroup;
@@ -419,14 +429,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   const CoherentBuf ml_buf(part_ml, static_cast<uint32_t>(n_part * 8));
   for (int item = tid; item < group * 16; item += kAttnThreads) {
     const int hh = item >> 4, dq = item & 15;
-    float4 o = *reinterpret_cast<const float4*>(&ow[0][hh][4 * dq]);
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int w = 1; w < 4; ++w) {
+    for (int w = 0; w < 4; ++w) {
       const float4 q = *reinterpret_cast<const float4*>(&ow[w][hh][4 * dq]);
-      o.x += q.x;
-      o.y += q.y;
-      o.z += q.z;
-      o.w += q.w;
+      const float sc = wm[w][hh];
+      o.x += q.x * sc;
+      o.y += q.y * sc;
+      o.z += q.z * sc;
+      o.w += q.w * sc;
     }
     if (n_spl == 1) {
       const float inv = 1.f / hl[hh];
