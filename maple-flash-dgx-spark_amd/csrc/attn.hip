@@ -26,7 +26,7 @@ constexpr int kHeadDim = 64;                // head_dim of the synthetic decoder
 constexpr int kSplit = 128;                 // positions per chunk
 constexpr int kAttnThreads = 256;           // 4 waves, 32 positions of a chunk each
 constexpr int kMaxGroup = 16;               // query heads per KV head
-constexpr int kVtRow = kSplit / 2 + 4;      // LDS row (one dim) of V position
+constexpr int kVtRow = kSplit / 2 + 2;      // LDS row (one dim) of V position
                                             // pairs in words, padded
 constexpr int kCombineChunk = 4;            // splits whose partials one merge lane loads together
 constexpr int kOWords = 4;                  // O projection: words of K per lane (K = 32 x 4 x 16 = 2048)
@@ -117,6 +117,9 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope_store(
 
 typedef __bf16 bf16x8a_t __attribute__((ext_vector_type(8)));
 typedef float f32x4a_t __attribute__((ext_vector_type(4)));
+
+// 2^x in one v_exp_f32 (2^-inf = 0).
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ f32x4a_t mfma_att(uint4 a, uint4 b, f32x4a_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8a_t, a),
@@ -211,6 +214,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   const int n_chunks = static_cast<int>(cdiv(kv_len - start, kSplit));
   const int cps = static_cast<int>(cdiv(n_chunks, gridDim.x));  // chunks per split
   const int n_spl = static_cast<int>(cdiv(n_chunks, cps));
+  const float scale2 = scale * 1.44269504088896341f;  // log2(e): maxima and sums in base 2
   auto attend = [&]() {
   const int c_beg = sp * cps;
   const int c_end = c_beg + cps < n_chunks ? c_beg + cps : n_chunks;
@@ -219,7 +223,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   const bool owns_pos = FUSED && sp == n_spl - 1;
 
   // K fragments: positions 32 wv + 16 pb + r16, dims 8 g + 32 ks.
-  // V rows: position 32 wv + (lane >> 1), dims 32 (lane & 1) .. +32.
+  // V: load i covers the wave's positions 32 wv + 8 i .. +7 contiguously
+  // (1 KB): lane l holds position 32 wv + 8 i + (l >> 3), dims 8 (l & 7) .. +8.
   auto load_chunk = [&](int c, uint4 (&kf)[2][2], uint4 (&vr)[4]) {
     const int64_t lo = start + static_cast<int64_t>(c) * kSplit;
     const int64_t hi = lo + kSplit < kv_len ? lo + kSplit : kv_len;
@@ -231,11 +236,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       for (int ks = 0; ks < 2; ++ks)
         kf[pb][ks] = *reinterpret_cast<const uint4*>(k_cache + (base + t) * kHeadDim + 8 * g + 32 * ks);
     }
-    int64_t tv = lo + 32 * wv + (lane >> 1);
-    tv = tv < hi ? tv : hi - 1;
-    const uint4* vp = reinterpret_cast<const uint4*>(v_cache + (base + tv) * kHeadDim + 32 * (lane & 1));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vr[i] = vp[i];
+    for (int i = 0; i < 4; ++i) {
+      int64_t tv = lo + 32 * wv + 8 * i + (lane >> 3);
+      tv = tv < hi ? tv : hi - 1;
+      vr[i] = *reinterpret_cast<const uint4*>(v_cache + (base + tv) * kHeadDim + 8 * (lane & 7));
+    }
   };
   uint4 kf[2][2], vr[4];
   uint16_t new_kv = 0;  // FUSED owner split: the new K (wave 0) or V (wave 1) element
@@ -311,48 +317,49 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
                                   sel32(nk, v.z, kf[pb][ks].z), sel32(nk, v.w, kf[pb][ks].w));
         }
       }
-      const bool nv = owns_pos && lo + 32 * wv + (lane >> 1) == pos;
+      const uint4 v = *reinterpret_cast<const uint4*>(&kvnew[1][8 * (lane & 7)]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint4 v = *reinterpret_cast<const uint4*>(&kvnew[1][32 * (lane & 1) + 8 * i]);
+        const bool nv = owns_pos && lo + 32 * wv + 8 * i + (lane >> 3) == pos;
         vr[i] = make_uint4(sel32(nv, v.x, vr[i].x), sel32(nv, v.y, vr[i].y), sel32(nv, v.z, vr[i].z),
                            sel32(nv, v.w, vr[i].w));
       }
     }
-    // V^T in position pairs: lanes l and l ^ 2 hold positions 2m and 2m + 1
-    // of the same 32 dims; the even one builds the half's dims 0..15, the
-    // odd one dims 16..31.
+    // V^T in position pairs: lanes l and l ^ 8 hold positions 2m and 2m + 1
+    // of the same 8 dims (one DPP rotate by 8 within each 16-lane row swaps
+    // them); the even one writes the pairs of dims 0..3 of its 8, the odd one
+    // dims 4..7.
     {
-      uint32_t v[16];
+      const bool odd = (lane >> 3) & 1;
+      const int d0 = 8 * (lane & 7) + (odd ? 4 : 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        v[4 * i] = vr[i].x;
-        v[4 * i + 1] = vr[i].y;
-        v[4 * i + 2] = vr[i].z;
-        v[4 * i + 3] = vr[i].w;
-      }
-      const bool odd = (lane >> 1) & 1;
-      const int d0 = 32 * (lane & 1) + (odd ? 16 : 0);
-      const int m = 16 * wv + (lane >> 2);
+        const uint32_t u[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+        uint32_t o[4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t mine = odd ? v[8 + j] : v[j];
-        const uint32_t send = odd ? v[j] : v[8 + j];
-        const uint32_t other = __builtin_amdgcn_update_dpp(0, send, 0x4E, 0xF, 0xF, false);
-        const uint32_t e = odd ? other : mine, o = odd ? mine : other;
-        vt[d0 + 2 * j][m] = (e & 0xffffu) | (o << 16);
-        vt[d0 + 2 * j + 1][m] = (e >> 16) | (o & 0xffff0000u);
+        for (int k = 0; k < 4; ++k) o[k] = __builtin_amdgcn_update_dpp(0, u[k], 0x128, 0xF, 0xF, false);
+        const int m = 16 * wv + 4 * i + (lane >> 4);
+        // dims d0 .. d0+3: words 2 (odd) .. +1 of this lane's (and the partner's) 4
+        const uint32_t a0 = odd ? o[2] : u[0], a1 = odd ? o[3] : u[1];  // position 2m
+        const uint32_t b0 = odd ? u[2] : o[0], b1 = odd ? u[3] : o[1];  // position 2m + 1
+        vt[d0][m] = (a0 & 0xffffu) | (b0 << 16);
+        vt[d0 + 1][m] = (a0 >> 16) | (b0 & 0xffff0000u);
+        vt[d0 + 2][m] = (a1 & 0xffffu) | (b1 << 16);
+        vt[d0 + 3][m] = (a1 >> 16) | (b1 & 0xffff0000u);
       }
     }
     // Scores and this wave's per-head maximum.
+    // (in the base-2 domain: scores times log2(e), so that every exponential
+    // of the softmax and of the merges is one v_exp_f32)
     float s[2][4];
+    const int span = static_cast<int>(hi - lo);
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb) {
       f32x4a_t acc = mfma_att(kf[pb][0], qf[0], f32x4a_t{0.f, 0.f, 0.f, 0.f});
       acc = mfma_att(kf[pb][1], qf[1], acc);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        s[pb][i] = lo + 32 * wv + 16 * pb + 4 * g + i < hi ? acc[i] * scale : -INFINITY;
+        s[pb][i] = 32 * wv + 16 * pb + 4 * g + i < span ? acc[i] * scale2 : -INFINITY;
     }
     if (c + 1 < c_end) load_chunk(c + 1, kf, vr);  // in flight during softmax and P.V
     float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
@@ -360,13 +367,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(mrun, mx);
-    const float r = m_new == -INFINITY ? 1.f : expf(mrun - m_new);  // 0 on the first valid chunk
+    const float r = m_new == -INFINITY ? 1.f : exp2_fast(mrun - m_new);  // 0 on the first valid chunk
     float p[2][4], ls = 0.f;
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        p[pb][i] = s[pb][i] == -INFINITY ? 0.f : expf(s[pb][i] - m_new);
+        p[pb][i] = s[pb][i] == -INFINITY ? 0.f : exp2_fast(s[pb][i] - m_new);
         ls += p[pb][i];
       }
     ls += __shfl_xor(ls, 16, 64);
@@ -415,7 +422,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     float L = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float sc = wm[w][tid] == -INFINITY ? 0.f : expf(wm[w][tid] - M);
+      const float sc = wm[w][tid] == -INFINITY ? 0.f : exp2_fast(wm[w][tid] - M);
       L += wl[w][tid] * sc;
       wm[w][tid] = sc;  // from here on: wave w's scale for head tid
     }
@@ -507,8 +514,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
           const bool ok = s0 + u * tpi + j < n_spl;
           const float m = ok ? ml[u].x : -INFINITY;
           const float mn = fmaxf(mx, m);
-          const float r = mx == -INFINITY ? 0.f : expf(mx - mn);
-          const float w = ok ? expf(m - mn) : 0.f;
+          const float r = mx == -INFINITY ? 0.f : exp2_fast(mx - mn);
+          const float w = ok ? exp2_fast(m - mn) : 0.f;
           den = den * r + w * ml[u].y;
           n0 = n0 * r + w * ac[u].x;
           n1 = n1 * r + w * ac[u].y;
@@ -523,8 +530,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       const float o0 = __shfl_xor(n0, off, 64), o1 = __shfl_xor(n1, off, 64);
       const float o2 = __shfl_xor(n2, off, 64), o3 = __shfl_xor(n3, off, 64);
       const float mn = fmaxf(mx, mo);
-      const float r = mx == -INFINITY ? 0.f : expf(mx - mn);
-      const float ro = mo == -INFINITY ? 0.f : expf(mo - mn);
+      const float r = mx == -INFINITY ? 0.f : exp2_fast(mx - mn);
+      const float ro = mo == -INFINITY ? 0.f : exp2_fast(mo - mn);
       den = den * r + dn * ro;
       n0 = n0 * r + o0 * ro;
       n1 = n1 * r + o1 * ro;

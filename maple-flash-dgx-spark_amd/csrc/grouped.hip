@@ -631,7 +631,7 @@ constexpr int kErChunksUp = 8, kErChunksDown = 3;
 
 // SwiGLU: BPW up blocks (and the matching gate blocks) per wave; x' pairs of
 // the tile's tokens (x_pairs [T, K / 2] uint32, x_corr [T]) staged in LDS.
-template <int BPW, int ADT, int NCH>
+template <int BPW, int ADT, int NCH, int QPB>
 __global__ __launch_bounds__(64 * kErWaves) void k_grouped_swiglu_er(
     const uint32_t* __restrict__ x_pairs, const float* __restrict__ x_corr, int64_t topk,
     const uint32_t* __restrict__ w, int64_t n_half, const void* __restrict__ alpha,
@@ -692,22 +692,27 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_swiglu_er(
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {  // one word per step (operand registers)
-      u32x4v_t av[2 * BPW][2], bv[2];
+    for (int q0 = 0; q0 < 4; q0 += QPB) {  // QPB words per MFMA block
+      u32x4v_t av[QPB][2 * BPW][2], bv[QPB][2];
 #pragma unroll
-      for (int j = 0; j < 2 * BPW; ++j) {
-        uint32_t ex[8];
-        expand_word(wq[j][c][q], ex, kc);
-        av[j][0] = u32x4v_t{ex[0], ex[1], ex[2], ex[3]};
-        av[j][1] = u32x4v_t{ex[4], ex[5], ex[6], ex[7]};
+      for (int qi = 0; qi < QPB; ++qi) {
+#pragma unroll
+        for (int j = 0; j < 2 * BPW; ++j) {
+          uint32_t ex[8];
+          expand_word(wq[j][c][q0 + qi], ex, kc);
+          av[qi][j][0] = u32x4v_t{ex[0], ex[1], ex[2], ex[3]};
+          av[qi][j][1] = u32x4v_t{ex[4], ex[5], ex[6], ex[7]};
+        }
+        bv[qi][0] = xs[16 * c + 4 * g + q0 + qi][0][r16];
+        bv[qi][1] = xs[16 * c + 4 * g + q0 + qi][1][r16];
       }
-      bv[0] = xs[16 * c + 4 * g + q][0][r16];
-      bv[1] = xs[16 * c + 4 * g + q][1][r16];
       mfma_block_begin();
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
+      for (int qi = 0; qi < QPB; ++qi)
 #pragma unroll
-        for (int j = 0; j < 2 * BPW; ++j) mfma_acc(acc[j], av[j][hf], bv[hf]);
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int j = 0; j < 2 * BPW; ++j) mfma_acc(acc[j], av[qi][j][hf], bv[qi][hf]);
       mfma_block_end();
       keep_b(av, acc);
       keep_b(bv, acc);
@@ -923,10 +928,24 @@ extern "C" int ma_moe_grouped(const void* x, int64_t ldx, const uint32_t* x_pair
     dim3 g2(static_cast<unsigned>(cdiv(hidden, 64)), max_tiles);
     // tile-resident forms: 16 rows (up + gate) / 32 rows per wave
     dim3 ge1(static_cast<unsigned>(cdiv(inter, 16 * kErWaves)), max_tiles);
+    dim3 ge1b(static_cast<unsigned>(cdiv(inter, 32 * kErWaves)), max_tiles);
+    const int sv = getenv("MA_SV") ? atoi(getenv("MA_SV")) : 0;  // TEMP experiment
     dim3 ge2(static_cast<unsigned>(cdiv(hidden, 32 * kErWaves)), max_tiles);
 #define MA_GROUPED_KS(ADT)                                                                       \
-  if (x_pairs && hidden == 16 * 16 * kErChunksUp)                                                \
-    hipLaunchKernelGGL((k_grouped_swiglu_er<1, ADT, kErChunksUp>), ge1, dim3(64 * kErWaves), 0,  \
+  if (x_pairs && hidden == 16 * 16 * kErChunksUp && sv == 1)                                     \
+    hipLaunchKernelGGL((k_grouped_swiglu_er<1, ADT, kErChunksUp, 2>), ge1, dim3(64 * kErWaves), 0,  \
+                       s, x_pairs, x_corr, top_k, up_gate, inter, up_gate_alpha, offsets,        \
+                       pair_ids, ne, hp, hb, ldh);                                               \
+  else if (x_pairs && hidden == 16 * 16 * kErChunksUp && sv == 2)                                \
+    hipLaunchKernelGGL((k_grouped_swiglu_er<2, ADT, kErChunksUp, 1>), ge1b, dim3(64 * kErWaves), 0,  \
+                       s, x_pairs, x_corr, top_k, up_gate, inter, up_gate_alpha, offsets,        \
+                       pair_ids, ne, hp, hb, ldh);                                               \
+  else if (x_pairs && hidden == 16 * 16 * kErChunksUp && sv == 3)                                \
+    hipLaunchKernelGGL((k_grouped_swiglu_er<2, ADT, kErChunksUp, 2>), ge1b, dim3(64 * kErWaves), 0,  \
+                       s, x_pairs, x_corr, top_k, up_gate, inter, up_gate_alpha, offsets,        \
+                       pair_ids, ne, hp, hb, ldh);                                               \
+  else if (x_pairs && hidden == 16 * 16 * kErChunksUp)                                           \
+    hipLaunchKernelGGL((k_grouped_swiglu_er<1, ADT, kErChunksUp, 1>), ge1, dim3(64 * kErWaves), 0,  \
                        s, x_pairs, x_corr, top_k, up_gate, inter, up_gate_alpha, offsets,        \
                        pair_ids, ne, hp, hb, ldh);                                               \
   else if (x_pairs)                                                                              \
