@@ -875,6 +875,60 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ ou
       static_cast<uint32_t>(f32_to_bf16(a0)) | (static_cast<uint32_t>(f32_to_bf16(a1)) << 16);
 }
 
+// The same combine for top-k <= K, bf16 rows, 8 outputs per thread: the
+// token's k (position, weight) pairs are wave-uniform scalar loads, then every
+// slot's 16-byte load and the residual's are issued before the sums (the
+// arithmetic and its order are k_combine's).
+template <int K>
+__global__ __launch_bounds__(256) void k_combine8(const uint16_t* __restrict__ out,
+                                                  const int32_t* __restrict__ inverse,
+                                                  const float* __restrict__ wts, int topk,
+                                                  int64_t n, const uint16_t* __restrict__ res,
+                                                  uint16_t* __restrict__ y) {
+  const int64_t t = blockIdx.y;
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
+  int64_t row[K];
+  float wj[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    row[j] = j < topk ? inverse[t * topk + j] : 0;
+    wj[j] = j < topk ? wts[t * topk + j] : 0.f;
+  }
+  if (i >= n) return;
+  uint4 v[K], r = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int j = 0; j < K; ++j)
+    if (j < topk) v[j] = *reinterpret_cast<const uint4*>(out + row[j] * n + i);
+  if (res) r = *reinterpret_cast<const uint4*>(res + t * n + i);
+  float a[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = 0.f;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    if (j >= topk) break;
+    const uint32_t u[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      a[2 * q] += wj[j] * __uint_as_float(u[q] << 16);
+      a[2 * q + 1] += wj[j] * __uint_as_float(u[q] & 0xffff0000u);
+    }
+  }
+  if (res) {
+    const uint32_t u[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      a[2 * q] += __uint_as_float(u[q] << 16);
+      a[2 * q + 1] += __uint_as_float(u[q] & 0xffff0000u);
+    }
+  }
+  uint4 o;
+  o.x = pack_bf16x2_rn(a[0], a[1]);
+  o.y = pack_bf16x2_rn(a[2], a[3]);
+  o.z = pack_bf16x2_rn(a[4], a[5]);
+  o.w = pack_bf16x2_rn(a[6], a[7]);
+  *reinterpret_cast<uint4*>(y + t * n + i) = o;
+}
+
 }  // namespace ma
 
 using namespace ma;
@@ -928,25 +982,11 @@ extern "C" int ma_moe_grouped(const void* x, int64_t ldx, const uint32_t* x_pair
     dim3 g2(static_cast<unsigned>(cdiv(hidden, 64)), max_tiles);
     // tile-resident forms: 16 rows (up + gate) / 32 rows per wave
     dim3 ge1(static_cast<unsigned>(cdiv(inter, 16 * kErWaves)), max_tiles);
-    dim3 ge1b(static_cast<unsigned>(cdiv(inter, 32 * kErWaves)), max_tiles);
-    const int sv = getenv("MA_SV") ? atoi(getenv("MA_SV")) : 0;  // TEMP experiment
     dim3 ge2(static_cast<unsigned>(cdiv(hidden, 32 * kErWaves)), max_tiles);
 #define MA_GROUPED_KS(ADT)                                                                       \
-  if (x_pairs && hidden == 16 * 16 * kErChunksUp && sv == 1)                                     \
-    hipLaunchKernelGGL((k_grouped_swiglu_er<1, ADT, kErChunksUp, 2>), ge1, dim3(64 * kErWaves), 0,  \
-                       s, x_pairs, x_corr, top_k, up_gate, inter, up_gate_alpha, offsets,        \
-                       pair_ids, ne, hp, hb, ldh);                                               \
-  else if (x_pairs && hidden == 16 * 16 * kErChunksUp && sv == 2)                                \
-    hipLaunchKernelGGL((k_grouped_swiglu_er<2, ADT, kErChunksUp, 1>), ge1b, dim3(64 * kErWaves), 0,  \
-                       s, x_pairs, x_corr, top_k, up_gate, inter, up_gate_alpha, offsets,        \
-                       pair_ids, ne, hp, hb, ldh);                                               \
-  else if (x_pairs && hidden == 16 * 16 * kErChunksUp && sv == 3)                                \
-    hipLaunchKernelGGL((k_grouped_swiglu_er<2, ADT, kErChunksUp, 2>), ge1b, dim3(64 * kErWaves), 0,  \
-                       s, x_pairs, x_corr, top_k, up_gate, inter, up_gate_alpha, offsets,        \
-                       pair_ids, ne, hp, hb, ldh);                                               \
-  else if (x_pairs && hidden == 16 * 16 * kErChunksUp)                                           \
-    hipLaunchKernelGGL((k_grouped_swiglu_er<1, ADT, kErChunksUp, 1>), ge1, dim3(64 * kErWaves), 0,  \
-                       s, x_pairs, x_corr, top_k, up_gate, inter, up_gate_alpha, offsets,        \
+  if (x_pairs && hidden == 16 * 16 * kErChunksUp)                                                \
+    hipLaunchKernelGGL((k_grouped_swiglu_er<1, ADT, kErChunksUp, 1>), ge1, dim3(64 * kErWaves),  \
+                       0, s, x_pairs, x_corr, top_k, up_gate, inter, up_gate_alpha, offsets,     \
                        pair_ids, ne, hp, hb, ldh);                                               \
   else if (x_pairs)                                                                              \
     hipLaunchKernelGGL((k_grouped_swiglu_ks<2, ADT, 8, true>), g1, dim3(512), 0, s, xb, ldx,     \
@@ -986,9 +1026,18 @@ extern "C" int ma_moe_grouped(const void* x, int64_t ldx, const uint32_t* x_pair
 #undef MA_GROUPED
   }
   if (y) {
-    dim3 g3(static_cast<unsigned>(cdiv(hidden, 512)), static_cast<unsigned>(tokens));
-    hipLaunchKernelGGL(k_combine, g3, dim3(256), 0, s, out, inverse, topk_weight, top_k, hidden,
-                       residual, residual_dtype, static_cast<uint16_t*>(y));
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (top_k <= 8 && (!residual || (residual_dtype == MA_BF16 && a16(residual))) && a16(y) &&
+        hidden % 8 == 0) {
+      dim3 g3(static_cast<unsigned>(cdiv(hidden, 256 * 8)), static_cast<unsigned>(tokens));
+      hipLaunchKernelGGL(k_combine8<8>, g3, dim3(256), 0, s, out, inverse, topk_weight,
+                         static_cast<int>(top_k), hidden, static_cast<const uint16_t*>(residual),
+                         static_cast<uint16_t*>(y));
+    } else {
+      dim3 g3(static_cast<unsigned>(cdiv(hidden, 512)), static_cast<unsigned>(tokens));
+      hipLaunchKernelGGL(k_combine, g3, dim3(256), 0, s, out, inverse, topk_weight, top_k, hidden,
+                         residual, residual_dtype, static_cast<uint16_t*>(y));
+    }
   }
   return check_launch("moe_grouped");
 }
