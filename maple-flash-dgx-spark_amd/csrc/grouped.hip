@@ -649,25 +649,16 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_swiglu_er(
   const int64_t nblk = n_half / 16;
   const int64_t b0 = (static_cast<int64_t>(blockIdx.x) * kErWaves + wv) * BPW;  // first up block
   const uint32_t* we = w + static_cast<int64_t>(e) * (2 * n_half) * NW;
-  // weights of this wave's blocks for all of K, issued first
-  u32x4v_t wq[2 * BPW][NCH];
-#pragma unroll
-  for (int j = 0; j < 2 * BPW; ++j) {
-    int64_t blk = b0 + (j % BPW);
-    blk = blk < nblk ? blk : nblk - 1;
-    const uint32_t* rp = we + ((j / BPW) * n_half + blk * 16 + r16) * NW + 4 * g;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) wq[j][c] = *reinterpret_cast<const u32x4v_t*>(rp + 16 * c);
-  }
+  // Issue order matters (memory counters complete in issue order): the pair
+  // ids, then the tile's x' pairs, then the weights, so that staging x' waits
+  // for nothing behind it and the weights stream while it happens.
   if (tid < 16) {
     const int p = tid < np ? pair_ids[pos0 + tid] : -1;
     s_pid[tid] = p;
     s_tok[tid] = p >= 0 ? static_cast<int>(p / topk) : -1;
   }
   __syncthreads();
-  if (tid < 16) s_c[tid] = s_tok[tid] >= 0 ? x_corr[s_tok[tid]] : 0.f;
-  // stage the tile's x' pairs: item = (col, word, half), 16-byte loads, all
-  // issued before the first LDS store
+  // the tile's x' pairs: item = (col, word, half), 16-byte loads
   constexpr int kItems = 16 * NW * 2, kPer = (kItems + 64 * kErWaves - 1) / (64 * kErWaves);
   u32x4v_t sv[kPer];
 #pragma unroll
@@ -679,15 +670,30 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_swiglu_er(
     if (it < kItems && tk >= 0)
       sv[k] = *reinterpret_cast<const u32x4v_t*>(x_pairs + static_cast<int64_t>(tk) * (NW * 8) + rem * 4);
   }
+  float cx = 0.f;
+  if (tid < 16 && s_tok[tid] >= 0) cx = x_corr[s_tok[tid]];
+  // weights of this wave's blocks for all of K
+  u32x4v_t wq[2 * BPW][NCH];
+#pragma unroll
+  for (int j = 0; j < 2 * BPW; ++j) {
+    int64_t blk = b0 + (j % BPW);
+    blk = blk < nblk ? blk : nblk - 1;
+    const uint32_t* rp = we + ((j / BPW) * n_half + blk * 16 + r16) * NW + 4 * g;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) wq[j][c] = *reinterpret_cast<const u32x4v_t*>(rp + 16 * c);
+  }
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int it = tid + 64 * kErWaves * k;
     if (it < kItems) xs[(it % (NW * 2)) >> 1][it & 1][it / (NW * 2)] = sv[k];
   }
+  if (tid < 16) s_c[tid] = cx;
   __syncthreads();
-  f32x4d_t acc[2 * BPW];
+  // two accumulators per block (the two halves of each word), so a block's
+  // MFMAs are independent of each other
+  f32x4d_t acc[2 * BPW][2];
 #pragma unroll
-  for (int j = 0; j < 2 * BPW; ++j) acc[j] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < 2 * BPW; ++j) acc[j][0] = acc[j][1] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
   const ExpandConsts kc;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -712,12 +718,15 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_swiglu_er(
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-          for (int j = 0; j < 2 * BPW; ++j) mfma_acc(acc[j], av[qi][j][hf], bv[qi][hf]);
+          for (int j = 0; j < 2 * BPW; ++j) mfma_acc(acc[j][hf], av[qi][j][hf], bv[qi][hf]);
       mfma_block_end();
-      keep_b(av, acc);
-      keep_b(bv, acc);
+      keep_b(av, acc[0]);
+      keep_b(bv, acc[0]);
     }
   }
+  f32x4d_t accs[2 * BPW];
+#pragma unroll
+  for (int j = 0; j < 2 * BPW; ++j) accs[j] = acc[j][0] + acc[j][1];
   // Epilogue: lane holds pair column r16, rows 4 g .. +3 of each block.
   if (r16 >= np) return;
   const float cc = s_c[r16];
@@ -732,7 +741,7 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_swiglu_er(
       const int64_t i = blk * 16 + 4 * g + r;
       const float au = ld_t<ADT>(alpha, static_cast<int64_t>(e) * 2 * n_half + i);
       const float ag = ld_t<ADT>(alpha, static_cast<int64_t>(e) * 2 * n_half + n_half + i);
-      const uint16_t hb = f32_to_bf16(swiglu_act(au * (acc[j][r] - cc), ag * (acc[BPW + j][r] - cc)));
+      const uint16_t hb = f32_to_bf16(swiglu_act(au * (accs[j][r] - cc), ag * (accs[BPW + j][r] - cc)));
       if (hp) {
         const int pos = static_cast<int>(i & 15), jj = pos & 7, hh = pos >> 3;
         const float hv = bf16_to_f32(hb) * pair_scale(jj);  // exact: power-of-two scale
