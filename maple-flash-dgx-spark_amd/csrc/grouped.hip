@@ -772,17 +772,9 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_down_er(
   const int64_t nblk = n_out / 16;
   const int64_t b0 = (static_cast<int64_t>(blockIdx.x) * kErWaves + wv) * BPW;
   const uint32_t* we = w + static_cast<int64_t>(e) * n_out * NW;
-  u32x4v_t wq[BPW][NCH];
-#pragma unroll
-  for (int j = 0; j < BPW; ++j) {
-    int64_t blk = b0 + j;
-    blk = blk < nblk ? blk : nblk - 1;
-    const uint32_t* rp = we + (blk * 16 + r16) * NW + 4 * g;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) wq[j][c] = *reinterpret_cast<const u32x4v_t*>(rp + 16 * c);
-  }
-  // stage: item = (col, word): both halves of the word and its correction,
-  // all loads issued before the first LDS store
+  // stage: item = (col, word): both halves of the word and its correction;
+  // these loads go out before the weights' (memory counters complete in issue
+  // order), so staging does not wait for the weight stream
   constexpr int kItems = 16 * NW, kPer = (kItems + 64 * kErWaves - 1) / (64 * kErWaves);
   u32x4v_t sv[kPer][2];
 #pragma unroll
@@ -795,6 +787,16 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_down_er(
       sv[k][0] = src[0];
       sv[k][1] = src[1];
     }
+  }
+  // weights of this wave's blocks for all of K
+  u32x4v_t wq[BPW][NCH];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) {
+    int64_t blk = b0 + j;
+    blk = blk < nblk ? blk : nblk - 1;
+    const uint32_t* rp = we + (blk * 16 + r16) * NW + 4 * g;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) wq[j][c] = *reinterpret_cast<const u32x4v_t*>(rp + 16 * c);
   }
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
@@ -813,9 +815,9 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_down_er(
     for (int wd = 0; wd < NW; ++wd) c += s_cw[tid][wd];
     s_c[tid] = c;
   }
-  f32x4d_t acc[BPW];
+  f32x4d_t acc[BPW][2];  // per word half: a block's MFMAs are independent
 #pragma unroll
-  for (int j = 0; j < BPW; ++j) acc[j] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < BPW; ++j) acc[j][0] = acc[j][1] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
   const ExpandConsts kc;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -835,12 +837,15 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_down_er(
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-        for (int j = 0; j < BPW; ++j) mfma_acc(acc[j], av[j][hf], bv[hf]);
+        for (int j = 0; j < BPW; ++j) mfma_acc(acc[j][hf], av[j][hf], bv[hf]);
       mfma_block_end();
-      keep_b(av, acc);
-      keep_b(bv, acc);
+      keep_b(av, acc[0]);
+      keep_b(bv, acc[0]);
     }
   }
+  f32x4d_t accs[BPW];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) accs[j] = acc[j][0] + acc[j][1];
   __syncthreads();  // s_c
   if (r16 >= np) return;
   const float cc = s_c[r16];
@@ -852,7 +857,7 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_down_er(
     const int64_t n0 = blk * 16 + 4 * g;
     float o[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) o[r] = ld_t<ADT>(alpha, static_cast<int64_t>(e) * n_out + n0 + r) * (acc[j][r] - cc);
+    for (int r = 0; r < 4; ++r) o[r] = ld_t<ADT>(alpha, static_cast<int64_t>(e) * n_out + n0 + r) * (accs[j][r] - cc);
     uint2 rr;
     rr.x = pack_bf16x2_rn(o[0], o[1]);
     rr.y = pack_bf16x2_rn(o[2], o[3]);
