@@ -196,6 +196,69 @@ __device__ __forceinline__ float lane_bcast(float v, int src) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
 }
 
+// Wave-uniform max and sum without an LDS round trip: prefix steps within each
+// 16-lane row (row_shr 1, 2, 4, 8), then row_bcast:15 (rows 1 and 3 take the
+// row below's lane 15) and row_bcast:31 (rows 2 and 3 take lane 31) carry the
+// total into lane 63, which is read back as a scalar.  Lanes whose DPP source
+// is outside the row or in a masked row keep `old` (the identity).
+#define MA_DPP_OLD(old, v, ctrl, rmask)                                                 \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, (old)), \
+                                                        __builtin_bit_cast(int, (v)), (ctrl), (rmask), 0xF, false))
+
+__device__ __forceinline__ float wave_max_u(float v) {
+  v = fmaxf(v, MA_DPP_OLD(v, v, 0x111, 0xF));
+  v = fmaxf(v, MA_DPP_OLD(v, v, 0x112, 0xF));
+  v = fmaxf(v, MA_DPP_OLD(v, v, 0x114, 0xF));
+  v = fmaxf(v, MA_DPP_OLD(v, v, 0x118, 0xF));
+  v = fmaxf(v, MA_DPP_OLD(v, v, 0x142, 0xA));
+  v = fmaxf(v, MA_DPP_OLD(v, v, 0x143, 0xC));
+  return lane_bcast(v, 63);
+}
+
+// Sum over aligned groups of WIDTH lanes (16, 32 or 64), complete only in the
+// last lane of each group (the same prefix steps, no LDS round trip).
+template <int WIDTH>
+__device__ __forceinline__ float group_sum_last(float v) {
+  static_assert(WIDTH == 16 || WIDTH == 32 || WIDTH == 64, "group width");
+  v += MA_DPP_OLD(0.f, v, 0x111, 0xF);
+  v += MA_DPP_OLD(0.f, v, 0x112, 0xF);
+  v += MA_DPP_OLD(0.f, v, 0x114, 0xF);
+  v += MA_DPP_OLD(0.f, v, 0x118, 0xF);
+  if constexpr (WIDTH >= 32) v += MA_DPP_OLD(0.f, v, 0x142, 0xA);
+  if constexpr (WIDTH == 64) v += MA_DPP_OLD(0.f, v, 0x143, 0xC);
+  return v;
+}
+
+// Integer form of wave_max_u (v_max_i32 needs no NaN canonicalisation).
+__device__ __forceinline__ int wave_max_ui(int v) {
+#define MA_DPP_I(v, ctrl, rmask) __builtin_amdgcn_update_dpp(INT_MIN, (v), (ctrl), (rmask), 0xF, false)
+  v = max(v, MA_DPP_I(v, 0x111, 0xF));
+  v = max(v, MA_DPP_I(v, 0x112, 0xF));
+  v = max(v, MA_DPP_I(v, 0x114, 0xF));
+  v = max(v, MA_DPP_I(v, 0x118, 0xF));
+  v = max(v, MA_DPP_I(v, 0x142, 0xA));
+  v = max(v, MA_DPP_I(v, 0x143, 0xC));
+#undef MA_DPP_I
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+// Signed-integer key with the order of the float v (for every non-NaN v).
+__device__ __forceinline__ int float_order_key(float v) {
+  const int b = __float_as_int(v);
+  return b ^ ((b >> 31) & 0x7fffffff);
+}
+__device__ __forceinline__ float float_from_order_key(int k) { return __int_as_float(k ^ ((k >> 31) & 0x7fffffff)); }
+
+__device__ __forceinline__ float wave_sum_u(float v) {
+  v += MA_DPP_OLD(0.f, v, 0x111, 0xF);
+  v += MA_DPP_OLD(0.f, v, 0x112, 0xF);
+  v += MA_DPP_OLD(0.f, v, 0x114, 0xF);
+  v += MA_DPP_OLD(0.f, v, 0x118, 0xF);
+  v += MA_DPP_OLD(0.f, v, 0x142, 0xA);
+  v += MA_DPP_OLD(0.f, v, 0x143, 0xC);
+  return lane_bcast(v, 63);
+}
+
 // Block-wide sum over 256 threads; every thread gets the total.
 __device__ __forceinline__ float block_sum256(float v, float* red) {
   v = group_sum<64>(v);

@@ -82,10 +82,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   __shared__ float cw[NWH];
   __shared__ __align__(16) uint32_t hs[TK][NWI][8];
   __shared__ float hc[TK][NWI];
-  __shared__ float s_p[64 * PER];
-  __shared__ int s_rank[kFusedWaves][64 * PER];
-  __shared__ int32_t s_ids[kFusedWaves][TK];  // one copy per wave
-  __shared__ float s_wts[kFusedWaves][TK];
+  __shared__ int32_t s_ids[TK];
+  __shared__ float s_wts[TK];
   __shared__ float red[kFusedWaves], red2[kFusedWaves];
   __shared__ float part[kFusedWaves][RPB];
   // next projection: y, and its RMS-folded x' pairs (hi and lo words, and the
@@ -219,13 +217,12 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     st_coh64(&logits[kLogitStride * wg], tag | __float_as_uint(l + (bias ? bias[wg] : 0.f)));
   }
 
-  // ---- 2. softmax + top-k in every workgroup (router semantics of reference
-  // kernels/router.py:78-126), once wave 0 has seen all E logits of this call
-  // (each lane polls its tagged logit words until they carry this call's tag).
-  // The rank of an expert (experts with a larger probability, or an equal one
-  // at a lower index) is counted by all four waves over a quarter of the
-  // experts each; then every wave finds, per slot s, the expert of rank s by
-  // a ballot, so each wave holds the routing without further hand-offs.
+  // ---- 2. softmax + top-k (router semantics of reference kernels/router.py:
+  // 78-126), by wave 0 of every workgroup once it has seen all E logits of
+  // this call (each lane polls its tagged logit words until they carry this
+  // call's tag).  Slot s takes the largest probability left (the lowest expert
+  // index among equal ones) -- one wave-wide max and one ballot per slot, all
+  // in registers -- and the routing goes to the other waves through LDS.
   if (wv == 0) {
     float p[PER];
     bool have[PER];
@@ -249,10 +246,10 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
       __builtin_amdgcn_s_sleep(2);
       timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
     }
-    float m = -INFINITY;
+    int mk = INT_MIN;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) m = fmaxf(m, p[i]);
-    m = wave_max(m);
+    for (int i = 0; i < PER; ++i) mk = max(mk, float_order_key(p[i]));
+    const float m = float_from_order_key(wave_max_ui(mk));
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -260,75 +257,47 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
       p[i] = e < n_exp ? expf(p[i] - m) : 0.f;
       sum += p[i];
     }
-    const float inv_sum = 1.0f / group_sum<64>(sum);
+    const float inv_sum = 1.0f / wave_sum_u(sum);
+    // probabilities are >= 0, so their bits order as integers; experts past
+    // E get -1 (below every probability), chosen ones INT_MIN
+    int key[PER];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int e = lane + 64 * i;
-      s_p[e] = e < n_exp ? p[i] * inv_sum : -INFINITY;
-    }
-  }
-  __syncthreads();
-  {
-    constexpr int NJ = 64 * PER / kFusedWaves;  // experts each wave compares against
-    float p[PER];
-    int rank[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      p[i] = s_p[lane + 64 * i];
-      rank[i] = 0;
-    }
-    const int j0 = wv * NJ;
-#pragma unroll
-    for (int jj = 0; jj < NJ; jj += 4) {
-      const float4 q4 = *reinterpret_cast<const float4*>(&s_p[j0 + jj]);  // same address in every lane
-      const float q[4] = {q4.x, q4.y, q4.z, q4.w};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int j = j0 + jj + t;
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-          rank[i] += (q[t] > p[i]) || (q[t] == p[i] && j < lane + 64 * i);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < PER; ++i) s_rank[wv][lane + 64 * i] = rank[i];
-  }
-  __syncthreads();
-  {
-    float p[PER], sel = 0.f;
-    int rank[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int e = lane + 64 * i;
-      p[i] = s_p[e];
-      rank[i] = s_rank[0][e];
-#pragma unroll
-      for (int w = 1; w < kFusedWaves; ++w) rank[i] += s_rank[w][e];
-      sel += rank[i] < TK ? p[i] : 0.f;  // invalid experts (p = -inf) rank behind every valid one
-    }
-    const float inv_total = 1.0f / (group_sum<64>(sel) + 1e-20f);
+    for (int i = 0; i < PER; ++i) key[i] = lane + 64 * i < n_exp ? __float_as_int(p[i] * inv_sum) : -1;
+    int my_e = 0;
+    float my_p = 0.f, sel = 0.f;
 #pragma unroll
     for (int s = 0; s < TK; ++s) {
-      int e_s = 0;
-      float p_s = 0.f;
+      int lk = key[0];
 #pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const uint64_t hit = __ballot(rank[i] == s);
-        if (hit) {
-          const int l = __builtin_ctzll(hit);
-          e_s = l + 64 * i;
-          p_s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[i]), l));
-        }
+      for (int i = 1; i < PER; ++i) lk = max(lk, key[i]);
+      const int mx = wave_max_ui(lk);
+      int e_s = 0;
+#pragma unroll
+      for (int i = PER - 1; i >= 0; --i) {  // the lowest i with a hit wins: the lowest expert index
+        const uint64_t hit = __ballot(key[i] == mx);
+        if (hit) e_s = __builtin_ctzll(hit) + 64 * i;
       }
-      // every lane writes the same values, so each lane's later reads follow its own writes
-      s_ids[wv][s] = e_s;
-      s_wts[wv][s] = p_s * inv_total;
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        if (lane + 64 * i == e_s) key[i] = INT_MIN;
+      const float p_s = __int_as_float(mx);
+      sel += p_s;
+      if (lane == s) {
+        my_e = e_s;
+        my_p = p_s;
+      }
+    }
+    const float inv_total = 1.0f / (sel + 1e-20f);
+    if (lane < TK) {
+      s_ids[lane] = my_e;
+      s_wts[lane] = my_p * inv_total;
+      if (wg == 0) {
+        ids_out[lane] = my_e;
+        wts_out[lane] = my_p * inv_total;
+      }
     }
   }
-  if (wg == 0 && wv == 0 && lane < TK) {
-    ids_out[lane] = s_ids[0][lane];
-    wts_out[lane] = s_wts[0][lane];
-  }
+  __syncthreads();
 
   // ---- 3. weights: SwiGLU rows of this wave's h outputs, then the down rows
   // of this workgroup's y rows (every load issued before any arithmetic)
@@ -341,7 +310,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     int ug_i = o0 + u * PPI + pi;
     ug_i = ug_i < TK * I ? ug_i : TK * I - 1;
     const int s = ug_i / I, j = ug_i % I;
-    const int64_t e = clamp_id(s_ids[wv][s], n_exp);
+    const int64_t e = clamp_id(s_ids[s], n_exp);
     const int64_t row = e * (2 * I) + j + half * I;
     load_words_v<KWH>(ug + row * NWH + klh * KWH, wu[u]);
     au[u] = bf16_to_f32(ug_alpha[row]);
@@ -354,8 +323,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   for (int q = 0; q < SPW; ++q) {
     const int js = wv + kFusedWaves * q;
     const int jj = js < TK ? js : 0;  // idle waves (TK < waves) read slot 0 and add nothing
-    const int64_t e = clamp_id(s_ids[wv][jj], n_exp);
-    wj[q] = js < TK ? s_wts[wv][jj] : 0.f;
+    const int64_t e = clamp_id(s_ids[jj], n_exp);
+    wj[q] = js < TK ? s_wts[jj] : 0.f;
 #pragma unroll
     for (int u = 0; u < UD; ++u) {
       int r = rbase + u * RPID + subd;
@@ -388,13 +357,25 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     XSlice<KWH> xsl;
     slice_from_lds<KWH>(xs, cw, klh, xsl);
     const ExpandConsts kc;
+    // output t = u * PPI + pi of this wave: its up row sums in lane group pi,
+    // its gate row in group PPI + pi; lane t gathers both, then one SwiGLU
+    // evaluation and one store for all of the wave's outputs
+    float up_t = 0.f, gate_t = 0.f;
 #pragma unroll
     for (int u = 0; u < US; ++u) {
-      const float v = group_sum<LPRH>(slice_dot<KWH>(wu[u], xsl, kc) * au[u]);
-      const float g = __shfl(v, lane + PPI * LPRH, 64);
-      const int ug_i = o0 + u * PPI + pi;
-      if (half == 0 && klh == 0 && ug_i < TK * I) st_coh16(&hbuf[ug_i], f32_to_bf16(swiglu_act(v, g)));
+      const float v = group_sum_last<LPRH>(slice_dot<KWH>(wu[u], xsl, kc) * au[u]);
+#pragma unroll
+      for (int q = 0; q < PPI; ++q) {
+        const float up = lane_bcast(v, q * LPRH + LPRH - 1);
+        const float gt = lane_bcast(v, (PPI + q) * LPRH + LPRH - 1);
+        if (lane == u * PPI + q) {
+          up_t = up;
+          gate_t = gt;
+        }
+      }
     }
+    const int ug_i = o0 + lane;
+    if (lane < OPW && ug_i < TK * I) st_coh16(&hbuf[ug_i], f32_to_bf16(swiglu_act(up_t, gate_t)));
   }
   __builtin_amdgcn_s_waitcnt(0);  // this workgroup's h stores have completed
   __syncthreads();
