@@ -189,6 +189,28 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
         for (int q = 0; q < 16; ++q) v[i][q] = bf16_to_f32(f32_to_bf16(v[i][q] * rstd * nw[i][q]));
       }
     }
+    // the router logit first (the bf16 x words against router row wg), so
+    // that it goes out before this workgroup stages its x' pairs
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+      if (tid + 256 * i < NWH) {
+        const uint32_t g[8] = {gr[i][0].x, gr[i][0].y, gr[i][0].z, gr[i][0].w,
+                               gr[i][1].x, gr[i][1].y, gr[i][1].z, gr[i][1].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dot = dot2(pack_bf16x2(v[i][2 * j], v[i][2 * j + 1]), g[j], dot);
+      }
+    }
+    if (router_wg) {
+      const float s = group_sum<64>(dot);
+      if (lane == 0) red2[wv] = s;
+    }
+    __syncthreads();
+    if (router_wg && tid == 0) {
+      float l = red2[0];
+#pragma unroll
+      for (int w = 1; w < kFusedWaves; ++w) l += red2[w];
+      st_coh64(&logits[kLogitStride * wg], tag | __float_as_uint(l + (bias ? bias[wg] : 0.f)));
+    }
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
       const int w = tid + 256 * i;
@@ -197,24 +219,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
         cw[w] = prep_word_pairs(v[i], pr);
 #pragma unroll
         for (int j = 0; j < 8; ++j) xs[w][j] = pr[j];
-        // the bf16 x words themselves, against the router row
-        const uint32_t g[8] = {gr[i][0].x, gr[i][0].y, gr[i][0].z, gr[i][0].w,
-                               gr[i][1].x, gr[i][1].y, gr[i][1].z, gr[i][1].w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) dot = dot2(pack_bf16x2(v[i][2 * j], v[i][2 * j + 1]), g[j], dot);
       }
     }
-  }
-  if (router_wg) {
-    const float s = group_sum<64>(dot);
-    if (lane == 0) red2[wv] = s;
-  }
-  __syncthreads();
-  if (router_wg && tid == 0) {
-    float l = red2[0];
-#pragma unroll
-    for (int w = 1; w < kFusedWaves; ++w) l += red2[w];
-    st_coh64(&logits[kLogitStride * wg], tag | __float_as_uint(l + (bias ? bias[wg] : 0.f)));
   }
 
   // ---- 2. softmax + top-k (router semantics of reference kernels/router.py:
