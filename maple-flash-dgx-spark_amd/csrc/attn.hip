@@ -187,8 +187,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   // of the launch on the sync area's last 33 lines, then each workgroup
   // computes its rows of o from the whole attention output.
   uint32_t* const gsub = sync + kSyncLine * (1 + 2 * gridDim.z * nkv);
-  uint32_t* const gtop = gsub + kSyncLine * kBarGroups;
-  uint32_t* const gflags = gtop + kSyncLine;
+  uint32_t* const gflags = gsub + kSyncLine * (kBarGroups + 1);
   const int wgl = (static_cast<int>(b) * static_cast<int>(gridDim.y) + kvh) * static_cast<int>(gridDim.x) + sp;
   const int n_wg = static_cast<int>(gridDim.x * gridDim.y * gridDim.z);
   const uint32_t f0o = o_w && wv == 0 ? ld_coh32(&gflags[kSyncLine * (wgl % kBarGroups)]) : 0u;
@@ -561,7 +560,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   __builtin_amdgcn_s_waitcnt(0);  // this workgroup's output stores have completed
   __syncthreads();
   bool o_timed_out = false;
-  if (wv == 0) o_timed_out = grid_barrier(gsub, gtop, gflags, f0o, n_wg, wgl, lane, t0);
+  if (wv == 0) o_timed_out = grid_barrier_flags(gsub, gflags, f0o, n_wg, wgl, lane, t0);
   __syncthreads();
   {  // entry (i, half, l) of os4 = values 8 half .. + 8 of word l * kOWords + i
     const int w = tid >> 1, half = tid & 1;
@@ -608,7 +607,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
 
 // Sync area: line 0 (word 2: timeout), then per (row, KV head) an arrival
 // counter line and a generation line, then the O projection's grid barrier
-// (16 sub-counter lines, a top counter line, 16 release-flag lines).
+// (16 group-counter lines, one unused line, 16 group-flag lines).
 size_t sync_bytes(int64_t batch, int nkv) {
   return (1 + 2 * static_cast<size_t>(batch) * nkv + 2 * kBarGroups + 1) * kSyncLine * sizeof(uint32_t);
 }

@@ -34,37 +34,39 @@ __device__ __forceinline__ void st_coh16(uint16_t* p, uint16_t v) {
 }
 
 // Grid barrier, run by all 64 lanes of wave 0 of every workgroup once its
-// global stores (and its read of the release flag, f_old) have completed.
-// Workgroup wg arrives on sub-counter wg % kBarGroups; the last arriver there
-// clears it and arrives on the top counter; the last arriver on top clears
-// that and writes f_old + 1 to all kBarGroups flags (one lane each), so the
-// flags always hold equal values and nothing needs clearing afterwards.  The
-// others poll their group's flag until it leaves f_old.  (One atomic per
-// workgroup on a single counter would serialise all G of them at one
-// address.)  Needs G >= kBarGroups, every workgroup resident.  Returns true
-// (on all lanes) if the wait timed out.
-__device__ inline bool grid_barrier(uint32_t* sub, uint32_t* top, uint32_t* flags, uint32_t f_old, int G,
-                             int wg, int lane, uint64_t t0) {
+// global stores (and its read of its group's flag, f_old) have completed.
+// Workgroup wg arrives on counter wg % kBarGroups of its group; the group's
+// last arriver clears the counter and writes f_old + 1 to the group's flag,
+// and every workgroup polls all kBarGroups group flags, one lane each, until
+// none holds f_old any more.  The flags thus all hold the number of barriers
+// passed once a barrier is over, and nothing needs clearing afterwards.  (One
+// atomic per workgroup on a single counter would serialise all G of them at
+// one address; a second level of counters above the groups put one more
+// returning atomic on the last arrival's path, about 0.2 us slower per
+// barrier; polling never-cleared counters directly collided with the
+// arrivals and took 2 us.)  Needs G >= kBarGroups, every workgroup
+// resident.  Returns true (on all lanes) if the wait timed out.
+__device__ inline bool grid_barrier_flags(uint32_t* sub, uint32_t* flags, uint32_t f_old, int G, int wg, int lane,
+                                          uint64_t t0) {
   const int g = wg % kBarGroups;
-  int release = 0;
   if (lane == 0) {
     const uint32_t n_g = static_cast<uint32_t>((G - g + kBarGroups - 1) / kBarGroups);
     if (atomicAdd(&sub[kLine * g], 1u) == n_g - 1) {
       st_coh32(&sub[kLine * g], 0u);
-      if (atomicAdd(top, 1u) == static_cast<uint32_t>(kBarGroups - 1)) {
-        st_coh32(top, 0u);
-        release = 1;
-      }
+      st_coh32(&flags[kLine * g], f_old + 1u);
     }
   }
-  if (__shfl(release, 0, 64) && lane < kBarGroups) st_coh32(&flags[kLine * lane], f_old + 1u);
   int timed_out = 0;
-  if (lane == 0)
-    while (ld_coh32(&flags[kLine * g]) == f_old && !timed_out) {
-      __builtin_amdgcn_s_sleep(2);
-      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+  for (;;) {
+    const bool seen = lane >= kBarGroups || ld_coh32(&flags[kLine * lane]) != f_old;
+    if (__all(seen)) break;
+    if ((__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin) {
+      timed_out = 1;
+      break;
     }
-  return __shfl(timed_out, 0, 64) != 0;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return timed_out != 0;
 }
 
 // Device-coherent 8- and 16-byte access through a buffer resource: the sc1 cache policy (the bit agent-scope atomic loads and

@@ -19,7 +19,8 @@
 //      and runs softmax + top-k itself;
 //   3. it issues its SwiGLU and down-projection weight loads (known once the
 //      ids are), computes its slice of the 8 x I SwiGLU outputs, publishes it;
-//   grid barrier (a two-level arrival tree, per-group release flags);
+//   grid barrier (per-group arrival counters; each group's last arriver
+//   sets the group's flag, and every workgroup polls all group flags);
 //   4. it stages h and finishes its rows of y.
 // (Polling all of h directly instead of the barrier measured slower: every
 // workgroup re-reading 12+ KB while the last outputs land loads the same
@@ -39,11 +40,11 @@ constexpr int kFusedWaves = 4;
 // Workspace layout (256-byte lines of uint32 words; every counter and flag has
 // a line of its own so that arrivals and polls on different ones do not meet):
 //   line 0, word 2     error (1 = a wait timed out)
-//   lines 1 .. 16, 17  h barrier: sub-counters, top counter
-//   lines 18 .. 33     release flags, all holding the number of barriers
-//                      passed on this workspace
-//   lines 34 .. 49, 50 y barrier (calls with a next projection): sub-counters,
-//                      top counter
+//   lines 1 .. 16      h barrier: group arrival counters (line 17 unused)
+//   lines 18 .. 33     group flags, all holding the number of barriers
+//                      passed on this workspace once a barrier is over
+//   lines 34 .. 49     y barrier (calls with a next projection): group
+//                      arrival counters (line 50 unused)
 //   [16 KB, 48 KB)     router logits: one tagged 64-bit word (tag << 32 |
 //                      float bits) per expert every 128 bytes, E <= 256
 //   [48 KB ...)        h, bf16 [TK * I]
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   __builtin_amdgcn_s_waitcnt(0);  // this workgroup's h stores have completed
   __syncthreads();
   // ---- 4. barrier (all of h out), stage h, finish this workgroup's rows of y
-  if (wv == 0) timed_out = grid_barrier(ws + kLine * kSubB, ws + kLine * kTopB, flags, f0, G, wg, lane, t0) || timed_out;
+  if (wv == 0) timed_out = grid_barrier_flags(ws + kLine * kSubB, flags, f0, G, wg, lane, t0) || timed_out;
   __syncthreads();
   {
     constexpr int HIT = (TK * NWI + 255) / 256;  // h words per thread, all loads issued first
@@ -470,8 +471,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     __builtin_amdgcn_s_waitcnt(0);  // this workgroup's y stores have completed
     __syncthreads();
     if (wv == 0)
-      timed_out = grid_barrier(ws + kLine * kSubC, ws + kLine * kTopC, flags, f0 + 1u, G, wg, lane, t0) ||
-                  timed_out;
+      timed_out = grid_barrier_flags(ws + kLine * kSubC, flags, f0 + 1u, G, wg, lane, t0) || timed_out;
     __syncthreads();  // every wave waits for the barrier before reading y
     {  // y (device-coherent) into LDS, and its x' pairs: thread t builds pairs
        // j0 .. j0 + 3 of word t / 2 (j0 = 4 (t & 1)), each from values j and
