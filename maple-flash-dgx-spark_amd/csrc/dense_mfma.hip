@@ -418,10 +418,29 @@ __global__ __launch_bounds__(64 * KW) void k_tgemm_ks(
 
 // ---------------------------------------------------------------------------
 // RTN4: y[t, n] = sum_g s[n,g] (sum_{k in g} q x) + b[n,g] sum_{k in g} x.
-// GW = words per RTN group (8: group 64, 16: group 128).  Lane group g takes
-// words g, g + 4, g + 8, g + 12 of a chunk, so k-slice s covers words
-// 4s .. 4s+3 and a group is a run of whole k-slices.
+// GW = words per RTN group (8: group 64, 16: group 128).  Lane group g loads
+// its words of a chunk with vector loads (one 16-byte load of words 4g ..
+// 4g+3 for GW = 16; two 8-byte loads of words 2g, 2g+1 and 8+2g, 9+2g for
+// GW = 8), and k-slice s takes word chunk_word(g, s) of each lane group, so
+// that every k-slice lies in one RTN group.
 // ---------------------------------------------------------------------------
+template <int GW>
+__device__ __forceinline__ int chunk_word(int g, int s) {
+  if constexpr (GW == 16) return 4 * g + s;
+  else return s < 2 ? 2 * g + s : 8 + 2 * g + (s - 2);
+}
+
+template <int GW>
+__device__ __forceinline__ void load_chunk_words(const uint32_t* p, uint32_t (&q)[4]) {
+  if constexpr (GW == 16) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    q[0] = v.x, q[1] = v.y, q[2] = v.z, q[3] = v.w;
+  } else {
+    const uint2 a = *reinterpret_cast<const uint2*>(p), b = *reinterpret_cast<const uint2*>(p + 8);
+    q[0] = a.x, q[1] = a.y, q[2] = b.x, q[3] = b.y;
+  }
+}
+
 template <int NB, int GW, int SDT>
 __global__ __launch_bounds__(256) void k_rtn4_mfma(
     const uint16_t* __restrict__ x, int64_t batch, int64_t ldx, const uint32_t* __restrict__ w,
@@ -445,7 +464,7 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
   for (int mb = 0; mb < MB; ++mb) {
     int64_t r = row0 + 16 * mb + r16;
     r = r < n_out ? r : n_out - 1;
-    rowp[mb] = w + r * nwords + g;
+    rowp[mb] = w + r * nwords + (GW == 16 ? 4 * g : 2 * g);
   }
   f32x4d_t out[MB][NB], acc[MB][NB];
 #pragma unroll
@@ -454,9 +473,7 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
     for (int nb = 0; nb < NB; ++nb) out[mb][nb] = acc[mb][nb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
   uint32_t wq[MB][4];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) wq[mb][s] = rowp[mb][4 * s];
+  for (int mb = 0; mb < MB; ++mb) load_chunk_words<GW>(rowp[mb], wq[mb]);
   for (int64_t c0 = 0; c0 < nwords; c0 += kDenseChunk) {
     const int64_t gb = c0 / GW;  // first group of this chunk
     // Stage x' (16 x pairs) per (token, word) and the group sums X.
@@ -482,9 +499,7 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
     uint32_t wn[MB][4];
     const int64_t cn = c0 + kDenseChunk < nwords ? c0 + kDenseChunk : c0;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) wn[mb][s] = rowp[mb][cn + 4 * s];
+    for (int mb = 0; mb < MB; ++mb) load_chunk_words<GW>(rowp[mb] + cn, wn[mb]);
     // (no sched_barrier here: with loads into loop-carried registers just
     // above, it produced wrong MFMA operands on this compiler)
     if (tid < NT * GPC) xg[tid / GPC][tid % GPC] = 0.f;
@@ -518,20 +533,28 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
     }
     __syncthreads();
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {  // k-slice s: words 4s .. 4s+3 of the chunk
-      uint4 a[MB];
+    for (int s = 0; s < 4; ++s) {  // k-slice s: word chunk_word(g, s) of lane group g
+      // operands first, then one block of in-place MFMAs (the hand-spaced
+      // discipline of mfma.h: compiler-scheduled chains here gave wrong sums
+      // for some instantiations)
+      u32x4v_t av[MB], bv[NB];
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         const uint32_t wd = wq[mb][s];
-        a[mb] = make_uint4(and_or(wd << 3, kMaskQ4d, kOneBf16x2), and_or(wd >> 1, kMaskQ4d, kOneBf16x2),
-                           and_or(wd >> 5, kMaskQ4d, kOneBf16x2), and_or(wd >> 9, kMaskQ4d, kOneBf16x2));
+        av[mb] = u32x4v_t{and_or(wd << 3, kMaskQ4d, kOneBf16x2), and_or(wd >> 1, kMaskQ4d, kOneBf16x2),
+                          and_or(wd >> 5, kMaskQ4d, kOneBf16x2), and_or(wd >> 9, kMaskQ4d, kOneBf16x2)};
       }
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const uint4 b = *reinterpret_cast<const uint4*>(&xs[4 * s + g][nb * 16 + r16][0]);
+      for (int nb = 0; nb < NB; ++nb)
+        bv[nb] = *reinterpret_cast<const u32x4v_t*>(&xs[chunk_word<GW>(g, s)][nb * 16 + r16][0]);
+      mfma_block_begin();
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb][nb] = mfma16(a[mb], b, acc[mb][nb]);
-      }
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) mfma_acc(acc[mb][nb], av[mb], bv[nb]);
+      mfma_block_end();
+      keep_b(av, acc[0]);
+      keep_b(bv, acc[0]);
       if ((s + 1) % SPG == 0) {  // end of an RTN group: fold and clear
         const int gi = s / SPG;
 #pragma unroll
