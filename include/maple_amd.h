@@ -74,6 +74,30 @@ int ma_ternary_gemv_ws(const void* x, int x_dtype, int64_t batch, int64_t ldx,
                        void* stream);
 
 /*
+ * The grouped MoE's combine and the next RMS-folded ternary GEMM in the same
+ * two launches as ma_ternary_gemv_ws: x[t] = sum_j topk_weight[t, j] *
+ * slot_out[inverse[t, j]] (+ residual[t]) in float32, slot order, rounded to
+ * bf16 -- the values ma_moe_grouped's combine stores -- is written to x_out
+ * (bf16 [batch, nwords * 16]) and is the GEMM's x; y as ma_ternary_gemv_ws
+ * with that x.  slot_out is the per-pair down output ma_moe_grouped leaves at
+ * byte offset n_pairs * inter * 2 of its workspace (bf16 [n_pairs, hidden]);
+ * call ma_moe_grouped with y = NULL to skip its own combine.  Needs
+ * rms_weight, batch >= 17, nwords % 16 == 0, top_k <= 8, bf16 rows and
+ * 16-byte aligned buffers (returns MA_EVALUE otherwise); workspace as for
+ * ma_ternary_gemv_ws.  Reference counterpart: moe_reduce_add
+ * (src/maple_run/kernels/fused_norm.py:59-96) at the end of one decoder
+ * layer, then the next layer's input RMSNorm + QKV ternary_gemv
+ * (src/maple_run/kernels/ternary_gemv.py:261-388) -- one boundary crossing
+ * fewer per layer.
+ */
+int ma_ternary_gemv_combine_ws(const void* slot_out, const int32_t* inverse,
+                               const float* topk_weight, int64_t top_k, const void* residual,
+                               void* x_out, int64_t batch, const uint32_t* packed, int64_t n_out,
+                               int64_t nwords, const void* row_alpha, int alpha_dtype,
+                               const void* rms_weight, int rms_dtype, float rms_eps, void* y,
+                               int64_t ldy, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Router: logits = x @ W^T (+ bias), softmax over the experts, the top_k
  * largest probabilities in descending order (ties: lowest expert index) and
  * their renormalised weights p / (sum p_top + 1e-20).
@@ -227,7 +251,10 @@ int ma_moe_route(const void* x, const void* x_add, int64_t tokens, int64_t hidde
  * x_pairs / x_corr (optional, both or neither): x as ma_moe_route writes it
  * in x' pair form (uint32 [tokens, hidden / 2]) with each token's correction
  * (float32 [tokens]); decode batches then read the operands from there
- * instead of building them from x (x is still passed).
+ * instead of building them from x (x is still passed).  The per-pair down
+ * outputs stay in the workspace at byte offset tokens * top_k * inter * 2
+ * (bf16 [tokens * top_k, hidden]); with y = NULL the combine is skipped
+ * (ma_ternary_gemv_combine_ws can run it in front of the next GEMM).
  * Replaces MapleSparseMoeBlock's SwiGLU -> down -> moe_reduce_add chain
  * (src/maple_run/model.py:468-473) for token counts where experts see many
  * tokens; the reference instead runs one program per (token, slot).

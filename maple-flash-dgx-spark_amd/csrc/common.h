@@ -277,4 +277,16 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// A grouped MoE combine run in front of a kernel that reads its output rows
+// (k_xprep): y[t] = sum_j wts[t, j] * slot_out[inverse[t, j]] + res[t].
+struct CombineIn {
+  const uint16_t* slot_out;  // bf16 [pairs, K * 16] (null: read x)
+  const int32_t* inverse;    // [batch, topk] row of each (token, slot) in slot_out
+  const float* wts;          // [batch, topk]
+  int topk;                  // <= 8
+  const uint16_t* res;       // bf16 [batch, K * 16] or null
+  uint16_t* x_out;           // bf16 [batch, K * 16]: the combined rows
+};
+
+
 }  // namespace ma

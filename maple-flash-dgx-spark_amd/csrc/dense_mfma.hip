@@ -68,23 +68,89 @@ __device__ __forceinline__ void load_rms16(const void* p, int rdt, int64_t wd, f
 //   xp [tile][v][word][half][NT] uint4 (v: hi, lo);  xc [tile * NT + col] = (c, scale)
 // Tokens past the batch are zero.  Per word the arithmetic is the one-launch
 // GEMM's; the per-token sums add up in another order.
+// With a MoE combine in front (cb.slot_out set), x is not read: each word of
+// token t is first built as the grouped MoE's combine builds it (k_combine8:
+// sum_j w[t, j] * slot_out[inverse[t, j]] in slot order, + residual, rounded
+// to bf16), stored to cb.x_out, and then prepared as above.
 // ---------------------------------------------------------------------------
 constexpr int kXpTile = 32;  // tokens per tile of the two-launch form
+
 
 __global__ __launch_bounds__(128) void k_xprep(const uint16_t* __restrict__ x, int64_t batch,
                                                int64_t ldx, int64_t nwords,
                                                const void* __restrict__ rms_w, int rms_dt,
                                                float rms_eps, int nt, uint4* __restrict__ xp,
-                                               float2* __restrict__ xc) {
+                                               float2* __restrict__ xc, CombineIn cb) {
   __shared__ float red_c[128], red_s[128];
   const int64_t t = blockIdx.x;
   const int64_t tile = t / nt, col = t % nt;
   const int tid = threadIdx.x;
   const bool valid = t < batch;
   float c = 0.f, ss = 0.f;
+  // the combine's (row, weight) pairs of this token (scalar loads)
+  int64_t crow[8];
+  float cw[8];
+  if (cb.slot_out && valid) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      crow[j] = j < cb.topk ? cb.inverse[t * cb.topk + j] : 0;
+      cw[j] = j < cb.topk ? cb.wts[t * cb.topk + j] : 0.f;
+    }
+  }
   for (int64_t wd = tid; wd < nwords; wd += 128) {
     float v[16];
-    if (valid) {
+    if (valid && cb.slot_out) {
+      const int64_t n = nwords * 16;
+      uint4 sv[8][2], r[2] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < cb.topk) {
+          const uint4* src = reinterpret_cast<const uint4*>(cb.slot_out + crow[j] * n + wd * 16);
+          sv[j][0] = src[0];
+          sv[j][1] = src[1];
+        }
+      if (cb.res) {
+        const uint4* src = reinterpret_cast<const uint4*>(cb.res + t * n + wd * 16);
+        r[0] = src[0];
+        r[1] = src[1];
+      }
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        float a[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (j >= cb.topk) break;
+          const uint32_t u[4] = {sv[j][hf].x, sv[j][hf].y, sv[j][hf].z, sv[j][hf].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            a[2 * q] += cw[j] * __uint_as_float(u[q] << 16);
+            a[2 * q + 1] += cw[j] * __uint_as_float(u[q] & 0xffff0000u);
+          }
+        }
+        if (cb.res) {
+          const uint32_t u[4] = {r[hf].x, r[hf].y, r[hf].z, r[hf].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            a[2 * q] += __uint_as_float(u[q] << 16);
+            a[2 * q + 1] += __uint_as_float(u[q] & 0xffff0000u);
+          }
+        }
+        uint4 o;
+        o.x = pack_bf16x2_rn(a[0], a[1]);
+        o.y = pack_bf16x2_rn(a[2], a[3]);
+        o.z = pack_bf16x2_rn(a[4], a[5]);
+        o.w = pack_bf16x2_rn(a[6], a[7]);
+        reinterpret_cast<uint4*>(cb.x_out + t * n + wd * 16)[hf] = o;
+        const uint32_t ou[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v[8 * hf + 2 * q] = __uint_as_float(ou[q] << 16);
+          v[8 * hf + 2 * q + 1] = __uint_as_float(ou[q] & 0xffff0000u);
+        }
+      }
+    } else if (valid) {
       const uint4* src = reinterpret_cast<const uint4*>(x + t * ldx + wd * 16);
       const uint4 a = src[0], b = src[1];
       const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
@@ -620,12 +686,12 @@ size_t tgemm_xp_bytes(int64_t batch, int64_t nwords) {
 int launch_tgemm_xp(const uint16_t* x, int64_t batch, int64_t ldx, const uint32_t* w,
                     int64_t n_out, int64_t nwords, const void* alpha, int alpha_dt,
                     const void* rms_w, int rms_dt, float rms_eps, uint16_t* y, int64_t ldy,
-                    void* workspace, hipStream_t s) {
+                    void* workspace, hipStream_t s, const CombineIn& cb) {
   const int64_t tiles = cdiv(batch, kXpTile);
   uint4* xp = static_cast<uint4*>(workspace);
   float2* xc = reinterpret_cast<float2*>(xp + tiles * 2 * nwords * 2 * kXpTile);
   hipLaunchKernelGGL(k_xprep, dim3(static_cast<unsigned>(tiles * kXpTile)), dim3(128), 0, s, x,
-                     batch, ldx, nwords, rms_w, rms_dt, rms_eps, kXpTile, xp, xc);
+                     batch, ldx, nwords, rms_w, rms_dt, rms_eps, kXpTile, xp, xc, cb);
   dim3 grid(static_cast<unsigned>(cdiv(n_out, 16)), static_cast<unsigned>(tiles));
   if (alpha_dt == MA_F32)
     hipLaunchKernelGGL((k_tgemm_xpk<kXpTile / 16, 2, MA_F32, 8>), grid, dim3(512), 0, s, xp, xc,

@@ -106,7 +106,7 @@ size_t tgemm_xp_bytes(int64_t batch, int64_t nwords);
 int launch_tgemm_xp(const uint16_t* x, int64_t batch, int64_t ldx, const uint32_t* w,
                     int64_t n_out, int64_t nwords, const void* alpha, int alpha_dt,
                     const void* rms_w, int rms_dt, float rms_eps, uint16_t* y, int64_t ldy,
-                    void* workspace, hipStream_t s);
+                    void* workspace, hipStream_t s, const ma::CombineIn& cb);
 constexpr int64_t kMfmaMinBatch = 5;
 constexpr int64_t kXpMinBatch = 17;
 
@@ -177,5 +177,45 @@ extern "C" int ma_ternary_gemv_ws(const void* x, int x_dtype, int64_t batch, int
                 need, workspace_bytes, workspace);
   return launch_tgemm_xp(static_cast<const uint16_t*>(x), batch, ldx, packed, n_out, nwords,
                          row_alpha, alpha_dtype, rms_weight, rms_dtype, rms_eps,
-                         static_cast<uint16_t*>(y), ldy, workspace, static_cast<hipStream_t>(stream));
+                         static_cast<uint16_t*>(y), ldy, workspace, static_cast<hipStream_t>(stream),
+                         ma::CombineIn{});
+}
+
+extern "C" int ma_ternary_gemv_combine_ws(const void* slot_out, const int32_t* inverse,
+                                          const float* topk_weight, int64_t top_k,
+                                          const void* residual, void* x_out, int64_t batch,
+                                          const uint32_t* packed, int64_t n_out, int64_t nwords,
+                                          const void* row_alpha, int alpha_dtype,
+                                          const void* rms_weight, int rms_dtype, float rms_eps,
+                                          void* y, int64_t ldy, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  using namespace ma;
+  if (batch < 0 || n_out < 0 || nwords < 1)
+    return fail(MA_EVALUE, "ternary_gemv_combine: bad sizes batch=%lld n=%lld nwords=%lld",
+                (long long)batch, (long long)n_out, (long long)nwords);
+  if (batch == 0 || n_out == 0) return MA_OK;
+  if (!slot_out || !inverse || !topk_weight || !x_out || !packed || !row_alpha || !y || !rms_weight)
+    return fail(MA_EVALUE, "ternary_gemv_combine: null pointer");
+  if (top_k < 1 || top_k > 8) return fail(MA_EVALUE, "ternary_gemv_combine: top_k must be 1..8");
+  if (ldy < n_out) return fail(MA_EVALUE, "ternary_gemv_combine: leading dimension too small");
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (batch < kXpMinBatch ||
+      !mfma_ok(x_out, MA_BF16, batch, nwords * 16, packed, nwords, 0, alpha_dtype, rms_weight,
+               rms_dtype, y) ||
+      !a16(slot_out) || (residual && !a16(residual)))
+    return fail(MA_EVALUE,
+                "ternary_gemv_combine: needs >= %lld tokens, K a multiple of 256, bf16 rows and "
+                "16-byte aligned buffers",
+                (long long)kXpMinBatch);
+  const size_t need = tgemm_xp_bytes(batch, nwords);
+  if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255))
+    return fail(MA_EVALUE,
+                "ternary_gemv_combine: workspace of %zu bytes (256-byte aligned) needed, got %zu at %p",
+                need, workspace_bytes, workspace);
+  const CombineIn cb{static_cast<const uint16_t*>(slot_out), inverse, topk_weight,
+                     static_cast<int>(top_k), static_cast<const uint16_t*>(residual),
+                     static_cast<uint16_t*>(x_out)};
+  return launch_tgemm_xp(static_cast<const uint16_t*>(x_out), batch, nwords * 16, packed, n_out,
+                         nwords, row_alpha, alpha_dtype, rms_weight, rms_dtype, rms_eps,
+                         static_cast<uint16_t*>(y), ldy, workspace, static_cast<hipStream_t>(stream), cb);
 }

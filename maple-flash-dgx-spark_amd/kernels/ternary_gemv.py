@@ -97,3 +97,37 @@ def ternary_gemv(
     else:
         _lib.call("ma_ternary_gemv", *args, _lib.stream_of(x))
     return y.reshape(*leading, n_out)
+
+
+def ternary_gemv_combine(pending, packed_weight: torch.Tensor, row_alpha: torch.Tensor, *,
+                         rms_weight: torch.Tensor, rms_eps: float = 1e-6):
+    """A grouped MoE combine left pending by ``moe_grouped(..., combine=False)``
+    run in front of the next RMS-folded GEMM (``ma_ternary_gemv_combine_ws``):
+    ``x = sum_j w[t, j] * slot_out[inverse[t, j]] + residual`` (bf16, the
+    values ``moe_grouped`` would have returned), ``y = ternary_gemv(x, W,
+    alpha, rms_weight)``.  Returns ``(x, y)``.  Needs ``combine_gemv_supported``."""
+    n_out, nwords = packed_weight.shape
+    tokens, hidden = pending.tokens, pending.hidden
+    if hidden != nwords * _CODES_PER_WORD:
+        raise ValueError(f"combined rows have {hidden} values, the GEMM takes {nwords * _CODES_PER_WORD}.")
+    x = torch.empty(tokens, hidden, device=pending.slot_out.device, dtype=torch.bfloat16)
+    y = torch.empty(tokens, n_out, device=x.device, dtype=torch.bfloat16)
+    rms_w = rms_weight.reshape(-1).contiguous()
+    alpha = row_alpha.reshape(-1).contiguous()
+    ws_bytes = _lib.load().ma_ternary_gemv_workspace_bytes(tokens, nwords, 1)
+    ws = torch.empty(max(int(ws_bytes), 1), device=x.device, dtype=torch.uint8)
+    _lib.call(
+        "ma_ternary_gemv_combine_ws",
+        _lib.ptr(pending.slot_out), _lib.ptr(pending.inverse), _lib.ptr(pending.weights),
+        pending.top_k, _lib.ptr(pending.residual), _lib.ptr(x), tokens,
+        _lib.ptr(packed_weight.contiguous()), n_out, nwords, _lib.ptr(alpha),
+        _lib.dtype_code(alpha, "row_alpha"), _lib.ptr(rms_w), _lib.dtype_code(rms_w, "rms_weight"),
+        float(rms_eps), _lib.ptr(y), n_out, _lib.ptr(ws), ws.numel(), _lib.stream_of(x),
+    )
+    return x, y
+
+
+def combine_gemv_supported(tokens: int, top_k: int, packed_weight: torch.Tensor) -> bool:
+    """Where ``ternary_gemv_combine`` runs: 17+ tokens, top-k <= 8, K a
+    multiple of 256 (row-major packed codes)."""
+    return tokens >= 17 and 1 <= top_k <= 8 and packed_weight.ndim == 2 and packed_weight.shape[1] % 16 == 0

@@ -13,7 +13,9 @@ One decode step, per layer:
   fused_moe is left True, the last two lines are one launch:
   moe_fused(hidden, add=o, norm_weight=post_ln), which in forward() also
   computes the next layer's qkv line from its output, so only layer 0 runs
-  the standalone QKV projection)
+  the standalone QKV projection; from 17 tokens, with combine_next left True,
+  the grouped MoE's top-k combine is left to the next layer's QKV projection,
+  which builds hidden from the slot outputs in its operand launch)
 then seqlen += 1, final rms_norm, RTN4 lm_head, greedy argmax.
 
 Weights are random with the synthetic distributions (``synthetic.py``): every
@@ -33,8 +35,8 @@ from .kernels.decode_attn import decode_attention, gqa_workspace, o_projection_s
 from .kernels.fused_norm import rms_norm
 from .kernels.greedy import greedy_argmax
 from .kernels.rtn4 import rtn4_embedding, rtn4_gemv
-from .kernels.ternary_gemv import ternary_gemv
-from .moe import fused_supported, moe_fused, moe_layer
+from .kernels.ternary_gemv import combine_gemv_supported, ternary_gemv, ternary_gemv_combine
+from .moe import PendingCombine, fused_supported, moe_fused, moe_layer
 
 
 @dataclass
@@ -101,9 +103,10 @@ class KVCache:
 
 class SyntheticDecoder:
     def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 4096 + 128,
-                 fused_moe: bool = True, fused_o: bool = False):
+                 fused_moe: bool = True, fused_o: bool = False, combine_next: bool = True):
         self.cfg = cfg
         self.fused_moe = fused_moe
+        self.combine_next = combine_next
         self.fused_o = fused_o
         self.device = torch.device(device)
         self.max_len = max_len
@@ -144,8 +147,13 @@ class SyntheticDecoder:
         """Layer ``i``; returns ``(y, next_qkv)``.  ``qkv``: this layer's input
         projection if an earlier launch already computed it.  ``next_qkv`` is
         layer ``i + 1``'s projection when the one-launch MoE kernel computed it
-        from ``y`` (batch 1, ``fuse_next``), else None."""
+        from ``y`` (batch 1, ``fuse_next``), else None.  ``y`` is a
+        ``PendingCombine`` where layer ``i + 1``'s QKV launch runs the MoE
+        combine (``combine_next``, 17+ tokens); ``hidden`` may be one."""
         c, L = self.cfg, self.layers[i]
+        if isinstance(hidden, PendingCombine):  # the previous layer's MoE combine runs here
+            hidden, qkv = ternary_gemv_combine(hidden, L.qkv, L.qkv_alpha, rms_weight=L.input_ln,
+                                               rms_eps=c.eps)
         bsz = hidden.shape[0]
         if qkv is None:
             qkv = ternary_gemv(hidden, L.qkv, L.qkv_alpha, rms_weight=L.input_ln, rms_eps=c.eps)
@@ -178,7 +186,10 @@ class SyntheticDecoder:
         else:
             # add + RMSNorm + router + dispatch in one launch from 4 tokens,
             # then the grouped experts
-            y, ids = moe_layer(hidden, L.moe, c.top_k, L.post_ln, c.eps, add=o.reshape(hidden.shape))
+            defer = (self.combine_next and fuse_next and i + 1 < c.layers
+                     and combine_gemv_supported(bsz, c.top_k, self.layers[i + 1].qkv))
+            y, ids = moe_layer(hidden, L.moe, c.top_k, L.post_ln, c.eps, add=o.reshape(hidden.shape),
+                               defer_combine=defer)
         if routing is not None:
             routing.append(ids)
         return y, next_qkv

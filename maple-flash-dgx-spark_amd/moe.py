@@ -26,6 +26,8 @@ device):
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 
 from . import _lib
@@ -199,14 +201,31 @@ def moe_route(x: torch.Tensor, layer: MoELayer, top_k: int, norm_weight: torch.T
     return h, xn, ids, wts, d
 
 
+@dataclass
+class PendingCombine:
+    """A grouped MoE layer whose top-k combine has not run yet: ``y[t] =
+    sum_j weights[t, j] * slot_out[inverse[t, j]] + residual[t]``.  The next
+    RMS-folded GEMM runs it (``kernels.ternary_gemv.ternary_gemv_combine``);
+    ``workspace`` keeps ``slot_out``'s storage alive."""
+    slot_out: torch.Tensor   # bf16 [T * k, H], inside workspace
+    inverse: torch.Tensor    # int32 [T * k]
+    weights: torch.Tensor    # float32 [T * k]
+    residual: torch.Tensor | None
+    top_k: int
+    tokens: int
+    hidden: int
+    workspace: torch.Tensor
+
+
 def moe_grouped(x: torch.Tensor, layer: MoELayer, ids: torch.Tensor, wts: torch.Tensor,
                 residual: torch.Tensor | None = None, *, return_h: bool = False, dispatch=None,
-                x_pairs=None):
+                x_pairs=None, combine: bool = True):
     """Dispatch + grouped MFMA SwiGLU/down + combine for ``x [T, H]`` (bf16).
 
     ``dispatch``: the lists for ``ids`` if already built (``moe_route``);
     ``x_pairs``: ``(xn_pairs, xn_corr)`` of ``x`` from ``moe_route(pairs=True)``.
-    Returns ``y [T, H]`` (bf16), and with ``return_h`` also ``h [T, k, I]``.
+    Returns ``y [T, H]`` (bf16), and with ``return_h`` also ``h [T, k, I]``;
+    with ``combine=False`` a ``PendingCombine`` in place of ``y``.
     """
     tokens, hidden = x.shape
     top_k = int(ids.shape[-1])
@@ -215,7 +234,7 @@ def moe_grouped(x: torch.Tensor, layer: MoELayer, ids: torch.Tensor, wts: torch.
     n_pairs = tokens * top_k
     nbytes = int(_lib.load().ma_grouped_workspace_bytes(n_pairs, inter, hidden))
     ws = torch.empty(nbytes, device=x.device, dtype=torch.uint8)
-    y = torch.empty(tokens, hidden, device=x.device, dtype=torch.bfloat16)
+    y = torch.empty(tokens, hidden, device=x.device, dtype=torch.bfloat16) if combine else None
     h = torch.empty(n_pairs, inter, device=x.device, dtype=torch.bfloat16) if return_h else None
     res = None if residual is None else residual.reshape(tokens, hidden).contiguous()
     xc = x.contiguous()
@@ -234,6 +253,11 @@ def moe_grouped(x: torch.Tensor, layer: MoELayer, ids: torch.Tensor, wts: torch.
         _lib.ptr(res), _lib.dtype_code(res, "residual") if res is not None else 0,
         _lib.ptr(h), inter, _lib.ptr(y), _lib.ptr(ws), ws.numel(), _lib.stream_of(x),
     )
+    if not combine:
+        # the per-pair down outputs sit after the pair-format h in the workspace
+        off = n_pairs * inter * 2
+        slot_out = ws[off:off + n_pairs * hidden * 2].view(torch.bfloat16).view(n_pairs, hidden)
+        y = PendingCombine(slot_out, d.inverse, w, res, top_k, tokens, hidden, ws)
     if return_h:
         return y, h.reshape(tokens, top_k, inter)
     return y
@@ -265,18 +289,19 @@ def moe_block(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
 
 
 def moe_layer(hidden: torch.Tensor, layer: MoELayer, top_k: int, norm_weight: torch.Tensor,
-              eps: float, add: torch.Tensor | None = None):
+              eps: float, add: torch.Tensor | None = None, defer_combine: bool = False):
     """Post-attention half of a decoder layer for ``hidden [T, H]``:
     ``h = hidden + add``, ``y = h + MoE(rms_norm(h) * norm_weight)``.
     Returns ``(y, ids)``.  From GROUPED_MIN_TOKENS tokens the add, norm, router
-    and dispatch are one launch (``moe_route``) ahead of the grouped experts."""
+    and dispatch are one launch (``moe_route``) ahead of the grouped experts;
+    there, ``defer_combine`` returns a ``PendingCombine`` in place of ``y``."""
     from .kernels.fused_norm import add_rms_norm, rms_norm
     tokens = hidden.shape[0]
     if (tokens >= GROUPED_MIN_TOKENS and route_supported(layer, top_k, hidden)
             and hidden.shape[-1] % 256 == 0 and layer.inter % 256 == 0):
         h, xn, ids, wts, d, xp = moe_route(hidden, layer, top_k, norm_weight, eps, add=add,
                                            pairs=True)
-        return moe_grouped(xn, layer, ids, wts, h, dispatch=d, x_pairs=xp), ids
+        return moe_grouped(xn, layer, ids, wts, h, dispatch=d, x_pairs=xp, combine=not defer_combine), ids
     if add is not None:
         h, xn = add_rms_norm(hidden, add, norm_weight, eps)
     else:

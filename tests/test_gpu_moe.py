@@ -191,3 +191,29 @@ def test_moe_route_equals_separate_launches(dev, tokens, n_exp, hidden, with_add
     assert all(int(ws.count_nonzero()) == 0 for ws in _ROUTE_WS.values())
     if tokens <= 128:
         _check_routing(xn, L, ids, wts, k)
+
+
+@pytest.mark.parametrize("tokens", [17, 32, 128])
+def test_combine_in_front_of_next_gemv_equals_separate(dev, layer, tokens):
+    """ma_ternary_gemv_combine_ws: the grouped MoE's combine run in the next
+    RMS-folded GEMM's operand launch gives, bit for bit, the combined rows
+    moe_grouped returns and the GEMM of those rows; twice in a row."""
+    from maple_amd.kernels import ternary_gemv
+    from maple_amd.kernels.ternary_gemv import combine_gemv_supported, ternary_gemv_combine
+    from maple_amd.moe import PendingCombine, moe_layer
+    x = synthetic.randn_bf16((tokens, H), 900 + tokens, dev)
+    add = synthetic.randn_bf16((tokens, H), 950 + tokens, dev)
+    nw = synthetic.uniform_bf16((H,), 0.5, 1.5, 960, dev)
+    qkv_w, qkv_a = synthetic.ternary_linear(3072, H, 970, dev)
+    rms = synthetic.uniform_bf16((H,), 0.5, 1.5, 980, dev)
+    assert combine_gemv_supported(tokens, K, qkv_w)
+    y_ref, ids_ref = moe_layer(x, layer, K, nw, 1e-6, add=add)
+    q_ref = ternary_gemv(y_ref, qkv_w, qkv_a, rms_weight=rms, rms_eps=1e-6)
+    for call in range(2):
+        pend, ids = moe_layer(x, layer, K, nw, 1e-6, add=add, defer_combine=True)
+        assert isinstance(pend, PendingCombine)
+        y, q = ternary_gemv_combine(pend, qkv_w, qkv_a, rms_weight=rms, rms_eps=1e-6)
+        torch.cuda.synchronize()
+        assert torch.equal(ids, ids_ref)
+        assert torch.equal(y, y_ref), f"combined rows (call {call})"
+        assert torch.equal(q, q_ref), f"GEMM (call {call})"
