@@ -221,7 +221,7 @@ int ma_rtn4_embedding(const void* ids, int ids_is_int64, int64_t n_ids,
  * ma_moe_dispatch gives them).  Same values, bit for bit, as ma_add_rms_norm
  * (or ma_rms_norm), ma_router_topk and ma_moe_dispatch run one after another
  * at these sizes.  tokens <= 1024, hidden % 8 == 0 and <= 4096, n_experts <=
- * 256; bf16 rows, 16-byte aligned.  workspace: 256-byte aligned, at least
+ * 256, top_k <= 64; bf16 rows, 16-byte aligned.  workspace: 256-byte aligned, at least
  * ma_moe_route_workspace_bytes(tokens, n_experts) bytes, zero-filled once
  * when allocated (the kernel leaves it zero; word 64 becomes non-zero if a
  * wait ever timed out); calls sharing a workspace must not overlap.

@@ -241,8 +241,9 @@ extern "C" int ma_moe_route(const void* x, const void* x_add, int64_t tokens, in
                 (long long)hidden);
   if (n_experts < 1 || n_experts > kRouteMaxExperts)
     return fail(MA_EVALUE, "moe_route: n_experts must be in [1, %d]", kRouteMaxExperts);
-  if (top_k < 1 || top_k > n_experts)
-    return fail(MA_EVALUE, "top_k=%d must be in [1, n_experts=%lld].", top_k, (long long)n_experts);
+  if (top_k < 1 || top_k > n_experts || top_k > 64)
+    return fail(MA_EVALUE, "top_k=%d must be in [1, min(n_experts=%lld, 64)].", top_k,
+                (long long)n_experts);
   if (norm_dtype != MA_F32 && norm_dtype != MA_BF16)
     return fail(MA_ETYPE, "moe_route: norm weight must be float32 or bfloat16");
   if (tokens == 0) return MA_OK;
