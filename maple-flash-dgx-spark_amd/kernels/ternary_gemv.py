@@ -114,13 +114,14 @@ def ternary_gemv_combine(pending, packed_weight: torch.Tensor, row_alpha: torch.
     y = torch.empty(tokens, n_out, device=x.device, dtype=torch.bfloat16)
     rms_w = rms_weight.reshape(-1).contiguous()
     alpha = row_alpha.reshape(-1).contiguous()
+    pw = packed_weight.contiguous()
     ws_bytes = _lib.load().ma_ternary_gemv_workspace_bytes(tokens, nwords, 1)
     ws = torch.empty(max(int(ws_bytes), 1), device=x.device, dtype=torch.uint8)
     _lib.call(
         "ma_ternary_gemv_combine_ws",
         _lib.ptr(pending.slot_out), _lib.ptr(pending.inverse), _lib.ptr(pending.weights),
         pending.top_k, _lib.ptr(pending.residual), _lib.ptr(x), tokens,
-        _lib.ptr(packed_weight.contiguous()), n_out, nwords, _lib.ptr(alpha),
+        _lib.ptr(pw), n_out, nwords, _lib.ptr(alpha),
         _lib.dtype_code(alpha, "row_alpha"), _lib.ptr(rms_w), _lib.dtype_code(rms_w, "rms_weight"),
         float(rms_eps), _lib.ptr(y), n_out, _lib.ptr(ws), ws.numel(), _lib.stream_of(x),
     )
