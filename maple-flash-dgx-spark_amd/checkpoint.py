@@ -1,0 +1,208 @@
+"""``packed-ternary-v1`` checkpoints for the decoder.
+
+Reference: ``src/maple_run/model.py:509-559`` (the format check, the
+``[q; k; v]`` and ``[up; gate]`` concatenations, the uint32 view),
+``:636-660`` (the config keys), ``:664-832`` (``from_packed``: shards and
+index, ``lm_head_flash.*`` dropped, router/scales/biases held in bf16, the
+per-layer assembly) and ``src/maple_run/convert.py:181-303`` (tensor names,
+``config.json["maple_run"]``).
+
+A checkpoint directory holds ``config.json`` -- the model config plus a
+``maple_run`` block whose ``format`` is ``packed-ternary-v1`` -- and
+safetensors shards (listed by ``model.safetensors.index.json`` when there is
+one).  Per layer ``model.layers.{i}.``:
+  ``self_attn.{q,k,v,o}_proj.weight`` (packed 2-bit codes, uint32 words viewed
+  as int32 in the file) and ``.row_alpha`` (float32);
+  ``self_attn.{q,k}_norm.weight``, ``input_layernorm.weight``,
+  ``post_attention_layernorm.weight``;
+  ``mlp.gate.weight`` (router ``[E, H]``);
+  ``mlp.switch_mlp.{up,gate,down}_proj.weight`` (stacked experts ``[E, N,
+  K/16]``) and ``.row_alpha`` (``[E, N]``);
+and ``model.word_embeddings.{weight,scales,biases}``, ``lm_head.{weight,
+scales,biases}`` (4-bit RTN), ``model.norm.weight``.
+
+Only what this decoder runs is accepted: every layer full attention with RoPE
+and QK-norm (``layer_types`` all ``full_attention``, ``nope_on_global_attention``
+false); other configs raise ``NotImplementedError`` instead of decoding wrongly.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import torch
+
+from . import synthetic
+from .model import DecoderConfig, DecoderLayerWeights, SyntheticDecoder
+
+FORMAT = "packed-ternary-v1"
+
+
+def require_packed_format(config: dict) -> None:
+    """``model.py:509-515``: only converted checkpoints load."""
+    meta = config.get("maple_run") or {}
+    if meta.get("format") != FORMAT:
+        raise ValueError(
+            "Checkpoint is not maple-run packed-ternary-v1 (config.json has no "
+            "maple_run.format == 'packed-ternary-v1'); convert the bf16 dump first."
+        )
+
+
+def as_uint32(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.uint32 else t.view(torch.uint32)
+
+
+def read_weights(model_dir, device) -> tuple[dict, dict]:
+    """``(config, {name: tensor})`` of a checkpoint directory, tensors on
+    ``device``; FlashHead tensors are skipped."""
+    from safetensors.torch import load_file
+
+    model_dir = Path(model_dir).expanduser()
+    config = json.loads((model_dir / "config.json").read_text())
+    require_packed_format(config)
+    index = model_dir / "model.safetensors.index.json"
+    if index.exists():
+        shards = sorted(set(json.loads(index.read_text())["weight_map"].values()))
+    else:
+        shards = sorted(p.name for p in model_dir.glob("*.safetensors"))
+    weights: dict[str, torch.Tensor] = {}
+    for name in shards:
+        if name == "model-flashhead.safetensors":
+            continue
+        shard = load_file(str(model_dir / name), device=str(device))
+        weights.update({k: v for k, v in shard.items() if not k.startswith("lm_head_flash.")})
+    return config, weights
+
+
+def cat_qkv(weights: dict, prefix: str) -> tuple[torch.Tensor, torch.Tensor]:
+    """``model.py:518-535``: q, k, v rows stacked in that order (popped)."""
+    names = [f"{prefix}.self_attn.{p}_proj" for p in ("q", "k", "v")]
+    packed = torch.cat([as_uint32(weights.pop(n + ".weight")) for n in names], dim=0)
+    alpha = torch.cat([weights.pop(n + ".row_alpha") for n in names], dim=0)
+    return packed, alpha
+
+
+def cat_up_gate(weights: dict, prefix: str) -> tuple[torch.Tensor, torch.Tensor]:
+    """``model.py:538-553``: per expert, the up rows then the gate rows (popped)."""
+    names = [f"{prefix}.mlp.switch_mlp.{p}_proj" for p in ("up", "gate")]
+    packed = torch.cat([as_uint32(weights.pop(n + ".weight")) for n in names], dim=1)
+    alpha = torch.cat([weights.pop(n + ".row_alpha") for n in names], dim=1)
+    return packed, alpha
+
+
+def decoder_config(config: dict) -> DecoderConfig:
+    """The ``DecoderConfig`` of a checkpoint config (keys of ``model.py:636-660``)."""
+    layer_types = list(config.get("layer_types") or [])
+    if any(t != "full_attention" for t in layer_types):
+        raise NotImplementedError("only full-attention layers are supported (layer_types)")
+    if bool(config.get("nope_on_global_attention", True)) and layer_types:
+        raise NotImplementedError("layers without RoPE (nope_on_global_attention) are not supported")
+    if not bool(config.get("use_qk_norm", True)):
+        raise NotImplementedError("attention without QK-norm is not supported")
+    meta = config.get("maple_run") or {}
+    return DecoderConfig(
+        hidden=int(config["hidden_size"]),
+        layers=int(config["num_hidden_layers"]),
+        heads=int(config["num_attention_heads"]),
+        kv_heads=int(config["num_key_value_heads"]),
+        head_dim=int(config["head_dim"]),
+        experts=int(config["num_experts"]),
+        inter=int(config["moe_intermediate_size"]),
+        top_k=int(config["num_experts_per_tok"]),
+        vocab=int(config["vocab_size"]),
+        rtn_group=int((meta.get("rtn_4bit") or {}).get("group_size", 128)),
+        rope_theta=float(config.get("rope_theta", 10000)),
+        partial_rotary=float(config.get("partial_rotary_factor", 0.5)),
+        eps=float(config.get("rms_norm_eps", 1e-6)),
+    )
+
+
+def load_decoder(model_dir, device="cuda", max_len: int = 4096 + 128, **flags) -> SyntheticDecoder:
+    """A decoder on the HIP kernels with a checkpoint's weights (``flags``:
+    the ``SyntheticDecoder`` launch options)."""
+    device = torch.device(device)
+    config, w = read_weights(model_dir, device)
+    cfg = decoder_config(config)
+    bf16 = lambda t: t.to(torch.bfloat16).contiguous()
+    f32 = lambda t: t.to(torch.float32).contiguous()
+    layers = []
+    for i in range(cfg.layers):
+        p = f"model.layers.{i}"
+        qkv, qkv_a = cat_qkv(w, p)
+        up_gate, up_gate_a = cat_up_gate(w, p)
+        moe = synthetic.MoELayer(
+            gate_weight=bf16(w.pop(f"{p}.mlp.gate.weight")),
+            up_gate_packed=up_gate.contiguous(),
+            up_gate_alpha=bf16(up_gate_a),
+            down_packed=as_uint32(w.pop(f"{p}.mlp.switch_mlp.down_proj.weight")).contiguous(),
+            down_alpha=bf16(w.pop(f"{p}.mlp.switch_mlp.down_proj.row_alpha")),
+        )
+        layers.append(DecoderLayerWeights(
+            qkv.contiguous(), bf16(qkv_a),
+            as_uint32(w.pop(f"{p}.self_attn.o_proj.weight")).contiguous(),
+            bf16(w.pop(f"{p}.self_attn.o_proj.row_alpha")),
+            f32(w.pop(f"{p}.input_layernorm.weight")), f32(w.pop(f"{p}.post_attention_layernorm.weight")),
+            f32(w.pop(f"{p}.self_attn.q_norm.weight")), f32(w.pop(f"{p}.self_attn.k_norm.weight")), moe))
+    rtn = lambda n: (as_uint32(w.pop(n + ".weight")).contiguous(), bf16(w.pop(n + ".scales")),
+                     bf16(w.pop(n + ".biases")))
+    embed = rtn("model.word_embeddings")
+    lm_head = rtn("lm_head")
+    final_norm = f32(w.pop("model.norm.weight"))
+    return SyntheticDecoder.from_weights(cfg, device, layers, embed, lm_head, final_norm,
+                                         max_len=max_len, **flags)
+
+
+def save_decoder(model, model_dir) -> None:
+    """Write a decoder's weights as a packed-ternary-v1 directory (one shard):
+    the layout ``load_decoder`` and the reference's ``from_packed`` read."""
+    from safetensors.torch import save_file
+
+    c = model.cfg
+    model_dir = Path(model_dir)
+    model_dir.mkdir(parents=True, exist_ok=True)
+    cpu = lambda t: t.detach().to("cpu").contiguous()
+    codes = lambda t: cpu(t).view(torch.int32)
+    f32 = lambda t: cpu(t).to(torch.float32)
+    out: dict[str, torch.Tensor] = {}
+    nq, nk = c.heads * c.head_dim, c.kv_heads * c.head_dim
+    for i, L in enumerate(model.layers):
+        p = f"model.layers.{i}"
+        for name, r0, r1 in (("q", 0, nq), ("k", nq, nq + nk), ("v", nq + nk, nq + 2 * nk)):
+            out[f"{p}.self_attn.{name}_proj.weight"] = codes(L.qkv[r0:r1])
+            out[f"{p}.self_attn.{name}_proj.row_alpha"] = f32(L.qkv_alpha[r0:r1])
+        out[f"{p}.self_attn.o_proj.weight"] = codes(L.o)
+        out[f"{p}.self_attn.o_proj.row_alpha"] = f32(L.o_alpha)
+        out[f"{p}.self_attn.q_norm.weight"] = f32(L.q_norm)
+        out[f"{p}.self_attn.k_norm.weight"] = f32(L.k_norm)
+        out[f"{p}.input_layernorm.weight"] = f32(L.input_ln)
+        out[f"{p}.post_attention_layernorm.weight"] = f32(L.post_ln)
+        m, inter = L.moe, L.moe.inter
+        out[f"{p}.mlp.gate.weight"] = f32(m.gate_weight)
+        out[f"{p}.mlp.switch_mlp.up_proj.weight"] = codes(m.up_gate_packed[:, :inter])
+        out[f"{p}.mlp.switch_mlp.gate_proj.weight"] = codes(m.up_gate_packed[:, inter:])
+        out[f"{p}.mlp.switch_mlp.up_proj.row_alpha"] = f32(m.up_gate_alpha[:, :inter])
+        out[f"{p}.mlp.switch_mlp.gate_proj.row_alpha"] = f32(m.up_gate_alpha[:, inter:])
+        out[f"{p}.mlp.switch_mlp.down_proj.weight"] = codes(m.down_packed)
+        out[f"{p}.mlp.switch_mlp.down_proj.row_alpha"] = f32(m.down_alpha)
+    for name, (wt, sc, bs) in (("model.word_embeddings", model.embed), ("lm_head", model.lm_head)):
+        out[f"{name}.weight"] = codes(wt)
+        out[f"{name}.scales"] = f32(sc)
+        out[f"{name}.biases"] = f32(bs)
+    out["model.norm.weight"] = f32(model.final_norm)
+    save_file(out, str(model_dir / "model.safetensors"))
+    config = {
+        "model_type": "maple", "hidden_size": c.hidden, "num_hidden_layers": c.layers,
+        "num_attention_heads": c.heads, "num_key_value_heads": c.kv_heads, "head_dim": c.head_dim,
+        "num_experts": c.experts, "num_experts_per_tok": c.top_k, "moe_intermediate_size": c.inter,
+        "vocab_size": c.vocab, "rms_norm_eps": c.eps, "rope_theta": c.rope_theta,
+        "partial_rotary_factor": c.partial_rotary, "layer_types": ["full_attention"] * c.layers,
+        "use_qk_norm": True, "nope_on_global_attention": False,
+        "maple_run": {
+            "format": FORMAT, "experts": "stacked_switch_mlp",
+            "expert_template": "model.layers.{layer}.mlp.switch_mlp.{proj}.weight",
+            "ternary": {"bits": 2, "pack": "uint32_lsb_first", "scale": "row_alpha"},
+            "rtn_4bit": {"bits": 4, "group_size": c.rtn_group, "mode": "affine", "pack": "uint32_lsb_first"},
+        },
+    }
+    (model_dir / "config.json").write_text(json.dumps(config, indent=2, sort_keys=True))

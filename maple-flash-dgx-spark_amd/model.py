@@ -125,6 +125,22 @@ class SyntheticDecoder:
         self.final_norm = ones(c.hidden)
         self.cos, self.sin = rope_tables(max_len, c.rotary_dim, c.rope_theta, dev)
 
+    @classmethod
+    def from_weights(cls, cfg: DecoderConfig, device, layers: list, embed: tuple, lm_head: tuple,
+                     final_norm: torch.Tensor, max_len: int = 4096 + 128, fused_moe: bool = True,
+                     fused_o: bool = False, combine_next: bool = True) -> "SyntheticDecoder":
+        """A decoder over given weights (``checkpoint.load_decoder``) instead of
+        the seeded synthetic ones."""
+        self = cls.__new__(cls)
+        self.cfg = cfg
+        self.fused_moe, self.fused_o, self.combine_next = fused_moe, fused_o, combine_next
+        self.device = torch.device(device)
+        self.max_len = max_len
+        self.layers = list(layers)
+        self.embed, self.lm_head, self.final_norm = embed, lm_head, final_norm
+        self.cos, self.sin = rope_tables(max_len, cfg.rotary_dim, cfg.rope_theta, self.device)
+        return self
+
     def make_cache(self, batch: int, prefill_len: int, seed: int = 0) -> KVCache:
         """Cache rows filled with seeded N(0, 1) bf16 K/V for ``prefill_len``
         positions; decoding then writes at ``prefill_len``."""

@@ -307,3 +307,20 @@ def test_full_decoder_one_step_vs_oracle(dev):
     # forward() gives the same bits as the layer-by-layer calls
     cache2 = model.make_cache(1, prefill_len=4096, seed=0)
     assert torch.equal(model.forward(ids, cache2), logits)
+
+
+def test_decoder_from_packed_checkpoint_equals_original(dev, tmp_path):
+    """A packed-ternary-v1 directory written from a decoder and loaded back
+    (maple_amd.checkpoint) decodes the same logits, bit for bit, over three
+    greedy steps."""
+    from maple_amd import checkpoint
+    model = SyntheticDecoder(SMALL, dev, seed=8, max_len=128)
+    checkpoint.save_decoder(model, tmp_path)
+    back = checkpoint.load_decoder(tmp_path, dev, max_len=128)
+    c1, c2 = model.make_cache(2, prefill_len=20, seed=2), back.make_cache(2, prefill_len=20, seed=2)
+    ids = torch.tensor([11, 700], device=dev)
+    for step in range(3):
+        l1, l2 = model.forward(ids, c1), back.forward(ids, c2)
+        torch.cuda.synchronize()
+        assert torch.equal(l1, l2), f"step {step}"
+        ids = torch.argmax(l1, dim=-1)
