@@ -21,9 +21,10 @@ one).  Per layer ``model.layers.{i}.``:
 and ``model.word_embeddings.{weight,scales,biases}``, ``lm_head.{weight,
 scales,biases}`` (4-bit RTN), ``model.norm.weight``.
 
-Only what this decoder runs is accepted: every layer full attention with RoPE
-and QK-norm (``layer_types`` all ``full_attention``, ``nope_on_global_attention``
-false); other configs raise ``NotImplementedError`` instead of decoding wrongly.
+Layers are ``full_attention`` or ``sliding_attention`` (the last
+``sliding_window`` positions), full-attention layers without RoPE when
+``nope_on_global_attention`` is set, all with QK-norm; other configs raise
+``NotImplementedError`` instead of decoding wrongly.
 """
 
 from __future__ import annotations
@@ -93,11 +94,12 @@ def cat_up_gate(weights: dict, prefix: str) -> tuple[torch.Tensor, torch.Tensor]
 
 def decoder_config(config: dict) -> DecoderConfig:
     """The ``DecoderConfig`` of a checkpoint config (keys of ``model.py:636-660``)."""
-    layer_types = list(config.get("layer_types") or [])
-    if any(t != "full_attention" for t in layer_types):
-        raise NotImplementedError("only full-attention layers are supported (layer_types)")
-    if bool(config.get("nope_on_global_attention", True)) and layer_types:
-        raise NotImplementedError("layers without RoPE (nope_on_global_attention) are not supported")
+    layer_types = tuple(config.get("layer_types") or ())
+    if any(t not in ("full_attention", "sliding_attention") for t in layer_types):
+        raise NotImplementedError(f"layer types {sorted(set(layer_types))}: only full_attention "
+                                  "and sliding_attention are supported")
+    if layer_types and len(layer_types) != int(config["num_hidden_layers"]):
+        raise ValueError("layer_types must name every layer")
     if not bool(config.get("use_qk_norm", True)):
         raise NotImplementedError("attention without QK-norm is not supported")
     meta = config.get("maple_run") or {}
@@ -115,6 +117,9 @@ def decoder_config(config: dict) -> DecoderConfig:
         rope_theta=float(config.get("rope_theta", 10000)),
         partial_rotary=float(config.get("partial_rotary_factor", 0.5)),
         eps=float(config.get("rms_norm_eps", 1e-6)),
+        layer_types=layer_types,
+        sliding_window=int(config.get("sliding_window", 512)),
+        nope_on_global=bool(config.get("nope_on_global_attention", True)) and bool(layer_types),
     )
 
 
@@ -196,8 +201,9 @@ def save_decoder(model, model_dir) -> None:
         "num_attention_heads": c.heads, "num_key_value_heads": c.kv_heads, "head_dim": c.head_dim,
         "num_experts": c.experts, "num_experts_per_tok": c.top_k, "moe_intermediate_size": c.inter,
         "vocab_size": c.vocab, "rms_norm_eps": c.eps, "rope_theta": c.rope_theta,
-        "partial_rotary_factor": c.partial_rotary, "layer_types": ["full_attention"] * c.layers,
-        "use_qk_norm": True, "nope_on_global_attention": False,
+        "partial_rotary_factor": c.partial_rotary,
+        "layer_types": list(c.layer_types) or ["full_attention"] * c.layers,
+        "sliding_window": c.sliding_window, "use_qk_norm": True, "nope_on_global_attention": c.nope_on_global,
         "maple_run": {
             "format": FORMAT, "experts": "stacked_switch_mlp",
             "expert_template": "model.layers.{layer}.mlp.switch_mlp.{proj}.weight",

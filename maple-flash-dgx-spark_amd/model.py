@@ -55,6 +55,18 @@ class DecoderConfig:
     partial_rotary: float = 0.5
     eps: float = 1e-6
     lm_scale: tuple = (0.003, 0.006)
+    # per-layer attention (model.py:646-649, 784-786): "full_attention" or
+    # "sliding_attention" (the last sliding_window positions); empty = all full.
+    # nope_on_global: full-attention layers skip RoPE.
+    layer_types: tuple = ()
+    sliding_window: int = 512
+    nope_on_global: bool = False
+
+    def layer_attention(self, i: int) -> tuple:
+        """``(window or None, use_rope)`` of layer ``i``."""
+        kind = self.layer_types[i] if self.layer_types else "full_attention"
+        window = self.sliding_window if kind == "sliding_attention" else None
+        return window, not (self.nope_on_global and kind == "full_attention")
 
     @property
     def qkv_rows(self) -> int:
@@ -173,10 +185,12 @@ class SyntheticDecoder:
         bsz = hidden.shape[0]
         if qkv is None:
             qkv = ternary_gemv(hidden, L.qkv, L.qkv_alpha, rms_weight=L.input_ln, rms_eps=c.eps)
+        window, use_rope = c.layer_attention(i)
         akw = dict(num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim,
-                   rotary_dim=c.rotary_dim, eps=c.eps, scale=c.head_dim ** -0.5)
+                   rotary_dim=c.rotary_dim, eps=c.eps, scale=c.head_dim ** -0.5, window=window,
+                   use_rope=use_rope)
         if bsz == 1 and self.fused_o and o_projection_supported(1, c.heads, c.kv_heads, c.head_dim,
-                                                                cache.max_len, None, c.hidden):
+                                                                cache.max_len, window, c.hidden):
             # attention and its output projection in one launch (measured: no
             # faster than two launches at 4096 positions -- the grid barrier
             # and the tail cost what the second launch does -- so off by default)

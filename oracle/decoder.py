@@ -64,7 +64,9 @@ def decoder_layer(L: dict, c: dict, h, cache: dict, i: int, *, router_ids=None):
     oracle's own top-k (top-k is discontinuous, so two paths that differ by
     rounding can pick different near-tied experts and then diverge); the
     weights are still the oracle's own probabilities of those experts,
-    renormalised.  Returns ``(h_out, (own ids, probs))``."""
+    renormalised.  ``L`` may carry ``window`` (sliding-window attention over
+    the last ``window`` positions, model.py:784-786) and ``use_rope`` (False
+    on NoPE layers).  Returns ``(h_out, (own ids, probs))``."""
     nq, nkv, d = c["heads"], c["kv_heads"], c["head_dim"]
     rot, eps = c["rotary_dim"], c["eps"]
     bsz = h.shape[0]
@@ -74,15 +76,15 @@ def decoder_layer(L: dict, c: dict, h, cache: dict, i: int, *, router_ids=None):
         pos = min(int(cache["seqlen"][b]), cache["k"][i].shape[2] - 1)
         cs = bf(c["cos"][pos]) if rot else None
         sn = bf(c["sin"][pos]) if rot else None
-        q = np.stack([bf(head_norm_rope(qkv[b, hh * d:(hh + 1) * d], L["q_norm"], cs, sn, rot, eps))
+        q = np.stack([bf(head_norm_rope(qkv[b, hh * d:(hh + 1) * d], L["q_norm"], cs, sn, rot, eps, use_rope=L.get("use_rope", True)))
                       for hh in range(nq)])
         for kh in range(nkv):
             o0 = (nq + kh) * d
-            cache["k"][i][b, kh, pos] = bf(head_norm_rope(qkv[b, o0:o0 + d], L["k_norm"], cs, sn, rot, eps))
+            cache["k"][i][b, kh, pos] = bf(head_norm_rope(qkv[b, o0:o0 + d], L["k_norm"], cs, sn, rot, eps, use_rope=L.get("use_rope", True)))
             o1 = (nq + nkv + kh) * d
             cache["v"][i][b, kh, pos] = qkv[b, o1:o1 + d]
         kv_len = min(pos + 1, cache["k"][i].shape[2])
-        attn[b] = bf(gqa(q, cache["k"][i][b], cache["v"][i][b], kv_len, d ** -0.5)).reshape(-1)
+        attn[b] = bf(gqa(q, cache["k"][i][b], cache["v"][i][b], kv_len, d ** -0.5, window=L.get("window"))).reshape(-1)
     o = bf(ok.ternary_gemv(attn, L["o"], L["o_alpha"]))
     s_full = h + o
     res = bf(s_full)

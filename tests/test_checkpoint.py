@@ -44,8 +44,11 @@ def _tensors(model):
 def test_round_trip_is_exact(saved):
     model, d = saved
     back = checkpoint.load_decoder(d, "cpu", max_len=64)
-    # lm_scale only seeds the synthetic RTN tables; it is not part of a checkpoint
-    assert dataclasses.replace(back.cfg, lm_scale=SMALL.lm_scale) == SMALL
+    # lm_scale only seeds the synthetic RTN tables (not part of a checkpoint);
+    # the layer types come back spelled out, with the same attention per layer
+    assert dataclasses.replace(back.cfg, lm_scale=SMALL.lm_scale, layer_types=()) == SMALL
+    assert [back.cfg.layer_attention(i) for i in range(SMALL.layers)] == \
+        [SMALL.layer_attention(i) for i in range(SMALL.layers)]
     a, b = _tensors(model), _tensors(back)
     assert a.keys() == b.keys()
     for k in a:
@@ -76,8 +79,11 @@ def test_unconverted_and_unsupported_configs_are_refused(saved, tmp_path):
     config = json.loads((d / "config.json").read_text())
     with pytest.raises(ValueError, match="packed-ternary-v1"):
         checkpoint.require_packed_format({k: v for k, v in config.items() if k != "maple_run"})
-    sliding = dict(config, layer_types=["sliding_attention", "full_attention"])
     with pytest.raises(NotImplementedError):
-        checkpoint.decoder_config(sliding)
+        checkpoint.decoder_config(dict(config, layer_types=["chunked_attention", "full_attention"]))
     with pytest.raises(NotImplementedError):
-        checkpoint.decoder_config(dict(config, nope_on_global_attention=True))
+        checkpoint.decoder_config(dict(config, use_qk_norm=False))
+    # the reference's layer pattern: sliding layers with a window, NoPE global layers
+    cfg = checkpoint.decoder_config(dict(config, layer_types=["sliding_attention", "full_attention"],
+                                         sliding_window=64, nope_on_global_attention=True))
+    assert cfg.layer_attention(0) == (64, True) and cfg.layer_attention(1) == (None, False)

@@ -172,6 +172,7 @@ def _to_np(model: SyntheticDecoder) -> dict:
             moe=dict(gate_weight=np_f(L.moe.gate_weight), up_gate_packed=np_u32(L.moe.up_gate_packed),
                      up_gate_alpha=np_f(L.moe.up_gate_alpha), down_packed=np_u32(L.moe.down_packed),
                      down_alpha=np_f(L.moe.down_alpha))))
+        layers[-1]["window"], layers[-1]["use_rope"] = c.layer_attention(len(layers) - 1)
     cfg = dict(hidden=c.hidden, heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim,
                rotary_dim=c.rotary_dim, eps=c.eps, rtn_group=c.rtn_group, top_k=c.top_k)
     w, s, b = model.embed
@@ -324,3 +325,24 @@ def test_decoder_from_packed_checkpoint_equals_original(dev, tmp_path):
         torch.cuda.synchronize()
         assert torch.equal(l1, l2), f"step {step}"
         ids = torch.argmax(l1, dim=-1)
+
+
+def test_sliding_and_nope_layers_vs_oracle(dev):
+    """The reference's layer pattern (model.py:784-786): a sliding-window layer
+    (the last 16 positions) and a full-attention layer without RoPE, three
+    greedy steps at batch 2 against the oracle with the same per-layer
+    attention."""
+    import dataclasses
+    cfg = dataclasses.replace(SMALL, layer_types=("sliding_attention", "full_attention"),
+                              sliding_window=16, nope_on_global=True)
+    model = SyntheticDecoder(cfg, dev, seed=9, max_len=128)
+    cache = model.make_cache(2, prefill_len=41, seed=3)
+    m = _to_np(model)
+    assert m["layers"][0]["window"] == 16 and m["layers"][1]["use_rope"] is False
+    cnp = _cache_np(cache)
+    ids = torch.tensor([3, 517], device=dev)
+    for step in range(3):
+        logits = model.forward(ids, cache)
+        ref, _ = od.decoder_step(m, cnp, ids.cpu().numpy())
+        _check_logits(logits, ref, f"step {step}")
+        ids = torch.argmax(logits, dim=-1)
