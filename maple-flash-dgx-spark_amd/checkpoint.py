@@ -23,8 +23,9 @@ scales,biases}`` (4-bit RTN), ``model.norm.weight``.
 
 Layers are ``full_attention`` or ``sliding_attention`` (the last
 ``sliding_window`` positions), full-attention layers without RoPE when
-``nope_on_global_attention`` is set, all with QK-norm; other configs raise
-``NotImplementedError`` instead of decoding wrongly.
+``nope_on_global_attention`` is set, all with QK-norm, head_dim 64 (the decode
+attention kernel's); other configs raise ``NotImplementedError`` instead of
+decoding wrongly.
 """
 
 from __future__ import annotations
@@ -102,6 +103,9 @@ def decoder_config(config: dict) -> DecoderConfig:
         raise ValueError("layer_types must name every layer")
     if not bool(config.get("use_qk_norm", True)):
         raise NotImplementedError("attention without QK-norm is not supported")
+    if int(config["head_dim"]) != 64:
+        raise NotImplementedError(f"head_dim {config['head_dim']}: the decode attention kernel is built "
+                                  "for head_dim 64")
     meta = config.get("maple_run") or {}
     return DecoderConfig(
         hidden=int(config["hidden_size"]),

@@ -83,6 +83,8 @@ def test_unconverted_and_unsupported_configs_are_refused(saved, tmp_path):
         checkpoint.decoder_config(dict(config, layer_types=["chunked_attention", "full_attention"]))
     with pytest.raises(NotImplementedError):
         checkpoint.decoder_config(dict(config, use_qk_norm=False))
+    with pytest.raises(NotImplementedError):
+        checkpoint.decoder_config(dict(config, head_dim=128))
     # the reference's layer pattern: sliding layers with a window, NoPE global layers
     cfg = checkpoint.decoder_config(dict(config, layer_types=["sliding_attention", "full_attention"],
                                          sliding_window=64, nope_on_global_attention=True))
