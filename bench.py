@@ -280,7 +280,7 @@ def main() -> int:
                     help="only time the full decoder at this batch (for profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
+        print("bench.py measures one GPU only: there is no multi-GPU path "
               "(run with --gpus 1).", file=sys.stderr)
         return 2
 

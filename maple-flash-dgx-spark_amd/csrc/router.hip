@@ -1,7 +1,7 @@
 // MoE router: logits GEMV, softmax, top-k, renormalisation (gfx950).
 //
 // Semantics of reference src/maple_run/kernels/router.py:39-126: float32
-// logits (+ this build's optional bias), p = exp(l - max) / sum, k passes of
+// logits (+ an optional additive bias), p = exp(l - max) / sum, k passes of
 // argmax with the winner masked out (descending; ties to the lowest index),
 // w_j = p_j / (sum p_top + 1e-20).  Products are bf16 x bf16 summed by
 // v_dot2_f32_bf16: exact products, float32 accumulation.

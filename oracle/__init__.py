@@ -1,7 +1,7 @@
 """CPU oracle for the packed-ternary MoE decode path -- TEST INFRASTRUCTURE ONLY.
 
 This package restates, in NumPy, what the reference (maple-run) computes on the
-hot path. It is the checker the HIP kernels are compared against and the CPU
+hot path. The HIP kernels are compared against it, and it is the CPU
 baseline ``bench.py`` times. Only ``tests/``, ``__graft_entry__.smoke()`` and
 ``bench.py``'s ``cpu_baseline`` leg may import it; the shipped package never
 does, and fails loudly when its HIP library is missing instead of falling back

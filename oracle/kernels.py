@@ -79,7 +79,7 @@ def router_topk(x, gate_weight, top_k, bias=None):
     ``p = softmax(x @ W^T [+ bias])`` over all experts; the top-k are taken in
     descending probability, ties to the lowest expert index (Triton
     ``argmax`` semantics, ``router.py:115-121``); weights are
-    ``p_j / (sum p_top + 1e-20)``.  ``bias`` is this build's optional additive
+    ``p_j / (sum p_top + 1e-20)``.  ``bias`` is an optional additive
     logit bias for skewed-routing workloads; ``None`` is the reference.
 
     Returns ``(ids int32 [..., k], weights float32 [..., k], probs float64
