@@ -277,8 +277,9 @@ int ma_moe_grouped(const void* x, int64_t ldx, const uint32_t* x_pairs, const fl
  * y bf16 [hidden], topk_ids int32 [top_k], topk_weight float32 [top_k].
  * With x_add != NULL the block first computes s = x + x_add (float32) and runs
  * on bf16(rms_norm(s) * norm_weight) with residual bf16(s) (the decoder's
- * post-attention add + RMSNorm); otherwise residual may be NULL.  bf16 x,
- * gate weight and row scales.  Built shapes (hidden, inter, top_k): (2048,
+ * post-attention add + RMSNorm); otherwise residual may be NULL.  bf16 x and
+ * gate weight; row scales (up_gate_alpha, down_alpha) float32 or bf16, both
+ * of alpha_dtype.  Built shapes (hidden, inter, top_k): (2048,
  * 768, 8) and (256, 128, 2); experts <= 256; other shapes return MA_EVALUE
  * (use the per-kernel entry points).  workspace:
  * ma_moe_fused_workspace_bytes(...) bytes, zero-filled before its first use
@@ -305,11 +306,22 @@ int ma_moe_fused(const void* x, const void* x_add, const void* norm_weight, int 
                  float eps, const void* residual, const void* gate_weight,
                  const float* router_bias, int64_t n_experts, int64_t hidden, int64_t inter,
                  int64_t top_k, const uint32_t* up_gate, const void* up_gate_alpha,
-                 const uint32_t* down, const void* down_alpha, void* y, int32_t* topk_ids,
+                 const uint32_t* down, const void* down_alpha, int alpha_dtype, void* y,
+                 int32_t* topk_ids,
                  float* topk_weight, void* workspace, size_t workspace_bytes,
                  const uint32_t* next_w, const void* next_alpha, int next_alpha_dtype,
                  const float* next_rms, float next_eps, int64_t next_rows, void* next_out,
                  void* stream);
+/* The one-launch layer's workgroups wait on each other (a grid barrier), so
+ * all of them must be resident at once: *needed = its grid for this shape,
+ * *capacity = compute units x resident workgroups per unit on the current
+ * device.  ma_moe_fused itself fails with MA_ERUNTIME where needed >
+ * capacity (a partitioned GPU, say); callers then run the multi-launch
+ * kernels.  MA_EVALUE if the shape is not built.  No reference counterpart
+ * (the reference has no persistent kernel); a query for the choice above. */
+int ma_moe_fused_resident(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k,
+                          int64_t* needed, int64_t* capacity);
+
 /* *out = 1 if any ma_moe_fused call on this workspace timed out waiting
  * (synchronises the stream).  No reference counterpart: the reference has no
  * cross-workgroup wait. */

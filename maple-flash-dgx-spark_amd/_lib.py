@@ -22,6 +22,7 @@ _I = ctypes.c_int
 _L = ctypes.c_int64
 _F = ctypes.c_float
 _Z = ctypes.c_size_t
+_PL = ctypes.POINTER(ctypes.c_int64)
 
 # name -> argtypes (restype is int unless listed in _RESTYPES)
 _SIGNATURES = {
@@ -51,9 +52,10 @@ _SIGNATURES = {
                              _P, _P, _P, _P, _L, _L, _L, _F, _P, _P, _Z, _P, _P, _I, _L, _P, _P],
     "ma_decode_attn_o_supported": [_L, _I, _I, _I, _L, _L, _L],
     "ma_moe_fused_workspace_bytes": [_L, _L, _L, _L],
-    "ma_moe_fused": [_P, _P, _P, _I, _F, _P, _P, _P, _L, _L, _L, _L, _P, _P, _P, _P, _P, _P, _P, _P,
-                     _Z, _P, _P, _I, _P, _F, _L, _P, _P],
+    "ma_moe_fused": [_P, _P, _P, _I, _F, _P, _P, _P, _L, _L, _L, _L, _P, _P, _P, _P, _I, _P, _P, _P,
+                     _P, _Z, _P, _P, _I, _P, _F, _L, _P, _P],
     "ma_moe_fused_timed_out": [_P, _P, _P],
+    "ma_moe_fused_resident": [_L, _L, _L, _L, _PL, _PL],
     "ma_moe_route_workspace_bytes": [_L, _L],
     "ma_moe_route": [_P, _P, _L, _L, _P, _I, _F, _P, _P, _L, _I, _P, _P, _P, _P, _P, _P, _P, _P,
                      _P, _P, _P, _Z, _P],

@@ -3,8 +3,10 @@
 Reference: ``src/maple_run/model.py:509-559`` (the format check, the
 ``[q; k; v]`` and ``[up; gate]`` concatenations, the uint32 view),
 ``:636-660`` (the config keys), ``:664-832`` (``from_packed``: shards and
-index, ``lm_head_flash.*`` dropped, router/scales/biases held in bf16, the
-per-layer assembly) and ``src/maple_run/convert.py:181-303`` (tensor names,
+index, ``lm_head_flash.*`` dropped, the router and the RTN scales/biases held
+in bf16 while ``row_alpha`` and the norms keep the float32 the converter
+wrote, the RTN group from ``maple_run.rtn_4bit.group_size`` with 64 as the
+default, the per-layer assembly) and ``src/maple_run/convert.py:181-303`` (tensor names,
 ``config.json["maple_run"]``).
 
 A checkpoint directory holds ``config.json`` -- the model config plus a
@@ -39,6 +41,7 @@ from . import synthetic
 from .model import DecoderConfig, DecoderLayerWeights, SyntheticDecoder
 
 FORMAT = "packed-ternary-v1"
+HEAD_GROUP_SIZE = 64  # RTN group of the head when the config names none (pack.py:14)
 
 
 def require_packed_format(config: dict) -> None:
@@ -117,7 +120,7 @@ def decoder_config(config: dict) -> DecoderConfig:
         inter=int(config["moe_intermediate_size"]),
         top_k=int(config["num_experts_per_tok"]),
         vocab=int(config["vocab_size"]),
-        rtn_group=int((meta.get("rtn_4bit") or {}).get("group_size", 128)),
+        rtn_group=int((meta.get("rtn_4bit") or {}).get("group_size", HEAD_GROUP_SIZE)),
         rope_theta=float(config.get("rope_theta", 10000)),
         partial_rotary=float(config.get("partial_rotary_factor", 0.5)),
         eps=float(config.get("rms_norm_eps", 1e-6)),
@@ -133,8 +136,16 @@ def load_decoder(model_dir, device="cuda", max_len: int = 4096 + 128, **flags) -
     device = torch.device(device)
     config, w = read_weights(model_dir, device)
     cfg = decoder_config(config)
+    # model.py:728-748: float32 router rows and RTN scales/biases go to bf16;
+    # row_alpha keeps the dtype it was written in (float32 from the converter)
     bf16 = lambda t: t.to(torch.bfloat16).contiguous()
     f32 = lambda t: t.to(torch.float32).contiguous()
+    keep = lambda t: t.contiguous()
+    for name in ("model.word_embeddings", "lm_head"):
+        n_groups = int(w[name + ".scales"].shape[-1])
+        if n_groups * cfg.rtn_group != cfg.hidden:
+            raise ValueError(f"{name}: {n_groups} RTN scale groups per row do not cover hidden "
+                             f"{cfg.hidden} with group_size {cfg.rtn_group}")
     layers = []
     for i in range(cfg.layers):
         p = f"model.layers.{i}"
@@ -143,14 +154,14 @@ def load_decoder(model_dir, device="cuda", max_len: int = 4096 + 128, **flags) -
         moe = synthetic.MoELayer(
             gate_weight=bf16(w.pop(f"{p}.mlp.gate.weight")),
             up_gate_packed=up_gate.contiguous(),
-            up_gate_alpha=bf16(up_gate_a),
+            up_gate_alpha=keep(up_gate_a),
             down_packed=as_uint32(w.pop(f"{p}.mlp.switch_mlp.down_proj.weight")).contiguous(),
-            down_alpha=bf16(w.pop(f"{p}.mlp.switch_mlp.down_proj.row_alpha")),
+            down_alpha=keep(w.pop(f"{p}.mlp.switch_mlp.down_proj.row_alpha")),
         )
         layers.append(DecoderLayerWeights(
-            qkv.contiguous(), bf16(qkv_a),
+            qkv.contiguous(), keep(qkv_a),
             as_uint32(w.pop(f"{p}.self_attn.o_proj.weight")).contiguous(),
-            bf16(w.pop(f"{p}.self_attn.o_proj.row_alpha")),
+            keep(w.pop(f"{p}.self_attn.o_proj.row_alpha")),
             f32(w.pop(f"{p}.input_layernorm.weight")), f32(w.pop(f"{p}.post_attention_layernorm.weight")),
             f32(w.pop(f"{p}.self_attn.q_norm.weight")), f32(w.pop(f"{p}.self_attn.k_norm.weight")), moe))
     rtn = lambda n: (as_uint32(w.pop(n + ".weight")).contiguous(), bf16(w.pop(n + ".scales")),

@@ -686,12 +686,26 @@ static int64_t attn_grid_splits(int64_t batch, int nkv, int64_t max_len, int64_t
   return grid_splits;
 }
 
+// The splits of one (row, KV head) wait on each other, so they must fit on the
+// device at once: their number is capped at the kernel's resident capacity
+// (compute units x occupancy).  Workgroups are dispatched in index order and a
+// (row, KV head)'s splits are consecutive, so every earlier pair has all of
+// its splits placed and finishes; with the O projection in the launch the
+// whole grid meets at one barrier and must be resident.
+static int attn_capacity(bool fused, int64_t* cap) {
+  const void* fn = fused ? reinterpret_cast<const void*>(&k_decode_attn<true>)
+                         : reinterpret_cast<const void*>(&k_decode_attn<false>);
+  return resident_capacity(fn, kAttnThreads, cap);
+}
+
 extern "C" int ma_decode_attn_o_supported(int64_t batch, int n_heads, int n_kv_heads, int head_dim,
                                           int64_t max_len, int64_t window, int64_t o_rows) {
   if (batch != 1 || n_kv_heads < 1 || max_len < 1 ||
       static_cast<int64_t>(n_heads) * head_dim != 32 * kOWords * 16)
     return 0;
   const int64_t n_wg = attn_grid_splits(batch, n_kv_heads, max_len, window) * n_kv_heads;
+  int64_t cap = 0;
+  if (attn_capacity(true, &cap) != MA_OK || n_wg > cap) return 0;
   return n_wg >= kBarGroups && o_rows >= 1 && o_rows <= n_wg * 8 * kOPass;
 }
 
@@ -712,7 +726,10 @@ static int launch_attn(bool fused, const void* src, int64_t ldq, const void* qn_
   const int64_t max_splits = max_splits_for(max_len);
   if (batch * nkv * max_splits * kMaxGroup * kHeadDim * 4 >= (int64_t{1} << 32))
     return fail(MA_EVALUE, "%s: batch x kv heads x max_len too large for one launch", what);
-  const int64_t grid_splits = attn_grid_splits(batch, nkv, max_len, window);
+  int64_t grid_splits = attn_grid_splits(batch, nkv, max_len, window);
+  int64_t capacity = 0;
+  if (int rc = attn_capacity(fused, &capacity)) return rc;
+  if (grid_splits > capacity) grid_splits = capacity;
   auto* sync = static_cast<uint32_t*>(workspace);
   float* acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + sync_bytes(batch, nkv));
   float* ml = acc + static_cast<size_t>(batch) * nkv * max_splits * kMaxGroup * kHeadDim;
@@ -723,6 +740,9 @@ static int launch_attn(bool fused, const void* src, int64_t ldq, const void* qn_
     if (batch != 1 || static_cast<int64_t>(nq) * kHeadDim != 32 * kOWords * 16)
       return fail(MA_EVALUE, "%s: the O projection in the launch needs batch 1 and n_heads x head_dim = %d",
                   what, 32 * kOWords * 16);
+    if (n_wg > capacity)
+      return fail(MA_ERUNTIME, "%s: the O projection's %lld workgroups wait on each other but the device holds %lld",
+                  what, static_cast<long long>(n_wg), static_cast<long long>(capacity));
     if (n_wg < kBarGroups || o_rows < 1 || o_rows > n_wg * 8 * kOPass)
       return fail(MA_EVALUE, "%s: O projection of %lld rows over %lld workgroups unsupported", what,
                   static_cast<long long>(o_rows), static_cast<long long>(n_wg));

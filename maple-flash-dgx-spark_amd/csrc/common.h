@@ -18,6 +18,10 @@ namespace ma {
 void set_error(const char* fmt, ...);
 int fail(int status, const char* fmt, ...);
 int check_launch(const char* what);
+// Workgroups of `kernel` (with `threads` threads, no dynamic LDS) resident at
+// once on the current device: compute units x occupancy.  Persistent kernels
+// whose workgroups wait on each other check their grid against it.
+int resident_capacity(const void* kernel, int threads, int64_t* capacity);
 
 // ---------------------------------------------------------------------------
 // Scalar conversions.  bf16 is carried as raw uint16 bits.

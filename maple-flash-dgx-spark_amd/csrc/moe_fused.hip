@@ -64,8 +64,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     const uint16_t* __restrict__ xa, const uint16_t* __restrict__ xb,
     const void* __restrict__ norm_w, int norm_dt, float eps, const uint16_t* __restrict__ residual,
     const uint16_t* __restrict__ gate_w, const float* __restrict__ bias, int n_exp,
-    const uint32_t* __restrict__ ug, const uint16_t* __restrict__ ug_alpha,
-    const uint32_t* __restrict__ dn, const uint16_t* __restrict__ dn_alpha,
+    const uint32_t* __restrict__ ug, const void* __restrict__ ug_alpha,
+    const uint32_t* __restrict__ dn, const void* __restrict__ dn_alpha, int alpha_dt,
     uint16_t* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ wts_out,
     uint32_t* __restrict__ ws, const uint32_t* __restrict__ nx_w, const void* __restrict__ nx_alpha,
     int nx_alpha_dt, const float* __restrict__ nx_rms, float nx_eps, int nx_rows,
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     const int64_t e = clamp_id(s_ids[s], n_exp);
     const int64_t row = e * (2 * I) + j + half * I;
     load_words_v<KWH>(ug + row * NWH + klh * KWH, wu[u]);
-    au[u] = bf16_to_f32(ug_alpha[row]);
+    au[u] = ld_f(ug_alpha, alpha_dt, row);
   }
   const int kld = lane % LPRI, subd = lane / LPRI;
   const int rbase = wg * RPB;
@@ -337,7 +337,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
       int r = rbase + u * RPID + subd;
       r = r < H ? r : H - 1;
       load_words_v<KWI>(dn + (e * H + r) * NWI + kld * KWI, wd[q][u]);
-      ad[q][u] = bf16_to_f32(dn_alpha[e * H + r]);
+      ad[q][u] = ld_f(dn_alpha, alpha_dt, e * H + r);
     }
   }
   // Next projection (optional): this workgroup's rows, issued after the
@@ -597,7 +597,26 @@ size_t ws_bytes(int64_t, int, int64_t inter, int64_t top_k) {
   return kMoeWsHeader + static_cast<size_t>(top_k * inter) * 2;
 }
 
+// The kernel instantiation a call launches (PER = 1 up to 64 experts, else 4).
+const void* fused_kernel(int64_t hidden, int64_t n_experts) {
+  if (hidden == 2048)
+    return n_experts <= 64 ? reinterpret_cast<const void*>(&k_moe_fused<4, 32, 6, 3, 16, 2, 8, 1>)
+                           : reinterpret_cast<const void*>(&k_moe_fused<4, 32, 6, 3, 16, 2, 8, 4>);
+  return reinterpret_cast<const void*>(&k_moe_fused<1, 16, 2, 1, 8, 1, 2, 1>);
+}
+
 }  // namespace
+
+// Whether every workgroup of the one-launch layer fits on the current device
+// at once (its grid barrier needs that): *needed = the grid, *capacity =
+// compute units x occupancy.  MA_EVALUE if the shape is not built.
+extern "C" int ma_moe_fused_resident(int64_t n_experts, int64_t hidden, int64_t inter,
+                                     int64_t top_k, int64_t* needed, int64_t* capacity) {
+  const FusedShape* s = find_shape(hidden, inter, top_k);
+  if (!s || !needed || !capacity) return fail(MA_EVALUE, "moe_fused_resident: shape not built");
+  *needed = s->grid;
+  return resident_capacity(fused_kernel(hidden, n_experts), 64 * kFusedWaves, capacity);
+}
 
 extern "C" size_t ma_moe_fused_workspace_bytes(int64_t n_experts, int64_t hidden, int64_t inter,
                                                int64_t top_k) {
@@ -611,7 +630,7 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
                             const void* gate_weight, const float* router_bias, int64_t n_experts,
                             int64_t hidden, int64_t inter, int64_t top_k,
                             const uint32_t* up_gate, const void* up_gate_alpha,
-                            const uint32_t* down, const void* down_alpha, void* y,
+                            const uint32_t* down, const void* down_alpha, int alpha_dtype, void* y,
                             int32_t* topk_ids, float* topk_weight, void* workspace,
                             size_t workspace_bytes, const uint32_t* next_w,
                             const void* next_alpha, int next_alpha_dtype, const float* next_rms,
@@ -624,6 +643,8 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
   if (n_experts < top_k || n_experts > 256 || n_experts > static_cast<int64_t>(s->grid))
     return fail(MA_EVALUE, "moe_fused: %lld experts unsupported", static_cast<long long>(n_experts));
   if (x_add && !norm_weight) return fail(MA_EVALUE, "moe_fused: add without norm weight");
+  if (alpha_dtype != MA_F32 && alpha_dtype != MA_BF16)
+    return fail(MA_ETYPE, "moe_fused: row_alpha dtype %d (float32 or bfloat16)", alpha_dtype);
   if (norm_weight && norm_dtype != MA_F32 && norm_dtype != MA_BF16)
     return fail(MA_ETYPE, "moe_fused: norm weight dtype %d", norm_dtype);
   if (!workspace || workspace_bytes < ws_bytes(n_experts, s->grid, inter, top_k))
@@ -642,13 +663,18 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
     if (!a16(next_w) || !a16(next_rms) || !a16(y))
       return fail(MA_EVALUE, "moe_fused: next projection weights, rms weight and y must be 16-byte aligned");
   }
+  int64_t capacity = 0;
+  if (int rc = resident_capacity(fused_kernel(hidden, n_experts), 64 * kFusedWaves, &capacity)) return rc;
+  if (capacity < s->grid)
+    return fail(MA_ERUNTIME, "moe_fused: its %d workgroups wait on each other but the device holds %lld at once",
+                s->grid, static_cast<long long>(capacity));
   const int per = n_experts <= 64 ? 1 : 4;
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define MA_FUSED_ARGS                                                                            \
   static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(x_add), norm_weight, norm_dtype, \
       eps, static_cast<const uint16_t*>(residual), static_cast<const uint16_t*>(gate_weight),    \
       router_bias, static_cast<int>(n_experts), up_gate,                                         \
-      static_cast<const uint16_t*>(up_gate_alpha), down, static_cast<const uint16_t*>(down_alpha), \
+      up_gate_alpha, down, down_alpha, alpha_dtype,                                              \
       static_cast<uint16_t*>(y), topk_ids, topk_weight, static_cast<uint32_t*>(workspace),       \
       next_w, next_alpha, next_alpha_dtype, next_rms, next_eps, static_cast<int>(next_rows),      \
       static_cast<uint16_t*>(next_out)

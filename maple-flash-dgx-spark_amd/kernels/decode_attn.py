@@ -19,7 +19,7 @@ from __future__ import annotations
 
 import torch
 
-from .. import _lib
+from .. import _lib, workspace
 
 
 def _check_rows(what, bsz, k_cache, v_cache, seqlen, row_map):
@@ -57,7 +57,7 @@ def gqa_workspace(batch: int, num_kv_heads: int, max_len: int, device) -> torch.
     """Zeroed workspace for ``decode_gqa_attn`` / ``decode_attention``; keep
     one per cache so decode allocates nothing inside a graph."""
     nbytes = int(_lib.load().ma_gqa_workspace_bytes(batch, num_kv_heads, max_len))
-    return torch.zeros(nbytes, device=device, dtype=torch.uint8)
+    return workspace.register_attention(torch.zeros(nbytes, device=device, dtype=torch.uint8))
 
 
 def apply_qkv_decode(

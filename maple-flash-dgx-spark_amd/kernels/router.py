@@ -9,30 +9,14 @@ from __future__ import annotations
 
 import torch
 
-from .. import _lib
-
-# One zero-filled workspace per device.  The single-launch decode router
-# returns it to all-zero before it finishes, so it is reused without a memset;
-# router calls on one device must therefore not overlap (the reference also
-# runs decode from a single stream, src/maple_run/server.py:370-373).
-_WORKSPACES: dict[int, torch.Tensor] = {}
-
-
-def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    ws = _WORKSPACES.get(idx)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 16), device=device, dtype=torch.uint8)
-        _WORKSPACES[idx] = ws
-    return ws
+from .. import _lib, workspace
 
 
 def router_wait_timed_out(device: torch.device | int = 0) -> bool:
-    """True if a single-launch router call on ``device`` ever timed out waiting
-    for its logits (the kernel records it instead of hanging).  Syncs."""
-    idx = device if isinstance(device, int) else (device.index or 0)
-    ws = _WORKSPACES.get(idx)
-    return bool(ws is not None and int(ws[4:8].view(torch.int32).item()) != 0)
+    """True if a single-launch router call on ``device`` timed out waiting for
+    its logits since its workspace was zeroed (the kernel records it instead
+    of hanging).  Syncs."""
+    return "router" in workspace.timed_out_kinds(device)
 
 
 def router_topk(
@@ -70,7 +54,8 @@ def router_topk(
     idx = torch.empty(tokens, top_k, device=x.device, dtype=torch.int32)
     wt = torch.empty(tokens, top_k, device=x.device, dtype=torch.float32)
     nbytes = int(_lib.load().ma_router_workspace_bytes(tokens, n_exp))
-    ws = _workspace(x.device, nbytes)
+    # zero-filled once; the single-launch decode router leaves it zero again
+    ws = workspace.get("router", x.device, nbytes, min_bytes=1 << 16)
     _lib.call(
         "ma_router_topk",
         _lib.ptr(x_mat), _lib.dtype_code(x_mat, "x"), tokens, x_mat.stride(0) if tokens else k_in,

@@ -26,11 +26,12 @@ device):
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
 
-from . import _lib
+from . import _lib, workspace
 from .kernels.dispatch import moe_dispatch
 from .kernels.router import router_topk
 from .kernels.ternary_expert import ternary_expert_down_sum, ternary_expert_swiglu
@@ -38,39 +39,45 @@ from .synthetic import MoELayer
 
 GROUPED_MIN_TOKENS = 4
 
-# One zero-filled workspace per device and built shape for the one-launch
-# layer kernel: its workgroups hand data to each other through it, tagged with
-# per-workgroup call counters the kernel keeps there, so it is never cleared
-# again.  Calls on one device must not overlap (decode runs from one stream).
-_FUSED_WS: dict[tuple, torch.Tensor] = {}
+_RESIDENT: dict[tuple, bool] = {}
 
 
-def _fused_workspace(device: torch.device, shape: tuple, nbytes: int) -> torch.Tensor:
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    key = (idx,) + shape
-    ws = _FUSED_WS.get(key)
-    if ws is None:
-        ws = torch.zeros(nbytes, device=device, dtype=torch.uint8)
-        _FUSED_WS[key] = ws
-    return ws
+def fused_resident(layer: MoELayer, top_k: int, device) -> bool:
+    """True if every workgroup of the one-launch layer fits on ``device`` at
+    once (its grid barrier needs that; not so on a partitioned GPU, say).
+    Queried once per device and shape."""
+    idx = torch.device(device).index
+    idx = torch.cuda.current_device() if idx is None else idx
+    key = (idx, layer.n_experts, layer.hidden, layer.inter, top_k)
+    ok = _RESIDENT.get(key)
+    if ok is None:
+        needed, capacity = ctypes.c_int64(0), ctypes.c_int64(0)
+        with torch.cuda.device(idx):
+            _lib.call("ma_moe_fused_resident", layer.n_experts, layer.hidden, layer.inter, top_k,
+                      ctypes.byref(needed), ctypes.byref(capacity))
+        ok = _RESIDENT[key] = capacity.value >= needed.value
+    return ok
 
 
 def fused_supported(layer: MoELayer, top_k: int, x: torch.Tensor) -> bool:
-    """True if ``ma_moe_fused`` is built for this layer's shape and dtypes."""
+    """True if ``ma_moe_fused`` is built for this layer's shape and dtypes and
+    its grid fits on ``x``'s device at once."""
     if x.dtype != torch.bfloat16 or layer.gate_weight.dtype != torch.bfloat16:
         return False
-    if layer.up_gate_alpha.dtype != torch.bfloat16 or layer.down_alpha.dtype != torch.bfloat16:
+    if layer.up_gate_alpha.dtype != layer.down_alpha.dtype or \
+            layer.up_gate_alpha.dtype not in (torch.bfloat16, torch.float32):
         return False
-    return int(_lib.load().ma_moe_fused_workspace_bytes(layer.n_experts, layer.hidden, layer.inter,
-                                                        top_k)) > 0
+    if int(_lib.load().ma_moe_fused_workspace_bytes(layer.n_experts, layer.hidden, layer.inter,
+                                                    top_k)) == 0:
+        return False
+    return fused_resident(layer, top_k, x.device)
 
 
 def moe_fused_timed_out(device: torch.device | int = 0) -> bool:
-    """True if a one-launch MoE call on ``device`` ever timed out waiting for
-    another workgroup (the kernel records it instead of hanging).  Syncs."""
-    idx = device if isinstance(device, int) else (device.index or 0)
-    return any(int(ws[8:12].view(torch.int32).item()) != 0
-               for key, ws in _FUSED_WS.items() if key[0] == idx)
+    """True if a one-launch MoE call on ``device`` timed out waiting for another
+    workgroup since its workspace was zeroed (the kernel records it instead of
+    hanging).  Syncs."""
+    return "moe_fused" in workspace.timed_out_kinds(device)
 
 
 def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tensor | None = None,
@@ -99,12 +106,17 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
     if nbytes == 0:
         raise ValueError(f"moe_fused: shape (hidden {hidden}, inter {layer.inter}, top_k {top_k}) "
                          "is not built into the one-launch kernel")
-    ws = _fused_workspace(x.device, (hidden, layer.inter, top_k), nbytes)
+    # zero-filled once: workgroups hand data to each other through it, tagged
+    # with call counters the kernel keeps there
+    ws = workspace.get("moe_fused", x.device, nbytes, (hidden, layer.inter, top_k))
     y = torch.empty(1, hidden, device=x.device, dtype=torch.bfloat16)
     ids = torch.empty(1, top_k, device=x.device, dtype=torch.int32)
     wts = torch.empty(1, top_k, device=x.device, dtype=torch.float32)
     nw = None if norm_weight is None else norm_weight.reshape(-1).contiguous()
     bias = None if layer.router_bias is None else layer.router_bias.float().contiguous()
+    alpha_dt = _lib.dtype_code(layer.up_gate_alpha, "row_alpha")
+    if _lib.dtype_code(layer.down_alpha, "row_alpha") != alpha_dt:
+        raise TypeError("up_gate and down row_alpha must share a dtype")
     nx_w = nx_a = nx_r = nx_out = None
     nx_eps, nx_rows = 0.0, 0
     if next_linear is not None:
@@ -122,7 +134,7 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
         _lib.dtype_code(nw, "norm_weight") if nw is not None else 0, float(eps), _lib.ptr(res),
         _lib.ptr(layer.gate_weight), _lib.ptr(bias), layer.n_experts, hidden, layer.inter, top_k,
         _lib.ptr(layer.up_gate_packed), _lib.ptr(layer.up_gate_alpha), _lib.ptr(layer.down_packed),
-        _lib.ptr(layer.down_alpha), _lib.ptr(y), _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(ws),
+        _lib.ptr(layer.down_alpha), alpha_dt, _lib.ptr(y), _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(ws),
         ws.numel(), _lib.ptr(nx_w), _lib.ptr(nx_a),
         _lib.dtype_code(nx_a, "row_alpha") if nx_a is not None else 0, _lib.ptr(nx_r),
         float(nx_eps), nx_rows, _lib.ptr(nx_out), _lib.stream_of(x),
@@ -133,7 +145,6 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
 
 
 ROUTE_MAX_TOKENS = 1024
-_ROUTE_WS: dict[tuple, torch.Tensor] = {}
 
 
 def route_supported(layer: MoELayer, top_k: int, x: torch.Tensor) -> bool:
@@ -145,11 +156,9 @@ def route_supported(layer: MoELayer, top_k: int, x: torch.Tensor) -> bool:
 
 
 def route_timed_out(device: torch.device | int = 0) -> bool:
-    """True if a routing launch on ``device`` ever timed out waiting for
-    another workgroup (recorded in word 64 of its workspace).  Syncs."""
-    idx = device if isinstance(device, int) else (device.index or 0)
-    return any(int(ws[256:260].view(torch.int32).item()) != 0
-               for key, ws in _ROUTE_WS.items() if key[0] == idx)
+    """True if a routing launch on ``device`` timed out waiting for another
+    workgroup since its workspace was zeroed.  Syncs."""
+    return "moe_route" in workspace.timed_out_kinds(device)
 
 
 def moe_route(x: torch.Tensor, layer: MoELayer, top_k: int, norm_weight: torch.Tensor,
@@ -165,13 +174,9 @@ def moe_route(x: torch.Tensor, layer: MoELayer, top_k: int, norm_weight: torch.T
     from .kernels.dispatch import Dispatch
     tokens, hidden = x.shape
     dev = x.device
-    idx = dev.index if dev.index is not None else torch.cuda.current_device()
     nbytes = int(_lib.load().ma_moe_route_workspace_bytes(ROUTE_MAX_TOKENS, layer.n_experts))
-    key = (idx, layer.n_experts)
-    ws = _ROUTE_WS.get(key)
-    if ws is None:
-        ws = torch.zeros(nbytes, device=dev, dtype=torch.uint8)
-        _ROUTE_WS[key] = ws
+    # zero-filled once; each launch leaves its ticket counter and tags cleared
+    ws = workspace.get("moe_route", dev, nbytes, (layer.n_experts,))
     xc = x.contiguous()
     ac = None if add is None else add.reshape(tokens, hidden).contiguous()
     h = torch.empty_like(xc) if ac is not None else xc
@@ -263,24 +268,42 @@ def moe_grouped(x: torch.Tensor, layer: MoELayer, ids: torch.Tensor, wts: torch.
     return y
 
 
+def choose_plan(tokens: int, fused_ok: bool, grouped_ok: bool) -> str:
+    """The execution plan of ``moe_block`` for ``tokens`` tokens: "fused" (one
+    token, where ``ma_moe_fused`` is built for the shape and its grid fits on
+    the device at once), "grouped" (from GROUPED_MIN_TOKENS tokens, where the
+    grouped MFMA kernels take the shape), else "per_slot" -- the multi-launch
+    kernels, which need no co-resident workgroups."""
+    if tokens == 1 and fused_ok:
+        return "fused"
+    if tokens >= GROUPED_MIN_TOKENS and grouped_ok:
+        return "grouped"
+    return "per_slot"
+
+
+def grouped_supported(layer: MoELayer, x: torch.Tensor) -> bool:
+    """True if the grouped MFMA kernels take this layer's shape and ``x``."""
+    return x.dtype == torch.bfloat16 and layer.hidden % 256 == 0 and layer.inter % 256 == 0
+
+
 def moe_block(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tensor | None = None,
               *, plan: str = "auto"):
     """One MoE layer on ``x [..., H]``; returns ``(y, ids, weights)``.
 
-    ``plan``: "auto" (the one-launch kernel for one token where it is built,
-    grouped MFMA from GROUPED_MIN_TOKENS tokens, per-slot kernels otherwise),
-    or "per_slot" / "grouped" / "fused" to force one."""
+    ``plan``: "auto" (``choose_plan``), or "per_slot" / "grouped" / "fused"
+    to force one."""
     hidden = x.shape[-1]
     xf = x.reshape(-1, hidden)
-    if plan == "auto" and xf.shape[0] == 1 and fused_supported(layer, top_k, xf):
-        plan = "fused"
+    if plan == "auto":
+        tokens = xf.shape[0]
+        plan = choose_plan(tokens, tokens == 1 and fused_supported(layer, top_k, xf),
+                           grouped_supported(layer, xf))
     if plan == "fused":
         y, ids, wts = moe_fused(xf, layer, top_k, residual)
         return y.reshape(x.shape), ids, wts
     ids, wts = router_topk(xf, layer.gate_weight, top_k, bias=layer.router_bias)
     res = None if residual is None else residual.reshape(-1, hidden)
-    if plan == "grouped" or plan == "auto" and xf.shape[0] >= GROUPED_MIN_TOKENS and xf.dtype == torch.bfloat16 \
-            and hidden % 256 == 0 and layer.inter % 256 == 0:
+    if plan == "grouped":
         y = moe_grouped(xf, layer, ids, wts, res)
     else:
         h = ternary_expert_swiglu(xf, layer.up_gate_packed, layer.up_gate_alpha, ids)

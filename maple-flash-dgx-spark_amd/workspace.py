@@ -1,0 +1,93 @@
+"""Device workspaces of the kernels whose workgroups hand data to each other,
+and the check of their timeout words.
+
+The single-launch router, the routing launch, the one-launch MoE layer and the
+decode attention keep cross-workgroup state in a zero-filled workspace: tagged
+values, call counters, barrier counters and flags that each call leaves ready
+for the next, so the workspace is zeroed once and never again.  Two calls on
+one workspace must therefore not overlap.  Workspaces here are keyed by
+(kind, device, stream, shape): calls issued on different streams use different
+workspaces and may run concurrently; calls on one stream are ordered by it.
+A HIP graph keeps the workspace of the stream it was captured on; replay it
+in that stream's order relative to eager calls made on the capture stream.
+(The attention workspace belongs to its KV cache, ``gqa_workspace``.)
+
+Every wait in those kernels is bounded (about 0.2 s); a wait that runs out
+sets the workspace's timeout word and the kernel finishes with wrong values
+instead of hanging.  ``check_timeouts`` reads every timeout word of a device
+in one copy (a host synchronisation) and raises ``RuntimeError`` if any is
+set, after zeroing the workspaces again so that later calls start clean.
+The decode loop (``generate.py``) calls it where it already synchronises.
+"""
+
+from __future__ import annotations
+
+import weakref
+
+import torch
+
+# uint32 index of the timeout word in each kind of workspace
+TIMEOUT_WORD = {
+    "router": 1,      # ma_router_topk's single-launch decode router
+    "moe_fused": 2,   # ma_moe_fused
+    "moe_route": 64,  # ma_moe_route
+    "attention": 2,   # ma_decode_attn_fused / ma_decode_gqa_attn (sync area, line 0)
+}
+
+_POOL: dict[tuple, torch.Tensor] = {}
+_ATTENTION: "weakref.WeakValueDictionary[int, torch.Tensor]" = weakref.WeakValueDictionary()
+
+
+def _device_index(device) -> int:
+    device = torch.device(device)
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def get(kind: str, device, nbytes: int, key: tuple = (), *, min_bytes: int = 0) -> torch.Tensor:
+    """The zero-filled workspace of ``kind`` for ``key`` on ``device`` and its
+    current stream (created, or grown, on first need)."""
+    idx = _device_index(device)
+    stream = torch.cuda.current_stream(idx).cuda_stream
+    k = (kind, idx, stream) + tuple(key)
+    ws = _POOL.get(k)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(int(nbytes), int(min_bytes)), device=torch.device("cuda", idx), dtype=torch.uint8)
+        _POOL[k] = ws
+    return ws
+
+
+def register_attention(ws: torch.Tensor) -> torch.Tensor:
+    """Track an attention workspace (one per KV cache) for ``check_timeouts``."""
+    _ATTENTION[id(ws)] = ws
+    return ws
+
+
+def _all(idx: int) -> list[tuple[str, torch.Tensor]]:
+    out = [(k[0], ws) for k, ws in _POOL.items() if k[1] == idx]
+    out += [("attention", ws) for ws in list(_ATTENTION.values()) if ws.device.index == idx]
+    return out
+
+
+def timed_out_kinds(device=None) -> list[str]:
+    """Kinds of workspace on ``device`` whose timeout word is set.  One small
+    device gather and one copy to the host (synchronises)."""
+    idx = _device_index(device if device is not None else torch.cuda.current_device())
+    wss = _all(idx)
+    if not wss:
+        return []
+    words = torch.stack([ws.view(torch.int32)[TIMEOUT_WORD[kind]] for kind, ws in wss]).cpu()
+    return sorted({kind for (kind, _), w in zip(wss, words.tolist()) if w != 0})
+
+
+def check_timeouts(device=None) -> None:
+    """Raise ``RuntimeError`` if any cross-workgroup wait on ``device`` timed
+    out since the workspaces were zeroed; zero them again first."""
+    kinds = timed_out_kinds(device)
+    if kinds:
+        idx = _device_index(device if device is not None else torch.cuda.current_device())
+        for _, ws in _all(idx):
+            ws.zero_()
+        raise RuntimeError(
+            "a cross-workgroup wait timed out in " + ", ".join(kinds)
+            + "; the results of the calls since the last check are invalid "
+            "(workspaces have been zeroed again)")

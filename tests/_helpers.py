@@ -2,6 +2,9 @@
 
 from __future__ import annotations
 
+import json
+from pathlib import Path
+
 import numpy as np
 import torch
 
@@ -48,3 +51,19 @@ def tie_safe_rows(probs: np.ndarray, k: int, gap: float = 1e-5) -> np.ndarray:
     p = np.sort(probs.reshape(-1, probs.shape[-1]), axis=-1)[:, ::-1][:, : k + 1]
     d = (p[:, :-1] - p[:, 1:]) / np.maximum(p[:, :-1], 1e-30)
     return (d > gap).all(axis=1)
+
+
+# Router bias of the Zipf(1.1)-skewed workloads (64 experts, top-8) and the
+# expert load it is fitted to: tests/golden/make_zipf_bias.py.
+ZIPF = json.loads((Path(__file__).parent / "golden" / "zipf_bias_e64.json").read_text())
+
+
+def zipf_bias(device) -> torch.Tensor:
+    return torch.tensor(ZIPF["bias"], dtype=torch.float32, device=device)
+
+
+def load_tv_distance(ids: np.ndarray, n_experts: int = 64) -> float:
+    """Total-variation distance between the share of (token, slot) pairs each
+    expert received and the fixture's target shares."""
+    c = np.bincount(np.asarray(ids).reshape(-1), minlength=n_experts).astype(np.float64)
+    return 0.5 * float(np.abs(c / c.sum() - np.asarray(ZIPF["target_share"])).sum())

@@ -2,8 +2,9 @@
 ``checkpoint.save_decoder`` reads back tensor for tensor through the
 reference's loading rules (reference model.py:509-559, 664-832) -- the
 ``[q; k; v]`` and ``[up; gate]`` concatenation orders, the uint32 view of the
-packed codes, bf16 router / alphas / RTN scales -- and configs the decoder
-cannot run are refused."""
+packed codes, bf16 router and RTN scales/biases, float32 ``row_alpha`` kept as
+written (model.py:728-748) -- and configs the decoder cannot run are
+refused."""
 
 from __future__ import annotations
 
@@ -52,6 +53,9 @@ def test_round_trip_is_exact(saved):
     a, b = _tensors(model), _tensors(back)
     assert a.keys() == b.keys()
     for k in a:
+        if k.endswith("alpha"):  # written as float32 and kept so: the same values
+            assert b[k].dtype == torch.float32 and torch.equal(a[k].float(), b[k]), k
+            continue
         assert a[k].dtype == b[k].dtype and a[k].shape == b[k].shape, k
         assert torch.equal(a[k], b[k]), k
     torch.testing.assert_close(back.cos, model.cos, rtol=0, atol=0)
@@ -71,7 +75,36 @@ def test_file_layout_follows_the_reference(saved):
     assert tuple(up.shape) == (SMALL.experts, SMALL.inter, SMALL.hidden // 16)
     assert torch.equal(up, L0.moe.up_gate_packed[:, :SMALL.inter])
     qkv, alpha = checkpoint.cat_qkv(dict(w), "model.layers.0")
-    assert torch.equal(qkv, L0.qkv) and torch.equal(alpha.to(torch.bfloat16), L0.qkv_alpha)
+    assert torch.equal(qkv, L0.qkv) and torch.equal(alpha, L0.qkv_alpha.float())
+
+
+def test_float32_alphas_stay_float32(tmp_path):
+    """row_alpha values bf16 cannot hold come back unrounded (the reference
+    keeps row_alpha in float32 and its kernels read it so)."""
+    model = SyntheticDecoder(SMALL, "cpu", seed=6, max_len=64)
+    g = torch.Generator().manual_seed(0)
+    for L in model.layers:
+        L.qkv_alpha = torch.rand(L.qkv_alpha.shape, generator=g) * 0.04 + 0.01
+        L.moe.down_alpha = torch.rand(L.moe.down_alpha.shape, generator=g) * 0.04 + 0.01
+    assert not torch.equal(model.layers[0].qkv_alpha, model.layers[0].qkv_alpha.bfloat16().float())
+    checkpoint.save_decoder(model, tmp_path)
+    back = checkpoint.load_decoder(tmp_path, "cpu", max_len=64)
+    for L, B in zip(model.layers, back.layers):
+        assert B.qkv_alpha.dtype == torch.float32 and torch.equal(B.qkv_alpha, L.qkv_alpha)
+        assert B.moe.down_alpha.dtype == torch.float32 and torch.equal(B.moe.down_alpha, L.moe.down_alpha)
+
+
+def test_rtn_group_defaults_to_64_and_must_cover_hidden(saved, tmp_path):
+    _, d = saved
+    config = json.loads((d / "config.json").read_text())
+    meta = dict(config["maple_run"], rtn_4bit={"bits": 4})
+    assert checkpoint.decoder_config(dict(config, maple_run=meta)).rtn_group == 64
+    # the saved tables have group 128: a config claiming 64 is refused on load
+    import shutil
+    shutil.copytree(d, tmp_path / "c", dirs_exist_ok=True)
+    (tmp_path / "c" / "config.json").write_text(json.dumps(dict(config, maple_run=meta)))
+    with pytest.raises(ValueError, match="group_size"):
+        checkpoint.load_decoder(tmp_path / "c", "cpu", max_len=64)
 
 
 def test_unconverted_and_unsupported_configs_are_refused(saved, tmp_path):

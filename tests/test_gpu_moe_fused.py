@@ -20,7 +20,7 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import assert_bf16_close, np_f, np_u32, tie_safe_rows
+from _helpers import assert_bf16_close, np_f, np_u32, tie_safe_rows, zipf_bias
 from maple_amd import synthetic
 from maple_amd.kernels import ternary_gemv
 from maple_amd.moe import moe_block, moe_fused, moe_fused_timed_out
@@ -62,10 +62,32 @@ def test_fused_plain_vs_oracle(dev, layers, with_res):
     assert not moe_fused_timed_out(dev)
 
 
+def test_fused_float32_alphas_vs_oracle(dev, layers):
+    """Row scales in float32 (as a converted checkpoint holds them) with
+    values bf16 cannot represent: read unrounded, against the oracle."""
+    L0 = layers[2]
+    g = torch.Generator(device=dev).manual_seed(3)
+    ua = torch.rand(L0.up_gate_alpha.shape, device=dev, generator=g) * 0.04 + 0.01
+    da = torch.rand(L0.down_alpha.shape, device=dev, generator=g) * 0.04 + 0.01
+    L = synthetic.MoELayer(L0.gate_weight, L0.up_gate_packed, ua, L0.down_packed, da)
+    assert not torch.equal(ua, ua.bfloat16().float())
+    from maple_amd.moe import fused_supported
+    for step in range(2):
+        x = synthetic.randn_bf16((1, 2048), 750 + step, dev)
+        assert fused_supported(L, 8, x)
+        y, ids, wts = moe_block(x, L, 8, plan="fused")
+        torch.cuda.synchronize()
+        assert_bf16_close(np_f(y), _oracle(np_f(x), L, ids, wts, 8), atol_frac=Y_ATOL, what=f"f32 alphas {step}")
+        y_bf, _, _ = moe_block(x, synthetic.MoELayer(L0.gate_weight, L0.up_gate_packed, ua.bfloat16(),
+                                                     L0.down_packed, da.bfloat16()), 8, plan="fused")
+        assert not torch.equal(y, y_bf)  # the float32 values were used, not rounded ones
+    assert not moe_fused_timed_out(dev)
+
+
 def test_fused_zipf_bias_vs_oracle(dev, layers):
     L0 = layers[0]
     L = synthetic.MoELayer(L0.gate_weight, L0.up_gate_packed, L0.up_gate_alpha, L0.down_packed,
-                           L0.down_alpha, synthetic.zipf_router_bias(64, 1.1, 1.0, seed=3).to(dev))
+                           L0.down_alpha, zipf_bias(dev))
     for step in range(3):
         x = synthetic.randn_bf16((1, 2048), 700 + step, dev)
         y, ids, wts = moe_block(x, L, 8, plan="fused")
