@@ -516,6 +516,7 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
   constexpr int GPC = kDenseChunk / GW;  // groups per chunk
   constexpr int SPG = GW / 4;            // k-slices per group
   __shared__ __align__(16) uint32_t xs[kDenseChunk][NT][4];  // word-major (see above)
+  __shared__ float xw[kDenseChunk][NT];  // each word's sum of x, added per group in word order
   __shared__ float xg[NT][GPC];
   __shared__ float sb[2][kDenseRows][GPC];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -568,7 +569,6 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
     for (int mb = 0; mb < MB; ++mb) load_chunk_words<GW>(rowp[mb] + cn, wn[mb]);
     // (no sched_barrier here: with loads into loop-carried registers just
     // above, it produced wrong MFMA operands on this compiler)
-    if (tid < NT * GPC) xg[tid / GPC][tid % GPC] = 0.f;
     {
       const int which = tid >> 7, rr = tid & 127;
 #pragma unroll
@@ -595,7 +595,15 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
         sx += xv[j] + xv[j + 4];
       }
       *reinterpret_cast<uint4*>(&xs[wd][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-      atomicAdd(&xg[col][wd / GW], sx);
+      xw[wd][col] = sx;
+    }
+    __syncthreads();
+    if (tid < NT * GPC) {  // group sums in a fixed order: the same bits on every run
+      const int col = tid / GPC, gi = tid % GPC;
+      float sx = 0.f;
+#pragma unroll
+      for (int wd = 0; wd < GW; ++wd) sx += xw[gi * GW + wd][col];
+      xg[col][gi] = sx;
     }
     __syncthreads();
 #pragma unroll

@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void k_grouped_swiglu(
     uint16_t* __restrict__ hp, uint16_t* __restrict__ h, int64_t ldh) {
   constexpr int NT = 16 * NB;
   __shared__ __align__(16) uint32_t xs[kChunkWords][2][NT][4];  // word-major: conflict-free B reads
-  __shared__ float cst[NT];
+  __shared__ float cst[NT], cw[kChunkWords][NT];  // corrections: per word, then summed in word order
   __shared__ int32_t tok[NT], pid[NT];
   int e, pos0, np;
   if (!decode_tile(offsets, n_exp, blockIdx.y, NT, e, pos0, np)) return;
@@ -176,9 +176,15 @@ __global__ __launch_bounds__(256) void k_grouped_swiglu(
       }
       *reinterpret_cast<uint4*>(&xs[wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
       *reinterpret_cast<uint4*>(&xs[wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
-      atomicAdd(&cst[col], c);
+      cw[wd][col] = c;
     }
     __syncthreads();
+    if (tid < NT) {  // a fixed order: the same bits on every run
+      float c = cst[tid];
+#pragma unroll
+      for (int wd = 0; wd < kChunkWords; ++wd) c += cw[wd][tid];
+      cst[tid] = c;
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {  // word q of the lane's 4 -> MFMA steps 2q, 2q+1
       uint4 a[4][2];
@@ -248,7 +254,7 @@ __global__ __launch_bounds__(256) void k_grouped_down(
     int n_exp, uint16_t* __restrict__ out) {
   constexpr int NT = 16 * NB;
   __shared__ __align__(16) uint32_t xs[kChunkWords][2][NT][4];  // word-major: conflict-free B reads
-  __shared__ float cst[NT];
+  __shared__ float cst[NT], cw[kChunkWords][NT];  // corrections: per word, then summed in word order
   int e, pos0, np;
   if (!decode_tile(offsets, n_exp, blockIdx.y, NT, e, pos0, np)) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -301,9 +307,15 @@ __global__ __launch_bounds__(256) void k_grouped_down(
       }
       *reinterpret_cast<uint4*>(&xs[wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
       *reinterpret_cast<uint4*>(&xs[wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
-      atomicAdd(&cst[col], pairs_cst(pr));
+      cw[wd][col] = pairs_cst(pr);
     }
     __syncthreads();
+    if (tid < NT) {  // a fixed order: the same bits on every run
+      float c = cst[tid];
+#pragma unroll
+      for (int wd = 0; wd < kChunkWords; ++wd) c += cw[wd][tid];
+      cst[tid] = c;
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       uint4 a[4][2];

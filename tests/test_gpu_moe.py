@@ -86,6 +86,9 @@ def test_moe_grouped_zipf_vs_oracle(dev, layer, tokens):
     np.testing.assert_array_equal(d.inverse.cpu().numpy(), inv)
     ref, href = ok.moe_experts(np_f(x), idn, wn, *_oracle_inputs(L))
     assert_bf16_close(np_f(h), href, what=f"h T={tokens}")
+    for _ in range(2):  # every sum has a fixed order: the same bits on every run
+        y2, h2 = moe_grouped(x, L, ids, wts, return_h=True)
+        assert torch.equal(y2, y) and torch.equal(h2, h), f"T={tokens}: a second run differs"
     # y passes two bf16 rounding points (h and each slot's down output, as in
     # the reference), so an element may differ by sum_j w_j * ulp(out_j):
     # about one bf16 ulp of the output scale, whatever |y| itself is.
