@@ -271,6 +271,30 @@ int ma_moe_grouped(const void* x, int64_t ldx, const uint32_t* x_pairs, const fl
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * ma_moe_grouped with no workspace argument that allocates nothing: the same
+ * kernels stage h and the per-pair down outputs in a device array built into
+ * the library (one per GPU, held until the process ends), of
+ * ma_moe_grouped_noalloc_max_bytes() bytes (16 MiB: up to 2978 (token,
+ * expert) pairs at hidden 2048 / intermediate 768, i.e. 372 tokens at top-8).
+ * Larger calls return MA_EVALUE.  y is required (the per-pair outputs stay in
+ * the internal array).  Every call on one GPU shares that array: calls that
+ * overlap on one GPU (other streams, other threads) race; calls ordered on a
+ * stream do not.  Nothing in the array needs clearing between calls.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).
+ */
+size_t ma_moe_grouped_noalloc_max_bytes(void);
+int ma_moe_grouped_noalloc(const void* x, int64_t ldx, const uint32_t* x_pairs,
+                           const float* x_corr, int64_t tokens, int64_t top_k,
+                           const uint32_t* up_gate, const void* up_gate_alpha,
+                           const uint32_t* down, const void* down_alpha, int alpha_dtype,
+                           int64_t n_experts, int64_t hidden, int64_t inter,
+                           const int32_t* offsets, const int32_t* pair_ids, const int32_t* inverse,
+                           const float* topk_weight, const void* residual, int residual_dtype,
+                           void* h_out, int64_t ldh, void* y, void* stream);
+
+/*
  * One token through the whole MoE layer in ONE launch (decode batch 1):
  * router (x @ gate_weight^T + bias, softmax, top-k, renormalise), expert
  * SwiGLU (h in bf16), down projections and the weighted combine, + residual;

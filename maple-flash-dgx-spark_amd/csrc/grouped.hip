@@ -25,6 +25,8 @@
 // pair's down output rounded to bf16 (ternary_expert.py:208); a gather
 // kernel then forms y[t] = sum_j w[t,j] out[pair(t,j)] (+ residual) in
 // float32 (fused_norm.py:83-96).
+#include <mutex>
+
 #include "mfma.h"
 
 namespace ma {
@@ -973,28 +975,32 @@ extern "C" size_t ma_grouped_workspace_bytes(int64_t n_pairs, int64_t inter, int
   return static_cast<size_t>(n_pairs) * (inter + hidden) * 2 + 256;
 }
 
-extern "C" int ma_moe_grouped(const void* x, int64_t ldx, const uint32_t* x_pairs,
-                              const float* x_corr, int64_t tokens, int64_t top_k,
-                              const uint32_t* up_gate, const void* up_gate_alpha,
-                              const uint32_t* down, const void* down_alpha, int alpha_dtype,
-                              int64_t n_experts, int64_t hidden, int64_t inter,
-                              const int32_t* offsets, const int32_t* pair_ids,
-                              const int32_t* inverse, const float* topk_weight,
-                              const void* residual, int residual_dtype, void* h_out, int64_t ldh,
-                              void* y, void* workspace, size_t workspace_bytes, void* stream) {
+// Argument checks shared by ma_moe_grouped and ma_moe_grouped_noalloc.
+static int grouped_check(const void* x, int64_t ldx, int64_t tokens, int64_t top_k,
+                         int alpha_dtype, int64_t n_experts, int64_t hidden, int64_t inter,
+                         const char* what) {
   if (tokens < 0 || top_k < 1 || n_experts < 1 || n_experts > 1024)
-    return fail(MA_EVALUE, "moe_grouped: bad sizes");
+    return fail(MA_EVALUE, "%s: bad sizes", what);
   if (hidden % 256 || inter % 256)
-    return fail(MA_EVALUE, "moe_grouped: hidden (%lld) and intermediate (%lld) must be multiples of 256",
+    return fail(MA_EVALUE, "%s: hidden (%lld) and intermediate (%lld) must be multiples of 256", what,
                 (long long)hidden, (long long)inter);
   if (alpha_dtype != MA_BF16 && alpha_dtype != MA_F32)
-    return fail(MA_ETYPE, "moe_grouped: row_alpha must be bfloat16 or float32");
+    return fail(MA_ETYPE, "%s: row_alpha must be bfloat16 or float32", what);
   if ((reinterpret_cast<uintptr_t>(x) & 15u) || (ldx % 8))
-    return fail(MA_EVALUE, "moe_grouped: x rows must be 16-byte aligned");
+    return fail(MA_EVALUE, "%s: x rows must be 16-byte aligned", what);
+  return MA_OK;
+}
+
+// The launches of one grouped MoE call; workspace holds
+// ma_grouped_workspace_bytes(tokens * top_k, inter, hidden) bytes.
+static int grouped_launch(const void* x, int64_t ldx, const uint32_t* x_pairs, const float* x_corr,
+                          int64_t tokens, int64_t top_k, const uint32_t* up_gate,
+                          const void* up_gate_alpha, const uint32_t* down, const void* down_alpha,
+                          int alpha_dtype, int64_t n_experts, int64_t hidden, int64_t inter,
+                          const int32_t* offsets, const int32_t* pair_ids, const int32_t* inverse,
+                          const float* topk_weight, const void* residual, int residual_dtype,
+                          void* h_out, int64_t ldh, void* y, void* workspace, void* stream) {
   const int64_t n_pairs = tokens * top_k;
-  if (n_pairs == 0) return MA_OK;
-  if (!workspace || workspace_bytes < ma_grouped_workspace_bytes(n_pairs, inter, hidden))
-    return fail(MA_EVALUE, "moe_grouped: workspace too small");
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint16_t* hp = static_cast<uint16_t*>(workspace);
   uint16_t* out = hp + n_pairs * inter;
@@ -1066,4 +1072,87 @@ extern "C" int ma_moe_grouped(const void* x, int64_t ldx, const uint32_t* x_pair
     }
   }
   return check_launch("moe_grouped");
+}
+
+extern "C" int ma_moe_grouped(const void* x, int64_t ldx, const uint32_t* x_pairs,
+                              const float* x_corr, int64_t tokens, int64_t top_k,
+                              const uint32_t* up_gate, const void* up_gate_alpha,
+                              const uint32_t* down, const void* down_alpha, int alpha_dtype,
+                              int64_t n_experts, int64_t hidden, int64_t inter,
+                              const int32_t* offsets, const int32_t* pair_ids,
+                              const int32_t* inverse, const float* topk_weight,
+                              const void* residual, int residual_dtype, void* h_out, int64_t ldh,
+                              void* y, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = grouped_check(x, ldx, tokens, top_k, alpha_dtype, n_experts, hidden, inter, "moe_grouped"))
+    return rc;
+  const int64_t n_pairs = tokens * top_k;
+  if (n_pairs == 0) return MA_OK;
+  if (!workspace || workspace_bytes < ma_grouped_workspace_bytes(n_pairs, inter, hidden))
+    return fail(MA_EVALUE, "moe_grouped: workspace too small");
+  return grouped_launch(x, ldx, x_pairs, x_corr, tokens, top_k, up_gate, up_gate_alpha, down,
+                        down_alpha, alpha_dtype, n_experts, hidden, inter, offsets, pair_ids,
+                        inverse, topk_weight, residual, residual_dtype, h_out, ldh, y, workspace,
+                        stream);
+}
+
+// ---------------------------------------------------------------------------
+// ma_moe_grouped without a workspace argument and without any allocation:
+// the staging buffer is this file-scope device array, one per GPU, held until
+// the process ends.  In host code `scratch` names a host-side stand-in, so
+// kernels get the device address from hipGetSymbolAddress, taken once per
+// device on that device's first call.
+// ---------------------------------------------------------------------------
+constexpr size_t kGroupedScratchBytes = size_t{16} << 20;
+static __device__ __align__(256) uint8_t scratch[kGroupedScratchBytes];
+
+static void* grouped_scratch_ptr() {
+  static std::mutex mu;
+  static void* ptrs[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    fail(MA_ERUNTIME, "moe_grouped_noalloc: no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+      fail(MA_ERUNTIME, "moe_grouped_noalloc: device address of the scratch array unavailable");
+      return nullptr;
+    }
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
+}
+
+extern "C" size_t ma_moe_grouped_noalloc_max_bytes(void) { return kGroupedScratchBytes; }
+
+extern "C" int ma_moe_grouped_noalloc(const void* x, int64_t ldx, const uint32_t* x_pairs,
+                                      const float* x_corr, int64_t tokens, int64_t top_k,
+                                      const uint32_t* up_gate, const void* up_gate_alpha,
+                                      const uint32_t* down, const void* down_alpha,
+                                      int alpha_dtype, int64_t n_experts, int64_t hidden,
+                                      int64_t inter, const int32_t* offsets,
+                                      const int32_t* pair_ids, const int32_t* inverse,
+                                      const float* topk_weight, const void* residual,
+                                      int residual_dtype, void* h_out, int64_t ldh, void* y,
+                                      void* stream) {
+  const char* what = "moe_grouped_noalloc";
+  if (int rc = grouped_check(x, ldx, tokens, top_k, alpha_dtype, n_experts, hidden, inter, what))
+    return rc;
+  if (!y)
+    return fail(MA_EVALUE, "%s: y is required (the per-pair outputs stay in the internal scratch)", what);
+  const int64_t n_pairs = tokens * top_k;
+  if (n_pairs == 0) return MA_OK;
+  const size_t need = ma_grouped_workspace_bytes(n_pairs, inter, hidden);
+  if (need > kGroupedScratchBytes)
+    return fail(MA_EVALUE,
+                "%s: %lld (token, expert) pairs need %zu bytes of staging; the built-in scratch holds %zu "
+                "(use ma_moe_grouped with a workspace)",
+                what, static_cast<long long>(n_pairs), need, kGroupedScratchBytes);
+  void* ws = grouped_scratch_ptr();
+  if (!ws) return MA_ERUNTIME;
+  return grouped_launch(x, ldx, x_pairs, x_corr, tokens, top_k, up_gate, up_gate_alpha, down,
+                        down_alpha, alpha_dtype, n_experts, hidden, inter, offsets, pair_ids,
+                        inverse, topk_weight, residual, residual_dtype, h_out, ldh, y, ws, stream);
 }
