@@ -318,7 +318,7 @@ int ma_moe_grouped_noalloc(const void* x, int64_t ldx, const uint32_t* x_pairs,
  * add_rms_norm, src/maple_run/kernels/fused_norm.py:128-161.
  * With next_w != NULL the same launch also computes the next layer's input
  * projection from y: next_out bf16 [next_rows] = ternary_gemv(y, next_w
- * [next_rows, hidden/16], next_alpha (f32/bf16), rms_weight = next_rms
+ * [next_rows, hidden/16], next_alpha (alpha_dtype), rms_weight = next_rms
  * float32 [hidden], next_eps) -- the bits ma_ternary_gemv gives (reference
  * src/maple_run/kernels/ternary_gemv.py:110-146, the QKV projection of
  * MapleAttention, model.py:368-414); y, next_w and next_rms 16-byte aligned,

@@ -34,9 +34,6 @@
 
 namespace ma {
 
-constexpr int kFusedWaves = 4;
-
-
 // Workspace layout (256-byte lines of uint32 words; every counter and flag has
 // a line of its own so that arrivals and polls on different ones do not meet):
 //   line 0, word 2     error (1 = a wait timed out)
@@ -58,17 +55,19 @@ static_assert(kLogitOff + 256 * kLogitStride * 8 <= kMoeWsHeader, "workspace log
 
 // Shapes: H = 16 * KWH * LPRH (SwiGLU rows split over LPRH lanes), I = 16 *
 // KWI * LPRI (down rows over LPRI lanes), US SwiGLU iterations and UD down
-// row iterations per wave, TK experts per token, PER = ceil(E / 64).
-template <int KWH, int LPRH, int US, int KWI, int LPRI, int UD, int TK, int PER>
-__global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
+// row iterations per wave, TK experts per token, PER = ceil(E / 64), W waves
+// per workgroup, ADT the row scales' dtype (fixed at compile time: a run-time
+// dtype switch among the weight loads delayed their issue by 4 us).
+template <int KWH, int LPRH, int US, int KWI, int LPRI, int UD, int TK, int PER, int W, int ADT>
+__global__ __launch_bounds__(64 * W) void k_moe_fused(
     const uint16_t* __restrict__ xa, const uint16_t* __restrict__ xb,
     const void* __restrict__ norm_w, int norm_dt, float eps, const uint16_t* __restrict__ residual,
     const uint16_t* __restrict__ gate_w, const float* __restrict__ bias, int n_exp,
     const uint32_t* __restrict__ ug, const void* __restrict__ ug_alpha,
-    const uint32_t* __restrict__ dn, const void* __restrict__ dn_alpha, int alpha_dt,
+    const uint32_t* __restrict__ dn, const void* __restrict__ dn_alpha,
     uint16_t* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ wts_out,
     uint32_t* __restrict__ ws, const uint32_t* __restrict__ nx_w, const void* __restrict__ nx_alpha,
-    int nx_alpha_dt, const float* __restrict__ nx_rms, float nx_eps, int nx_rows,
+    const float* __restrict__ nx_rms, float nx_eps, int nx_rows,
     uint16_t* __restrict__ nx_out) {
   constexpr int NWH = KWH * LPRH, H = 16 * NWH;
   constexpr int NWI = KWI * LPRI, I = 16 * NWI;
@@ -76,8 +75,9 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   constexpr int OPW = US * PPI;                        // SwiGLU outputs per wave
   constexpr int RPID = 64 / LPRI;                      // down rows per wave pass
   constexpr int RPB = RPID * UD;                       // y rows per workgroup
-  constexpr int SPW = TK >= kFusedWaves ? TK / kFusedWaves : 1;
-  static_assert(TK % kFusedWaves == 0 || TK < kFusedWaves, "top-k split over waves");
+  constexpr int SPW = TK >= W ? TK / W : 1;
+  constexpr int NTH = 64 * W;                          // threads per workgroup
+  static_assert(TK % W == 0 || TK < W, "top-k split over waves");
 
   __shared__ __align__(16) uint32_t xs[NWH][8];
   __shared__ float cw[NWH];
@@ -85,8 +85,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   __shared__ float hc[TK][NWI];
   __shared__ int32_t s_ids[TK];
   __shared__ float s_wts[TK];
-  __shared__ float red[kFusedWaves], red2[kFusedWaves];
-  __shared__ float part[kFusedWaves][RPB];
+  __shared__ float red[W], red2[W];
+  __shared__ float part[W][RPB];
   // next projection: y, and its RMS-folded x' pairs (hi and lo words, and the
   // value each pair carries) for every word of y, laid out so that the LPRH
   // lanes sharing a row read consecutive entries: word w = LPRH-lane l's
@@ -122,14 +122,14 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   // takes the dot product with router row e (loaded alongside x)
   float dot = 0.f;
   {
-    // thread t owns words t, t + 256, ... (16 values each)
-    constexpr int WPT = (NWH + 255) / 256;
+    // thread t owns words t, t + NTH, ... (16 values each)
+    constexpr int WPT = (NWH + NTH - 1) / NTH;
     float v[WPT][16], nw[WPT][16];
     uint4 gr[WPT][2];
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
-      const int w = tid + 256 * i;
+      const int w = tid + NTH * i;
       const int wc = w < NWH ? w : NWH - 1;
       if (xb) {  // the norm weights, loaded with x
         if (norm_dt == MA_F32) {
@@ -183,7 +183,10 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
       ss = group_sum<64>(ss);
       if (lane == 0) red[wv] = ss;
       __syncthreads();
-      const float rstd = rsqrtf((red[0] + red[1] + red[2] + red[3]) / static_cast<float>(H) + eps);
+      float ssum = red[0];
+#pragma unroll
+      for (int w = 1; w < W; ++w) ssum += red[w];
+      const float rstd = rsqrtf(ssum / static_cast<float>(H) + eps);
 #pragma unroll
       for (int i = 0; i < WPT; ++i) {
 #pragma unroll
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     // that it goes out before this workgroup stages its x' pairs
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
-      if (tid + 256 * i < NWH) {
+      if (tid + NTH * i < NWH) {
         const uint32_t g[8] = {gr[i][0].x, gr[i][0].y, gr[i][0].z, gr[i][0].w,
                                gr[i][1].x, gr[i][1].y, gr[i][1].z, gr[i][1].w};
 #pragma unroll
@@ -209,12 +212,12 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     if (router_wg && tid == 0) {
       float l = red2[0];
 #pragma unroll
-      for (int w = 1; w < kFusedWaves; ++w) l += red2[w];
+      for (int w = 1; w < W; ++w) l += red2[w];
       st_coh64(&logits[kLogitStride * wg], tag | __float_as_uint(l + (bias ? bias[wg] : 0.f)));
     }
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
-      const int w = tid + 256 * i;
+      const int w = tid + NTH * i;
       if (w < NWH) {
         uint32_t pr[8];
         cw[w] = prep_word_pairs(v[i], pr);
@@ -224,19 +227,24 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     }
   }
 
-  // ---- 2. softmax + top-k (router semantics of reference kernels/router.py:
-  // 78-126), by wave 0 of every workgroup once it has seen all E logits of
-  // this call (each lane polls its tagged logit words until they carry this
-  // call's tag).  Slot s takes the largest probability left (the lowest expert
-  // index among equal ones) -- one wave-wide max and one ballot per slot, all
-  // in registers -- and the routing goes to the other waves through LDS.
+  // ---- 2. top-k (router semantics of reference kernels/router.py:78-126),
+  // by wave 0 of every workgroup once it has seen all E logits of this call
+  // (each lane polls its tagged logit words until they carry this call's
+  // tag).  The softmax is monotonic, so the experts are picked on the logits
+  // themselves: slot s takes the largest logit left (the lowest expert index
+  // among equal ones) -- one wave-wide integer max on order-preserving keys
+  // and one ballot per slot, all in registers.  The ids go to the other waves
+  // through LDS at once, so the expert weight loads are issued before the
+  // softmax is evaluated; the routing weights (p / (sum p_top + 1e-20), p the
+  // softmax over all E) follow while those loads are in flight.
+  float lg[PER];  // wave 0: the logits of experts lane, lane + 64, ...
+  int my_e = 0;
   if (wv == 0) {
-    float p[PER];
     bool have[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       have[i] = lane + 64 * i >= n_exp;
-      p[i] = -INFINITY;
+      lg[i] = -INFINITY;
     }
     for (;;) {
       bool done = true;
@@ -245,7 +253,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
         if (!have[i]) {
           const uint64_t v = ld_coh64(&logits[kLogitStride * (lane + 64 * i)]);
           have[i] = (v & 0xffffffff00000000ull) == tag;
-          p[i] = __uint_as_float(static_cast<uint32_t>(v));
+          lg[i] = __uint_as_float(static_cast<uint32_t>(v));
           done = done && have[i];
         }
       }
@@ -253,25 +261,10 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
       __builtin_amdgcn_s_sleep(2);
       timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
     }
-    int mk = INT_MIN;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) mk = max(mk, float_order_key(p[i]));
-    const float m = float_from_order_key(wave_max_ui(mk));
-    float sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int e = lane + 64 * i;
-      p[i] = e < n_exp ? expf(p[i] - m) : 0.f;
-      sum += p[i];
-    }
-    const float inv_sum = 1.0f / wave_sum_u(sum);
-    // probabilities are >= 0, so their bits order as integers; experts past
-    // E get -1 (below every probability), chosen ones INT_MIN
+    // experts past E get INT_MIN + 1 (below every logit), chosen ones INT_MIN
     int key[PER];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) key[i] = lane + 64 * i < n_exp ? __float_as_int(p[i] * inv_sum) : -1;
-    int my_e = 0;
-    float my_p = 0.f, sel = 0.f;
+    for (int i = 0; i < PER; ++i) key[i] = lane + 64 * i < n_exp ? float_order_key(lg[i]) : INT_MIN + 1;
 #pragma unroll
     for (int s = 0; s < TK; ++s) {
       int lk = key[0];
@@ -287,21 +280,11 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
 #pragma unroll
       for (int i = 0; i < PER; ++i)
         if (lane + 64 * i == e_s) key[i] = INT_MIN;
-      const float p_s = __int_as_float(mx);
-      sel += p_s;
-      if (lane == s) {
-        my_e = e_s;
-        my_p = p_s;
-      }
+      if (lane == s) my_e = e_s;
     }
-    const float inv_total = 1.0f / (sel + 1e-20f);
     if (lane < TK) {
       s_ids[lane] = my_e;
-      s_wts[lane] = my_p * inv_total;
-      if (wg == 0) {
-        ids_out[lane] = my_e;
-        wts_out[lane] = my_p * inv_total;
-      }
+      if (wg == 0) ids_out[lane] = my_e;
     }
   }
   __syncthreads();
@@ -309,7 +292,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   // ---- 3. weights: SwiGLU rows of this wave's h outputs, then the down rows
   // of this workgroup's y rows (every load issued before any arithmetic)
   const int klh = lane % LPRH, subh = lane / LPRH, half = subh / PPI, pi = subh % PPI;
-  const int o0 = (wg * kFusedWaves + wv) * OPW;  // this wave's first SwiGLU output
+  const int o0 = (wg * W + wv) * OPW;  // this wave's first SwiGLU output
   uint32_t wu[US][KWH];
   float au[US];
 #pragma unroll
@@ -320,44 +303,75 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     const int64_t e = clamp_id(s_ids[s], n_exp);
     const int64_t row = e * (2 * I) + j + half * I;
     load_words_v<KWH>(ug + row * NWH + klh * KWH, wu[u]);
-    au[u] = ld_f(ug_alpha, alpha_dt, row);
+    au[u] = ld_t<ADT>(ug_alpha, row);
   }
   const int kld = lane % LPRI, subd = lane / LPRI;
   const int rbase = wg * RPB;
   uint32_t wd[SPW][UD][KWI];
-  float ad[SPW][UD], wj[SPW];
+  float ad[SPW][UD];
 #pragma unroll
   for (int q = 0; q < SPW; ++q) {
-    const int js = wv + kFusedWaves * q;
+    const int js = wv + W * q;
     const int jj = js < TK ? js : 0;  // idle waves (TK < waves) read slot 0 and add nothing
     const int64_t e = clamp_id(s_ids[jj], n_exp);
-    wj[q] = js < TK ? s_wts[jj] : 0.f;
 #pragma unroll
     for (int u = 0; u < UD; ++u) {
       int r = rbase + u * RPID + subd;
       r = r < H ? r : H - 1;
       load_words_v<KWI>(dn + (e * H + r) * NWI + kld * KWI, wd[q][u]);
-      ad[q][u] = ld_f(dn_alpha, alpha_dt, e * H + r);
+      ad[q][u] = ld_t<ADT>(dn_alpha, e * H + r);
     }
   }
   // Next projection (optional): this workgroup's rows, issued after the
   // expert loads so that waiting for those never waits for these.  Lanes
   // split a row as the standalone GEMV does (LPRH lanes of KWH words), RPIH
   // rows per wave pass, NXP passes.
-  constexpr int NXP = 2;
+  constexpr int NXP = W == 4 ? 2 : 1;
   const int nx_rq = nx_w ? (nx_rows + G - 1) / G : 0;
   uint32_t nxw[NXP][KWH];
   float nxa[NXP];
   if (nx_w) {
 #pragma unroll
     for (int p = 0; p < NXP; ++p) {
-      int r = wg * nx_rq + p * kFusedWaves * RPIH + wv * RPIH + subh;
+      int r = wg * nx_rq + p * W * RPIH + wv * RPIH + subh;
       r = r < nx_rows ? r : nx_rows - 1;
       load_words_v<KWH>(nx_w + static_cast<int64_t>(r) * NWH + klh * KWH, nxw[p]);
-      nxa[p] = ld_f(nx_alpha, nx_alpha_dt, r);
+      nxa[p] = ld_t<ADT>(nx_alpha, r);
     }
   }
   MA_ISSUE_FENCE();
+
+  // routing weights, while the expert weights are in flight (read after the
+  // barrier below): the softmax over all E logits with the max-subtracted
+  // exp, then each chosen expert's probability over their sum + 1e-20 in slot
+  // order
+  if (wv == 0) {
+    int mk = INT_MIN;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) mk = max(mk, float_order_key(lg[i]));
+    const float m = float_from_order_key(wave_max_ui(mk));
+    float ex[PER], sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      ex[i] = lane + 64 * i < n_exp ? expf(lg[i] - m) : 0.f;
+      sum += ex[i];
+    }
+    const float inv_sum = 1.0f / wave_sum_u(sum);
+    float prob = 0.f;  // lane s < TK: the probability of the expert in slot s
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const float v = __shfl(ex[i] * inv_sum, my_e & 63, 64);
+      if ((my_e >> 6) == i) prob = v;
+    }
+    float sel = 0.f;
+#pragma unroll
+    for (int s = 0; s < TK; ++s) sel += lane_bcast(prob, s);
+    const float w = prob * (1.0f / (sel + 1e-20f));
+    if (lane < TK) {
+      s_wts[lane] = w;
+      if (wg == 0) wts_out[lane] = w;
+    }
+  }
 
   // SwiGLU outputs of this wave
   {
@@ -390,12 +404,12 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
   if (wv == 0) timed_out = grid_barrier_flags(ws + kLine * kSubB, flags, f0, G, wg, lane, t0) || timed_out;
   __syncthreads();
   {
-    constexpr int HIT = (TK * NWI + 255) / 256;  // h words per thread, all loads issued first
+    constexpr int HIT = (TK * NWI + NTH - 1) / NTH;  // h words per thread, all loads issued first
     const CoherentBuf hcb(hbuf, TK * I * 2);
     uint64_t d[HIT][4];
 #pragma unroll
     for (int it = 0; it < HIT; ++it) {
-      const int wi = tid + 256 * it;
+      const int wi = tid + NTH * it;
       const int wc = wi < TK * NWI ? wi : TK * NWI - 1;
       const uint32_t off = static_cast<uint32_t>(((wc / NWI) * I + (wc % NWI) * 16) * 2);
       const uint4 q0 = hcb.ld4u(off), q1 = hcb.ld4u(off + 16);
@@ -406,7 +420,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     }
 #pragma unroll
     for (int it = 0; it < HIT; ++it) {
-      const int wi = tid + 256 * it;
+      const int wi = tid + NTH * it;
       if (wi < TK * NWI) {
         const int s = wi / NWI, w = wi % NWI;
         float vv[16];
@@ -435,8 +449,9 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     for (int u = 0; u < UD; ++u) acc[u] = 0.f;
 #pragma unroll
     for (int q = 0; q < SPW; ++q) {
-      const int js = wv + kFusedWaves * q;
+      const int js = wv + W * q;
       const int jj = js < TK ? js : 0;
+      const float wjq = js < TK ? s_wts[jj] : 0.f;  // idle waves (TK < waves) add nothing
       XSlice<KWI> hsl;
       slice_from_lds<KWI>(hs[jj], hc[jj], kld, hsl);
 #pragma unroll
@@ -444,7 +459,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
         // each slot's down output is rounded to bf16 before the weighted sum,
         // as the reference's ternary_expert_gemv -> moe_reduce_add chain stores it
         const float eo = group_sum<LPRI>(slice_dot<KWI>(wd[q][u], hsl, kc) * ad[q][u]);
-        acc[u] += wj[q] * bf16_to_f32(f32_to_bf16(eo));
+        acc[u] += wjq * bf16_to_f32(f32_to_bf16(eo));
       }
     }
 #pragma unroll
@@ -456,7 +471,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     float v = xb ? bf16_to_f32(f32_to_bf16(__uint_as_float(ra << 16) + __uint_as_float(rb << 16)))
                  : residual ? __uint_as_float(ra << 16) : 0.f;
 #pragma unroll
-    for (int ww = 0; ww < kFusedWaves; ++ww) v += part[ww][tid];
+    for (int ww = 0; ww < W; ++ww) v += part[ww][tid];
     if (nx_w)
       st_coh16(&y[ro], f32_to_bf16(v));  // read back by every workgroup below
     else
@@ -476,11 +491,11 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
     {  // y (device-coherent) into LDS, and its x' pairs: thread t builds pairs
        // j0 .. j0 + 3 of word t / 2 (j0 = 4 (t & 1)), each from values j and
        // j + 8 of the word times their RMS weights
-      constexpr int PIT = (NWH * 2 + 255) / 256;
+      constexpr int PIT = (NWH * 2 + NTH - 1) / NTH;
       uint64_t y0[PIT], y1[PIT], ya[PIT], yb[PIT], wa[PIT][2], wb[PIT][2];
 #pragma unroll
       for (int k = 0; k < PIT; ++k) {
-        const int t = tid + 256 * k < NWH * 2 ? tid + 256 * k : NWH * 2 - 1;
+        const int t = tid + NTH * k < NWH * 2 ? tid + NTH * k : NWH * 2 - 1;
         const int w = t >> 1, j0 = 4 * (t & 1);
         const uint64_t* yp = reinterpret_cast<const uint64_t*>(y + w * 16 + 8 * (t & 1));
         y0[k] = ld_coh64(yp);  // values 8 (t & 1) .. + 8 of word w, raw
@@ -494,7 +509,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
       }
 #pragma unroll
       for (int k = 0; k < PIT; ++k) {
-        const int t = tid + 256 * k;
+        const int t = tid + NTH * k;
         if (t < NWH * 2) {
           const int w = t >> 1, j0 = 4 * (t & 1);
           const int col = (w % KWH) * LPRH + w / KWH;
@@ -561,7 +576,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_moe_fused(
         }
       }
       const float d = group_sum<LPRH>(((acc[0] + acc[1]) - c) * (nxa[p] * rstd));
-      const int rl = p * kFusedWaves * RPIH + wv * RPIH + subh;
+      const int rl = p * W * RPIH + wv * RPIH + subh;
       const int r = wg * nx_rq + rl;
       if (klh == 0 && rl < nx_rq && r < nx_rows) nx_out[r] = f32_to_bf16(d);
     }
@@ -580,11 +595,11 @@ namespace {
 // Supported (hidden, intermediate, top_k) shapes and their grid (at least
 // kBarGroups workgroups, and at least one per expert).
 struct FusedShape {
-  int hidden, inter, top_k, grid;
+  int hidden, inter, top_k, grid, waves;
 };
-// (2048, 768, 8): SwiGLU 24 outputs and down 8 rows per workgroup -> 256 groups.
-// (256, 128, 2): SwiGLU 16 outputs, down 8 rows per workgroup -> 32 groups.
-constexpr FusedShape kShapes[] = {{2048, 768, 8, 256}, {256, 128, 2, 32}};
+// (2048, 768, 8): 8 waves, SwiGLU 24 outputs and down 8 rows per workgroup -> 256 groups.
+// (256, 128, 2): 4 waves, SwiGLU 16 outputs, down 8 rows per workgroup -> 32 groups.
+constexpr FusedShape kShapes[] = {{2048, 768, 8, 256, 8}, {256, 128, 2, 32, 4}};
 static_assert(kShapes[0].grid >= kBarGroups && kShapes[1].grid >= kBarGroups, "barrier groups");
 
 const FusedShape* find_shape(int64_t hidden, int64_t inter, int64_t top_k) {
@@ -598,11 +613,16 @@ size_t ws_bytes(int64_t, int, int64_t inter, int64_t top_k) {
 }
 
 // The kernel instantiation a call launches (PER = 1 up to 64 experts, else 4).
-const void* fused_kernel(int64_t hidden, int64_t n_experts) {
+template <int ADT>
+const void* fused_kernel_t(int64_t hidden, int64_t n_experts) {
   if (hidden == 2048)
-    return n_experts <= 64 ? reinterpret_cast<const void*>(&k_moe_fused<4, 32, 6, 3, 16, 2, 8, 1>)
-                           : reinterpret_cast<const void*>(&k_moe_fused<4, 32, 6, 3, 16, 2, 8, 4>);
-  return reinterpret_cast<const void*>(&k_moe_fused<1, 16, 2, 1, 8, 1, 2, 1>);
+    return n_experts <= 64 ? reinterpret_cast<const void*>(&k_moe_fused<4, 32, 3, 3, 16, 2, 8, 1, 8, ADT>)
+                           : reinterpret_cast<const void*>(&k_moe_fused<4, 32, 3, 3, 16, 2, 8, 4, 8, ADT>);
+  return reinterpret_cast<const void*>(&k_moe_fused<1, 16, 2, 1, 8, 1, 2, 1, 4, ADT>);
+}
+const void* fused_kernel(int64_t hidden, int64_t n_experts, int alpha_dtype) {
+  return alpha_dtype == MA_F32 ? fused_kernel_t<MA_F32>(hidden, n_experts)
+                               : fused_kernel_t<MA_BF16>(hidden, n_experts);
 }
 
 }  // namespace
@@ -615,7 +635,7 @@ extern "C" int ma_moe_fused_resident(int64_t n_experts, int64_t hidden, int64_t 
   const FusedShape* s = find_shape(hidden, inter, top_k);
   if (!s || !needed || !capacity) return fail(MA_EVALUE, "moe_fused_resident: shape not built");
   *needed = s->grid;
-  return resident_capacity(fused_kernel(hidden, n_experts), 64 * kFusedWaves, capacity);
+  return resident_capacity(fused_kernel(hidden, n_experts, MA_BF16), 64 * s->waves, capacity);
 }
 
 extern "C" size_t ma_moe_fused_workspace_bytes(int64_t n_experts, int64_t hidden, int64_t inter,
@@ -654,17 +674,19 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
       !a16(up_gate) || !a16(workspace))
     return fail(MA_EVALUE, "moe_fused: x, x_add, norm weight, weights and workspace must be 16-byte aligned");
   if (next_w) {
-    const int64_t max_rows = static_cast<int64_t>(s->grid) * 2 * 4 * (hidden == 2048 ? 2 : 4);
+    // rows per workgroup pass: waves x rows per wave (2 at hidden 2048, 4 at 256), passes 8 / waves
+    const int64_t max_rows = static_cast<int64_t>(s->grid) * 8 * (hidden == 2048 ? 2 : 4);
     if (!next_alpha || !next_rms || !next_out || next_rows < 1 || next_rows > max_rows)
       return fail(MA_EVALUE, "moe_fused: next projection needs alpha, rms weight, output and 1..%lld rows",
                   static_cast<long long>(max_rows));
-    if (next_alpha_dtype != MA_F32 && next_alpha_dtype != MA_BF16)
-      return fail(MA_ETYPE, "moe_fused: next projection alpha dtype %d", next_alpha_dtype);
+    if (next_alpha_dtype != alpha_dtype)
+      return fail(MA_ETYPE, "moe_fused: next projection alpha dtype %d differs from the experts' %d",
+                  next_alpha_dtype, alpha_dtype);
     if (!a16(next_w) || !a16(next_rms) || !a16(y))
       return fail(MA_EVALUE, "moe_fused: next projection weights, rms weight and y must be 16-byte aligned");
   }
   int64_t capacity = 0;
-  if (int rc = resident_capacity(fused_kernel(hidden, n_experts), 64 * kFusedWaves, &capacity)) return rc;
+  if (int rc = resident_capacity(fused_kernel(hidden, n_experts, alpha_dtype), 64 * s->waves, &capacity)) return rc;
   if (capacity < s->grid)
     return fail(MA_ERUNTIME, "moe_fused: its %d workgroups wait on each other but the device holds %lld at once",
                 s->grid, static_cast<long long>(capacity));
@@ -674,18 +696,26 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
   static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(x_add), norm_weight, norm_dtype, \
       eps, static_cast<const uint16_t*>(residual), static_cast<const uint16_t*>(gate_weight),    \
       router_bias, static_cast<int>(n_experts), up_gate,                                         \
-      up_gate_alpha, down, down_alpha, alpha_dtype,                                              \
+      up_gate_alpha, down, down_alpha,                                                           \
       static_cast<uint16_t*>(y), topk_ids, topk_weight, static_cast<uint32_t*>(workspace),       \
-      next_w, next_alpha, next_alpha_dtype, next_rms, next_eps, static_cast<int>(next_rows),      \
+      next_w, next_alpha, next_rms, next_eps, static_cast<int>(next_rows),                        \
       static_cast<uint16_t*>(next_out)
-  if (hidden == 2048) {
-    if (per == 1)
-      hipLaunchKernelGGL((k_moe_fused<4, 32, 6, 3, 16, 2, 8, 1>), dim3(s->grid), dim3(256), 0, st, MA_FUSED_ARGS);
-    else
-      hipLaunchKernelGGL((k_moe_fused<4, 32, 6, 3, 16, 2, 8, 4>), dim3(s->grid), dim3(256), 0, st, MA_FUSED_ARGS);
-  } else {
-    hipLaunchKernelGGL((k_moe_fused<1, 16, 2, 1, 8, 1, 2, 1>), dim3(s->grid), dim3(256), 0, st, MA_FUSED_ARGS);
+  const dim3 grid(s->grid), block(64 * s->waves);
+#define MA_FUSED_LAUNCH(ADT)                                                                      \
+  if (hidden == 2048) {                                                                          \
+    if (per == 1)                                                                                \
+      hipLaunchKernelGGL((k_moe_fused<4, 32, 3, 3, 16, 2, 8, 1, 8, ADT>), grid, block, 0, st, MA_FUSED_ARGS); \
+    else                                                                                         \
+      hipLaunchKernelGGL((k_moe_fused<4, 32, 3, 3, 16, 2, 8, 4, 8, ADT>), grid, block, 0, st, MA_FUSED_ARGS); \
+  } else {                                                                                       \
+    hipLaunchKernelGGL((k_moe_fused<1, 16, 2, 1, 8, 1, 2, 1, 4, ADT>), grid, block, 0, st, MA_FUSED_ARGS); \
   }
+  if (alpha_dtype == MA_F32) {
+    MA_FUSED_LAUNCH(MA_F32)
+  } else {
+    MA_FUSED_LAUNCH(MA_BF16)
+  }
+#undef MA_FUSED_LAUNCH
 #undef MA_FUSED_ARGS
   return check_launch("moe_fused");
 }

@@ -205,7 +205,7 @@ class SyntheticDecoder:
             # add + RMSNorm + router + experts + combine (+ the next layer's
             # RMS-folded QKV projection) in one launch
             nl = None
-            if fuse_next and i + 1 < c.layers:
+            if fuse_next and i + 1 < c.layers and self.layers[i + 1].qkv_alpha.dtype == L.moe.up_gate_alpha.dtype:
                 n = self.layers[i + 1]
                 nl = (n.qkv, n.qkv_alpha, n.input_ln, c.eps)
             out = moe_fused(hidden, L.moe, c.top_k, add=o, norm_weight=L.post_ln, eps=c.eps,

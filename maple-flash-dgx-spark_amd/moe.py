@@ -127,6 +127,8 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
             raise ValueError("next_linear must be ([N, hidden/16] uint32, alpha [N], float32 rms [hidden], eps)")
         nx_rows = int(nx_w.shape[0])
         nx_a, nx_r = nx_a.contiguous(), nx_r.contiguous()
+        if nx_a.dtype != layer.up_gate_alpha.dtype:
+            raise TypeError("next_linear alpha must have the experts' row_alpha dtype")
         nx_out = torch.empty(1, nx_rows, device=x.device, dtype=torch.bfloat16)
     _lib.call(
         "ma_moe_fused",
