@@ -80,7 +80,8 @@ int ma_ternary_gemv_ws(const void* x, int x_dtype, int64_t batch, int64_t ldx,
  * bf16 -- the values ma_moe_grouped's combine stores -- is written to x_out
  * (bf16 [batch, nwords * 16]) and is the GEMM's x; y as ma_ternary_gemv_ws
  * with that x.  slot_out is the per-pair down output ma_moe_grouped leaves at
- * byte offset n_pairs * inter * 2 of its workspace (bf16 [n_pairs, hidden]);
+ * byte offset n_pairs * inter * 2 (rounded up to a multiple of 256) of its
+ * workspace (bf16 [n_pairs, hidden]);
  * call ma_moe_grouped with y = NULL to skip its own combine.  Needs
  * rms_weight, batch >= 17, nwords % 16 == 0, top_k <= 8, bf16 rows and
  * 16-byte aligned buffers (returns MA_EVALUE otherwise); workspace as for
@@ -253,7 +254,8 @@ int ma_moe_route(const void* x, const void* x_add, int64_t tokens, int64_t hidde
  * (float32 [tokens]); decode batches then read the operands from there
  * instead of building them from x (x is still passed).  The per-pair down
  * outputs stay in the workspace at byte offset tokens * top_k * inter * 2
- * (bf16 [tokens * top_k, hidden]); with y = NULL the combine is skipped
+ * rounded up to a multiple of 256 (bf16 [tokens * top_k, hidden]); with
+ * y = NULL the combine is skipped
  * (ma_ternary_gemv_combine_ws can run it in front of the next GEMM).
  * Replaces MapleSparseMoeBlock's SwiGLU -> down -> moe_reduce_add chain
  * (src/maple_run/model.py:468-473) for token counts where experts see many
@@ -274,8 +276,8 @@ int ma_moe_grouped(const void* x, int64_t ldx, const uint32_t* x_pairs, const fl
  * ma_moe_grouped with no workspace argument that allocates nothing: the same
  * kernels stage h and the per-pair down outputs in a device array built into
  * the library (one per GPU, held until the process ends), of
- * ma_moe_grouped_noalloc_max_bytes() bytes (16 MiB: up to 2978 (token,
- * expert) pairs at hidden 2048 / intermediate 768, i.e. 372 tokens at top-8).
+ * ma_moe_grouped_noalloc_max_bytes() bytes (16 MiB: up to 339 tokens at
+ * top-8, 2712 (token, expert) pairs, at hidden 2048 / intermediate 768).
  * Larger calls return MA_EVALUE.  y is required (the per-pair outputs stay in
  * the internal array).  Every call on one GPU shares that array: calls that
  * overlap on one GPU (other streams, other threads) race; calls ordered on a

@@ -4,27 +4,27 @@
 // [tokens x K] operand, so the SwiGLU up+gate projection and the down
 // projection become per-expert GEMMs: y = W_e (rows x K) . X_e^T (K x tokens).
 //
-// A operand (weights): a lane loads 16 bytes = 4 words = 64 codes of one row
-// per 256-code chunk and expands each word with expand_word (common.h) into
-// 8 bf16x2 dwords of 1 + c/f -- exactly the dword order of the bf16 x' pairs,
-// which is an (arbitrary but shared) permutation of K inside each word.
-// B operand (activations): x' = f * x pairs staged in LDS per chunk.  The
-// MFMA then accumulates sum (f + c) x; subtracting C_t = sum (f + 1) x per
-// token leaves sum (c - 1) x, the ternary product (float32 accumulation).
+// A operand (weights): each lane expands its own packed words with
+// expand_word (common.h) into bf16x2 dwords of 1 + c/f -- exactly the dword
+// order of the bf16 x' pairs, an (arbitrary but shared) permutation of K
+// inside each word.  B operand (activations): x' = f * x pairs.  The MFMA then
+// accumulates sum (f + c) x; subtracting C_t = sum (f + 1) x per token
+// leaves sum (c - 1) x, the ternary product (float32 accumulation).
 //
 // v_mfma_f32_16x16x32_bf16 lane layout (checked on the device):
 //   A: lane l holds row l%16, k 8(l/16)..+8;  B: col l%16, k 8(l/16)..+8;
 //   C: lane l holds col l%16, rows 4(l/16)..+4.
 //
-// Stage 1: a workgroup owns 128 intermediate rows (each wave 32 up rows and
-// the 32 matching gate rows, so SwiGLU is applied in registers) and a tile of
-// 16*NB pairs of one expert.  It writes h (rounded to bf16 like the
-// reference's x.dtype store, ternary_expert.py:441) in the x' pair layout the
-// down stage reads, and optionally in the plain [slot, I] layout.
-// Stage 2: a workgroup owns 256 output rows (each wave 64) and writes each
-// pair's down output rounded to bf16 (ternary_expert.py:208); a gather
-// kernel then forms y[t] = sum_j w[t,j] out[pair(t,j)] (+ residual) in
-// float32 (fused_norm.py:83-96).
+// Two forms: decode batches (few pairs per expert: 16-pair tiles, K split
+// over the waves, operands in registers) and prefill (128-pair x 256-row
+// tiles with the x' operands staged in LDS).  Stage 1 computes h (each wave
+// holds up rows and the matching gate rows, so SwiGLU is applied in
+// registers), rounded to bf16 like the reference's x.dtype store
+// (ternary_expert.py:441), in the x' pair layout the down stage reads and
+// optionally in the plain [slot, I] layout.  Stage 2 writes each pair's down
+// output rounded to bf16 (ternary_expert.py:208); a gather kernel then forms
+// y[t] = sum_j w[t,j] out[pair(t,j)] (+ residual) in float32
+// (fused_norm.py:83-96).
 #include <mutex>
 
 #include "mfma.h"
@@ -34,7 +34,6 @@ namespace ma {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kChunkWords = 16;  // 256 codes of K per step
 
 __device__ __forceinline__ f32x4_t mfma_bf16(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -103,266 +102,6 @@ __device__ __forceinline__ float pairs_cst(const uint32_t pr[8]) {
     c += ((f + 1.0f) / f) * (__uint_as_float(pr[j] << 16) + __uint_as_float(pr[j] & 0xffff0000u));
   }
   return c;
-}
-
-template <int NB, int ADT>
-__global__ __launch_bounds__(256) void k_grouped_swiglu(
-    const uint16_t* __restrict__ x, int64_t ldx, int64_t topk,
-    const uint32_t* __restrict__ w, int64_t n_half, int64_t nwords,
-    const void* __restrict__ alpha, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ pair_ids, int n_exp,
-    uint16_t* __restrict__ hp, uint16_t* __restrict__ h, int64_t ldh) {
-  constexpr int NT = 16 * NB;
-  __shared__ __align__(16) uint32_t xs[kChunkWords][2][NT][4];  // word-major: conflict-free B reads
-  __shared__ float cst[NT], cw[kChunkWords][NT];  // corrections: per word, then summed in word order
-  __shared__ int32_t tok[NT], pid[NT];
-  int e, pos0, np;
-  if (!decode_tile(offsets, n_exp, blockIdx.y, NT, e, pos0, np)) return;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int r16 = lane & 15, g = lane >> 4;
-  if (tid < NT) {
-    const int p = tid < np ? pair_ids[pos0 + tid] : -1;
-    pid[tid] = p;
-    tok[tid] = p >= 0 ? static_cast<int>(p / topk) : -1;
-    cst[tid] = 0.f;
-  }
-  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * 128 + 32 * wv;
-  const uint32_t* we = w + static_cast<int64_t>(e) * (2 * n_half) * nwords;
-  const uint32_t* rowp[4];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    int64_t i = i0 + 16 * (mb & 1) + r16;
-    i = i < n_half ? i : n_half - 1;
-    rowp[mb] = we + (i + (mb >> 1) * n_half) * nwords + 4 * g;
-  }
-  f32x4_t acc[4][NB];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const ExpandConsts kc;
-  __syncthreads();
-  // Weights and x of chunk c0 (x' staging items: NT columns x 16 words, NB
-  // per thread); the next chunk's are in flight during this chunk's work.
-  auto load_chunk = [&](int64_t c0, uint4 (&wq)[4], uint4 (&xa)[NB], uint4 (&xb)[NB]) {
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) wq[mb] = *reinterpret_cast<const uint4*>(rowp[mb] + c0);
-#pragma unroll
-    for (int it = 0; it < NB; ++it) {
-      const int item = tid + 256 * it;
-      const int col = item % NT, wd = item / NT;
-      const int t = tok[col];
-      const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t < 0 ? 0 : t) * ldx + (c0 + wd) * 16);
-      xa[it] = src[0];
-      xb[it] = src[1];
-    }
-  };
-  uint4 wq[4], xa[NB], xb[NB];
-  load_chunk(0, wq, xa, xb);
-  for (int64_t c0 = 0; c0 < nwords; c0 += kChunkWords) {
-    uint4 wn[4], xan[NB], xbn[NB];
-    load_chunk(c0 + kChunkWords < nwords ? c0 + kChunkWords : c0, wn, xan, xbn);
-    // (no sched_barrier here: with loads into loop-carried registers just
-    // above, it produced wrong MFMA operands on this compiler)
-#pragma unroll
-    for (int it = 0; it < NB; ++it) {
-      const int item = tid + 256 * it;
-      const int col = item % NT, wd = item / NT;
-      uint32_t pr[8];
-      float c = 0.f;
-      if (tok[col] >= 0) {
-        c = x16_to_pairs(xa[it], xb[it], pr);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pr[j] = 0u;
-      }
-      *reinterpret_cast<uint4*>(&xs[wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-      *reinterpret_cast<uint4*>(&xs[wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
-      cw[wd][col] = c;
-    }
-    __syncthreads();
-    if (tid < NT) {  // a fixed order: the same bits on every run
-      float c = cst[tid];
-#pragma unroll
-      for (int wd = 0; wd < kChunkWords; ++wd) c += cw[wd][tid];
-      cst[tid] = c;
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {  // word q of the lane's 4 -> MFMA steps 2q, 2q+1
-      uint4 a[4][2];
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const uint32_t wsel = q == 0 ? wq[mb].x : q == 1 ? wq[mb].y : q == 2 ? wq[mb].z : wq[mb].w;
-        uint32_t ex[8];
-        expand_word(wsel, ex, kc);
-        a[mb][0] = make_uint4(ex[0], ex[1], ex[2], ex[3]);
-        a[mb][1] = make_uint4(ex[4], ex[5], ex[6], ex[7]);
-      }
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const uint4 b = *reinterpret_cast<const uint4*>(&xs[4 * g + q][hf][nb * 16 + r16][0]);
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb) acc[mb][nb] = mfma_bf16(a[mb][hf], b, acc[mb][nb]);
-        }
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) wq[mb] = wn[mb];
-#pragma unroll
-    for (int it = 0; it < NB; ++it) {
-      xa[it] = xan[it];
-      xb[it] = xbn[it];
-    }
-  }
-  // Epilogue: rows i0 + 16 mb + 4 g + r (up: mb 0,1; gate: mb 2,3 -> same rows).
-  const int64_t nwh = n_half / 16;
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t i = i0 + 16 * mb + 4 * g + r;
-      if (i >= n_half) continue;
-      const int64_t ia = i < n_half ? i : n_half - 1;
-      const float au = ld_t<ADT>(alpha, static_cast<int64_t>(e) * 2 * n_half + ia);
-      const float ag = ld_t<ADT>(alpha, static_cast<int64_t>(e) * 2 * n_half + n_half + ia);
-      const int pos = static_cast<int>(i & 15), j = pos & 7, hh = pos >> 3;
-      const float f = pair_scale(j);
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int col = nb * 16 + r16;
-        if (col >= np) continue;
-        const float c = cst[col];
-        const float up = au * (acc[mb][nb][r] - c);
-        const float gt = ag * (acc[mb + 2][nb][r] - c);
-        const uint16_t hb = f32_to_bf16(swiglu_act(up, gt));
-        if (hp) {
-          const float hv = bf16_to_f32(hb) * f;  // exact: power-of-two scale
-          hp[((static_cast<int64_t>(pos0 + col) * nwh + (i >> 4)) * 8 + j) * 2 + hh] =
-              static_cast<uint16_t>(bf16_bits_exact(hv));
-        }
-        if (h) h[static_cast<int64_t>(pid[col]) * ldh + i] = hb;
-      }
-    }
-  }
-}
-
-template <int NB, int ADT>
-__global__ __launch_bounds__(256) void k_grouped_down(
-    const uint32_t* __restrict__ hp, const uint32_t* __restrict__ w, int64_t n_out,
-    int64_t nwk, const void* __restrict__ alpha, const int32_t* __restrict__ offsets,
-    int n_exp, uint16_t* __restrict__ out) {
-  constexpr int NT = 16 * NB;
-  __shared__ __align__(16) uint32_t xs[kChunkWords][2][NT][4];  // word-major: conflict-free B reads
-  __shared__ float cst[NT], cw[kChunkWords][NT];  // corrections: per word, then summed in word order
-  int e, pos0, np;
-  if (!decode_tile(offsets, n_exp, blockIdx.y, NT, e, pos0, np)) return;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int r16 = lane & 15, g = lane >> 4;
-  if (tid < NT) cst[tid] = 0.f;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 256 + 64 * wv;
-  const uint32_t* we = w + static_cast<int64_t>(e) * n_out * nwk;
-  const uint32_t* rowp[4];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    int64_t n = n0 + 16 * mb + r16;
-    n = n < n_out ? n : n_out - 1;
-    rowp[mb] = we + n * nwk + 4 * g;
-  }
-  f32x4_t acc[4][NB];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const ExpandConsts kc;
-  __syncthreads();
-  auto load_chunk = [&](int64_t c0, uint4 (&wq)[4], uint4 (&ha)[NB], uint4 (&hb)[NB]) {
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) wq[mb] = *reinterpret_cast<const uint4*>(rowp[mb] + c0);
-#pragma unroll
-    for (int it = 0; it < NB; ++it) {
-      const int item = tid + 256 * it;
-      const int col = item % NT, wd = item / NT;
-      const int64_t prow = pos0 + (col < np ? col : 0);
-      const uint4* src = reinterpret_cast<const uint4*>(hp + (prow * nwk + c0 + wd) * 8);
-      ha[it] = src[0];
-      hb[it] = src[1];
-    }
-  };
-  uint4 wq[4], ha[NB], hb[NB];
-  load_chunk(0, wq, ha, hb);
-  for (int64_t c0 = 0; c0 < nwk; c0 += kChunkWords) {
-    uint4 wn[4], han[NB], hbn[NB];
-    load_chunk(c0 + kChunkWords < nwk ? c0 + kChunkWords : c0, wn, han, hbn);
-    // (no sched_barrier here: with loads into loop-carried registers just
-    // above, it produced wrong MFMA operands on this compiler)
-#pragma unroll
-    for (int it = 0; it < NB; ++it) {
-      const int item = tid + 256 * it;
-      const int col = item % NT, wd = item / NT;
-      uint32_t pr[8] = {ha[it].x, ha[it].y, ha[it].z, ha[it].w, hb[it].x, hb[it].y, hb[it].z, hb[it].w};
-      if (col >= np) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pr[j] = 0u;
-      }
-      *reinterpret_cast<uint4*>(&xs[wd][0][col][0]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-      *reinterpret_cast<uint4*>(&xs[wd][1][col][0]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
-      cw[wd][col] = pairs_cst(pr);
-    }
-    __syncthreads();
-    if (tid < NT) {  // a fixed order: the same bits on every run
-      float c = cst[tid];
-#pragma unroll
-      for (int wd = 0; wd < kChunkWords; ++wd) c += cw[wd][tid];
-      cst[tid] = c;
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint4 a[4][2];
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const uint32_t wsel = q == 0 ? wq[mb].x : q == 1 ? wq[mb].y : q == 2 ? wq[mb].z : wq[mb].w;
-        uint32_t ex[8];
-        expand_word(wsel, ex, kc);
-        a[mb][0] = make_uint4(ex[0], ex[1], ex[2], ex[3]);
-        a[mb][1] = make_uint4(ex[4], ex[5], ex[6], ex[7]);
-      }
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const uint4 b = *reinterpret_cast<const uint4*>(&xs[4 * g + q][hf][nb * 16 + r16][0]);
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb) acc[mb][nb] = mfma_bf16(a[mb][hf], b, acc[mb][nb]);
-        }
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) wq[mb] = wn[mb];
-#pragma unroll
-    for (int it = 0; it < NB; ++it) {
-      ha[it] = han[it];
-      hb[it] = hbn[it];
-    }
-  }
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t n = n0 + 16 * mb + 4 * g + r;
-      if (n >= n_out) continue;
-      const float a = ld_t<ADT>(alpha, static_cast<int64_t>(e) * n_out + n);
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int col = nb * 16 + r16;
-        if (col >= np) continue;
-        out[static_cast<int64_t>(pos0 + col) * n_out + n] = f32_to_bf16(a * (acc[mb][nb][r] - cst[col]));
-      }
-    }
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -957,6 +696,377 @@ __global__ __launch_bounds__(256) void k_combine8(const uint16_t* __restrict__ o
   *reinterpret_cast<uint4*>(y + t * n + i) = o;
 }
 
+// ---------------------------------------------------------------------------
+// Prefill form (many pairs per expert): tiles of 128 pairs x 256 weight rows,
+// eight waves (4 along the rows x 2 along the pairs, 64 x 64 each), K walked
+// in steps of 8 words (128 codes) with the pairs' x' operands double-buffered
+// in LDS (one barrier per step) and the next step's weights and x' loaded
+// during this step's MFMAs.  x' pairs and the per-token correction are built
+// once per token (k_gp_prep), so staging is a copy.  Each lane expands its
+// own weight words in registers: a lane group g takes words 2g and 2g+1 of
+// a step, substep s (K = 32) the pairs 4(s & 1)..+3 of word 2g + (s >> 1) --
+// the same K permutation on both operands.  Tiles go to workgroups so that
+// the row tiles of one pair tile share an XCD (workgroups are placed on the 8
+// XCDs round-robin), which keeps that tile's x' in one L2.
+// ---------------------------------------------------------------------------
+namespace gp {
+constexpr int kTok = 128;    // pairs per tile
+constexpr int kRows = 256;   // weight rows per tile (SwiGLU: 128 up + the 128 matching gate rows)
+constexpr int kWords = 8;    // packed words of K per step
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kXcds = 8;
+constexpr int kTokPad = kTok + 1;  // LDS row of one (word, half): 129 x 16 B, so both
+                                   // the copies (16 halves of a pair) and the B reads
+                                   // (16 pairs of a half) are free of bank conflicts
+constexpr int kXsDwords = 2 * kWords * kTokPad * 4;  // one buffer
+// After the K loop the same LDS stages the output tile for coalesced stores:
+// h as [pair][128 outputs] (rows padded to 136 bf16), the down outputs as
+// [pair][256 rows] (rows padded to 264 bf16); the padding keeps the 16 pair
+// columns of a lane group on different banks and every row 16-byte aligned.
+constexpr int kHRow = 136, kORow = 264;
+constexpr int kLdsDwords = (2 * kXsDwords > kTok * kORow / 2) ? 2 * kXsDwords : kTok * kORow / 2;
+}  // namespace gp
+
+// x' pairs of every token once: xp [T, nwords * 8] (word w: pair j =
+// (f_j x[16w+j], f_j x[16w+j+8])) and xc[t] = sum (f + 1) x over the row, in
+// a fixed order.
+__global__ __launch_bounds__(128) void k_gp_prep(const uint16_t* __restrict__ x, int64_t ldx,
+                                                 int64_t nwords, uint32_t* __restrict__ xp,
+                                                 float* __restrict__ xc) {
+  __shared__ float red[2];
+  const int64_t t = blockIdx.x;
+  const int tid = threadIdx.x;
+  float c = 0.f;
+  for (int64_t wd = tid; wd < nwords; wd += 128) {
+    const uint4* src = reinterpret_cast<const uint4*>(x + t * ldx + wd * 16);
+    uint32_t pr[8];
+    c += x16_to_pairs(src[0], src[1], pr);
+    uint4* dst = reinterpret_cast<uint4*>(xp + (t * nwords + wd) * 8);
+    dst[0] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+    dst[1] = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+  }
+  c = group_sum<64>(c);
+  if ((tid & 63) == 0) red[tid >> 6] = c;
+  __syncthreads();
+  if (tid == 0) xc[t] = red[0] + red[1];
+}
+
+// Tile of workgroup L: the row tiles of a pair tile on one XCD.
+__device__ __forceinline__ void gp_tile(int n_rtiles, int& mtile, int& rtile) {
+  const int L = blockIdx.x, xcd = L % gp::kXcds, slot = L / gp::kXcds;
+  mtile = (slot / n_rtiles) * gp::kXcds + xcd;
+  rtile = slot % n_rtiles;
+}
+
+// One K step of a wave: 4 row blocks x 4 pair blocks x 4 substeps of
+// v_mfma_f32_16x16x32_bf16.  wq: the lane's two words of its 4 row blocks.
+__device__ __forceinline__ void gp_step(const uint2 (&wq)[4], const uint32_t* __restrict__ xsb,
+                                        int g, int r16, int col0, f32x4_t (&acc)[4][4],
+                                        const ExpandConsts& kc) {
+#pragma unroll
+  for (int ww = 0; ww < 2; ++ww) {
+    uint32_t ex[4][8];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) expand_word(ww ? wq[mb].y : wq[mb].x, ex[mb], kc);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      // xs layout [word][half][pair (padded to 129)][4 dwords]
+      const uint32_t* bp = xsb + ((2 * g + ww) * 2 + hh) * gp::kTokPad * 4;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const uint4 b = *reinterpret_cast<const uint4*>(bp + (col0 + nb * 16 + r16) * 4);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const uint4 a = make_uint4(ex[mb][4 * hh], ex[mb][4 * hh + 1], ex[mb][4 * hh + 2], ex[mb][4 * hh + 3]);
+          acc[mb][nb] = mfma_bf16(a, b, acc[mb][nb]);
+        }
+      }
+    }
+  }
+}
+
+// One step's x' operands are 128 pairs x 8 words x 2 halves of 16 B, 4 per
+// thread: copy i of thread tid is chunk c = tid + 512 i, (word, half) c % 16
+// and pair column c / 16, so 16 consecutive lanes copy one pair's 256
+// contiguous bytes (the LDS layout is [word][half][pair][4 dwords], pairs
+// padded to 129).
+// (Plain named members rather than arrays, and no lambdas capturing
+// locals: either put the copies in scratch memory on this compiler.)
+struct GpX {
+  uint4 a, b, c, d;
+};
+struct GpSrc {
+  const uint32_t *a, *b, *c, *d;
+};
+__device__ __forceinline__ void gp_load_x(const GpSrc& s, int64_t k0, GpX& x) {
+  x.a = *reinterpret_cast<const uint4*>(s.a + k0 * 8);
+  x.b = *reinterpret_cast<const uint4*>(s.b + k0 * 8);
+  x.c = *reinterpret_cast<const uint4*>(s.c + k0 * 8);
+  x.d = *reinterpret_cast<const uint4*>(s.d + k0 * 8);
+}
+__device__ __forceinline__ void gp_store_x(uint32_t* __restrict__ xsb, const GpX& x) {
+  constexpr int kStep = gp::kThreads / 16;  // pair columns between a thread's copies
+  uint4* p = reinterpret_cast<uint4*>(xsb) + (threadIdx.x % 16) * gp::kTokPad + threadIdx.x / 16;
+  p[0] = x.a;
+  p[kStep] = x.b;
+  p[2 * kStep] = x.c;
+  p[3 * kStep] = x.d;
+}
+// Sources of a thread's copies: rows[t] is the row of pair column t in the
+// uint32 array base with row length ld.
+__device__ __forceinline__ const uint32_t* gp_x_source(const uint32_t* base, int64_t ld,
+                                                       const int32_t* rows, int i) {
+  const int c = threadIdx.x + gp::kThreads * i;
+  const int t = c / 16, rest = c % 16;
+  return base + static_cast<int64_t>(rows[t]) * ld + (rest >> 1) * 8 + 4 * (rest & 1);
+}
+__device__ __forceinline__ GpSrc gp_x_sources(const uint32_t* base, int64_t ld, const int32_t* rows) {
+  return GpSrc{gp_x_source(base, ld, rows, 0), gp_x_source(base, ld, rows, 1),
+               gp_x_source(base, ld, rows, 2), gp_x_source(base, ld, rows, 3)};
+}
+
+// SwiGLU stage: h = SwiGLU(up, gate) of 128 outputs (rows [o, o+128) of the
+// up half and the matching gate rows) for a tile of 128 pairs of expert e,
+// rounded to bf16 and written in the x' pair layout the down stage reads (hp)
+// and optionally in slot order (h); hcorr[pos * n_rtiles + rtile] gets the
+// tile's part of the down stage's correction sum (f + 1) h.
+template <int ADT>
+__global__ __launch_bounds__(gp::kThreads) void k_gp_swiglu(
+    const uint32_t* __restrict__ xp, const float* __restrict__ xc, int64_t topk,
+    const uint32_t* __restrict__ w, int64_t n_half, int64_t nwords,
+    const void* __restrict__ alpha, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ pair_ids, int n_exp, uint16_t* __restrict__ hp,
+    float* __restrict__ hcorr, uint16_t* __restrict__ h, int64_t ldh) {
+  using namespace gp;
+  __shared__ __align__(16) uint32_t xs[kLdsDwords];
+  __shared__ float cst[kTok], hcp[4][kTok];
+  __shared__ int32_t tokrow[kTok], pid[kTok];
+  const int n_rtiles = static_cast<int>((n_half + kRows / 2 - 1) / (kRows / 2));
+  int mtile, rtile;
+  gp_tile(n_rtiles, mtile, rtile);
+  int e, pos0, np;
+  if (!decode_tile(offsets, n_exp, mtile, kTok, e, pos0, np)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wr = wv & 3, wm = wv >> 2, r16 = lane & 15, g = lane >> 4;
+  if (tid < kTok) {
+    const int p = tid < np ? pair_ids[pos0 + tid] : -1;
+    pid[tid] = p;
+    const int t = p >= 0 ? static_cast<int>(p / topk) : 0;
+    tokrow[tid] = t;
+    cst[tid] = p >= 0 ? xc[t] : 0.f;
+  }
+  const int64_t o0 = static_cast<int64_t>(rtile) * (kRows / 2) + wr * 32;  // this wave's first output
+  const uint32_t* we = w + static_cast<int64_t>(e) * 2 * n_half * nwords;
+  const uint32_t* rowp[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    int64_t i = o0 + 16 * (mb & 1) + r16;
+    i = i < n_half ? i : n_half - 1;
+    rowp[mb] = we + (i + (mb >> 1) * n_half) * nwords + 2 * g;
+  }
+  __syncthreads();  // tokrow
+  const GpSrc xsrc = gp_x_sources(xp, nwords * 8, tokrow);
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const ExpandConsts kc;
+  // Weights are loaded two steps ahead (the compiler places those loads at
+  // the end of a step, next to their loop-carried use), x' one step ahead.
+  uint2 wq[4], wn[4];
+  GpX xq;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    wq[mb] = *reinterpret_cast<const uint2*>(rowp[mb]);
+    wn[mb] = *reinterpret_cast<const uint2*>(rowp[mb] + (kWords < nwords ? kWords : 0));
+  }
+  gp_load_x(xsrc, 0, xq);
+  gp_store_x(xs, xq);
+  __syncthreads();
+  int buf = 0;
+  for (int64_t k0 = 0; k0 < nwords; k0 += kWords) {
+    const int64_t kn = k0 + kWords < nwords ? k0 + kWords : k0;
+    const int64_t knn = k0 + 2 * kWords < nwords ? k0 + 2 * kWords : k0;
+    gp_load_x(xsrc, kn, xq);
+    MA_ISSUE_FENCE();  // the next step's x' loads stay ahead of this step's MFMAs
+    gp_step(wq, xs + buf * kXsDwords, g, r16, wm * 64, acc, kc);
+    uint2 wnn[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) wnn[mb] = *reinterpret_cast<const uint2*>(rowp[mb] + knn);
+    gp_store_x(xs + (buf ^ 1) * kXsDwords, xq);
+    __syncthreads();
+    buf ^= 1;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      wq[mb] = wn[mb];
+      wn[mb] = wnn[mb];
+    }
+  }
+  // Epilogue: lane (r16, g) of row block mb holds rows 4g..4g+3 of the block
+  // for pair column wm*64 + nb*16 + r16.  h goes to LDS in the x' pair layout
+  // of its 8 words (the loop's last barrier has freed the LDS), then out in
+  // 16-byte pieces, each pair's 256 bytes contiguous.
+  uint16_t* hst = reinterpret_cast<uint16_t*>(xs);
+  const int64_t otile = static_cast<int64_t>(rtile) * (kRows / 2);
+  float hcl[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t i = o0 + 16 * mb + 4 * g + r;
+      const int64_t ia = i < n_half ? i : n_half - 1;
+      const float au = ld_t<ADT>(alpha, static_cast<int64_t>(e) * 2 * n_half + ia);
+      const float ag = ld_t<ADT>(alpha, static_cast<int64_t>(e) * 2 * n_half + n_half + ia);
+      const int pos = static_cast<int>(i & 15), j = pos & 7, hh = pos >> 3;
+      const float f = pair_scale(j);
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const int col = wm * 64 + nb * 16 + r16;
+        const float c = cst[col];
+        const float up = au * (acc[mb][nb][r] - c);
+        const float gt = ag * (acc[mb + 2][nb][r] - c);
+        const uint16_t hb = f32_to_bf16(swiglu_act(up, gt));
+        const float hv = bf16_to_f32(hb);
+        const int ii = static_cast<int>(i - otile);
+        hst[col * kHRow + ((ii >> 4) * 8 + j) * 2 + hh] =
+            static_cast<uint16_t>(bf16_bits_exact(hv * f));  // exact: power-of-two scale
+        if (i < n_half && col < np) {
+          if (h) h[static_cast<int64_t>(pid[col]) * ldh + i] = hb;
+          hcl[nb] += (f + 1.0f) * hv;
+        }
+      }
+    }
+  }
+  // the tile's correction part per pair: lane groups, then row waves, in order
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    float v = hcl[nb];
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (g == 0) hcp[wr][wm * 64 + nb * 16 + r16] = v;
+  }
+  __syncthreads();
+  if (tid < np) {
+    const float v = ((hcp[0][tid] + hcp[1][tid]) + hcp[2][tid]) + hcp[3][tid];
+    hcorr[static_cast<int64_t>(pos0 + tid) * n_rtiles + rtile] = v;
+  }
+  // the tile's h (n_half % 128 == 0: whole words), 16 B per copy
+#pragma unroll
+  for (int k = 0; k < kTok * 16 / kThreads; ++k) {
+    const int c = tid + kThreads * k, col = c / 16, part = c % 16;
+    if (col < np)
+      *reinterpret_cast<uint4*>(hp + static_cast<int64_t>(pos0 + col) * n_half + otile + part * 8) =
+          *reinterpret_cast<const uint4*>(hst + col * kHRow + part * 8);
+  }
+}
+
+// Down stage: out[pos, n] = bf16(alpha[e, n] * sum_k (c - 1) h) for a tile of
+// 128 pairs and 256 output rows; the correction is the sum of the SwiGLU
+// stage's n_ctiles parts, added in tile order.
+template <int ADT>
+__global__ __launch_bounds__(gp::kThreads) void k_gp_down(
+    const uint32_t* __restrict__ hp, const float* __restrict__ hcorr, int n_ctiles,
+    const uint32_t* __restrict__ w, int64_t n_out, int64_t nwk, const void* __restrict__ alpha,
+    const int32_t* __restrict__ offsets, int n_exp, uint16_t* __restrict__ out) {
+  using namespace gp;
+  __shared__ __align__(16) uint32_t xs[kLdsDwords];
+  __shared__ float cst[kTok];
+  __shared__ int32_t prow[kTok];
+  const int n_rtiles = static_cast<int>((n_out + kRows - 1) / kRows);
+  int mtile, rtile;
+  gp_tile(n_rtiles, mtile, rtile);
+  int e, pos0, np;
+  if (!decode_tile(offsets, n_exp, mtile, kTok, e, pos0, np)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wr = wv & 3, wm = wv >> 2, r16 = lane & 15, g = lane >> 4;
+  if (tid < kTok) {
+    float c = 0.f;
+    if (tid < np)
+      for (int ct = 0; ct < n_ctiles; ++ct) c += hcorr[static_cast<int64_t>(pos0 + tid) * n_ctiles + ct];
+    cst[tid] = c;
+    prow[tid] = pos0 + (tid < np ? tid : np - 1);
+  }
+  const int64_t n0 = static_cast<int64_t>(rtile) * kRows + wr * 64;
+  const uint32_t* we = w + static_cast<int64_t>(e) * n_out * nwk;
+  const uint32_t* rowp[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    int64_t n = n0 + 16 * mb + r16;
+    n = n < n_out ? n : n_out - 1;
+    rowp[mb] = we + n * nwk + 2 * g;
+  }
+  __syncthreads();  // prow
+  const GpSrc xsrc = gp_x_sources(hp, nwk * 8, prow);
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const ExpandConsts kc;
+  // Weights are loaded two steps ahead (the compiler places those loads at
+  // the end of a step, next to their loop-carried use), x' one step ahead.
+  uint2 wq[4], wn[4];
+  GpX xq;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    wq[mb] = *reinterpret_cast<const uint2*>(rowp[mb]);
+    wn[mb] = *reinterpret_cast<const uint2*>(rowp[mb] + (kWords < nwk ? kWords : 0));
+  }
+  gp_load_x(xsrc, 0, xq);
+  gp_store_x(xs, xq);
+  __syncthreads();
+  int buf = 0;
+  for (int64_t k0 = 0; k0 < nwk; k0 += kWords) {
+    const int64_t kn = k0 + kWords < nwk ? k0 + kWords : k0;
+    const int64_t knn = k0 + 2 * kWords < nwk ? k0 + 2 * kWords : k0;
+    gp_load_x(xsrc, kn, xq);
+    MA_ISSUE_FENCE();  // the next step's x' loads stay ahead of this step's MFMAs
+    gp_step(wq, xs + buf * kXsDwords, g, r16, wm * 64, acc, kc);
+    uint2 wnn[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) wnn[mb] = *reinterpret_cast<const uint2*>(rowp[mb] + knn);
+    gp_store_x(xs + (buf ^ 1) * kXsDwords, xq);
+    __syncthreads();
+    buf ^= 1;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      wq[mb] = wn[mb];
+      wn[mb] = wnn[mb];
+    }
+  }
+  // The tile goes to LDS as [pair][256 rows] (the loop's last barrier has
+  // freed the LDS), then out in 16-byte pieces, each pair's 512 bytes
+  // contiguous (n_out % 256 == 0).
+  uint16_t* ost = reinterpret_cast<uint16_t*>(xs);
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const int64_t n = n0 + 16 * mb + 4 * g;
+    float a[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) a[r] = ld_t<ADT>(alpha, static_cast<int64_t>(e) * n_out + (n + r < n_out ? n + r : n_out - 1));
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int col = wm * 64 + nb * 16 + r16;
+      const float c = cst[col];
+      uint2 v;
+      v.x = pack_bf16x2_rn(a[0] * (acc[mb][nb][0] - c), a[1] * (acc[mb][nb][1] - c));
+      v.y = pack_bf16x2_rn(a[2] * (acc[mb][nb][2] - c), a[3] * (acc[mb][nb][3] - c));
+      *reinterpret_cast<uint2*>(ost + col * kORow + wr * 64 + 16 * mb + 4 * g) = v;
+    }
+  }
+  __syncthreads();
+  const int64_t ntile0 = static_cast<int64_t>(rtile) * kRows;
+#pragma unroll
+  for (int k = 0; k < kTok * 32 / kThreads; ++k) {
+    const int c = tid + kThreads * k, col = c / 32, part = c % 32;
+    if (col < np)
+      *reinterpret_cast<uint4*>(out + static_cast<int64_t>(pos0 + col) * n_out + ntile0 + part * 8) =
+          *reinterpret_cast<const uint4*>(ost + col * kORow + part * 8);
+  }
+}
+
 }  // namespace ma
 
 using namespace ma;
@@ -965,14 +1075,26 @@ using namespace ma;
 // kernels run; above it (prefill) the LDS-staged tiles of up to 64 pairs.
 constexpr int64_t kKsMaxPairsPerExpert = 16;
 
-static int grouped_nb(int64_t n_pairs, int64_t n_exp) {
-  const int64_t per = n_pairs / (n_exp > 0 ? n_exp : 1);
-  return per >= 48 ? 4 : (per >= 24 ? 2 : 1);
+static size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+// Workspace of one call: pair-format h [P, inter] bf16, per-pair down outputs
+// [P, hidden] bf16; in the prefill form also the x' pairs of the tokens
+// [T, hidden / 2] uint32, their corrections [T] float32 and the SwiGLU tiles'
+// correction parts [P, inter / 128] float32.
+static bool grouped_prefill_form(int64_t n_pairs, int64_t n_experts) {
+  return n_pairs > kKsMaxPairsPerExpert * n_experts;
+}
+static size_t grouped_bytes(int64_t n_pairs, int64_t tokens, int64_t inter, int64_t hidden, bool prefill) {
+  size_t b = align256(static_cast<size_t>(n_pairs) * inter * 2) + align256(static_cast<size_t>(n_pairs) * hidden * 2);
+  if (prefill)
+    b += align256(static_cast<size_t>(tokens) * hidden * 2) + align256(static_cast<size_t>(tokens) * 4) +
+         align256(static_cast<size_t>(n_pairs) * cdiv(inter, gp::kRows / 2) * 4);
+  return b;
 }
 
 extern "C" size_t ma_grouped_workspace_bytes(int64_t n_pairs, int64_t inter, int64_t hidden) {
-  // pair-format h [P, inter] bf16 + per-pair down outputs [P, hidden] bf16
-  return static_cast<size_t>(n_pairs) * (inter + hidden) * 2 + 256;
+  // an upper bound over both forms (tokens <= pairs)
+  return grouped_bytes(n_pairs, n_pairs, inter, hidden, true);
 }
 
 // Argument checks shared by ma_moe_grouped and ma_moe_grouped_noalloc.
@@ -1002,12 +1124,13 @@ static int grouped_launch(const void* x, int64_t ldx, const uint32_t* x_pairs, c
                           void* h_out, int64_t ldh, void* y, void* workspace, void* stream) {
   const int64_t n_pairs = tokens * top_k;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  uint16_t* hp = static_cast<uint16_t*>(workspace);
-  uint16_t* out = hp + n_pairs * inter;
+  char* wsb = static_cast<char*>(workspace);
+  uint16_t* hp = reinterpret_cast<uint16_t*>(wsb);
+  uint16_t* out = reinterpret_cast<uint16_t*>(wsb + align256(static_cast<size_t>(n_pairs) * inter * 2));
   const int ne = static_cast<int>(n_experts);
   const auto* xb = static_cast<const uint16_t*>(x);
   auto* hb = static_cast<uint16_t*>(h_out);
-  if (n_pairs <= kKsMaxPairsPerExpert * n_experts) {
+  if (!grouped_prefill_form(n_pairs, n_experts)) {
     // decode: 16-pair tiles, K split over the waves of a workgroup
     const unsigned max_tiles = static_cast<unsigned>(n_pairs / 16 + n_experts);
     dim3 g1(static_cast<unsigned>(cdiv(inter, 32)), max_tiles);
@@ -1039,23 +1162,36 @@ static int grouped_launch(const void* x, int64_t ldx, const uint32_t* x_pairs, c
     if (alpha_dtype == MA_BF16) { MA_GROUPED_KS(MA_BF16) } else { MA_GROUPED_KS(MA_F32) }
 #undef MA_GROUPED_KS
   } else {
-  const int nb = grouped_nb(n_pairs, n_experts);
-  const int nt = 16 * nb;
-  const unsigned max_tiles = static_cast<unsigned>(n_pairs / nt + n_experts);
-  dim3 g1(static_cast<unsigned>(cdiv(inter, 128)), max_tiles);
-  dim3 g2(static_cast<unsigned>(cdiv(hidden, 256)), max_tiles);
-#define MA_GROUPED(NB, ADT)                                                                      \
-  hipLaunchKernelGGL((k_grouped_swiglu<NB, ADT>), g1, dim3(256), 0, s, xb, ldx, top_k, up_gate,  \
-                     inter, hidden / 16, up_gate_alpha, offsets, pair_ids, ne, hp, hb, ldh);     \
-  hipLaunchKernelGGL((k_grouped_down<NB, ADT>), g2, dim3(256), 0, s,                             \
-                     reinterpret_cast<const uint32_t*>(hp), down, hidden, inter / 16, down_alpha, \
-                     offsets, ne, out);
-  if (alpha_dtype == MA_BF16) {
-    if (nb == 4) { MA_GROUPED(4, MA_BF16) } else if (nb == 2) { MA_GROUPED(2, MA_BF16) } else { MA_GROUPED(1, MA_BF16) }
-  } else {
-    if (nb == 4) { MA_GROUPED(4, MA_F32) } else if (nb == 2) { MA_GROUPED(2, MA_F32) } else { MA_GROUPED(1, MA_F32) }
-  }
-#undef MA_GROUPED
+    // prefill: the tokens' x' pairs once (or those of ma_moe_route), then
+    // tiles of 128 pairs x 256 weight rows
+    char* p = reinterpret_cast<char*>(out) + align256(static_cast<size_t>(n_pairs) * hidden * 2);
+    const uint32_t* xpp = x_pairs;
+    const float* xcc = x_corr;
+    if (!x_pairs) {
+      uint32_t* xw = reinterpret_cast<uint32_t*>(p);
+      float* cw = reinterpret_cast<float*>(p + align256(static_cast<size_t>(tokens) * hidden * 2));
+      hipLaunchKernelGGL(k_gp_prep, dim3(static_cast<unsigned>(tokens)), dim3(128), 0, s, xb, ldx, hidden / 16, xw, cw);
+      xpp = xw;
+      xcc = cw;
+    }
+    float* hcorr = reinterpret_cast<float*>(p + align256(static_cast<size_t>(tokens) * hidden * 2) +
+                                            align256(static_cast<size_t>(tokens) * 4));
+    const int64_t mtiles = cdiv(n_pairs, gp::kTok) + n_experts;  // an upper bound
+    const int64_t mt8 = cdiv(mtiles, gp::kXcds) * gp::kXcds;
+    const int rt1 = static_cast<int>(cdiv(inter, gp::kRows / 2)), rt2 = static_cast<int>(cdiv(hidden, gp::kRows));
+    const dim3 g1(static_cast<unsigned>(mt8 * rt1)), g2(static_cast<unsigned>(mt8 * rt2));
+#define MA_GP(ADT)                                                                                 \
+  hipLaunchKernelGGL((k_gp_swiglu<ADT>), g1, dim3(gp::kThreads), 0, s, xpp, xcc, top_k, up_gate, \
+                     inter, hidden / 16, up_gate_alpha, offsets, pair_ids, ne, hp, hcorr, hb, ldh);  \
+  hipLaunchKernelGGL((k_gp_down<ADT>), g2, dim3(gp::kThreads), 0, s,                              \
+                     reinterpret_cast<const uint32_t*>(hp), hcorr, rt1, down, hidden, inter / 16, \
+                     down_alpha, offsets, ne, out);
+    if (alpha_dtype == MA_BF16) {
+      MA_GP(MA_BF16)
+    } else {
+      MA_GP(MA_F32)
+    }
+#undef MA_GP
   }
   if (y) {
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -1087,7 +1223,8 @@ extern "C" int ma_moe_grouped(const void* x, int64_t ldx, const uint32_t* x_pair
     return rc;
   const int64_t n_pairs = tokens * top_k;
   if (n_pairs == 0) return MA_OK;
-  if (!workspace || workspace_bytes < ma_grouped_workspace_bytes(n_pairs, inter, hidden))
+  if (!workspace || workspace_bytes < grouped_bytes(n_pairs, tokens, inter, hidden,
+                                                    grouped_prefill_form(n_pairs, n_experts)))
     return fail(MA_EVALUE, "moe_grouped: workspace too small");
   return grouped_launch(x, ldx, x_pairs, x_corr, tokens, top_k, up_gate, up_gate_alpha, down,
                         down_alpha, alpha_dtype, n_experts, hidden, inter, offsets, pair_ids,
@@ -1144,7 +1281,7 @@ extern "C" int ma_moe_grouped_noalloc(const void* x, int64_t ldx, const uint32_t
     return fail(MA_EVALUE, "%s: y is required (the per-pair outputs stay in the internal scratch)", what);
   const int64_t n_pairs = tokens * top_k;
   if (n_pairs == 0) return MA_OK;
-  const size_t need = ma_grouped_workspace_bytes(n_pairs, inter, hidden);
+  const size_t need = grouped_bytes(n_pairs, tokens, inter, hidden, grouped_prefill_form(n_pairs, n_experts));
   if (need > kGroupedScratchBytes)
     return fail(MA_EVALUE,
                 "%s: %lld (token, expert) pairs need %zu bytes of staging; the built-in scratch holds %zu "

@@ -262,7 +262,7 @@ def moe_grouped(x: torch.Tensor, layer: MoELayer, ids: torch.Tensor, wts: torch.
     )
     if not combine:
         # the per-pair down outputs sit after the pair-format h in the workspace
-        off = n_pairs * inter * 2
+        off = (n_pairs * inter * 2 + 255) // 256 * 256
         slot_out = ws[off:off + n_pairs * hidden * 2].view(torch.bfloat16).view(n_pairs, hidden)
         y = PendingCombine(slot_out, d.inverse, w, res, top_k, tokens, hidden, ws)
     if return_h:

@@ -3,7 +3,7 @@
 Both are called through the C ABI on the same inputs; the no-allocation form
 stages in the library's own device array and runs the same kernels, so y and
 h must be equal bit for bit.  Two calls in a row, the second smaller (the
-array keeps the first call's contents): 256 tokens (2048 pairs, the
+array keeps the first call's contents): 200 tokens (1600 pairs, the
 prefill-sized tiles) then 16 tokens (128 pairs, the decode-sized tiles);
 then a call larger than the array is refused.
 """
@@ -37,7 +37,7 @@ def _noalloc(x, L, ids, wts, d, residual, h_out, y):
 def test_noalloc_equals_workspace_entry_point(dev):
     L = synthetic.make_moe_layer(H, E, I, seed=21, device=dev)
     assert int(_lib.load().ma_moe_grouped_noalloc_max_bytes()) == 16 << 20
-    for step, tokens in enumerate((256, 16)):
+    for step, tokens in enumerate((200, 16)):
         x = synthetic.randn_bf16((tokens, H), 900 + tokens, dev)
         res = synthetic.randn_bf16((tokens, H), 950 + tokens, dev)
         ids, wts = router_topk(x, L.gate_weight, K)
