@@ -6,29 +6,30 @@ one-launch MoE kernel (router top-k, up+gate SwiGLU, down projections and the
 weighted combine in one persistent launch; the three-launch per-slot chain is
 timed beside it).  ``--layers`` distinct layers (default 96: 7.3 GB of packed
 weights, of which the 8 selected experts per layer are 0.91 GB, 3.6 times the
-256 MB Infinity Cache) are captured in one HIP graph and replayed in a cycle,
-so every layer's weights come from HBM.
+256 MB Infinity Cache) are chained -- each layer's output is the next
+layer's input, as in a decoder -- and captured in one HIP graph replayed in a
+cycle, so every layer's weights come from HBM.
 
-A step is one graph replay: ``--layers`` MoE-layer decodes, each on its own
-cold layer.  ``value`` is the whole-layer algorithmic HBM throughput:
+A step is one graph replay: ``--layers`` dependent MoE-layer decodes, each on
+its own cold layer.  ``value`` is the whole-layer algorithmic HBM throughput:
 (selected experts' packed codes + scales, the router weight, x in and y out)
-per layer, times layers and steps, over the timed wall time.
+per layer, times layers and steps, over the timed time.
 
 ``roofline`` covers the dominant kernel, which is the whole layer here
 (``k_moe_fused``): algorithmic bytes per launch over its average launch
 period, timed with HIP events on the stream it runs on over the graph of
-back-to-back launches on the cold layers (the period includes the dispatch
-gap between dependent kernels, so it is an upper bound on the kernel's own
-duration).  ``traffic`` is read from the rocprofv3 counter summary under
-profiles/ when present.
+back-to-back launches (the period includes the dispatch gap between dependent
+kernels, so it is an upper bound on the kernel's own duration).  ``traffic``
+is read from the rocprofv3 counter summary under profiles/ when present.
 
-``cpu_baseline`` times the CPU oracle path (NumPy unpack -> dequantise ->
-float32 matmul over the 8 selected experts, the reference's own test
-oracle) on a bounded sample of the same workload on this host's cores.
+``cpu_baseline`` times the reference's CPU path (NumPy unpack -> dequantise
+-> float32 ``torch.nn.functional.linear``, oracle/cpu_baseline.py) for the same
+layer on this host's cores; ``extra.cpu_configs`` times the other
+configurations the same way (bounded samples, each stated).
 
     python bench.py [--steps 20] [--warmup 3] [--layers 96] [--no-cpu]
                     [--no-decoder] [--no-extra]
-    python bench.py --counters-pass   # MoE layer graph + a 256 MiB copy, for rocprofv3 --pmc
+    python bench.py --counters-pass moe_bs1|prefill|decode32   # for rocprofv3 --pmc
     python bench.py --decode-batch 32 # only the full decoder at one batch size
 """
 
@@ -37,6 +38,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
 import re
 import sys
 import time
@@ -47,7 +49,9 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "decode tok/s (bs1, bs32); packed-ternary MoE layer HBM GB/s vs 8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0
 HIDDEN, EXPERTS, INTER, TOPK = 2048, 64, 768, 8
+ZIPF_FIXTURE = ROOT / "tests" / "golden" / "zipf_bias_e64.json"
 
 
 def log(msg: str) -> None:
@@ -61,6 +65,24 @@ def layer_bytes() -> dict:
     router = EXPERTS * HIDDEN * 2
     act = HIDDEN * 2 * 2
     return {"expert": expert, "selected": TOPK * expert, "layer": TOPK * expert + router + act}
+
+
+def zipf_fixture() -> dict:
+    """Router bias for Zipf(1.1)-skewed top-8 routing over 64 experts and the
+    expert load it is fitted to (tests/golden/make_zipf_bias.py)."""
+    return json.loads(ZIPF_FIXTURE.read_text())
+
+
+def load_report(ids, fixture: dict) -> dict:
+    """Achieved expert load of a routing against the fixture's target."""
+    import numpy as np
+
+    c = np.bincount(np.asarray(ids).reshape(-1), minlength=EXPERTS).astype(np.float64)
+    share = c / c.sum()
+    target = np.asarray(fixture["target_share"])
+    top = np.sort(share)[::-1]
+    return {"tv_distance_to_target": round(0.5 * float(np.abs(share - target).sum()), 4),
+            "top_shares": [round(float(v), 4) for v in top[:4]], "experts_hit": int((c > 0).sum())}
 
 
 def graph_of(fn):
@@ -112,6 +134,10 @@ def extra_workloads(layers, dev, steps: int) -> dict:
     from maple_amd.moe import moe_block
 
     out = {}
+    # The dispatch floor of one dependent launch in a graph (a 1-element fill).
+    one = torch.zeros(1, device=dev)
+    g = graph_of(lambda: [one.add_(1.0) for _ in range(256)])
+    out["launch_floor_us"] = round(time_graph(g, 5, 2) / 256 * 1e6, 3)
     # Single packed ternary GEMV, 1536 x 2048, batch 1, 1024 distinct cold copies.
     n, k, reps = 1536, 2048, 1024
     base = synthetic.ternary_packed((8, n, k), 77, dev)
@@ -121,35 +147,41 @@ def extra_workloads(layers, dev, steps: int) -> dict:
     g = graph_of(lambda: [ternary_gemv(xg, ws[i], alpha) for i in range(reps)])
     t = time_graph(g, 3, 1) / reps
     nbytes = n * k // 4 + n * 2 + k * 2 + n * 2
-    out["gemv_1536x2048_bs1"] = {"us_per_call": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1)}
+    out["gemv_1536x2048_bs1"] = {"us_per_call": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1),
+                                 "bytes_per_call": nbytes}
     del ws, base, g
     # Zipf(1.1)-routed MoE layers at 32 and 128 tokens.
-    bias = synthetic.zipf_router_bias(EXPERTS, 1.1, 1.0, seed=3).to(dev)
+    fx = zipf_fixture()
+    bias = torch.tensor(fx["bias"], dtype=torch.float32, device=dev)
     zl = [synthetic.MoELayer(l.gate_weight, l.up_gate_packed, l.up_gate_alpha, l.down_packed,
                              l.down_alpha, bias) for l in layers]
     for tokens in (32, 128):
         x = synthetic.randn_bf16((tokens, HIDDEN), 1000 + tokens, dev)
-        touched = 0
+        touched, all_ids = 0, []
         for l in zl:
             ids, _ = router_topk(x, l.gate_weight, TOPK, bias=l.router_bias)
             touched += int(torch.unique(ids).numel())
+            all_ids.append(ids.cpu())
         nbytes = touched * layer_bytes()["expert"] + len(zl) * (EXPERTS * HIDDEN * 2 + tokens * HIDDEN * 4)
         g = graph_of(lambda: [moe_block(x, l, TOPK) for l in zl])
         t = time_graph(g, max(steps // 2, 3), 2)
         out[f"moe_layer_zipf_T{tokens}"] = {
             "us_per_layer": round(t * 1e6 / len(zl), 2), "GB/s": round(nbytes / t / 1e9, 1),
             "experts_touched_per_layer": round(touched / len(zl), 1),
-            "tokens_per_s": round(tokens * len(zl) / t, 0)}
+            "tokens_per_s": round(tokens * len(zl) / t, 0),
+            "expert_load": load_report(torch.cat(all_ids).numpy(), fx)}
         del g
     # Prefill chunk: 2048 tokens through one MoE layer (grouped MFMA path).
     tokens = 2048
     x = synthetic.randn_bf16((tokens, HIDDEN), 2048, dev)
     pl = zl[:4]
+    ids, _ = router_topk(x, pl[0].gate_weight, TOPK, bias=bias)
     g = graph_of(lambda: [moe_block(x, l, TOPK) for l in pl])
     t = time_graph(g, 5, 2) / len(pl)
     flops = tokens * TOPK * (3 * 2 * INTER * HIDDEN)
     out["moe_prefill_T2048"] = {"us_per_layer": round(t * 1e6, 1), "TFLOP/s": round(flops / t / 1e12, 1),
-                                "mfma_frac_of_2500": round(flops / t / 2.5e15, 4)}
+                                "mfma_frac_of_2500": round(flops / t / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                                "expert_load": load_report(ids.cpu().numpy(), fx)}
     return out
 
 
@@ -160,6 +192,7 @@ def decoder_tokens_per_s(dev, batch: int, steps: int, warmup: int) -> dict:
     (the whole step captured).  Each replay appends one position per row."""
     import torch
 
+    from maple_amd import workspace
     from maple_amd.model import DecoderConfig, SyntheticDecoder
 
     cfg = DecoderConfig()
@@ -177,6 +210,7 @@ def decoder_tokens_per_s(dev, batch: int, steps: int, warmup: int) -> dict:
         g.replay()
     e1.record()
     torch.cuda.synchronize()
+    workspace.check_timeouts(dev)
     t = e0.elapsed_time(e1) * 1e-3 / steps
     nbytes = model.decode_bytes(batch, 4096 + warmup + steps // 2)
     out = {"tokens_per_s": round(batch / t, 1), "ms_per_step": round(t * 1e3, 4),
@@ -187,81 +221,241 @@ def decoder_tokens_per_s(dev, batch: int, steps: int, warmup: int) -> dict:
     return out
 
 
-def cpu_baseline(seconds: float = 12.0) -> dict:
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def _median_time(fn, warmup: int, runs: int, budget_s: float) -> tuple[float, int]:
     import numpy as np
 
-    from oracle import kernels as ok
+    for _ in range(warmup):
+        fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < runs or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def _np_layer(seed: int):
+    import numpy as np
+
     from oracle import pack
 
+    rng = np.random.default_rng(seed)
+    return dict(
+        gate=(rng.standard_normal((EXPERTS, HIDDEN)) * 0.02).astype(np.float32),
+        ug=pack.pack_2bit(rng.integers(0, 3, (EXPERTS, 2 * INTER, HIDDEN), dtype=np.uint32)),
+        ua=rng.uniform(0.01, 0.05, (EXPERTS, 2 * INTER)).astype(np.float32),
+        dn=pack.pack_2bit(rng.integers(0, 3, (EXPERTS, HIDDEN, INTER), dtype=np.uint32)),
+        da=rng.uniform(0.01, 0.05, (EXPERTS, HIDDEN)).astype(np.float32))
+
+
+def cpu_baseline() -> dict:
+    """Config 2 (one MoE layer, bs1) on the reference's CPU path: 3 warm-ups,
+    median of >= 20 runs, the unpack in every call."""
+    import numpy as np
+    import torch
+
+    from oracle import cpu_baseline as cb
+
     cores = len(os.sched_getaffinity(0))
-    rng = np.random.default_rng(0)
-    ug = pack.pack_2bit(rng.integers(0, 3, (EXPERTS, 2 * INTER, HIDDEN), dtype=np.uint32))
-    ua = rng.uniform(0.01, 0.05, (EXPERTS, 2 * INTER)).astype(np.float32)
-    dn = pack.pack_2bit(rng.integers(0, 3, (EXPERTS, HIDDEN, INTER), dtype=np.uint32))
-    da = rng.uniform(0.01, 0.05, (EXPERTS, HIDDEN)).astype(np.float32)
-    gw = (rng.standard_normal((EXPERTS, HIDDEN)) * 0.02).astype(np.float32)
-    xs = rng.standard_normal((64, 1, HIDDEN)).astype(np.float32)
-    for i in range(3):
-        ok.moe_layer_cpu_fp32(xs[i], gw, ug, ua, dn, da, TOPK)
-    times = []
-    t_end = time.perf_counter() + seconds
-    i = 0
-    while len(times) < 20 or (time.perf_counter() < t_end and len(times) < 200):
-        t0 = time.perf_counter()
-        ok.moe_layer_cpu_fp32(xs[i % 64], gw, ug, ua, dn, da, TOPK)
-        times.append(time.perf_counter() - t0)
-        i += 1
-    med = float(np.median(times))
+    torch.set_num_threads(cores)
+    L = _np_layer(0)
+    xs = np.random.default_rng(1).standard_normal((64, 1, HIDDEN)).astype(np.float32)
+    i = [0]
+
+    def run():
+        cb.moe_layer(xs[i[0] % 64], L["gate"], L["ug"], L["ua"], L["dn"], L["da"], TOPK)
+        i[0] += 1
+
+    med, n = _median_time(run, 3, 20, 10.0)
     return {
         "value": round(layer_bytes()["layer"] / med / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"{len(times)} MoE-layer decodes (bs1, H2048 E64 I768 top-8), median "
-                  f"{med * 1e3:.1f} ms; NumPy unpack + float32 matmul per selected expert, "
-                  f"BLAS threads = {cores}, os.cpu_count() = {os.cpu_count()}",
+        "sample": f"{n} MoE-layer decodes (bs1, H2048 E64 I768 top-8), median {med * 1e3:.1f} ms; "
+                  f"NumPy unpack + float32 torch F.linear per selected expert (the reference's CPU "
+                  f"oracle path), torch threads = {cores}, os.cpu_count() = {os.cpu_count()}, "
+                  f"CPU {_cpu_model()}",
     }
 
 
-def counters_pass(dev, n_layers: int) -> int:
-    """Workload for rocprofv3 --pmc passes (FETCH_SIZE / WRITE_SIZE per
-    dispatch): the one-launch MoE layer kernel over ``n_layers`` cold layers,
-    twice, then a plain 256 MiB device copy four times to calibrate the
-    counter against a known byte count.  Traffic does not depend on the weight
-    values, so the expert weights are left uninitialised; the router rows are
-    set (by fill kernels, no random numbers under the profiler) so that layer
-    l selects 8 distinct experts, 8l + 56 .. 8l + 63 mod 64."""
+def cpu_configs(decoder_seconds: bool = True) -> dict:
+    """The other configurations on the same CPU path (bounded samples)."""
+    import numpy as np
+    import torch
+
+    from oracle import cpu_baseline as cb
+    from oracle import pack
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    out = {"cores": cores, "cpu": _cpu_model()}
+    rng = np.random.default_rng(2)
+    # config 1: one GEMV 1536 x 2048
+    packed = pack.pack_2bit(rng.integers(0, 3, (1536, 2048), dtype=np.uint32))
+    alpha = rng.uniform(0.01, 0.05, 1536).astype(np.float32)
+    x = rng.standard_normal((1, 2048)).astype(np.float32)
+    med, n = _median_time(lambda: cb.ternary_gemv(x, packed, alpha), 3, 20, 3.0)
+    nbytes = 1536 * 2048 // 4 + 1536 * 2 + 2048 * 2 + 1536 * 2
+    out["gemv_1536x2048_bs1"] = {"us_per_call": round(med * 1e6, 1), "GB/s": round(nbytes / med / 1e9, 3),
+                                 "sample": f"median of {n}"}
+    # configs 3 and 5: Zipf-routed layers
+    L = _np_layer(3)
+    bias = np.asarray(zipf_fixture()["bias"], np.float32)
+    for tokens, warm, runs, budget in ((32, 3, 20, 8.0), (128, 3, 20, 10.0), (2048, 1, 3, 0.0)):
+        xt = rng.standard_normal((tokens, HIDDEN)).astype(np.float32)
+        med, n = _median_time(lambda: cb.moe_layer(xt, L["gate"], L["ug"], L["ua"], L["dn"], L["da"], TOPK,
+                                                   bias=bias), warm, runs, budget)
+        key = f"moe_layer_zipf_T{tokens}" if tokens < 2048 else "moe_prefill_T2048"
+        out[key] = {"ms_per_layer": round(med * 1e3, 2), "tokens_per_s": round(tokens / med, 1),
+                    "sample": f"median of {n} ({warm} warm-up)"}
+        if tokens == 2048:
+            out[key]["TFLOP/s"] = round(tokens * TOPK * 3 * 2 * INTER * HIDDEN / med / 1e12, 4)
+    if decoder_seconds:
+        out["decoder_bs1_token"] = cpu_decoder_token()
+    return out
+
+
+def cpu_decoder_token() -> dict:
+    """One bs1 token of the full synthetic decoder (24 layers, 4096-token cache)
+    on the CPU path: a single timed token after one warm-up layer pass."""
+    import numpy as np
+    import torch
+
+    from oracle import cpu_baseline as cb
+    from oracle import decoder as od
+    from oracle import pack
+
+    rng = np.random.default_rng(4)
+    H, nq, nkv, d, vocab, grp = HIDDEN, 32, 4, 64, 151936, 128
+    qkv_rows = (nq + 2 * nkv) * d
+    ones = np.ones
+    shared = _np_layer(5)  # the MoE weights are shared by the layers here (same work per layer)
+    layers = []
+    for i in range(24):
+        layers.append(dict(
+            qkv=pack.pack_2bit(rng.integers(0, 3, (qkv_rows, H), dtype=np.uint32)),
+            qkv_alpha=rng.uniform(0.01, 0.05, qkv_rows).astype(np.float32),
+            o=pack.pack_2bit(rng.integers(0, 3, (H, nq * d), dtype=np.uint32)),
+            o_alpha=rng.uniform(0.01, 0.05, H).astype(np.float32),
+            input_ln=ones(H, np.float32), post_ln=ones(H, np.float32), q_norm=ones(d, np.float32),
+            k_norm=ones(d, np.float32),
+            moe=dict(gate_weight=shared["gate"], up_gate_packed=shared["ug"], up_gate_alpha=shared["ua"],
+                     down_packed=shared["dn"], down_alpha=shared["da"])))
+    words = rng.integers(0, 2 ** 32, (vocab, H // 8), dtype=np.uint64).astype(np.uint32)
+    sc = rng.uniform(0.003, 0.006, (vocab, H // grp)).astype(np.float32)
+    table = (words, sc, (-7.5 * sc).astype(np.float32))
+    cos, sin = od.rope_tables(4096 + 8, 32, 1e4)
+    m = dict(cfg=dict(hidden=H, heads=nq, kv_heads=nkv, head_dim=d, rotary_dim=32, eps=1e-6, rtn_group=grp,
+                      top_k=TOPK), layers=layers, embed=table, lm_head=table, final_norm=ones(H, np.float32),
+             cos=cos, sin=sin)
+    kv = lambda: rng.standard_normal((1, nkv, 4096 + 8, d), dtype=np.float32)  # noqa: E731
+    cache = dict(k=[kv() for _ in range(24)], v=[kv() for _ in range(24)], seqlen=np.array([4096]))
+    t0 = time.perf_counter()
+    cb.decoder_token(m, cache, 12345)
+    t = time.perf_counter() - t0
+    return {"s_per_token": round(t, 3), "tokens_per_s": round(1.0 / t, 3),
+            "sample": "1 token (24 layers over a 4096-position cache + the 151936-row RTN4 head), "
+                      f"torch threads = {torch.get_num_threads()}"}
+
+
+def counters_pass(dev, kind: str, n_layers: int) -> int:
+    """Workloads for rocprofv3 --pmc passes (no device random numbers: torch's
+    RNG kernels have faulted under the counter collector here).  Each runs its
+    kernels, then a plain 256 MiB device copy four times to calibrate the
+    counters against a known byte count.
+
+    moe_bs1:  the one-launch MoE layer kernel over ``n_layers`` cold layers,
+              twice; router rows set by fill kernels so that layer l selects 8
+              distinct experts (8l + 56 .. 8l + 63 mod 64); expert weights left
+              uninitialised (traffic does not depend on their values).
+    prefill:  the 2048-token grouped MoE layer on 4 layers generated on the
+              host (CPU random numbers) and copied over, with the Zipf bias.
+    decode32: the batch-32 RTN4 lm_head GEMM (151936 x 2048, group 128) and the
+              batch-32 fused decode attention over a 4096-position cache, on
+              zero-filled tensors."""
     import torch
 
     from maple_amd import synthetic
     from maple_amd.moe import moe_block
 
-    kw = HIDDEN // 16
-    layers = []
-    e = torch.arange(EXPERTS, device=dev, dtype=torch.float32)
-    for l in range(n_layers):
-        rank = torch.remainder(e - 8 * l, EXPERTS)  # logit of expert e with x = ones: rank / 64
-        gate = (rank / (EXPERTS * HIDDEN))[:, None].expand(EXPERTS, HIDDEN).to(torch.bfloat16).contiguous()
-        ug = torch.empty(EXPERTS, 2 * INTER, kw, device=dev, dtype=torch.int32).view(torch.uint32)
-        ua = torch.empty(EXPERTS, 2 * INTER, device=dev, dtype=torch.bfloat16)
-        dn = torch.empty(EXPERTS, HIDDEN, INTER // 16, device=dev, dtype=torch.int32).view(torch.uint32)
-        da = torch.empty(EXPERTS, HIDDEN, device=dev, dtype=torch.bfloat16)
-        layers.append(synthetic.MoELayer(gate, ug, ua, dn, da, None))
-    x = torch.ones(1, HIDDEN, dtype=torch.bfloat16).to(dev)
-    torch.cuda.synchronize()
-    for _ in range(2):
+    if kind == "moe_bs1":
+        kw = HIDDEN // 16
+        layers = []
+        e = torch.arange(EXPERTS, device=dev, dtype=torch.float32)
         for l in range(n_layers):
-            moe_block(x, layers[l], TOPK, plan="fused")
+            rank = torch.remainder(e - 8 * l, EXPERTS)  # logit of expert e with x = ones: rank / 64
+            gate = (rank / (EXPERTS * HIDDEN))[:, None].expand(EXPERTS, HIDDEN).to(torch.bfloat16).contiguous()
+            ug = torch.empty(EXPERTS, 2 * INTER, kw, device=dev, dtype=torch.int32).view(torch.uint32)
+            ua = torch.empty(EXPERTS, 2 * INTER, device=dev, dtype=torch.bfloat16)
+            dn = torch.empty(EXPERTS, HIDDEN, INTER // 16, device=dev, dtype=torch.int32).view(torch.uint32)
+            da = torch.empty(EXPERTS, HIDDEN, device=dev, dtype=torch.bfloat16)
+            layers.append(synthetic.MoELayer(gate, ug, ua, dn, da, None))
+        x = torch.ones(1, HIDDEN, dtype=torch.bfloat16).to(dev)
+        torch.cuda.synchronize()
+        for _ in range(2):
+            for l in range(n_layers):
+                moe_block(x, layers[l], TOPK, plan="fused")
+        info = {"moe_fused_launches": 2 * n_layers, "layer_bytes_per_launch": layer_bytes()["layer"]}
+    elif kind == "prefill":
+        fx = zipf_fixture()
+        layers = []
+        for i in range(4):
+            c = synthetic.make_moe_layer(HIDDEN, EXPERTS, INTER, seed=200 + i, device="cpu")
+            layers.append(synthetic.MoELayer(
+                c.gate_weight.to(dev), c.up_gate_packed.view(torch.int32).to(dev).view(torch.uint32),
+                c.up_gate_alpha.to(dev), c.down_packed.view(torch.int32).to(dev).view(torch.uint32),
+                c.down_alpha.to(dev), torch.tensor(fx["bias"], dtype=torch.float32, device=dev)))
+        x = synthetic.randn_bf16((2048, HIDDEN), 2048, "cpu").to(dev)
+        torch.cuda.synchronize()
+        for _ in range(2):
+            for l in layers:
+                moe_block(x, l, TOPK)
+        info = {"prefill_layers": 8, "tokens": 2048, "flops_per_layer": 2048 * TOPK * 3 * 2 * INTER * HIDDEN}
+    elif kind == "decode32":
+        from maple_amd.kernels.decode_attn import decode_attention, gqa_workspace
+        from maple_amd.kernels.rtn4 import rtn4_gemv
+
+        vocab, batch, max_len = 151936, 32, 4096 + 64
+        w = torch.zeros(vocab, HIDDEN // 8, device=dev, dtype=torch.int32).view(torch.uint32)
+        sc = torch.zeros(vocab, HIDDEN // 128, device=dev, dtype=torch.bfloat16)
+        xh = torch.zeros(batch, HIDDEN, device=dev, dtype=torch.bfloat16)
+        kc = torch.zeros(batch, 4, max_len, 64, device=dev, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        qkv = torch.zeros(batch, (32 + 8) * 64, device=dev, dtype=torch.bfloat16)
+        nw = torch.ones(64, device=dev)
+        cos = torch.ones(max_len, 32, device=dev)
+        sin = torch.zeros(max_len, 32, device=dev)
+        seqlen = torch.full((batch,), 4096, device=dev, dtype=torch.int64)
+        ws = gqa_workspace(batch, 4, max_len, dev)
+        torch.cuda.synchronize()
+        for _ in range(4):
+            rtn4_gemv(xh, w, sc, sc, group_size=128)
+            decode_attention(qkv, nw, nw, cos, sin, kc, vc, seqlen, ws, num_heads=32, num_kv_heads=4,
+                             head_dim=64, rotary_dim=32, scale=0.125)
+        info = {"rtn4_launches": 4, "rtn4_bytes_per_launch": vocab * HIDDEN // 2 + 2 * vocab * 16 * 2,
+                "attn_launches": 4, "attn_kv_bytes_per_launch": batch * 2 * 4 * 4097 * 64 * 2}
+    else:
+        raise ValueError(f"unknown counters pass {kind}")
     torch.cuda.synchronize()
     a = torch.empty(128 << 20, device=dev, dtype=torch.bfloat16)
     b = torch.empty_like(a)
     for _ in range(4):
         b.copy_(a)
     torch.cuda.synchronize()
-    print(json.dumps({"counters_pass": True, "moe_fused_launches": 2 * n_layers,
-                      "layer_bytes_per_launch": layer_bytes()["layer"],
-                      "copy_bytes_read": a.numel() * 2, "copy_bytes_written": a.numel() * 2}),
-          flush=True)
+    print(json.dumps({"counters_pass": kind, **info, "copy_bytes_read": a.numel() * 2,
+                      "copy_bytes_written": a.numel() * 2}), flush=True)
     return 0
 
 
@@ -271,8 +465,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=96)
-    ap.add_argument("--counters-pass", action="store_true",
-                    help="only run the MoE layer kernel and a plain 256 MiB copy (for counters)")
+    ap.add_argument("--counters-pass", choices=("moe_bs1", "prefill", "decode32"), default=None,
+                    help="only run one workload and a plain 256 MiB copy (for counters)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-decoder", action="store_true")
@@ -289,7 +483,7 @@ def main() -> int:
     import __graft_entry__
 
     __graft_entry__.load_package()
-    from maple_amd import synthetic
+    from maple_amd import synthetic, workspace
     from maple_amd.moe import moe_block
 
     dev = torch.device("cuda:0")
@@ -297,7 +491,7 @@ def main() -> int:
     nb = layer_bytes()
     L = args.layers
     if args.counters_pass:
-        return counters_pass(dev, L)
+        return counters_pass(dev, args.counters_pass, L)
     if args.decode_batch > 0:
         res = decoder_tokens_per_s(dev, args.decode_batch, max(args.steps, 10), args.warmup)
         print(json.dumps({"decode": {f"bs{args.decode_batch}": res}}), flush=True)
@@ -307,8 +501,13 @@ def main() -> int:
     x = synthetic.randn_bf16((1, HIDDEN), 12345, dev)
     torch.cuda.synchronize()
 
-    # Whole-layer timing: L layer decodes per graph replay (one launch each).
-    g = graph_of(lambda: [moe_block(x, layers[i], TOPK) for i in range(L)])
+    def chain(plan):
+        h = x
+        for layer in layers:
+            h, _, _ = moe_block(h, layer, TOPK, plan=plan)
+
+    # Whole-layer timing: L dependent layer decodes per graph replay (one launch each).
+    g = graph_of(lambda: chain("fused"))
     for _ in range(args.warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -327,18 +526,15 @@ def main() -> int:
     achieved = nb["layer"] / per_launch / 1e9
     log(f"MoE layer bs1: {ms * 1e3 / L:.2f} us/layer, {value:.1f} GB/s (wall {wall:.3f} s)")
     del g
-    from maple_amd.moe import moe_fused_timed_out
-
     # The three-launch chain (router, SwiGLU, down + combine) on the same layers.
-    gc = graph_of(lambda: [moe_block(x, layers[i], TOPK, plan="per_slot") for i in range(L)])
-    chain = time_graph(gc, args.steps, args.warmup) / L
+    gc = graph_of(lambda: chain("per_slot"))
+    per_slot = time_graph(gc, args.steps, args.warmup) / L
     del gc
-    log(f"per-slot chain: {chain * 1e6:.2f} us/layer")
-
-    from maple_amd.kernels.router import router_wait_timed_out
-
-    if router_wait_timed_out(dev) or moe_fused_timed_out(dev):
-        log("a kernel reported a timed-out cross-workgroup wait: results invalid")
+    log(f"per-slot chain: {per_slot * 1e6:.2f} us/layer")
+    try:
+        workspace.check_timeouts(dev)
+    except RuntimeError as exc:
+        log(f"{exc}: results invalid")
         return 1
     out = {
         "metric": METRIC,
@@ -355,8 +551,9 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "moe_ffn_layer_decode_bs1", "hidden": HIDDEN, "experts": EXPERTS,
                    "intermediate": INTER, "top_k": TOPK, "tokens": 1, "cold_layers": L,
-                   "bytes_per_layer": nb["layer"], "us_per_layer": round(ms * 1e3 / L, 3),
-                   "per_slot_chain_us_per_layer": round(chain * 1e6, 3)},
+                   "chained": True, "bytes_per_layer": nb["layer"],
+                   "us_per_layer": round(ms * 1e3 / L, 3),
+                   "per_slot_chain_us_per_layer": round(per_slot * 1e6, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic("moe_fused_bs1"), "kernel": "k_moe_fused",
@@ -379,6 +576,12 @@ def main() -> int:
     if not args.no_cpu:
         log("timing the CPU baseline ...")
         out["cpu_baseline"] = cpu_baseline()
+        log(json.dumps(out["cpu_baseline"]))
+        if not args.no_extra:
+            log("timing the other configurations on the CPU ...")
+            out["extra"] = out["extra"] or {}
+            out["extra"]["cpu_configs"] = cpu_configs()
+            log(json.dumps(out["extra"]["cpu_configs"]))
     print(json.dumps(out), flush=True)
     return 0
 
