@@ -435,6 +435,28 @@ int ma_decode_attn_o_supported(int64_t batch, int n_heads, int n_kv_heads, int h
 int ma_argmax_rows(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t ldx,
                    int64_t* out, void* stream);
 
+/* Workspace bytes ma_fused_sample needs for rows x vocab at top_k (0 for bad
+ * sizes).  Replaces sampler_workspace / batched_sampler_workspace,
+ * src/maple_run/kernels/sampler.py:202-232. */
+size_t ma_sampler_workspace_bytes(int64_t rows, int64_t vocab, int top_k);
+
+/*
+ * Fused top-k / temperature / nucleus draw, one token per row: the top_k
+ * largest logits of row r (bf16, fp16 or float32, row stride ld; descending,
+ * ties at the lower index), p = exp((v - v_max) * inv_temperature) normalised
+ * over them, tokens dropped once the mass before them exceeds top_p, then the
+ * first token whose inclusive prefix of the kept p exceeds
+ * uniform[r] * (kept mass); out int64 [rows].  Two launches; every row draws
+ * exactly what it draws alone.  1 <= top_k <= min(64, vocab),
+ * inv_temperature finite > 0, 0 < top_p <= 1, ceil(vocab / 4096) * top_k <=
+ * 4096.  Replaces fused_sample / fused_sample_batched
+ * (src/maple_run/kernels/sampler.py:106-199: _topk_partial_kernel :24-53,
+ * _sample_final_kernel :56-103).
+ */
+int ma_fused_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                    const float* uniform, int top_k, float inv_temperature, float top_p,
+                    void* workspace, size_t ws_bytes, int64_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
