@@ -189,25 +189,31 @@ def decoder_tokens_per_s(dev, batch: int, steps: int, warmup: int) -> dict:
     """Greedy decode of the full synthetic decoder (24 layers, hidden 2048,
     32/4 heads of 64, 64 experts top-8, RTN4 lm_head over 151936 tokens) at
     ``batch`` rows over a 4096-token KV cache, one HIP graph replay per step
-    (the whole step captured).  Each replay appends one position per row."""
+    (the whole step captured by the decode-graph runner, which first checks
+    8 replayed steps against 8 eager ones).  Each replay appends one position
+    per row and feeds the chosen ids to the next step."""
     import torch
 
     from maple_amd import workspace
+    from maple_amd.decode_graph import Sampling, try_decode_graph
     from maple_amd.model import DecoderConfig, SyntheticDecoder
 
     cfg = DecoderConfig()
-    model = SyntheticDecoder(cfg, dev, seed=0, max_len=4096 + steps + warmup + 8)
+    model = SyntheticDecoder(cfg, dev, seed=0, max_len=4096 + steps + warmup + 32)
     cache = model.make_cache(batch, prefill_len=4096, seed=0)
     gen = torch.Generator(device=dev).manual_seed(batch)
     ids = torch.randint(0, cfg.vocab, (batch,), device=dev, generator=gen)
-    g = graph_of(lambda: model.greedy_step(ids, cache))
+    g = try_decode_graph(model, cache, ids, log=log)
+    if g is None:
+        raise RuntimeError("the decode graph did not validate against eager decoding")
+    greedy = Sampling()
     for _ in range(warmup):
-        g.replay()
+        g.step(greedy)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(True), torch.cuda.Event(True)
     e0.record()
     for _ in range(steps):
-        g.replay()
+        g.step(greedy)
     e1.record()
     torch.cuda.synchronize()
     workspace.check_timeouts(dev)

@@ -102,15 +102,79 @@ def rope_tables(max_len: int, rotary_dim: int, theta: float, device):
 
 @dataclass
 class KVCache:
-    """Preallocated bf16 K/V per layer ``[B, n_kv, max_len, D]``, one write
-    position per row (``model.py:116-143``) and the attention workspace
-    (zeroed once; the kernels leave its barrier counters zero)."""
+    """Preallocated bf16 K/V per layer ``[rows, n_kv, max_len, D]``, one write
+    position per slot (``model.py:116-143``) and the attention workspace
+    (zeroed once; the kernels leave its barrier counters zero).
+
+    Slots and cache rows (``model.py:145-156, 196-214``): ``seqlen`` is
+    indexed by slot, K/V by cache row, and ``row_map[slot]`` names the row.
+    With ``remap`` off the map is the identity; a scheduler turns it on to
+    keep live sequences in the low slots by swapping indices (never K/V), so
+    a decode step can run at a narrow width.  A step of width ``w`` covers
+    slots ``[0, w)``."""
 
     k: list
     v: list
     seqlen: torch.Tensor
     max_len: int
     attn_ws: torch.Tensor = field(default=None)
+    row_map: torch.Tensor = field(default=None)
+    remap: bool = False
+
+    def __post_init__(self):
+        if self.row_map is None:
+            self.row_map = torch.arange(self.rows, device=self.seqlen.device, dtype=torch.int64)
+
+    @property
+    def rows(self) -> int:
+        return int(self.k[0].shape[0])
+
+    def slot_rows(self, width: int):
+        """``(seqlen, row_map)`` views for a step over slots ``[0, width)``;
+        ``row_map`` is None when the kernels may read row == slot."""
+        if not 0 < width <= self.rows:
+            raise ValueError(f"step width {width} outside the cache's {self.rows} slots.")
+        rm = self.row_map[:width] if (self.remap or width != self.rows) else None
+        return self.seqlen[:width], rm
+
+    def swap_slots(self, i: int, j: int) -> None:
+        """Exchange two slots: their row map entries and write positions."""
+        if i == j:
+            return
+        if not self.remap:
+            raise RuntimeError("swap_slots needs cache.remap: without the map the kernels read "
+                               "cache row == slot, and a swap would read another sequence's K/V.")
+        for t in (self.row_map, self.seqlen):
+            a = t[i].clone()
+            t[i] = t[j]
+            t[j] = a
+
+    def reset_slot(self, slot: int) -> None:
+        """Forget a slot's history so a new sequence can take it."""
+        self.seqlen[slot] = 0
+
+    def snapshot(self, steps: int | None = None) -> dict:
+        """Write positions, slot map and a copy of the K/V that the next
+        ``steps`` decode steps can overwrite (all of it when ``steps`` is
+        None); ``restore`` puts them back (``model.py:276-291``)."""
+        lo, hi = 0, self.max_len
+        if steps is not None:
+            sl = self.seqlen.cpu()
+            lo = int(sl.min()) if sl.numel() else 0
+            hi = min(self.max_len, int(sl.max()) + int(steps) + 1) if sl.numel() else 0
+        return {"seqlen": self.seqlen.clone(), "row_map": self.row_map.clone(), "remap": self.remap,
+                "span": (lo, hi), "k": [t[:, :, lo:hi].clone() for t in self.k],
+                "v": [t[:, :, lo:hi].clone() for t in self.v]}
+
+    def restore(self, snap: dict) -> None:
+        self.seqlen.copy_(snap["seqlen"])
+        self.row_map.copy_(snap["row_map"])
+        self.remap = snap["remap"]
+        lo, hi = snap["span"]
+        for dst, src in zip(self.k, snap["k"]):
+            dst[:, :, lo:hi].copy_(src)
+        for dst, src in zip(self.v, snap["v"]):
+            dst[:, :, lo:hi].copy_(src)
 
 
 class SyntheticDecoder:
@@ -189,16 +253,18 @@ class SyntheticDecoder:
         akw = dict(num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim,
                    rotary_dim=c.rotary_dim, eps=c.eps, scale=c.head_dim ** -0.5, window=window,
                    use_rope=use_rope)
+        seqlen, row_map = cache.slot_rows(bsz)
+        akw["row_map"] = row_map
         if bsz == 1 and self.fused_o and o_projection_supported(1, c.heads, c.kv_heads, c.head_dim,
                                                                 cache.max_len, window, c.hidden):
             # attention and its output projection in one launch (measured: no
             # faster than two launches at 4096 positions -- the grid barrier
             # and the tail cost what the second launch does -- so off by default)
             _, o = decode_attention(qkv, L.q_norm, L.k_norm, self.cos, self.sin, cache.k[i], cache.v[i],
-                                    cache.seqlen, cache.attn_ws, o_linear=(L.o, L.o_alpha), **akw)
+                                    seqlen, cache.attn_ws, o_linear=(L.o, L.o_alpha), **akw)
         else:
             attn = decode_attention(qkv, L.q_norm, L.k_norm, self.cos, self.sin, cache.k[i], cache.v[i],
-                                    cache.seqlen, cache.attn_ws, **akw)
+                                    seqlen, cache.attn_ws, **akw)
             o = ternary_gemv(attn.reshape(bsz, -1), L.o, L.o_alpha)
         next_qkv = None
         if bsz == 1 and self.fused_moe and fused_supported(L.moe, c.top_k, hidden):
@@ -229,13 +295,16 @@ class SyntheticDecoder:
         return self._layer(i, hidden, cache, routing, fuse_next=False)[0]
 
     def forward(self, input_ids: torch.Tensor, cache: KVCache, routing: list | None = None) -> torch.Tensor:
-        """One decode step for ``input_ids [B]``; returns bf16 logits ``[B, vocab]``.
-        ``routing``, if a list, receives each layer's expert ids."""
-        hidden = self.embed_tokens(input_ids)
+        """One decode step for ``input_ids [w]`` over cache slots ``[0, w)``;
+        returns bf16 logits ``[w, vocab]``.  ``routing``, if a list, receives
+        each layer's expert ids."""
+        width = int(input_ids.numel())
+        cache.slot_rows(width)
+        hidden = self.embed_tokens(input_ids.reshape(-1))
         qkv = None
         for i in range(self.cfg.layers):
             hidden, qkv = self._layer(i, hidden, cache, routing, qkv)
-        cache.seqlen.add_(1)
+        cache.seqlen[:width].add_(1)
         return self.head(hidden)
 
     def embed_tokens(self, input_ids: torch.Tensor) -> torch.Tensor:
