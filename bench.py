@@ -444,7 +444,7 @@ def counters_pass(dev, kind: str, n_layers: int) -> int:
         cos = torch.ones(max_len, 32, device=dev)
         sin = torch.zeros(max_len, 32, device=dev)
         seqlen = torch.full((batch,), 4096, device=dev, dtype=torch.int64)
-        ws = gqa_workspace(batch, 4, max_len, dev)
+        ws = gqa_workspace(batch, 4, max_len, dev, 64)
         torch.cuda.synchronize()
         for _ in range(4):
             rtn4_gemv(xh, w, sc, sc, group_size=128)

@@ -382,17 +382,17 @@ int ma_qk_norm_rope_store(const void* qkv, int64_t ldq, int64_t batch, int n_hea
  * [batch, n_heads, head_dim], float32 accumulation, P rounded to bf16, split
  * over the sequence (128 positions per split) and merged in the same launch
  * (the splits of a (row, KV head) meet at a barrier, then each merges a slice).
- * workspace: ma_gqa_workspace_bytes(batch, n_kv_heads, max_len) bytes,
+ * workspace: ma_gqa_workspace_bytes(batch, n_kv_heads, max_len, head_dim) bytes,
  * 16-byte aligned, zero-filled before the first call: it starts with a sync
  * area of 256-byte lines (line 0, int32 word 2: set to 1 if a barrier wait
  * ever exceeded about 0.2 s; then per (row, KV head) an arrival-counter line,
  * which each call leaves at zero, and a generation line; then 33 lines of a
  * grid barrier for the fused entry point's O projection).  Calls that share
- * a workspace must not overlap.  head_dim must be 64.
+ * a workspace must not overlap.  head_dim must be 64 or 128.
  * Replaces decode_gqa_attn, src/maple_run/kernels/decode_attn.py:470-592
  * (which merges the splits in a second kernel, :317-359).
  */
-size_t ma_gqa_workspace_bytes(int64_t batch, int n_kv_heads, int64_t max_len);
+size_t ma_gqa_workspace_bytes(int64_t batch, int n_kv_heads, int64_t max_len, int head_dim);
 int ma_decode_gqa_attn(const void* q, int64_t batch, int n_heads, int n_kv_heads, int head_dim,
                        const void* k_cache, const void* v_cache, int64_t cache_rows,
                        int64_t max_len, const int64_t* seqlen, const int64_t* row_map,

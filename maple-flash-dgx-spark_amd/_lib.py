@@ -46,7 +46,7 @@ _SIGNATURES = {
     "ma_grouped_workspace_bytes": [_L, _L, _L],
     "ma_qk_norm_rope_store": [_P, _L, _L, _I, _I, _I, _P, _P, _I, _P, _P, _I, _L, _L, _I, _I, _F,
                               _P, _P, _P, _P, _L, _L, _P, _P],
-    "ma_gqa_workspace_bytes": [_L, _I, _L],
+    "ma_gqa_workspace_bytes": [_L, _I, _L, _I],
     "ma_decode_gqa_attn": [_P, _L, _I, _I, _I, _P, _P, _L, _L, _P, _P, _L, _F, _P, _P, _Z, _P],
     "ma_decode_attn_fused": [_P, _L, _L, _I, _I, _I, _P, _P, _I, _P, _P, _I, _L, _L, _I, _I, _F,
                              _P, _P, _P, _P, _L, _L, _L, _F, _P, _P, _Z, _P, _P, _I, _L, _P, _P],

@@ -22,7 +22,8 @@
 
 namespace ma {
 
-constexpr int kHeadDim = 64;                // head_dim of the synthetic decoder
+// head_dim 64 (the synthetic decoder) and 128 (Maple-Preview) are built: each
+// lane of a wave owns dims lane + 64 e, e < HD / 64.
 constexpr int kSplit = 128;                 // positions per chunk
 constexpr int kAttnThreads = 256;           // 4 waves, 32 positions of a chunk each
 constexpr int kMaxGroup = 16;               // query heads per KV head
@@ -55,30 +56,52 @@ struct RopeSrc {
   int use_rope;
 };
 
-// cos/sin for lane d of the row used at position ``pos`` of batch row b,
-// rounded to bf16 (the activation dtype) as the reference's table gather does.
-__device__ __forceinline__ float2 rope_coeffs(const RopeSrc& r, int64_t b, int64_t pos) {
+// cos/sin for dim d = lane + 64 e of the row used at position ``pos`` of batch
+// row b, rounded to bf16 (the activation dtype) as the reference's table
+// gather does.
+__device__ __forceinline__ float2 rope_coeffs(const RopeSrc& r, int64_t b, int64_t pos, int e) {
   if (!r.use_rope || r.rot <= 0) return make_float2(1.f, 0.f);
-  const int d = threadIdx.x & 63;
+  const int d = (threadIdx.x & 63) + 64 * e;
   const int64_t row = r.n_pos > 0 ? (pos < r.n_pos ? pos : r.n_pos - 1) : b;
   const int dd = d < r.rot ? d : 0;
   return make_float2(bf16_to_f32(f32_to_bf16(ld_f(r.cos, r.dt, row * r.ld + dd))),
                      bf16_to_f32(f32_to_bf16(ld_f(r.sin, r.dt, row * r.ld + dd))));
 }
 
-// RMSNorm of one head held one dim per lane (wave-wide), then rotate-half
-// RoPE on the first ``rot`` dims with this lane's coefficients ``cs``.
-__device__ __forceinline__ float norm_rope_lane(float x, float w, float2 cs, const RopeSrc& r,
-                                                float eps) {
-  const int d = threadIdx.x & 63;
-  const float ss = group_sum<64>(x * x);
-  float y = x * rsqrtf(ss / kHeadDim + eps) * w;
+// RMSNorm of one head held wave-wide (lane owns dims lane + 64 e), then
+// rotate-half RoPE on the first ``rot`` dims with the lane's coefficients.
+template <int E>
+__device__ __forceinline__ void norm_rope_lane(float (&y)[E], const float (&x)[E], const float (&w)[E],
+                                               const float2 (&cs)[E], const RopeSrc& r, float eps) {
+  const int lane = threadIdx.x & 63;
+  float sq = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) sq += x[e] * x[e];
+  const float ss = group_sum<64>(sq);
+  const float inv = rsqrtf(ss / (64 * E) + eps);
+#pragma unroll
+  for (int e = 0; e < E; ++e) y[e] = x[e] * inv * w[e];
   if (r.use_rope && r.rot > 0) {
     const int half = r.rot / 2;
-    const float other = __shfl(y, d < half ? d + half : d - half, 64);
-    if (d < r.rot) y = d < half ? y * cs.x - other * cs.y : y * cs.x + other * cs.y;
+    float other[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int d = lane + 64 * e;
+      const int pd = d < half ? d + half : d - half;
+      float o = 0.f;
+#pragma unroll
+      for (int f = 0; f < E; ++f) {
+        const float v = __shfl(y[f], pd & 63, 64);
+        o = (pd >> 6) == f ? v : o;
+      }
+      other[e] = o;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int d = lane + 64 * e;
+      if (d < r.rot) y[e] = d < half ? y[e] * cs[e].x - other[e] * cs[e].y : y[e] * cs[e].x + other[e] * cs[e].y;
+    }
   }
-  return y;
 }
 
 __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
@@ -86,14 +109,16 @@ __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
 }
 
 // One wave per (head slot, row): q heads [0, nq), k heads [nq, nq + nkv), v
-// heads after that.  Lane d owns dimension d.
+// heads after that.  Lane l owns dimensions l + 64 e.
+template <int HD>
 __global__ __launch_bounds__(64) void k_qk_norm_rope_store(
     const uint16_t* __restrict__ qkv, int64_t ldq, const void* __restrict__ q_w,
     const void* __restrict__ k_w, int w_dt, RopeSrc rope, float eps,
     uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
     uint16_t* __restrict__ v_cache, const int64_t* __restrict__ seqlen,
     const int64_t* __restrict__ row_map, int64_t cache_rows, int nq, int nkv, int64_t max_len) {
-  const int d = threadIdx.x;
+  constexpr int E = HD / 64;
+  const int lane = threadIdx.x;
   const int hs = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int64_t pos = clamp64(seqlen[b], 0, max_len - 1);
@@ -101,18 +126,29 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope_store(
   const uint16_t* row = qkv + b * ldq;
   if (hs >= nq + nkv) {  // V: copy
     const int h = hs - nq - nkv;
-    v_cache[((crow * nkv + h) * max_len + pos) * kHeadDim + d] = row[(nq + nkv + h) * kHeadDim + d];
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      v_cache[((crow * nkv + h) * max_len + pos) * HD + lane + 64 * e] = row[(nq + nkv + h) * HD + lane + 64 * e];
     return;
   }
   const bool is_q = hs < nq;
-  const float x = bf16_to_f32(row[hs * kHeadDim + d]);
-  const float w = ld_f(is_q ? q_w : k_w, w_dt, d);
-  const float2 cs = rope_coeffs(rope, b, pos);
-  const uint16_t yb = f32_to_bf16(norm_rope_lane(x, w, cs, rope, eps));
-  if (is_q)
-    q_out[(b * nq + hs) * kHeadDim + d] = yb;
-  else
-    k_cache[((crow * nkv + (hs - nq)) * max_len + pos) * kHeadDim + d] = yb;
+  float x[E], w[E], y[E];
+  float2 cs[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    x[e] = bf16_to_f32(row[hs * HD + lane + 64 * e]);
+    w[e] = ld_f(is_q ? q_w : k_w, w_dt, lane + 64 * e);
+    cs[e] = rope_coeffs(rope, b, pos, e);
+  }
+  norm_rope_lane<E>(y, x, w, cs, rope, eps);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const uint16_t yb = f32_to_bf16(y[e]);
+    if (is_q)
+      q_out[(b * nq + hs) * HD + lane + 64 * e] = yb;
+    else
+      k_cache[((crow * nkv + (hs - nq)) * max_len + pos) * HD + lane + 64 * e] = yb;
+  }
 }
 
 typedef __bf16 bf16x8a_t __attribute__((ext_vector_type(8)));
@@ -155,7 +191,7 @@ __device__ __forceinline__ uint32_t sel32(bool c, uint32_t a, uint32_t b) { retu
 // dispatch order and far fewer than the GPU holds at once, so they are all
 // resident; the wait is bounded (about 0.2 s) and records a timeout in word 2
 // of the sync area instead of hanging.
-template <bool FUSED>
+template <bool FUSED, int HD>
 __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     const uint16_t* __restrict__ src, int64_t ldq, const void* __restrict__ qn_w,
     const void* __restrict__ kn_w, int w_dt, RopeSrc rope, float eps,
@@ -165,9 +201,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     float* __restrict__ part_acc, float* __restrict__ part_ml, uint16_t* __restrict__ out,
     const uint32_t* __restrict__ o_w, const void* __restrict__ o_alpha, int o_alpha_dt, int o_rows,
     uint16_t* __restrict__ o_out) {
-  __shared__ __align__(16) uint16_t qs[kMaxGroup][kHeadDim];
-  __shared__ __align__(16) uint32_t vt[kHeadDim][kVtRow];
-  __shared__ __align__(16) uint16_t kvnew[2][kHeadDim];
+  constexpr int E = HD / 64;   // dims per lane in the wave-wide head layouts
+  constexpr int KS = HD / 32;  // 32-dim slices of K per score MFMA chain
+  constexpr int NB = HD / 16;  // 16-dim output blocks of P.V
+  constexpr int IPH = HD / 4;  // 4-dim output items per head
+  __shared__ __align__(16) uint16_t qs[kMaxGroup][HD];
+  __shared__ __align__(16) uint32_t vt[HD][kVtRow];
+  __shared__ __align__(16) uint16_t kvnew[2][HD];
   __shared__ float wm[4][kMaxGroup], wl[4][kMaxGroup];
   __shared__ float hm[kMaxGroup], hl[kMaxGroup];
   __shared__ __align__(16) uint4 os4[kOWords * 2][32];  // O projection input
@@ -222,9 +262,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   const bool owns_pos = FUSED && sp == n_spl - 1;
 
   // K fragments: positions 32 wv + 16 pb + r16, dims 8 g + 32 ks.
-  // V: load i covers the wave's positions 32 wv + 8 i .. +7 contiguously
-  // (1 KB): lane l holds position 32 wv + 8 i + (l >> 3), dims 8 (l & 7) .. +8.
-  auto load_chunk = [&](int c, uint4 (&kf)[2][2], uint4 (&vr)[4]) {
+  // V: load (i, e) covers the wave's positions 32 wv + 8 i .. +7: lane l
+  // holds position 32 wv + 8 i + (l >> 3), dims 64 e + 8 (l & 7) .. +8.
+  auto load_chunk = [&](int c, uint4 (&kf)[2][KS], uint4 (&vr)[4][E]) {
     const int64_t lo = start + static_cast<int64_t>(c) * kSplit;
     const int64_t hi = lo + kSplit < kv_len ? lo + kSplit : kv_len;
 #pragma unroll
@@ -232,66 +272,90 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       int64_t t = lo + 32 * wv + 16 * pb + r16;
       t = t < hi ? t : hi - 1;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        kf[pb][ks] = *reinterpret_cast<const uint4*>(k_cache + (base + t) * kHeadDim + 8 * g + 32 * ks);
+      for (int ks = 0; ks < KS; ++ks)
+        kf[pb][ks] = *reinterpret_cast<const uint4*>(k_cache + (base + t) * HD + 8 * g + 32 * ks);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       int64_t tv = lo + 32 * wv + 8 * i + (lane >> 3);
       tv = tv < hi ? tv : hi - 1;
-      vr[i] = *reinterpret_cast<const uint4*>(v_cache + (base + tv) * kHeadDim + 8 * (lane & 7));
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        vr[i][e] = *reinterpret_cast<const uint4*>(v_cache + (base + tv) * HD + 64 * e + 8 * (lane & 7));
     }
   };
-  uint4 kf[2][2], vr[4];
-  uint16_t new_kv = 0;  // FUSED owner split: the new K (wave 0) or V (wave 1) element
+  uint4 kf[2][KS], vr[4][E];
+  uint16_t new_kv[E] = {};  // FUSED owner split: the new K (wave 0) or V (wave 1) elements
   if constexpr (FUSED) {
     // Every load of the prologue is issued before any of them is used, and
     // before the first chunk's (memory counters complete in issue order, so
     // q would otherwise wait for the K/V chunk).
     const uint16_t* row = src + b * ldq;
-    uint16_t xq[kMaxGroup / 4];
+    uint16_t xq[kMaxGroup / 4][E];
 #pragma unroll
     for (int i = 0; i < kMaxGroup / 4; ++i) {
       const int hh = wv + 4 * i;
-      xq[i] = hh < group ? row[(kvh * group + hh) * kHeadDim + lane] : uint16_t(0);
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        xq[i][e] = hh < group ? row[(kvh * group + hh) * HD + lane + 64 * e] : uint16_t(0);
     }
-    const uint16_t xkv =
-        owns_pos && wv < 2 ? row[(nq + kvh + (wv ? nkv : 0)) * kHeadDim + lane] : uint16_t(0);
-    const float wq = ld_f(qn_w, w_dt, lane);
-    const float wk = ld_f(kn_w, w_dt, lane);
-    const float2 cs = rope_coeffs(rope, b, pos);
+    uint16_t xkv[E];
+    float wq[E], wk[E];
+    float2 cs[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      xkv[e] = owns_pos && wv < 2 ? row[(nq + kvh + (wv ? nkv : 0)) * HD + lane + 64 * e] : uint16_t(0);
+      wq[e] = ld_f(qn_w, w_dt, lane + 64 * e);
+      wk[e] = ld_f(kn_w, w_dt, lane + 64 * e);
+      cs[e] = rope_coeffs(rope, b, pos, e);
+    }
     load_chunk(c_beg, kf, vr);
 #pragma unroll
     for (int i = 0; i < kMaxGroup / 4; ++i) {
       const int hh = wv + 4 * i;
-      if (hh < kMaxGroup)
-        qs[hh][lane] = hh < group ? f32_to_bf16(norm_rope_lane(bf16_to_f32(xq[i]), wq, cs, rope, eps))
-                                  : uint16_t(0);
+      if (hh < kMaxGroup) {
+        float xf[E], yf[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) xf[e] = bf16_to_f32(xq[i][e]);
+        norm_rope_lane<E>(yf, xf, wq, cs, rope, eps);
+#pragma unroll
+        for (int e = 0; e < E; ++e) qs[hh][lane + 64 * e] = hh < group ? f32_to_bf16(yf[e]) : uint16_t(0);
+      }
     }
     if (owns_pos && wv < 2) {
-      new_kv = xkv;  // wave 1: V is stored as is
-      if (wv == 0) new_kv = f32_to_bf16(norm_rope_lane(bf16_to_f32(xkv), wk, cs, rope, eps));
-      kvnew[wv][lane] = new_kv;
+      float xf[E], yf[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        new_kv[e] = xkv[e];  // wave 1: V is stored as is
+        xf[e] = bf16_to_f32(xkv[e]);
+      }
+      if (wv == 0) {
+        norm_rope_lane<E>(yf, xf, wk, cs, rope, eps);
+#pragma unroll
+        for (int e = 0; e < E; ++e) new_kv[e] = f32_to_bf16(yf[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) kvnew[wv][lane + 64 * e] = new_kv[e];
     }
   } else {
-    const uint16_t* qsrc = src + (b * nq + kvh * group) * kHeadDim;
-    uint16_t xq[kMaxGroup * kHeadDim / kAttnThreads];
+    const uint16_t* qsrc = src + (b * nq + kvh * group) * HD;
+    uint16_t xq[kMaxGroup * HD / kAttnThreads];
 #pragma unroll
-    for (int k = 0; k < kMaxGroup * kHeadDim / kAttnThreads; ++k) {
+    for (int k = 0; k < kMaxGroup * HD / kAttnThreads; ++k) {
       const int i = tid + kAttnThreads * k;
-      xq[k] = i / kHeadDim < group ? qsrc[i] : uint16_t(0);
+      xq[k] = i / HD < group ? qsrc[i] : uint16_t(0);
     }
     load_chunk(c_beg, kf, vr);
 #pragma unroll
-    for (int k = 0; k < kMaxGroup * kHeadDim / kAttnThreads; ++k) {
+    for (int k = 0; k < kMaxGroup * HD / kAttnThreads; ++k) {
       const int i = tid + kAttnThreads * k;
-      qs[i / kHeadDim][i % kHeadDim] = xq[k];
+      qs[i / HD][i % HD] = xq[k];
     }
   }
   __syncthreads();
-  uint4 qf[2];
+  uint4 qf[KS];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) qf[ks] = *reinterpret_cast<const uint4*>(&qs[r16][8 * g + 32 * ks]);
+  for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const uint4*>(&qs[r16][8 * g + 32 * ks]);
 
   // Each wave keeps its own running softmax state over its 32 positions of
   // every chunk (head r16's max and sum, in the 4 lanes holding that head), so
@@ -299,9 +363,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   // after the last chunk.  V^T of a chunk sits in the wave's own columns of
   // vt (positions 32 wv .. +31), which only that wave writes and reads.
   float mrun = -INFINITY, lrun = 0.f;
-  f32x4a_t oacc[4];
+  f32x4a_t oacc[NB];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) oacc[nb] = f32x4a_t{0.f, 0.f, 0.f, 0.f};
+  for (int nb = 0; nb < NB; ++nb) oacc[nb] = f32x4a_t{0.f, 0.f, 0.f, 0.f};
   for (int c = c_beg; c < c_end; ++c) {
     const int64_t lo = start + static_cast<int64_t>(c) * kSplit;
     const int64_t hi = lo + kSplit < kv_len ? lo + kSplit : kv_len;
@@ -310,30 +374,34 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       for (int pb = 0; pb < 2; ++pb) {
         const bool nk = owns_pos && lo + 32 * wv + 16 * pb + r16 == pos;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int ks = 0; ks < KS; ++ks) {
           const uint4 v = *reinterpret_cast<const uint4*>(&kvnew[0][8 * g + 32 * ks]);
           kf[pb][ks] = make_uint4(sel32(nk, v.x, kf[pb][ks].x), sel32(nk, v.y, kf[pb][ks].y),
                                   sel32(nk, v.z, kf[pb][ks].z), sel32(nk, v.w, kf[pb][ks].w));
         }
       }
-      const uint4 v = *reinterpret_cast<const uint4*>(&kvnew[1][8 * (lane & 7)]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool nv = owns_pos && lo + 32 * wv + 8 * i + (lane >> 3) == pos;
-        vr[i] = make_uint4(sel32(nv, v.x, vr[i].x), sel32(nv, v.y, vr[i].y), sel32(nv, v.z, vr[i].z),
-                           sel32(nv, v.w, vr[i].w));
+      for (int e = 0; e < E; ++e) {
+        const uint4 v = *reinterpret_cast<const uint4*>(&kvnew[1][64 * e + 8 * (lane & 7)]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool nv = owns_pos && lo + 32 * wv + 8 * i + (lane >> 3) == pos;
+          vr[i][e] = make_uint4(sel32(nv, v.x, vr[i][e].x), sel32(nv, v.y, vr[i][e].y),
+                                sel32(nv, v.z, vr[i][e].z), sel32(nv, v.w, vr[i][e].w));
+        }
       }
     }
     // V^T in position pairs: lanes l and l ^ 8 hold positions 2m and 2m + 1
     // of the same 8 dims (one DPP rotate by 8 within each 16-lane row swaps
     // them); the even one writes the pairs of dims 0..3 of its 8, the odd one
     // dims 4..7.
-    {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
       const bool odd = (lane >> 3) & 1;
-      const int d0 = 8 * (lane & 7) + (odd ? 4 : 0);
+      const int d0 = 64 * e + 8 * (lane & 7) + (odd ? 4 : 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t u[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+        const uint32_t u[4] = {vr[i][e].x, vr[i][e].y, vr[i][e].z, vr[i][e].w};
         uint32_t o[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) o[k] = __builtin_amdgcn_update_dpp(0, u[k], 0x128, 0xF, 0xF, false);
@@ -355,7 +423,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb) {
       f32x4a_t acc = mfma_att(kf[pb][0], qf[0], f32x4a_t{0.f, 0.f, 0.f, 0.f});
-      acc = mfma_att(kf[pb][1], qf[1], acc);
+#pragma unroll
+      for (int ks = 1; ks < KS; ++ks) acc = mfma_att(kf[pb][ks], qf[ks], acc);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         s[pb][i] = 32 * wv + 16 * pb + 4 * g + i < span ? acc[i] * scale2 : -INFINITY;
@@ -388,7 +457,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     for (int i = 0; i < 4; ++i) rr[i] = __shfl(r, 4 * g + i, 64);
     const int mp = 16 * wv + 2 * g;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
       const int d = 16 * nb + r16;
       const uint2 b0 = *reinterpret_cast<const uint2*>(&vt[d][mp]);
       const uint2 b1 = *reinterpret_cast<const uint2*>(&vt[d][mp + 8]);
@@ -399,19 +468,22 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     }
   if (o_w) o_prefetch();  // after the K/V stream, in flight through the merge and the barrier
   // The new K/V go to the cache last (after every read of the cache).
-  if (owns_pos && wv < 2) (wv == 0 ? k_cache : v_cache)[(base + pos) * kHeadDim + lane] = new_kv;
+  if (owns_pos && wv < 2) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) (wv == 0 ? k_cache : v_cache)[(base + pos) * HD + lane + 64 * e] = new_kv[e];
+  }
   // Combine the waves' states in a fixed order, through LDS that V no longer
   // needs: head h's max M = max_w m_w, sum = sum_w l_w exp(m_w - M), output
   // sum_w acc_w exp(m_w - M).
-  static_assert(sizeof(vt) >= 4 * kMaxGroup * kHeadDim * sizeof(float), "reduction buffer");
-  float (*ow)[kMaxGroup][kHeadDim] = reinterpret_cast<float (*)[kMaxGroup][kHeadDim]>(&vt[0][0]);
+  static_assert(sizeof(vt) >= 4 * kMaxGroup * HD * sizeof(float), "reduction buffer");
+  float (*ow)[kMaxGroup][HD] = reinterpret_cast<float (*)[kMaxGroup][HD]>(&vt[0][0]);
   __syncthreads();  // every wave's last P.V has read its vt columns
   if (g == 0) {
     wm[wv][r16] = mrun;
     wl[wv][r16] = lrun;
   }
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
+  for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (4 * g + i < group) ow[wv][4 * g + i][16 * nb + r16] = oacc[nb][i];
@@ -431,10 +503,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   __syncthreads();
   const int64_t pidx = (b * nkv + kvh) * max_splits + sp;
   const int64_t n_part = static_cast<int64_t>(gridDim.z) * nkv * max_splits * kMaxGroup;
-  const CoherentBuf acc_buf(part_acc, static_cast<uint32_t>(n_part * kHeadDim * 4));
+  const CoherentBuf acc_buf(part_acc, static_cast<uint32_t>(n_part * HD * 4));
   const CoherentBuf ml_buf(part_ml, static_cast<uint32_t>(n_part * 8));
-  for (int item = tid; item < group * 16; item += kAttnThreads) {
-    const int hh = item >> 4, dq = item & 15;
+  for (int item = tid; item < group * IPH; item += kAttnThreads) {
+    const int hh = item / IPH, dq = item % IPH;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -450,9 +522,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       uint2 r;
       r.x = pack_bf16x2_rn(o.x * inv, o.y * inv);
       r.y = pack_bf16x2_rn(o.z * inv, o.w * inv);
-      store_out(out + (b * nq + kvh * group + hh) * kHeadDim + 4 * dq, r, o_w != nullptr);
+      store_out(out + (b * nq + kvh * group + hh) * HD + 4 * dq, r, o_w != nullptr);
     } else {
-      acc_buf.st4(static_cast<uint32_t>(((pidx * kMaxGroup + hh) * kHeadDim + 4 * dq) * 4), o);
+      acc_buf.st4(static_cast<uint32_t>(((pidx * kMaxGroup + hh) * HD + 4 * dq) * 4), o);
     }
   }
   if (n_spl == 1) return;
@@ -482,7 +554,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   // running (max, sum, acc) state, and the TPI states combine through lane
   // exchanges in a fixed order.
   const int64_t p0 = (b * nkv + kvh) * max_splits;
-  const int n_items = group * 16;
+  const int n_items = group * IPH;
   const int ipw = (n_items + n_spl - 1) / n_spl;
   const int it_lo = sp * ipw, it_hi = it_lo + ipw < n_items ? it_lo + ipw : n_items;
   int tpi = 1;
@@ -490,7 +562,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   for (int ib = it_lo; ib < it_hi; ib += kAttnThreads / tpi) {
     const int item = ib + tid / tpi, j = tid % tpi;
     const bool live = item < it_hi;
-    const int hh = live ? item >> 4 : 0, dq = item & 15;
+    const int hh = live ? item / IPH : 0, dq = item % IPH;
     float mx = -INFINITY, den = 0.f, n0 = 0.f, n1 = 0.f, n2 = 0.f, n3 = 0.f;
     for (int s0 = 0; s0 < n_spl; s0 += kCombineChunk * tpi) {  // uniform over the wave
       float2 ml[kCombineChunk];
@@ -503,7 +575,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
         if (s < n_spl) {
           const uint32_t q = static_cast<uint32_t>((p0 + s) * kMaxGroup + hh);
           ml[u] = ml_buf.ld2(q * 8);
-          ac[u] = acc_buf.ld4((q * kHeadDim + 4 * dq) * 4);
+          ac[u] = acc_buf.ld4((q * HD + 4 * dq) * 4);
         }
       }
       MA_ISSUE_FENCE();
@@ -542,7 +614,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       uint2 r;
       r.x = pack_bf16x2_rn(n0 / den, n1 / den);
       r.y = pack_bf16x2_rn(n2 / den, n3 / den);
-      store_out(out + (b * nq + kvh * group + hh) * kHeadDim + 4 * dq, r, o_w != nullptr);
+      store_out(out + (b * nq + kvh * group + hh) * HD + 4 * dq, r, o_w != nullptr);
     }
   }
   };
@@ -564,7 +636,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   __syncthreads();
   {  // entry (i, half, l) of os4 = values 8 half .. + 8 of word l * kOWords + i
     const int w = tid >> 1, half = tid & 1;
-    const uint64_t* p = reinterpret_cast<const uint64_t*>(out + static_cast<int64_t>(b) * nq * kHeadDim +
+    const uint64_t* p = reinterpret_cast<const uint64_t*>(out + static_cast<int64_t>(b) * nq * HD +
                                                           w * 16 + 8 * half);
     const uint64_t v0 = ld_coh64(p), v1 = ld_coh64(p + 1);
     os4[(w % kOWords) * 2 + half][w / kOWords] =
@@ -630,8 +702,8 @@ int check_rope(const RopeSrc& r, int head_dim, const char* what) {
 
 int check_heads(int64_t batch, int nq, int nkv, int head_dim, int64_t max_len, int64_t cache_rows,
                 const void* row_map, const char* what) {
-  if (head_dim != kHeadDim)
-    return fail(MA_EVALUE, "%s: head_dim %d unsupported (64)", what, head_dim);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(MA_EVALUE, "%s: head_dim %d unsupported (64 or 128)", what, head_dim);
   if (batch < 0 || nq < 1 || nkv < 1 || nq % nkv || nq / nkv > kMaxGroup || max_len < 1)
     return fail(MA_EVALUE, "%s: bad sizes", what);
   if (!row_map && cache_rows < batch)
@@ -664,18 +736,24 @@ extern "C" int ma_qk_norm_rope_store(const void* qkv, int64_t ldq, int64_t batch
     return fail(MA_EVALUE, "%s: qkv row stride too small", what);
   if (batch == 0) return MA_OK;
   dim3 grid(static_cast<unsigned>(n_heads + 2 * n_kv_heads), static_cast<unsigned>(batch));
-  hipLaunchKernelGGL(k_qk_norm_rope_store, grid, dim3(64), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(qkv), ldq, q_norm_w, k_norm_w, w_dtype, rope,
-                     eps, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache),
-                     static_cast<uint16_t*>(v_cache), seqlen, row_map, cache_rows, n_heads,
-                     n_kv_heads, max_len);
+#define MA_QK_ARGS                                                                               \
+  static_cast<const uint16_t*>(qkv), ldq, q_norm_w, k_norm_w, w_dtype, rope, eps,                \
+      static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), \
+      seqlen, row_map, cache_rows, n_heads, n_kv_heads, max_len
+  if (head_dim == 128)
+    hipLaunchKernelGGL(k_qk_norm_rope_store<128>, grid, dim3(64), 0, static_cast<hipStream_t>(stream),
+                       MA_QK_ARGS);
+  else
+    hipLaunchKernelGGL(k_qk_norm_rope_store<64>, grid, dim3(64), 0, static_cast<hipStream_t>(stream),
+                       MA_QK_ARGS);
+#undef MA_QK_ARGS
   return check_launch(what);
 }
 
-extern "C" size_t ma_gqa_workspace_bytes(int64_t batch, int n_kv_heads, int64_t max_len) {
-  if (batch < 0 || n_kv_heads < 1 || max_len < 1) return 0;
+extern "C" size_t ma_gqa_workspace_bytes(int64_t batch, int n_kv_heads, int64_t max_len, int head_dim) {
+  if (batch < 0 || n_kv_heads < 1 || max_len < 1 || (head_dim != 64 && head_dim != 128)) return 0;
   const size_t parts = static_cast<size_t>(batch) * n_kv_heads * max_splits_for(max_len) * kMaxGroup;
-  return sync_bytes(batch, n_kv_heads) + parts * (kHeadDim + 2) * sizeof(float);
+  return sync_bytes(batch, n_kv_heads) + parts * (head_dim + 2) * sizeof(float);
 }
 
 // Workgroups of one attention launch.
@@ -692,10 +770,15 @@ static int64_t attn_grid_splits(int64_t batch, int nkv, int64_t max_len, int64_t
 // (row, KV head)'s splits are consecutive, so every earlier pair has all of
 // its splits placed and finishes; with the O projection in the launch the
 // whole grid meets at one barrier and must be resident.
-static int attn_capacity(bool fused, int64_t* cap) {
-  const void* fn = fused ? reinterpret_cast<const void*>(&k_decode_attn<true>)
-                         : reinterpret_cast<const void*>(&k_decode_attn<false>);
-  return resident_capacity(fn, kAttnThreads, cap);
+template <int HD>
+static const void* attn_kernel(bool fused) {
+  return fused ? reinterpret_cast<const void*>(&k_decode_attn<true, HD>)
+               : reinterpret_cast<const void*>(&k_decode_attn<false, HD>);
+}
+
+static int attn_capacity(bool fused, int head_dim, int64_t* cap) {
+  return resident_capacity(head_dim == 128 ? attn_kernel<128>(fused) : attn_kernel<64>(fused),
+                           kAttnThreads, cap);
 }
 
 extern "C" int ma_decode_attn_o_supported(int64_t batch, int n_heads, int n_kv_heads, int head_dim,
@@ -703,9 +786,10 @@ extern "C" int ma_decode_attn_o_supported(int64_t batch, int n_heads, int n_kv_h
   if (batch != 1 || n_kv_heads < 1 || max_len < 1 ||
       static_cast<int64_t>(n_heads) * head_dim != 32 * kOWords * 16)
     return 0;
+  if (head_dim != 64 && head_dim != 128) return 0;
   const int64_t n_wg = attn_grid_splits(batch, n_kv_heads, max_len, window) * n_kv_heads;
   int64_t cap = 0;
-  if (attn_capacity(true, &cap) != MA_OK || n_wg > cap) return 0;
+  if (attn_capacity(true, head_dim, &cap) != MA_OK || n_wg > cap) return 0;
   return n_wg >= kBarGroups && o_rows >= 1 && o_rows <= n_wg * 8 * kOPass;
 }
 
@@ -714,30 +798,30 @@ static int launch_attn(bool fused, const void* src, int64_t ldq, const void* qn_
                        const void* kn_w, int w_dt, const RopeSrc& rope, float eps,
                        void* k_cache, void* v_cache, int64_t cache_rows, int64_t max_len,
                        const int64_t* seqlen, const int64_t* row_map, int64_t batch, int nq,
-                       int nkv, int64_t window, float scale, void* out, void* workspace,
+                       int nkv, int hd, int64_t window, float scale, void* out, void* workspace,
                        size_t workspace_bytes, const uint32_t* o_w, const void* o_alpha,
                        int o_alpha_dt, int64_t o_rows, void* o_out, hipStream_t s,
                        const char* what) {
-  if (!workspace || workspace_bytes < ma_gqa_workspace_bytes(batch, nkv, max_len))
+  if (!workspace || workspace_bytes < ma_gqa_workspace_bytes(batch, nkv, max_len, hd))
     return fail(MA_EVALUE, "%s: workspace too small", what);
   if (!aligned16(workspace) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out) ||
       (!fused && !aligned16(src)))
     return fail(MA_EVALUE, "%s: buffers must be 16-byte aligned", what);
   const int64_t max_splits = max_splits_for(max_len);
-  if (batch * nkv * max_splits * kMaxGroup * kHeadDim * 4 >= (int64_t{1} << 32))
+  if (batch * nkv * max_splits * kMaxGroup * hd * 4 >= (int64_t{1} << 32))
     return fail(MA_EVALUE, "%s: batch x kv heads x max_len too large for one launch", what);
   int64_t grid_splits = attn_grid_splits(batch, nkv, max_len, window);
   int64_t capacity = 0;
-  if (int rc = attn_capacity(fused, &capacity)) return rc;
+  if (int rc = attn_capacity(fused, hd, &capacity)) return rc;
   if (grid_splits > capacity) grid_splits = capacity;
   auto* sync = static_cast<uint32_t*>(workspace);
   float* acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + sync_bytes(batch, nkv));
-  float* ml = acc + static_cast<size_t>(batch) * nkv * max_splits * kMaxGroup * kHeadDim;
+  float* ml = acc + static_cast<size_t>(batch) * nkv * max_splits * kMaxGroup * hd;
   dim3 grid(static_cast<unsigned>(grid_splits), static_cast<unsigned>(nkv),
             static_cast<unsigned>(batch));
   if (o_w) {
     const int64_t n_wg = grid_splits * nkv * batch;
-    if (batch != 1 || static_cast<int64_t>(nq) * kHeadDim != 32 * kOWords * 16)
+    if (batch != 1 || static_cast<int64_t>(nq) * hd != 32 * kOWords * 16)
       return fail(MA_EVALUE, "%s: the O projection in the launch needs batch 1 and n_heads x head_dim = %d",
                   what, 32 * kOWords * 16);
     if (n_wg > capacity)
@@ -757,10 +841,14 @@ static int launch_attn(bool fused, const void* src, int64_t ldq, const void* qn_
       seqlen, row_map, nq, nkv, window, scale, static_cast<int>(max_splits), sync, acc, ml,   \
       static_cast<uint16_t*>(out), o_w, o_alpha, o_alpha_dt, static_cast<int>(o_rows),         \
       static_cast<uint16_t*>(o_out)
-  if (fused)
-    hipLaunchKernelGGL(k_decode_attn<true>, grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
+  if (fused && hd == 128)
+    hipLaunchKernelGGL((k_decode_attn<true, 128>), grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
+  else if (fused)
+    hipLaunchKernelGGL((k_decode_attn<true, 64>), grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
+  else if (hd == 128)
+    hipLaunchKernelGGL((k_decode_attn<false, 128>), grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
   else
-    hipLaunchKernelGGL(k_decode_attn<false>, grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
+    hipLaunchKernelGGL((k_decode_attn<false, 64>), grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
 #undef MA_ATTN_ARGS
   return check_launch(what);
 }
@@ -777,7 +865,7 @@ extern "C" int ma_decode_gqa_attn(const void* q, int64_t batch, int n_heads, int
   const RopeSrc none{nullptr, nullptr, MA_F32, 0, 0, 0, 0};
   return launch_attn(false, q, 0, nullptr, nullptr, MA_F32, none, 0.f,
                      const_cast<void*>(k_cache), const_cast<void*>(v_cache), cache_rows, max_len,
-                     seqlen, row_map, batch, n_heads, n_kv_heads, window, scale, out, workspace,
+                     seqlen, row_map, batch, n_heads, n_kv_heads, head_dim, window, scale, out, workspace,
                      workspace_bytes, nullptr, nullptr, 0, 0, nullptr,
                      static_cast<hipStream_t>(stream), what);
 }
@@ -804,7 +892,7 @@ extern "C" int ma_decode_attn_fused(const void* qkv, int64_t ldq, int64_t batch,
     return fail(MA_EVALUE, "%s: qkv row stride too small", what);
   if (batch == 0) return MA_OK;
   return launch_attn(true, qkv, ldq, q_norm_w, k_norm_w, w_dtype, rope, eps, k_cache, v_cache,
-                     cache_rows, max_len, seqlen, row_map, batch, n_heads, n_kv_heads, window,
+                     cache_rows, max_len, seqlen, row_map, batch, n_heads, n_kv_heads, head_dim, window,
                      scale, out, workspace, workspace_bytes, o_w, o_alpha, o_alpha_dtype, o_rows,
                      o_out, static_cast<hipStream_t>(stream), what);
 }

@@ -12,7 +12,7 @@ arguments and checks.  Differences at the boundary:
   ``apply_qkv_decode``, ``decode_gqa_attn``) in one launch, reading the
   float32 RoPE tables at ``seqlen[b]`` itself.
 
-head_dim must be 64 and at most 16 query heads may share a KV head.
+head_dim must be 64 or 128 and at most 16 query heads may share a KV head.
 """
 
 from __future__ import annotations
@@ -53,10 +53,12 @@ def o_projection_supported(batch: int, num_heads: int, num_kv_heads: int, head_d
                                                          max_len, int(window or 0), o_rows))
 
 
-def gqa_workspace(batch: int, num_kv_heads: int, max_len: int, device) -> torch.Tensor:
+def gqa_workspace(batch: int, num_kv_heads: int, max_len: int, device, head_dim: int = 64) -> torch.Tensor:
     """Zeroed workspace for ``decode_gqa_attn`` / ``decode_attention``; keep
     one per cache so decode allocates nothing inside a graph."""
-    nbytes = int(_lib.load().ma_gqa_workspace_bytes(batch, num_kv_heads, max_len))
+    nbytes = int(_lib.load().ma_gqa_workspace_bytes(batch, num_kv_heads, max_len, head_dim))
+    if nbytes == 0:
+        raise ValueError(f"head_dim {head_dim} unsupported (64 or 128).")
     return workspace.register_attention(torch.zeros(nbytes, device=device, dtype=torch.uint8))
 
 
@@ -131,9 +133,9 @@ def decode_gqa_attn(
     if n_q % n_kv != 0:
         raise ValueError(f"n_q={n_q} not divisible by n_kv={n_kv}.")
     out = torch.empty_like(q)
-    nbytes = int(_lib.load().ma_gqa_workspace_bytes(bsz, n_kv, max_len))
+    nbytes = int(_lib.load().ma_gqa_workspace_bytes(bsz, n_kv, max_len, head_dim))
     if workspace is None:
-        workspace = gqa_workspace(bsz, n_kv, max_len, q.device)
+        workspace = gqa_workspace(bsz, n_kv, max_len, q.device, head_dim)
     elif workspace.numel() < nbytes:
         raise ValueError(f"workspace holds {workspace.numel()} bytes, needs {nbytes}.")
     sl, rm = _i64(seqlen), _i64(row_map)

@@ -231,7 +231,7 @@ class SyntheticDecoder:
             ks.append(k)
             vs.append(v)
         seqlen = torch.full((batch,), prefill_len, device=self.device, dtype=torch.int64)
-        ws = gqa_workspace(batch, c.kv_heads, self.max_len, self.device)
+        ws = gqa_workspace(batch, c.kv_heads, self.max_len, self.device, c.head_dim)
         return KVCache(ks, vs, seqlen, self.max_len, ws)
 
     def _layer(self, i: int, hidden: torch.Tensor, cache: KVCache, routing=None,

@@ -25,14 +25,22 @@ from oracle import decoder as od
 pytestmark = pytest.mark.gpu
 
 
+# (query heads, KV heads, head_dim, rotary_dim): the synthetic decoder's, the
+# Maple-Preview shape (16 / 4 heads of 128, partial rotary 0.5) and a full
+# rotary over 128 (rotate-half pairs dims 64 apart, across a lane's two dims).
+HEADS = [(32, 4, 64, 32), (16, 4, 128, 64), (16, 4, 128, 128)]
+
+
 def _rope_rows(table, seqlen, dev):
     """The reference's gather: float32 table rows at seqlen, cast to bf16."""
     return torch.from_numpy(table).to(dev)[seqlen.clamp(0, table.shape[0] - 1)].to(torch.bfloat16)
 
 
+@pytest.mark.parametrize("heads", HEADS)
 @pytest.mark.parametrize("mapped", [False, True])
-def test_qk_norm_rope_store_vs_oracle(dev, mapped):
-    nq, nkv, d, max_len, rot = 32, 4, 64, 4224, 32
+def test_qk_norm_rope_store_vs_oracle(dev, mapped, heads):
+    nq, nkv, d, rot = heads
+    max_len = 4224
     seqlen = torch.tensor([0, 100, 4095], device=dev)
     rows = 5 if mapped else 3
     row_map = torch.tensor([4, 0, 2], device=dev) if mapped else None
@@ -67,9 +75,11 @@ def test_qk_norm_rope_store_vs_oracle(dev, mapped):
         assert torch.equal(vc[r][:, untouched[r]], v0[r][:, untouched[r]])
 
 
+@pytest.mark.parametrize("heads", HEADS[:2])
 @pytest.mark.parametrize("window", [None, 512])
-def test_gqa_ragged_vs_oracle(dev, window):
-    nq, nkv, d, max_len = 32, 4, 64, 4096
+def test_gqa_ragged_vs_oracle(dev, window, heads):
+    nq, nkv, d, _ = heads
+    max_len = 4096
     lens = [1, 63, 64, 65, 300, 511, 1000, 4096]
     seqlen = torch.tensor([n - 1 for n in lens], device=dev)
     q = synthetic.randn_bf16((len(lens), nq, 1, d), 11, dev)
@@ -84,13 +94,15 @@ def test_gqa_ragged_vs_oracle(dev, window):
     assert torch.equal(solo, out[6:7])
 
 
+@pytest.mark.parametrize("heads", HEADS)
 @pytest.mark.parametrize("window", [None, 300])
-def test_fused_attention_equals_two_step(dev, window):
+def test_fused_attention_equals_two_step(dev, window, heads):
     """decode_attention gives the bits of apply_qkv_decode + decode_gqa_attn
     (q, the written K/V and the output), for ragged rows through a row map,
     leaves the per-(row, KV head) arrival counters of the split barrier at zero
     and records no timed-out wait."""
-    nq, nkv, d, max_len, rot = 32, 4, 64, 1100, 32
+    nq, nkv, d, rot = heads
+    max_len = 1100
     seqlen = torch.tensor([0, 127, 128, 700, 1099], device=dev)
     row_map = torch.tensor([3, 5, 0, 1, 4], device=dev)
     qkv = synthetic.randn_bf16((5, (nq + 2 * nkv) * d), 21, dev)
@@ -104,7 +116,7 @@ def test_fused_attention_equals_two_step(dev, window):
                          kc, vc, seqlen, row_map=row_map, num_heads=nq, num_kv_heads=nkv,
                          head_dim=d, rotary_dim=rot, use_rope=True, use_qk_norm=True, eps=1e-6)
     ref = decode_gqa_attn(q, kc, vc, seqlen, row_map=row_map, scale=d ** -0.5, window=window)
-    ws = gqa_workspace(5, nkv, max_len, dev)
+    ws = gqa_workspace(5, nkv, max_len, dev, d)
     for _ in range(2):
         out = decode_attention(qkv, qw, kw, torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev),
                                kc2, vc2, seqlen, ws, row_map=row_map, num_heads=nq, num_kv_heads=nkv,
@@ -122,13 +134,15 @@ def test_fused_attention_equals_two_step(dev, window):
         assert_bf16_close(np_f(out[b, :, 0]), o, atol_frac=2e-3, what=f"row {b}")
 
 
+@pytest.mark.parametrize("heads", HEADS[:2])
 @pytest.mark.parametrize("seqlen", [0, 130, 2000, 4100])
-def test_fused_attention_o_projection_equals_gemv(dev, seqlen):
+def test_fused_attention_o_projection_equals_gemv(dev, seqlen, heads):
     """decode_attention(..., o_linear=...) at batch 1 returns the plain call's
     attention output and, from the same launch, the bits of ternary_gemv on
     it (the 2048 x 2048 o_proj), over consecutive calls on one workspace,
     with no timed-out wait recorded."""
-    nq, nkv, d, max_len, rot = 32, 4, 64, 4224, 32
+    nq, nkv, d, rot = heads
+    max_len = 4224
     qkv = synthetic.randn_bf16((1, (nq + 2 * nkv) * d), 31 + seqlen, dev)
     kc = synthetic.randn_bf16((1, nkv, max_len, d), 32, dev)
     vc = synthetic.randn_bf16((1, nkv, max_len, d), 33, dev)
@@ -139,8 +153,8 @@ def test_fused_attention_o_projection_equals_gemv(dev, seqlen):
     assert o_projection_supported(1, nq, nkv, d, max_len, None, 2048)
     kw = dict(num_heads=nq, num_kv_heads=nkv, head_dim=d, rotary_dim=rot, eps=1e-6, scale=d ** -0.5)
     kc2, vc2 = kc.clone(), vc.clone()
-    ref = decode_attention(qkv, w, w, cos, sin, kc, vc, sl, gqa_workspace(1, nkv, max_len, dev), **kw)
-    ws = gqa_workspace(1, nkv, max_len, dev)
+    ref = decode_attention(qkv, w, w, cos, sin, kc, vc, sl, gqa_workspace(1, nkv, max_len, dev, d), **kw)
+    ws = gqa_workspace(1, nkv, max_len, dev, d)
     for _ in range(3):
         out, o = decode_attention(qkv, w, w, cos, sin, kc2, vc2, sl, ws, o_linear=(wo, ao), **kw)
         o_ref = ternary_gemv(out.reshape(1, -1), wo, ao)
@@ -151,8 +165,8 @@ def test_fused_attention_o_projection_equals_gemv(dev, seqlen):
 
 
 def test_attention_rejects_bad_shapes(dev):
-    q = torch.zeros(2, 32, 1, 128, device=dev, dtype=torch.bfloat16)
-    kc = torch.zeros(2, 4, 64, 128, device=dev, dtype=torch.bfloat16)
+    q = torch.zeros(2, 32, 1, 96, device=dev, dtype=torch.bfloat16)
+    kc = torch.zeros(2, 4, 64, 96, device=dev, dtype=torch.bfloat16)
     with pytest.raises(ValueError):
         decode_gqa_attn(q, kc, kc, torch.zeros(2, device=dev, dtype=torch.int64), scale=1.0, window=None)
     q = torch.zeros(2, 34, 1, 64, device=dev, dtype=torch.bfloat16)
