@@ -106,9 +106,9 @@ def decoder_config(config: dict) -> DecoderConfig:
         raise ValueError("layer_types must name every layer")
     if not bool(config.get("use_qk_norm", True)):
         raise NotImplementedError("attention without QK-norm is not supported")
-    if int(config["head_dim"]) != 64:
+    if int(config["head_dim"]) not in (64, 128):
         raise NotImplementedError(f"head_dim {config['head_dim']}: the decode attention kernel is built "
-                                  "for head_dim 64")
+                                  "for head_dim 64 and 128")
     meta = config.get("maple_run") or {}
     return DecoderConfig(
         hidden=int(config["hidden_size"]),

@@ -598,9 +598,12 @@ struct FusedShape {
   int hidden, inter, top_k, grid, waves;
 };
 // (2048, 768, 8): 8 waves, SwiGLU 24 outputs and down 8 rows per workgroup -> 256 groups.
+// (2048, 512, 8): Maple-Preview (E = 256): 8 waves, SwiGLU 16 outputs and
+//                 down 8 rows per workgroup -> 256 groups (one per expert).
 // (256, 128, 2): 4 waves, SwiGLU 16 outputs, down 8 rows per workgroup -> 32 groups.
-constexpr FusedShape kShapes[] = {{2048, 768, 8, 256, 8}, {256, 128, 2, 32, 4}};
-static_assert(kShapes[0].grid >= kBarGroups && kShapes[1].grid >= kBarGroups, "barrier groups");
+constexpr FusedShape kShapes[] = {{2048, 768, 8, 256, 8}, {2048, 512, 8, 256, 8}, {256, 128, 2, 32, 4}};
+static_assert(kShapes[0].grid >= kBarGroups && kShapes[1].grid >= kBarGroups &&
+                  kShapes[2].grid >= kBarGroups, "barrier groups");
 
 const FusedShape* find_shape(int64_t hidden, int64_t inter, int64_t top_k) {
   for (const auto& s : kShapes)
@@ -614,15 +617,19 @@ size_t ws_bytes(int64_t, int, int64_t inter, int64_t top_k) {
 
 // The kernel instantiation a call launches (PER = 1 up to 64 experts, else 4).
 template <int ADT>
-const void* fused_kernel_t(int64_t hidden, int64_t n_experts) {
+const void* fused_kernel_t(int64_t hidden, int64_t inter, int64_t n_experts) {
+  const bool p1 = n_experts <= 64;
+  if (hidden == 2048 && inter == 768)
+    return p1 ? reinterpret_cast<const void*>(&k_moe_fused<4, 32, 3, 3, 16, 2, 8, 1, 8, ADT>)
+              : reinterpret_cast<const void*>(&k_moe_fused<4, 32, 3, 3, 16, 2, 8, 4, 8, ADT>);
   if (hidden == 2048)
-    return n_experts <= 64 ? reinterpret_cast<const void*>(&k_moe_fused<4, 32, 3, 3, 16, 2, 8, 1, 8, ADT>)
-                           : reinterpret_cast<const void*>(&k_moe_fused<4, 32, 3, 3, 16, 2, 8, 4, 8, ADT>);
+    return p1 ? reinterpret_cast<const void*>(&k_moe_fused<4, 32, 2, 2, 16, 2, 8, 1, 8, ADT>)
+              : reinterpret_cast<const void*>(&k_moe_fused<4, 32, 2, 2, 16, 2, 8, 4, 8, ADT>);
   return reinterpret_cast<const void*>(&k_moe_fused<1, 16, 2, 1, 8, 1, 2, 1, 4, ADT>);
 }
-const void* fused_kernel(int64_t hidden, int64_t n_experts, int alpha_dtype) {
-  return alpha_dtype == MA_F32 ? fused_kernel_t<MA_F32>(hidden, n_experts)
-                               : fused_kernel_t<MA_BF16>(hidden, n_experts);
+const void* fused_kernel(int64_t hidden, int64_t inter, int64_t n_experts, int alpha_dtype) {
+  return alpha_dtype == MA_F32 ? fused_kernel_t<MA_F32>(hidden, inter, n_experts)
+                               : fused_kernel_t<MA_BF16>(hidden, inter, n_experts);
 }
 
 }  // namespace
@@ -635,7 +642,7 @@ extern "C" int ma_moe_fused_resident(int64_t n_experts, int64_t hidden, int64_t 
   const FusedShape* s = find_shape(hidden, inter, top_k);
   if (!s || !needed || !capacity) return fail(MA_EVALUE, "moe_fused_resident: shape not built");
   *needed = s->grid;
-  return resident_capacity(fused_kernel(hidden, n_experts, MA_BF16), 64 * s->waves, capacity);
+  return resident_capacity(fused_kernel(hidden, inter, n_experts, MA_BF16), 64 * s->waves, capacity);
 }
 
 extern "C" size_t ma_moe_fused_workspace_bytes(int64_t n_experts, int64_t hidden, int64_t inter,
@@ -686,11 +693,11 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
       return fail(MA_EVALUE, "moe_fused: next projection weights, rms weight and y must be 16-byte aligned");
   }
   int64_t capacity = 0;
-  if (int rc = resident_capacity(fused_kernel(hidden, n_experts, alpha_dtype), 64 * s->waves, &capacity)) return rc;
+  if (int rc = resident_capacity(fused_kernel(hidden, inter, n_experts, alpha_dtype), 64 * s->waves, &capacity))
+    return rc;
   if (capacity < s->grid)
     return fail(MA_ERUNTIME, "moe_fused: its %d workgroups wait on each other but the device holds %lld at once",
                 s->grid, static_cast<long long>(capacity));
-  const int per = n_experts <= 64 ? 1 : 4;
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define MA_FUSED_ARGS                                                                            \
   static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(x_add), norm_weight, norm_dtype, \
@@ -701,12 +708,18 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
       next_w, next_alpha, next_rms, next_eps, static_cast<int>(next_rows),                        \
       static_cast<uint16_t*>(next_out)
   const dim3 grid(s->grid), block(64 * s->waves);
+  const int per = n_experts <= 64 ? 1 : 4;
 #define MA_FUSED_LAUNCH(ADT)                                                                      \
-  if (hidden == 2048) {                                                                          \
+  if (hidden == 2048 && inter == 768) {                                                          \
     if (per == 1)                                                                                \
       hipLaunchKernelGGL((k_moe_fused<4, 32, 3, 3, 16, 2, 8, 1, 8, ADT>), grid, block, 0, st, MA_FUSED_ARGS); \
     else                                                                                         \
       hipLaunchKernelGGL((k_moe_fused<4, 32, 3, 3, 16, 2, 8, 4, 8, ADT>), grid, block, 0, st, MA_FUSED_ARGS); \
+  } else if (hidden == 2048) {                                                                   \
+    if (per == 1)                                                                                \
+      hipLaunchKernelGGL((k_moe_fused<4, 32, 2, 2, 16, 2, 8, 1, 8, ADT>), grid, block, 0, st, MA_FUSED_ARGS); \
+    else                                                                                         \
+      hipLaunchKernelGGL((k_moe_fused<4, 32, 2, 2, 16, 2, 8, 4, 8, ADT>), grid, block, 0, st, MA_FUSED_ARGS); \
   } else {                                                                                       \
     hipLaunchKernelGGL((k_moe_fused<1, 16, 2, 1, 8, 1, 2, 1, 4, ADT>), grid, block, 0, st, MA_FUSED_ARGS); \
   }

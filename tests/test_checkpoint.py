@@ -117,8 +117,30 @@ def test_unconverted_and_unsupported_configs_are_refused(saved, tmp_path):
     with pytest.raises(NotImplementedError):
         checkpoint.decoder_config(dict(config, use_qk_norm=False))
     with pytest.raises(NotImplementedError):
-        checkpoint.decoder_config(dict(config, head_dim=128))
+        checkpoint.decoder_config(dict(config, head_dim=96))
     # the reference's layer pattern: sliding layers with a window, NoPE global layers
     cfg = checkpoint.decoder_config(dict(config, layer_types=["sliding_attention", "full_attention"],
                                          sliding_window=64, nope_on_global_attention=True))
     assert cfg.layer_attention(0) == (64, True) and cfg.layer_attention(1) == (None, False)
+
+
+def test_maple_preview_config_maps_to_the_kernels(saved):
+    """Maple-Preview's shapes (docs/HANDOFF.md:190-199 of the reference): 24
+    layers, hidden 2048, 16 query / 4 KV heads of 128, 256 experts top-8 with
+    intermediate 512, vocab 151936, layer_types 3 sliding (window 512) : 1
+    full, NoPE on the full layers, RTN group 64 when the converter names none."""
+    _, d = saved
+    config = json.loads((d / "config.json").read_text())
+    meta = dict(config["maple_run"])
+    meta.pop("rtn_4bit")
+    maple = dict(config, hidden_size=2048, num_hidden_layers=24, num_attention_heads=16,
+                 num_key_value_heads=4, head_dim=128, num_experts=256, num_experts_per_tok=8,
+                 moe_intermediate_size=512, vocab_size=151936, partial_rotary_factor=0.5,
+                 layer_types=["sliding_attention"] * 3 + ["full_attention"], sliding_window=512,
+                 nope_on_global_attention=True, maple_run=meta)
+    maple["layer_types"] = maple["layer_types"] * 6
+    cfg = checkpoint.decoder_config(maple)
+    assert (cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.qkv_rows) == (2048, 16, 4, 128, 3072)
+    assert (cfg.experts, cfg.inter, cfg.top_k, cfg.rtn_group, cfg.rotary_dim) == (256, 512, 8, 64, 64)
+    assert [cfg.layer_attention(i) for i in range(4)] == [(512, True)] * 3 + [(None, False)]
+    assert cfg.layer_attention(23) == (None, False) and cfg.layer_attention(22) == (512, True)
