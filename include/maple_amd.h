@@ -435,6 +435,48 @@ int ma_decode_attn_o_supported(int64_t batch, int n_heads, int n_kv_heads, int h
 int ma_argmax_rows(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t ldx,
                    int64_t* out, void* stream);
 
+/*
+ * GEMV over the rows of selected clusters: packed [n_clusters, cluster_size,
+ * nwords] (the head's rows grouped by cluster), scales / biases [n_clusters,
+ * cluster_size, groups] (bf16 or float32, one dtype), cluster_ids int32
+ * [n_probes]; y[b, p * cluster_size + m] = row m of cluster cluster_ids[p]
+ * dotted with x[b] -- the value ma_rtn4_gemv gives for that row, bit for bit.
+ * x bf16 with 16-byte aligned rows; ids outside [0, n_clusters) are clamped.
+ * Replaces rtn4_indexed_gemv, src/maple_run/kernels/rtn4.py:418-611.
+ */
+int ma_rtn4_indexed_gemv(const void* x, int x_dtype, int64_t batch, int64_t ldx,
+                         const uint32_t* packed, int64_t n_clusters, int64_t cluster_size,
+                         int64_t nwords, const void* scales, int scales_dtype, const void* biases,
+                         int biases_dtype, int64_t group_size, const int32_t* cluster_ids,
+                         int64_t n_probes, void* y, int64_t ldy, void* stream);
+
+/* Workspace bytes of ma_flash_head (256-byte aligned): the centroid scores
+ * and, when cluster_ids is NULL, the selected ids. */
+size_t ma_flash_head_workspace_bytes(int64_t n_clusters, int64_t n_probes);
+
+/*
+ * FlashHead for one token x (bf16 [nwords * 8]): scores = the RTN4 GEMV of
+ * the n_clusters centroid rows (bf16, as ma_rtn4_gemv stores them); the
+ * n_probes highest-scoring clusters (equal scores: the lower cluster index;
+ * written to cluster_ids in ascending order when it is not NULL); logits
+ * (bf16 [vocab]) = -inf, then for every token of a probed cluster its exact
+ * head logit at token_map[c * cluster_size + m] (head = the lm_head rows
+ * permuted by token_map, [n_clusters, cluster_size, nwords]), and the n_force
+ * forced tokens' exact logits (their own rows, force_ids int32).  The exact
+ * logits are ma_rtn4_gemv's values bit for bit.  Four launches, no
+ * allocation; n_clusters <= 8192.  Replaces FlashHead.__call__,
+ * src/maple_run/flash_head.py:334-370 (centroid rtn4_gemv, torch.topk,
+ * rtn4_indexed_gemv, the force rows, fill + index_put).
+ */
+int ma_flash_head(const void* x, const uint32_t* centroids, const void* c_scales,
+                  const void* c_biases, int c_dtype, int64_t n_clusters, int64_t c_group,
+                  const uint32_t* head, const void* h_scales, const void* h_biases, int h_dtype,
+                  int64_t cluster_size, int64_t h_group, const int32_t* token_map,
+                  int64_t n_probes, const uint32_t* force_w, const void* force_scales,
+                  const void* force_biases, const int32_t* force_ids, int64_t n_force,
+                  int64_t nwords, int64_t vocab, void* logits, int32_t* cluster_ids,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes ma_fused_sample needs for rows x vocab at top_k (0 for bad
  * sizes).  Replaces sampler_workspace / batched_sampler_workspace,
  * src/maple_run/kernels/sampler.py:202-232. */

@@ -67,6 +67,10 @@ _SIGNATURES = {
     "ma_moe_grouped_noalloc_max_bytes": [],
     "ma_sampler_workspace_bytes": [_L, _L, _I],
     "ma_fused_sample": [_P, _I, _L, _L, _L, _P, _I, _F, _F, _P, _Z, _P, _P],
+    "ma_rtn4_indexed_gemv": [_P, _I, _L, _L, _P, _L, _L, _L, _P, _I, _P, _I, _L, _P, _L, _P, _L, _P],
+    "ma_flash_head_workspace_bytes": [_L, _L],
+    "ma_flash_head": [_P, _P, _P, _P, _I, _L, _L, _P, _P, _P, _I, _L, _L, _P, _L, _P, _P, _P, _P, _L, _L,
+                      _L, _P, _P, _P, _Z, _P],
     "ma_moe_grouped_noalloc": [_P, _L, _P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _L, _L, _P, _P, _P, _P,
                                _P, _I, _P, _L, _P, _P],
 }
@@ -74,7 +78,8 @@ _RESTYPES = {"ma_last_error": ctypes.c_char_p, "ma_router_workspace_bytes": _Z,
              "ma_ternary_gemv_workspace_bytes": _Z,
              "ma_grouped_workspace_bytes": _Z, "ma_gqa_workspace_bytes": _Z,
              "ma_moe_fused_workspace_bytes": _Z, "ma_moe_route_workspace_bytes": _Z,
-             "ma_moe_grouped_noalloc_max_bytes": _Z, "ma_sampler_workspace_bytes": _Z}
+             "ma_moe_grouped_noalloc_max_bytes": _Z, "ma_sampler_workspace_bytes": _Z,
+             "ma_flash_head_workspace_bytes": _Z}
 
 _lib = None
 

@@ -25,9 +25,12 @@ scales,biases}`` (4-bit RTN), ``model.norm.weight``.
 
 Layers are ``full_attention`` or ``sliding_attention`` (the last
 ``sliding_window`` positions), full-attention layers without RoPE when
-``nope_on_global_attention`` is set, all with QK-norm, head_dim 64 (the decode
-attention kernel's); other configs raise ``NotImplementedError`` instead of
-decoding wrongly.
+``nope_on_global_attention`` is set, all with QK-norm, head_dim 64 or 128
+(the decode attention kernel's); other configs raise ``NotImplementedError``
+instead of decoding wrongly.  With ``flash_head=True`` the ``lm_head_flash.*``
+tensors (``model-flashhead.safetensors``) and the ``flash_head`` metadata
+build a FlashHead for batch-1 decode (``model.py:750-770``,
+``flash_head.py:373-463``).
 """
 
 from __future__ import annotations
@@ -58,9 +61,9 @@ def as_uint32(t: torch.Tensor) -> torch.Tensor:
     return t if t.dtype == torch.uint32 else t.view(torch.uint32)
 
 
-def read_weights(model_dir, device) -> tuple[dict, dict]:
+def read_weights(model_dir, device, flash_head: bool = False) -> tuple[dict, dict]:
     """``(config, {name: tensor})`` of a checkpoint directory, tensors on
-    ``device``; FlashHead tensors are skipped."""
+    ``device``; FlashHead tensors only when ``flash_head``."""
     from safetensors.torch import load_file
 
     model_dir = Path(model_dir).expanduser()
@@ -72,11 +75,14 @@ def read_weights(model_dir, device) -> tuple[dict, dict]:
     else:
         shards = sorted(p.name for p in model_dir.glob("*.safetensors"))
     weights: dict[str, torch.Tensor] = {}
+    flash_shard = model_dir / "model-flashhead.safetensors"
+    if flash_head and flash_shard.exists() and flash_shard.name not in shards:
+        shards.append(flash_shard.name)
     for name in shards:
-        if name == "model-flashhead.safetensors":
+        if name == flash_shard.name and not flash_head:
             continue
         shard = load_file(str(model_dir / name), device=str(device))
-        weights.update({k: v for k, v in shard.items() if not k.startswith("lm_head_flash.")})
+        weights.update({k: v for k, v in shard.items() if flash_head or not k.startswith("lm_head_flash.")})
     return config, weights
 
 
@@ -130,11 +136,13 @@ def decoder_config(config: dict) -> DecoderConfig:
     )
 
 
-def load_decoder(model_dir, device="cuda", max_len: int = 4096 + 128, **flags) -> SyntheticDecoder:
+def load_decoder(model_dir, device="cuda", max_len: int = 4096 + 128, flash_head: bool = False,
+                 **flags) -> SyntheticDecoder:
     """A decoder on the HIP kernels with a checkpoint's weights (``flags``:
-    the ``SyntheticDecoder`` launch options)."""
+    the ``SyntheticDecoder`` launch options; ``flash_head``: decode batch 1
+    through the checkpoint's FlashHead)."""
     device = torch.device(device)
-    config, w = read_weights(model_dir, device)
+    config, w = read_weights(model_dir, device, flash_head)
     cfg = decoder_config(config)
     # model.py:728-748: float32 router rows and RTN scales/biases go to bf16;
     # row_alpha keeps the dtype it was written in (float32 from the converter)
@@ -169,8 +177,13 @@ def load_decoder(model_dir, device="cuda", max_len: int = 4096 + 128, **flags) -
     embed = rtn("model.word_embeddings")
     lm_head = rtn("lm_head")
     final_norm = f32(w.pop("model.norm.weight"))
-    return SyntheticDecoder.from_weights(cfg, device, layers, embed, lm_head, final_norm,
-                                         max_len=max_len, **flags)
+    model = SyntheticDecoder.from_weights(cfg, device, layers, embed, lm_head, final_norm,
+                                          max_len=max_len, **flags)
+    if flash_head:
+        from .flash_head import build_flash_head
+
+        model.flash_head = build_flash_head(config=config, lm_head=lm_head, weights=w, device=device)
+    return model
 
 
 def save_decoder(model, model_dir) -> None:

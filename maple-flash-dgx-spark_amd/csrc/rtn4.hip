@@ -36,12 +36,20 @@ __device__ __forceinline__ void load_words_r(const uint32_t* __restrict__ p, uin
   }
 }
 
-template <int KW, int LPR, int BT, int U, int SDT>
+// Rows: output row r reads weight row r; with MAP, weight row src(r) =
+// cid[r / cs] * cs + r % cs (cid NULL: src = r), clamped to [0, n_src), and
+// the output goes to y[out_idx[src]] (out_idx NULL: y[r]), clamped to
+// [0, n_dst) -- the FlashHead gathers and scatters; no index read from
+// memory can send an access outside the buffers.  The per-row arithmetic is
+// the same either way.
+template <int KW, int LPR, int BT, int U, int SDT, bool MAP = false>
 __global__ __launch_bounds__(64) void k_rtn4_fast(
     const uint16_t* __restrict__ x, int64_t batch, int64_t ldx,
     const uint32_t* __restrict__ w, int64_t n_out, int64_t n_groups, int64_t gw,
     const void* __restrict__ scales, const void* __restrict__ biases,
-    uint16_t* __restrict__ y, int64_t ldy) {
+    uint16_t* __restrict__ y, int64_t ldy, const int32_t* __restrict__ cid = nullptr,
+    int64_t cs = 1, const int32_t* __restrict__ out_idx = nullptr, int64_t n_src = 1,
+    int64_t n_dst = 1) {
   constexpr int NW = KW * LPR;
   constexpr int RPI = 64 / LPR;
   const int lane = threadIdx.x & 63;
@@ -52,10 +60,20 @@ __global__ __launch_bounds__(64) void k_rtn4_fast(
 
   uint32_t wv[U][KW];
   float sc[U], bi[U];
+  int64_t src[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     int64_t r = r0 + u * RPI + sub;
     r = r < n_out ? r : n_out - 1;
+    if constexpr (MAP) {
+      r = cid ? static_cast<int64_t>(cid[r / cs]) * cs + r % cs : r;
+      r = r < 0 ? 0 : (r >= n_src ? n_src - 1 : r);
+    }
+    src[u] = r;
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t r = src[u];
     load_words_r<KW>(w + r * NW + kl * KW, wv[u]);
     sc[u] = ld_t<SDT>(scales, r * n_groups + g);
     bi[u] = ld_t<SDT>(biases, r * n_groups + g);
@@ -114,7 +132,12 @@ __global__ __launch_bounds__(64) void k_rtn4_fast(
       const float part = sc[u] * ((acc[bt][0] + acc[bt][1]) - 16.f * xsum[bt]) + bi[u] * xsum[bt];
       const float v = group_sum<LPR>(part);
       const int64_t b = b0 + bt;
-      if (kl == 0 && r < n_out && b < batch) y[b * ldy + r] = f32_to_bf16(v);
+      int64_t o = r;
+      if constexpr (MAP) {
+        o = out_idx ? static_cast<int64_t>(out_idx[src[u]]) : r;
+        o = o < 0 ? 0 : (o >= n_dst ? n_dst - 1 : o);
+      }
+      if (kl == 0 && r < n_out && b < batch) y[b * ldy + o] = f32_to_bf16(v);
     }
   }
 }
@@ -199,6 +222,179 @@ static bool rtn4_fast_launch(const void* x, int64_t batch, int64_t ldx, const ui
   return false;
 }
 
+// The same GEMV over mapped rows (batch rows on the grid's y, one at a time):
+// MA_EVALUE-free launcher; false when no fast shape fits.
+static bool rtn4_rows_launch(const void* x, int64_t batch, int64_t ldx, const uint32_t* w,
+                             int64_t n_out, int64_t nwords, const void* sc, const void* bs, int s_dt,
+                             int64_t group, void* y, int64_t ldy, const int32_t* cid, int64_t cs,
+                             const int32_t* out_idx, int64_t n_src, int64_t n_dst, hipStream_t s) {
+  const int64_t gw = group / 8;
+  const int64_t n_groups = nwords / gw;
+#define MA_RTN4_MAP(L, K)                                                                        \
+  if (nwords == (L) * (K) && gw % (K) == 0) {                                                    \
+    constexpr int U = 4;                                                                         \
+    dim3 grid(static_cast<unsigned>(cdiv(n_out, (64 / L) * U)), static_cast<unsigned>(batch));   \
+    if (s_dt == MA_BF16)                                                                         \
+      hipLaunchKernelGGL((k_rtn4_fast<K, L, 1, U, MA_BF16, true>), grid, dim3(64), 0, s,         \
+                         static_cast<const uint16_t*>(x), batch, ldx, w, n_out, n_groups, gw, sc, \
+                         bs, static_cast<uint16_t*>(y), ldy, cid, cs, out_idx, n_src, n_dst);     \
+    else                                                                                         \
+      hipLaunchKernelGGL((k_rtn4_fast<K, L, 1, U, MA_F32, true>), grid, dim3(64), 0, s,          \
+                         static_cast<const uint16_t*>(x), batch, ldx, w, n_out, n_groups, gw, sc, \
+                         bs, static_cast<uint16_t*>(y), ldy, cid, cs, out_idx, n_src, n_dst);     \
+    return true;                                                                                 \
+  }
+  MA_RTN4_MAP(32, 8)
+  MA_RTN4_MAP(32, 4)
+  MA_RTN4_MAP(32, 2)
+  MA_RTN4_MAP(16, 4)
+  MA_RTN4_MAP(16, 2)
+  MA_RTN4_MAP(8, 2)
+#undef MA_RTN4_MAP
+  return false;
+}
+
+// ---------------------------------------------------------------------------
+// FlashHead cluster selection (reference flash_head.py:345-351: torch.topk of
+// the centroid scores): the n_probes largest of n_clusters bf16 scores, equal
+// scores at the lower cluster index, written as ascending cluster ids.  One
+// 1024-thread workgroup: a radix select of the n_probes-th largest
+// order-preserving key (four 8-bit digit passes over per-wave LDS
+// histograms), then the ids in index order (keys above it, and the lowest
+// indices among the keys equal to it).  Workgroups 1 .. fill the full
+// vocabulary row of logits with -inf meanwhile.
+constexpr int kSelThreads = 1024;
+constexpr int kSelPer = 8;  // up to 8192 clusters
+constexpr int kSelWaves = kSelThreads / 64;
+
+__device__ __forceinline__ uint32_t score_key(uint16_t b) {
+  const uint32_t f = static_cast<uint32_t>(b) << 16;
+  return (f & 0x80000000u) ? ~f : (f | 0x80000000u);
+}
+
+// Exclusive prefix over the workgroup of per-thread counts (thread order);
+// *total gets the sum.  Uses sh[kSelWaves + 1].
+__device__ __forceinline__ int block_excl_scan(int v, int* sh, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  int inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += u;
+  }
+  if (lane == 63) sh[wv] = inc;
+  __syncthreads();
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    base += w < wv ? sh[w] : 0;
+    tot += sh[w];
+  }
+  __syncthreads();
+  *total = tot;
+  return base + inc - v;
+}
+
+__global__ __launch_bounds__(kSelThreads) void k_flash_select(const uint16_t* __restrict__ scores,
+                                                              int n, int k, int32_t* __restrict__ ids,
+                                                              uint16_t* __restrict__ full, int64_t vocab) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (blockIdx.x > 0) {  // fill: 8 bf16 of -inf per thread
+    const int64_t i = (static_cast<int64_t>(blockIdx.x - 1) * kSelThreads + tid) * 8;
+    if (i + 8 <= vocab) {
+      *reinterpret_cast<uint4*>(full + i) = make_uint4(0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u);
+    } else {
+      for (int64_t j = i; j < vocab; ++j) full[j] = 0xff80u;
+    }
+    return;
+  }
+  __shared__ int hist[kSelWaves][256];
+  __shared__ int tot[256];
+  __shared__ int sh[kSelWaves + 1];
+  __shared__ uint32_t s_prefix;
+  __shared__ int s_need;
+  uint32_t key[kSelPer];
+#pragma unroll
+  for (int j = 0; j < kSelPer; ++j) {
+    const int i = tid + kSelThreads * j;
+    key[j] = i < n ? score_key(scores[i]) : 0u;  // 0: below every score (-inf has key 0x007fffff)
+  }
+  uint32_t prefix = 0, mask = 0;
+  int need = k;  // how many of the keys matching the prefix are still to take
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int i = tid; i < kSelWaves * 256; i += kSelThreads) (&hist[0][0])[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kSelPer; ++j)
+      if (tid + kSelThreads * j < n && (key[j] & mask) == prefix) atomicAdd(&hist[wv][(key[j] >> shift) & 255u], 1);
+    __syncthreads();
+    if (tid < 256) {
+      int c = 0;
+#pragma unroll
+      for (int w = 0; w < kSelWaves; ++w) c += hist[w][tid];
+      tot[tid] = c;
+    }
+    __syncthreads();
+    if (wv == 0) {
+      // lane l holds digits 4l .. 4l+3; count above digit d = suffix sums
+      int c4[4], own = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        c4[q] = tot[4 * lane + q];
+        own += c4[q];
+      }
+      int suf = own;  // inclusive suffix over lanes >= lane
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int u = __shfl_down(suf, off, 64);
+        if (lane + off < 64) suf += u;
+      }
+      const int above_lane = suf - own;  // keys with digits in lanes > lane
+      // the digit d with above(d) < need <= above(d) + count(d)
+      int hit_d = -1, hit_above = 0;
+      int above = above_lane;
+#pragma unroll
+      for (int q = 3; q >= 0; --q) {
+        if (hit_d < 0 && above < need && need <= above + c4[q]) {
+          hit_d = 4 * lane + q;
+          hit_above = above;
+        }
+        above += c4[q];
+      }
+      const uint64_t hb = __ballot(hit_d >= 0);
+      const int src = hb ? __builtin_ctzll(hb) : 0;
+      const int d = __shfl(hit_d, src, 64), a = __shfl(hit_above, src, 64);
+      if (lane == 0) {
+        s_prefix = prefix | (static_cast<uint32_t>(d < 0 ? 0 : d) << shift);
+        s_need = need - a;
+      }
+    }
+    __syncthreads();
+    prefix = s_prefix;
+    need = s_need;
+    mask |= 255u << shift;
+    __syncthreads();
+  }
+  // prefix is the k-th largest key; take every key above it and the lowest
+  // `need` indices equal to it, in index order (index i = tid + 1024 j)
+  int ties_before = 0, out_base = 0;
+#pragma unroll
+  for (int j = 0; j < kSelPer; ++j) {
+    const int i = tid + kSelThreads * j;
+    const bool valid = i < n;
+    const bool tie = valid && key[j] == prefix;
+    int tie_total;
+    const int tie_rank = ties_before + block_excl_scan(tie ? 1 : 0, sh, &tie_total);
+    const bool take = valid && (key[j] > prefix || (tie && tie_rank < need));
+    int take_total;
+    const int pos = out_base + block_excl_scan(take ? 1 : 0, sh, &take_total);
+    if (take && pos < k) ids[pos] = i;
+    ties_before += tie_total;
+    out_base += take_total;
+  }
+}
+
 }  // namespace ma
 
 using namespace ma;
@@ -255,4 +451,87 @@ extern "C" int ma_rtn4_embedding(const void* ids, int ids_is_int64, int64_t n_id
                      static_cast<hipStream_t>(stream), ids, ids_is_int64, vocab, packed, nwords,
                      scales, scales_dtype, biases, biases_dtype, group_size, out);
   return check_launch("rtn4_embedding");
+}
+
+extern "C" int ma_rtn4_indexed_gemv(const void* x, int x_dtype, int64_t batch, int64_t ldx,
+                                    const uint32_t* packed, int64_t n_clusters, int64_t cluster_size,
+                                    int64_t nwords, const void* scales, int scales_dtype,
+                                    const void* biases, int biases_dtype, int64_t group_size,
+                                    const int32_t* cluster_ids, int64_t n_probes, void* y, int64_t ldy,
+                                    void* stream) {
+  if (batch < 0 || n_clusters < 1 || cluster_size < 1 || n_probes < 0 || nwords < 1 ||
+      group_size < 8 || group_size % 8 || (nwords * 8) % group_size || ldy < n_probes * cluster_size)
+    return fail(MA_EVALUE, "rtn4_indexed_gemv: bad sizes");
+  if (x_dtype != MA_BF16 || scales_dtype != biases_dtype || (scales_dtype != MA_BF16 && scales_dtype != MA_F32))
+    return fail(MA_ETYPE, "rtn4_indexed_gemv: needs bf16 x and bf16 or float32 scales/biases of one dtype");
+  if ((ldx % 8) || ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(packed)) & 15u))
+    return fail(MA_EVALUE, "rtn4_indexed_gemv: x rows and codes must be 16-byte aligned");
+  if (batch == 0 || n_probes == 0) return MA_OK;
+  if (!rtn4_rows_launch(x, batch, ldx, packed, n_probes * cluster_size, nwords, scales, biases,
+                        scales_dtype, group_size, y, ldy, cluster_ids, cluster_size, nullptr,
+                        n_clusters * cluster_size, n_probes * cluster_size, static_cast<hipStream_t>(stream)))
+    return fail(MA_EVALUE, "rtn4_indexed_gemv: %lld words per row with group %lld not built",
+                (long long)nwords, (long long)group_size);
+  return check_launch("rtn4_indexed_gemv");
+}
+
+extern "C" size_t ma_flash_head_workspace_bytes(int64_t n_clusters, int64_t n_probes) {
+  if (n_clusters < 1 || n_probes < 1) return 0;
+  return ((static_cast<size_t>(n_clusters) * 2 + 255) / 256) * 256 + static_cast<size_t>(n_probes) * 4;
+}
+
+extern "C" int ma_flash_head(const void* x, const uint32_t* centroids, const void* c_scales,
+                             const void* c_biases, int c_dtype, int64_t n_clusters, int64_t c_group,
+                             const uint32_t* head, const void* h_scales, const void* h_biases,
+                             int h_dtype, int64_t cluster_size, int64_t h_group,
+                             const int32_t* token_map, int64_t n_probes, const uint32_t* force_w,
+                             const void* force_scales, const void* force_biases,
+                             const int32_t* force_ids, int64_t n_force, int64_t nwords, int64_t vocab,
+                             void* logits, int32_t* cluster_ids, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  const char* what = "flash_head";
+  if (n_clusters < 1 || cluster_size < 1 || n_probes < 1 || n_probes > n_clusters ||
+      n_clusters > static_cast<int64_t>(kSelThreads) * kSelPer || nwords < 1 || vocab < 1 || n_force < 0)
+    return fail(MA_EVALUE, "%s: bad sizes (n_probes %lld of %lld clusters, at most %d clusters)", what,
+                (long long)n_probes, (long long)n_clusters, kSelThreads * kSelPer);
+  for (int64_t gsz : {c_group, h_group})
+    if (gsz < 8 || gsz % 8 || (nwords * 8) % gsz) return fail(MA_EVALUE, "%s: bad group size %lld", what, (long long)gsz);
+  if ((c_dtype != MA_BF16 && c_dtype != MA_F32) || (h_dtype != MA_BF16 && h_dtype != MA_F32))
+    return fail(MA_ETYPE, "%s: scales/biases must be bf16 or float32", what);
+  if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(centroids) |
+        reinterpret_cast<uintptr_t>(head) | reinterpret_cast<uintptr_t>(logits) |
+        (force_w ? reinterpret_cast<uintptr_t>(force_w) : 0)) & 15u))
+    return fail(MA_EVALUE, "%s: x, codes and logits must be 16-byte aligned", what);
+  if (n_force > 0 && (!force_w || !force_scales || !force_biases || !force_ids))
+    return fail(MA_EVALUE, "%s: force rows missing", what);
+  if (!workspace || workspace_bytes < ma_flash_head_workspace_bytes(n_clusters, n_probes) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 255u))
+    return fail(MA_EVALUE, "%s: workspace too small or not 256-byte aligned", what);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint16_t* scores = static_cast<uint16_t*>(workspace);
+  int32_t* ids = cluster_ids ? cluster_ids
+                             : reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
+                                                          ((n_clusters * 2 + 255) / 256) * 256);
+  // 1. centroid scores (the exact head's GEMV on the centroid rows), bf16
+  if (!rtn4_fast_launch<1>(x, 1, nwords * 8, centroids, n_clusters, nwords, c_scales, c_biases, c_dtype,
+                           c_group, scores, n_clusters, s))
+    return fail(MA_EVALUE, "%s: %lld words per row with group %lld not built", what, (long long)nwords,
+                (long long)c_group);
+  // 2. the probed clusters; the rest of the grid fills the logits with -inf
+  const unsigned fill = static_cast<unsigned>(cdiv(vocab, static_cast<int64_t>(kSelThreads) * 8));
+  hipLaunchKernelGGL(k_flash_select, dim3(1 + fill), dim3(kSelThreads), 0, s, scores,
+                     static_cast<int>(n_clusters), static_cast<int>(n_probes), ids,
+                     static_cast<uint16_t*>(logits), vocab);
+  // 3. exact logits of the probed clusters' tokens, scattered through token_map
+  if (!rtn4_rows_launch(x, 1, nwords * 8, head, n_probes * cluster_size, nwords, h_scales, h_biases,
+                        h_dtype, h_group, logits, vocab, ids, cluster_size, token_map,
+                        n_clusters * cluster_size, vocab, s))
+    return fail(MA_EVALUE, "%s: %lld words per row with group %lld not built", what, (long long)nwords,
+                (long long)h_group);
+  // 4. forced tokens (EOS and the like) from their own rows of the head
+  if (n_force > 0 &&
+      !rtn4_rows_launch(x, 1, nwords * 8, force_w, n_force, nwords, force_scales, force_biases, h_dtype,
+                        h_group, logits, vocab, nullptr, 1, force_ids, n_force, vocab, s))
+    return fail(MA_EVALUE, "%s: force rows not built", what);
+  return check_launch(what);
 }

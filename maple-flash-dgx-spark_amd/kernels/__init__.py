@@ -14,7 +14,7 @@ from .dispatch import moe_dispatch
 from .fused_norm import add_rms_norm, moe_reduce_add, rms_norm
 from .greedy import greedy_argmax
 from .router import router_topk
-from .rtn4 import rtn4_embedding, rtn4_gemv
+from .rtn4 import rtn4_embedding, rtn4_gemv, rtn4_indexed_gemv
 from .ternary_expert import ternary_expert_down_sum, ternary_expert_gemv, ternary_expert_swiglu
 from .ternary_gemv import ternary_gemv
 
@@ -27,6 +27,7 @@ __all__ = [
     "moe_dispatch",
     "rtn4_gemv",
     "rtn4_embedding",
+    "rtn4_indexed_gemv",
     "rms_norm",
     "add_rms_norm",
     "moe_reduce_add",

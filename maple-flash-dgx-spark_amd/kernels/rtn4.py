@@ -1,7 +1,8 @@
 """4-bit RTN embedding lookup and GEMV (lm_head / embeddings).
 
 Drop-ins for reference ``src/maple_run/kernels/rtn4.py``: ``rtn4_embedding``
-(:27-47) and ``rtn4_gemv`` (:285-415).  Dequant is ``code * scale + bias`` per
+(:27-47), ``rtn4_gemv`` (:285-415) and ``rtn4_indexed_gemv`` (:418-611, the
+FlashHead probe GEMV).  Dequant is ``code * scale + bias`` per
 group, 8 LSB-first codes per uint32.  Unlike the reference, every batch size
 works with group 64 and 128 (the reference rejects group 128 above batch 16,
 ``rtn4.py:79-81,349-353``).
@@ -105,3 +106,50 @@ def rtn4_gemv(
         int(group_size), _lib.ptr(y), n_out, _lib.stream_of(x),
     )
     return y.reshape(*leading, n_out)
+
+
+def rtn4_indexed_gemv(
+    x: torch.Tensor,
+    packed_weight: torch.Tensor,
+    scales: torch.Tensor,
+    biases: torch.Tensor,
+    cluster_ids: torch.Tensor,
+    group_size: int = HEAD_GROUP_SIZE,
+) -> torch.Tensor:
+    """GEMV over the rows of the probed clusters: ``packed_weight`` is
+    ``[n_clusters, cluster_size, nwords]`` (the head's rows grouped by
+    cluster), ``cluster_ids`` ``[n_probes]``; the output ``[..., n_probes *
+    cluster_size]`` is cluster-major, so entry ``p * cluster_size + m`` is
+    row ``m`` of cluster ``cluster_ids[p]`` -- the same values ``rtn4_gemv``
+    gives for those rows."""
+    if packed_weight.dtype != torch.uint32:
+        raise TypeError(f"packed_weight must be uint32 codes, got {packed_weight.dtype}; "
+                        "refusing to run a dense-weight path.")
+    if packed_weight.ndim != 3:
+        raise ValueError("packed_weight must be 3-D [n_clusters, cluster_size, nwords]; got shape "
+                         f"{tuple(packed_weight.shape)}.")
+    if not x.is_cuda or not packed_weight.is_cuda:
+        raise RuntimeError("rtn4_indexed_gemv requires CUDA tensors.")
+    if cluster_ids.ndim != 1:
+        raise ValueError(f"cluster_ids must be 1-D [n_probes]; got shape {tuple(cluster_ids.shape)}.")
+    n_clusters, cluster_size, nwords = packed_weight.shape
+    n_groups = nwords * _CODES_PER_WORD // group_size
+    expect = (n_clusters, cluster_size, n_groups)
+    if tuple(scales.shape) != expect or tuple(biases.shape) != expect:
+        raise ValueError(f"scales/biases expected {expect}, got {tuple(scales.shape)} and {tuple(biases.shape)}.")
+    k_in = nwords * _CODES_PER_WORD
+    if x.shape[-1] != k_in:
+        raise ValueError(f"x last dim {x.shape[-1]} != packed K ({k_in}).")
+    leading = x.shape[:-1]
+    batch = int(x.numel() // k_in)
+    x_mat = x.reshape(batch, k_in).contiguous()
+    n_probes = int(cluster_ids.numel())
+    ids = cluster_ids.to(torch.int32).contiguous()
+    y = torch.empty(batch, n_probes * cluster_size, device=x.device, dtype=x.dtype)
+    sc, bs = scales.contiguous(), biases.contiguous()
+    _lib.call("ma_rtn4_indexed_gemv", _lib.ptr(x_mat), _lib.dtype_code(x_mat, "x"), batch, k_in,
+              _lib.ptr(packed_weight.contiguous()), n_clusters, cluster_size, nwords,
+              _lib.ptr(sc), _lib.dtype_code(sc, "scales"), _lib.ptr(bs), _lib.dtype_code(bs, "biases"),
+              int(group_size), _lib.ptr(ids), n_probes, _lib.ptr(y), n_probes * cluster_size,
+              _lib.stream_of(x))
+    return y.reshape(*leading, n_probes * cluster_size)

@@ -200,6 +200,7 @@ class SyntheticDecoder:
         self.embed = synthetic.rtn4_table(c.vocab, c.hidden, c.rtn_group, s + 902, dev, lo, hi)
         self.final_norm = ones(c.hidden)
         self.cos, self.sin = rope_tables(max_len, c.rotary_dim, c.rope_theta, dev)
+        self.flash_head = None
 
     @classmethod
     def from_weights(cls, cfg: DecoderConfig, device, layers: list, embed: tuple, lm_head: tuple,
@@ -215,6 +216,7 @@ class SyntheticDecoder:
         self.layers = list(layers)
         self.embed, self.lm_head, self.final_norm = embed, lm_head, final_norm
         self.cos, self.sin = rope_tables(max_len, cfg.rotary_dim, cfg.rope_theta, self.device)
+        self.flash_head = None
         return self
 
     def make_cache(self, batch: int, prefill_len: int, seed: int = 0) -> KVCache:
@@ -312,8 +314,12 @@ class SyntheticDecoder:
         return rtn4_embedding(input_ids, w, sc, bs, group_size=self.cfg.rtn_group).to(torch.bfloat16)
 
     def head(self, hidden: torch.Tensor) -> torch.Tensor:
-        """Final RMSNorm and the RTN4 lm_head: bf16 logits ``[B, vocab]``."""
+        """Final RMSNorm and the RTN4 lm_head: bf16 logits ``[B, vocab]``
+        (at batch 1 through the FlashHead when one is attached: -inf outside
+        the probed clusters and forced tokens, model.py:874-886)."""
         hidden = rms_norm(hidden, self.final_norm, self.cfg.eps)
+        if self.flash_head is not None and hidden.shape[0] == 1:
+            return self.flash_head(hidden).reshape(1, -1)
         w, sc, bs = self.lm_head
         return rtn4_gemv(hidden, w, sc, bs, group_size=self.cfg.rtn_group)
 

@@ -74,7 +74,7 @@ def test_plan_by_token_count():
 
 def test_fused_supported_rejects_unbuilt_shapes_and_dtypes():
     x = torch.zeros(1, 2048, dtype=torch.bfloat16)
-    assert not moe.fused_supported(_layer(inter=512), 8, x)  # shape not built: no device query
+    assert not moe.fused_supported(_layer(inter=640), 8, x)  # shape not built: no device query
     assert not moe.fused_supported(_layer(), 8, x.float())
 
 
