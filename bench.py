@@ -185,13 +185,15 @@ def extra_workloads(layers, dev, steps: int) -> dict:
     return out
 
 
-def decoder_tokens_per_s(dev, batch: int, steps: int, warmup: int) -> dict:
+def decoder_tokens_per_s(dev, batch: int, steps: int, warmup: int, flash: bool = False) -> dict:
     """Greedy decode of the full synthetic decoder (24 layers, hidden 2048,
     32/4 heads of 64, 64 experts top-8, RTN4 lm_head over 151936 tokens) at
     ``batch`` rows over a 4096-token KV cache, one HIP graph replay per step
     (the whole step captured by the decode-graph runner, which first checks
     8 replayed steps against 8 eager ones).  Each replay appends one position
-    per row and feeds the chosen ids to the next step."""
+    per row and feeds the chosen ids to the next step.  ``flash``: the lm_head
+    through a FlashHead (4748 clusters of 32 tokens, 512 probed, one forced
+    token; synthetic clusters)."""
     import torch
 
     from maple_amd import workspace
@@ -201,6 +203,10 @@ def decoder_tokens_per_s(dev, batch: int, steps: int, warmup: int) -> dict:
     cfg = DecoderConfig()
     model = SyntheticDecoder(cfg, dev, seed=0, max_len=4096 + steps + warmup + 32)
     cache = model.make_cache(batch, prefill_len=4096, seed=0)
+    if flash:
+        from maple_amd.synthetic import flash_head_for
+
+        model.flash_head = flash_head_for(model.lm_head, 4748, 512, 9, dev, force=(151643,))
     gen = torch.Generator(device=dev).manual_seed(batch)
     ids = torch.randint(0, cfg.vocab, (batch,), device=dev, generator=gen)
     g = try_decode_graph(model, cache, ids, log=log)
@@ -219,6 +225,11 @@ def decoder_tokens_per_s(dev, batch: int, steps: int, warmup: int) -> dict:
     workspace.check_timeouts(dev)
     t = e0.elapsed_time(e1) * 1e-3 / steps
     nbytes = model.decode_bytes(batch, 4096 + warmup + steps // 2)
+    if flash:
+        fh, c = model.flash_head, cfg
+        row = c.hidden // 2 + 2 * (c.hidden // 64) * 2
+        head_exact = c.vocab * c.hidden // 2 + 2 * c.vocab * (c.hidden // c.rtn_group) * 2
+        nbytes += (fh.n_clusters + fh.n_probes * fh.cluster_size + fh.n_force) * row - head_exact
     out = {"tokens_per_s": round(batch / t, 1), "ms_per_step": round(t * 1e3, 4),
            "kv_len": 4096, "algorithmic_GB/s": round(nbytes / t / 1e9, 1),
            "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
@@ -478,6 +489,8 @@ def main() -> int:
     ap.add_argument("--no-decoder", action="store_true")
     ap.add_argument("--decode-batch", type=int, default=0,
                     help="only time the full decoder at this batch (for profiling runs)")
+    ap.add_argument("--flash-head", action="store_true",
+                    help="with --decode-batch 1: the lm_head through a FlashHead")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: there is no multi-GPU path "
@@ -499,7 +512,8 @@ def main() -> int:
     if args.counters_pass:
         return counters_pass(dev, args.counters_pass, L)
     if args.decode_batch > 0:
-        res = decoder_tokens_per_s(dev, args.decode_batch, max(args.steps, 10), args.warmup)
+        res = decoder_tokens_per_s(dev, args.decode_batch, max(args.steps, 10), args.warmup,
+                                   flash=args.flash_head)
         print(json.dumps({"decode": {f"bs{args.decode_batch}": res}}), flush=True)
         return 0
     log(f"building {L} cold MoE layers ...")
@@ -575,6 +589,9 @@ def main() -> int:
             log(f"timing the full decoder at batch {bsz} ...")
             out["decode"][f"bs{bsz}"] = decoder_tokens_per_s(dev, bsz, max(args.steps, 10), args.warmup)
             log(json.dumps(out["decode"][f"bs{bsz}"]))
+        log("timing the full decoder at batch 1 with the FlashHead ...")
+        out["decode"]["bs1_flash_head"] = decoder_tokens_per_s(dev, 1, max(args.steps, 10), args.warmup, flash=True)
+        log(json.dumps(out["decode"]["bs1_flash_head"]))
     if not args.no_extra:
         log("timing the other workloads ...")
         out["extra"] = extra_workloads(layers, dev, args.steps)

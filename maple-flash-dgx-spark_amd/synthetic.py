@@ -149,3 +149,32 @@ def to_numpy_u32(t: torch.Tensor):
     import numpy as np
 
     return t.view(torch.int32).cpu().numpy().view(np.uint32)
+
+
+def flash_head_for(lm_head: tuple, n_clusters: int, n_probes: int, seed: int, device, force=()):
+    """A FlashHead over ``lm_head`` with synthetic cluster data: a seeded token
+    permutation split into ``n_clusters`` equal clusters and random RTN4
+    centroid rows (group 64).  For timing the FlashHead path; real clusters
+    come from the converter's k-means."""
+    from .flash_head import FlashHead
+
+    w, sc, bs = lm_head
+    vocab, nwords = int(w.shape[0]), int(w.shape[1])
+    if vocab % n_clusters:
+        raise ValueError(f"{n_clusters} clusters do not divide the vocabulary ({vocab}).")
+    g = _gen(seed, device)
+    tm = torch.randperm(vocab, generator=g, device=device).to(torch.int32).reshape(n_clusters, -1)
+    cw, cs, cb = rtn4_table(n_clusters, nwords * 8, 64, seed + 1, device)
+    order = tm.reshape(-1).to(torch.int64)
+    fid = torch.tensor(list(force), device=device, dtype=torch.int64)
+    rows = lambda t: t.view(torch.int32).index_select(0, fid).view(torch.uint32)  # noqa: E731
+    return FlashHead(
+        centroids_weight=cw, centroids_scales=cs, centroids_biases=cb, token_map=tm,
+        head_weight=w.view(torch.int32).index_select(0, order).view(torch.uint32).reshape(n_clusters, -1, nwords),
+        head_scales=sc.index_select(0, order).reshape(n_clusters, vocab // n_clusters, -1),
+        head_biases=bs.index_select(0, order).reshape(n_clusters, vocab // n_clusters, -1),
+        force_ids=fid, force_weight=rows(w) if len(force) else None,
+        force_scales=sc.index_select(0, fid) if len(force) else None,
+        force_biases=bs.index_select(0, fid) if len(force) else None,
+        n_probes=n_probes, vocab_size=vocab, group_size=int(nwords * 8 // sc.shape[1]), device=device,
+        centroid_group_size=64)
