@@ -227,9 +227,9 @@ def decoder_tokens_per_s(dev, batch: int, steps: int, warmup: int, flash: bool =
     nbytes = model.decode_bytes(batch, 4096 + warmup + steps // 2)
     if flash:
         fh, c = model.flash_head, cfg
-        row = c.hidden // 2 + 2 * (c.hidden // 64) * 2
-        head_exact = c.vocab * c.hidden // 2 + 2 * c.vocab * (c.hidden // c.rtn_group) * 2
-        nbytes += (fh.n_clusters + fh.n_probes * fh.cluster_size + fh.n_force) * row - head_exact
+        row = lambda grp: c.hidden // 2 + 2 * (c.hidden // grp) * 2  # noqa: E731  codes + scales + biases
+        nbytes += (fh.n_clusters * row(64) + (fh.n_probes * fh.cluster_size + fh.n_force) * row(c.rtn_group)
+                   - c.vocab * row(c.rtn_group))
     out = {"tokens_per_s": round(batch / t, 1), "ms_per_step": round(t * 1e3, 4),
            "kv_len": 4096, "algorithmic_GB/s": round(nbytes / t / 1e9, 1),
            "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
