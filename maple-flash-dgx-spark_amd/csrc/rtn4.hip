@@ -258,22 +258,22 @@ static bool rtn4_rows_launch(const void* x, int64_t batch, int64_t ldx, const ui
 // FlashHead cluster selection (reference flash_head.py:345-351: torch.topk of
 // the centroid scores): the n_probes largest of n_clusters bf16 scores, equal
 // scores at the lower cluster index, written as ascending cluster ids.  One
-// 1024-thread workgroup: a radix select of the n_probes-th largest
-// order-preserving key (four 8-bit digit passes over per-wave LDS
-// histograms), then the ids in index order (keys above it, and the lowest
-// indices among the keys equal to it).  Workgroups 1 .. fill the full
+// 1024-thread workgroup, thread t holding scores 8t .. 8t+7 (one 16-byte
+// load).  A bf16 score's order-preserving key has 16 bits, so the radix
+// select of the n_probes-th largest key takes two 8-bit digit passes over
+// per-wave LDS histograms; then one workgroup scan places the keys above it
+// and one the lowest-index keys equal to it.  Workgroups 1 .. fill the full
 // vocabulary row of logits with -inf meanwhile.
 constexpr int kSelThreads = 1024;
 constexpr int kSelPer = 8;  // up to 8192 clusters
 constexpr int kSelWaves = kSelThreads / 64;
 
-__device__ __forceinline__ uint32_t score_key(uint16_t b) {
-  const uint32_t f = static_cast<uint32_t>(b) << 16;
-  return (f & 0x80000000u) ? ~f : (f | 0x80000000u);
+__device__ __forceinline__ uint32_t score_key(uint32_t b) {  // bf16 bits -> 16-bit order key
+  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
 }
 
 // Exclusive prefix over the workgroup of per-thread counts (thread order);
-// *total gets the sum.  Uses sh[kSelWaves + 1].
+// *total gets the sum.  Uses sh[kSelWaves].
 __device__ __forceinline__ int block_excl_scan(int v, int* sh, int* total) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   int inc = v;
@@ -310,24 +310,35 @@ __global__ __launch_bounds__(kSelThreads) void k_flash_select(const uint16_t* __
   }
   __shared__ int hist[kSelWaves][256];
   __shared__ int tot[256];
-  __shared__ int sh[kSelWaves + 1];
+  __shared__ int sh[kSelWaves];
   __shared__ uint32_t s_prefix;
   __shared__ int s_need;
-  uint32_t key[kSelPer];
+  uint32_t key[kSelPer];  // 16-bit order keys; indices past n are not valid
+  bool valid[kSelPer];
+  const int i0 = tid * kSelPer;
+  if (i0 + kSelPer <= n && (n & 7) == 0) {
+    const uint4 v = *reinterpret_cast<const uint4*>(scores + i0);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-  for (int j = 0; j < kSelPer; ++j) {
-    const int i = tid + kSelThreads * j;
-    key[j] = i < n ? score_key(scores[i]) : 0u;  // 0: below every score (-inf has key 0x007fffff)
+    for (int q = 0; q < 4; ++q) {
+      key[2 * q] = score_key(w[q] & 0xffffu);
+      key[2 * q + 1] = score_key(w[q] >> 16);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kSelPer; ++j) key[j] = i0 + j < n ? score_key(scores[i0 + j]) : 0u;
   }
+#pragma unroll
+  for (int j = 0; j < kSelPer; ++j) valid[j] = i0 + j < n;
   uint32_t prefix = 0, mask = 0;
-  int need = k;  // how many of the keys matching the prefix are still to take
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
+  int need = k;  // rank, from the top, of the wanted key among those matching the prefix
+  for (int pass = 0; pass < 2; ++pass) {
+    const int shift = 8 - 8 * pass;  // digits: key bits 15..8, then 7..0
     for (int i = tid; i < kSelWaves * 256; i += kSelThreads) (&hist[0][0])[i] = 0;
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < kSelPer; ++j)
-      if (tid + kSelThreads * j < n && (key[j] & mask) == prefix) atomicAdd(&hist[wv][(key[j] >> shift) & 255u], 1);
+      if (valid[j] && (key[j] & mask) == prefix) atomicAdd(&hist[wv][(key[j] >> shift) & 255u], 1);
     __syncthreads();
     if (tid < 256) {
       int c = 0;
@@ -337,7 +348,6 @@ __global__ __launch_bounds__(kSelThreads) void k_flash_select(const uint16_t* __
     }
     __syncthreads();
     if (wv == 0) {
-      // lane l holds digits 4l .. 4l+3; count above digit d = suffix sums
       int c4[4], own = 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -350,10 +360,8 @@ __global__ __launch_bounds__(kSelThreads) void k_flash_select(const uint16_t* __
         const int u = __shfl_down(suf, off, 64);
         if (lane + off < 64) suf += u;
       }
-      const int above_lane = suf - own;  // keys with digits in lanes > lane
-      // the digit d with above(d) < need <= above(d) + count(d)
-      int hit_d = -1, hit_above = 0;
-      int above = above_lane;
+      // the digit d with (count above d) < need <= (count above d) + count(d)
+      int hit_d = -1, hit_above = 0, above = suf - own;
 #pragma unroll
       for (int q = 3; q >= 0; --q) {
         if (hit_d < 0 && above < need && need <= above + c4[q]) {
@@ -374,25 +382,31 @@ __global__ __launch_bounds__(kSelThreads) void k_flash_select(const uint16_t* __
     prefix = s_prefix;
     need = s_need;
     mask |= 255u << shift;
-    __syncthreads();
   }
-  // prefix is the k-th largest key; take every key above it and the lowest
-  // `need` indices equal to it, in index order (index i = tid + 1024 j)
-  int ties_before = 0, out_base = 0;
+  // prefix is the k-th largest key: take every key above it and the lowest
+  // `need` indices equal to it, in index order
+  int ties = 0;
+#pragma unroll
+  for (int j = 0; j < kSelPer; ++j) ties += (valid[j] && key[j] == prefix) ? 1 : 0;
+  int tie_total;
+  int tie_rank = block_excl_scan(ties, sh, &tie_total);
+  bool take[kSelPer];
+  int cnt = 0;
 #pragma unroll
   for (int j = 0; j < kSelPer; ++j) {
-    const int i = tid + kSelThreads * j;
-    const bool valid = i < n;
-    const bool tie = valid && key[j] == prefix;
-    int tie_total;
-    const int tie_rank = ties_before + block_excl_scan(tie ? 1 : 0, sh, &tie_total);
-    const bool take = valid && (key[j] > prefix || (tie && tie_rank < need));
-    int take_total;
-    const int pos = out_base + block_excl_scan(take ? 1 : 0, sh, &take_total);
-    if (take && pos < k) ids[pos] = i;
-    ties_before += tie_total;
-    out_base += take_total;
+    const bool tie = valid[j] && key[j] == prefix;
+    take[j] = (valid[j] && key[j] > prefix) || (tie && tie_rank < need);
+    tie_rank += tie ? 1 : 0;
+    cnt += take[j] ? 1 : 0;
   }
+  int take_total;
+  int pos = block_excl_scan(cnt, sh, &take_total);
+#pragma unroll
+  for (int j = 0; j < kSelPer; ++j)
+    if (take[j]) {
+      if (pos < k) ids[pos] = i0 + j;
+      ++pos;
+    }
 }
 
 }  // namespace ma
