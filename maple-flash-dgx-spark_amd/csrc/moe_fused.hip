@@ -53,6 +53,17 @@ constexpr size_t kMoeWsHeader = 49152;
 static_assert(kTopC < static_cast<int>(kLogitOff / 256), "workspace lines");
 static_assert(kLogitOff + 256 * kLogitStride * 8 <= kMoeWsHeader, "workspace logits");
 
+// The expert of top-k slot s: with BALLOT (E <= 64, s the same in every lane
+// of the wave) the one lane whose expert has rank s, in scalar registers;
+// otherwise entry s of a slot table in LDS.
+template <bool BALLOT>
+__device__ __forceinline__ int slot_expert(uint32_t rank, int s, const int32_t* tbl) {
+  if constexpr (BALLOT)
+    return __builtin_ctzll(__ballot(rank == static_cast<uint32_t>(s)));
+  else
+    return tbl[s];
+}
+
 // Shapes: H = 16 * KWH * LPRH (SwiGLU rows split over LPRH lanes), I = 16 *
 // KWI * LPRI (down rows over LPRI lanes), US SwiGLU iterations and UD down
 // row iterations per wave, TK experts per token, PER = ceil(E / 64), W waves
@@ -84,6 +95,9 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
   __shared__ __align__(16) uint32_t hs[TK][NWI][8];
   __shared__ float hc[TK][NWI];
   __shared__ int32_t s_ids[TK];
+  __shared__ uint64_t s_key[64];
+  __shared__ uint32_t s_cnt[W][64];
+  __shared__ int32_t s_slot[W][TK];
   __shared__ float s_wts[TK];
   __shared__ float red[W], red2[W];
   __shared__ float part[W][RPB];
@@ -228,17 +242,22 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
   }
 
   // ---- 2. top-k (router semantics of reference kernels/router.py:78-126),
-  // by wave 0 of every workgroup once it has seen all E logits of this call
-  // (each lane polls its tagged logit words until they carry this call's
-  // tag).  The softmax is monotonic, so the experts are picked on the logits
-  // themselves: slot s takes the largest logit left (the lowest expert index
-  // among equal ones) -- one wave-wide integer max on order-preserving keys
-  // and one ballot per slot, all in registers.  The ids go to the other waves
-  // through LDS at once, so the expert weight loads are issued before the
-  // softmax is evaluated; the routing weights (p / (sum p_top + 1e-20), p the
-  // softmax over all E) follow while those loads are in flight.
+  // once wave 0 of every workgroup has seen all E logits of this call (each
+  // lane polls its tagged logit words until they carry this call's tag).  The
+  // softmax is monotonic, so the experts are picked on the logits themselves,
+  // the largest first and the lowest expert index among equal ones.
+  //   E <= 64: every expert's rank is counted at once.  Wave 0 puts one
+  //     64-bit key per expert in LDS (the logit's order-preserving bits over
+  //     the complemented index, so all keys differ and ties go to the lower
+  //     index); wave w counts, for every expert, how many of keys [64/W w,
+  //     64/W (w + 1)) exceed its key; the W counts sum to the expert's rank,
+  //     and slot s is the one expert of rank s (a ballot).
+  //   E > 64: wave 0 takes TK rounds of one wave-wide integer max and one
+  //     ballot, and hands the ids over through LDS.
+  // Every wave ends with the slots' experts in scalar registers and issues
+  // its weight loads at once; the routing weights (p / (sum p_top + 1e-20),
+  // p the softmax over all E) follow while those loads are in flight.
   float lg[PER];  // wave 0: the logits of experts lane, lane + 64, ...
-  int my_e = 0;
   if (wv == 0) {
     bool have[PER];
 #pragma unroll
@@ -261,33 +280,54 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
       __builtin_amdgcn_s_sleep(2);
       timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
     }
-    // experts past E get INT_MIN + 1 (below every logit), chosen ones INT_MIN
+    // experts past E get INT_MIN + 1 (below every logit)
     int key[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) key[i] = lane + 64 * i < n_exp ? float_order_key(lg[i]) : INT_MIN + 1;
+    if constexpr (PER == 1) {
+      s_key[lane] = (static_cast<uint64_t>(static_cast<uint32_t>(key[0]) ^ 0x80000000u) << 32) |
+                    static_cast<uint32_t>(~lane);
+    } else {
+      int my_e = 0;
 #pragma unroll
-    for (int s = 0; s < TK; ++s) {
-      int lk = key[0];
+      for (int s = 0; s < TK; ++s) {
+        int lk = key[0];
 #pragma unroll
-      for (int i = 1; i < PER; ++i) lk = max(lk, key[i]);
-      const int mx = wave_max_ui(lk);
-      int e_s = 0;
+        for (int i = 1; i < PER; ++i) lk = max(lk, key[i]);
+        const int mx = wave_max_ui(lk);
+        int e_s = 0;
 #pragma unroll
-      for (int i = PER - 1; i >= 0; --i) {  // the lowest i with a hit wins: the lowest expert index
-        const uint64_t hit = __ballot(key[i] == mx);
-        if (hit) e_s = __builtin_ctzll(hit) + 64 * i;
+        for (int i = PER - 1; i >= 0; --i) {  // the lowest i with a hit wins: the lowest expert index
+          const uint64_t hit = __ballot(key[i] == mx);
+          if (hit) e_s = __builtin_ctzll(hit) + 64 * i;
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i)  // chosen experts drop below every key left
+          if (lane + 64 * i == e_s) key[i] = INT_MIN;
+        if (lane == s) my_e = e_s;
       }
-#pragma unroll
-      for (int i = 0; i < PER; ++i)
-        if (lane + 64 * i == e_s) key[i] = INT_MIN;
-      if (lane == s) my_e = e_s;
-    }
-    if (lane < TK) {
-      s_ids[lane] = my_e;
-      if (wg == 0) ids_out[lane] = my_e;
+      if (lane < TK) s_ids[lane] = my_e;
     }
   }
   __syncthreads();
+  uint32_t rank = 0;  // E <= 64: the rank of this lane's expert
+  if constexpr (PER == 1) {
+    constexpr int KPW = 64 / W;
+    static_assert(64 % W == 0, "keys per wave");
+    const uint64_t mine = s_key[lane];
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) rank += s_key[KPW * wv + j] > mine ? 1u : 0u;
+    s_cnt[wv][lane] = rank;
+    __syncthreads();
+    rank = 0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) rank += s_cnt[w][lane];
+    // this wave's own slot table (one wave's LDS accesses complete in order)
+    if (rank < static_cast<uint32_t>(TK)) s_slot[wv][rank] = lane;
+  }
+  const int32_t* const slot_tbl = PER == 1 ? s_slot[wv] : s_ids;
+  const int my_e = slot_tbl[lane < TK ? lane : 0];  // lane s < TK: slot s's expert
+  if (wv == 0 && wg == 0 && lane < TK) ids_out[lane] = my_e;
 
   // ---- 3. weights: SwiGLU rows of this wave's h outputs, then the down rows
   // of this workgroup's y rows (every load issued before any arithmetic)
@@ -300,7 +340,7 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
     int ug_i = o0 + u * PPI + pi;
     ug_i = ug_i < TK * I ? ug_i : TK * I - 1;
     const int s = ug_i / I, j = ug_i % I;
-    const int64_t e = clamp_id(s_ids[s], n_exp);
+    const int64_t e = clamp_id(slot_expert<PER == 1 && PPI == 1>(rank, s, slot_tbl), n_exp);
     const int64_t row = e * (2 * I) + j + half * I;
     load_words_v<KWH>(ug + row * NWH + klh * KWH, wu[u]);
     au[u] = ld_t<ADT>(ug_alpha, row);
@@ -313,7 +353,7 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
   for (int q = 0; q < SPW; ++q) {
     const int js = wv + W * q;
     const int jj = js < TK ? js : 0;  // idle waves (TK < waves) read slot 0 and add nothing
-    const int64_t e = clamp_id(s_ids[jj], n_exp);
+    const int64_t e = clamp_id(slot_expert<PER == 1>(rank, jj, slot_tbl), n_exp);
 #pragma unroll
     for (int u = 0; u < UD; ++u) {
       int r = rbase + u * RPID + subd;
