@@ -11,7 +11,8 @@
 // time.  Lanes holding the same expert find each other with ballots over the
 // bits of the id (a match-any), the lowest such lane is the group's leader,
 // and a lane's rank inside the group is the popcount of the group mask below
-// it.  Pass 1 counts per (wave, expert); a scan turns the counts into
+// it.  Pass 1 counts per (wave, expert) with LDS atomic adds (integers: the
+// order does not matter); a scan turns the counts into
 // per-(wave, expert) bases; pass 2 writes every pair at base + rank, so the
 // order inside an expert is the pair order.
 #pragma once
@@ -19,6 +20,8 @@
 #include "common.h"
 
 namespace ma {
+
+constexpr int kIdBatch = 8;  // rows of 64 pairs whose ids a wave loads at once
 
 // Mask of the lanes whose (valid) expert id equals this lane's.
 __device__ __forceinline__ uint64_t match_any(int e, int bits, bool valid) {
@@ -49,14 +52,21 @@ __device__ __forceinline__ void dispatch_block(LoadId load_id, int64_t n_pairs, 
   const int64_t p1 = p0 + chunk < n_pairs ? p0 + chunk : n_pairs;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
-  // Pass 1: per-wave counts.
-  for (int64_t p = p0; p < p1; p += 64) {
-    const int64_t q = p + lane;
-    const bool valid = q < p1;
-    int e = valid ? load_id(q) : 0;
-    e = e < 0 ? 0 : (e >= n_exp ? n_exp - 1 : e);
-    const uint64_t m = match_any(e, bits, valid);
-    if (valid && (m & below) == 0) base[wv][e] += __popcll(m);
+  // Pass 1: per-wave counts.  The ids of kIdBatch rows of 64 pairs are
+  // loaded together, so a wave waits for memory once per batch.
+  for (int64_t pb = p0; pb < p1; pb += 64 * kIdBatch) {
+    int eb[kIdBatch];
+#pragma unroll
+    for (int u = 0; u < kIdBatch; ++u) {  // unconditional loads (clamped index): no wait between them
+      const int64_t q = pb + 64 * u + lane;
+      eb[u] = load_id(q < p1 ? q : p1 - 1);
+    }
+#pragma unroll
+    for (int u = 0; u < kIdBatch; ++u) {
+      if (pb + 64 * u >= p1) break;  // (wave-uniform) rows past the range
+      const int e = eb[u] < 0 ? 0 : (eb[u] >= n_exp ? n_exp - 1 : eb[u]);
+      if (pb + 64 * u + lane < p1) atomicAdd(&base[wv][e], 1);  // integer counts: any order
+    }
   }
   __syncthreads();
 
@@ -89,22 +99,30 @@ __device__ __forceinline__ void dispatch_block(LoadId load_id, int64_t n_pairs, 
   if (tid == 0) offsets[n_exp] = static_cast<int32_t>(n_pairs);
   __syncthreads();
 
-  // Pass 2: stable placement.
-  for (int64_t p = p0; p < p1; p += 64) {
-    const int64_t q = p + lane;
-    const bool valid = q < p1;
-    int ee = valid ? load_id(q) : 0;
-    ee = ee < 0 ? 0 : (ee >= n_exp ? n_exp - 1 : ee);
-    const uint64_t m = match_any(ee, bits, valid);
-    int32_t pos = 0;
-    if (valid) {
-      pos = base[wv][ee] + __popcll(m & below);
-      pair_ids[pos] = static_cast<int32_t>(q);
-      inverse[q] = pos;
+  // Pass 2: stable placement (ids batched as in pass 1).
+  for (int64_t pb = p0; pb < p1; pb += 64 * kIdBatch) {
+    int eb[kIdBatch];
+#pragma unroll
+    for (int u = 0; u < kIdBatch; ++u) {  // unconditional loads (clamped index): no wait between them
+      const int64_t q = pb + 64 * u + lane;
+      eb[u] = load_id(q < p1 ? q : p1 - 1);
     }
-    __builtin_amdgcn_wave_barrier();
-    if (valid && (m & below) == 0) base[wv][ee] += __popcll(m);
-    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int u = 0; u < kIdBatch; ++u) {
+      if (pb + 64 * u >= p1) break;  // (wave-uniform) rows past the range
+      const int64_t q = pb + 64 * u + lane;
+      const bool valid = q < p1;
+      const int ee = eb[u] < 0 ? 0 : (eb[u] >= n_exp ? n_exp - 1 : eb[u]);
+      const uint64_t m = match_any(ee, bits, valid);
+      if (valid) {
+        const int32_t pos = base[wv][ee] + __popcll(m & below);
+        pair_ids[pos] = static_cast<int32_t>(q);
+        inverse[q] = pos;
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (valid && (m & below) == 0) base[wv][ee] += __popcll(m);
+      __builtin_amdgcn_wave_barrier();
+    }
   }
 }
 

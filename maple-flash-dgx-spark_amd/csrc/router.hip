@@ -15,7 +15,9 @@
 // overlap.  The wait is bounded (about 0.2 s): on timeout the kernel records
 // an error in the workspace instead of hanging.
 //
-// Otherwise: two launches, like the reference (logits kernel, then top-k).
+// Otherwise: two launches, like the reference (logits kernel, then top-k);
+// prefill-sized batches take the logits as a GEMM on MFMA.
+#include "mfma.h"
 #include "topk.h"
 
 namespace ma {
@@ -111,6 +113,78 @@ __global__ __launch_bounds__(256) void k_router_logits(
   if (lane == 0) logits[t * n_exp + e] = s + (bias ? bias[e] : 0.f);
 }
 
+// The logits of prefill-sized batches as a GEMM on v_mfma_f32_16x16x32_bf16
+// (A = 16 tokens, B = 16 experts, both straight from memory): a workgroup
+// takes 16 tokens x 64 experts, its 8 waves each a K range of K / 8, walked
+// in steps of kRgStep 32-wide k-slices whose operands are all loaded before
+// the step's MFMAs; the waves' partial tiles are then added through LDS in
+// wave order (the same bits on every run).  bf16 x bf16 products are exact;
+// the sums are float32 (in another order than the dot-product kernel's).
+constexpr int kRgWaves = 8, kRgExperts = 64, kRgStep = 4;
+
+__global__ __launch_bounds__(64 * kRgWaves) void k_router_gemm(
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t tokens, const uint16_t* __restrict__ w,
+    int64_t k_in, const float* __restrict__ bias, float* __restrict__ logits, int64_t n_exp) {
+  __shared__ float part[kRgWaves][16][kRgExperts + 1];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 16;
+  const int64_t e0 = static_cast<int64_t>(blockIdx.y) * kRgExperts;
+  const int64_t t = t0 + r16 < tokens ? t0 + r16 : tokens - 1;
+  const uint16_t* const xr = x + t * ldx + 8 * g;
+  const uint16_t* wr[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) wr[nb] = w + (e0 + 16 * nb + r16) * k_in + 8 * g;
+  const int64_t kw = k_in / kRgWaves;
+  f32x4d_t acc[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) acc[nb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+  for (int64_t k0 = wv * kw; k0 < (wv + 1) * kw; k0 += 32 * kRgStep) {
+    u32x4v_t a[kRgStep], b[kRgStep][4];
+#pragma unroll
+    for (int s = 0; s < kRgStep; ++s) {
+      a[s] = *reinterpret_cast<const u32x4v_t*>(xr + k0 + 32 * s);
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) b[s][nb] = *reinterpret_cast<const u32x4v_t*>(wr[nb] + k0 + 32 * s);
+    }
+    mfma_block_begin();
+#pragma unroll
+    for (int s = 0; s < kRgStep; ++s)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) mfma_acc(acc[nb], a[s], b[s][nb]);
+    mfma_block_end();
+    keep_b(a, acc);
+#pragma unroll
+    for (int s = 0; s < kRgStep; ++s) keep_b(b[s], acc);
+  }
+  // lane (r16, g) holds tokens 4 g .. 4 g + 3 of expert 16 nb + r16
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[wv][4 * g + i][16 * nb + r16] = acc[nb][i];
+  __syncthreads();
+  for (int o = tid; o < 16 * kRgExperts; o += 64 * kRgWaves) {
+    const int tr = o / kRgExperts, ec = o % kRgExperts;
+    float v = part[0][tr][ec];
+#pragma unroll
+    for (int ww = 1; ww < kRgWaves; ++ww) v += part[ww][tr][ec];
+    const int64_t e = e0 + ec;
+    if (t0 + tr < tokens) logits[(t0 + tr) * n_exp + e] = v + (bias ? bias[e] : 0.f);
+  }
+}
+
+// The GEMM form pays off from kRgMinTokens tokens (below, its few
+// workgroups leave most of the GPU idle and the dot-product kernel is faster).
+constexpr int64_t kRgMinTokens = 256;
+
+static bool gemm_ok(int x_dtype, int w_dtype, int64_t tokens, int64_t n_exp, int64_t k_in, int64_t ldx,
+                    const void* x, const void* w) {
+  return x_dtype == MA_BF16 && w_dtype == MA_BF16 && tokens >= kRgMinTokens && n_exp % kRgExperts == 0 &&
+         k_in % (32 * kRgStep * kRgWaves) == 0 && (ldx % 8) == 0 &&
+         ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15u) == 0;
+}
+
 template <int PER>
 __global__ __launch_bounds__(64) void k_router_topk(const float* __restrict__ logits,
                                                     int64_t n_exp, int top_k,
@@ -181,9 +255,15 @@ extern "C" int ma_router_topk(const void* x, int x_dtype, int64_t tokens, int64_
   const int fast = x_dtype == MA_BF16 && w_dtype == MA_BF16 && (k_in % 8) == 0 &&
                    (ldx % 8) == 0 &&
                    ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gate_weight)) & 15u) == 0;
-  dim3 g1(static_cast<unsigned>(cdiv(n_experts, 4)), static_cast<unsigned>(tokens));
-  hipLaunchKernelGGL(k_router_logits, g1, dim3(256), 0, s, x, x_dtype, ldx, gate_weight, w_dtype,
-                     n_experts, k_in, bias, logits, fast);
+  if (gemm_ok(x_dtype, w_dtype, tokens, n_experts, k_in, ldx, x, gate_weight)) {
+    dim3 gg(static_cast<unsigned>(cdiv(tokens, 16)), static_cast<unsigned>(n_experts / kRgExperts));
+    hipLaunchKernelGGL(k_router_gemm, gg, dim3(64 * kRgWaves), 0, s, static_cast<const uint16_t*>(x), ldx,
+                       tokens, static_cast<const uint16_t*>(gate_weight), k_in, bias, logits, n_experts);
+  } else {
+    dim3 g1(static_cast<unsigned>(cdiv(n_experts, 4)), static_cast<unsigned>(tokens));
+    hipLaunchKernelGGL(k_router_logits, g1, dim3(256), 0, s, x, x_dtype, ldx, gate_weight, w_dtype,
+                       n_experts, k_in, bias, logits, fast);
+  }
   const dim3 gt(static_cast<unsigned>(tokens));
   if (n_experts <= 64)
     hipLaunchKernelGGL(k_router_topk<1>, gt, dim3(64), 0, s, logits, n_experts, top_k, ids, weights);

@@ -160,8 +160,12 @@ def test_router_ties_and_bias(dev):
 
 
 # ---------------------------------------------------------------- dispatch
+# Beyond 4096 pairs (up to 256 experts) the lists are placed by several
+# workgroups, 2048 pairs each: ragged last chunks and 512 experts (one
+# workgroup) are covered too.
 @pytest.mark.parametrize("tokens,top_k,n_exp", [(1, 8, 64), (32, 8, 64), (128, 8, 64), (2048, 8, 64),
-                                                (7, 3, 5), (0, 8, 64), (1000, 8, 256)])
+                                                (7, 3, 5), (0, 8, 64), (1000, 8, 256), (700, 7, 64),
+                                                (2500, 8, 200), (4096, 8, 512), (512, 8, 64), (513, 8, 64)])
 def test_dispatch_bit_exact(dev, tokens, top_k, n_exp):
     g = torch.Generator(device=dev).manual_seed(tokens * 7 + n_exp)
     ids = torch.randint(0, n_exp, (tokens, top_k), generator=g, device=dev, dtype=torch.int32)
@@ -173,15 +177,19 @@ def test_dispatch_bit_exact(dev, tokens, top_k, n_exp):
     np.testing.assert_array_equal(d.inverse.cpu().numpy(), inv)
 
 
-def test_dispatch_skewed_int64(dev):
-    """All pairs on one expert plus a few singletons, int64 ids."""
-    ids = torch.full((300, 8), 17, device=dev, dtype=torch.int64)
+@pytest.mark.parametrize("tokens", [300, 1200])
+def test_dispatch_skewed_int64(dev, tokens):
+    """All pairs on one expert plus a few singletons, int64 ids (one
+    workgroup, and several)."""
+    ids = torch.full((tokens, 8), 17, device=dev, dtype=torch.int64)
     ids[5, 3] = 0
-    ids[299, 7] = 63
+    ids[tokens - 1, 7] = 63
     d = moe_dispatch(ids, 64)
     c, o, p, inv = ok.dispatch(ids.cpu().numpy(), 64)
     np.testing.assert_array_equal(d.pair_ids.cpu().numpy(), p)
     np.testing.assert_array_equal(d.offsets.cpu().numpy(), o)
+    np.testing.assert_array_equal(d.counts.cpu().numpy(), c)
+    np.testing.assert_array_equal(d.inverse.cpu().numpy(), inv)
 
 
 # ---------------------------------------------------------------- experts
