@@ -699,15 +699,18 @@ __global__ __launch_bounds__(256) void k_combine8(const uint16_t* __restrict__ o
 // ---------------------------------------------------------------------------
 // Prefill form (many pairs per expert): tiles of 128 pairs x 256 weight rows,
 // eight waves (4 along the rows x 2 along the pairs, 64 x 64 each), K walked
-// in steps of 8 words (128 codes) with the pairs' x' operands double-buffered
-// in LDS (one barrier per step) and the next step's weights and x' loaded
-// during this step's MFMAs.  x' pairs and the per-token correction are built
-// once per token (k_gp_prep), so staging is a copy.  Each lane expands its
-// own weight words in registers: a lane group g takes words 2g and 2g+1 of
-// a step, substep s (K = 32) the pairs 4(s & 1)..+3 of word 2g + (s >> 1) --
-// the same K permutation on both operands.  Tiles go to workgroups so that
-// the row tiles of one pair tile share an XCD (workgroups are placed on the 8
-// XCDs round-robin), which keeps that tile's x' in one L2.
+// in steps of 8 words (128 codes).  The pairs' x' operands of a step (32 KB)
+// are copied into LDS by the LDS DMA (global_load_lds_dwordx4: no staging
+// registers), double-buffered: the next step's copy and weights are in flight
+// during this step's MFMAs, one barrier per step.  That keeps a workgroup
+// under 128 VGPRs and 70 KB of LDS, so two run on a CU.  x' pairs and the
+// per-token correction are built once per token (k_gp_prep), so staging is a
+// copy.  Each lane expands its own weight words in registers, half a word
+// (the 4 operand dwords one MFMA takes) at a time: a lane group g takes
+// words 2g and 2g+1 of a step, substep s (K = 32) the pairs 4(s & 1)..+3 of
+// word 2g + (s >> 1) -- the same K permutation on both operands.  Tiles go to
+// workgroups so that the row tiles of one pair tile share an XCD (workgroups
+// are placed on the 8 XCDs round-robin), which keeps that tile's x' in one L2.
 // ---------------------------------------------------------------------------
 namespace gp {
 constexpr int kTok = 128;    // pairs per tile
@@ -716,10 +719,12 @@ constexpr int kWords = 8;    // packed words of K per step
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kXcds = 8;
-constexpr int kTokPad = kTok + 1;  // LDS row of one (word, half): 129 x 16 B, so both
-                                   // the copies (16 halves of a pair) and the B reads
-                                   // (16 pairs of a half) are free of bank conflicts
-constexpr int kXsDwords = 2 * kWords * kTokPad * 4;  // one buffer
+// One step's x' in LDS: 16-byte slot p * 16 + (c ^ (p % 16)) holds chunk c
+// (word c / 2, half c % 2) of pair p -- each pair's 256 bytes in one run, the
+// chunks XOR-swizzled so that the B reads (16 pairs of one chunk) hit 16
+// different bank groups; the DMA fills slots in order, so each copy's source
+// is chosen to match.
+constexpr int kXsDwords = kTok * 2 * kWords * 4;  // one buffer (32 KB)
 // After the K loop the same LDS stages the output tile for coalesced stores:
 // h as [pair][128 outputs] (rows padded to 136 bf16), the down outputs as
 // [pair][256 rows] (rows padded to 264 bf16); the padding keeps the 16 pair
@@ -759,71 +764,96 @@ __device__ __forceinline__ void gp_tile(int n_rtiles, int& mtile, int& rtile) {
   rtile = slot % n_rtiles;
 }
 
+// Half hh of a packed word's 8 bf16x2 operands (expand_word's e[4 hh .. +3]).
+__device__ __forceinline__ uint4 expand_half(uint32_t w, int hh, const ExpandConsts& k) {
+  const uint32_t s0 = hh ? w >> 5 : w << 3, s1 = hh ? w >> 9 : w >> 1;
+  return make_uint4(and_or(s0, k.m3, k.one), and_or(s0, k.m5, k.one), and_or(s1, k.m3, k.one),
+                    and_or(s1, k.m5, k.one));
+}
+
 // One K step of a wave: 4 row blocks x 4 pair blocks x 4 substeps of
-// v_mfma_f32_16x16x32_bf16.  wq: the lane's two words of its 4 row blocks.
+// v_mfma_f32_16x16x32_bf16.  wq: the lane's two words of its 4 row blocks;
+// xsb: the step's x' in the swizzled layout (pair col0 + 16 nb + r16 has
+// p % 16 == r16).
 __device__ __forceinline__ void gp_step(const uint2 (&wq)[4], const uint32_t* __restrict__ xsb,
                                         int g, int r16, int col0, f32x4_t (&acc)[4][4],
                                         const ExpandConsts& kc) {
 #pragma unroll
   for (int ww = 0; ww < 2; ++ww) {
-    uint32_t ex[4][8];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) expand_word(ww ? wq[mb].y : wq[mb].x, ex[mb], kc);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
-      // xs layout [word][half][pair (padded to 129)][4 dwords]
-      const uint32_t* bp = xsb + ((2 * g + ww) * 2 + hh) * gp::kTokPad * 4;
+      const int c = (2 * g + ww) * 2 + hh;
+      uint4 b[4];
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        const uint4 b = *reinterpret_cast<const uint4*>(bp + (col0 + nb * 16 + r16) * 4);
+      for (int nb = 0; nb < 4; ++nb)
+        b[nb] = *reinterpret_cast<const uint4*>(xsb + ((col0 + nb * 16 + r16) * 16 + (c ^ r16)) * 4);
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const uint4 a = make_uint4(ex[mb][4 * hh], ex[mb][4 * hh + 1], ex[mb][4 * hh + 2], ex[mb][4 * hh + 3]);
-          acc[mb][nb] = mfma_bf16(a, b, acc[mb][nb]);
-        }
+      for (int mb = 0; mb < 4; ++mb) {
+        const uint4 a = expand_half(ww ? wq[mb].y : wq[mb].x, hh, kc);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mfma_bf16(a, b[nb], acc[mb][nb]);
       }
     }
   }
 }
 
-// One step's x' operands are 128 pairs x 8 words x 2 halves of 16 B, 4 per
-// thread: copy i of thread tid is chunk c = tid + 512 i, (word, half) c % 16
-// and pair column c / 16, so 16 consecutive lanes copy one pair's 256
-// contiguous bytes (the LDS layout is [word][half][pair][4 dwords], pairs
-// padded to 129).
-// (Plain named members rather than arrays, and no lambdas capturing
-// locals: either put the copies in scratch memory on this compiler.)
-struct GpX {
-  uint4 a, b, c, d;
+// A step's x' copies: 2048 slots of 16 B, 4 per thread; copy i of thread tid
+// fills slot S = tid + 512 i (so each wave's copy i fills 64 consecutive
+// slots, as the LDS DMA writes them) with chunk c = (S % 16) ^ (p % 16) of
+// pair p = S / 16.  rows[p] is pair p's row in the uint32 array base (row
+// length ld); src[i] is copy i's source at K word 0.
+struct GpDma {
+  const uint32_t* src[4];
 };
-struct GpSrc {
-  const uint32_t *a, *b, *c, *d;
-};
-__device__ __forceinline__ void gp_load_x(const GpSrc& s, int64_t k0, GpX& x) {
-  x.a = *reinterpret_cast<const uint4*>(s.a + k0 * 8);
-  x.b = *reinterpret_cast<const uint4*>(s.b + k0 * 8);
-  x.c = *reinterpret_cast<const uint4*>(s.c + k0 * 8);
-  x.d = *reinterpret_cast<const uint4*>(s.d + k0 * 8);
+__device__ __forceinline__ GpDma gp_dma_sources(const uint32_t* base, int64_t ld, const int32_t* rows) {
+  GpDma d;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int S = threadIdx.x + gp::kThreads * i, p = S / 16, c = (S % 16) ^ (p % 16);
+    d.src[i] = base + static_cast<int64_t>(rows[p]) * ld + (c >> 1) * 8 + 4 * (c & 1);
+  }
+  return d;
 }
-__device__ __forceinline__ void gp_store_x(uint32_t* __restrict__ xsb, const GpX& x) {
-  constexpr int kStep = gp::kThreads / 16;  // pair columns between a thread's copies
-  uint4* p = reinterpret_cast<uint4*>(xsb) + (threadIdx.x % 16) * gp::kTokPad + threadIdx.x / 16;
-  p[0] = x.a;
-  p[kStep] = x.b;
-  p[2 * kStep] = x.c;
-  p[3 * kStep] = x.d;
+typedef __attribute__((address_space(3))) void* lds_void_t;
+
+// The copies of the step at K word k0 into the LDS buffer xsb (in flight
+// until the issuing wave's vector memory counter drains).
+__device__ __forceinline__ void gp_dma(const GpDma& d, int64_t k0, uint32_t* xsb) {
+  const int wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    __builtin_amdgcn_global_load_lds(d.src[i] + k0 * 8, (lds_void_t)(xsb + 4 * (64 * wv + gp::kThreads * i)),
+                                     16, 0, 0);
 }
-// Sources of a thread's copies: rows[t] is the row of pair column t in the
-// uint32 array base with row length ld.
-__device__ __forceinline__ const uint32_t* gp_x_source(const uint32_t* base, int64_t ld,
-                                                       const int32_t* rows, int i) {
-  const int c = threadIdx.x + gp::kThreads * i;
-  const int t = c / 16, rest = c % 16;
-  return base + static_cast<int64_t>(rows[t]) * ld + (rest >> 1) * 8 + 4 * (rest & 1);
-}
-__device__ __forceinline__ GpSrc gp_x_sources(const uint32_t* base, int64_t ld, const int32_t* rows) {
-  return GpSrc{gp_x_source(base, ld, rows, 0), gp_x_source(base, ld, rows, 1),
-               gp_x_source(base, ld, rows, 2), gp_x_source(base, ld, rows, 3)};
+
+// The K loop shared by both stages: acc += W (rows rowp, nwk words) x x'
+// (pairs' rows in d), weights one step ahead in registers, x' one step ahead
+// by DMA into the other LDS buffer.
+__device__ __forceinline__ void gp_kloop(const uint32_t* const (&rowp)[4], int64_t nwk, const GpDma& d,
+                                         uint32_t* xs, int g, int r16, int col0, f32x4_t (&acc)[4][4]) {
+  using namespace gp;
+  const ExpandConsts kc;
+  uint2 wq[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) wq[mb] = *reinterpret_cast<const uint2*>(rowp[mb]);
+  gp_dma(d, 0, xs);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
+  __syncthreads();                // and every other wave's
+  int buf = 0;
+  for (int64_t k0 = 0; k0 < nwk; k0 += kWords) {
+    const int64_t kn = k0 + kWords < nwk ? k0 + kWords : k0;
+    if (k0 + kWords < nwk) gp_dma(d, kn, xs + (buf ^ 1) * kXsDwords);
+    uint2 wn[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) wn[mb] = *reinterpret_cast<const uint2*>(rowp[mb] + kn);
+    MA_ISSUE_FENCE();  // the next step's loads go out before this step's MFMAs
+    gp_step(wq, xs + buf * kXsDwords, g, r16, col0, acc, kc);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // the next buffer is in; this one is free to refill
+    buf ^= 1;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) wq[mb] = wn[mb];
+  }
 }
 
 // SwiGLU stage: h = SwiGLU(up, gate) of 128 outputs (rows [o, o+128) of the
@@ -832,7 +862,7 @@ __device__ __forceinline__ GpSrc gp_x_sources(const uint32_t* base, int64_t ld, 
 // and optionally in slot order (h); hcorr[pos * n_rtiles + rtile] gets the
 // tile's part of the down stage's correction sum (f + 1) h.
 template <int ADT>
-__global__ __launch_bounds__(gp::kThreads) void k_gp_swiglu(
+__global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_gp_swiglu(
     const uint32_t* __restrict__ xp, const float* __restrict__ xc, int64_t topk,
     const uint32_t* __restrict__ w, int64_t n_half, int64_t nwords,
     const void* __restrict__ alpha, const int32_t* __restrict__ offsets,
@@ -866,44 +896,13 @@ __global__ __launch_bounds__(gp::kThreads) void k_gp_swiglu(
     rowp[mb] = we + (i + (mb >> 1) * n_half) * nwords + 2 * g;
   }
   __syncthreads();  // tokrow
-  const GpSrc xsrc = gp_x_sources(xp, nwords * 8, tokrow);
+  const GpDma xsrc = gp_dma_sources(xp, nwords * 8, tokrow);
   f32x4_t acc[4][4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const ExpandConsts kc;
-  // Weights are loaded two steps ahead (the compiler places those loads at
-  // the end of a step, next to their loop-carried use), x' one step ahead.
-  uint2 wq[4], wn[4];
-  GpX xq;
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    wq[mb] = *reinterpret_cast<const uint2*>(rowp[mb]);
-    wn[mb] = *reinterpret_cast<const uint2*>(rowp[mb] + (kWords < nwords ? kWords : 0));
-  }
-  gp_load_x(xsrc, 0, xq);
-  gp_store_x(xs, xq);
-  __syncthreads();
-  int buf = 0;
-  for (int64_t k0 = 0; k0 < nwords; k0 += kWords) {
-    const int64_t kn = k0 + kWords < nwords ? k0 + kWords : k0;
-    const int64_t knn = k0 + 2 * kWords < nwords ? k0 + 2 * kWords : k0;
-    gp_load_x(xsrc, kn, xq);
-    MA_ISSUE_FENCE();  // the next step's x' loads stay ahead of this step's MFMAs
-    gp_step(wq, xs + buf * kXsDwords, g, r16, wm * 64, acc, kc);
-    uint2 wnn[4];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) wnn[mb] = *reinterpret_cast<const uint2*>(rowp[mb] + knn);
-    gp_store_x(xs + (buf ^ 1) * kXsDwords, xq);
-    __syncthreads();
-    buf ^= 1;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      wq[mb] = wn[mb];
-      wn[mb] = wnn[mb];
-    }
-  }
+  gp_kloop(rowp, nwords, xsrc, xs, g, r16, wm * 64, acc);
   // Epilogue: lane (r16, g) of row block mb holds rows 4g..4g+3 of the block
   // for pair column wm*64 + nb*16 + r16.  h goes to LDS in the x' pair layout
   // of its 8 words (the loop's last barrier has freed the LDS), then out in
@@ -966,7 +965,7 @@ __global__ __launch_bounds__(gp::kThreads) void k_gp_swiglu(
 // 128 pairs and 256 output rows; the correction is the sum of the SwiGLU
 // stage's n_ctiles parts, added in tile order.
 template <int ADT>
-__global__ __launch_bounds__(gp::kThreads) void k_gp_down(
+__global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_gp_down(
     const uint32_t* __restrict__ hp, const float* __restrict__ hcorr, int n_ctiles,
     const uint32_t* __restrict__ w, int64_t n_out, int64_t nwk, const void* __restrict__ alpha,
     const int32_t* __restrict__ offsets, int n_exp, uint16_t* __restrict__ out) {
@@ -998,44 +997,13 @@ __global__ __launch_bounds__(gp::kThreads) void k_gp_down(
     rowp[mb] = we + n * nwk + 2 * g;
   }
   __syncthreads();  // prow
-  const GpSrc xsrc = gp_x_sources(hp, nwk * 8, prow);
+  const GpDma xsrc = gp_dma_sources(hp, nwk * 8, prow);
   f32x4_t acc[4][4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const ExpandConsts kc;
-  // Weights are loaded two steps ahead (the compiler places those loads at
-  // the end of a step, next to their loop-carried use), x' one step ahead.
-  uint2 wq[4], wn[4];
-  GpX xq;
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    wq[mb] = *reinterpret_cast<const uint2*>(rowp[mb]);
-    wn[mb] = *reinterpret_cast<const uint2*>(rowp[mb] + (kWords < nwk ? kWords : 0));
-  }
-  gp_load_x(xsrc, 0, xq);
-  gp_store_x(xs, xq);
-  __syncthreads();
-  int buf = 0;
-  for (int64_t k0 = 0; k0 < nwk; k0 += kWords) {
-    const int64_t kn = k0 + kWords < nwk ? k0 + kWords : k0;
-    const int64_t knn = k0 + 2 * kWords < nwk ? k0 + 2 * kWords : k0;
-    gp_load_x(xsrc, kn, xq);
-    MA_ISSUE_FENCE();  // the next step's x' loads stay ahead of this step's MFMAs
-    gp_step(wq, xs + buf * kXsDwords, g, r16, wm * 64, acc, kc);
-    uint2 wnn[4];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) wnn[mb] = *reinterpret_cast<const uint2*>(rowp[mb] + knn);
-    gp_store_x(xs + (buf ^ 1) * kXsDwords, xq);
-    __syncthreads();
-    buf ^= 1;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      wq[mb] = wn[mb];
-      wn[mb] = wnn[mb];
-    }
-  }
+  gp_kloop(rowp, nwk, xsrc, xs, g, r16, wm * 64, acc);
   // The tile goes to LDS as [pair][256 rows] (the loop's last barrier has
   // freed the LDS), then out in 16-byte pieces, each pair's 512 bytes
   // contiguous (n_out % 256 == 0).
