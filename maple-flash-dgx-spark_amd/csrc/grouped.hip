@@ -730,7 +730,10 @@ constexpr int kXsDwords = kTok * 2 * kWords * 4;  // one buffer (32 KB)
 // [pair][256 rows] (rows padded to 264 bf16); the padding keeps the 16 pair
 // columns of a lane group on different banks and every row 16-byte aligned.
 constexpr int kHRow = 136, kORow = 264;
-constexpr int kLdsDwords = (2 * kXsDwords > kTok * kORow / 2) ? 2 * kXsDwords : kTok * kORow / 2;
+// Buffer A also stages the output tile: all of h (128 x 136 bf16), or half of
+// the down tile's pairs at a time (64 x 264 bf16).
+constexpr int kXaDwords = (kTok * kHRow / 2 > kTok / 2 * kORow / 2) ? kTok * kHRow / 2 : kTok / 2 * kORow / 2;
+static_assert(kXaDwords >= kXsDwords, "buffer A holds a step");
 }  // namespace gp
 
 // x' pairs of every token once: xp [T, nwords * 8] (word w: pair j =
@@ -803,18 +806,22 @@ __device__ __forceinline__ void gp_step(const uint2 (&wq)[4], const uint32_t* __
 // pair p = S / 16.  rows[p] is pair p's row in the uint32 array base (row
 // length ld); src[i] is copy i's source at K word 0.
 struct GpDma {
-  const uint32_t* src[4];
+  const uint32_t* base;  // the same in every lane
+  uint32_t off[4];       // copy i's source at K word 0, in uint32 from base (< 2^32: checked by the host)
 };
 __device__ __forceinline__ GpDma gp_dma_sources(const uint32_t* base, int64_t ld, const int32_t* rows) {
   GpDma d;
+  d.base = base;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int S = threadIdx.x + gp::kThreads * i, p = S / 16, c = (S % 16) ^ (p % 16);
-    d.src[i] = base + static_cast<int64_t>(rows[p]) * ld + (c >> 1) * 8 + 4 * (c & 1);
+    d.off[i] = static_cast<uint32_t>(static_cast<int64_t>(rows[p]) * ld + (c >> 1) * 8 + 4 * (c & 1));
   }
   return d;
 }
 typedef __attribute__((address_space(3))) void* lds_void_t;
+// s_waitcnt immediate (gfx9 encoding): vmcnt(4), expcnt and lgkmcnt left open.
+constexpr int kVmcnt4 = 0x4 | (0x7 << 4) | (0xF << 8);
 
 // The copies of the step at K word k0 into the LDS buffer xsb (in flight
 // until the issuing wave's vector memory counter drains).
@@ -822,37 +829,61 @@ __device__ __forceinline__ void gp_dma(const GpDma& d, int64_t k0, uint32_t* xsb
   const int wv = threadIdx.x >> 6;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    __builtin_amdgcn_global_load_lds(d.src[i] + k0 * 8, (lds_void_t)(xsb + 4 * (64 * wv + gp::kThreads * i)),
-                                     16, 0, 0);
+    __builtin_amdgcn_global_load_lds(d.base + d.off[i] + k0 * 8,
+                                     (lds_void_t)(xsb + 4 * (64 * wv + gp::kThreads * i)), 16, 0, 0);
 }
 
-// The K loop shared by both stages: acc += W (rows rowp, nwk words) x x'
-// (pairs' rows in d), weights one step ahead in registers, x' one step ahead
-// by DMA into the other LDS buffer.
-__device__ __forceinline__ void gp_kloop(const uint32_t* const (&rowp)[4], int64_t nwk, const GpDma& d,
-                                         uint32_t* xs, int g, int r16, int col0, f32x4_t (&acc)[4][4]) {
+// One step of the K loop: issue the next step's x' copies into ``nxt`` (if
+// there is a next step) and its weights into wn, then this step's MFMAs on
+// ``cur``, then wait for the copies and meet at the barrier.
+__device__ __forceinline__ void gp_kstep(const uint32_t* rp, const int64_t (&moff)[4], int64_t k0, int64_t nwk,
+                                         const GpDma& d, const uint32_t* cur, uint32_t* nxt,
+                                         uint2 (&wq)[4], int g, int r16, int col0, f32x4_t (&acc)[4][4],
+                                         const ExpandConsts& kc) {
+  using namespace gp;
+  const int64_t kn = k0 + kWords < nwk ? k0 + kWords : k0;
+  // This step's weights (loaded during the last step) are in: nothing else
+  // is outstanding, so the copies and loads below are all this wave has in
+  // flight during the MFMAs.
+  __builtin_amdgcn_s_waitcnt(0);
+  MA_ISSUE_FENCE();
+  if (k0 + kWords < nwk) gp_dma(d, kn, nxt);
+  MA_ISSUE_FENCE();  // the copies are issued before the weights
+  uint2 wn[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) wn[mb] = *reinterpret_cast<const uint2*>(rp + moff[mb] + kn);
+  MA_ISSUE_FENCE();  // the next step's loads go out before this step's MFMAs
+  gp_step(wq, cur, g, r16, col0, acc, kc);
+  // This wave's copies have landed: at most the 4 weight loads issued after
+  // them are outstanding (vector memory completes in issue order); those
+  // are waited for where the next step uses them.
+  __builtin_amdgcn_s_waitcnt(kVmcnt4);
+  __syncthreads();  // the next buffer is in; this one is free to refill
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) wq[mb] = wn[mb];
+}
+
+// The K loop shared by both stages: acc += W x x', the lane's weight row of
+// block mb at rp + moff[mb] (moff the same in every lane; nwk words), the
+// pairs' x' rows in d; weights one step ahead in registers, x' one step ahead
+// by DMA into the other LDS buffer.  The two buffers are distinct arrays and
+// the loop is unrolled by two, so the compiler sees that a step's LDS reads
+// and the copies in flight into the other buffer do not overlap (it would
+// otherwise wait for the copies before the reads).
+__device__ __forceinline__ void gp_kloop(const uint32_t* rp, const int64_t (&moff)[4], int64_t nwk, const GpDma& d,
+                                         uint32_t* xa, uint32_t* xb, int g, int r16, int col0,
+                                         f32x4_t (&acc)[4][4]) {
   using namespace gp;
   const ExpandConsts kc;
   uint2 wq[4];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) wq[mb] = *reinterpret_cast<const uint2*>(rowp[mb]);
-  gp_dma(d, 0, xs);
+  for (int mb = 0; mb < 4; ++mb) wq[mb] = *reinterpret_cast<const uint2*>(rp + moff[mb]);
+  gp_dma(d, 0, xa);
   __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
   __syncthreads();                // and every other wave's
-  int buf = 0;
-  for (int64_t k0 = 0; k0 < nwk; k0 += kWords) {
-    const int64_t kn = k0 + kWords < nwk ? k0 + kWords : k0;
-    if (k0 + kWords < nwk) gp_dma(d, kn, xs + (buf ^ 1) * kXsDwords);
-    uint2 wn[4];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) wn[mb] = *reinterpret_cast<const uint2*>(rowp[mb] + kn);
-    MA_ISSUE_FENCE();  // the next step's loads go out before this step's MFMAs
-    gp_step(wq, xs + buf * kXsDwords, g, r16, col0, acc, kc);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();  // the next buffer is in; this one is free to refill
-    buf ^= 1;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) wq[mb] = wn[mb];
+  for (int64_t k0 = 0; k0 < nwk; k0 += 2 * kWords) {
+    gp_kstep(rp, moff, k0, nwk, d, xa, xb, wq, g, r16, col0, acc, kc);
+    if (k0 + kWords < nwk) gp_kstep(rp, moff, k0 + kWords, nwk, d, xb, xa, wq, g, r16, col0, acc, kc);
   }
 }
 
@@ -869,7 +900,8 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
     const int32_t* __restrict__ pair_ids, int n_exp, uint16_t* __restrict__ hp,
     float* __restrict__ hcorr, uint16_t* __restrict__ h, int64_t ldh) {
   using namespace gp;
-  __shared__ __align__(16) uint32_t xs[kLdsDwords];
+  __shared__ __align__(16) uint32_t xa[kXaDwords];
+  __shared__ __align__(16) uint32_t xb[kXsDwords];
   __shared__ float cst[kTok], hcp[4][kTok];
   __shared__ int32_t tokrow[kTok], pid[kTok];
   const int n_rtiles = static_cast<int>((n_half + kRows / 2 - 1) / (kRows / 2));
@@ -888,13 +920,11 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
   }
   const int64_t o0 = static_cast<int64_t>(rtile) * (kRows / 2) + wr * 32;  // this wave's first output
   const uint32_t* we = w + static_cast<int64_t>(e) * 2 * n_half * nwords;
-  const uint32_t* rowp[4];
+  // (n_half % 128 == 0: every row of the tile exists)
+  const uint32_t* rp = we + (o0 + r16) * nwords + 2 * g;
+  int64_t moff[4];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    int64_t i = o0 + 16 * (mb & 1) + r16;
-    i = i < n_half ? i : n_half - 1;
-    rowp[mb] = we + (i + (mb >> 1) * n_half) * nwords + 2 * g;
-  }
+  for (int mb = 0; mb < 4; ++mb) moff[mb] = (16 * (mb & 1) + (mb >> 1) * n_half) * nwords;
   __syncthreads();  // tokrow
   const GpDma xsrc = gp_dma_sources(xp, nwords * 8, tokrow);
   f32x4_t acc[4][4];
@@ -902,12 +932,12 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  gp_kloop(rowp, nwords, xsrc, xs, g, r16, wm * 64, acc);
+  gp_kloop(rp, moff, nwords, xsrc, xa, xb, g, r16, wm * 64, acc);
   // Epilogue: lane (r16, g) of row block mb holds rows 4g..4g+3 of the block
   // for pair column wm*64 + nb*16 + r16.  h goes to LDS in the x' pair layout
   // of its 8 words (the loop's last barrier has freed the LDS), then out in
   // 16-byte pieces, each pair's 256 bytes contiguous.
-  uint16_t* hst = reinterpret_cast<uint16_t*>(xs);
+  uint16_t* hst = reinterpret_cast<uint16_t*>(xa);
   const int64_t otile = static_cast<int64_t>(rtile) * (kRows / 2);
   float hcl[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -970,7 +1000,8 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
     const uint32_t* __restrict__ w, int64_t n_out, int64_t nwk, const void* __restrict__ alpha,
     const int32_t* __restrict__ offsets, int n_exp, uint16_t* __restrict__ out) {
   using namespace gp;
-  __shared__ __align__(16) uint32_t xs[kLdsDwords];
+  __shared__ __align__(16) uint32_t xa[kXaDwords];
+  __shared__ __align__(16) uint32_t xb[kXsDwords];
   __shared__ float cst[kTok];
   __shared__ int32_t prow[kTok];
   const int n_rtiles = static_cast<int>((n_out + kRows - 1) / kRows);
@@ -989,13 +1020,11 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
   }
   const int64_t n0 = static_cast<int64_t>(rtile) * kRows + wr * 64;
   const uint32_t* we = w + static_cast<int64_t>(e) * n_out * nwk;
-  const uint32_t* rowp[4];
+  // (n_out % 256 == 0: every row of the tile exists)
+  const uint32_t* rp = we + (n0 + r16) * nwk + 2 * g;
+  int64_t moff[4];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    int64_t n = n0 + 16 * mb + r16;
-    n = n < n_out ? n : n_out - 1;
-    rowp[mb] = we + n * nwk + 2 * g;
-  }
+  for (int mb = 0; mb < 4; ++mb) moff[mb] = 16 * mb * nwk;
   __syncthreads();  // prow
   const GpDma xsrc = gp_dma_sources(hp, nwk * 8, prow);
   f32x4_t acc[4][4];
@@ -1003,11 +1032,12 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  gp_kloop(rowp, nwk, xsrc, xs, g, r16, wm * 64, acc);
-  // The tile goes to LDS as [pair][256 rows] (the loop's last barrier has
-  // freed the LDS), then out in 16-byte pieces, each pair's 512 bytes
-  // contiguous (n_out % 256 == 0).
-  uint16_t* ost = reinterpret_cast<uint16_t*>(xs);
+  gp_kloop(rp, moff, nwk, xsrc, xa, xb, g, r16, wm * 64, acc);
+  // The tile goes out through LDS buffer A as [pair][256 rows], half of the
+  // pairs at a time (the waves holding them write, then every thread copies
+  // them out in 16-byte pieces, each pair's 512 bytes contiguous; n_out % 256
+  // == 0).  The loop's last barrier has freed the buffer.
+  uint2 v[4][4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
     const int64_t n = n0 + 16 * mb + 4 * g;
@@ -1016,22 +1046,30 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
     for (int r = 0; r < 4; ++r) a[r] = ld_t<ADT>(alpha, static_cast<int64_t>(e) * n_out + (n + r < n_out ? n + r : n_out - 1));
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
-      const int col = wm * 64 + nb * 16 + r16;
-      const float c = cst[col];
-      uint2 v;
-      v.x = pack_bf16x2_rn(a[0] * (acc[mb][nb][0] - c), a[1] * (acc[mb][nb][1] - c));
-      v.y = pack_bf16x2_rn(a[2] * (acc[mb][nb][2] - c), a[3] * (acc[mb][nb][3] - c));
-      *reinterpret_cast<uint2*>(ost + col * kORow + wr * 64 + 16 * mb + 4 * g) = v;
+      const float c = cst[wm * 64 + nb * 16 + r16];
+      v[mb][nb].x = pack_bf16x2_rn(a[0] * (acc[mb][nb][0] - c), a[1] * (acc[mb][nb][1] - c));
+      v[mb][nb].y = pack_bf16x2_rn(a[2] * (acc[mb][nb][2] - c), a[3] * (acc[mb][nb][3] - c));
     }
   }
-  __syncthreads();
+  uint16_t* ost = reinterpret_cast<uint16_t*>(xa);
   const int64_t ntile0 = static_cast<int64_t>(rtile) * kRows;
+  for (int half = 0; half < 2; ++half) {
+    if (wm == half) {
 #pragma unroll
-  for (int k = 0; k < kTok * 32 / kThreads; ++k) {
-    const int c = tid + kThreads * k, col = c / 32, part = c % 32;
-    if (col < np)
-      *reinterpret_cast<uint4*>(out + static_cast<int64_t>(pos0 + col) * n_out + ntile0 + part * 8) =
-          *reinterpret_cast<const uint4*>(ost + col * kORow + part * 8);
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          *reinterpret_cast<uint2*>(ost + (nb * 16 + r16) * kORow + wr * 64 + 16 * mb + 4 * g) = v[mb][nb];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kTok / 2 * 32 / kThreads; ++k) {
+      const int c = tid + kThreads * k, colh = c / 32, part = c % 32, col = half * (kTok / 2) + colh;
+      if (col < np)
+        *reinterpret_cast<uint4*>(out + static_cast<int64_t>(pos0 + col) * n_out + ntile0 + part * 8) =
+            *reinterpret_cast<const uint4*>(ost + colh * kORow + part * 8);
+    }
+    __syncthreads();  // the buffer is free for the next half
   }
 }
 
