@@ -631,16 +631,23 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
       keep_b(bv, acc[0]);
       if ((s + 1) % SPG == 0) {  // end of an RTN group: fold and clear
         const int gi = s / SPG;
+        // s (acc - 16 X) + b X = s acc + (b - 16 s) X: two FMAs per output
+        float sr[MB][4], br[MB][4];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int rr = 32 * wv + 16 * mb + 4 * g + i;
+            sr[mb][i] = sb[0][rr][gi];
+            br[mb][i] = sb[1][rr][gi] - 16.f * sr[mb][i];
+          }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           const float X = xg[nb * 16 + r16][gi];
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int rr = 32 * wv + 16 * mb + 4 * g + i;
-              out[mb][nb][i] += sb[0][rr][gi] * (acc[mb][nb][i] - 16.f * X) + sb[1][rr][gi] * X;
-            }
+            for (int i = 0; i < 4; ++i) out[mb][nb][i] += sr[mb][i] * acc[mb][nb][i] + br[mb][i] * X;
             acc[mb][nb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
           }
         }
