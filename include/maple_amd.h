@@ -204,6 +204,22 @@ int ma_rtn4_gemv(const void* x, int x_dtype, int64_t batch, int64_t ldx,
                  int64_t group_size, void* y, int64_t ldy, void* stream);
 
 /*
+ * ma_rtn4_gemv with a workspace: from batch 5 in groups of 128 (N a multiple
+ * of 32, bf16 x, [N, K/8] codes, 16-byte aligned) the x' operands and group
+ * sums are built once into the workspace and copied into LDS by the LDS DMA
+ * while the weights stream (the same bits as ma_rtn4_gemv); any other call
+ * is ma_rtn4_gemv's.  workspace: ma_rtn4_gemv_workspace_bytes(batch, nwords,
+ * group_size) bytes (0: none needed), 256-byte aligned; calls sharing one
+ * must not overlap.  Replaces rtn4_gemv, src/maple_run/kernels/rtn4.py:285-415.
+ */
+size_t ma_rtn4_gemv_workspace_bytes(int64_t batch, int64_t nwords, int64_t group_size);
+int ma_rtn4_gemv_ws(const void* x, int x_dtype, int64_t batch, int64_t ldx,
+                    const uint32_t* packed, int64_t n_out, int64_t nwords, int packed_kn,
+                    const void* scales, int scales_dtype, const void* biases, int biases_dtype,
+                    int64_t group_size, void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/*
  * out[i, k] = q[ids[i], k] * scale[ids[i], g] + bias[ids[i], g] in float32.
  * Replaces rtn4_embedding, src/maple_run/kernels/rtn4.py:27-47.
  */

@@ -42,6 +42,8 @@ _SIGNATURES = {
     "ma_rms_norm": [_P, _I, _L, _L, _P, _I, _F, _P, _P],
     "ma_add_rms_norm": [_P, _P, _I, _L, _L, _P, _I, _F, _P, _P, _P],
     "ma_rtn4_gemv": [_P, _I, _L, _L, _P, _L, _L, _I, _P, _I, _P, _I, _L, _P, _L, _P],
+    "ma_rtn4_gemv_ws": [_P, _I, _L, _L, _P, _L, _L, _I, _P, _I, _P, _I, _L, _P, _L, _P, _Z, _P],
+    "ma_rtn4_gemv_workspace_bytes": [_L, _L, _L],
     "ma_rtn4_embedding": [_P, _I, _L, _P, _L, _L, _P, _I, _P, _I, _L, _P, _P],
     "ma_grouped_workspace_bytes": [_L, _L, _L],
     "ma_qk_norm_rope_store": [_P, _L, _L, _I, _I, _I, _P, _P, _I, _P, _P, _I, _L, _L, _I, _I, _F,
@@ -79,7 +81,7 @@ _RESTYPES = {"ma_last_error": ctypes.c_char_p, "ma_router_workspace_bytes": _Z,
              "ma_grouped_workspace_bytes": _Z, "ma_gqa_workspace_bytes": _Z,
              "ma_moe_fused_workspace_bytes": _Z, "ma_moe_route_workspace_bytes": _Z,
              "ma_moe_grouped_noalloc_max_bytes": _Z, "ma_sampler_workspace_bytes": _Z,
-             "ma_flash_head_workspace_bytes": _Z}
+             "ma_flash_head_workspace_bytes": _Z, "ma_rtn4_gemv_workspace_bytes": _Z}
 
 _lib = None
 

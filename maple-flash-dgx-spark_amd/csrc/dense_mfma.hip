@@ -647,7 +647,8 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) out[mb][nb][i] += sr[mb][i] * acc[mb][nb][i] + br[mb][i] * X;
+            for (int i = 0; i < 4; ++i)  // explicit FMAs: every build rounds the fold alike
+              out[mb][nb][i] = __builtin_fmaf(sr[mb][i], acc[mb][nb][i], __builtin_fmaf(br[mb][i], X, out[mb][nb][i]));
             acc[mb][nb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
           }
         }
@@ -658,6 +659,250 @@ __global__ __launch_bounds__(256) void k_rtn4_mfma(
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int s = 0; s < 4; ++s) wq[mb][s] = wn[mb][s];
+  }
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int64_t t = t0 + nb * 16 + r16;
+    if (t >= batch) continue;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int64_t n0 = row0 + 16 * mb + 4 * g;
+      if (n0 + 3 < n_out && (ldy % 4) == 0) {
+        uint2 r;
+        r.x = pack_bf16x2_rn(out[mb][nb][0], out[mb][nb][1]);
+        r.y = pack_bf16x2_rn(out[mb][nb][2], out[mb][nb][3]);
+        *reinterpret_cast<uint2*>(y + t * ldy + n0) = r;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (n0 + i < n_out) y[t * ldy + n0 + i] = f32_to_bf16(out[mb][nb][i]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RTN4 with a workspace: the x' operands and group sums of every token tile
+// are built once (k_rtn4_xprep), then each workgroup of k_rtn4_mfma_dma copies
+// chunk c + 1's x' and group sums into LDS with the LDS DMA while chunk c
+// multiplies: no staging arithmetic or registers in the K loop, one barrier
+// per chunk, and every load of the loop issued a chunk ahead.  Same per-word
+// arithmetic and fixed-order sums as k_rtn4_mfma (the group sums are added in
+// word order by the prep launch), so the two give the same bits.
+// ---------------------------------------------------------------------------
+// Workspace: per token tile and chunk, the x' words in k_rtn4_mfma's LDS
+// layout [word][token][4 u32] (NT x 256 B), then the group sums [token][GPC].
+size_t rtn4_ws_bytes(int64_t batch, int64_t nwords, int64_t group) {
+  const int64_t nt = batch <= 16 ? 16 : 32, tiles = cdiv(batch, nt), chunks = nwords / kDenseChunk;
+  const int64_t gpc = kDenseChunk / (group / 8);
+  return static_cast<size_t>(tiles * chunks * nt) * (kDenseChunk * 16 + gpc * 4);
+}
+
+template <int NB, int GW>
+__global__ __launch_bounds__(256) void k_rtn4_xprep(const uint16_t* __restrict__ x, int64_t batch, int64_t ldx,
+                                                    int64_t nwords, uint4* __restrict__ xq, float* __restrict__ xgs) {
+  constexpr int NT = 16 * NB, GPC = kDenseChunk / GW;
+  __shared__ float xw[kDenseChunk][NT];
+  const int tid = threadIdx.x;
+  const int64_t tile = blockIdx.x, c = blockIdx.y, nch = nwords / kDenseChunk;
+  const int64_t t0 = tile * NT, c0 = c * kDenseChunk;
+  uint4* const dst = xq + (tile * nch + c) * (kDenseChunk * NT);
+#pragma unroll
+  for (int it = 0; it < NB; ++it) {
+    const int item = tid + 256 * it;
+    const int col = item % NT, wd = item / NT;
+    const bool valid = t0 + col < batch;
+    const int64_t t = valid ? t0 + col : batch - 1;
+    const uint4 xr = reinterpret_cast<const uint4*>(x + t * ldx + (c0 + wd) * 8)[0];
+    const uint32_t u4[4] = {xr.x, xr.y, xr.z, xr.w};
+    float xv[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      xv[2 * q] = valid ? __uint_as_float(u4[q] << 16) : 0.f;
+      xv[2 * q + 1] = valid ? __uint_as_float(u4[q] & 0xffff0000u) : 0.f;
+    }
+    float sx = 0.f;
+    uint32_t pr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pr[j] = pack_bf16x2(16.f * xv[j], 16.f * xv[j + 4]);
+      sx += xv[j] + xv[j + 4];
+    }
+    dst[wd * NT + col] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+    xw[wd][col] = sx;
+  }
+  __syncthreads();
+  if (tid < NT * GPC) {  // group sums in word order (as k_rtn4_mfma adds them)
+    const int col = tid / GPC, gi = tid % GPC;
+    float sx = 0.f;
+#pragma unroll
+    for (int wd = 0; wd < GW; ++wd) sx += xw[gi * GW + wd][col];
+    xgs[(tile * nch + c) * (NT * GPC) + tid] = sx;
+  }
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+// s_waitcnt immediate (gfx9 encoding): vmcnt(n), expcnt and lgkmcnt left open.
+constexpr int vmcnt_only(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
+
+// One chunk of k_rtn4_mfma_dma: issue chunk c + 1's copies (x' into xn, the
+// group sums into gn), its scales / biases and its weights, then chunk c's
+// MFMAs and folds on xc / gc / sbc, then wait for the copies and the scales,
+// stage the scales into sbn, and meet at the barrier.
+template <int NB, int GW, int SDT>
+__device__ __forceinline__ void rtn4_dma_chunk(
+    const uint32_t* rp, int64_t moff1, int64_t c0, int64_t nwords, const uint4* __restrict__ xq_t,
+    const float* __restrict__ xg_t, const void* __restrict__ scales, const void* __restrict__ biases,
+    int64_t rw0, int64_t n_out, int64_t n_groups, const uint32_t* xc, const float* gc, uint32_t* xn, float* gn,
+    float (*sbc)[kDenseRows][kDenseChunk / GW], float (*sbn)[kDenseRows][kDenseChunk / GW],
+    uint32_t (&wq)[2][4], f32x4d_t (&out)[2][NB], f32x4d_t (&acc)[2][NB]) {
+  constexpr int NT = 16 * NB, MB = 2, GPC = kDenseChunk / GW, SPG = GW / 4;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const bool more = c0 + kDenseChunk < nwords;
+  const int64_t cn = more ? c0 + kDenseChunk : c0, chn = cn / kDenseChunk;
+  // this chunk's weights (loaded during the last one) are in, nothing else is outstanding
+  __builtin_amdgcn_s_waitcnt(0);
+  MA_ISSUE_FENCE();
+  if (more) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i)  // x': NT * 16 slots of 16 bytes, in order
+      __builtin_amdgcn_global_load_lds(xq_t + chn * (kDenseChunk * NT) + tid + 256 * i,
+                                       (lds_ptr_t)(xn + 4 * (64 * wv + 256 * i)), 16, 0, 0);
+    if (wv == 0 && lane < NT * GPC)  // group sums: NT * GPC floats
+      __builtin_amdgcn_global_load_lds(xg_t + chn * (NT * GPC) + lane, (lds_ptr_t)gn, 4, 0, 0);
+  }
+  float sbv[2];
+  {
+    const int which = tid >> 7, rr = tid & 127;
+    int64_t r = rw0 + rr;
+    r = r < n_out ? r : n_out - 1;
+    const void* src = which ? biases : scales;
+#pragma unroll
+    for (int gi = 0; gi < GPC; ++gi) sbv[gi & 1] = ld_t<SDT>(src, r * n_groups + cn / GW + gi);
+  }
+  MA_ISSUE_FENCE();  // the weights are issued last
+  uint32_t wn[MB][4];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) load_chunk_words<GW>(rp + mb * moff1 + cn, wn[mb]);
+  MA_ISSUE_FENCE();
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {  // k-slice s: word chunk_word(g, s) of lane group g
+    u32x4v_t av[MB], bv[NB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const uint32_t wd = wq[mb][s];
+      av[mb] = u32x4v_t{and_or(wd << 3, kMaskQ4d, kOneBf16x2), and_or(wd >> 1, kMaskQ4d, kOneBf16x2),
+                        and_or(wd >> 5, kMaskQ4d, kOneBf16x2), and_or(wd >> 9, kMaskQ4d, kOneBf16x2)};
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      bv[nb] = *reinterpret_cast<const u32x4v_t*>(xc + (chunk_word<GW>(g, s) * NT + nb * 16 + r16) * 4);
+    mfma_block_begin();
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) mfma_acc(acc[mb][nb], av[mb], bv[nb]);
+    mfma_block_end();
+    keep_b(av, acc[0]);
+    keep_b(bv, acc[0]);
+    if ((s + 1) % SPG == 0) {  // end of an RTN group: s acc + (b - 16 s) X, then clear
+      const int gi = s / SPG;
+      float sr[MB][4], br[MB][4];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rr = 32 * wv + 16 * mb + 4 * g + i;
+          sr[mb][i] = sbc[0][rr][gi];
+          br[mb][i] = sbc[1][rr][gi] - 16.f * sr[mb][i];
+        }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const float X = gc[(nb * 16 + r16) * GPC + gi];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)  // the FMAs of k_rtn4_mfma, in its order
+            out[mb][nb][i] = __builtin_fmaf(sr[mb][i], acc[mb][nb][i], __builtin_fmaf(br[mb][i], X, out[mb][nb][i]));
+          acc[mb][nb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
+  }
+  // the copies and the scales have landed (the weights, issued after them, may not have)
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(MB * (GW == 16 ? 1 : 2)));
+  {
+    const int which = tid >> 7, rr = tid & 127;
+#pragma unroll
+    for (int gi = 0; gi < GPC; ++gi) sbn[which][rr][gi] = sbv[gi & 1];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wq[mb][q] = wn[mb][q];
+}
+
+template <int NB, int GW, int SDT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) void k_rtn4_mfma_dma(
+    const uint4* __restrict__ xq, const float* __restrict__ xgs, int64_t batch, const uint32_t* __restrict__ w,
+    int64_t n_out, int64_t nwords, const void* __restrict__ scales, const void* __restrict__ biases,
+    uint16_t* __restrict__ y, int64_t ldy) {
+  constexpr int NT = 16 * NB, MB = 2, GPC = kDenseChunk / GW;
+  // two copies of each buffer, distinct arrays (the compiler then sees that a
+  // chunk's LDS reads and the copies in flight into the other do not overlap)
+  __shared__ __align__(16) uint32_t xa[kDenseChunk * NT * 4], xb[kDenseChunk * NT * 4];
+  __shared__ __align__(16) float ga[NT * GPC], gb[NT * GPC];
+  __shared__ float sb[2][2][kDenseRows][GPC];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t tile = blockIdx.y, t0 = tile * NT;
+  const int64_t rw0 = static_cast<int64_t>(blockIdx.x) * kDenseRows;
+  const int64_t row0 = rw0 + 32 * wv;
+  const int64_t n_groups = nwords / GW, nch = nwords / kDenseChunk;
+  const uint4* const xq_t = xq + tile * nch * (kDenseChunk * NT);
+  const float* const xg_t = xgs + tile * nch * (NT * GPC);
+  // the lane's row of block 0, and block 1's 16 rows further (n_out % 32 ==
+  // 0, so a wave's 32 rows are all in or all past n_out; those past it read
+  // row n_out - 1 and store nothing)
+  const int64_t rb0 = row0 + r16 < n_out ? row0 + r16 : n_out - 1;
+  const int64_t moff1 = row0 + 16 < n_out ? 16 * nwords : 0;
+  const uint32_t* const rp = w + rb0 * nwords + (GW == 16 ? 4 * g : 2 * g);
+  f32x4d_t out[MB][NB], acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) out[mb][nb] = acc[mb][nb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+  // chunk 0: weights, copies, scales
+  uint32_t wq[MB][4];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) load_chunk_words<GW>(rp + mb * moff1, wq[mb]);
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+    __builtin_amdgcn_global_load_lds(xq_t + tid + 256 * i, (lds_ptr_t)(xa + 4 * (64 * wv + 256 * i)), 16, 0, 0);
+  if (wv == 0 && lane < NT * GPC) __builtin_amdgcn_global_load_lds(xg_t + lane, (lds_ptr_t)ga, 4, 0, 0);
+  {
+    const int which = tid >> 7, rr = tid & 127;
+    int64_t r = rw0 + rr;
+    r = r < n_out ? r : n_out - 1;
+    const void* src = which ? biases : scales;
+    float v[2];
+#pragma unroll
+    for (int gi = 0; gi < GPC; ++gi) v[gi & 1] = ld_t<SDT>(src, r * n_groups + gi);
+#pragma unroll
+    for (int gi = 0; gi < GPC; ++gi) sb[0][which][rr][gi] = v[gi & 1];
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < nwords; c0 += 2 * kDenseChunk) {
+    rtn4_dma_chunk<NB, GW, SDT>(rp, moff1, c0, nwords, xq_t, xg_t, scales, biases, rw0, n_out, n_groups, xa, ga, xb, gb,
+                                sb[0], sb[1], wq, out, acc);
+    if (c0 + kDenseChunk < nwords)
+      rtn4_dma_chunk<NB, GW, SDT>(rp, moff1, c0 + kDenseChunk, nwords, xq_t, xg_t, scales, biases, rw0, n_out, n_groups,
+                                  xb, gb, xa, ga, sb[1], sb[0], wq, out, acc);
   }
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -753,4 +998,32 @@ int launch_rtn4_mfma(const uint16_t* x, int64_t batch, int64_t ldx, const uint32
 #undef MA_RT_S
 #undef MA_RT
   return check_launch("rtn4_gemv (mfma)");
+}
+
+// The workspace form: prep launch, then the DMA-fed GEMM (groups of 128;
+// workspace of rtn4_ws_bytes(batch, nwords, 128) bytes, 256-byte aligned;
+// n_out % 32 == 0).  (Groups of 64 hold twice the scales per chunk and spill
+// at the occupancy this form needs; they keep the one-launch k_rtn4_mfma.)
+int launch_rtn4_mfma_ws(const uint16_t* x, int64_t batch, int64_t ldx, const uint32_t* w,
+                        int64_t n_out, int64_t nwords, int64_t group, const void* scales,
+                        const void* biases, int s_dt, uint16_t* y, int64_t ldy, void* workspace,
+                        hipStream_t s) {
+  if (group != 128) return fail(MA_EVALUE, "rtn4_gemv_ws: the workspace form takes groups of 128");
+  const int nb = batch <= 16 ? 1 : 2;
+  const int64_t nt = 16 * nb, tiles = cdiv(batch, nt), chunks = nwords / kDenseChunk;
+  uint4* xq = static_cast<uint4*>(workspace);
+  float* xg = reinterpret_cast<float*>(xq + tiles * chunks * kDenseChunk * nt);
+  dim3 gp(static_cast<unsigned>(tiles), static_cast<unsigned>(chunks));
+  dim3 grid(static_cast<unsigned>(cdiv(n_out, kDenseRows)), static_cast<unsigned>(tiles));
+#define MA_RD(NB, SDT)                                                                                  \
+  hipLaunchKernelGGL((k_rtn4_xprep<NB, 16>), gp, dim3(256), 0, s, x, batch, ldx, nwords, xq, xg);       \
+  hipLaunchKernelGGL((k_rtn4_mfma_dma<NB, 16, SDT>), grid, dim3(256), 0, s, xq, xg, batch, w, n_out,     \
+                     nwords, scales, biases, y, ldy)
+  if (nb == 1) {
+    if (s_dt == MA_F32) { MA_RD(1, MA_F32); } else { MA_RD(1, MA_BF16); }
+  } else {
+    if (s_dt == MA_F32) { MA_RD(2, MA_F32); } else { MA_RD(2, MA_BF16); }
+  }
+#undef MA_RD
+  return check_launch("rtn4_gemv (mfma, workspace)");
 }

@@ -413,10 +413,30 @@ __global__ __launch_bounds__(kSelThreads) void k_flash_select(const uint16_t* __
 
 using namespace ma;
 
-// Batched MFMA path (dense_mfma.hip) for batch >= 5.
+// Batched MFMA path (dense_mfma.hip) for batch >= 5, and its workspace form.
 int launch_rtn4_mfma(const uint16_t* x, int64_t batch, int64_t ldx, const uint32_t* w,
                      int64_t n_out, int64_t nwords, int64_t group, const void* scales,
                      const void* biases, int s_dt, uint16_t* y, int64_t ldy, hipStream_t s);
+int launch_rtn4_mfma_ws(const uint16_t* x, int64_t batch, int64_t ldx, const uint32_t* w,
+                        int64_t n_out, int64_t nwords, int64_t group, const void* scales,
+                        const void* biases, int s_dt, uint16_t* y, int64_t ldy, void* workspace,
+                        hipStream_t s);
+namespace ma {
+size_t rtn4_ws_bytes(int64_t batch, int64_t nwords, int64_t group);
+}  // namespace ma
+
+// Whether a call takes the workspace form: the batched MFMA path (bf16 x,
+// [N, K/8] codes, 16-byte aligned) in groups of 128 over a whole number of
+// 32-row blocks.
+static bool rtn4_ws_form(int x_dtype, int64_t batch, int64_t ldx, const void* x, const void* packed,
+                         int64_t n_out, int64_t nwords, int packed_kn, int scales_dtype, int biases_dtype,
+                         int64_t group_size, const void* y) {
+  return x_dtype == MA_BF16 && !packed_kn && scales_dtype == biases_dtype &&
+         (scales_dtype == MA_BF16 || scales_dtype == MA_F32) && (ldx % 8) == 0 && batch >= 5 &&
+         group_size == 128 && nwords % 16 == 0 && n_out % 32 == 0 &&
+         ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(packed) |
+           reinterpret_cast<uintptr_t>(y)) & 15u) == 0;
+}
 
 extern "C" int ma_rtn4_gemv(const void* x, int x_dtype, int64_t batch, int64_t ldx,
                             const uint32_t* packed, int64_t n_out, int64_t nwords, int packed_kn,
@@ -452,6 +472,31 @@ extern "C" int ma_rtn4_gemv(const void* x, int x_dtype, int64_t batch, int64_t l
                      nwords, packed_kn, scales, scales_dtype, biases, biases_dtype, group_size, y,
                      ldy);
   return check_launch("rtn4_gemv");
+}
+
+extern "C" size_t ma_rtn4_gemv_workspace_bytes(int64_t batch, int64_t nwords, int64_t group_size) {
+  if (batch < 5 || group_size != 128 || nwords < 16 || nwords % 16) return 0;
+  return rtn4_ws_bytes(batch, nwords, group_size);
+}
+
+extern "C" int ma_rtn4_gemv_ws(const void* x, int x_dtype, int64_t batch, int64_t ldx,
+                               const uint32_t* packed, int64_t n_out, int64_t nwords, int packed_kn,
+                               const void* scales, int scales_dtype, const void* biases,
+                               int biases_dtype, int64_t group_size, void* y, int64_t ldy,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  if (batch > 0 && n_out > 0 &&
+      rtn4_ws_form(x_dtype, batch, ldx, x, packed, n_out, nwords, packed_kn, scales_dtype, biases_dtype,
+                   group_size, y)) {
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u) ||
+        workspace_bytes < rtn4_ws_bytes(batch, nwords, group_size))
+      return fail(MA_EVALUE, "rtn4_gemv_ws: workspace missing, misaligned or under %zu bytes",
+                  rtn4_ws_bytes(batch, nwords, group_size));
+    return launch_rtn4_mfma_ws(static_cast<const uint16_t*>(x), batch, ldx, packed, n_out, nwords, group_size,
+                               scales, biases, scales_dtype, static_cast<uint16_t*>(y), ldy, workspace,
+                               static_cast<hipStream_t>(stream));
+  }
+  return ma_rtn4_gemv(x, x_dtype, batch, ldx, packed, n_out, nwords, packed_kn, scales, scales_dtype, biases,
+                      biases_dtype, group_size, y, ldy, stream);
 }
 
 extern "C" int ma_rtn4_embedding(const void* ids, int ids_is_int64, int64_t n_ids,

@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from .. import _lib
+from .. import _lib, workspace
 
 _CODES_PER_WORD = 8
 HEAD_GROUP_SIZE = 64
@@ -98,13 +98,20 @@ def rtn4_gemv(
         x_mat = x_mat.contiguous()
     y = torch.empty(batch, n_out, device=x.device, dtype=x.dtype)
     pw, sc, bs = packed_weight.contiguous(), scales.contiguous(), biases.contiguous()
-    _lib.call(
-        "ma_rtn4_gemv",
+    args = (
         _lib.ptr(x_mat), _lib.dtype_code(x_mat, "x"), batch, x_mat.stride(0) if batch else k_in,
         _lib.ptr(pw), n_out, nwords, int(bool(packed_kn)),
         _lib.ptr(sc), _lib.dtype_code(sc, "scales"), _lib.ptr(bs), _lib.dtype_code(bs, "biases"),
-        int(group_size), _lib.ptr(y), n_out, _lib.stream_of(x),
+        int(group_size), _lib.ptr(y), n_out,
     )
+    # Batched calls in groups of 128 build their x' operands once into a
+    # per-stream workspace (ma_rtn4_gemv_ws); others need none.
+    nbytes = 0 if packed_kn else int(_lib.load().ma_rtn4_gemv_workspace_bytes(batch, nwords, int(group_size)))
+    if nbytes:
+        ws = workspace.get("rtn4", x.device, nbytes, (nwords, int(group_size)))
+        _lib.call("ma_rtn4_gemv_ws", *args, _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
+    else:
+        _lib.call("ma_rtn4_gemv", *args, _lib.stream_of(x))
     return y.reshape(*leading, n_out)
 
 

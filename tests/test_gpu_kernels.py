@@ -389,6 +389,40 @@ def test_rtn4_mfma_batched_vs_oracle(dev, batch, group, n_out):
         assert torch.equal(rtn4_gemv(x, w, sc, bs, group_size=group), y)
 
 
+@pytest.mark.parametrize("batch,n_out", [(5, 4096), (17, 4096), (32, 8192), (64, 4064)])
+def test_rtn4_workspace_form_equals_one_launch(dev, batch, n_out):
+    """ma_rtn4_gemv_ws (groups of 128: x' and group sums built once, copied
+    into LDS by the LDS DMA) gives the bits of the one-launch ma_rtn4_gemv,
+    on two calls in a row; a workspace one byte short is refused."""
+    from maple_amd import _lib
+    group = 128
+    w, sc, bs = synthetic.rtn4_table(n_out, 2048, group, 95 + batch, dev)
+    x = synthetic.randn_bf16((batch, 2048), 96 + batch, dev)
+    nwords = 2048 // 8
+    nbytes = int(_lib.load().ma_rtn4_gemv_workspace_bytes(batch, nwords, group))
+    assert nbytes > 0
+    ws = torch.zeros(nbytes, device=dev, dtype=torch.uint8)
+    args = lambda y: (_lib.ptr(x), _lib.dtype_code(x, "x"), batch, x.stride(0), _lib.ptr(w), n_out, nwords, 0,
+                      _lib.ptr(sc), _lib.dtype_code(sc, "s"), _lib.ptr(bs), _lib.dtype_code(bs, "b"), group,
+                      _lib.ptr(y), n_out)
+    y1 = torch.empty(batch, n_out, device=dev, dtype=torch.bfloat16)
+    _lib.call("ma_rtn4_gemv", *args(y1), _lib.stream_of(x))
+    for _ in range(2):
+        y2 = torch.full((batch, n_out), 7.0, device=dev, dtype=torch.bfloat16)
+        _lib.call("ma_rtn4_gemv_ws", *args(y2), _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2)
+    with pytest.raises(ValueError):
+        _lib.call("ma_rtn4_gemv_ws", *args(y2), _lib.ptr(ws), nbytes - 1, _lib.stream_of(x))
+    # n_out not a whole number of 32-row blocks: the one-launch kernel (no workspace needed)
+    y3 = torch.empty(batch, n_out - 16, device=dev, dtype=torch.bfloat16)
+    _lib.call("ma_rtn4_gemv_ws", _lib.ptr(x), _lib.dtype_code(x, "x"), batch, x.stride(0), _lib.ptr(w),
+              n_out - 16, nwords, 0, _lib.ptr(sc), _lib.dtype_code(sc, "s"), _lib.ptr(bs), _lib.dtype_code(bs, "b"),
+              group, _lib.ptr(y3), n_out - 16, None, 0, _lib.stream_of(x))
+    torch.cuda.synchronize()
+    assert torch.equal(y3, y1[:, : n_out - 16])
+
+
 def test_rtn4_reference_fixture_fp32_and_kn(dev):
     rng = np.random.default_rng(1)
     wf = rng.standard_normal((64, 256)).astype(np.float32)
