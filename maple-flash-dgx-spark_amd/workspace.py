@@ -11,6 +11,8 @@ workspaces and may run concurrently; calls on one stream are ordered by it.
 A HIP graph keeps the workspace of the stream it was captured on; replay it
 in that stream's order relative to eager calls made on the capture stream.
 (The attention workspace belongs to its KV cache, ``gqa_workspace``.)
+The pool also holds per-call scratch that a kernel rewrites on every call (the
+RTN4 GEMM's operands); it carries no timeout word and is never zeroed here.
 
 Every wait in those kernels is bounded (about 0.2 s); a wait that runs out
 sets the workspace's timeout word and the kernel finishes with wrong values
@@ -63,7 +65,9 @@ def register_attention(ws: torch.Tensor) -> torch.Tensor:
 
 
 def _all(idx: int) -> list[tuple[str, torch.Tensor]]:
-    out = [(k[0], ws) for k, ws in _POOL.items() if k[1] == idx]
+    """The workspaces on device ``idx`` that carry a timeout word (per-call
+    scratch kept in the pool, such as the RTN4 GEMM's operands, has none)."""
+    out = [(k[0], ws) for k, ws in _POOL.items() if k[1] == idx and k[0] in TIMEOUT_WORD]
     out += [("attention", ws) for ws in list(_ATTENTION.values()) if ws.device.index == idx]
     return out
 

@@ -96,3 +96,19 @@ def test_check_timeouts_raises_and_rezeroes(monkeypatch):
         workspace.check_timeouts(0)
     assert int(a.count_nonzero()) == 0 and int(b.count_nonzero()) == 0
     workspace.check_timeouts(0)
+
+
+def test_check_timeouts_skips_pooled_scratch(monkeypatch):
+    """Per-call scratch kept in the pool (the RTN4 GEMM's operands) has no
+    timeout word: its contents are never read as one and are left alone."""
+    a = torch.zeros(1024, dtype=torch.uint8)
+    s = torch.full((1024,), 255, dtype=torch.uint8)
+    pool = {("moe_fused", 0, 1, 2048): a, ("rtn4", 0, 1, 256, 64): s}
+    monkeypatch.setattr(workspace, "_POOL", pool)
+    monkeypatch.setattr(workspace, "_ATTENTION", {})
+    monkeypatch.setattr(workspace, "_device_index", lambda d: 0)
+    assert workspace.timed_out_kinds(0) == []
+    a.view(torch.int32)[workspace.TIMEOUT_WORD["moe_fused"]] = 1
+    with pytest.raises(RuntimeError, match="moe_fused"):
+        workspace.check_timeouts(0)
+    assert int(a.count_nonzero()) == 0 and bool((s == 255).all())
