@@ -322,8 +322,15 @@ int ma_moe_grouped_noalloc(const void* x, int64_t ldx, const uint32_t* x_pairs,
  * post-attention add + RMSNorm); otherwise residual may be NULL.  bf16 x and
  * gate weight; row scales (up_gate_alpha, down_alpha) float32 or bf16, both
  * of alpha_dtype.  Built shapes (hidden, inter, top_k): (2048,
- * 768, 8) and (256, 128, 2); experts <= 256; other shapes return MA_EVALUE
- * (use the per-kernel entry points).  workspace:
+ * 768, 8), (2048, 512, 8) and (256, 128, 2); experts <= 256; other shapes
+ * return MA_EVALUE (use the per-kernel entry points).  Two forms of the
+ * launch give the same results to float32 rounding: at top-8 with hidden
+ * 2048 and at most 64 experts, on a GPU of 8 XCDs x 32 compute units that
+ * hands a launch's workgroups to its XCDs in turn (checked once per device),
+ * XCD x computes slot x and its workgroups hand data to each other through
+ * that XCD's L2; otherwise one grid barrier separates SwiGLU and down
+ * (ma_moe_fused_form says which; the environment variable
+ * MAPLE_AMD_MOE_FUSED=grid forces the second form).  workspace:
  * ma_moe_fused_workspace_bytes(...) bytes, zero-filled before its first use
  * and never cleared again (the kernel keeps a call counter there and tags
  * the data it hands between workgroups with it); calls sharing a workspace
@@ -363,6 +370,10 @@ int ma_moe_fused(const void* x, const void* x_add, const void* norm_weight, int 
  * (the reference has no persistent kernel); a query for the choice above. */
 int ma_moe_fused_resident(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k,
                           int64_t* needed, int64_t* capacity);
+
+/* The form ma_moe_fused runs for this shape on the current device: 1 the
+ * XCD split, 0 the one-barrier grid, -1 not built.  No reference counterpart. */
+int ma_moe_fused_form(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k);
 
 /* *out = 1 if any ma_moe_fused call on this workspace timed out waiting
  * (synchronises the stream).  No reference counterpart: the reference has no

@@ -117,6 +117,14 @@ __device__ __forceinline__ void expand_word(uint32_t w, uint32_t e[8], const Exp
   e[7] = and_or(s3, k.m5, k.one);
 }
 
+// Half hh of a packed word's 8 bf16x2 operands (expand_word's e[4 hh .. +3]):
+// one MFMA A operand (8 bf16) per lane.
+__device__ __forceinline__ uint4 expand_half(uint32_t w, int hh, const ExpandConsts& k) {
+  const uint32_t s0 = hh ? w >> 5 : w << 3, s1 = hh ? w >> 9 : w >> 1;
+  return make_uint4(and_or(s0, k.m3, k.one), and_or(s0, k.m5, k.one), and_or(s1, k.m3, k.one),
+                    and_or(s1, k.m5, k.one));
+}
+
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {

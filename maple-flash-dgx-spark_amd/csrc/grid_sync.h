@@ -69,6 +69,11 @@ __device__ inline bool grid_barrier_flags(uint32_t* sub, uint32_t* flags, uint32
   return timed_out != 0;
 }
 
+// At the head of every iteration of a wait loop that reads through a
+// CoherentBuf: the buffer-load builtins count as reads of unchanging memory,
+// so without this clobber the compiler hoists them out of the loop.
+#define MA_POLL_RELOAD() asm volatile("" ::: "memory")
+
 // Device-coherent 8- and 16-byte access through a buffer resource: the sc1 cache policy (the bit agent-scope atomic loads and
 // stores carry on this GPU) sends each access to the coherent level, so a
 // store is visible to workgroups on every XCD once it has completed, without

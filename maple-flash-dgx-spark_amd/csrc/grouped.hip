@@ -767,13 +767,6 @@ __device__ __forceinline__ void gp_tile(int n_rtiles, int& mtile, int& rtile) {
   rtile = slot % n_rtiles;
 }
 
-// Half hh of a packed word's 8 bf16x2 operands (expand_word's e[4 hh .. +3]).
-__device__ __forceinline__ uint4 expand_half(uint32_t w, int hh, const ExpandConsts& k) {
-  const uint32_t s0 = hh ? w >> 5 : w << 3, s1 = hh ? w >> 9 : w >> 1;
-  return make_uint4(and_or(s0, k.m3, k.one), and_or(s0, k.m5, k.one), and_or(s1, k.m3, k.one),
-                    and_or(s1, k.m5, k.one));
-}
-
 // One K step of a wave: 4 row blocks x 4 pair blocks x 4 substeps of
 // v_mfma_f32_16x16x32_bf16.  wq: the lane's two words of its 4 row blocks;
 // xsb: the step's x' in the swizzled layout (pair col0 + 16 nb + r16 has

@@ -1,0 +1,178 @@
+// Shared pieces of the one-launch MoE layer kernels (moe_fused.hip: one grid
+// barrier between SwiGLU and down; moe_xcd.hip: the work split by XCD): the
+// workspace layout and the optional next-projection tail.
+#pragma once
+
+#include "grid_sync.h"
+#include "ternary_engine.h"
+#include "tgemv_fast.h"
+
+namespace ma {
+
+// Workspace layout (256-byte lines of uint32 words; every counter and flag has
+// a line of its own so that arrivals and polls on different ones do not meet):
+//   line 0, word 2     error (1 = a wait timed out)
+//   lines 1 .. 16      h barrier: group arrival counters (line 17 unused)
+//   lines 18 .. 33     group flags, all holding the number of barriers
+//                      passed on this workspace once a barrier is over
+//   lines 34 .. 49     y barrier (calls with a next projection): group
+//                      arrival counters (line 50 unused)
+//   [16 KB, 48 KB)     grid kernel: router logits, one tagged 64-bit word
+//                      (tag << 32 | float bits) per expert every 128 bytes
+//   [48 KB, 64 KB)     grid kernel: h, bf16 [TK * I]
+//   [64 KB, 96 KB)     XCD kernel: each workgroup's call count (one uint32
+//                      every 128 bytes, written only by its workgroup)
+//   [96 KB, 128 KB)    XCD kernel: one 4 KB region per XCD, touched only by
+//                      that XCD's workgroups: 64 tagged router logits, then
+//                      h of the XCD's slot as (tag16 << 16 | bf16) words
+//   [128 KB, 256 KB)   XCD kernel: the weighted down outputs of every slot,
+//                      tagged 64-bit words [8][H]
+constexpr int kSubB = 1, kTopB = kSubB + kBarGroups, kFlags = kTopB + 1;
+constexpr int kSubC = kFlags + kBarGroups, kTopC = kSubC + kBarGroups;
+constexpr size_t kLogitOff = 16384;
+constexpr int kLogitStride = 16;  // uint64 words between logits
+constexpr size_t kMoeWsHeader = 49152;
+constexpr size_t kXEpochOff = 65536, kXRegionOff = 98304, kXRegion = 4096, kXPartOff = 131072;
+constexpr size_t kXWsBytes = kXPartOff + 8 * 2048 * 8;
+static_assert(kTopC < static_cast<int>(kLogitOff / 256), "workspace lines");
+static_assert(kLogitOff + 256 * kLogitStride * 8 <= kMoeWsHeader, "workspace logits");
+static_assert(kMoeWsHeader + 8 * 768 * 2 <= kXEpochOff, "grid kernel h");
+static_assert(kXEpochOff + 256 * 128 <= kXRegionOff && kXRegionOff + 8 * kXRegion <= kXPartOff, "XCD layout");
+
+// Next projection, run by every workgroup of a one-launch layer once its rows
+// of y have been stored with device-coherent stores: nx_out = ternary_gemv(y,
+// nx_w, nx_alpha, rms_weight = nx_rms) -- reference kernels/ternary_gemv.py:
+// 110-146 -- with the standalone fast GEMV's per-lane arithmetic in the same
+// order (so the same bits).  nxw / nxa hold this workgroup's rows (prefetched
+// by the caller: row wg * nx_rq + p * W * RPIH + wv * RPIH + lane / LPRH).
+// A grid barrier (counters at kSubC, release flags at kFlags holding f_old)
+// waits for every workgroup's y.  Returns true if that wait timed out.
+template <int KWH, int LPRH, int W, int NXP>
+__device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, const float* __restrict__ nx_rms,
+                                                float nx_eps, int nx_rows, int nx_rq,
+                                                uint16_t* __restrict__ nx_out, const uint32_t (&nxw)[NXP][KWH],
+                                                const float (&nxa)[NXP], uint32_t* ws, uint32_t f_old, int G,
+                                                int wg, int tid, int lane, int wv, uint64_t t0) {
+  constexpr int NWH = KWH * LPRH;
+  constexpr int NTH = 64 * W;
+  constexpr int RPIH = 64 / LPRH;
+  // y, and its RMS-folded x' pairs (hi and lo words, and the value each pair
+  // carries) for every word of y, laid out so that the LPRH lanes sharing a
+  // row read consecutive entries: word w = LPRH-lane l's KWH-th word i sits at
+  // column i * LPRH + l
+  __shared__ __align__(16) uint4 ys4[KWH * 2][LPRH];  // 8 bf16 of y per entry
+  __shared__ __align__(16) uint32_t pxh[8][NWH], pxl[8][NWH];
+  __shared__ __align__(16) float prr[8][NWH];
+  const int klh = lane % LPRH, subh = lane / LPRH;
+
+  __builtin_amdgcn_s_waitcnt(0);  // this workgroup's y stores have completed
+  __syncthreads();
+  bool timed_out = false;
+  if (wv == 0) timed_out = grid_barrier_flags(ws + kLine * kSubC, ws + kLine * kFlags, f_old, G, wg, lane, t0);
+  __syncthreads();  // every wave waits for the barrier before reading y
+  {  // y (device-coherent) into LDS, and its x' pairs: thread t builds pairs
+     // j0 .. j0 + 3 of word t / 2 (j0 = 4 (t & 1)), each from values j and
+     // j + 8 of the word times their RMS weights
+    constexpr int PIT = (NWH * 2 + NTH - 1) / NTH;
+    uint64_t y0[PIT], y1[PIT], ya[PIT], yb[PIT], wa[PIT][2], wb[PIT][2];
+#pragma unroll
+    for (int k = 0; k < PIT; ++k) {
+      const int t = tid + NTH * k < NWH * 2 ? tid + NTH * k : NWH * 2 - 1;
+      const int w = t >> 1, j0 = 4 * (t & 1);
+      const uint64_t* yp = reinterpret_cast<const uint64_t*>(y + w * 16 + 8 * (t & 1));
+      y0[k] = ld_coh64(yp);  // values 8 (t & 1) .. + 8 of word w, raw
+      y1[k] = ld_coh64(yp + 1);
+      ya[k] = ld_coh64(reinterpret_cast<const uint64_t*>(y + w * 16 + j0));
+      yb[k] = ld_coh64(reinterpret_cast<const uint64_t*>(y + w * 16 + j0 + 8));
+      wa[k][0] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0)[0];
+      wa[k][1] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0)[1];
+      wb[k][0] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0 + 8)[0];
+      wb[k][1] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0 + 8)[1];
+    }
+#pragma unroll
+    for (int k = 0; k < PIT; ++k) {
+      const int t = tid + NTH * k;
+      if (t < NWH * 2) {
+        const int w = t >> 1, j0 = 4 * (t & 1);
+        const int col = (w % KWH) * LPRH + w / KWH;
+        ys4[(w % KWH) * 2 + (t & 1)][w / KWH] =
+            make_uint4(static_cast<uint32_t>(y0[k]), static_cast<uint32_t>(y0[k] >> 32),
+                       static_cast<uint32_t>(y1[k]), static_cast<uint32_t>(y1[k] >> 32));
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j = j0 + jj;
+          const uint32_t ua = static_cast<uint32_t>(ya[k] >> (16 * jj)) & 0xffffu;
+          const uint32_t ub = static_cast<uint32_t>(yb[k] >> (16 * jj)) & 0xffffu;
+          const float ra_w = __uint_as_float(static_cast<uint32_t>(wa[k][jj >> 1] >> (32 * (jj & 1))));
+          const float rb_w = __uint_as_float(static_cast<uint32_t>(wb[k][jj >> 1] >> (32 * (jj & 1))));
+          const float xa = __uint_as_float(ua << 16) * ra_w, xb2 = __uint_as_float(ub << 16) * rb_w;
+          const float f = pair_scale(j);
+          uint16_t ha, la, hb, lb;
+          const float r0 = split_hi_lo(f * xa, ha, la);
+          const float r1 = split_hi_lo(f * xb2, hb, lb);
+          pxh[j][col] = static_cast<uint32_t>(ha) | (static_cast<uint32_t>(hb) << 16);
+          pxl[j][col] = static_cast<uint32_t>(la) | (static_cast<uint32_t>(lb) << 16);
+          prr[j][col] = r0 + r1;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // This lane's slice, in the standalone GEMV's order: sum of squares of
+  // the raw values, then the pairs' correction term.
+  uint32_t xh[KWH][8], xl[KWH][8];
+  float c = 0.f, ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < KWH; ++i) {
+    const uint4 a0 = ys4[i * 2][klh];
+    const uint4 a1 = ys4[i * 2 + 1][klh];
+    const uint32_t u[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float v0 = __uint_as_float(u[q] << 16), v1 = __uint_as_float(u[q] & 0xffff0000u);
+      ss += v0 * v0;
+      ss += v1 * v1;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      xh[i][j] = pxh[j][i * LPRH + klh];
+      xl[i][j] = pxl[j][i * LPRH + klh];
+      const float f = pair_scale(j);
+      c += ((f + 1.0f) / f) * prr[j][i * LPRH + klh];
+    }
+  }
+  ss = group_sum<LPRH>(ss);
+  const float rstd = rsqrtf(ss / static_cast<float>(NWH * 16) + nx_eps);
+  const ExpandConsts kc;
+#pragma unroll
+  for (int p = 0; p < NXP; ++p) {
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < KWH; ++i) {
+      uint32_t e[8];
+      expand_word(nxw[p][i], e, kc);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        acc[j & 1] = dot2(e[j], xh[i][j], acc[j & 1]);
+        acc[j & 1] = dot2(e[j], xl[i][j], acc[j & 1]);
+      }
+    }
+    const float d = group_sum<LPRH>(((acc[0] + acc[1]) - c) * (nxa[p] * rstd));
+    const int rl = p * W * RPIH + wv * RPIH + subh;
+    const int r = wg * nx_rq + rl;
+    if (klh == 0 && rl < nx_rq && r < nx_rows) nx_out[r] = f32_to_bf16(d);
+  }
+  return timed_out;
+}
+
+// The XCD kernel's launcher (moe_xcd.hip): whether it is built for the call's
+// shape, and the launch (same arguments as ma_moe_fused after validation).
+bool moe_xcd_supported(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k);
+int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, int norm_dtype, float eps,
+                   const void* residual, const void* gate_weight, const float* router_bias, int64_t n_experts,
+                   int64_t hidden, int64_t inter, const uint32_t* up_gate, const void* up_gate_alpha,
+                   const uint32_t* down, const void* down_alpha, int alpha_dtype, void* y, int32_t* topk_ids,
+                   float* topk_weight, void* workspace, const uint32_t* next_w, const void* next_alpha,
+                   const float* next_rms, float next_eps, int64_t next_rows, void* next_out, hipStream_t st);
+
+}  // namespace ma

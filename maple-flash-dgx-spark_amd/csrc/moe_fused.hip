@@ -27,31 +27,12 @@
 // coherent path the producers are writing through.)
 // Every wait is bounded (about 0.2 s); on timeout the workspace error word is
 // set and the kernel finishes with wrong values instead of hanging.
-#include "grid_sync.h"
-#include "ternary_engine.h"
-#include "tgemv_fast.h"
+#include "moe_fused.h"
 #include "topk.h"
 
 namespace ma {
 
-// Workspace layout (256-byte lines of uint32 words; every counter and flag has
-// a line of its own so that arrivals and polls on different ones do not meet):
-//   line 0, word 2     error (1 = a wait timed out)
-//   lines 1 .. 16      h barrier: group arrival counters (line 17 unused)
-//   lines 18 .. 33     group flags, all holding the number of barriers
-//                      passed on this workspace once a barrier is over
-//   lines 34 .. 49     y barrier (calls with a next projection): group
-//                      arrival counters (line 50 unused)
-//   [16 KB, 48 KB)     router logits: one tagged 64-bit word (tag << 32 |
-//                      float bits) per expert every 128 bytes, E <= 256
-//   [48 KB ...)        h, bf16 [TK * I]
-constexpr int kSubB = 1, kTopB = kSubB + kBarGroups, kFlags = kTopB + 1;
-constexpr int kSubC = kFlags + kBarGroups, kTopC = kSubC + kBarGroups;
-constexpr size_t kLogitOff = 16384;
-constexpr int kLogitStride = 16;  // uint64 words between logits
-constexpr size_t kMoeWsHeader = 49152;
-static_assert(kTopC < static_cast<int>(kLogitOff / 256), "workspace lines");
-static_assert(kLogitOff + 256 * kLogitStride * 8 <= kMoeWsHeader, "workspace logits");
+// Workspace layout: moe_fused.h.
 
 // The expert of top-k slot s: with BALLOT (E <= 64, s the same in every lane
 // of the wave) the one lane whose expert has rank s, in scalar registers;
@@ -101,13 +82,6 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
   __shared__ float s_wts[TK];
   __shared__ float red[W], red2[W];
   __shared__ float part[W][RPB];
-  // next projection: y, and its RMS-folded x' pairs (hi and lo words, and the
-  // value each pair carries) for every word of y, laid out so that the LPRH
-  // lanes sharing a row read consecutive entries: word w = LPRH-lane l's
-  // KWH-th word i sits at column i * LPRH + l
-  __shared__ __align__(16) uint4 ys4[KWH * 2][LPRH];  // 8 bf16 of y per entry
-  __shared__ __align__(16) uint32_t pxh[8][NWH], pxl[8][NWH];
-  __shared__ __align__(16) float prr[8][NWH];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -518,109 +492,11 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
       y[ro] = f32_to_bf16(v);
   }
 
-  // ---- 5. next projection (optional): nx_out = ternary_gemv(y, nx_w, nx_alpha,
-  // rms_weight = nx_rms) -- reference kernels/ternary_gemv.py:110-146 -- once
-  // every workgroup's rows of y are out, with the standalone fast GEMV's
-  // per-lane arithmetic in the same order (so the same bits).
-  if (nx_w) {
-    __builtin_amdgcn_s_waitcnt(0);  // this workgroup's y stores have completed
-    __syncthreads();
-    if (wv == 0)
-      timed_out = grid_barrier_flags(ws + kLine * kSubC, flags, f0 + 1u, G, wg, lane, t0) || timed_out;
-    __syncthreads();  // every wave waits for the barrier before reading y
-    {  // y (device-coherent) into LDS, and its x' pairs: thread t builds pairs
-       // j0 .. j0 + 3 of word t / 2 (j0 = 4 (t & 1)), each from values j and
-       // j + 8 of the word times their RMS weights
-      constexpr int PIT = (NWH * 2 + NTH - 1) / NTH;
-      uint64_t y0[PIT], y1[PIT], ya[PIT], yb[PIT], wa[PIT][2], wb[PIT][2];
-#pragma unroll
-      for (int k = 0; k < PIT; ++k) {
-        const int t = tid + NTH * k < NWH * 2 ? tid + NTH * k : NWH * 2 - 1;
-        const int w = t >> 1, j0 = 4 * (t & 1);
-        const uint64_t* yp = reinterpret_cast<const uint64_t*>(y + w * 16 + 8 * (t & 1));
-        y0[k] = ld_coh64(yp);  // values 8 (t & 1) .. + 8 of word w, raw
-        y1[k] = ld_coh64(yp + 1);
-        ya[k] = ld_coh64(reinterpret_cast<const uint64_t*>(y + w * 16 + j0));
-        yb[k] = ld_coh64(reinterpret_cast<const uint64_t*>(y + w * 16 + j0 + 8));
-        wa[k][0] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0)[0];
-        wa[k][1] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0)[1];
-        wb[k][0] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0 + 8)[0];
-        wb[k][1] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0 + 8)[1];
-      }
-#pragma unroll
-      for (int k = 0; k < PIT; ++k) {
-        const int t = tid + NTH * k;
-        if (t < NWH * 2) {
-          const int w = t >> 1, j0 = 4 * (t & 1);
-          const int col = (w % KWH) * LPRH + w / KWH;
-          ys4[(w % KWH) * 2 + (t & 1)][w / KWH] =
-              make_uint4(static_cast<uint32_t>(y0[k]), static_cast<uint32_t>(y0[k] >> 32),
-                         static_cast<uint32_t>(y1[k]), static_cast<uint32_t>(y1[k] >> 32));
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const int j = j0 + jj;
-            const uint32_t ua = static_cast<uint32_t>(ya[k] >> (16 * jj)) & 0xffffu;
-            const uint32_t ub = static_cast<uint32_t>(yb[k] >> (16 * jj)) & 0xffffu;
-            const float ra_w = __uint_as_float(static_cast<uint32_t>(wa[k][jj >> 1] >> (32 * (jj & 1))));
-            const float rb_w = __uint_as_float(static_cast<uint32_t>(wb[k][jj >> 1] >> (32 * (jj & 1))));
-            const float xa = __uint_as_float(ua << 16) * ra_w, xb2 = __uint_as_float(ub << 16) * rb_w;
-            const float f = pair_scale(j);
-            uint16_t ha, la, hb, lb;
-            const float r0 = split_hi_lo(f * xa, ha, la);
-            const float r1 = split_hi_lo(f * xb2, hb, lb);
-            pxh[j][col] = static_cast<uint32_t>(ha) | (static_cast<uint32_t>(hb) << 16);
-            pxl[j][col] = static_cast<uint32_t>(la) | (static_cast<uint32_t>(lb) << 16);
-            prr[j][col] = r0 + r1;
-          }
-        }
-      }
-    }
-    __syncthreads();
-    // This lane's slice, in the standalone GEMV's order: sum of squares of
-    // the raw values, then the pairs' correction term.
-    uint32_t xh[KWH][8], xl[KWH][8];
-    float c = 0.f, ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < KWH; ++i) {
-      const uint4 a0 = ys4[i * 2][klh];
-      const uint4 a1 = ys4[i * 2 + 1][klh];
-      const uint32_t u[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const float v0 = __uint_as_float(u[q] << 16), v1 = __uint_as_float(u[q] & 0xffff0000u);
-        ss += v0 * v0;
-        ss += v1 * v1;
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        xh[i][j] = pxh[j][i * LPRH + klh];
-        xl[i][j] = pxl[j][i * LPRH + klh];
-        const float f = pair_scale(j);
-        c += ((f + 1.0f) / f) * prr[j][i * LPRH + klh];
-      }
-    }
-    ss = group_sum<LPRH>(ss);
-    const float rstd = rsqrtf(ss / static_cast<float>(NWH * 16) + nx_eps);
-    const ExpandConsts kc;
-#pragma unroll
-    for (int p = 0; p < NXP; ++p) {
-      float acc[2] = {0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < KWH; ++i) {
-        uint32_t e[8];
-        expand_word(nxw[p][i], e, kc);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          acc[j & 1] = dot2(e[j], xh[i][j], acc[j & 1]);
-          acc[j & 1] = dot2(e[j], xl[i][j], acc[j & 1]);
-        }
-      }
-      const float d = group_sum<LPRH>(((acc[0] + acc[1]) - c) * (nxa[p] * rstd));
-      const int rl = p * W * RPIH + wv * RPIH + subh;
-      const int r = wg * nx_rq + rl;
-      if (klh == 0 && rl < nx_rq && r < nx_rows) nx_out[r] = f32_to_bf16(d);
-    }
-  }
+  // ---- 5. next projection (optional), once every workgroup's rows of y are out
+  if (nx_w)
+    timed_out = next_projection<KWH, LPRH, W, NXP>(y, nx_rms, nx_eps, nx_rows, nx_rq, nx_out, nxw, nxa, ws,
+                                                   f0 + 1u, G, wg, tid, lane, wv, t0) ||
+                timed_out;
   if (__ballot(timed_out) && lane == 0) st_coh32(&ws[2], 1u);
 }
 
@@ -652,7 +528,8 @@ const FusedShape* find_shape(int64_t hidden, int64_t inter, int64_t top_k) {
 }
 
 size_t ws_bytes(int64_t, int, int64_t inter, int64_t top_k) {
-  return kMoeWsHeader + static_cast<size_t>(top_k * inter) * 2;
+  // the XCD form's layout lies past the grid form's (either may run on it)
+  return top_k == 8 && inter <= 768 ? kXWsBytes : kMoeWsHeader + static_cast<size_t>(top_k * inter) * 2;
 }
 
 // The kernel instantiation a call launches (PER = 1 up to 64 experts, else 4).
@@ -739,6 +616,10 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
     return fail(MA_ERUNTIME, "moe_fused: its %d workgroups wait on each other but the device holds %lld at once",
                 s->grid, static_cast<long long>(capacity));
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (moe_xcd_supported(n_experts, hidden, inter, top_k))
+    return moe_xcd_launch(x, x_add, norm_weight, norm_dtype, eps, residual, gate_weight, router_bias, n_experts,
+                          hidden, inter, up_gate, up_gate_alpha, down, down_alpha, alpha_dtype, y, topk_ids,
+                          topk_weight, workspace, next_w, next_alpha, next_rms, next_eps, next_rows, next_out, st);
 #define MA_FUSED_ARGS                                                                            \
   static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(x_add), norm_weight, norm_dtype, \
       eps, static_cast<const uint16_t*>(residual), static_cast<const uint16_t*>(gate_weight),    \
@@ -771,6 +652,11 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
 #undef MA_FUSED_LAUNCH
 #undef MA_FUSED_ARGS
   return check_launch("moe_fused");
+}
+
+extern "C" int ma_moe_fused_form(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k) {
+  if (!find_shape(hidden, inter, top_k)) return -1;
+  return moe_xcd_supported(n_experts, hidden, inter, top_k) ? 1 : 0;
 }
 
 extern "C" int ma_moe_fused_timed_out(const void* workspace, int* out, void* stream) {

@@ -1,0 +1,528 @@
+// One-launch MoE FFN layer for one token, split by XCD (gfx950).
+//
+// Semantics: those of k_moe_fused (moe_fused.hip), i.e. MapleSparseMoeBlock.
+// __call__ at T = 1 (reference src/maple_run/model.py:448-474): router_topk
+// (kernels/router.py:39-126), the expert SwiGLU (kernels/ternary_expert.py:
+// 240-319, h stored bf16), each slot's down projection rounded to bf16
+// (ternary_expert.py:58-122), and the top-k weighted float32 combine in slot
+// order with the residual (fused_norm.py:59-96), y stored bf16; optionally the
+// add + RMSNorm ahead of it (fused_norm.py:31-56) and the next layer's
+// RMS-folded projection after it.
+//
+// Why a second form.  The GPU has 8 XCDs, each with its own L2, and the
+// hardware hands the workgroups of a launch to them in turn (workgroup i runs
+// on XCD (i + o) mod 8, so i / 8 numbers the workgroups of one XCD 0..31).  A
+// store seen through another XCD has to travel through memory: a round trip
+// between workgroups on different XCDs costs ~1.2 us, while a plain store read
+// back with an sc1 load by a workgroup of the same XCD (both through that
+// XCD's L2) costs ~0.33 us.  With top-8 routing there are as many slots as
+// XCDs, so XCD x takes slot x:
+//   1. workgroups 0..7 of each XCD compute the 64 router logits (one per
+//      wave) and publish them, tagged with the call's number, in the XCD's
+//      own region; every workgroup polls its XCD's copy (L2 hits) and ranks
+//      the experts (ties to the lower index), so it knows the expert of its
+//      slot and issues that expert's SwiGLU and down rows at once;
+//   2. workgroup j of XCD x computes outputs [24 j, 24 j + 24) of h_x and
+//      publishes them as tagged bf16 words in the XCD's region; each
+//      workgroup polls all of h_x there (3 KB from its L2), no barrier;
+//   3. it computes rows [64 j, 64 j + 64) of slot x's down projection, rounds
+//      each to bf16, scales it by the slot's routing weight and publishes it
+//      as a tagged float with a device-coherent store;
+//   4. workgroup g polls the 8 slots' values of rows [8 g, 8 g + 8) (one lane
+//      each, the only hand-off between XCDs after the routing), adds them to
+//      the residual in slot order and stores y.
+// Tags: each workgroup keeps its own count of calls on the workspace (written
+// only by itself at the end of a call); every call runs every workgroup, so
+// all counts agree and this call's tag is the count + 1.  Nothing needs
+// clearing between calls.  Every wait is bounded (about 0.2 s); on timeout
+// the workspace error word is set and the kernel finishes with wrong values
+// instead of hanging (and if the workgroups were not spread over the XCDs as
+// assumed, a slot's h would be missing and its waits would time out).
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+
+#include "moe_fused.h"
+
+namespace ma {
+
+constexpr int kXcds = 8;
+constexpr int kXcdWgs = 32;  // workgroups per XCD
+
+__device__ __forceinline__ int xcc_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return static_cast<int>(v & 0xf);
+}
+
+// Stores read back only by workgroups of the same XCD: plain stores, which
+// land in the XCD's L2 (the vector L1 is write-through); the readers' sc1
+// loads (ld_coh*) are served by that L2.
+__device__ __forceinline__ void st_l2_32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void st_l2_64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Shapes: H = 16 * KWH * LPRH with LPRH = 32 (one up/gate row pair per
+// SwiGLU pass), I = 16 * KWI * LPRI, US SwiGLU outputs and UD down passes
+// (64 / LPRI rows each) per wave, 8 waves per workgroup, E <= 64 experts,
+// top-8; ADT the row scales' dtype.
+template <int KWH, int US, int KWI, int LPRI, int UD, int ADT>
+__global__ __launch_bounds__(512) void k_moe_xcd(
+    const uint16_t* __restrict__ xa, const uint16_t* __restrict__ xb,
+    const void* __restrict__ norm_w, int norm_dt, float eps, const uint16_t* __restrict__ residual,
+    const uint16_t* __restrict__ gate_w, const float* __restrict__ bias, int n_exp,
+    const uint32_t* __restrict__ ug, const void* __restrict__ ug_alpha,
+    const uint32_t* __restrict__ dn, const void* __restrict__ dn_alpha,
+    uint16_t* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ wts_out,
+    uint32_t* __restrict__ ws, const uint32_t* __restrict__ nx_w, const void* __restrict__ nx_alpha,
+    const float* __restrict__ nx_rms, float nx_eps, int nx_rows,
+    uint16_t* __restrict__ nx_out) {
+  constexpr int TK = kXcds;  // one slot per XCD
+  constexpr int W = 8;
+  constexpr int LPRH = 32;
+  constexpr int NWH = KWH * LPRH, H = 16 * NWH;
+  constexpr int NWI = KWI * LPRI, I = 16 * NWI;
+  constexpr int XPL = NWH / 64;       // words of x per lane of a router wave
+  constexpr int RPID = 64 / LPRI;     // down rows per wave pass
+  constexpr int RPW = RPID * UD;      // down rows per wave
+  constexpr int FR = H / (kXcds * kXcdWgs);  // y rows finished per workgroup
+  constexpr int RPIH = 64 / LPRH;
+  static_assert(NWH % 64 == 0, "x layout");
+  static_assert(W * US * kXcdWgs == I, "h outputs per XCD");
+  static_assert(W * RPW * kXcdWgs == H, "down rows per XCD");
+  static_assert(FR * TK == 64, "combine: one slot value per lane");
+  static_assert(NWI <= 64 && 4 * I + 512 <= static_cast<int>(kXRegion), "h region");
+
+  __shared__ __align__(16) uint32_t xs[NWH][8];
+  __shared__ float cw[NWH];
+  __shared__ __align__(16) uint32_t hs[NWI][8];
+  __shared__ float hc[NWI];
+  __shared__ uint64_t s_key[64];
+  __shared__ uint32_t s_cnt[W][64];
+  __shared__ __align__(16) uint32_t xbf[NWH][8];  // x in bf16 pairs, for the router waves
+  __shared__ float s_red[W];
+  __shared__ float s_w;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = gridDim.x, wg = blockIdx.x;
+  const int xcd = xcc_id();
+  const int lw = wg >> 3;  // this workgroup's number among its XCD's
+  char* const wsb = reinterpret_cast<char*>(ws);
+  uint32_t* const calls = reinterpret_cast<uint32_t*>(wsb + kXEpochOff) + 32 * wg;
+  uint64_t* const xlog = reinterpret_cast<uint64_t*>(wsb + kXRegionOff + xcd * kXRegion);
+  uint32_t* const xh = reinterpret_cast<uint32_t*>(wsb + kXRegionOff + xcd * kXRegion + 512);
+  uint64_t* const part = reinterpret_cast<uint64_t*>(wsb + kXPartOff);
+  const uint32_t tag = ld_coh32(calls) + 1u;
+  const uint32_t tag16 = tag & 0xffffu;
+  const uint32_t f0 = nx_w ? ld_coh32(&ws[kLine * kFlags + kLine * (wg % kBarGroups)]) : 0u;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  bool timed_out = false;
+
+  // The residual of the y rows this workgroup finishes (wave 0, lanes < FR).
+  const int ro = wg * FR + (lane < FR ? lane : 0);
+  const uint16_t* const res_a = xb ? xa : (residual ? residual : xa);
+  const uint16_t* const res_b = xb ? xb : xa;
+  const uint32_t ra = res_a[ro], rb = res_b[ro];
+
+  // ---- 1. x (optionally add + RMSNorm) staged once per workgroup: thread
+  // t < NWH takes word t, in bf16 (for the router waves) and as x' pairs (for
+  // the SwiGLU rows); then wave w of workgroup j < 8 of an XCD takes router row
+  // 8 j + w (loaded at the start) against x from LDS, lane l words l + 64 i
+  const int re = 8 * lw + wv;
+  const bool router_wave = lw < 8 && re < n_exp;  // wave-uniform
+  uint4 gr[XPL][2];
+  if (router_wave) {
+#pragma unroll
+    for (int i = 0; i < XPL; ++i) {
+      const uint4* gp = reinterpret_cast<const uint4*>(gate_w + static_cast<int64_t>(re) * H + (lane + 64 * i) * 16);
+      gr[i][0] = gp[0];
+      gr[i][1] = gp[1];
+    }
+  }
+  {
+    static_assert(NWH <= 512, "one word of x per thread");
+    const int wc = tid < NWH ? tid : NWH - 1;
+    float v[16];
+    {
+      const uint4 a0 = reinterpret_cast<const uint4*>(xa + wc * 16)[0];
+      const uint4 a1 = reinterpret_cast<const uint4*>(xa + wc * 16)[1];
+      const uint32_t u[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        v[2 * q] = __uint_as_float(u[q] << 16);
+        v[2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
+      }
+    }
+    if (xb) {
+      float nw[16];
+      const uint4 b0 = reinterpret_cast<const uint4*>(xb + wc * 16)[0];
+      const uint4 b1 = reinterpret_cast<const uint4*>(xb + wc * 16)[1];
+      const uint32_t ub[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+      if (norm_dt == MA_F32) {
+        const float4* np = reinterpret_cast<const float4*>(static_cast<const float*>(norm_w) + wc * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 f = np[q];
+          nw[4 * q] = f.x;
+          nw[4 * q + 1] = f.y;
+          nw[4 * q + 2] = f.z;
+          nw[4 * q + 3] = f.w;
+        }
+      } else {
+        const uint4* np = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(norm_w) + wc * 16);
+        const uint4 n0 = np[0], n1 = np[1];
+        const uint32_t un[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          nw[2 * q] = __uint_as_float(un[q] << 16);
+          nw[2 * q + 1] = __uint_as_float(un[q] & 0xffff0000u);
+        }
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        v[2 * q] += __uint_as_float(ub[q] << 16);
+        v[2 * q + 1] += __uint_as_float(ub[q] & 0xffff0000u);
+      }
+      if (tid < NWH) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) ss += v[q] * v[q];
+      }
+      ss = group_sum<64>(ss);
+      if (lane == 0) s_red[wv] = ss;
+      __syncthreads();
+      float ssum = s_red[0];
+#pragma unroll
+      for (int w = 1; w < W; ++w) ssum += s_red[w];
+      const float rstd = rsqrtf(ssum / static_cast<float>(H) + eps);
+#pragma unroll
+      for (int q = 0; q < 16; ++q) v[q] = bf16_to_f32(f32_to_bf16(v[q] * rstd * nw[q]));
+    }
+    if (tid < NWH) {
+      uint32_t pr[8];
+      cw[tid] = prep_word_pairs(v, pr);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        xs[tid][j] = pr[j];
+        xbf[tid][j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
+      }
+    }
+  }
+  __syncthreads();
+  if (router_wave) {
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < XPL; ++i) {
+      const uint4 x0 = *reinterpret_cast<const uint4*>(&xbf[lane + 64 * i][0]);
+      const uint4 x1 = *reinterpret_cast<const uint4*>(&xbf[lane + 64 * i][4]);
+      const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      const uint32_t gw[8] = {gr[i][0].x, gr[i][0].y, gr[i][0].z, gr[i][0].w,
+                              gr[i][1].x, gr[i][1].y, gr[i][1].z, gr[i][1].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dot = dot2(xw[j], gw[j], dot);
+    }
+    const float l = group_sum<64>(dot) + (bias ? bias[re] : 0.f);
+    if (lane == 0) st_l2_64(&xlog[re], (static_cast<uint64_t>(tag) << 32) | __float_as_uint(l));
+  }
+
+  // ---- 2. ranks: wave 0 polls its XCD's copy of the logits (lane e, expert
+  // e) and puts one 64-bit key per expert in LDS (the logit's order bits over
+  // the complemented index: keys differ, ties go to the lower index); wave w
+  // counts, for every expert, the keys [8 w, 8 w + 8) above its own; the
+  // counts sum to the expert's rank, and slot s is the expert of rank s.
+  float lg = -INFINITY;
+  int key = INT_MIN + 1;  // experts past E rank below every logit
+  if (wv == 0) {
+    bool have = lane >= n_exp;
+    for (;;) {
+      if (!have) {
+        const uint64_t q = ld_coh64(&xlog[lane]);
+        have = static_cast<uint32_t>(q >> 32) == tag;
+        lg = __uint_as_float(static_cast<uint32_t>(q));
+      }
+      if (__all(have) || timed_out) break;
+      __builtin_amdgcn_s_sleep(1);
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+    }
+    if (lane < n_exp) key = float_order_key(lg);
+    s_key[lane] = (static_cast<uint64_t>(static_cast<uint32_t>(key) ^ 0x80000000u) << 32) |
+                  static_cast<uint32_t>(~lane);
+  }
+  __syncthreads();
+  uint32_t rank = 0;
+  {
+    const uint64_t mine = s_key[lane];
+#pragma unroll
+    for (int j = 0; j < 64 / W; ++j) rank += s_key[(64 / W) * wv + j] > mine ? 1u : 0u;
+    s_cnt[wv][lane] = rank;
+    __syncthreads();
+    rank = 0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) rank += s_cnt[w][lane];
+  }
+  // this XCD's expert (clamped: only a timed-out wait can leave an absent
+  // expert among the first 8 ranks)
+  const int64_t ex = clamp_id(__builtin_ctzll(__ballot(rank == static_cast<uint32_t>(xcd))), n_exp);
+
+  // ---- 3. weights of slot xcd: this wave's SwiGLU rows (outputs o0 .. o0 +
+  // US, lanes 0..31 the up row and 32..63 the gate row, each lane 16 KWH
+  // contiguous bytes), then its down rows (rows r0 .. r0 + RPW, LPRI lanes per
+  // row), all issued before any arithmetic
+  const int klh = lane % LPRH, half = lane / LPRH;
+  const int o0 = (lw * W + wv) * US;
+  uint32_t wu[US][KWH];
+  float au[US];
+#pragma unroll
+  for (int u = 0; u < US; ++u) {
+    const int64_t row = ex * (2 * I) + o0 + u + half * I;
+    load_words_v<KWH>(ug + row * NWH + klh * KWH, wu[u]);
+    au[u] = ld_t<ADT>(ug_alpha, row);
+  }
+  const int kld = lane % LPRI, subd = lane / LPRI;
+  const int r0 = (lw * W + wv) * RPW;
+  uint32_t wd[UD][KWI];
+  float ad[UD];
+#pragma unroll
+  for (int u = 0; u < UD; ++u) {
+    const int64_t r = ex * H + r0 + u * RPID + subd;
+    load_words_v<KWI>(dn + r * NWI + kld * KWI, wd[u]);
+    ad[u] = ld_t<ADT>(dn_alpha, r);
+  }
+  // Next projection (optional): this workgroup's rows, as in k_moe_fused.
+  constexpr int NXP = 1;
+  const int nx_rq = nx_w ? (nx_rows + G - 1) / G : 0;
+  uint32_t nxw[NXP][KWH];
+  float nxa[NXP];
+  if (nx_w) {
+    const int subh = lane / LPRH;
+#pragma unroll
+    for (int p = 0; p < NXP; ++p) {
+      int r = wg * nx_rq + p * W * RPIH + wv * RPIH + subh;
+      r = r < nx_rows ? r : nx_rows - 1;
+      load_words_v<KWH>(nx_w + static_cast<int64_t>(r) * NWH + klh * KWH, nxw[p]);
+      nxa[p] = ld_t<ADT>(nx_alpha, r);
+    }
+  }
+  MA_ISSUE_FENCE();
+
+  // routing weights while the loads are in flight (wave 0): the softmax over
+  // all E logits with the max-subtracted exp, then p / (sum of the selected p
+  // in slot order + 1e-20)
+  if (wv == 0) {
+    const float m = float_from_order_key(wave_max_ui(key));
+    const float e = lane < n_exp ? expf(lg - m) : 0.f;
+    const float p = e * (1.0f / wave_sum_u(e));
+    float sel = 0.f;
+#pragma unroll
+    for (int s = 0; s < TK; ++s) sel += lane_bcast(p, __builtin_ctzll(__ballot(rank == static_cast<uint32_t>(s))));
+    const float w = p * (1.0f / (sel + 1e-20f));
+    if (lane == ex) s_w = w;
+    if (wg == 0 && rank < static_cast<uint32_t>(TK)) {
+      ids_out[rank] = lane < n_exp ? lane : n_exp - 1;
+      wts_out[rank] = w;
+    }
+  }
+
+  // SwiGLU outputs o0 .. o0 + US of slot xcd, published in the XCD's region
+  {
+    XSlice<KWH> xsl;
+    slice_from_lds<KWH>(xs, cw, klh, xsl);
+    const ExpandConsts kc;
+    float up_t = 0.f, gate_t = 0.f;
+#pragma unroll
+    for (int u = 0; u < US; ++u) {
+      const float v = group_sum_last<LPRH>(slice_dot<KWH>(wu[u], xsl, kc) * au[u]);
+      const float up = lane_bcast(v, LPRH - 1), gt = lane_bcast(v, 2 * LPRH - 1);
+      if (lane == u) {
+        up_t = up;
+        gate_t = gt;
+      }
+    }
+    if (lane < US) st_l2_32(&xh[o0 + lane], (tag16 << 16) | f32_to_bf16(swiglu_act(up_t, gate_t)));
+  }
+
+  // ---- 4. h of slot xcd from the XCD's region: thread t < NWI polls the 16
+  // values of h word t until all carry this call's tag, then builds its x'
+  // pairs
+  if (tid < NWI) {
+    const CoherentBuf hb(xh, 4 * I);
+    uint4 q[4];
+    for (;;) {
+      MA_POLL_RELOAD();
+#pragma unroll
+      for (int k = 0; k < 4; ++k) q[k] = hb.ld4u(static_cast<uint32_t>((16 * tid + 4 * k) * 4));
+      uint32_t bad = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        bad |= ((q[k].x >> 16) ^ tag16) | ((q[k].y >> 16) ^ tag16) | ((q[k].z >> 16) ^ tag16) |
+               ((q[k].w >> 16) ^ tag16);
+      if (__all(bad == 0) || timed_out) break;
+      __builtin_amdgcn_s_sleep(1);
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+    }
+    float hv[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      hv[4 * k] = __uint_as_float(q[k].x << 16);
+      hv[4 * k + 1] = __uint_as_float(q[k].y << 16);
+      hv[4 * k + 2] = __uint_as_float(q[k].z << 16);
+      hv[4 * k + 3] = __uint_as_float(q[k].w << 16);
+    }
+    uint32_t pr[8];
+    hc[tid] = prep_word_pairs(hv, pr);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) hs[tid][j] = pr[j];
+  }
+  __syncthreads();
+
+  // ---- 5. slot xcd's down rows r0 .. r0 + RPW, each rounded to bf16 (as the
+  // reference's ternary_expert_gemv stores it) and scaled by the slot's
+  // routing weight, published for the combining workgroups
+  {
+    XSlice<KWI> hsl;
+    slice_from_lds<KWI>(hs, hc, kld, hsl);
+    const ExpandConsts kc;
+    const float wx = s_w;
+#pragma unroll
+    for (int u = 0; u < UD; ++u) {
+      const float eo = group_sum<LPRI>(slice_dot<KWI>(wd[u], hsl, kc) * ad[u]);
+      const float pv = wx * bf16_to_f32(f32_to_bf16(eo));
+      if (kld == 0)
+        st_coh64(&part[xcd * H + r0 + u * RPID + subd], (static_cast<uint64_t>(tag) << 32) | __float_as_uint(pv));
+    }
+  }
+
+  // ---- 6. rows wg * FR .. + FR of y: lane l of wave 0 polls slot l / FR's
+  // value of row wg * FR + l % FR; y = residual + the slots' values in slot
+  // order
+  if (wv == 0) {
+    const int s = lane / FR, r = lane % FR;
+    float pv = 0.f;
+    for (;;) {
+      const uint64_t q = ld_coh64(&part[s * H + wg * FR + r]);
+      const bool ok = static_cast<uint32_t>(q >> 32) == tag;
+      pv = __uint_as_float(static_cast<uint32_t>(q));
+      if (__all(ok) || timed_out) break;
+      __builtin_amdgcn_s_sleep(1);
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+    }
+    float v = xb ? bf16_to_f32(f32_to_bf16(__uint_as_float(ra << 16) + __uint_as_float(rb << 16)))
+                 : residual ? __uint_as_float(ra << 16) : 0.f;
+#pragma unroll
+    for (int k = 0; k < TK; ++k) v += __shfl(pv, k * FR + r, 64);
+    if (lane < FR) {
+      if (nx_w)
+        st_coh16(&y[wg * FR + lane], f32_to_bf16(v));  // read back by every workgroup below
+      else
+        y[wg * FR + lane] = f32_to_bf16(v);
+    }
+  }
+
+  // ---- 7. next projection (optional), once every workgroup's rows of y are out
+  if (nx_w)
+    timed_out = next_projection<KWH, LPRH, W, NXP>(y, nx_rms, nx_eps, nx_rows, nx_rq, nx_out, nxw, nxa, ws, f0,
+                                                   G, wg, tid, lane, wv, t0) ||
+                timed_out;
+  if (__ballot(timed_out) && lane == 0) st_coh32(&ws[2], 1u);
+  if (tid == 0) st_coh32(calls, tag);
+}
+
+// Whether workgroup i of a launch runs on XCD (i + o) mod 8 for one o, so
+// that i / 8 numbers each XCD's workgroups 0..31: one probe launch per device
+// (the grid and block of the layer) that records every workgroup's XCD.
+__global__ __launch_bounds__(512) void k_xcd_probe(uint32_t* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = static_cast<uint32_t>(xcc_id());
+}
+
+namespace {
+
+int xcd_layout_ok(bool* ok) {
+  static std::mutex mu;
+  static int known[64];  // 0 unknown, 1 yes, 2 no
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(MA_ERUNTIME, "no current HIP device");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!known[dev]) {
+    constexpr int G = kXcds * kXcdWgs;
+    uint32_t* d = nullptr;
+    uint32_t h[G];
+    if (hipMalloc(&d, G * 4) != hipSuccess) return fail(MA_ERUNTIME, "moe_fused: XCD probe allocation failed");
+    hipLaunchKernelGGL(k_xcd_probe, dim3(G), dim3(512), 0, nullptr, d);
+    const bool copied = hipGetLastError() == hipSuccess && hipMemcpy(h, d, G * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    hipFree(d);
+    if (!copied) return fail(MA_ERUNTIME, "moe_fused: XCD probe failed");
+    bool good = true;
+    const uint32_t o = (h[0] + kXcds) % kXcds;  // XCD of workgroup 0
+    for (int i = 0; i < G; ++i) good = good && h[i] == (i + o) % kXcds;
+    known[dev] = good ? 1 : 2;
+  }
+  *ok = known[dev] == 1;
+  return MA_OK;
+}
+
+template <int ADT>
+const void* xcd_kernel_t(int64_t inter) {
+  return inter == 768 ? reinterpret_cast<const void*>(&k_moe_xcd<4, 3, 3, 16, 2, ADT>)
+                      : reinterpret_cast<const void*>(&k_moe_xcd<4, 2, 2, 16, 2, ADT>);
+}
+
+}  // namespace
+
+bool moe_xcd_supported(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k) {
+  if (!(hidden == 2048 && (inter == 768 || inter == 512) && top_k == kXcds && n_experts >= top_k &&
+        n_experts <= 64))
+    return false;
+  const char* force = getenv("MAPLE_AMD_MOE_FUSED");  // "grid": the one-barrier form (A/B timing)
+  if (force && strcmp(force, "grid") == 0) return false;
+  int cus = 0, dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus != kXcds * kXcdWgs)
+    return false;
+  int64_t capacity = 0;  // every workgroup resident (the grid form is used otherwise)
+  if (resident_capacity(xcd_kernel_t<MA_BF16>(inter), 512, &capacity) != MA_OK || capacity < kXcds * kXcdWgs)
+    return false;
+  bool ok = false;
+  return xcd_layout_ok(&ok) == MA_OK && ok;
+}
+
+int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, int norm_dtype, float eps,
+                   const void* residual, const void* gate_weight, const float* router_bias, int64_t n_experts,
+                   int64_t hidden, int64_t inter, const uint32_t* up_gate, const void* up_gate_alpha,
+                   const uint32_t* down, const void* down_alpha, int alpha_dtype, void* y, int32_t* topk_ids,
+                   float* topk_weight, void* workspace, const uint32_t* next_w, const void* next_alpha,
+                   const float* next_rms, float next_eps, int64_t next_rows, void* next_out, hipStream_t st) {
+  (void)hidden;
+  const void* kern = alpha_dtype == MA_F32 ? xcd_kernel_t<MA_F32>(inter) : xcd_kernel_t<MA_BF16>(inter);
+  int64_t capacity = 0;
+  if (int rc = resident_capacity(kern, 512, &capacity)) return rc;
+  if (capacity < kXcds * kXcdWgs)
+    return fail(MA_ERUNTIME, "moe_fused: its %d workgroups wait on each other but the device holds %lld at once",
+                kXcds * kXcdWgs, static_cast<long long>(capacity));
+#define MA_XCD_ARGS                                                                                      \
+  static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(x_add), norm_weight, norm_dtype, eps,   \
+      static_cast<const uint16_t*>(residual), static_cast<const uint16_t*>(gate_weight), router_bias,    \
+      static_cast<int>(n_experts), up_gate, up_gate_alpha, down, down_alpha, static_cast<uint16_t*>(y), \
+      topk_ids, topk_weight, static_cast<uint32_t*>(workspace), next_w, next_alpha, next_rms, next_eps, \
+      static_cast<int>(next_rows), static_cast<uint16_t*>(next_out)
+  const dim3 grid(kXcds * kXcdWgs), block(512);
+  if (alpha_dtype == MA_F32) {
+    if (inter == 768)
+      hipLaunchKernelGGL((k_moe_xcd<4, 3, 3, 16, 2, MA_F32>), grid, block, 0, st, MA_XCD_ARGS);
+    else
+      hipLaunchKernelGGL((k_moe_xcd<4, 2, 2, 16, 2, MA_F32>), grid, block, 0, st, MA_XCD_ARGS);
+  } else {
+    if (inter == 768)
+      hipLaunchKernelGGL((k_moe_xcd<4, 3, 3, 16, 2, MA_BF16>), grid, block, 0, st, MA_XCD_ARGS);
+    else
+      hipLaunchKernelGGL((k_moe_xcd<4, 2, 2, 16, 2, MA_BF16>), grid, block, 0, st, MA_XCD_ARGS);
+  }
+#undef MA_XCD_ARGS
+  return check_launch("moe_fused");
+}
+
+}  // namespace ma

@@ -73,6 +73,13 @@ def fused_supported(layer: MoELayer, top_k: int, x: torch.Tensor) -> bool:
     return fused_resident(layer, top_k, x.device)
 
 
+def fused_form(layer: MoELayer, top_k: int) -> int:
+    """The form ``ma_moe_fused`` runs for this layer on the current device:
+    1 the XCD split (each XCD one top-k slot), 0 the one-barrier grid, -1 not
+    built."""
+    return int(_lib.load().ma_moe_fused_form(layer.n_experts, layer.hidden, layer.inter, top_k))
+
+
 def moe_fused_timed_out(device: torch.device | int = 0) -> bool:
     """True if a one-launch MoE call on ``device`` timed out waiting for another
     workgroup since its workspace was zeroed (the kernel records it instead of

@@ -215,3 +215,42 @@ def test_fused_rejects_unbuilt_shape(dev):
     L = synthetic.make_moe_layer(512, 8, 256, seed=1, device=dev)
     with pytest.raises(ValueError):
         moe_fused(synthetic.randn_bf16((1, 512), 1, dev), L, 2)
+
+
+@pytest.mark.parametrize("inter", [768, 512])
+def test_fused_forms_vs_oracle_on_one_workspace(dev, monkeypatch, inter):
+    """Both forms of the one-launch layer (the XCD split and the one-barrier
+    grid, forced by MAPLE_AMD_MOE_FUSED=grid) against the oracle, alternating
+    on one workspace (each form's tags must survive the other's calls), and
+    against each other: the same ids on tie-safe rows, y within the bar."""
+    from maple_amd.moe import fused_form
+
+    Ls = [synthetic.make_moe_layer(2048, 64, inter, seed=70 + i, device=dev) for i in range(2)]
+    assert fused_form(Ls[0], 8) == 1, "the XCD split is expected on an 8-XCD MI355X"
+    outs = {}
+    for step in range(6):
+        form = "grid" if step % 2 else "xcd"
+        if form == "grid":
+            monkeypatch.setenv("MAPLE_AMD_MOE_FUSED", "grid")
+            assert fused_form(Ls[0], 8) == 0
+        else:
+            monkeypatch.delenv("MAPLE_AMD_MOE_FUSED", raising=False)
+        L = Ls[(step // 2) % 2]
+        x = synthetic.randn_bf16((1, 2048), 800 + step // 2, dev)
+        res = synthetic.randn_bf16((1, 2048), 900 + step // 2, dev)
+        y, ids, wts = moe_fused(x, L, 8, res)
+        torch.cuda.synchronize()
+        ref = _oracle(np_f(x), L, ids, wts, 8, np_f(res))
+        assert_bf16_close(np_f(y), ref, atol_frac=Y_ATOL, what=f"{form} I{inter} step {step}")
+        outs.setdefault(step // 2, {})[form] = (y, ids, wts)
+    monkeypatch.delenv("MAPLE_AMD_MOE_FUSED", raising=False)
+    for k, pair in outs.items():
+        (y1, i1, w1), (y2, i2, w2) = pair["xcd"], pair["grid"]
+        x = synthetic.randn_bf16((1, 2048), 800 + k, dev)
+        _, _, probs = ok.router_topk(np_f(x), np_f(Ls[k % 2].gate_weight), 8)
+        if not tie_safe_rows(probs, 8).all():
+            continue  # a near-tie may order the two forms' experts differently
+        assert torch.equal(i1, i2), f"pair {k}: ids"
+        torch.testing.assert_close(w1, w2, rtol=1e-5, atol=1e-7)
+        assert_bf16_close(np_f(y1), np_f(y2), atol_frac=Y_ATOL, what=f"xcd vs grid {k}")
+    assert not moe_fused_timed_out(dev)
