@@ -381,6 +381,7 @@ constexpr int kErWaves = 8;
 // synthetic model's hidden 2048 and intermediate 768; other sizes take the
 // K-split forms).
 constexpr int kErChunksUp = 8, kErChunksDown = 3;
+constexpr int kErAhead = 2;  // weight chunks in flight per wave ahead of the MFMAs
 
 // SwiGLU: BPW up blocks (and the matching gate blocks) per wave; x' pairs of
 // the tile's tokens (x_pairs [T, K / 2] uint32, x_corr [T]) staged in LDS.
@@ -425,16 +426,24 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_swiglu_er(
   }
   float cx = 0.f;
   if (tid < 16 && s_tok[tid] >= 0) cx = x_corr[s_tok[tid]];
-  // weights of this wave's blocks for all of K
-  u32x4v_t wq[2 * BPW][NCH];
+  // weights of this wave's blocks, chunk by chunk, kErAhead chunks ahead of
+  // their use: with every wave's whole share requested at once (16 KB), the
+  // tile's x' loads queued behind the other workgroups' weight streams for
+  // ~6 us before the first MFMA could start; a short pipeline keeps the
+  // queues short, and the MFMAs run while the later chunks stream
+  const uint32_t* rp[2 * BPW];
 #pragma unroll
   for (int j = 0; j < 2 * BPW; ++j) {
     int64_t blk = b0 + (j % BPW);
     blk = blk < nblk ? blk : nblk - 1;
-    const uint32_t* rp = we + ((j / BPW) * n_half + blk * 16 + r16) * NW + 4 * g;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) wq[j][c] = *reinterpret_cast<const u32x4v_t*>(rp + 16 * c);
+    rp[j] = we + ((j / BPW) * n_half + blk * 16 + r16) * NW + 4 * g;
   }
+  u32x4v_t wq[2 * BPW][NCH];
+#pragma unroll
+  for (int c = 0; c < kErAhead && c < NCH; ++c)
+#pragma unroll
+    for (int j = 0; j < 2 * BPW; ++j) wq[j][c] = *reinterpret_cast<const u32x4v_t*>(rp[j] + 16 * c);
+  MA_ISSUE_FENCE();
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int it = tid + 64 * kErWaves * k;
@@ -450,6 +459,12 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_swiglu_er(
   const ExpandConsts kc;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
+    if (c + kErAhead < NCH) {
+#pragma unroll
+      for (int j = 0; j < 2 * BPW; ++j)
+        wq[j][c + kErAhead] = *reinterpret_cast<const u32x4v_t*>(rp[j] + 16 * (c + kErAhead));
+    }
+    MA_ISSUE_FENCE();
 #pragma unroll
     for (int q0 = 0; q0 < 4; q0 += QPB) {  // QPB words per MFMA block
       u32x4v_t av[QPB][2 * BPW][2], bv[QPB][2];
@@ -541,7 +556,8 @@ __global__ __launch_bounds__(64 * kErWaves) void k_grouped_down_er(
       sv[k][1] = src[1];
     }
   }
-  // weights of this wave's blocks for all of K
+  // weights of this wave's blocks for all of K (a pipeline as in the SwiGLU
+  // stage measured no faster here: K is only 3 chunks)
   u32x4v_t wq[BPW][NCH];
 #pragma unroll
   for (int j = 0; j < BPW; ++j) {
