@@ -16,7 +16,9 @@ its own cold layer.  ``value`` is the whole-layer algorithmic HBM throughput:
 per layer, times layers and steps, over the timed time.
 
 ``roofline`` covers the dominant kernel, which is the whole layer here
-(``k_moe_fused``): algorithmic bytes per launch over its average launch
+(``k_moe_xcd``, the form of ``ma_moe_fused`` that splits the layer by XCD, or
+``k_moe_fused`` where that form does not apply -- ``ma_moe_fused_form`` says
+which ran): algorithmic bytes per launch over its average launch
 period, timed with HIP events on the stream it runs on over the graph of
 back-to-back launches (the period includes the dispatch gap between dependent
 kernels, so it is an upper bound on the kernel's own duration).  ``traffic``
@@ -542,7 +544,10 @@ def main() -> int:
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
     value = nb["layer"] * L / (ms * 1e-3) / 1e9
-    per_launch = ms * 1e-3 / L  # the whole layer is one k_moe_fused launch
+    per_launch = ms * 1e-3 / L  # the whole layer is one launch of ma_moe_fused
+    from maple_amd.moe import fused_form
+    xcd_form = fused_form(layers[0], TOPK) == 1
+    kname, tname = ("k_moe_xcd", "moe_xcd_bs1") if xcd_form else ("k_moe_fused", "moe_fused_bs1")
     achieved = nb["layer"] / per_launch / 1e9
     log(f"MoE layer bs1: {ms * 1e3 / L:.2f} us/layer, {value:.1f} GB/s (wall {wall:.3f} s)")
     del g
@@ -576,7 +581,7 @@ def main() -> int:
                    "per_slot_chain_us_per_layer": round(per_slot * 1e6, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic("moe_fused_bs1"), "kernel": "k_moe_fused",
+                     "traffic": read_traffic(tname), "kernel": kname,
                      "bytes_per_launch": nb["layer"],
                      "us_per_launch": round(per_launch * 1e6, 3)},
         "cpu_baseline": None,
