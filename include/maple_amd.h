@@ -454,6 +454,20 @@ int ma_decode_attn_o_supported(int64_t batch, int n_heads, int n_kv_heads, int h
                                int64_t max_len, int64_t window, int64_t o_rows);
 
 /*
+ * Row-wise ternarisation (the converter's step): for each of `rows` rows of
+ * k_in values of `weight` (float32, bfloat16 or float16; k_in a multiple of
+ * 128, at most 8192): thr = threshold_scale * mean|w|, mask = |w| > thr,
+ * row_alpha = sum(|w| * mask) / max(sum(mask), 1) in the weight dtype, and
+ * packed uint32 [rows, k_in / 16] = codes sign(w) * mask + 1, 16 per word,
+ * least significant first.  The means and sums are taken in float32 in
+ * NumPy's pairwise summation order, so codes and row_alpha are the bits the
+ * reference's NumPy converter produces.  Replaces ternarize,
+ * src/maple_run/pack.py:120-149.
+ */
+int ma_ternarize(const void* weight, int dtype, int64_t rows, int64_t k_in, float threshold_scale,
+                 uint32_t* packed, void* row_alpha, void* stream);
+
+/*
  * Greedy choice: out[r] = argmax over the n values of row r (bf16 or float32,
  * row stride ldx), the lowest index on ties; out int64
  * [rows].  Replaces torch.argmax(logits, dim=-1) of the greedy step,

@@ -63,6 +63,7 @@ _SIGNATURES = {
     "ma_moe_route": [_P, _P, _L, _L, _P, _I, _F, _P, _P, _L, _I, _P, _P, _P, _P, _P, _P, _P, _P,
                      _P, _P, _P, _Z, _P],
     "ma_argmax_rows": [_P, _I, _L, _L, _L, _P, _P],
+    "ma_ternarize": [_P, _I, _L, _L, _F, _P, _P, _P],
     "ma_ternary_gemv_combine_ws": [_P, _P, _P, _L, _P, _P, _L, _P, _L, _L, _P, _I, _P, _I, _F, _P, _L,
                                    _P, _Z, _P],
     "ma_moe_grouped": [_P, _L, _P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _L, _L, _P, _P, _P, _P, _P,

@@ -19,6 +19,12 @@ __device__ __forceinline__ void load_words_v(const uint32_t* __restrict__ p, uin
       out[4 * i + 2] = v.z;
       out[4 * i + 3] = v.w;
     }
+  } else if constexpr (KW == 3) {  // one 12-byte load (global_load_dwordx3) instead of three
+    typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
+    const u32x3_t v = *reinterpret_cast<const u32x3_t*>(p);
+    out[0] = v.x;
+    out[1] = v.y;
+    out[2] = v.z;
   } else if constexpr (KW % 2 == 0) {
 #pragma unroll
     for (int i = 0; i < KW / 2; ++i) {

@@ -151,3 +151,46 @@ def test_bf16_round_known_values():
     # 1 + 3*2^-8 ties between 1+2^-7 and 1+2^-6: even is 1 + 2^-6.
     np.testing.assert_array_equal(out[:4], np.array([1.0, 1.0, 1.0 + 2**-6, -2.5], np.float32))
     assert out[5] == np.inf
+
+
+def _pairwise_f32(a: np.ndarray) -> np.float32:
+    """NumPy's float32 pairwise summation restated step by step -- the order
+    the device ternarisation (csrc/ternarize.hip) uses for its means and sums."""
+    n = len(a)
+    if n < 8:
+        r = np.float32(0)
+        for x in a:
+            r = np.float32(r + x)
+        return r
+    if n <= 128:
+        r = [np.float32(a[j]) for j in range(8)]
+        i = 8
+        while i < n - n % 8:
+            for j in range(8):
+                r[j] = np.float32(r[j] + a[i + j])
+            i += 8
+        res = np.float32(np.float32(np.float32(r[0] + r[1]) + np.float32(r[2] + r[3]))
+                         + np.float32(np.float32(r[4] + r[5]) + np.float32(r[6] + r[7])))
+        while i < n:
+            res = np.float32(res + a[i])
+            i += 1
+        return res
+    n2 = n // 2
+    n2 -= n2 % 8
+    return np.float32(_pairwise_f32(a[:n2]) + _pairwise_f32(a[n2:]))
+
+
+@pytest.mark.parametrize("k", [128, 384, 640, 768, 2048, 4096])
+def test_pairwise_order_is_numpys(k):
+    """The summation order the device ternarisation follows gives the bits of
+    NumPy's float32 np.sum and np.mean over a row (the reference's mean|w| and
+    sum(|w| * mask)); a first-element start, a plausible alternative, differs."""
+    rng = np.random.default_rng(k)
+    differs = 0
+    for t in range(24):
+        a = np.abs(rng.standard_normal(k).astype(np.float32) * np.float32(10.0 ** rng.uniform(-3, 3)))
+        s = _pairwise_f32(a)
+        assert s == np.sum(a[None, :], axis=-1)[0]
+        assert np.float32(s / np.float32(k)) == np.mean(a[None, :], axis=-1, keepdims=True)[0, 0]
+        differs += np.float32(a[0] + _pairwise_f32(a[1:])) != s
+    assert differs > 0
