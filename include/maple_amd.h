@@ -326,7 +326,10 @@ int ma_moe_grouped_noalloc(const void* x, int64_t ldx, const uint32_t* x_pairs,
  * return MA_EVALUE (use the per-kernel entry points).  Two forms of the
  * launch give the same results to float32 rounding: at top-8 with hidden
  * 2048 and at most 64 experts, on a GPU of 8 XCDs x 32 compute units that
- * hands a launch's workgroups to its XCDs in turn (checked once per device),
+ * hands a launch's workgroups to its XCDs in turn (checked once per device,
+ * by a probe launch on the call's stream that synchronises it -- the first
+ * call outside graph capture; a call captured before that runs the second
+ * form),
  * XCD x computes slot x and its workgroups hand data to each other through
  * that XCD's L2; otherwise one grid barrier separates SwiGLU and down
  * (ma_moe_fused_form says which; the environment variable
@@ -372,7 +375,8 @@ int ma_moe_fused_resident(int64_t n_experts, int64_t hidden, int64_t inter, int6
                           int64_t* needed, int64_t* capacity);
 
 /* The form ma_moe_fused runs for this shape on the current device: 1 the
- * XCD split, 0 the one-barrier grid, -1 not built.  No reference counterpart. */
+ * XCD split, 0 the one-barrier grid, -1 not built (may run the one-time probe
+ * above on the null stream).  No reference counterpart. */
 int ma_moe_fused_form(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k);
 
 /* *out = 1 if any ma_moe_fused call on this workspace timed out waiting

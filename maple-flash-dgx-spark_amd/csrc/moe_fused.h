@@ -167,7 +167,7 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
 
 // The XCD kernel's launcher (moe_xcd.hip): whether it is built for the call's
 // shape, and the launch (same arguments as ma_moe_fused after validation).
-bool moe_xcd_supported(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k);
+bool moe_xcd_supported(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k, hipStream_t st);
 int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, int norm_dtype, float eps,
                    const void* residual, const void* gate_weight, const float* router_bias, int64_t n_experts,
                    int64_t hidden, int64_t inter, const uint32_t* up_gate, const void* up_gate_alpha,

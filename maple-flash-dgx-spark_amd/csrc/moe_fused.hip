@@ -616,7 +616,7 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
     return fail(MA_ERUNTIME, "moe_fused: its %d workgroups wait on each other but the device holds %lld at once",
                 s->grid, static_cast<long long>(capacity));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (moe_xcd_supported(n_experts, hidden, inter, top_k))
+  if (moe_xcd_supported(n_experts, hidden, inter, top_k, st))
     return moe_xcd_launch(x, x_add, norm_weight, norm_dtype, eps, residual, gate_weight, router_bias, n_experts,
                           hidden, inter, up_gate, up_gate_alpha, down, down_alpha, alpha_dtype, y, topk_ids,
                           topk_weight, workspace, next_w, next_alpha, next_rms, next_eps, next_rows, next_out, st);
@@ -656,7 +656,7 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
 
 extern "C" int ma_moe_fused_form(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k) {
   if (!find_shape(hidden, inter, top_k)) return -1;
-  return moe_xcd_supported(n_experts, hidden, inter, top_k) ? 1 : 0;
+  return moe_xcd_supported(n_experts, hidden, inter, top_k, nullptr) ? 1 : 0;
 }
 
 extern "C" int ma_moe_fused_timed_out(const void* workspace, int* out, void* stream) {

@@ -254,3 +254,51 @@ def test_fused_forms_vs_oracle_on_one_workspace(dev, monkeypatch, inter):
         torch.testing.assert_close(w1, w2, rtol=1e-5, atol=1e-7)
         assert_bf16_close(np_f(y1), np_f(y2), atol_frac=Y_ATOL, what=f"xcd vs grid {k}")
     assert not moe_fused_timed_out(dev)
+
+
+_FIRST_CALL_CAPTURED = r"""
+import os, sys, torch
+sys.path.insert(0, sys.argv[1])
+import __graft_entry__ as ge
+ge.load_package()
+from maple_amd import synthetic
+from maple_amd.moe import moe_fused, fused_form, moe_fused_timed_out
+dev = torch.device("cuda:0")
+L = synthetic.make_moe_layer(2048, 64, 768, seed=91, device=dev)
+x = synthetic.randn_bf16((1, 2048), 92, dev)
+torch.cuda.synchronize()
+s = torch.cuda.Stream()
+with torch.cuda.stream(s):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):          # the process's first ma_moe_fused call
+        y, ids, wts = moe_fused(x, L, 8)
+    outs = []
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        outs.append(y.clone())
+form = fused_form(L, 8)                          # the probe runs now, outside capture
+os.environ["MAPLE_AMD_MOE_FUSED"] = "grid"
+y_grid, ids_grid, _ = moe_fused(x, L, 8)
+torch.cuda.synchronize()
+assert all(torch.equal(o, y_grid) for o in outs), "captured call != eager one-barrier form"
+assert torch.equal(ids, ids_grid)
+assert not moe_fused_timed_out(dev)
+print("FORM", form)
+"""
+
+
+def test_first_call_inside_graph_capture(dev):
+    """The XCD form's one-time probe synchronises, so it cannot run under graph
+    capture: a process whose first one-launch call is captured gets the
+    one-barrier form in the graph (the same bits as that form eagerly), and
+    the probe runs at the first call outside capture."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parents[1])
+    res = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED, root], capture_output=True, text=True,
+                         timeout=300)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-3000:]
+    assert "FORM 1" in res.stdout, res.stdout[-2000:]
