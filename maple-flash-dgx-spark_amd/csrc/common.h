@@ -23,6 +23,20 @@ int check_launch(const char* what);
 // whose workgroups wait on each other check their grid against it.
 int resident_capacity(const void* kernel, int threads, int64_t* capacity);
 
+// The GPU's XCDs (gfx950: 8, each with its own L2) and the XCD a workgroup
+// runs on.  Workgroups on one XCD can hand data to each other through its L2
+// (a plain store read back with a device-coherent load); across XCDs the data
+// goes through memory.  xcd_round_robin: whether the current device hands a
+// launch's workgroups to its XCDs in turn (workgroup i on XCD (i + o) mod
+// kXcds), checked once per device by a probe launch on ``st`` (runtime.hip).
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcc_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return static_cast<int>(v & 0xf);
+}
+int xcd_round_robin(hipStream_t st, bool* ok);
+
 // ---------------------------------------------------------------------------
 // Scalar conversions.  bf16 is carried as raw uint16 bits.
 // ---------------------------------------------------------------------------

@@ -40,20 +40,12 @@
 // assumed, a slot's h would be missing and its waits would time out).
 #include <cstdlib>
 #include <cstring>
-#include <mutex>
 
 #include "moe_fused.h"
 
 namespace ma {
 
-constexpr int kXcds = 8;
 constexpr int kXcdWgs = 32;  // workgroups per XCD
-
-__device__ __forceinline__ int xcc_id() {
-  uint32_t v;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-  return static_cast<int>(v & 0xf);
-}
 
 // Stores read back only by workgroups of the same XCD: plain stores, which
 // land in the XCD's L2 (the vector L1 is write-through); the readers' sc1
@@ -431,49 +423,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   if (tid == 0) st_coh32(calls, tag);
 }
 
-// Whether workgroup i of a launch runs on XCD (i + o) mod 8 for one o, so
-// that i / 8 numbers each XCD's workgroups 0..31: one probe launch per device
-// (the grid and block of the layer) records every workgroup's XCD into a
-// static array (no allocation), read back once.
-constexpr int kProbeWgs = kXcds * kXcdWgs;
-__device__ uint32_t g_xcd_probe[kProbeWgs];
-
-__global__ __launch_bounds__(512) void k_xcd_probe(uint32_t* out) {
-  if (threadIdx.x == 0) out[blockIdx.x] = static_cast<uint32_t>(xcc_id());
-}
-
 namespace {
-
-// Runs the probe on stream ``st`` the first time per device (it synchronises
-// the stream); while ``st`` is being captured into a graph the probe cannot
-// run, so the answer is "no" (the one-barrier form) and nothing is cached.
-int xcd_layout_ok(hipStream_t st, bool* ok) {
-  static std::mutex mu;
-  static int known[64];  // 0 unknown, 1 yes, 2 no
-  *ok = false;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(MA_ERUNTIME, "no current HIP device");
-  std::lock_guard<std::mutex> lock(mu);
-  if (!known[dev]) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return fail(MA_ERUNTIME, "moe_fused: stream query failed");
-    if (cs != hipStreamCaptureStatusNone) return MA_OK;
-    uint32_t* d = nullptr;
-    uint32_t h[kProbeWgs];
-    if (hipGetSymbolAddress(reinterpret_cast<void**>(&d), HIP_SYMBOL(g_xcd_probe)) != hipSuccess)
-      return fail(MA_ERUNTIME, "moe_fused: XCD probe symbol");
-    hipLaunchKernelGGL(k_xcd_probe, dim3(kProbeWgs), dim3(512), 0, st, d);
-    if (hipGetLastError() != hipSuccess || hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, st) != hipSuccess ||
-        hipStreamSynchronize(st) != hipSuccess)
-      return fail(MA_ERUNTIME, "moe_fused: XCD probe failed");
-    bool good = true;
-    const uint32_t o = h[0] % kXcds;  // XCD of workgroup 0
-    for (int i = 0; i < kProbeWgs; ++i) good = good && h[i] == (i + o) % kXcds;
-    known[dev] = good ? 1 : 2;
-  }
-  *ok = known[dev] == 1;
-  return MA_OK;
-}
 
 template <int ADT>
 const void* xcd_kernel_t(int64_t inter) {
@@ -498,7 +448,7 @@ bool moe_xcd_supported(int64_t n_experts, int64_t hidden, int64_t inter, int64_t
   if (resident_capacity(xcd_kernel_t<MA_BF16>(inter), 512, &capacity) != MA_OK || capacity < kXcds * kXcdWgs)
     return false;
   bool ok = false;
-  return xcd_layout_ok(st, &ok) == MA_OK && ok;
+  return xcd_round_robin(st, &ok) == MA_OK && ok;
 }
 
 int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, int norm_dtype, float eps,

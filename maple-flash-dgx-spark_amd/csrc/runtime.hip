@@ -9,6 +9,53 @@
 
 namespace ma {
 
+// Whether workgroup i of a launch runs on XCD (i + o) mod kXcds for one o (o
+// changes from launch to launch), so that the workgroups with equal i mod
+// kXcds share an XCD and its L2: one probe launch per device (256 workgroups
+// of 512 threads) records every workgroup's XCD into a static array (no
+// allocation), read back once.  It synchronises ``st``; while ``st`` is
+// being captured into a graph it cannot run, so the answer is "no" and
+// nothing is cached.
+constexpr int kProbeWgs = 256;
+__device__ uint32_t g_xcd_probe[kProbeWgs];
+
+__global__ __launch_bounds__(512) void k_xcd_probe(uint32_t* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = static_cast<uint32_t>(xcc_id());
+}
+
+int xcd_round_robin(hipStream_t st, bool* ok) {
+  static std::mutex mu;
+  static int known[64];  // 0 unknown, 1 yes, 2 no
+  *ok = false;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(MA_ERUNTIME, "no current HIP device");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!known[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return fail(MA_ERUNTIME, "XCD probe: stream query failed");
+    if (cs != hipStreamCaptureStatusNone) return MA_OK;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return fail(MA_ERUNTIME, "XCD probe: device query failed");
+    bool good = cus % kXcds == 0;
+    if (good) {
+      uint32_t* d = nullptr;
+      uint32_t h[kProbeWgs];
+      if (hipGetSymbolAddress(reinterpret_cast<void**>(&d), HIP_SYMBOL(g_xcd_probe)) != hipSuccess)
+        return fail(MA_ERUNTIME, "XCD probe: symbol");
+      hipLaunchKernelGGL(k_xcd_probe, dim3(kProbeWgs), dim3(512), 0, st, d);
+      if (hipGetLastError() != hipSuccess || hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, st) != hipSuccess ||
+          hipStreamSynchronize(st) != hipSuccess)
+        return fail(MA_ERUNTIME, "XCD probe failed");
+      const uint32_t o = h[0] % kXcds;  // XCD of workgroup 0
+      for (int i = 0; i < kProbeWgs; ++i) good = good && h[i] == (i + o) % kXcds;
+    }
+    known[dev] = good ? 1 : 2;
+  }
+  *ok = known[dev] == 1;
+  return MA_OK;
+}
+
 static thread_local char g_err[512] = "";
 
 void set_error(const char* fmt, ...) {
