@@ -456,6 +456,17 @@ int ma_decode_attn_fused(const void* qkv, int64_t ldq, int64_t batch, int n_head
  * query for the fused output projection above). */
 int ma_decode_attn_o_supported(int64_t batch, int n_heads, int n_kv_heads, int head_dim,
                                int64_t max_len, int64_t window, int64_t o_rows);
+/* Which form ma_decode_gqa_attn (fused = 0) / ma_decode_attn_fused (fused = 1,
+ * with_o = 1 with the O projection) launches for these sizes: 1 the
+ * XCD-local form (every split of a (row, KV head) on one XCD, partials and
+ * flags handed over through that XCD's L2; used where the GPU hands
+ * workgroup i to XCD (i + o) mod 8, checked once per device by a small probe
+ * kernel that is skipped while the stream is being captured), 0 the
+ * cross-XCD form (arrival counter and generation word), -1 bad sizes.  Both
+ * give the same bits.  MAPLE_AMD_ATTN=grid forces the cross-XCD form.  No
+ * reference counterpart. */
+int ma_decode_attn_form(int64_t batch, int n_kv_heads, int head_dim, int64_t max_len, int64_t window,
+                        int fused, int with_o);
 
 /*
  * Row-wise ternarisation (the converter's step): for each of `rows` rows of

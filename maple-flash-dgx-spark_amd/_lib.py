@@ -53,6 +53,7 @@ _SIGNATURES = {
     "ma_decode_attn_fused": [_P, _L, _L, _I, _I, _I, _P, _P, _I, _P, _P, _I, _L, _L, _I, _I, _F,
                              _P, _P, _P, _P, _L, _L, _L, _F, _P, _P, _Z, _P, _P, _I, _L, _P, _P],
     "ma_decode_attn_o_supported": [_L, _I, _I, _I, _L, _L, _L],
+    "ma_decode_attn_form": [_L, _I, _I, _L, _L, _I, _I],
     "ma_moe_fused_workspace_bytes": [_L, _L, _L, _L],
     "ma_moe_fused": [_P, _P, _P, _I, _F, _P, _P, _P, _L, _L, _L, _L, _P, _P, _P, _P, _I, _P, _P, _P,
                      _P, _Z, _P, _P, _I, _P, _F, _L, _P, _P],

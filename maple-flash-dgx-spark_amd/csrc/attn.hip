@@ -17,6 +17,9 @@
 //     splits merged with exp(m_s - max) weights.
 // Positions are clamped to [0, max_len) and mapped rows to [0, cache_rows), so
 // nothing is written or read outside the cache.
+#include <cstdlib>
+#include <cstring>
+
 #include "grid_sync.h"
 #include "tgemv_fast.h"
 
@@ -191,7 +194,19 @@ __device__ __forceinline__ uint32_t sel32(bool c, uint32_t a, uint32_t b) { retu
 // dispatch order and far fewer than the GPU holds at once, so they are all
 // resident; the wait is bounded (about 0.2 s) and records a timeout in word 2
 // of the sync area instead of hanging.
-template <bool FUSED, int HD>
+//
+// XL (used where the GPU hands workgroup i to XCD (i + o) mod 8): a 1-D grid
+// of 8 * S * ceil(n_pairs / 8) workgroups, S = splits per pair.  Workgroup L
+// is split (L / 8) mod S of pair 8 * (L / 8 / S) + L mod 8, so every split of
+// a pair runs on one XCD and the hand-off stays in that XCD's L2: partials go
+// out as plain stores, each split then raises its own flag (word 1 + split of
+// the pair's arrival line) to the pair's generation + 1 and polls its
+// siblings' flags with L1-bypassing loads; split 0 advances the generation
+// once it has seen every flag.  Workgroups past the last pair only take part
+// in the O projection.  A pair's S splits are consecutive in its XCD's
+// dispatch order, so they are resident together when S workgroups fit on one
+// XCD.
+template <bool FUSED, int HD, bool XL>
 __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     const uint16_t* __restrict__ src, int64_t ldq, const void* __restrict__ qn_w,
     const void* __restrict__ kn_w, int w_dt, RopeSrc rope, float eps,
@@ -200,7 +215,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     int nq, int nkv, int64_t window, float scale, int max_splits, uint32_t* __restrict__ sync,
     float* __restrict__ part_acc, float* __restrict__ part_ml, uint16_t* __restrict__ out,
     const uint32_t* __restrict__ o_w, const void* __restrict__ o_alpha, int o_alpha_dt, int o_rows,
-    uint16_t* __restrict__ o_out) {
+    uint16_t* __restrict__ o_out, int n_rows, int xl_splits) {
   constexpr int E = HD / 64;   // dims per lane in the wave-wide head layouts
   constexpr int KS = HD / 32;  // 32-dim slices of K per score MFMA chain
   constexpr int NB = HD / 16;  // 16-dim output blocks of P.V
@@ -211,8 +226,29 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   __shared__ float wm[4][kMaxGroup], wl[4][kMaxGroup];
   __shared__ float hm[kMaxGroup], hl[kMaxGroup];
   __shared__ __align__(16) uint4 os4[kOWords * 2][32];  // O projection input
-  const int sp = blockIdx.x, kvh = blockIdx.y;
-  const int64_t b = blockIdx.z;
+  // (split, KV head, row) of this workgroup; the grid's split count; its
+  // index and size for the O projection's barrier
+  int sp, kvh, S, wgl, n_wg;
+  int64_t b;
+  bool active = true;
+  if constexpr (XL) {
+    const int L = static_cast<int>(blockIdx.x), q = L >> 3;
+    S = xl_splits;
+    sp = q % S;
+    const int P = (q / S) * kXcds + (L & (kXcds - 1));
+    active = P < n_rows * nkv;
+    b = active ? P / nkv : 0;
+    kvh = active ? P % nkv : 0;
+    wgl = L;
+    n_wg = static_cast<int>(gridDim.x);
+  } else {
+    sp = blockIdx.x;
+    kvh = blockIdx.y;
+    b = blockIdx.z;
+    S = static_cast<int>(gridDim.x);
+    wgl = (static_cast<int>(b) * static_cast<int>(gridDim.y) + kvh) * static_cast<int>(gridDim.x) + sp;
+    n_wg = static_cast<int>(gridDim.x * gridDim.y * gridDim.z);
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g = lane >> 4;
@@ -226,10 +262,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   // O projection in the same launch (batch 1): a barrier over every workgroup
   // of the launch on the sync area's last 33 lines, then each workgroup
   // computes its rows of o from the whole attention output.
-  uint32_t* const gsub = sync + kSyncLine * (1 + 2 * gridDim.z * nkv);
+  uint32_t* const gsub = sync + kSyncLine * (1 + 2 * n_rows * nkv);
   uint32_t* const gflags = gsub + kSyncLine * (kBarGroups + 1);
-  const int wgl = (static_cast<int>(b) * static_cast<int>(gridDim.y) + kvh) * static_cast<int>(gridDim.x) + sp;
-  const int n_wg = static_cast<int>(gridDim.x * gridDim.y * gridDim.z);
   const uint32_t f0o = o_w && wv == 0 ? ld_coh32(&gflags[kSyncLine * (wgl % kBarGroups)]) : 0u;
   // This workgroup's O rows (as the standalone GEMV splits them: 32 lanes of
   // kOWords words per row, 2 rows per wave pass, kOPass passes), loaded once
@@ -251,7 +285,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   const int64_t kv_len = pos + 1;
   const int64_t start = (window > 0 && kv_len > window) ? kv_len - window : 0;
   const int n_chunks = static_cast<int>(cdiv(kv_len - start, kSplit));
-  const int cps = static_cast<int>(cdiv(n_chunks, gridDim.x));  // chunks per split
+  const int cps = static_cast<int>(cdiv(n_chunks, S));  // chunks per split
   const int n_spl = static_cast<int>(cdiv(n_chunks, cps));
   const float scale2 = scale * 1.44269504088896341f;  // log2(e): maxima and sums in base 2
   auto attend = [&]() {
@@ -502,7 +536,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   }
   __syncthreads();
   const int64_t pidx = (b * nkv + kvh) * max_splits + sp;
-  const int64_t n_part = static_cast<int64_t>(gridDim.z) * nkv * max_splits * kMaxGroup;
+  const int64_t n_part = static_cast<int64_t>(n_rows) * nkv * max_splits * kMaxGroup;
   const CoherentBuf acc_buf(part_acc, static_cast<uint32_t>(n_part * HD * 4));
   const CoherentBuf ml_buf(part_ml, static_cast<uint32_t>(n_part * 8));
   for (int item = tid; item < group * IPH; item += kAttnThreads) {
@@ -523,18 +557,43 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       r.x = pack_bf16x2_rn(o.x * inv, o.y * inv);
       r.y = pack_bf16x2_rn(o.z * inv, o.w * inv);
       store_out(out + (b * nq + kvh * group + hh) * HD + 4 * dq, r, o_w != nullptr);
+    } else if constexpr (XL) {  // read back through this XCD's L2 only
+      *reinterpret_cast<float4*>(part_acc + (pidx * kMaxGroup + hh) * HD + 4 * dq) = o;
     } else {
       acc_buf.st4(static_cast<uint32_t>(((pidx * kMaxGroup + hh) * HD + 4 * dq) * 4), o);
     }
   }
   if (n_spl == 1) return;
-  if (tid < group) ml_buf.st2(static_cast<uint32_t>((pidx * kMaxGroup + tid) * 8), make_float2(hm[tid], hl[tid]));
+  if (tid < group) {
+    if constexpr (XL)
+      *reinterpret_cast<float2*>(part_ml + (pidx * kMaxGroup + tid) * 2) = make_float2(hm[tid], hl[tid]);
+    else
+      ml_buf.st2(static_cast<uint32_t>((pidx * kMaxGroup + tid) * 8), make_float2(hm[tid], hl[tid]));
+  }
   // Barrier among the n_spl splits of this (row, KV head), once this split's
   // partials have completed (no device-scope fence: on this GPU that writes
   // back the whole L2).
+  if constexpr (XL) MA_STORES_DONE();
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (tid == 0) {
+  if constexpr (XL) {
+    // n_spl <= S <= 63 flags, one lane each
+    uint32_t* const flags = arrive + 1;
+    const uint32_t tag = g0 + 1u;
+    if (wv == 0) {
+      if (lane == 0) st_l2_32(&flags[sp], tag);
+      bool timed_out = false;
+      for (;;) {
+        MA_POLL_RELOAD();
+        const bool seen = lane >= n_spl || ld_coh32(&flags[lane]) == tag;
+        if (__builtin_amdgcn_ballot_w64(!seen) == 0 || timed_out) break;
+        __builtin_amdgcn_s_sleep(1);
+        timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kAttnSpin;
+      }
+      if (timed_out && lane == 0) st_coh32(sync + 2, 1u);
+      if (sp == 0 && lane == 0) st_coh32(gen, tag);
+    }
+  } else if (tid == 0) {
     if (atomicAdd(arrive, 1u) == static_cast<uint32_t>(n_spl - 1)) {
       __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(gen, g0 + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -618,7 +677,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     }
   }
   };
-  if (sp < n_spl)
+  if (active && sp < n_spl)
     attend();
   else if (o_w)
     o_prefetch();
@@ -678,8 +737,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
 }
 
 // Sync area: line 0 (word 2: timeout), then per (row, KV head) an arrival
-// counter line and a generation line, then the O projection's grid barrier
-// (16 group-counter lines, one unused line, 16 group-flag lines).
+// counter line (word 0: the counter; words 1 .. 63: the XCD-local form's
+// per-split flags) and a generation line, then the O projection's grid
+// barrier (16 group-counter lines, one unused line, 16 group-flag lines).
 size_t sync_bytes(int64_t batch, int nkv) {
   return (1 + 2 * static_cast<size_t>(batch) * nkv + 2 * kBarGroups + 1) * kSyncLine * sizeof(uint32_t);
 }
@@ -770,15 +830,33 @@ static int64_t attn_grid_splits(int64_t batch, int nkv, int64_t max_len, int64_t
 // (row, KV head)'s splits are consecutive, so every earlier pair has all of
 // its splits placed and finishes; with the O projection in the launch the
 // whole grid meets at one barrier and must be resident.
-template <int HD>
+template <int HD, bool XL>
 static const void* attn_kernel(bool fused) {
-  return fused ? reinterpret_cast<const void*>(&k_decode_attn<true, HD>)
-               : reinterpret_cast<const void*>(&k_decode_attn<false, HD>);
+  return fused ? reinterpret_cast<const void*>(&k_decode_attn<true, HD, XL>)
+               : reinterpret_cast<const void*>(&k_decode_attn<false, HD, XL>);
 }
 
-static int attn_capacity(bool fused, int head_dim, int64_t* cap) {
-  return resident_capacity(head_dim == 128 ? attn_kernel<128>(fused) : attn_kernel<64>(fused),
-                           kAttnThreads, cap);
+static int attn_capacity(bool fused, int head_dim, int64_t* cap, bool xl = false) {
+  const void* k = head_dim == 128 ? (xl ? attn_kernel<128, true>(fused) : attn_kernel<128, false>(fused))
+                                  : (xl ? attn_kernel<64, true>(fused) : attn_kernel<64, false>(fused));
+  return resident_capacity(k, kAttnThreads, cap);
+}
+
+// The XCD-local form (XL in k_decode_attn): chosen when the pair's splits
+// need merging, their flags fit the pair's arrival line, one XCD holds a
+// pair's splits at once (the whole grid when the O projection's barrier spans
+// it) and the GPU hands workgroups to XCDs round robin.  MAPLE_AMD_ATTN=grid
+// keeps the cross-XCD form (for A/B timing).
+static bool attn_xcd_form(bool fused, int hd, int64_t n_pairs, int64_t splits, bool with_o, hipStream_t s) {
+  if (splits < 2 || splits > kSyncLine - 1) return false;
+  const char* force = getenv("MAPLE_AMD_ATTN");
+  if (force && strcmp(force, "grid") == 0) return false;
+  int64_t cap = 0;
+  if (attn_capacity(fused, hd, &cap, true) != MA_OK) return false;
+  const int64_t n_wg = kXcds * splits * cdiv(n_pairs, kXcds);
+  if (kXcds * splits > cap || (with_o && n_wg > cap)) return false;
+  bool ok = false;
+  return xcd_round_robin(s, &ok) == MA_OK && ok;
 }
 
 extern "C" int ma_decode_attn_o_supported(int64_t batch, int n_heads, int n_kv_heads, int head_dim,
@@ -791,6 +869,13 @@ extern "C" int ma_decode_attn_o_supported(int64_t batch, int n_heads, int n_kv_h
   int64_t cap = 0;
   if (attn_capacity(true, head_dim, &cap) != MA_OK || n_wg > cap) return 0;
   return n_wg >= kBarGroups && o_rows >= 1 && o_rows <= n_wg * 8 * kOPass;
+}
+
+extern "C" int ma_decode_attn_form(int64_t batch, int n_kv_heads, int head_dim, int64_t max_len, int64_t window,
+                                   int fused, int with_o) {
+  if (batch < 1 || n_kv_heads < 1 || max_len < 1 || (head_dim != 64 && head_dim != 128)) return -1;
+  const int64_t splits = attn_grid_splits(batch, n_kv_heads, max_len, window);
+  return attn_xcd_form(fused != 0, head_dim, batch * n_kv_heads, splits, with_o != 0, nullptr) ? 1 : 0;
 }
 
 // Shared launch of k_decode_attn for the two entry points below.
@@ -817,10 +902,12 @@ static int launch_attn(bool fused, const void* src, int64_t ldq, const void* qn_
   auto* sync = static_cast<uint32_t*>(workspace);
   float* acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + sync_bytes(batch, nkv));
   float* ml = acc + static_cast<size_t>(batch) * nkv * max_splits * kMaxGroup * hd;
-  dim3 grid(static_cast<unsigned>(grid_splits), static_cast<unsigned>(nkv),
-            static_cast<unsigned>(batch));
+  const bool xl = attn_xcd_form(fused, hd, batch * nkv, grid_splits, o_w != nullptr, s);
+  const dim3 grid = xl ? dim3(static_cast<unsigned>(kXcds * grid_splits * cdiv(batch * nkv, kXcds)))
+                       : dim3(static_cast<unsigned>(grid_splits), static_cast<unsigned>(nkv),
+                              static_cast<unsigned>(batch));
   if (o_w) {
-    const int64_t n_wg = grid_splits * nkv * batch;
+    const int64_t n_wg = static_cast<int64_t>(grid.x) * grid.y * grid.z;
     if (batch != 1 || static_cast<int64_t>(nq) * hd != 32 * kOWords * 16)
       return fail(MA_EVALUE, "%s: the O projection in the launch needs batch 1 and n_heads x head_dim = %d",
                   what, 32 * kOWords * 16);
@@ -840,15 +927,23 @@ static int launch_attn(bool fused, const void* src, int64_t ldq, const void* qn_
       static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), cache_rows, max_len,    \
       seqlen, row_map, nq, nkv, window, scale, static_cast<int>(max_splits), sync, acc, ml,   \
       static_cast<uint16_t*>(out), o_w, o_alpha, o_alpha_dt, static_cast<int>(o_rows),         \
-      static_cast<uint16_t*>(o_out)
+      static_cast<uint16_t*>(o_out), static_cast<int>(batch), static_cast<int>(grid_splits)
+#define MA_ATTN_LAUNCH(F, H)                                                                      \
+  do {                                                                                          \
+    if (xl)                                                                                     \
+      hipLaunchKernelGGL((k_decode_attn<F, H, true>), grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS); \
+    else                                                                                        \
+      hipLaunchKernelGGL((k_decode_attn<F, H, false>), grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS); \
+  } while (0)
   if (fused && hd == 128)
-    hipLaunchKernelGGL((k_decode_attn<true, 128>), grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
+    MA_ATTN_LAUNCH(true, 128);
   else if (fused)
-    hipLaunchKernelGGL((k_decode_attn<true, 64>), grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
+    MA_ATTN_LAUNCH(true, 64);
   else if (hd == 128)
-    hipLaunchKernelGGL((k_decode_attn<false, 128>), grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
+    MA_ATTN_LAUNCH(false, 128);
   else
-    hipLaunchKernelGGL((k_decode_attn<false, 64>), grid, dim3(kAttnThreads), 0, s, MA_ATTN_ARGS);
+    MA_ATTN_LAUNCH(false, 64);
+#undef MA_ATTN_LAUNCH
 #undef MA_ATTN_ARGS
   return check_launch(what);
 }

@@ -29,6 +29,16 @@ __device__ __forceinline__ void st_coh64(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Stores read back only by workgroups of the same XCD: plain stores, which
+// land in the XCD's L2 (the vector L1 is write-through); the readers' sc1
+// loads (ld_coh*) are served by that L2.
+__device__ __forceinline__ void st_l2_32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void st_l2_64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 __device__ __forceinline__ void st_coh16(uint16_t* p, uint16_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -73,6 +83,10 @@ __device__ inline bool grid_barrier_flags(uint32_t* sub, uint32_t* flags, uint32
 // CoherentBuf: the buffer-load builtins count as reads of unchanging memory,
 // so without this clobber the compiler hoists them out of the loop.
 #define MA_POLL_RELOAD() asm volatile("" ::: "memory")
+
+// Waits until this wave's stores have been acknowledged by the L2, and keeps
+// the compiler from moving any memory access across the wait.
+#define MA_STORES_DONE() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
 
 // Device-coherent 8- and 16-byte access through a buffer resource: the sc1 cache policy (the bit agent-scope atomic loads and
 // stores carry on this GPU) sends each access to the coherent level, so a

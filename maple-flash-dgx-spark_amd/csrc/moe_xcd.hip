@@ -47,16 +47,6 @@ namespace ma {
 
 constexpr int kXcdWgs = 32;  // workgroups per XCD
 
-// Stores read back only by workgroups of the same XCD: plain stores, which
-// land in the XCD's L2 (the vector L1 is write-through); the readers' sc1
-// loads (ld_coh*) are served by that L2.
-__device__ __forceinline__ void st_l2_32(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-__device__ __forceinline__ void st_l2_64(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
 // Shapes: H = 16 * KWH * LPRH with LPRH = 32 (one up/gate row pair per
 // SwiGLU pass), I = 16 * KWI * LPRI, US SwiGLU outputs and UD down passes
 // (64 / LPRI rows each) per wave, 8 waves per workgroup, E <= 64 experts,

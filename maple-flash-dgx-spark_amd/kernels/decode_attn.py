@@ -53,6 +53,18 @@ def o_projection_supported(batch: int, num_heads: int, num_kv_heads: int, head_d
                                                          max_len, int(window or 0), o_rows))
 
 
+def attention_form(batch: int, num_kv_heads: int, head_dim: int, max_len: int, window: int | None = None,
+                   fused: bool = True, with_o: bool = False) -> str:
+    """``"xcd"`` if the attention launch for these sizes keeps every split of
+    a (row, KV head) on one XCD (merged through that XCD's L2), ``"grid"``
+    for the cross-XCD form; both give the same bits."""
+    f = _lib.load().ma_decode_attn_form(batch, num_kv_heads, head_dim, max_len, int(window or 0),
+                                        int(fused), int(with_o))
+    if f < 0:
+        raise ValueError("attention_form: bad sizes")
+    return "xcd" if f == 1 else "grid"
+
+
 def gqa_workspace(batch: int, num_kv_heads: int, max_len: int, device, head_dim: int = 64) -> torch.Tensor:
     """Zeroed workspace for ``decode_gqa_attn`` / ``decode_attention``; keep
     one per cache so decode allocates nothing inside a graph."""

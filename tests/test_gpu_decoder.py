@@ -18,7 +18,7 @@ import torch
 from _helpers import assert_bf16_close, np_f, np_u32
 from maple_amd import synthetic
 from maple_amd.kernels import apply_qkv_decode, decode_attention, decode_gqa_attn, gqa_workspace, ternary_gemv
-from maple_amd.kernels.decode_attn import o_projection_supported
+from maple_amd.kernels.decode_attn import attention_form, o_projection_supported
 from maple_amd.model import DecoderConfig, SyntheticDecoder
 from oracle import decoder as od
 
@@ -162,6 +162,53 @@ def test_fused_attention_o_projection_equals_gemv(dev, seqlen, heads):
         assert torch.equal(out, ref)
         assert torch.equal(o, o_ref)
     assert int(ws[8:12].view(torch.int32).item()) == 0, "a barrier wait timed out"
+
+
+@pytest.mark.parametrize("heads", HEADS[:2])
+@pytest.mark.parametrize("batch,window", [(1, None), (3, 300), (9, None), (32, None)])
+def test_attention_xcd_form_equals_grid_form(dev, monkeypatch, batch, window, heads):
+    """The XCD-local attention form (every split of a (row, KV head) on one
+    XCD: 1 row leaves 4 of 8 XCD slots idle, 9 rows a part-filled last block
+    of 8 pairs) gives the cross-XCD form's bits, the forms alternating on one
+    workspace (their arrival lines are shared), with no timed-out wait and the
+    arrival counters at zero; and the output matches the oracle."""
+    nq, nkv, d, rot = heads
+    max_len = 4224
+    g = torch.Generator().manual_seed(batch)
+    seqlen = torch.randint(0, max_len, (batch,), generator=g).to(dev)
+    seqlen[0] = 4100
+    qkv = synthetic.randn_bf16((batch, (nq + 2 * nkv) * d), 41, dev)
+    kc = synthetic.randn_bf16((batch, nkv, max_len, d), 42, dev)
+    vc = synthetic.randn_bf16((batch, nkv, max_len, d), 43, dev)
+    w = torch.ones(d, device=dev)
+    cos, sin = (torch.from_numpy(t).to(dev) for t in od.rope_tables(max_len, rot, 1e4))
+    kw = dict(num_heads=nq, num_kv_heads=nkv, head_dim=d, rotary_dim=rot, eps=1e-6, scale=d ** -0.5,
+              window=window)
+    assert attention_form(batch, nkv, d, max_len, window) == "xcd"
+    ws = gqa_workspace(batch, nkv, max_len, dev, d)
+    outs = []
+    for form in ("xcd", "grid", "xcd", "grid", "xcd"):
+        if form == "grid":
+            monkeypatch.setenv("MAPLE_AMD_ATTN", "grid")
+        else:
+            monkeypatch.delenv("MAPLE_AMD_ATTN", raising=False)
+        assert attention_form(batch, nkv, d, max_len, window) == form
+        kc2, vc2 = kc.clone(), vc.clone()
+        outs.append(decode_attention(qkv, w, w, cos, sin, kc2, vc2, seqlen, ws, **kw))
+        torch.cuda.synchronize()
+        sync = ws[:256 * (1 + 2 * batch * nkv)].view(torch.int32)
+        assert int(sync[2]) == 0, f"{form}: a split barrier wait timed out"
+        assert int(sync[64::128][:batch * nkv].count_nonzero()) == 0, "arrival counters not reset"
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    for b in range(0, batch, 8):  # the oracle over every row is slow; rows 0, 8, ... suffice
+        n = int(seqlen[b]) + 1
+        qn = apply_qkv_decode(qkv[b:b + 1], w, w, cos[seqlen[b:b + 1]].to(torch.bfloat16),
+                              sin[seqlen[b:b + 1]].to(torch.bfloat16), kc[b:b + 1].clone(), vc[b:b + 1].clone(),
+                              seqlen[b:b + 1], num_heads=nq, num_kv_heads=nkv, head_dim=d, rotary_dim=rot,
+                              use_rope=True, use_qk_norm=True, eps=1e-6)
+        ref = od.gqa(np_f(qn[0, :, 0]), np_f(kc2[b]), np_f(vc2[b]), n, d ** -0.5, window)
+        assert_bf16_close(np_f(outs[0][b, :, 0]), ref, atol_frac=2e-3, what=f"row {b}")
 
 
 def test_attention_rejects_bad_shapes(dev):
