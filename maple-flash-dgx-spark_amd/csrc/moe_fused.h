@@ -27,32 +27,40 @@ namespace ma {
 //                      h of the XCD's slot as (tag16 << 16 | bf16) words
 //   [128 KB, 256 KB)   XCD kernel: the weighted down outputs of every slot,
 //                      tagged 64-bit words [8][H]
+//   [256 KB, 320 KB)   XCD kernel with a next projection: one 8 KB region per
+//                      XCD holding that XCD's copy of y, two bf16 values per
+//                      tagged 64-bit word (tag << 32 | y[2m + 1] << 16 | y[2m])
 constexpr int kSubB = 1, kTopB = kSubB + kBarGroups, kFlags = kTopB + 1;
 constexpr int kSubC = kFlags + kBarGroups, kTopC = kSubC + kBarGroups;
 constexpr size_t kLogitOff = 16384;
 constexpr int kLogitStride = 16;  // uint64 words between logits
 constexpr size_t kMoeWsHeader = 49152;
 constexpr size_t kXEpochOff = 65536, kXRegionOff = 98304, kXRegion = 4096, kXPartOff = 131072;
-constexpr size_t kXWsBytes = kXPartOff + 8 * 2048 * 8;
+constexpr size_t kXYOff = kXPartOff + 8 * 2048 * 8, kXYRegion = 8192;
+constexpr size_t kXWsBytes = kXYOff + 8 * kXYRegion;
 static_assert(kTopC < static_cast<int>(kLogitOff / 256), "workspace lines");
 static_assert(kLogitOff + 256 * kLogitStride * 8 <= kMoeWsHeader, "workspace logits");
 static_assert(kMoeWsHeader + 8 * 768 * 2 <= kXEpochOff, "grid kernel h");
 static_assert(kXEpochOff + 256 * 128 <= kXRegionOff && kXRegionOff + 8 * kXRegion <= kXPartOff, "XCD layout");
+static_assert(2048 / 2 * 8 <= kXYRegion, "XCD y region");
 
 // Next projection, run by every workgroup of a one-launch layer once its rows
-// of y have been stored with device-coherent stores: nx_out = ternary_gemv(y,
-// nx_w, nx_alpha, rms_weight = nx_rms) -- reference kernels/ternary_gemv.py:
-// 110-146 -- with the standalone fast GEMV's per-lane arithmetic in the same
-// order (so the same bits).  nxw / nxa hold this workgroup's rows (prefetched
-// by the caller: row wg * nx_rq + p * W * RPIH + wv * RPIH + lane / LPRH).
-// A grid barrier (counters at kSubC, release flags at kFlags holding f_old)
-// waits for every workgroup's y.  Returns true if that wait timed out.
-template <int KWH, int LPRH, int W, int NXP>
+// of y are out: nx_out = ternary_gemv(y, nx_w, nx_alpha, rms_weight = nx_rms)
+// -- reference kernels/ternary_gemv.py:110-146 -- with the standalone fast
+// GEMV's per-lane arithmetic in the same order (so the same bits).  nxw / nxa
+// hold this workgroup's rows (prefetched by the caller: row wg * nx_rq + p * W
+// * RPIH + wv * RPIH + lane / LPRH).  y comes either from global memory, stored
+// there with device-coherent stores, after a grid barrier (counters at kSubC,
+// release flags at kFlags holding f_old), or (XY) from the XCD's own tagged
+// copy yx (two values per 64-bit word, tag ytag), polled word by word.
+// Returns true if a wait timed out.
+template <int KWH, int LPRH, int W, int NXP, bool XY = false>
 __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, const float* __restrict__ nx_rms,
                                                 float nx_eps, int nx_rows, int nx_rq,
                                                 uint16_t* __restrict__ nx_out, const uint32_t (&nxw)[NXP][KWH],
                                                 const float (&nxa)[NXP], uint32_t* ws, uint32_t f_old, int G,
-                                                int wg, int tid, int lane, int wv, uint64_t t0) {
+                                                int wg, int tid, int lane, int wv, uint64_t t0,
+                                                const uint64_t* yx = nullptr, uint32_t ytag = 0) {
   constexpr int NWH = KWH * LPRH;
   constexpr int NTH = 64 * W;
   constexpr int RPIH = 64 / LPRH;
@@ -65,29 +73,54 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
   __shared__ __align__(16) float prr[8][NWH];
   const int klh = lane % LPRH, subh = lane / LPRH;
 
-  __builtin_amdgcn_s_waitcnt(0);  // this workgroup's y stores have completed
-  __syncthreads();
   bool timed_out = false;
-  if (wv == 0) timed_out = grid_barrier_flags(ws + kLine * kSubC, ws + kLine * kFlags, f_old, G, wg, lane, t0);
-  __syncthreads();  // every wave waits for the barrier before reading y
-  {  // y (device-coherent) into LDS, and its x' pairs: thread t builds pairs
-     // j0 .. j0 + 3 of word t / 2 (j0 = 4 (t & 1)), each from values j and
-     // j + 8 of the word times their RMS weights
+  if constexpr (!XY) {
+    __builtin_amdgcn_s_waitcnt(0);  // this workgroup's y stores have completed
+    __syncthreads();
+    if (wv == 0) timed_out = grid_barrier_flags(ws + kLine * kSubC, ws + kLine * kFlags, f_old, G, wg, lane, t0);
+    __syncthreads();  // every wave waits for the barrier before reading y
+  }
+  {  // y into LDS, and its x' pairs: thread t builds pairs j0 .. j0 + 3 of
+     // word t / 2 (j0 = 4 (t & 1)), each from values j and j + 8 of the word
+     // times their RMS weights
     constexpr int PIT = (NWH * 2 + NTH - 1) / NTH;
     uint64_t y0[PIT], y1[PIT], ya[PIT], yb[PIT], wa[PIT][2], wb[PIT][2];
 #pragma unroll
     for (int k = 0; k < PIT; ++k) {
       const int t = tid + NTH * k < NWH * 2 ? tid + NTH * k : NWH * 2 - 1;
       const int w = t >> 1, j0 = 4 * (t & 1);
-      const uint64_t* yp = reinterpret_cast<const uint64_t*>(y + w * 16 + 8 * (t & 1));
-      y0[k] = ld_coh64(yp);  // values 8 (t & 1) .. + 8 of word w, raw
-      y1[k] = ld_coh64(yp + 1);
-      ya[k] = ld_coh64(reinterpret_cast<const uint64_t*>(y + w * 16 + j0));
-      yb[k] = ld_coh64(reinterpret_cast<const uint64_t*>(y + w * 16 + j0 + 8));
       wa[k][0] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0)[0];
       wa[k][1] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0)[1];
       wb[k][0] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0 + 8)[0];
       wb[k][1] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0 + 8)[1];
+      if constexpr (XY) {  // the 16 values of word w: tagged words 8 w .. 8 w + 7
+        const CoherentBuf yq(yx, NWH * 8 * 8);
+        uint4 q[4];
+        for (;;) {
+          MA_POLL_RELOAD();
+#pragma unroll
+          for (int i = 0; i < 4; ++i) q[i] = yq.ld4u(static_cast<uint32_t>((8 * w + 2 * i) * 8));
+          uint32_t bad = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) bad |= (q[i].y ^ ytag) | (q[i].w ^ ytag);
+          if (__all(bad == 0) || timed_out) break;
+          __builtin_amdgcn_s_sleep(1);
+          timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+        }
+        // u[m]: values 2 m and 2 m + 1 of the word, as in memory
+        const uint32_t u[8] = {q[0].x, q[0].z, q[1].x, q[1].z, q[2].x, q[2].z, q[3].x, q[3].z};
+        const int h = t & 1;
+        y0[k] = u[4 * h] | (static_cast<uint64_t>(u[4 * h + 1]) << 32);
+        y1[k] = u[4 * h + 2] | (static_cast<uint64_t>(u[4 * h + 3]) << 32);
+        ya[k] = u[2 * h] | (static_cast<uint64_t>(u[2 * h + 1]) << 32);
+        yb[k] = u[4 + 2 * h] | (static_cast<uint64_t>(u[5 + 2 * h]) << 32);
+      } else {
+        const uint64_t* yp = reinterpret_cast<const uint64_t*>(y + w * 16 + 8 * (t & 1));
+        y0[k] = ld_coh64(yp);  // values 8 (t & 1) .. + 8 of word w, raw
+        y1[k] = ld_coh64(yp + 1);
+        ya[k] = ld_coh64(reinterpret_cast<const uint64_t*>(y + w * 16 + j0));
+        yb[k] = ld_coh64(reinterpret_cast<const uint64_t*>(y + w * 16 + j0 + 8));
+      }
     }
 #pragma unroll
     for (int k = 0; k < PIT; ++k) {

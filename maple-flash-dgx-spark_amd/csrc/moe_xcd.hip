@@ -30,7 +30,12 @@
 //      as a tagged float with a device-coherent store;
 //   4. workgroup g polls the 8 slots' values of rows [8 g, 8 g + 8) (one lane
 //      each, the only hand-off between XCDs after the routing), adds them to
-//      the residual in slot order and stores y.
+//      the residual in slot order and stores y;
+//   5. with the next layer's projection in the launch, step 4 instead runs on
+//      every XCD for all of y (workgroup j of the XCD polls the 8 slots'
+//      values of rows [64 j, 64 j + 64)), so that each XCD hands its own copy
+//      of y to its workgroups through its L2 (tagged words, no grid barrier)
+//      and each workgroup then computes its rows of the projection.
 // Tags: each workgroup keeps its own count of calls on the workspace (written
 // only by itself at the end of a call); every call runs every workgroup, so
 // all counts agree and this call's tag is the count + 1.  Nothing needs
@@ -87,6 +92,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   __shared__ __align__(16) uint32_t xbf[NWH][8];  // x in bf16 pairs, for the router waves
   __shared__ float s_red[W];
   __shared__ float s_w;
+  __shared__ float s_pv[TK][64];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -98,14 +104,16 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   uint64_t* const xlog = reinterpret_cast<uint64_t*>(wsb + kXRegionOff + xcd * kXRegion);
   uint32_t* const xh = reinterpret_cast<uint32_t*>(wsb + kXRegionOff + xcd * kXRegion + 512);
   uint64_t* const part = reinterpret_cast<uint64_t*>(wsb + kXPartOff);
+  uint64_t* const yx = reinterpret_cast<uint64_t*>(wsb + kXYOff + xcd * kXYRegion);
   const uint32_t tag = ld_coh32(calls) + 1u;
   const uint32_t tag16 = tag & 0xffffu;
-  const uint32_t f0 = nx_w ? ld_coh32(&ws[kLine * kFlags + kLine * (wg % kBarGroups)]) : 0u;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   bool timed_out = false;
 
-  // The residual of the y rows this workgroup finishes (wave 0, lanes < FR).
-  const int ro = wg * FR + (lane < FR ? lane : 0);
+  // The residual of the y rows this workgroup finishes (wave 0): rows
+  // 64 lw + lane with a next projection (every XCD combines all of y), else
+  // rows wg * FR + lane, lanes < FR.
+  const int ro = nx_w ? 64 * lw + lane : wg * FR + (lane < FR ? lane : 0);
   const uint16_t* const res_a = xb ? xa : (residual ? residual : xa);
   const uint16_t* const res_b = xb ? xb : xa;
   const uint32_t ra = res_a[ro], rb = res_b[ro];
@@ -378,10 +386,37 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     }
   }
 
-  // ---- 6. rows wg * FR .. + FR of y: lane l of wave 0 polls slot l / FR's
-  // value of row wg * FR + l % FR; y = residual + the slots' values in slot
-  // order
-  if (wv == 0) {
+  // ---- 6. y = residual + the slots' values in slot order.  With a next
+  // projection every XCD combines all of y for its own workgroups (wave w of
+  // workgroup lw polls slot w's values of rows 64 lw .. + 64) and hands it
+  // over through its L2, two values per tagged word; each XCD stores an
+  // eighth of y.  Otherwise workgroup wg finishes rows wg * FR .. + FR:
+  // lane l of wave 0 polls slot l / FR's value of row wg * FR + l % FR.
+  if (nx_w) {
+    static_assert(H == 64 * kXcdWgs, "64 rows of y per workgroup of an XCD");
+    const int row = 64 * lw + lane;
+    float pv = 0.f;
+    for (;;) {
+      const uint64_t q = ld_coh64(&part[wv * H + row]);
+      const bool ok = static_cast<uint32_t>(q >> 32) == tag;
+      pv = __uint_as_float(static_cast<uint32_t>(q));
+      if (__all(ok) || timed_out) break;
+      __builtin_amdgcn_s_sleep(1);
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+    }
+    s_pv[wv][lane] = pv;
+    __syncthreads();
+    if (wv == 0) {
+      float v = xb ? bf16_to_f32(f32_to_bf16(__uint_as_float(ra << 16) + __uint_as_float(rb << 16)))
+                   : residual ? __uint_as_float(ra << 16) : 0.f;
+#pragma unroll
+      for (int k = 0; k < TK; ++k) v += s_pv[k][lane];
+      const uint32_t bits = f32_to_bf16(v);
+      if ((lane >> 3) == xcd) y[row] = static_cast<uint16_t>(bits);
+      const uint32_t odd = __shfl_xor(bits, 1, 64);
+      if (!(lane & 1)) st_l2_64(&yx[row >> 1], (static_cast<uint64_t>(tag) << 32) | bits | (odd << 16));
+    }
+  } else if (wv == 0) {
     const int s = lane / FR, r = lane % FR;
     float pv = 0.f;
     for (;;) {
@@ -396,18 +431,13 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
                  : residual ? __uint_as_float(ra << 16) : 0.f;
 #pragma unroll
     for (int k = 0; k < TK; ++k) v += __shfl(pv, k * FR + r, 64);
-    if (lane < FR) {
-      if (nx_w)
-        st_coh16(&y[wg * FR + lane], f32_to_bf16(v));  // read back by every workgroup below
-      else
-        y[wg * FR + lane] = f32_to_bf16(v);
-    }
+    if (lane < FR) y[wg * FR + lane] = f32_to_bf16(v);
   }
 
-  // ---- 7. next projection (optional), once every workgroup's rows of y are out
+  // ---- 7. next projection (optional), from the XCD's copy of y
   if (nx_w)
-    timed_out = next_projection<KWH, LPRH, W, NXP>(y, nx_rms, nx_eps, nx_rows, nx_rq, nx_out, nxw, nxa, ws, f0,
-                                                   G, wg, tid, lane, wv, t0) ||
+    timed_out = next_projection<KWH, LPRH, W, NXP, true>(y, nx_rms, nx_eps, nx_rows, nx_rq, nx_out, nxw, nxa, ws,
+                                                         0u, G, wg, tid, lane, wv, t0, yx, tag) ||
                 timed_out;
   if (__ballot(timed_out) && lane == 0) st_coh32(&ws[2], 1u);
   if (tid == 0) st_coh32(calls, tag);

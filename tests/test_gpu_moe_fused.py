@@ -256,6 +256,41 @@ def test_fused_forms_vs_oracle_on_one_workspace(dev, monkeypatch, inter):
     assert not moe_fused_timed_out(dev)
 
 
+def test_fused_forms_next_projection_on_one_workspace(dev, monkeypatch, layers):
+    """The next projection in the launch gives ternary_gemv's bits on the
+    launch's y in both forms (the XCD form hands y to each XCD's workgroups
+    through that XCD's L2, the one-barrier form through memory after a grid
+    barrier), with calls of either form, with and without the projection,
+    interleaved on one workspace (the XCD form's copies of y are written only
+    by calls with a projection, so a later one must not take an older copy)."""
+    from maple_amd.moe import fused_form
+
+    nl = _next_linear(2560, 2048, 81, dev)
+    seq = [("xcd", True), ("xcd", False), ("grid", True), ("xcd", True), ("xcd", False), ("xcd", True),
+           ("grid", False), ("xcd", True)]
+    for step, (form, proj) in enumerate(seq):
+        if form == "grid":
+            monkeypatch.setenv("MAPLE_AMD_MOE_FUSED", "grid")
+        else:
+            monkeypatch.delenv("MAPLE_AMD_MOE_FUSED", raising=False)
+        assert fused_form(layers[0], 8) == (1 if form == "xcd" else 0)
+        L = layers[step % len(layers)]
+        x = synthetic.randn_bf16((1, 2048), 1600 + step, dev)
+        res = synthetic.randn_bf16((1, 2048), 1700 + step, dev)
+        if proj:
+            y, ids, wts, q = moe_fused(x, L, 8, res, next_linear=nl)
+            ref = ternary_gemv(y, nl[0], nl[1], rms_weight=nl[2], rms_eps=nl[3])
+        else:
+            y, ids, wts = moe_fused(x, L, 8, res)
+        torch.cuda.synchronize()
+        assert_bf16_close(np_f(y), _oracle(np_f(x), L, ids, wts, 8, np_f(res)), atol_frac=Y_ATOL,
+                          what=f"{form} step {step}")
+        if proj:
+            assert torch.equal(q, ref), f"{form} next projection, step {step}"
+    monkeypatch.delenv("MAPLE_AMD_MOE_FUSED", raising=False)
+    assert not moe_fused_timed_out(dev)
+
+
 _FIRST_CALL_CAPTURED = r"""
 import os, sys, torch
 sys.path.insert(0, sys.argv[1])
