@@ -173,12 +173,14 @@ __device__ __forceinline__ float prep_word_pairs(const float xs[16], uint32_t xp
 }
 
 // SwiGLU of the reference's expert MLP (kernels/ternary_expert.py:314-318):
-// clamp(up, -7, 7) * g * sigmoid(g) with g = min(gate, 7).
+// clamp(up, -7, 7) * g * sigmoid(g) with g = min(gate, 7), in that order;
+// sigmoid(g) = 1 / (1 + exp(-g)) with the hardware reciprocal (v_rcp_f32,
+// 1 ulp; the reference's Triton sigmoid divides approximately too).
 constexpr float kMlpClamp = 7.0f;
 __device__ __forceinline__ float swiglu_act(float up, float gate) {
   up = fminf(fmaxf(up, -kMlpClamp), kMlpClamp);
   gate = fminf(gate, kMlpClamp);
-  return up * (gate / (1.0f + expf(-gate)));
+  return (up * gate) * __builtin_amdgcn_rcpf(1.0f + expf(-gate));
 }
 
 // ---------------------------------------------------------------------------

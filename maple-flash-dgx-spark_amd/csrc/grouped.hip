@@ -814,19 +814,24 @@ __device__ __forceinline__ void gp_step(const uint2 (&wq)[4], const uint32_t* __
 // slots, as the LDS DMA writes them) with chunk c = (S % 16) ^ (p % 16) of
 // pair p = S / 16.  rows[p] is pair p's row in the uint32 array base (row
 // length ld); src[i] is copy i's source at K word 0.
+// The four offsets live in LDS (soff[thread], read back at each step): in
+// registers they pushed the K loop past its 128 VGPRs, and the compiler
+// reloaded a spilled value from scratch memory at every step.
 struct GpDma {
   const uint32_t* base;  // the same in every lane
-  uint32_t off[4];       // copy i's source at K word 0, in uint32 from base (< 2^32: checked by the host)
+  const uint4* soff;     // LDS: soff[t].x .. .w = thread t's copy i source at K word 0, in uint32 from base
+                         // (< 2^32: checked by the host)
 };
-__device__ __forceinline__ GpDma gp_dma_sources(const uint32_t* base, int64_t ld, const int32_t* rows) {
-  GpDma d;
-  d.base = base;
+__device__ __forceinline__ GpDma gp_dma_sources(const uint32_t* base, int64_t ld, const int32_t* rows,
+                                                uint4* soff) {
+  uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int S = threadIdx.x + gp::kThreads * i, p = S / 16, c = (S % 16) ^ (p % 16);
-    d.off[i] = static_cast<uint32_t>(static_cast<int64_t>(rows[p]) * ld + (c >> 1) * 8 + 4 * (c & 1));
+    o[i] = static_cast<uint32_t>(static_cast<int64_t>(rows[p]) * ld + (c >> 1) * 8 + 4 * (c & 1));
   }
-  return d;
+  soff[threadIdx.x] = make_uint4(o[0], o[1], o[2], o[3]);  // read back only by this thread
+  return GpDma{base, soff};
 }
 typedef __attribute__((address_space(3))) void* lds_void_t;
 // s_waitcnt immediate (gfx9 encoding): vmcnt(4), expcnt and lgkmcnt left open.
@@ -836,9 +841,11 @@ constexpr int kVmcnt4 = 0x4 | (0x7 << 4) | (0xF << 8);
 // until the issuing wave's vector memory counter drains).
 __device__ __forceinline__ void gp_dma(const GpDma& d, int64_t k0, uint32_t* xsb) {
   const int wv = threadIdx.x >> 6;
+  const uint4 o4 = d.soff[threadIdx.x];
+  const uint32_t off[4] = {o4.x, o4.y, o4.z, o4.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    __builtin_amdgcn_global_load_lds(d.base + d.off[i] + k0 * 8,
+    __builtin_amdgcn_global_load_lds(d.base + off[i] + k0 * 8,
                                      (lds_void_t)(xsb + 4 * (64 * wv + gp::kThreads * i)), 16, 0, 0);
 }
 
@@ -913,6 +920,7 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
   __shared__ __align__(16) uint32_t xb[kXsDwords];
   __shared__ float cst[kTok], hcp[4][kTok];
   __shared__ int32_t tokrow[kTok], pid[kTok];
+  __shared__ uint4 dsoff[kThreads];
   const int n_rtiles = static_cast<int>((n_half + kRows / 2 - 1) / (kRows / 2));
   int mtile, rtile;
   gp_tile(n_rtiles, mtile, rtile);
@@ -935,7 +943,7 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) moff[mb] = (16 * (mb & 1) + (mb >> 1) * n_half) * nwords;
   __syncthreads();  // tokrow
-  const GpDma xsrc = gp_dma_sources(xp, nwords * 8, tokrow);
+  const GpDma xsrc = gp_dma_sources(xp, nwords * 8, tokrow, dsoff);
   f32x4_t acc[4][4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
@@ -946,32 +954,43 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
   // for pair column wm*64 + nb*16 + r16.  h goes to LDS in the x' pair layout
   // of its 8 words (the loop's last barrier has freed the LDS), then out in
   // 16-byte pieces, each pair's 256 bytes contiguous.
+  // Output i = o0 + 16 mb + 4 g + r (< n_half: n_half % 128 == 0) sits at
+  // position 4 g + r of its 16-output word, i.e. pair j = (4 g + r) & 7 (so
+  // pair_scale(j) = pair_scale(r)), half g >> 1, word 2 wr + mb of the tile.
   uint16_t* hst = reinterpret_cast<uint16_t*>(xa);
   const int64_t otile = static_cast<int64_t>(rtile) * (kRows / 2);
+  const int64_t abase = static_cast<int64_t>(e) * 2 * n_half;
+  float au[2][4], ag[2][4];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t i = o0 + 16 * mb + 4 * g + r;
+      au[mb][r] = ld_t<ADT>(alpha, abase + i);
+      ag[mb][r] = ld_t<ADT>(alpha, abase + n_half + i);
+    }
+  float cc[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) cc[nb] = cst[wm * 64 + nb * 16 + r16];
+  const int hbase = (2 * wr * 8) * 2 + (g >> 1);
   float hcl[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int64_t i = o0 + 16 * mb + 4 * g + r;
-      const int64_t ia = i < n_half ? i : n_half - 1;
-      const float au = ld_t<ADT>(alpha, static_cast<int64_t>(e) * 2 * n_half + ia);
-      const float ag = ld_t<ADT>(alpha, static_cast<int64_t>(e) * 2 * n_half + n_half + ia);
-      const int pos = static_cast<int>(i & 15), j = pos & 7, hh = pos >> 3;
-      const float f = pair_scale(j);
+      const int j = (4 * g + r) & 7;
+      const float f = pair_scale(r);
+      const int hoff = hbase + (mb * 8 + j) * 2;
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
         const int col = wm * 64 + nb * 16 + r16;
-        const float c = cst[col];
-        const float up = au * (acc[mb][nb][r] - c);
-        const float gt = ag * (acc[mb + 2][nb][r] - c);
+        const float up = au[mb][r] * (acc[mb][nb][r] - cc[nb]);
+        const float gt = ag[mb][r] * (acc[mb + 2][nb][r] - cc[nb]);
         const uint16_t hb = f32_to_bf16(swiglu_act(up, gt));
         const float hv = bf16_to_f32(hb);
-        const int ii = static_cast<int>(i - otile);
-        hst[col * kHRow + ((ii >> 4) * 8 + j) * 2 + hh] =
-            static_cast<uint16_t>(bf16_bits_exact(hv * f));  // exact: power-of-two scale
-        if (i < n_half && col < np) {
-          if (h) h[static_cast<int64_t>(pid[col]) * ldh + i] = hb;
+        hst[col * kHRow + hoff] = static_cast<uint16_t>(bf16_bits_exact(hv * f));  // exact: power-of-two scale
+        if (col < np) {
+          if (h) h[static_cast<int64_t>(pid[col]) * ldh + o0 + 16 * mb + 4 * g + r] = hb;
           hcl[nb] += (f + 1.0f) * hv;
         }
       }
@@ -1013,6 +1032,7 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
   __shared__ __align__(16) uint32_t xb[kXsDwords];
   __shared__ float cst[kTok];
   __shared__ int32_t prow[kTok];
+  __shared__ uint4 dsoff[kThreads];
   const int n_rtiles = static_cast<int>((n_out + kRows - 1) / kRows);
   int mtile, rtile;
   gp_tile(n_rtiles, mtile, rtile);
@@ -1035,7 +1055,7 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) moff[mb] = 16 * mb * nwk;
   __syncthreads();  // prow
-  const GpDma xsrc = gp_dma_sources(hp, nwk * 8, prow);
+  const GpDma xsrc = gp_dma_sources(hp, nwk * 8, prow, dsoff);
   f32x4_t acc[4][4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
