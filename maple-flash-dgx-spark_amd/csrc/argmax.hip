@@ -3,7 +3,7 @@
 // Semantics of the reference's greedy step (src/maple_run/generate.py:146-148,
 // torch.argmax over the vocabulary): the index of the largest value, the
 // lowest such index on ties.  One 1024-thread workgroup per row; every thread
-// scans 16-byte vectors (bf16 or float32), then (value, index) pairs meet
+// scans 16-byte vectors (bf16 or float32) by their maxima, then (value, index) pairs meet
 // through shuffles within waves and LDS across waves (rows that are not
 // 16-byte aligned take a scalar loop).  NaN logits are
 // not expected (the reference's output would be its own NaN handling).
@@ -19,6 +19,31 @@ __device__ __forceinline__ void take_better(float& v, int64_t& i, float v2, int6
     v = v2;
     i = i2;
   }
+}
+
+// The PER values of a 16-byte vector (bf16: 8, float32: 4) as floats.
+template <int DT>
+__device__ __forceinline__ void vec_unpack(const uint4& q, float (&f)[DT == MA_BF16 ? 8 : 4]) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  if constexpr (DT == MA_BF16) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      f[2 * k] = __uint_as_float(w[k] << 16);
+      f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) f[k] = __uint_as_float(w[k]);
+  }
+}
+template <int DT>
+__device__ __forceinline__ float vec_max(const uint4& q) {
+  float f[DT == MA_BF16 ? 8 : 4];
+  vec_unpack<DT>(q, f);
+  if constexpr (DT == MA_BF16)
+    return fmaxf(fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3])), fmaxf(fmaxf(f[4], f[5]), fmaxf(f[6], f[7])));
+  else
+    return fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3]));
 }
 
 __device__ __forceinline__ void wave_argmax(float& v, int64_t& i) {
@@ -44,7 +69,11 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_rows(const void* __re
   const int64_t nvec = vec ? n / PER : 0;  // rows not 16-byte aligned: scalar loop only
   const uint4* p = reinterpret_cast<const uint4*>(static_cast<const char*>(x) +
                                                   row * ldx * (DT == MA_BF16 ? 2 : 4));
-  constexpr int U = 20;  // 1024 x 20 x 16 B = 320 KB in flight: one round for a 151936-token bf16 row
+  // Per 16-byte vector: its maximum (v_max3), one compare against the
+  // thread's best; strict, so the thread keeps its first vector holding its
+  // maximum, and the lowest index in that vector is found once at the end.
+  int64_t bv = -1;
+  constexpr int U = 19;  // 1024 x 19 x 16 B = 304 KB in flight: one round for a 151936-token bf16 row
   for (int64_t v0 = tid; v0 < nvec; v0 += static_cast<int64_t>(kArgmaxThreads) * U) {
     uint4 q[U];
 #pragma unroll
@@ -54,22 +83,21 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_rows(const void* __re
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t vi = v0 + static_cast<int64_t>(kArgmaxThreads) * u;
-      if (vi >= nvec) continue;
-      const uint32_t w[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        float f;
-        if constexpr (DT == MA_BF16)
-          f = __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
-        else
-          f = __uint_as_float(w[e]);
-        if (f > best) {  // strict: within a thread indices only grow
-          best = f;
-          bi = vi * PER + e;
-        }
+      const float m = vec_max<DT>(q[u]);
+      if (m > best) {  // absent vectors hold -inf and never win
+        best = m;
+        bv = v0 + static_cast<int64_t>(kArgmaxThreads) * u;
       }
     }
+  }
+  if (bv >= 0) {  // the lowest index of the winning vector holding the maximum
+    float f[PER];
+    vec_unpack<DT>(p[bv], f);
+    int e = PER - 1;
+#pragma unroll
+    for (int k = PER - 1; k >= 0; --k)
+      if (f[k] == best) e = k;
+    bi = bv * PER + e;
   }
   // Tail elements that do not fill a vector.
   for (int64_t k = nvec * PER + tid; k < n; k += kArgmaxThreads) {

@@ -468,3 +468,28 @@ def test_greedy_argmax_matches_torch(dev, rows, n, dtype):
     torch.testing.assert_close(got, torch.argmax(x.float(), dim=-1), rtol=0, atol=0)
     out = torch.empty(rows, dtype=torch.int64, device=dev)
     assert greedy_argmax(x, out=out) is out and torch.equal(out, got)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_greedy_argmax_ties_within_and_across_vectors(dev, dtype):
+    """The kernel compares whole 16-byte vectors by their maxima and rescans
+    the winning one: the lowest index still wins for ties inside one vector,
+    across vectors of one thread (vectors v and v + 1024), across threads,
+    and a row of -inf gives 0 (torch.argmax's answer)."""
+    from maple_amd.kernels import greedy_argmax
+
+    n = 151936
+    per = 8 if dtype == torch.bfloat16 else 4
+    x = torch.full((5, n), -3.0, device=dev).to(dtype)
+    x[0, 8 * per + 3] = 5.0
+    x[0, 8 * per + 1] = 5.0  # same vector, lower index
+    x[1, (7 + 1024) * per] = 2.0
+    x[1, 7 * per + per - 1] = 2.0  # same thread, earlier vector
+    x[2, 4000 * per + 2] = 1.0
+    x[2, 17 * per + 2] = 1.0  # another thread, lower index
+    x[2, 90000] = 1.0
+    x[3] = -float("inf")
+    x[4, n - 1] = 7.0  # the last element
+    got = greedy_argmax(x)
+    torch.testing.assert_close(got, torch.argmax(x.float(), dim=-1), rtol=0, atol=0)
+    assert got.tolist()[:3] == [8 * per + 1, 7 * per + per - 1, 17 * per + 2]
