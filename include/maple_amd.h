@@ -379,6 +379,29 @@ int ma_moe_fused_resident(int64_t n_experts, int64_t hidden, int64_t inter, int6
  * above on the null stream).  No reference counterpart. */
 int ma_moe_fused_form(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k);
 
+/*
+ * ma_moe_fused with the attention's output projection in front, in place of
+ * x_add: the launch computes x_add = ternary_gemv(attn, o_w, o_alpha) itself
+ * (attn bf16 [hidden], o_w [hidden, hidden / 16] uint32 codes, o_alpha
+ * [hidden] of alpha_dtype; the bits ma_ternary_gemv gives), then the add +
+ * RMSNorm (norm_weight required) and the layer as ma_moe_fused, optionally
+ * with the next projection; the residual added back is bf16(x + x_add).
+ * Only in the XCD-split form (ma_moe_fused_form == 1; MA_EVALUE otherwise):
+ * each XCD computes all of the projection and hands it to its own
+ * workgroups through its L2.  Same workspace as ma_moe_fused.  Replaces the
+ * o_proj of MapleAttention (src/maple_run/model.py:412-414, ternary_gemv)
+ * and the add + RMSNorm + MapleSparseMoeBlock of the decoder layer
+ * (model.py:448-474, fused_norm.py:128-161) at T = 1, two launches there.
+ */
+int ma_moe_fused_o(const void* x, const void* attn, const uint32_t* o_w, const void* o_alpha,
+                   const void* norm_weight, int norm_dtype, float eps, const void* gate_weight,
+                   const float* router_bias, int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k,
+                   const uint32_t* up_gate, const void* up_gate_alpha, const uint32_t* down,
+                   const void* down_alpha, int alpha_dtype, void* y, int32_t* topk_ids, float* topk_weight,
+                   void* workspace, size_t workspace_bytes, const uint32_t* next_w, const void* next_alpha,
+                   int next_alpha_dtype, const float* next_rms, float next_eps, int64_t next_rows,
+                   void* next_out, void* stream);
+
 /* *out = 1 if any ma_moe_fused call on this workspace timed out waiting
  * (synchronises the stream).  No reference counterpart: the reference has no
  * cross-workgroup wait. */

@@ -73,24 +73,26 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_rows(const void* __re
   // thread's best; strict, so the thread keeps its first vector holding its
   // maximum, and the lowest index in that vector is found once at the end.
   int64_t bv = -1;
+  constexpr uint32_t kNegInf4 = DT == MA_BF16 ? 0xff80ff80u : 0xff800000u;  // -inf in every element
   constexpr int U = 19;  // 1024 x 19 x 16 B = 304 KB in flight: one round for a 151936-token bf16 row
   for (int64_t v0 = tid; v0 < nvec; v0 += static_cast<int64_t>(kArgmaxThreads) * U) {
     uint4 q[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t vi = v0 + static_cast<int64_t>(kArgmaxThreads) * u;
-      q[u] = vi < nvec ? p[vi] : make_uint4(0xff80ff80u, 0xff80ff80u, 0xff800000u, 0xff800000u);
+      q[u] = vi < nvec ? p[vi] : make_uint4(kNegInf4, kNegInf4, kNegInf4, kNegInf4);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      const int64_t vi = v0 + static_cast<int64_t>(kArgmaxThreads) * u;
       const float m = vec_max<DT>(q[u]);
-      if (m > best) {  // absent vectors hold -inf and never win
+      if (m > best && vi < nvec) {  // vectors past the row never win (and are never re-read)
         best = m;
-        bv = v0 + static_cast<int64_t>(kArgmaxThreads) * u;
+        bv = vi;
       }
     }
   }
-  if (bv >= 0) {  // the lowest index of the winning vector holding the maximum
+  if (bv >= 0 && bv < nvec) {  // the lowest index of the winning vector holding the maximum
     float f[PER];
     vec_unpack<DT>(p[bv], f);
     int e = PER - 1;

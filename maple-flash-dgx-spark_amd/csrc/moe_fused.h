@@ -30,6 +30,8 @@ namespace ma {
 //   [256 KB, 320 KB)   XCD kernel with a next projection: one 8 KB region per
 //                      XCD holding that XCD's copy of y, two bf16 values per
 //                      tagged 64-bit word (tag << 32 | y[2m + 1] << 16 | y[2m])
+//   [320 KB, 384 KB)   XCD kernel with the O projection in front: each XCD's
+//                      copy of o, laid out as y
 constexpr int kSubB = 1, kTopB = kSubB + kBarGroups, kFlags = kTopB + 1;
 constexpr int kSubC = kFlags + kBarGroups, kTopC = kSubC + kBarGroups;
 constexpr size_t kLogitOff = 16384;
@@ -37,7 +39,8 @@ constexpr int kLogitStride = 16;  // uint64 words between logits
 constexpr size_t kMoeWsHeader = 49152;
 constexpr size_t kXEpochOff = 65536, kXRegionOff = 98304, kXRegion = 4096, kXPartOff = 131072;
 constexpr size_t kXYOff = kXPartOff + 8 * 2048 * 8, kXYRegion = 8192;
-constexpr size_t kXWsBytes = kXYOff + 8 * kXYRegion;
+constexpr size_t kXOOff = kXYOff + 8 * kXYRegion;
+constexpr size_t kXWsBytes = kXOOff + 8 * kXYRegion;
 static_assert(kTopC < static_cast<int>(kLogitOff / 256), "workspace lines");
 static_assert(kLogitOff + 256 * kLogitStride * 8 <= kMoeWsHeader, "workspace logits");
 static_assert(kMoeWsHeader + 8 * 768 * 2 <= kXEpochOff, "grid kernel h");
@@ -206,6 +209,7 @@ int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, in
                    int64_t hidden, int64_t inter, const uint32_t* up_gate, const void* up_gate_alpha,
                    const uint32_t* down, const void* down_alpha, int alpha_dtype, void* y, int32_t* topk_ids,
                    float* topk_weight, void* workspace, const uint32_t* next_w, const void* next_alpha,
-                   const float* next_rms, float next_eps, int64_t next_rows, void* next_out, hipStream_t st);
+                   const float* next_rms, float next_eps, int64_t next_rows, void* next_out, const void* attn,
+                   const uint32_t* o_w, const void* o_alpha, hipStream_t st);
 
 }  // namespace ma

@@ -569,16 +569,14 @@ extern "C" size_t ma_moe_fused_workspace_bytes(int64_t n_experts, int64_t hidden
   return ws_bytes(n_experts, s->grid, inter, top_k);
 }
 
-extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_weight,
-                            int norm_dtype, float eps, const void* residual,
-                            const void* gate_weight, const float* router_bias, int64_t n_experts,
-                            int64_t hidden, int64_t inter, int64_t top_k,
-                            const uint32_t* up_gate, const void* up_gate_alpha,
-                            const uint32_t* down, const void* down_alpha, int alpha_dtype, void* y,
-                            int32_t* topk_ids, float* topk_weight, void* workspace,
-                            size_t workspace_bytes, const uint32_t* next_w,
-                            const void* next_alpha, int next_alpha_dtype, const float* next_rms,
-                            float next_eps, int64_t next_rows, void* next_out, void* stream) {
+static int moe_fused_impl(const void* x, const void* x_add, const void* norm_weight, int norm_dtype, float eps,
+                          const void* residual, const void* gate_weight, const float* router_bias,
+                          int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k, const uint32_t* up_gate,
+                          const void* up_gate_alpha, const uint32_t* down, const void* down_alpha, int alpha_dtype,
+                          void* y, int32_t* topk_ids, float* topk_weight, void* workspace, size_t workspace_bytes,
+                          const uint32_t* next_w, const void* next_alpha, int next_alpha_dtype,
+                          const float* next_rms, float next_eps, int64_t next_rows, void* next_out, void* stream,
+                          const void* attn, const uint32_t* o_w, const void* o_alpha) {
   const FusedShape* s = find_shape(hidden, inter, top_k);
   if (!s)
     return fail(MA_EVALUE, "moe_fused: shape (hidden %lld, inter %lld, top_k %lld) not built",
@@ -586,7 +584,7 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
                 static_cast<long long>(top_k));
   if (n_experts < top_k || n_experts > 256 || n_experts > static_cast<int64_t>(s->grid))
     return fail(MA_EVALUE, "moe_fused: %lld experts unsupported", static_cast<long long>(n_experts));
-  if (x_add && !norm_weight) return fail(MA_EVALUE, "moe_fused: add without norm weight");
+  if ((x_add || o_w) && !norm_weight) return fail(MA_EVALUE, "moe_fused: add without norm weight");
   if (alpha_dtype != MA_F32 && alpha_dtype != MA_BF16)
     return fail(MA_ETYPE, "moe_fused: row_alpha dtype %d (float32 or bfloat16)", alpha_dtype);
   if (norm_weight && norm_dtype != MA_F32 && norm_dtype != MA_BF16)
@@ -616,10 +614,15 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
     return fail(MA_ERUNTIME, "moe_fused: its %d workgroups wait on each other but the device holds %lld at once",
                 s->grid, static_cast<long long>(capacity));
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (o_w && (!attn || !o_alpha || !a16(attn) || !a16(o_w)))
+    return fail(MA_EVALUE, "moe_fused_o: the attention output and O weights (16-byte aligned) and row scales are needed");
   if (moe_xcd_supported(n_experts, hidden, inter, top_k, st))
     return moe_xcd_launch(x, x_add, norm_weight, norm_dtype, eps, residual, gate_weight, router_bias, n_experts,
                           hidden, inter, up_gate, up_gate_alpha, down, down_alpha, alpha_dtype, y, topk_ids,
-                          topk_weight, workspace, next_w, next_alpha, next_rms, next_eps, next_rows, next_out, st);
+                          topk_weight, workspace, next_w, next_alpha, next_rms, next_eps, next_rows, next_out, attn,
+                          o_w, o_alpha, st);
+  if (o_w)
+    return fail(MA_EVALUE, "moe_fused_o: the O projection in the launch needs the XCD-split form (ma_moe_fused_form)");
 #define MA_FUSED_ARGS                                                                            \
   static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(x_add), norm_weight, norm_dtype, \
       eps, static_cast<const uint16_t*>(residual), static_cast<const uint16_t*>(gate_weight),    \
@@ -652,6 +655,38 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
 #undef MA_FUSED_LAUNCH
 #undef MA_FUSED_ARGS
   return check_launch("moe_fused");
+}
+
+extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_weight,
+                            int norm_dtype, float eps, const void* residual,
+                            const void* gate_weight, const float* router_bias, int64_t n_experts,
+                            int64_t hidden, int64_t inter, int64_t top_k,
+                            const uint32_t* up_gate, const void* up_gate_alpha,
+                            const uint32_t* down, const void* down_alpha, int alpha_dtype, void* y,
+                            int32_t* topk_ids, float* topk_weight, void* workspace,
+                            size_t workspace_bytes, const uint32_t* next_w,
+                            const void* next_alpha, int next_alpha_dtype, const float* next_rms,
+                            float next_eps, int64_t next_rows, void* next_out, void* stream) {
+  return moe_fused_impl(x, x_add, norm_weight, norm_dtype, eps, residual, gate_weight, router_bias, n_experts,
+                        hidden, inter, top_k, up_gate, up_gate_alpha, down, down_alpha, alpha_dtype, y, topk_ids,
+                        topk_weight, workspace, workspace_bytes, next_w, next_alpha, next_alpha_dtype, next_rms,
+                        next_eps, next_rows, next_out, stream, nullptr, nullptr, nullptr);
+}
+
+extern "C" int ma_moe_fused_o(const void* x, const void* attn, const uint32_t* o_w, const void* o_alpha,
+                              const void* norm_weight, int norm_dtype, float eps, const void* gate_weight,
+                              const float* router_bias, int64_t n_experts, int64_t hidden, int64_t inter,
+                              int64_t top_k, const uint32_t* up_gate, const void* up_gate_alpha,
+                              const uint32_t* down, const void* down_alpha, int alpha_dtype, void* y,
+                              int32_t* topk_ids, float* topk_weight, void* workspace, size_t workspace_bytes,
+                              const uint32_t* next_w, const void* next_alpha, int next_alpha_dtype,
+                              const float* next_rms, float next_eps, int64_t next_rows, void* next_out,
+                              void* stream) {
+  if (!o_w) return fail(MA_EVALUE, "moe_fused_o: no O weights");
+  return moe_fused_impl(x, nullptr, norm_weight, norm_dtype, eps, nullptr, gate_weight, router_bias, n_experts,
+                        hidden, inter, top_k, up_gate, up_gate_alpha, down, down_alpha, alpha_dtype, y, topk_ids,
+                        topk_weight, workspace, workspace_bytes, next_w, next_alpha, next_alpha_dtype, next_rms,
+                        next_eps, next_rows, next_out, stream, attn, o_w, o_alpha);
 }
 
 extern "C" int ma_moe_fused_form(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k) {

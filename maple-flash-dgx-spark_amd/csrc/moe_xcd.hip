@@ -66,7 +66,8 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     uint16_t* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ wts_out,
     uint32_t* __restrict__ ws, const uint32_t* __restrict__ nx_w, const void* __restrict__ nx_alpha,
     const float* __restrict__ nx_rms, float nx_eps, int nx_rows,
-    uint16_t* __restrict__ nx_out) {
+    uint16_t* __restrict__ nx_out, const uint16_t* __restrict__ attn, const uint32_t* __restrict__ o_w,
+    const void* __restrict__ o_alpha) {
   constexpr int TK = kXcds;  // one slot per XCD
   constexpr int W = 8;
   constexpr int LPRH = 32;
@@ -105,6 +106,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   uint32_t* const xh = reinterpret_cast<uint32_t*>(wsb + kXRegionOff + xcd * kXRegion + 512);
   uint64_t* const part = reinterpret_cast<uint64_t*>(wsb + kXPartOff);
   uint64_t* const yx = reinterpret_cast<uint64_t*>(wsb + kXYOff + xcd * kXYRegion);
+  uint64_t* const ox = reinterpret_cast<uint64_t*>(wsb + kXOOff + xcd * kXYRegion);
   const uint32_t tag = ld_coh32(calls) + 1u;
   const uint32_t tag16 = tag & 0xffffu;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -114,9 +116,11 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   // 64 lw + lane with a next projection (every XCD combines all of y), else
   // rows wg * FR + lane, lanes < FR.
   const int ro = nx_w ? 64 * lw + lane : wg * FR + (lane < FR ? lane : 0);
-  const uint16_t* const res_a = xb ? xa : (residual ? residual : xa);
+  const bool addp = xb || o_w;  // x + (add or the O projection), then RMSNorm
+  const uint16_t* const res_a = addp ? xa : (residual ? residual : xa);
   const uint16_t* const res_b = xb ? xb : xa;
-  const uint32_t ra = res_a[ro], rb = res_b[ro];
+  const uint32_t ra = res_a[ro];
+  uint32_t rb = o_w ? 0u : res_b[ro];  // with the O projection: from the XCD's copy of o, below
 
   // ---- 1. x (optionally add + RMSNorm) staged once per workgroup: thread
   // t < NWH takes word t, in bf16 (for the router waves) and as x' pairs (for
@@ -133,6 +137,38 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       gr[i][1] = gp[1];
     }
   }
+  // ---- 0. the O projection (optional): o = ternary_gemv(attn, o_w, o_alpha)
+  // with the standalone fast GEMV's per-lane arithmetic (so the same bits);
+  // every XCD computes all of o (wave w of workgroup j: rows 64 j + 8 w ..
+  // + 8, two per pass) and hands it to its workgroups through its L2, two
+  // bf16 values per tagged word, as y below.
+  __shared__ __align__(16) uint32_t os[NWH][8];
+  __shared__ float oc[NWH];
+  if (o_w) {
+    const int okl = lane % LPRH, osub = lane / LPRH;
+    constexpr int OP = 64 / (W * RPIH);  // passes of RPIH rows per wave
+    uint32_t wo[OP][KWH];
+    float ao[OP];
+#pragma unroll
+    for (int p = 0; p < OP; ++p) {
+      const int r = 64 * lw + (64 / W) * wv + RPIH * p + osub;
+      load_words_v<KWH>(o_w + static_cast<int64_t>(r) * NWH + okl * KWH, wo[p]);
+      ao[p] = ld_t<ADT>(o_alpha, r);
+    }
+    stage_row(attn, NWH, os, oc);
+    __syncthreads();
+    XSlice<KWH> osl;
+    slice_from_lds<KWH>(os, oc, okl, osl);
+    const ExpandConsts kc;
+#pragma unroll
+    for (int p = 0; p < OP; ++p) {
+      const float d = group_sum<LPRH>(slice_dot<KWH>(wo[p], osl, kc) * ao[p]);
+      const uint32_t bits = f32_to_bf16(d);
+      const uint32_t odd = __shfl(bits, LPRH, 64);  // row r + 1, held by lane LPRH
+      const int r = 64 * lw + (64 / W) * wv + RPIH * p;
+      if (lane == 0) st_l2_64(&ox[r >> 1], (static_cast<uint64_t>(tag) << 32) | bits | (odd << 16));
+    }
+  }
   {
     static_assert(NWH <= 512, "one word of x per thread");
     const int wc = tid < NWH ? tid : NWH - 1;
@@ -147,11 +183,34 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
         v[2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
       }
     }
-    if (xb) {
+    if (addp) {
       float nw[16];
-      const uint4 b0 = reinterpret_cast<const uint4*>(xb + wc * 16)[0];
-      const uint4 b1 = reinterpret_cast<const uint4*>(xb + wc * 16)[1];
-      const uint32_t ub[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+      uint32_t ub[8];
+      if (o_w) {  // word wc of o: tagged words 8 wc .. + 8 of the XCD's copy
+        const CoherentBuf oq(ox, NWH * 8 * 8);
+        uint4 q[4];
+        for (;;) {
+          MA_POLL_RELOAD();
+#pragma unroll
+          for (int i = 0; i < 4; ++i) q[i] = oq.ld4u(static_cast<uint32_t>((8 * wc + 2 * i) * 8));
+          uint32_t bad = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) bad |= (q[i].y ^ tag) | (q[i].w ^ tag);
+          if (__all(bad == 0) || timed_out) break;
+          __builtin_amdgcn_s_sleep(1);
+          timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ub[2 * i] = q[i].x;
+          ub[2 * i + 1] = q[i].z;
+        }
+      } else {
+        const uint4 b0 = reinterpret_cast<const uint4*>(xb + wc * 16)[0];
+        const uint4 b1 = reinterpret_cast<const uint4*>(xb + wc * 16)[1];
+        ub[0] = b0.x, ub[1] = b0.y, ub[2] = b0.z, ub[3] = b0.w;
+        ub[4] = b1.x, ub[5] = b1.y, ub[6] = b1.z, ub[7] = b1.w;
+      }
       if (norm_dt == MA_F32) {
         const float4* np = reinterpret_cast<const float4*>(static_cast<const float*>(norm_w) + wc * 16);
 #pragma unroll
@@ -386,6 +445,18 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     }
   }
 
+  // The O values of this workgroup's combine rows (wave 0), from the XCD's copy.
+  if (o_w && wv == 0) {
+    for (;;) {
+      const uint64_t q = ld_coh64(&ox[ro >> 1]);
+      const bool ok = static_cast<uint32_t>(q >> 32) == tag;
+      rb = (ro & 1) ? (static_cast<uint32_t>(q) >> 16) : (static_cast<uint32_t>(q) & 0xffffu);
+      if (__all(ok) || timed_out) break;
+      __builtin_amdgcn_s_sleep(1);
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+    }
+  }
+
   // ---- 6. y = residual + the slots' values in slot order.  With a next
   // projection every XCD combines all of y for its own workgroups (wave w of
   // workgroup lw polls slot w's values of rows 64 lw .. + 64) and hands it
@@ -407,7 +478,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     s_pv[wv][lane] = pv;
     __syncthreads();
     if (wv == 0) {
-      float v = xb ? bf16_to_f32(f32_to_bf16(__uint_as_float(ra << 16) + __uint_as_float(rb << 16)))
+      float v = addp ? bf16_to_f32(f32_to_bf16(__uint_as_float(ra << 16) + __uint_as_float(rb << 16)))
                    : residual ? __uint_as_float(ra << 16) : 0.f;
 #pragma unroll
       for (int k = 0; k < TK; ++k) v += s_pv[k][lane];
@@ -427,7 +498,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       __builtin_amdgcn_s_sleep(1);
       timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
     }
-    float v = xb ? bf16_to_f32(f32_to_bf16(__uint_as_float(ra << 16) + __uint_as_float(rb << 16)))
+    float v = addp ? bf16_to_f32(f32_to_bf16(__uint_as_float(ra << 16) + __uint_as_float(rb << 16)))
                  : residual ? __uint_as_float(ra << 16) : 0.f;
 #pragma unroll
     for (int k = 0; k < TK; ++k) v += __shfl(pv, k * FR + r, 64);
@@ -476,7 +547,8 @@ int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, in
                    int64_t hidden, int64_t inter, const uint32_t* up_gate, const void* up_gate_alpha,
                    const uint32_t* down, const void* down_alpha, int alpha_dtype, void* y, int32_t* topk_ids,
                    float* topk_weight, void* workspace, const uint32_t* next_w, const void* next_alpha,
-                   const float* next_rms, float next_eps, int64_t next_rows, void* next_out, hipStream_t st) {
+                   const float* next_rms, float next_eps, int64_t next_rows, void* next_out, const void* attn,
+                   const uint32_t* o_w, const void* o_alpha, hipStream_t st) {
   (void)hidden;
   const void* kern = alpha_dtype == MA_F32 ? xcd_kernel_t<MA_F32>(inter) : xcd_kernel_t<MA_BF16>(inter);
   int64_t capacity = 0;
@@ -489,7 +561,8 @@ int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, in
       static_cast<const uint16_t*>(residual), static_cast<const uint16_t*>(gate_weight), router_bias,    \
       static_cast<int>(n_experts), up_gate, up_gate_alpha, down, down_alpha, static_cast<uint16_t*>(y), \
       topk_ids, topk_weight, static_cast<uint32_t*>(workspace), next_w, next_alpha, next_rms, next_eps, \
-      static_cast<int>(next_rows), static_cast<uint16_t*>(next_out)
+      static_cast<int>(next_rows), static_cast<uint16_t*>(next_out), static_cast<const uint16_t*>(attn), o_w, \
+      o_alpha
   const dim3 grid(kXcds * kXcdWgs), block(512);
   if (alpha_dtype == MA_F32) {
     if (inter == 768)

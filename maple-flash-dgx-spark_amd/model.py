@@ -36,7 +36,7 @@ from .kernels.fused_norm import rms_norm
 from .kernels.greedy import greedy_argmax
 from .kernels.rtn4 import rtn4_embedding, rtn4_gemv
 from .kernels.ternary_gemv import combine_gemv_supported, ternary_gemv, ternary_gemv_combine
-from .moe import PendingCombine, fused_supported, moe_fused, moe_layer
+from .moe import PendingCombine, fused_form, fused_supported, moe_fused, moe_layer
 
 
 @dataclass
@@ -179,11 +179,13 @@ class KVCache:
 
 class SyntheticDecoder:
     def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 4096 + 128,
-                 fused_moe: bool = True, fused_o: bool = False, combine_next: bool = True):
+                 fused_moe: bool = True, fused_o: bool = False, combine_next: bool = True,
+                 o_in_moe: bool = False):
         self.cfg = cfg
         self.fused_moe = fused_moe
         self.combine_next = combine_next
         self.fused_o = fused_o
+        self.o_in_moe = o_in_moe
         self.device = torch.device(device)
         self.max_len = max_len
         c, dev, s = cfg, self.device, seed * 1000
@@ -205,12 +207,14 @@ class SyntheticDecoder:
     @classmethod
     def from_weights(cls, cfg: DecoderConfig, device, layers: list, embed: tuple, lm_head: tuple,
                      final_norm: torch.Tensor, max_len: int = 4096 + 128, fused_moe: bool = True,
-                     fused_o: bool = False, combine_next: bool = True) -> "SyntheticDecoder":
+                     fused_o: bool = False, combine_next: bool = True,
+                     o_in_moe: bool = False) -> "SyntheticDecoder":
         """A decoder over given weights (``checkpoint.load_decoder``) instead of
         the seeded synthetic ones."""
         self = cls.__new__(cls)
         self.cfg = cfg
         self.fused_moe, self.fused_o, self.combine_next = fused_moe, fused_o, combine_next
+        self.o_in_moe = o_in_moe
         self.device = torch.device(device)
         self.max_len = max_len
         self.layers = list(layers)
@@ -267,7 +271,13 @@ class SyntheticDecoder:
         else:
             attn = decode_attention(qkv, L.q_norm, L.k_norm, self.cos, self.sin, cache.k[i], cache.v[i],
                                     seqlen, cache.attn_ws, **akw)
-            o = ternary_gemv(attn.reshape(bsz, -1), L.o, L.o_alpha)
+            # o_in_moe: at batch 1 the XCD-split MoE launch computes the output
+            # projection itself (same bits; measured 1,294 against 1,306 tok/s
+            # with the separate launch, so off by default)
+            o_moe = (bsz == 1 and self.o_in_moe and self.fused_moe and fused_supported(L.moe, c.top_k, hidden)
+                     and fused_form(L.moe, c.top_k) == 1 and c.heads * c.head_dim == c.hidden
+                     and L.o_alpha.dtype == L.moe.up_gate_alpha.dtype)
+            o = None if o_moe else ternary_gemv(attn.reshape(bsz, -1), L.o, L.o_alpha)
         next_qkv = None
         if bsz == 1 and self.fused_moe and fused_supported(L.moe, c.top_k, hidden):
             # add + RMSNorm + router + experts + combine (+ the next layer's
@@ -277,7 +287,8 @@ class SyntheticDecoder:
                 n = self.layers[i + 1]
                 nl = (n.qkv, n.qkv_alpha, n.input_ln, c.eps)
             out = moe_fused(hidden, L.moe, c.top_k, add=o, norm_weight=L.post_ln, eps=c.eps,
-                            next_linear=nl)
+                            next_linear=nl,
+                            o_linear=None if o is not None else (attn.reshape(1, -1), L.o, L.o_alpha))
             y, ids = out[0], out[1]
             if nl is not None:
                 next_qkv = out[3]

@@ -89,7 +89,7 @@ def moe_fused_timed_out(device: torch.device | int = 0) -> bool:
 
 def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tensor | None = None,
               *, add: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None,
-              eps: float = 1e-6, next_linear: tuple | None = None):
+              eps: float = 1e-6, next_linear: tuple | None = None, o_linear: tuple | None = None):
     """One token through the whole MoE layer in one launch.
 
     Plain: ``y = x_res + sum_j w_j down_j(swiglu_j(x))`` with ``x_res =
@@ -102,13 +102,30 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
     [H], rms_eps)``: the same launch also computes the next layer's input
     projection ``ternary_gemv(y, packed, alpha, rms_weight=..., rms_eps=...)``
     (the same bits) and returns it as a fourth output ``[1, N]``.
+
+    ``o_linear = (attn [1, H] bf16, packed [H, H/16] uint32, alpha [H])`` in
+    place of ``add``: the launch computes ``add = ternary_gemv(attn, packed,
+    alpha)`` itself (the attention's output projection, the same bits as the
+    separate GEMV; alpha of the experts' row_alpha dtype); needs the XCD-split
+    form (``fused_form(layer, top_k) == 1``).
     """
     hidden = x.shape[-1]
     xf = x.reshape(1, hidden).contiguous()
     ad = None if add is None else add.reshape(1, hidden).contiguous()
-    if ad is not None and norm_weight is None:
+    if o_linear is not None:
+        if ad is not None:
+            raise ValueError("moe_fused: add and o_linear are exclusive")
+        o_in, o_w, o_a = o_linear
+        o_in = o_in.reshape(1, hidden).contiguous()
+        if o_in.dtype != torch.bfloat16 or o_w.dtype != torch.uint32 or tuple(o_w.shape) != (hidden, hidden // 16):
+            raise TypeError("o_linear must be (bf16 [1, H], uint32 [H, H/16], alpha [H])")
+        if o_a.dtype != layer.up_gate_alpha.dtype:
+            raise TypeError("o_linear alpha must have the experts' row_alpha dtype")
+        o_a = o_a.contiguous()
+    if (ad is not None or o_linear is not None) and norm_weight is None:
         raise ValueError("moe_fused: add needs norm_weight")
-    res = None if residual is None or ad is not None else residual.reshape(1, hidden).contiguous()
+    res = (None if residual is None or ad is not None or o_linear is not None
+           else residual.reshape(1, hidden).contiguous())
     nbytes = int(_lib.load().ma_moe_fused_workspace_bytes(layer.n_experts, hidden, layer.inter, top_k))
     if nbytes == 0:
         raise ValueError(f"moe_fused: shape (hidden {hidden}, inter {layer.inter}, top_k {top_k}) "
@@ -137,6 +154,19 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
         if nx_a.dtype != layer.up_gate_alpha.dtype:
             raise TypeError("next_linear alpha must have the experts' row_alpha dtype")
         nx_out = torch.empty(1, nx_rows, device=x.device, dtype=torch.bfloat16)
+    if o_linear is not None:
+        _lib.call(
+            "ma_moe_fused_o",
+            _lib.ptr(xf), _lib.ptr(o_in), _lib.ptr(o_w), _lib.ptr(o_a), _lib.ptr(nw),
+            _lib.dtype_code(nw, "norm_weight"), float(eps),
+            _lib.ptr(layer.gate_weight), _lib.ptr(bias), layer.n_experts, hidden, layer.inter, top_k,
+            _lib.ptr(layer.up_gate_packed), _lib.ptr(layer.up_gate_alpha), _lib.ptr(layer.down_packed),
+            _lib.ptr(layer.down_alpha), alpha_dt, _lib.ptr(y), _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(ws),
+            ws.numel(), _lib.ptr(nx_w), _lib.ptr(nx_a),
+            _lib.dtype_code(nx_a, "row_alpha") if nx_a is not None else 0, _lib.ptr(nx_r),
+            float(nx_eps), nx_rows, _lib.ptr(nx_out), _lib.stream_of(x),
+        )
+        return (y, ids, wts, nx_out) if next_linear is not None else (y, ids, wts)
     _lib.call(
         "ma_moe_fused",
         _lib.ptr(xf), _lib.ptr(ad), _lib.ptr(nw),

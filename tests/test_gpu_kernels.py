@@ -493,3 +493,17 @@ def test_greedy_argmax_ties_within_and_across_vectors(dev, dtype):
     got = greedy_argmax(x)
     torch.testing.assert_close(got, torch.argmax(x.float(), dim=-1), rtol=0, atol=0)
     assert got.tolist()[:3] == [8 * per + 1, 7 * per + per - 1, 17 * per + 2]
+
+
+@pytest.mark.parametrize("n", [1024, 4096, 20000])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_greedy_argmax_all_negative_short_rows(dev, n, dtype):
+    """Rows whose every value is negative, short enough that most threads of
+    the workgroup have no vector of the row at all: the vectors past the row
+    (filled with -inf, never re-read) must not win."""
+    from maple_amd.kernels import greedy_argmax
+
+    g = torch.Generator(device=dev).manual_seed(n)
+    x = (-1.0 - torch.rand(4, n, generator=g, device=dev)).to(dtype)
+    got = greedy_argmax(x)
+    torch.testing.assert_close(got, torch.argmax(x.float(), dim=-1), rtol=0, atol=0)

@@ -291,6 +291,43 @@ def test_fused_forms_next_projection_on_one_workspace(dev, monkeypatch, layers):
     assert not moe_fused_timed_out(dev)
 
 
+@pytest.mark.parametrize("alpha_dtype", [torch.bfloat16, torch.float32])
+def test_fused_o_projection_equals_two_launches(dev, alpha_dtype):
+    """moe_fused(..., o_linear=(attn, W_o, alpha_o)) -- the attention's output
+    projection computed by every XCD in the MoE launch -- gives the bits of
+    ternary_gemv followed by moe_fused(..., add=o): y, ids, weights and the
+    next projection, over consecutive calls interleaved with plain calls on
+    one workspace."""
+    from maple_amd.moe import fused_form
+
+    Ls = [synthetic.make_moe_layer(2048, 64, 768, seed=120 + i, device=dev) for i in range(2)]
+    if alpha_dtype == torch.float32:
+        for L in Ls:
+            L.up_gate_alpha = L.up_gate_alpha.float()
+            L.down_alpha = L.down_alpha.float()
+    assert fused_form(Ls[0], 8) == 1, "the XCD split is expected on an 8-XCD MI355X"
+    wo, ao = synthetic.ternary_linear(2048, 2048, 131, dev)
+    ao = ao.to(alpha_dtype)
+    nl = _next_linear(2560, 2048, 132, dev)
+    nl = (nl[0], nl[1].to(alpha_dtype), nl[2], nl[3])
+    w = torch.rand(2048, device=dev) + 0.5
+    for step in range(6):
+        L = Ls[step % 2]
+        x = synthetic.randn_bf16((1, 2048), 1800 + step, dev)
+        attn = synthetic.randn_bf16((1, 2048), 1900 + step, dev)
+        proj = step % 3 != 2
+        o = ternary_gemv(attn, wo, ao)
+        ref = moe_fused(x, L, 8, add=o, norm_weight=w, eps=1e-6, next_linear=nl if proj else None)
+        got = moe_fused(x, L, 8, norm_weight=w, eps=1e-6, next_linear=nl if proj else None,
+                        o_linear=(attn, wo, ao))
+        moe_fused(x, L, 8)  # a plain call between
+        torch.cuda.synchronize()
+        assert len(got) == len(ref)
+        for k, (a, b) in enumerate(zip(got, ref)):
+            assert torch.equal(a, b), f"step {step} output {k}"
+    assert not moe_fused_timed_out(dev)
+
+
 _FIRST_CALL_CAPTURED = r"""
 import os, sys, torch
 sys.path.insert(0, sys.argv[1])
