@@ -39,7 +39,7 @@ def _check_routing(x, L, ids, wts, k=K):
     rid, rw, probs = ok.router_topk(np_f(x), np_f(L.gate_weight), k,
                                     bias=None if L.router_bias is None else np_f(L.router_bias))
     safe = tie_safe_rows(probs, k)
-    assert safe.mean() > 0.98
+    assert safe.sum() >= len(safe) - max(1, len(safe) // 50), "too many near-tie rows for the check to mean much"
     np.testing.assert_array_equal(ids.cpu().numpy()[safe], rid[safe])
     np.testing.assert_allclose(wts.cpu().numpy()[safe], rw[safe], rtol=1e-4, atol=1e-6)
 
@@ -180,7 +180,8 @@ def test_moe_route_equals_separate_launches(dev, tokens, n_exp, hidden, with_add
     k = min(K, n_exp)
     x = synthetic.randn_bf16((tokens, hidden), 300 + tokens, dev)
     add = synthetic.randn_bf16((tokens, hidden), 400 + tokens, dev) if with_add else None
-    nw = (torch.rand(hidden, device=dev) + 0.5).to(nw_dtype)
+    g = torch.Generator(device=dev).manual_seed(500 + tokens)
+    nw = (torch.rand(hidden, device=dev, generator=g) + 0.5).to(nw_dtype)
     for call in range(2):
         h, xn, ids, wts, d = moe_route(x, L, k, nw, 1e-6, add=add)
         if with_add:
