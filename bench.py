@@ -463,8 +463,23 @@ def counters_pass(dev, kind: str, n_layers: int) -> int:
             rtn4_gemv(xh, w, sc, sc, group_size=128)
             decode_attention(qkv, nw, nw, cos, sin, kc, vc, seqlen, ws, num_heads=32, num_kv_heads=4,
                              head_dim=64, rotary_dim=32, scale=0.125)
+        # the decoder's MoE layer at 32 tokens (routing launch, grouped SwiGLU and down)
+        from maple_amd.moe import moe_layer
+
+        layer = synthetic.make_moe_layer(HIDDEN, 64, INTER, seed=5, device=dev)
+        xm = synthetic.randn_bf16((batch, HIDDEN), 6, dev)
+        am = synthetic.randn_bf16((batch, HIDDEN), 7, dev)
+        lnw = torch.ones(HIDDEN, device=dev)
+        torch.cuda.synchronize()
+        hit = 0
+        for _ in range(4):
+            _, ids = moe_layer(xm, layer, TOPK, lnw, 1e-6, add=am)
+            hit = int(torch.unique(ids).numel())
         info = {"rtn4_launches": 4, "rtn4_bytes_per_launch": vocab * HIDDEN // 2 + 2 * vocab * 16 * 2,
-                "attn_launches": 4, "attn_kv_bytes_per_launch": batch * 2 * 4 * 4097 * 64 * 2}
+                "attn_launches": 4, "attn_kv_bytes_per_launch": batch * 2 * 4 * 4097 * 64 * 2,
+                "grouped_launches": 4, "experts_hit": hit,
+                "swiglu_weight_bytes_per_launch": hit * (2 * INTER * HIDDEN // 4 + 2 * INTER * 2),
+                "down_weight_bytes_per_launch": hit * (HIDDEN * INTER // 4 + HIDDEN * 2)}
     else:
         raise ValueError(f"unknown counters pass {kind}")
     torch.cuda.synchronize()
