@@ -41,7 +41,14 @@ def head_norm_rope(x, w, cos_row, sin_row, rotary_dim, eps, use_rope=True):
 
 
 def gqa(q, k_cache, v_cache, kv_len, scale, window=None):
-    """Attention of one row's query heads over positions [start, kv_len)."""
+    """Attention of one row's query heads over positions [start, kv_len)
+    (``decode_attn.py:236-289``): scores ``K q * scale``, ``p = exp(s - max)``,
+    the sum ``l`` over the unrounded ``p``, and ``P`` rounded to bf16 (the
+    cache dtype) before ``P V`` (``:282-289``); output ``(bf16(P) V) / l``.
+    The reference takes the max per tile of positions as it streams (running
+    max); here it is the max over all positions, the same thing when every
+    position sits in one tile, and otherwise a different bf16 rounding point
+    of P (relative error 2^-9 of a term either way)."""
     nq, d = q.shape
     nkv = k_cache.shape[0]
     group = nq // nkv
@@ -52,8 +59,33 @@ def gqa(q, k_cache, v_cache, kv_len, scale, window=None):
         V = np.asarray(v_cache[h // group, start:kv_len], np.float64)
         s = K @ q[h] * scale
         p = np.exp(s - s.max())
-        out[h] = (p / p.sum()) @ V
+        out[h] = (bf(p) @ V) / p.sum()
     return out
+
+
+def attend_row(qkv_row, L: dict, c: dict, k_rows, v_rows, pos: int):
+    """The attention of one batch row at position ``pos`` (``model.py:368-414``
+    decode branch, ``decode_attn.py:15-163,166-359``): the ``[q; k; v]`` row
+    split into heads; q and the new k RMS-normalised per head and roped
+    (rotate-half over the first ``rotary_dim`` dims, skipped on NoPE layers);
+    the new k and v written at ``pos`` of this row's cache ``k_rows`` /
+    ``v_rows`` ``[n_kv, max_len, D]``; GQA over positions up to ``pos`` at
+    scale ``head_dim ** -0.5`` (``model.py:343``).  Returns the attention
+    output ``[heads * head_dim]`` in float64 (not yet rounded)."""
+    nq, nkv, d = c["heads"], c["kv_heads"], c["head_dim"]
+    rot, eps = c["rotary_dim"], c["eps"]
+    use_rope = L.get("use_rope", True)
+    cs = bf(c["cos"][pos]) if rot else None
+    sn = bf(c["sin"][pos]) if rot else None
+    q = np.stack([bf(head_norm_rope(qkv_row[hh * d:(hh + 1) * d], L["q_norm"], cs, sn, rot, eps, use_rope=use_rope))
+                  for hh in range(nq)])
+    for kh in range(nkv):
+        o0 = (nq + kh) * d
+        k_rows[kh, pos] = bf(head_norm_rope(qkv_row[o0:o0 + d], L["k_norm"], cs, sn, rot, eps, use_rope=use_rope))
+        o1 = (nq + nkv + kh) * d
+        v_rows[kh, pos] = qkv_row[o1:o1 + d]
+    kv_len = min(pos + 1, k_rows.shape[1])
+    return gqa(q, k_rows, v_rows, kv_len, d ** -0.5, window=L.get("window")).reshape(-1)
 
 
 def decoder_layer(L: dict, c: dict, h, cache: dict, i: int, *, router_ids=None):
@@ -74,17 +106,7 @@ def decoder_layer(L: dict, c: dict, h, cache: dict, i: int, *, router_ids=None):
     attn = np.zeros((bsz, nq * d))
     for b in range(bsz):
         pos = min(int(cache["seqlen"][b]), cache["k"][i].shape[2] - 1)
-        cs = bf(c["cos"][pos]) if rot else None
-        sn = bf(c["sin"][pos]) if rot else None
-        q = np.stack([bf(head_norm_rope(qkv[b, hh * d:(hh + 1) * d], L["q_norm"], cs, sn, rot, eps, use_rope=L.get("use_rope", True)))
-                      for hh in range(nq)])
-        for kh in range(nkv):
-            o0 = (nq + kh) * d
-            cache["k"][i][b, kh, pos] = bf(head_norm_rope(qkv[b, o0:o0 + d], L["k_norm"], cs, sn, rot, eps, use_rope=L.get("use_rope", True)))
-            o1 = (nq + nkv + kh) * d
-            cache["v"][i][b, kh, pos] = qkv[b, o1:o1 + d]
-        kv_len = min(pos + 1, cache["k"][i].shape[2])
-        attn[b] = bf(gqa(q, cache["k"][i][b], cache["v"][i][b], kv_len, d ** -0.5, window=L.get("window"))).reshape(-1)
+        attn[b] = bf(attend_row(qkv[b], L, c, cache["k"][i][b], cache["v"][i][b], pos))
     o = bf(ok.ternary_gemv(attn, L["o"], L["o_alpha"]))
     s_full = h + o
     res = bf(s_full)

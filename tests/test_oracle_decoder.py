@@ -7,11 +7,21 @@ is the identity at position 0, and makes q(a).k(b) depend on a - b only;
 GQA (src/maple_run/kernels/decode_attn.py:167-359) gives the mean of V for
 equal scores, picks V's row for a dominant key, maps query head h to KV head
 h // group, and reads only the last ``window`` positions.
+
+Those properties hold for either rotation direction and any score scale, so
+known answers fix the rest: the rotation direction and the half split of
+rotate-half (``_rotate_half`` = cat(-x2, x1), ``q cos + rotate_half(q) sin``,
+model.py:48-61), the layer's score scale head_dim ** -0.5 (model.py:343,
+through ``attend_row``), and P rounded to bf16 before P V with the sum over
+the unrounded P (decode_attn.py:270-289).
 """
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
+import pytest
 
 from oracle import decoder as od
 
@@ -80,3 +90,69 @@ def test_gqa_dominant_key_and_window():
     # window 3 over kv_len 10 reads positions 7, 8, 9 only: key 6 is outside
     out_w = od.gqa(q, k, v, n, 1.0, window=3)
     np.testing.assert_allclose(out_w, np.repeat(v[0, 7:10].mean(0)[None], nq, 0), atol=1e-12)
+
+
+def test_rope_known_answer_direction_and_pairing():
+    """rotary_dim 2 at position p: (1, 0) -> (cos p, sin p) and (0, 1) ->
+    (-sin p, cos p) (inv_freq_0 = theta^0 = 1).  rotary_dim 4 of head_dim 8:
+    dim i pairs with dim i + 2 (the halves, not neighbours), dim 1 turning at
+    theta^(-1/2) per position; dims 4.. pass through."""
+    for p in (1, 5, 1000):
+        for x, want in (((1.0, 0.0), (math.cos(p), math.sin(p))),
+                        ((0.0, 1.0), (-math.sin(p), math.cos(p)))):
+            xs = np.array(x) * math.sqrt(2.0)  # unit RMS: the norm step is the identity
+            got = _rope(xs, p, rot=2)
+            np.testing.assert_allclose(got / math.sqrt(2.0), want, atol=2e-6)
+    theta, p = 1e4, 7
+    w1 = p * theta ** -0.5
+    x = np.zeros(8)
+    x[1] = math.sqrt(8.0)  # unit RMS
+    got = _rope(x, p, rot=4, theta=theta) / math.sqrt(8.0)
+    want = np.zeros(8)
+    want[1], want[3] = math.cos(w1), math.sin(w1)
+    np.testing.assert_allclose(got, want, atol=2e-6)
+    x = np.zeros(8)
+    x[2] = math.sqrt(8.0)
+    got = _rope(x, p, rot=4, theta=theta) / math.sqrt(8.0)
+    want = np.zeros(8)
+    want[0], want[2] = -math.sin(p), math.cos(p)
+    np.testing.assert_allclose(got, want, atol=2e-6)
+
+
+def test_gqa_rounds_p_to_bf16_and_sums_unrounded():
+    """Two keys with p = (1, 1/3): P V uses bf16(1/3) = 171/512 and the sum
+    uses 1 + 1/3, so with V = (0, 1) the output is (171/512) / (4/3)."""
+    q = np.array([[1.0]])
+    k = np.array([[[0.0], [math.log(1.0 / 3.0)]]])
+    v = np.array([[[0.0], [1.0]]])
+    out = od.gqa(q, k, v, 2, 1.0)
+    assert abs(out[0, 0] - (171 / 512) * 0.75) < 1e-14
+
+
+@pytest.mark.parametrize("d", [4, 64])
+def test_attend_row_scale_is_inverse_sqrt_head_dim(d):
+    """One query head over two positions: the cached key at position 0 is
+    orthogonal to q (score 0), the new key equals q (q.k = d after the unit
+    RMS norm), so the scores are (0, d * scale) = (0, sqrt(d)) for the
+    reference's scale and the output is the softmax weights on V = (e_0, e_1),
+    P rounded to bf16 as above."""
+    c = dict(heads=1, kv_heads=1, head_dim=d, rotary_dim=0, eps=0.0,
+             cos=np.ones((4, 1)), sin=np.zeros((4, 1)))
+    L = dict(q_norm=np.ones(d), k_norm=np.ones(d))
+    ones = np.ones(d)
+    v_new = np.zeros(d)
+    v_new[1] = 1.0
+    row = np.concatenate([ones, ones, v_new])
+    k_rows = np.zeros((1, 4, d))
+    v_rows = np.zeros((1, 4, d))
+    k_rows[0, 0] = np.where(np.arange(d) % 2 == 0, 1.0, -1.0)
+    v_rows[0, 0, 0] = 1.0
+    out = od.attend_row(row, L, c, k_rows, v_rows, 1)
+    s1 = math.sqrt(d)
+    p0 = math.exp(-s1)
+    want = np.zeros(d)
+    want[0] = float(od.bf(np.array([p0]))[0]) / (1.0 + p0)
+    want[1] = 1.0 / (1.0 + p0)
+    np.testing.assert_allclose(out, want, rtol=0, atol=1e-14)
+    np.testing.assert_array_equal(k_rows[0, 1], ones)  # the new k written at pos 1
+    np.testing.assert_array_equal(v_rows[0, 1], v_new)
