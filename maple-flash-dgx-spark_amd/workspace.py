@@ -7,12 +7,27 @@ values, call counters, barrier counters and flags that each call leaves ready
 for the next, so the workspace is zeroed once and never again.  Two calls on
 one workspace must therefore not overlap.  Workspaces here are keyed by
 (kind, device, stream, shape): calls issued on different streams use different
-workspaces and may run concurrently; calls on one stream are ordered by it.
+workspaces, and calls on one stream are ordered by it.
 A HIP graph keeps the workspace of the stream it was captured on; replay it
 in that stream's order relative to eager calls made on the capture stream.
 (The attention workspace belongs to its KV cache, ``gqa_workspace``.)
 The pool also holds per-call scratch that a kernel rewrites on every call (the
 RTN4 GEMM's operands); it carries no timeout word and is never zeroed here.
+
+A workspace that has to grow is replaced by a larger one (at least twice the
+size, so the replaced ones add up to less than the current one), and the one
+it replaces is retired, not freed: a graph captured while it was current
+still writes into it on every replay, and stream handles are reused (torch
+hands them out from a fixed pool), so a later capture or eager call on the
+same handle at a larger size must not hand that memory back to the caching
+allocator.  Retired workspaces stay in the timeout check.
+
+Persistent launches (the one-launch MoE layer, the routing launch, the
+single-launch router and the decode attention) assume that their whole grid
+is resident at once, checked against the whole device.  Two of them must not
+overlap on one GPU, even on different streams: their grids could then not all
+fit, and the waits would run out (wrong values, reported by the timeout
+check).  Issue them from one stream per device, or order the streams.
 
 Every wait in those kernels is bounded (about 0.2 s); a wait that runs out
 sets the workspace's timeout word and the kernel finishes with wrong values
@@ -37,6 +52,8 @@ TIMEOUT_WORD = {
 }
 
 _POOL: dict[tuple, torch.Tensor] = {}
+# (key, tensor) of workspaces replaced by larger ones; kept until the process ends
+_RETIRED: list[tuple[tuple, torch.Tensor]] = []
 _ATTENTION: "weakref.WeakValueDictionary[int, torch.Tensor]" = weakref.WeakValueDictionary()
 
 
@@ -47,15 +64,24 @@ def _device_index(device) -> int:
 
 def get(kind: str, device, nbytes: int, key: tuple = (), *, min_bytes: int = 0) -> torch.Tensor:
     """The zero-filled workspace of ``kind`` for ``key`` on ``device`` and its
-    current stream (created, or grown, on first need)."""
+    current stream (created, or grown, on first need; a grown workspace
+    retires the one it replaces instead of freeing it)."""
     idx = _device_index(device)
     stream = torch.cuda.current_stream(idx).cuda_stream
     k = (kind, idx, stream) + tuple(key)
     ws = _POOL.get(k)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(int(nbytes), int(min_bytes)), device=torch.device("cuda", idx), dtype=torch.uint8)
+        size = max(int(nbytes), int(min_bytes))
+        if ws is not None:
+            size = max(size, 2 * ws.numel())
+            _RETIRED.append((k, ws))
+        ws = _alloc(size, idx)
         _POOL[k] = ws
     return ws
+
+
+def _alloc(nbytes: int, idx: int) -> torch.Tensor:
+    return torch.zeros(nbytes, device=torch.device("cuda", idx), dtype=torch.uint8)
 
 
 def register_attention(ws: torch.Tensor) -> torch.Tensor:
@@ -67,7 +93,7 @@ def register_attention(ws: torch.Tensor) -> torch.Tensor:
 def _all(idx: int) -> list[tuple[str, torch.Tensor]]:
     """The workspaces on device ``idx`` that carry a timeout word (per-call
     scratch kept in the pool, such as the RTN4 GEMM's operands, has none)."""
-    out = [(k[0], ws) for k, ws in _POOL.items() if k[1] == idx and k[0] in TIMEOUT_WORD]
+    out = [(k[0], ws) for k, ws in list(_POOL.items()) + _RETIRED if k[1] == idx and k[0] in TIMEOUT_WORD]
     out += [("attention", ws) for ws in list(_ATTENTION.values()) if ws.device.index == idx]
     return out
 

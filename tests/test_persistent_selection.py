@@ -112,3 +112,36 @@ def test_check_timeouts_skips_pooled_scratch(monkeypatch):
     with pytest.raises(RuntimeError, match="moe_fused"):
         workspace.check_timeouts(0)
     assert int(a.count_nonzero()) == 0 and bool((s == 255).all())
+
+
+class _Stream:
+    cuda_stream = 7  # one reused stream handle
+
+
+def test_grown_workspace_is_retired_not_freed(monkeypatch):
+    """A graph captured against a workspace keeps writing into it on every
+    replay; a later call on the same (reused) stream handle that needs more
+    room gets a new, larger tensor while the old one stays referenced (and
+    in the timeout check)."""
+    monkeypatch.setattr(workspace, "_POOL", {})
+    monkeypatch.setattr(workspace, "_RETIRED", [])
+    monkeypatch.setattr(workspace, "_ATTENTION", {})
+    monkeypatch.setattr(workspace, "_device_index", lambda d: 0)
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda idx=None: _Stream())
+    monkeypatch.setattr(workspace, "_alloc", lambda n, idx: torch.zeros(n, dtype=torch.uint8))
+    first = workspace.get("router", 0, 4096)
+    assert workspace.get("router", 0, 1000) is first  # fits: same tensor
+    grown = workspace.get("router", 0, 5000)
+    assert grown is not first and grown.numel() >= 2 * first.numel()
+    assert any(t is first for _, t in workspace._RETIRED)
+    # the retired workspace is still read by the timeout check
+    first.view(torch.int32)[workspace.TIMEOUT_WORD["router"]] = 1
+    assert workspace.timed_out_kinds(0) == ["router"]
+    with pytest.raises(RuntimeError, match="router"):
+        workspace.check_timeouts(0)
+    assert int(first.count_nonzero()) == 0
+    # growth is geometric, so retired bytes stay below the current size
+    for n in range(5001, 40000, 3001):
+        workspace.get("router", 0, n)
+    cur = workspace._POOL[("router", 0, 7)].numel()
+    assert sum(t.numel() for _, t in workspace._RETIRED) < cur
