@@ -33,6 +33,7 @@ configurations the same way (bounded samples, each stated).
                     [--no-decoder] [--no-extra]
     python bench.py --counters-pass moe_bs1|prefill|decode32   # for rocprofv3 --pmc
     python bench.py --decode-batch 32 # only the full decoder at one batch size
+    python bench.py --timeline        # the one-launch MoE layer's phase stamps
 """
 
 from __future__ import annotations
@@ -493,6 +494,83 @@ def counters_pass(dev, kind: str, n_layers: int) -> int:
     return 0
 
 
+PHASES = ["start", "router logit out", "logits seen", "ranked", "weight loads issued", "h published",
+          "h seen", "h staged", "down values out", "down values seen", "y out", "end"]
+
+
+def timeline(dev, n_layers: int, reps: int) -> int:
+    """Per-phase timeline of the one-launch MoE layer: the library's stamped
+    variant (libmaple_amd_stamps.so, ma_moe_phase_stamps) runs ``n_layers``
+    chained cold layers in one graph; after each replay the stamps of the
+    chain's last layer are read from the workspace.  Prints one JSON line:
+    per phase the median / p90 / max over workgroups and replays of the time
+    since the launch's first workgroup started (us), and the stamped build's
+    period per layer (the stamps' own stores and waits lengthen it)."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from maple_amd import _lib, synthetic, workspace
+    from maple_amd.moe import fused_form, moe_block
+
+    _lib.use_stamped_library()
+    lib = _lib.load()
+    off, words, wgs = ctypes.c_size_t(), ctypes.c_int(), ctypes.c_int()
+    if lib.ma_moe_phase_stamps(ctypes.byref(off), ctypes.byref(words), ctypes.byref(wgs)) != 0:
+        log("timeline: " + lib.ma_last_error().decode(errors="replace"))
+        return 1
+    layers = [synthetic.make_moe_layer(HIDDEN, EXPERTS, INTER, seed=i, device=dev) for i in range(n_layers)]
+    if fused_form(layers[0], TOPK) != 1:
+        log("timeline: the XCD-split form does not run on this device")
+        return 1
+    x = synthetic.randn_bf16((1, HIDDEN), 12345, dev)
+
+    def chain():
+        h = x
+        for layer in layers:
+            h, _, _ = moe_block(h, layer, TOPK, plan="fused")
+
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        chain()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        chain()
+    ws = [w for k, w in workspace._POOL.items() if k[0] == "moe_fused" and k[2] == s.cuda_stream][-1]
+    n0, nw, ng = off.value // 4, words.value, wgs.value
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    rows = []
+    e0, e1 = torch.cuda.Event(True), torch.cuda.Event(True)
+    elapsed = 0.0
+    for _ in range(reps):
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        elapsed += e0.elapsed_time(e1) * 1e-3
+        rows.append(ws.view(torch.int32)[n0:n0 + nw * ng].cpu().numpy().astype(np.int64).reshape(ng, nw))
+    workspace.check_timeouts(dev)
+    d = np.stack(rows) & 0xFFFFFFFF  # [reps, workgroups, words], 32-bit counter values
+    t0 = d[:, :, 0].min(axis=1, keepdims=True)
+    rel = ((d[:, :, :len(PHASES)] - t0[:, :, None]) & 0xFFFFFFFF) * 0.01  # 100 MHz ticks -> us
+    out = {}
+    router_wgs = np.arange(ng) < 64  # workgroups 0..7 of each XCD (i / 8 < 8)
+    for i, name in enumerate(PHASES):
+        v = rel[:, router_wgs, i] if i == 1 else rel[:, :, i]
+        out[name] = {"median": round(float(np.median(v)), 2), "p90": round(float(np.percentile(v, 90)), 2),
+                     "max": round(float(v.max()), 2)}
+    xcds = sorted(set(int(v) for v in d[0, :, 15]))
+    print(json.dumps({"timeline": "k_moe_xcd phase stamps, us from the launch's first workgroup",
+                      "layers_in_chain": n_layers, "replays": reps, "xcds_seen": xcds,
+                      "stamped_us_per_layer": round(elapsed / reps / n_layers * 1e6, 3), "phases": out}),
+          flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -508,6 +586,8 @@ def main() -> int:
                     help="only time the full decoder at this batch (for profiling runs)")
     ap.add_argument("--flash-head", action="store_true",
                     help="with --decode-batch 1: the lm_head through a FlashHead")
+    ap.add_argument("--timeline", action="store_true",
+                    help="only the one-launch MoE layer's per-phase timeline (stamped library)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: there is no multi-GPU path "
@@ -528,6 +608,8 @@ def main() -> int:
     L = args.layers
     if args.counters_pass:
         return counters_pass(dev, args.counters_pass, L)
+    if args.timeline:
+        return timeline(dev, L, max(args.steps, 10))
     if args.decode_batch > 0:
         res = decoder_tokens_per_s(dev, args.decode_batch, max(args.steps, 10), args.warmup,
                                    flash=args.flash_head)

@@ -402,6 +402,19 @@ int ma_moe_fused_o(const void* x, const void* attn, const uint32_t* o_w, const v
                    int next_alpha_dtype, const float* next_rms, float next_eps, int64_t next_rows,
                    void* next_out, void* stream);
 
+/* Phase stamps of the XCD-split form (diagnostics, no reference
+ * counterpart).  In the library's stamped variant (libmaple_amd_stamps.so,
+ * built from the same sources with -DMA_PHASE_STAMPS) every call writes, per
+ * workgroup, words_per_workgroup uint32 words at byte `offset` of its
+ * workspace (workgroup g's row at offset + 4 * words * g): word i is the
+ * 100 MHz real-time counter when the workgroup reached phase i (0 start,
+ * 1 router logit out (workgroups 0..7 of an XCD), 2 all logits seen,
+ * 3 ranked, 4 weight loads issued, 5 h published, 6 h seen, 7 h staged,
+ * 8 weighted down values published, 9 the slots' values seen, 10 y out,
+ * 11 end), word 15 its XCD.  Returns MA_OK there and MA_EVALUE in the
+ * normal library, which writes none. */
+int ma_moe_phase_stamps(size_t* offset, int* words_per_workgroup, int* workgroups);
+
 /* *out = 1 if any ma_moe_fused call on this workspace timed out waiting
  * (synchronises the stream).  No reference counterpart: the reference has no
  * cross-workgroup wait. */

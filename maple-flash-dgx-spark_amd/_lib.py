@@ -13,6 +13,9 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libmaple_amd.so")
+# The same library with the one-launch MoE layer's phase stamps compiled in
+# (ma_moe_phase_stamps); for timelines only, never loaded unless asked for.
+STAMPED_LIB_PATH = Path(__file__).resolve().with_name("libmaple_amd_stamps.so")
 
 F32, BF16, F16 = 0, 1, 2
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
@@ -64,6 +67,7 @@ _SIGNATURES = {
     "ma_moe_fused_timed_out": [_P, _P, _P],
     "ma_moe_fused_resident": [_L, _L, _L, _L, _PL, _PL],
     "ma_moe_fused_form": [_L, _L, _L, _L],
+    "ma_moe_phase_stamps": [_P, _P, _P],
     "ma_moe_route_workspace_bytes": [_L, _L],
     "ma_moe_route": [_P, _P, _L, _L, _P, _I, _F, _P, _P, _L, _I, _P, _P, _P, _P, _P, _P, _P, _P,
                      _P, _P, _P, _Z, _P],
@@ -95,6 +99,14 @@ _lib = None
 
 def declared_symbols() -> list[str]:
     return list(_SIGNATURES)
+
+
+def use_stamped_library() -> None:
+    """Make ``load`` bind the stamped variant instead (before the first load)."""
+    global LIB_PATH
+    if _lib is not None and LIB_PATH != STAMPED_LIB_PATH:
+        raise RuntimeError("the maple_amd library is already loaded; select the stamped one first")
+    LIB_PATH = STAMPED_LIB_PATH
 
 
 def load() -> ctypes.CDLL:

@@ -32,6 +32,10 @@ namespace ma {
 //                      tagged 64-bit word (tag << 32 | y[2m + 1] << 16 | y[2m])
 //   [320 KB, 384 KB)   XCD kernel with the O projection in front: each XCD's
 //                      copy of o, laid out as y
+//   [384 KB, 400 KB)   XCD kernel built with MA_PHASE_STAMPS only: per
+//                      workgroup 16 words, word i the 100 MHz real-time
+//                      counter when the workgroup reached phase i, word 15
+//                      its XCD (unused otherwise)
 constexpr int kSubB = 1, kTopB = kSubB + kBarGroups, kFlags = kTopB + 1;
 constexpr int kSubC = kFlags + kBarGroups, kTopC = kSubC + kBarGroups;
 constexpr size_t kLogitOff = 16384;
@@ -40,12 +44,24 @@ constexpr size_t kMoeWsHeader = 49152;
 constexpr size_t kXEpochOff = 65536, kXRegionOff = 98304, kXRegion = 4096, kXPartOff = 131072;
 constexpr size_t kXYOff = kXPartOff + 8 * 2048 * 8, kXYRegion = 8192;
 constexpr size_t kXOOff = kXYOff + 8 * kXYRegion;
-constexpr size_t kXWsBytes = kXOOff + 8 * kXYRegion;
+constexpr size_t kXStampOff = kXOOff + 8 * kXYRegion;
+constexpr int kXStampWords = 16;
+constexpr size_t kXWsBytes = kXStampOff + 256 * kXStampWords * 4;
 static_assert(kTopC < static_cast<int>(kLogitOff / 256), "workspace lines");
 static_assert(kLogitOff + 256 * kLogitStride * 8 <= kMoeWsHeader, "workspace logits");
 static_assert(kMoeWsHeader + 8 * 768 * 2 <= kXEpochOff, "grid kernel h");
 static_assert(kXEpochOff + 256 * 128 <= kXRegionOff && kXRegionOff + 8 * kXRegion <= kXPartOff, "XCD layout");
 static_assert(2048 / 2 * 8 <= kXYRegion, "XCD y region");
+
+// Phase stamps of the XCD kernel (builds with -DMA_PHASE_STAMPS, the
+// library's stamped variant; a no-op otherwise): lane 0 of the calling wave
+// writes the real-time counter into word i of its workgroup's stamp row.
+#ifdef MA_PHASE_STAMPS
+#define MA_XSTAMP(i) \
+  do { if (lane == 0) stamps[i] = static_cast<uint32_t>(__builtin_amdgcn_s_memrealtime()); } while (0)
+#else
+#define MA_XSTAMP(i) do {} while (0)
+#endif
 
 // Next projection, run by every workgroup of a one-launch layer once its rows
 // of y are out: nx_out = ternary_gemv(y, nx_w, nx_alpha, rms_weight = nx_rms)

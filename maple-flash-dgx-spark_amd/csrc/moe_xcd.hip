@@ -111,6 +111,13 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   const uint32_t tag16 = tag & 0xffffu;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   bool timed_out = false;
+#ifdef MA_PHASE_STAMPS
+  uint32_t* const stamps = reinterpret_cast<uint32_t*>(wsb + kXStampOff) + kXStampWords * wg;
+  if (wv == 0) {
+    MA_XSTAMP(0);  // start
+    if (lane == 0) stamps[15] = static_cast<uint32_t>(xcd);
+  }
+#endif
 
   // The residual of the y rows this workgroup finishes (wave 0): rows
   // 64 lw + lane with a next projection (every XCD combines all of y), else
@@ -276,6 +283,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     }
     const float l = group_sum<64>(dot) + (bias ? bias[re] : 0.f);
     if (lane == 0) st_l2_64(&xlog[re], (static_cast<uint64_t>(tag) << 32) | __float_as_uint(l));
+    if (wv == 0) MA_XSTAMP(1);  // router logit out (workgroups 0..7 of an XCD)
   }
 
   // ---- 2. ranks: wave 0 polls its XCD's copy of the logits (lane e, expert
@@ -297,6 +305,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       __builtin_amdgcn_s_sleep(1);
       timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
     }
+    MA_XSTAMP(2);  // every logit of the XCD seen
     if (lane < n_exp) key = float_order_key(lg);
     s_key[lane] = (static_cast<uint64_t>(static_cast<uint32_t>(key) ^ 0x80000000u) << 32) |
                   static_cast<uint32_t>(~lane);
@@ -316,6 +325,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   // this XCD's expert (clamped: only a timed-out wait can leave an absent
   // expert among the first 8 ranks)
   const int64_t ex = clamp_id(__builtin_ctzll(__ballot(rank == static_cast<uint32_t>(xcd))), n_exp);
+  if (wv == 0) MA_XSTAMP(3);  // ranked
 
   // ---- 3. weights of slot xcd: this wave's SwiGLU rows (outputs o0 .. o0 +
   // US, lanes 0..31 the up row and 32..63 the gate row, each lane 16 KWH
@@ -357,6 +367,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     }
   }
   MA_ISSUE_FENCE();
+  if (wv == 0) MA_XSTAMP(4);  // weight loads issued
 
   // routing weights while the loads are in flight (wave 0): the softmax over
   // all E logits with the max-subtracted exp, then p / (sum of the selected p
@@ -393,6 +404,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     }
     if (lane < US) st_l2_32(&xh[o0 + lane], (tag16 << 16) | f32_to_bf16(swiglu_act(up_t, gate_t)));
   }
+  if (wv == 0) MA_XSTAMP(5);  // this wave's h outputs published
 
   // ---- 4. h of slot xcd from the XCD's region: thread t < NWI polls the 16
   // values of h word t until all carry this call's tag, then builds its x'
@@ -413,6 +425,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       __builtin_amdgcn_s_sleep(1);
       timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
     }
+    if (wv == 0) MA_XSTAMP(6);  // h word 0 .. 15 seen (thread 0)
     float hv[16];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -427,6 +440,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     for (int j = 0; j < 8; ++j) hs[tid][j] = pr[j];
   }
   __syncthreads();
+  if (wv == 0) MA_XSTAMP(7);  // all of h staged in LDS
 
   // ---- 5. slot xcd's down rows r0 .. r0 + RPW, each rounded to bf16 (as the
   // reference's ternary_expert_gemv stores it) and scaled by the slot's
@@ -444,6 +458,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
         st_coh64(&part[xcd * H + r0 + u * RPID + subd], (static_cast<uint64_t>(tag) << 32) | __float_as_uint(pv));
     }
   }
+  if (wv == 0) MA_XSTAMP(8);  // this wave's weighted down values published
 
   // The O values of this workgroup's combine rows (wave 0), from the XCD's copy.
   if (o_w && wv == 0) {
@@ -475,6 +490,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       __builtin_amdgcn_s_sleep(1);
       timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
     }
+    if (wv == 0) MA_XSTAMP(9);  // the slots' values of this workgroup's rows seen
     s_pv[wv][lane] = pv;
     __syncthreads();
     if (wv == 0) {
@@ -486,6 +502,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       if ((lane >> 3) == xcd) y[row] = static_cast<uint16_t>(bits);
       const uint32_t odd = __shfl_xor(bits, 1, 64);
       if (!(lane & 1)) st_l2_64(&yx[row >> 1], (static_cast<uint64_t>(tag) << 32) | bits | (odd << 16));
+      MA_XSTAMP(10);  // y out
     }
   } else if (wv == 0) {
     const int s = lane / FR, r = lane % FR;
@@ -498,11 +515,13 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       __builtin_amdgcn_s_sleep(1);
       timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
     }
+    MA_XSTAMP(9);
     float v = addp ? bf16_to_f32(f32_to_bf16(__uint_as_float(ra << 16) + __uint_as_float(rb << 16)))
                  : residual ? __uint_as_float(ra << 16) : 0.f;
 #pragma unroll
     for (int k = 0; k < TK; ++k) v += __shfl(pv, k * FR + r, 64);
     if (lane < FR) y[wg * FR + lane] = f32_to_bf16(v);
+    MA_XSTAMP(10);
   }
 
   // ---- 7. next projection (optional), from the XCD's copy of y
@@ -510,6 +529,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     timed_out = next_projection<KWH, LPRH, W, NXP, true>(y, nx_rms, nx_eps, nx_rows, nx_rq, nx_out, nxw, nxa, ws,
                                                          0u, G, wg, tid, lane, wv, t0, yx, tag) ||
                 timed_out;
+  if (wv == 0) MA_XSTAMP(11);  // end
   if (__ballot(timed_out) && lane == 0) st_coh32(&ws[2], 1u);
   if (tid == 0) st_coh32(calls, tag);
 }
@@ -523,6 +543,29 @@ const void* xcd_kernel_t(int64_t inter) {
 }
 
 }  // namespace
+
+}  // namespace ma
+
+// Where the XCD kernel's phase stamps sit in the workspace (MA_OK only in the
+// library's stamped variant, built with -DMA_PHASE_STAMPS).
+extern "C" int ma_moe_phase_stamps(size_t* offset, int* words_per_workgroup, int* workgroups) {
+  using namespace ma;
+  if (!offset || !words_per_workgroup || !workgroups) return fail(MA_EVALUE, "moe_phase_stamps: null output");
+#ifdef MA_PHASE_STAMPS
+  *offset = kXStampOff;
+  *words_per_workgroup = kXStampWords;
+  *workgroups = kXcds * kXcdWgs;
+  return MA_OK;
+#else
+  *offset = 0;
+  *words_per_workgroup = 0;
+  *workgroups = 0;
+  return fail(MA_EVALUE, "moe_phase_stamps: this library was built without phase stamps "
+                         "(libmaple_amd_stamps.so has them)");
+#endif
+}
+
+namespace ma {
 
 bool moe_xcd_supported(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k, hipStream_t st) {
   if (!(hidden == 2048 && (inter == 768 || inter == 512) && top_k == kXcds && n_experts >= top_k &&

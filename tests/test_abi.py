@@ -59,3 +59,26 @@ def test_size_errors_map_without_a_gpu():
         _lib.call("ma_moe_dispatch", None, 0, 8, 0, None, None, None, None, None)
     with pytest.raises(ValueError, match="groups"):
         _lib.call("ma_rtn4_gemv", None, 1, 1, 96, None, 4, 12, 0, None, 1, None, 1, 64, None, 4, None)
+
+
+def test_stamped_variant_exports_the_same_symbols_and_its_stamps_fit():
+    """libmaple_amd_stamps.so (the one-launch layer with phase stamps) exports
+    everything the header declares; only it reports a stamp layout, and the
+    stamp rows lie inside the workspace ma_moe_fused_workspace_bytes sizes."""
+    if not _lib.STAMPED_LIB_PATH.exists():
+        pytest.fail(f"{_lib.STAMPED_LIB_PATH} not built; run __graft_entry__.build()")
+    st = ctypes.CDLL(str(_lib.STAMPED_LIB_PATH))
+    missing = [n for n in declared_in_header() if not hasattr(st, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    off, words, wgs = ctypes.c_size_t(), ctypes.c_int(), ctypes.c_int()
+    fn = st.ma_moe_phase_stamps
+    fn.argtypes = [ctypes.c_void_p] * 3
+    assert fn(ctypes.byref(off), ctypes.byref(words), ctypes.byref(wgs)) == 0
+    assert words.value == 16 and wgs.value == 256 and off.value % 256 == 0
+    size = st.ma_moe_fused_workspace_bytes
+    size.argtypes = [ctypes.c_int64] * 4
+    size.restype = ctypes.c_size_t
+    for inter in (768, 512):
+        assert off.value + 4 * words.value * wgs.value <= size(64, 2048, inter, 8)
+    plain = _lib.load()
+    assert plain.ma_moe_phase_stamps(ctypes.byref(off), ctypes.byref(words), ctypes.byref(wgs)) != 0

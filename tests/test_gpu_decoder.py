@@ -29,6 +29,15 @@ pytestmark = pytest.mark.gpu
 # Maple-Preview shape (16 / 4 heads of 128, partial rotary 0.5) and a full
 # rotary over 128 (rotate-half pairs dims 64 apart, across a lane's two dims).
 HEADS = [(32, 4, 64, 32), (16, 4, 128, 64), (16, 4, 128, 128)]
+# Attention outputs against the oracle: elementwise |y - ref| <= 2^-8 |ref| +
+# ATTN_ATOL * max|ref|.  Both sides round P to bf16 before P V, at different
+# maxima: the oracle at the max over all positions (the reference's rounding
+# when the positions fit one tile), the kernel at each wave's running max over
+# its 32-position blocks, so each term's rounding differs by up to 2^-9
+# relative; over ~4k positions the two P V sums differ by ~2e-3 of the output
+# scale (a CPU simulation of both schemes on this distribution: 1.4e-4 at a
+# scale of 0.07), on top of the output's own bf16 rounding.
+ATTN_ATOL = 4e-3
 
 
 def _rope_rows(table, seqlen, dev):
@@ -88,7 +97,7 @@ def test_gqa_ragged_vs_oracle(dev, window, heads):
     out = decode_gqa_attn(q, kc, vc, seqlen, scale=d ** -0.5, window=window)
     for b, n in enumerate(lens):
         ref = od.gqa(np_f(q[b, :, 0]), np_f(kc[b]), np_f(vc[b]), n, d ** -0.5, window)
-        assert_bf16_close(np_f(out[b, :, 0]), ref, atol_frac=2e-3, what=f"len {n}")
+        assert_bf16_close(np_f(out[b, :, 0]), ref, atol_frac=ATTN_ATOL, what=f"len {n}")
     # a row alone gives the same bits as in the batch
     solo = decode_gqa_attn(q[6:7], kc[6:7], vc[6:7], seqlen[6:7], scale=d ** -0.5, window=window)
     assert torch.equal(solo, out[6:7])
@@ -131,7 +140,7 @@ def test_fused_attention_equals_two_step(dev, window, heads):
     for b, n in enumerate((seqlen + 1).tolist()):
         r = int(row_map[b])
         o = od.gqa(np_f(q[b, :, 0]), np_f(kc[r]), np_f(vc[r]), n, d ** -0.5, window)
-        assert_bf16_close(np_f(out[b, :, 0]), o, atol_frac=2e-3, what=f"row {b}")
+        assert_bf16_close(np_f(out[b, :, 0]), o, atol_frac=ATTN_ATOL, what=f"row {b}")
 
 
 @pytest.mark.parametrize("heads", HEADS[:2])
@@ -208,7 +217,7 @@ def test_attention_xcd_form_equals_grid_form(dev, monkeypatch, batch, window, he
                               seqlen[b:b + 1], num_heads=nq, num_kv_heads=nkv, head_dim=d, rotary_dim=rot,
                               use_rope=True, use_qk_norm=True, eps=1e-6)
         ref = od.gqa(np_f(qn[0, :, 0]), np_f(kc2[b]), np_f(vc2[b]), n, d ** -0.5, window)
-        assert_bf16_close(np_f(outs[0][b, :, 0]), ref, atol_frac=2e-3, what=f"row {b}")
+        assert_bf16_close(np_f(outs[0][b, :, 0]), ref, atol_frac=ATTN_ATOL, what=f"row {b}")
 
 
 def test_attention_rejects_bad_shapes(dev):
