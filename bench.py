@@ -34,6 +34,7 @@ configurations the same way (bounded samples, each stated).
     python bench.py --counters-pass moe_bs1|prefill|decode32   # for rocprofv3 --pmc
     python bench.py --decode-batch 32 # only the full decoder at one batch size
     python bench.py --timeline        # the one-launch MoE layer's phase stamps
+    python bench.py --gemv | --preview # config 1 alone | Maple-Preview shapes alone
 """
 
 from __future__ import annotations
@@ -128,12 +129,33 @@ def time_graph(g, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) * 1e-3 / steps
 
 
+def gemv_config1(dev, steps: int) -> dict:
+    """Config 1: one packed ternary GEMV, 1536 x 2048, batch 1, bf16 x and
+    row scales; 1024 distinct cold weight copies (0.8 GB) called back to
+    back in one HIP graph, so each call reads its codes from HBM."""
+    import torch  # noqa: F401
+
+    from maple_amd import synthetic
+    from maple_amd.kernels import ternary_gemv
+
+    n, k, reps = 1536, 2048, 1024
+    base = synthetic.ternary_packed((8, n, k), 77, dev)
+    ws = [base[i % 8].clone() for i in range(reps)]
+    alpha = synthetic.uniform_bf16((n,), 0.01, 0.05, 78, dev)
+    xg = synthetic.randn_bf16((1, k), 79, dev)
+    g = graph_of(lambda: [ternary_gemv(xg, ws[i], alpha) for i in range(reps)])
+    t = time_graph(g, steps, 1) / reps
+    nbytes = n * k // 4 + n * 2 + k * 2 + n * 2
+    return {"us_per_call": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1), "bytes_per_call": nbytes,
+            "calls_per_replay": reps}
+
+
 def extra_workloads(layers, dev, steps: int) -> dict:
     """The other configurations: one GEMV, Zipf-routed batches, a prefill chunk."""
     import torch
 
     from maple_amd import synthetic
-    from maple_amd.kernels import router_topk, ternary_gemv
+    from maple_amd.kernels import router_topk
     from maple_amd.moe import moe_block
 
     out = {}
@@ -141,18 +163,7 @@ def extra_workloads(layers, dev, steps: int) -> dict:
     one = torch.zeros(1, device=dev)
     g = graph_of(lambda: [one.add_(1.0) for _ in range(256)])
     out["launch_floor_us"] = round(time_graph(g, 5, 2) / 256 * 1e6, 3)
-    # Single packed ternary GEMV, 1536 x 2048, batch 1, 1024 distinct cold copies.
-    n, k, reps = 1536, 2048, 1024
-    base = synthetic.ternary_packed((8, n, k), 77, dev)
-    ws = [base[i % 8].clone() for i in range(reps)]
-    alpha = synthetic.uniform_bf16((n,), 0.01, 0.05, 78, dev)
-    xg = synthetic.randn_bf16((1, k), 79, dev)
-    g = graph_of(lambda: [ternary_gemv(xg, ws[i], alpha) for i in range(reps)])
-    t = time_graph(g, 3, 1) / reps
-    nbytes = n * k // 4 + n * 2 + k * 2 + n * 2
-    out["gemv_1536x2048_bs1"] = {"us_per_call": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1),
-                                 "bytes_per_call": nbytes}
-    del ws, base, g
+    out["gemv_1536x2048_bs1"] = gemv_config1(dev, 3)
     # Zipf(1.1)-routed MoE layers at 32 and 128 tokens.
     fx = zipf_fixture()
     bias = torch.tensor(fx["bias"], dtype=torch.float32, device=dev)
@@ -188,56 +199,97 @@ def extra_workloads(layers, dev, steps: int) -> dict:
     return out
 
 
-def decoder_tokens_per_s(dev, batch: int, steps: int, warmup: int, flash: bool = False) -> dict:
-    """Greedy decode of the full synthetic decoder (24 layers, hidden 2048,
-    32/4 heads of 64, 64 experts top-8, RTN4 lm_head over 151936 tokens) at
-    ``batch`` rows over a 4096-token KV cache, one HIP graph replay per step
-    (the whole step captured by the decode-graph runner, which first checks
-    8 replayed steps against 8 eager ones).  Each replay appends one position
-    per row and feeds the chosen ids to the next step.  ``flash``: the lm_head
-    through a FlashHead (4748 clusters of 32 tokens, 512 probed, one forced
-    token; synthetic clusters)."""
+def maple_preview_config():
+    """Maple-Preview's decoder shapes (the reference's published model,
+    docs/HANDOFF.md:279-299): 24 layers, hidden 2048, 16/4 heads of 128 at
+    half rotary, 256 experts top-8 with intermediate 512, RTN4 head and
+    embeddings in groups of 64 over 151936 tokens, three sliding-window (512)
+    layers to every full-attention layer, no RoPE on the full layers.
+    Random-init weights of those shapes (no checkpoint here)."""
+    from maple_amd.model import DecoderConfig
+
+    return DecoderConfig(hidden=2048, layers=24, heads=16, kv_heads=4, head_dim=128, experts=256, inter=512,
+                         top_k=8, vocab=151936, rtn_group=64,
+                         layer_types=(("sliding_attention",) * 3 + ("full_attention",)) * 6,
+                         sliding_window=512, nope_on_global=True)
+
+
+def decoder_tokens_per_s(dev, batch: int, steps: int, warmup: int, flash: bool = False, cfg=None,
+                         prefill: int = 4096, sampled: bool = False) -> dict:
+    """Decode of the full synthetic decoder (by default config 4: 24 layers,
+    hidden 2048, 32/4 heads of 64, 64 experts top-8, RTN4 lm_head over 151936
+    tokens; ``cfg`` for other shapes) at ``batch`` rows over a ``prefill``-token
+    KV cache, one HIP graph replay per step (the whole step captured by the
+    decode-graph runner, which first checks 8 replayed steps against 8 eager
+    ones).  Each replay appends one position per row and feeds the chosen ids
+    to the next step.  Greedy, or with ``sampled`` the reference's benchmark
+    sampling (temperature 1.0, top-p 0.95, top-k 20: the fused sampler inside
+    the graph, one uniform per row drawn before each replay).  ``flash``: the
+    lm_head through a FlashHead (4748 clusters of 32 tokens, 512 probed, one
+    forced token; synthetic clusters)."""
     import torch
 
     from maple_amd import workspace
     from maple_amd.decode_graph import Sampling, try_decode_graph
     from maple_amd.model import DecoderConfig, SyntheticDecoder
 
-    cfg = DecoderConfig()
-    model = SyntheticDecoder(cfg, dev, seed=0, max_len=4096 + steps + warmup + 32)
-    cache = model.make_cache(batch, prefill_len=4096, seed=0)
+    cfg = cfg or DecoderConfig()
+    model = SyntheticDecoder(cfg, dev, seed=0, max_len=prefill + steps + warmup + 64)
+    cache = model.make_cache(batch, prefill_len=prefill, seed=0)
     if flash:
         from maple_amd.synthetic import flash_head_for
 
         model.flash_head = flash_head_for(model.lm_head, 4748, 512, 9, dev, force=(151643,))
     gen = torch.Generator(device=dev).manual_seed(batch)
     ids = torch.randint(0, cfg.vocab, (batch,), device=dev, generator=gen)
-    g = try_decode_graph(model, cache, ids, log=log)
+    mode = (Sampling(temperature=1.0, top_p=0.95, top_k=20, generator=torch.Generator(device=dev).manual_seed(7))
+            if sampled else Sampling())
+    g = try_decode_graph(model, cache, ids, mode, log=log)
     if g is None:
         raise RuntimeError("the decode graph did not validate against eager decoding")
-    greedy = Sampling()
     for _ in range(warmup):
-        g.step(greedy)
+        g.step(mode)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(True), torch.cuda.Event(True)
     e0.record()
     for _ in range(steps):
-        g.step(greedy)
+        g.step(mode)
     e1.record()
     torch.cuda.synchronize()
     workspace.check_timeouts(dev)
     t = e0.elapsed_time(e1) * 1e-3 / steps
-    nbytes = model.decode_bytes(batch, 4096 + warmup + steps // 2)
+    nbytes = model.decode_bytes(batch, prefill + warmup + steps // 2)
     if flash:
         fh, c = model.flash_head, cfg
         row = lambda grp: c.hidden // 2 + 2 * (c.hidden // grp) * 2  # noqa: E731  codes + scales + biases
         nbytes += (fh.n_clusters * row(64) + (fh.n_probes * fh.cluster_size + fh.n_force) * row(c.rtn_group)
                    - c.vocab * row(c.rtn_group))
     out = {"tokens_per_s": round(batch / t, 1), "ms_per_step": round(t * 1e3, 4),
-           "kv_len": 4096, "algorithmic_GB/s": round(nbytes / t / 1e9, 1),
-           "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+           "kv_len": prefill, "algorithmic_GB/s": round(nbytes / t / 1e9, 1),
+           "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+           "bytes_per_step": int(nbytes), "sampling": "T1.0 top-p 0.95 top-k 20" if sampled else "greedy"}
     del g, cache, model
     torch.cuda.empty_cache()
+    return out
+
+
+def preview_decode(dev, steps: int, warmup: int) -> dict:
+    """Maple-Preview shapes at the reference's published setting (bs1,
+    sampled, exact head and FlashHead; a 512-token context, inside the
+    reference's 256-700-token haiku runs), greedy bs1 and bs32 beside it.
+    The reference's numbers come from a GB10 (~368 tok/s sampled with the
+    exact head, 417 MB/token; ~487 tok/s with its FlashHead): context only."""
+    cfg = maple_preview_config()
+    out = {}
+    for key, kw in (("bs1_sampled", dict(batch=1, sampled=True)),
+                    ("bs1_sampled_flash_head", dict(batch=1, sampled=True, flash=True)),
+                    ("bs1_greedy", dict(batch=1)),
+                    ("bs32_greedy", dict(batch=32))):
+        log(f"timing Maple-Preview shapes: {key} ...")
+        out[key] = decoder_tokens_per_s(dev, kw.pop("batch"), steps, warmup, cfg=cfg, prefill=512, **kw)
+        log(json.dumps(out[key]))
+    out["reference_gb10_context"] = {"bs1_sampled_tok_s": 368, "bs1_sampled_flash_head_tok_s": 487,
+                                     "packed_MB_per_token": 417, "source": "docs/HANDOFF.md:279-299"}
     return out
 
 
@@ -586,6 +638,10 @@ def main() -> int:
                     help="only time the full decoder at this batch (for profiling runs)")
     ap.add_argument("--flash-head", action="store_true",
                     help="with --decode-batch 1: the lm_head through a FlashHead")
+    ap.add_argument("--gemv", action="store_true",
+                    help="only the config-1 GEMV (1024 cold 1536 x 2048 calls per graph replay)")
+    ap.add_argument("--preview", action="store_true",
+                    help="only the decoder at Maple-Preview shapes (bs1 sampled / greedy, bs32)")
     ap.add_argument("--timeline", action="store_true",
                     help="only the one-launch MoE layer's per-phase timeline (stamped library)")
     args = ap.parse_args()
@@ -610,6 +666,13 @@ def main() -> int:
         return counters_pass(dev, args.counters_pass, L)
     if args.timeline:
         return timeline(dev, L, max(args.steps, 10))
+    if args.gemv:
+        print(json.dumps({"gemv_1536x2048_bs1": gemv_config1(dev, max(args.steps, 3))}), flush=True)
+        return 0
+    if args.preview:
+        print(json.dumps({"decode": {"maple_preview": preview_decode(dev, max(args.steps, 10), args.warmup)}}),
+              flush=True)
+        return 0
     if args.decode_batch > 0:
         res = decoder_tokens_per_s(dev, args.decode_batch, max(args.steps, 10), args.warmup,
                                    flash=args.flash_head)
@@ -694,6 +757,7 @@ def main() -> int:
         log("timing the full decoder at batch 1 with the FlashHead ...")
         out["decode"]["bs1_flash_head"] = decoder_tokens_per_s(dev, 1, max(args.steps, 10), args.warmup, flash=True)
         log(json.dumps(out["decode"]["bs1_flash_head"]))
+        out["decode"]["maple_preview"] = preview_decode(dev, max(args.steps, 10), args.warmup)
     if not args.no_extra:
         log("timing the other workloads ...")
         out["extra"] = extra_workloads(layers, dev, args.steps)

@@ -341,14 +341,22 @@ class SyntheticDecoder:
         return logits
 
     def decode_bytes(self, batch: int, kv_len: int) -> int:
-        """Algorithmic HBM bytes of one decode step (weights touched once, the
-        KV read for every row; experts counted as 8 selected per token at most
-        the 64 that exist)."""
+        """Algorithmic HBM bytes of one decode step: weights touched once; the
+        experts a step touches counted as the expected number of distinct
+        experts among ``batch`` rows of top-k picks under uniform routing,
+        E (1 - (1 - k/E)^batch) (k at batch 1, all E at large batches); the
+        KV read for every row over the positions each layer attends (the last
+        ``sliding_window`` on sliding layers)."""
         c = self.cfg
         lay = (c.qkv_rows + c.hidden) * c.hidden // 4 + (c.qkv_rows + c.hidden) * 2
         router = c.experts * c.hidden * 2
         expert = (3 * c.inter * c.hidden) // 4 + (2 * c.inter + c.hidden) * 2
-        experts = min(c.experts, c.top_k * batch) * expert
-        kv = batch * 2 * c.kv_heads * kv_len * c.head_dim * 2
+        hit = c.experts * (1.0 - (1.0 - c.top_k / c.experts) ** batch)
+        experts = int(round(hit * expert))
+        kv = 0
+        for i in range(c.layers):
+            window, _ = c.layer_attention(i)
+            span = min(kv_len, window) if window else kv_len
+            kv += batch * 2 * c.kv_heads * span * c.head_dim * 2
         head = c.vocab * c.hidden // 2 + 2 * c.vocab * (c.hidden // c.rtn_group) * 2
-        return c.layers * (lay + router + experts + kv) + head
+        return c.layers * (lay + router + experts) + kv + head
