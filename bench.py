@@ -10,6 +10,11 @@ weights, of which the 8 selected experts per layer are 0.91 GB, 3.6 times the
 layer's input, as in a decoder -- and captured in one HIP graph replayed in a
 cycle, so every layer's weights come from HBM.
 
+Each layer's launch also reads the next layer's router rows ahead into the
+caches while its workgroups wait for h (``prefetch``: routing-independent
+bytes, fetched once and counted once, in the layer that uses them), as a
+decoder's MoE launch can for the next MoE layer.
+
 A step is one graph replay: ``--layers`` dependent MoE-layer decodes, each on
 its own cold layer.  ``value`` is the whole-layer algorithmic HBM throughput:
 (selected experts' packed codes + scales, the router weight, x in and y out)
@@ -580,8 +585,8 @@ def timeline(dev, n_layers: int, reps: int) -> int:
 
     def chain():
         h = x
-        for layer in layers:
-            h, _, _ = moe_block(h, layer, TOPK, plan="fused")
+        for i, layer in enumerate(layers):
+            h, _, _ = moe_block(h, layer, TOPK, plan="fused", prefetch=layers[(i + 1) % n_layers].gate_weight)
 
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
@@ -684,9 +689,12 @@ def main() -> int:
     torch.cuda.synchronize()
 
     def chain(plan):
+        # each layer's launch reads the next layer's router rows ahead into
+        # the caches (the one-launch plan; routing-independent bytes, counted
+        # once, in the layer that uses them)
         h = x
-        for layer in layers:
-            h, _, _ = moe_block(h, layer, TOPK, plan=plan)
+        for i, layer in enumerate(layers):
+            h, _, _ = moe_block(h, layer, TOPK, plan=plan, prefetch=layers[(i + 1) % L].gate_weight)
 
     # Whole-layer timing: L dependent layer decodes per graph replay (one launch each).
     g = graph_of(lambda: chain("fused"))

@@ -351,6 +351,13 @@ int ma_moe_grouped_noalloc(const void* x, int64_t ldx, const uint32_t* x_pairs,
  * src/maple_run/kernels/ternary_gemv.py:110-146, the QKV projection of
  * MapleAttention, model.py:368-414); y, next_w and next_rms 16-byte aligned,
  * next_rows <= 4096 at hidden 2048.
+ * prefetch / prefetch_bytes (optional, 16-byte aligned; NULL / 0 for none):
+ * memory the launch only reads ahead into the caches for a later kernel,
+ * such as the next MoE layer's router rows (routing-independent bytes): in
+ * the XCD-split form every XCD reads the first min(prefetch_bytes, 448 KB)
+ * bytes while its workgroups wait for h, so the next layer's router loads
+ * hit.  No effect on the results; the one-barrier form ignores it.  No
+ * reference counterpart (a scheduling hint).
  */
 size_t ma_moe_fused_workspace_bytes(int64_t n_experts, int64_t hidden, int64_t inter,
                                     int64_t top_k);
@@ -363,7 +370,7 @@ int ma_moe_fused(const void* x, const void* x_add, const void* norm_weight, int 
                  float* topk_weight, void* workspace, size_t workspace_bytes,
                  const uint32_t* next_w, const void* next_alpha, int next_alpha_dtype,
                  const float* next_rms, float next_eps, int64_t next_rows, void* next_out,
-                 void* stream);
+                 const void* prefetch, int64_t prefetch_bytes, void* stream);
 /* The one-launch layer's workgroups wait on each other (a grid barrier), so
  * all of them must be resident at once: *needed = its grid for this shape,
  * *capacity = compute units x resident workgroups per unit on the current
@@ -400,7 +407,7 @@ int ma_moe_fused_o(const void* x, const void* attn, const uint32_t* o_w, const v
                    const void* down_alpha, int alpha_dtype, void* y, int32_t* topk_ids, float* topk_weight,
                    void* workspace, size_t workspace_bytes, const uint32_t* next_w, const void* next_alpha,
                    int next_alpha_dtype, const float* next_rms, float next_eps, int64_t next_rows,
-                   void* next_out, void* stream);
+                   void* next_out, const void* prefetch, int64_t prefetch_bytes, void* stream);
 
 /* Phase stamps of the XCD-split form (diagnostics, no reference
  * counterpart).  In the library's stamped variant (libmaple_amd_stamps.so,

@@ -59,11 +59,11 @@ _SIGNATURES = {
     "ma_decode_attn_form": [_L, _I, _I, _L, _L, _I, _I],
     "ma_moe_fused_workspace_bytes": [_L, _L, _L, _L],
     "ma_moe_fused": [_P, _P, _P, _I, _F, _P, _P, _P, _L, _L, _L, _L, _P, _P, _P, _P, _I, _P, _P, _P,
-                     _P, _Z, _P, _P, _I, _P, _F, _L, _P, _P],
+                     _P, _Z, _P, _P, _I, _P, _F, _L, _P, _P, _L, _P],
     # x, attn, o_w, o_alpha, norm_w, norm_dt, eps, gate, bias, E, H, I, K, ug, ug_a, dn, dn_a, adt, y, ids,
-    # wts, ws, ws_bytes, nx_w, nx_a, nx_adt, nx_rms, nx_eps, nx_rows, nx_out, stream
+    # wts, ws, ws_bytes, nx_w, nx_a, nx_adt, nx_rms, nx_eps, nx_rows, nx_out, pf, pf_bytes, stream
     "ma_moe_fused_o": [_P, _P, _P, _P, _P, _I, _F, _P, _P, _L, _L, _L, _L, _P, _P, _P, _P, _I, _P, _P,
-                       _P, _P, _Z, _P, _P, _I, _P, _F, _L, _P, _P],
+                       _P, _P, _Z, _P, _P, _I, _P, _F, _L, _P, _P, _L, _P],
     "ma_moe_fused_timed_out": [_P, _P, _P],
     "ma_moe_fused_resident": [_L, _L, _L, _L, _PL, _PL],
     "ma_moe_fused_form": [_L, _L, _L, _L],

@@ -226,6 +226,7 @@ int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, in
                    const uint32_t* down, const void* down_alpha, int alpha_dtype, void* y, int32_t* topk_ids,
                    float* topk_weight, void* workspace, const uint32_t* next_w, const void* next_alpha,
                    const float* next_rms, float next_eps, int64_t next_rows, void* next_out, const void* attn,
-                   const uint32_t* o_w, const void* o_alpha, hipStream_t st);
+                   const uint32_t* o_w, const void* o_alpha, const void* prefetch, int64_t prefetch_bytes,
+                   hipStream_t st);
 
 }  // namespace ma

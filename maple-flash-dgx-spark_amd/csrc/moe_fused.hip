@@ -576,7 +576,8 @@ static int moe_fused_impl(const void* x, const void* x_add, const void* norm_wei
                           void* y, int32_t* topk_ids, float* topk_weight, void* workspace, size_t workspace_bytes,
                           const uint32_t* next_w, const void* next_alpha, int next_alpha_dtype,
                           const float* next_rms, float next_eps, int64_t next_rows, void* next_out, void* stream,
-                          const void* attn, const uint32_t* o_w, const void* o_alpha) {
+                          const void* attn, const uint32_t* o_w, const void* o_alpha, const void* prefetch,
+                          int64_t prefetch_bytes) {
   const FusedShape* s = find_shape(hidden, inter, top_k);
   if (!s)
     return fail(MA_EVALUE, "moe_fused: shape (hidden %lld, inter %lld, top_k %lld) not built",
@@ -620,7 +621,7 @@ static int moe_fused_impl(const void* x, const void* x_add, const void* norm_wei
     return moe_xcd_launch(x, x_add, norm_weight, norm_dtype, eps, residual, gate_weight, router_bias, n_experts,
                           hidden, inter, up_gate, up_gate_alpha, down, down_alpha, alpha_dtype, y, topk_ids,
                           topk_weight, workspace, next_w, next_alpha, next_rms, next_eps, next_rows, next_out, attn,
-                          o_w, o_alpha, st);
+                          o_w, o_alpha, prefetch, prefetch_bytes, st);
   if (o_w)
     return fail(MA_EVALUE, "moe_fused_o: the O projection in the launch needs the XCD-split form (ma_moe_fused_form)");
 #define MA_FUSED_ARGS                                                                            \
@@ -666,11 +667,12 @@ extern "C" int ma_moe_fused(const void* x, const void* x_add, const void* norm_w
                             int32_t* topk_ids, float* topk_weight, void* workspace,
                             size_t workspace_bytes, const uint32_t* next_w,
                             const void* next_alpha, int next_alpha_dtype, const float* next_rms,
-                            float next_eps, int64_t next_rows, void* next_out, void* stream) {
+                            float next_eps, int64_t next_rows, void* next_out, const void* prefetch,
+                            int64_t prefetch_bytes, void* stream) {
   return moe_fused_impl(x, x_add, norm_weight, norm_dtype, eps, residual, gate_weight, router_bias, n_experts,
                         hidden, inter, top_k, up_gate, up_gate_alpha, down, down_alpha, alpha_dtype, y, topk_ids,
                         topk_weight, workspace, workspace_bytes, next_w, next_alpha, next_alpha_dtype, next_rms,
-                        next_eps, next_rows, next_out, stream, nullptr, nullptr, nullptr);
+                        next_eps, next_rows, next_out, stream, nullptr, nullptr, nullptr, prefetch, prefetch_bytes);
 }
 
 extern "C" int ma_moe_fused_o(const void* x, const void* attn, const uint32_t* o_w, const void* o_alpha,
@@ -681,12 +683,12 @@ extern "C" int ma_moe_fused_o(const void* x, const void* attn, const uint32_t* o
                               int32_t* topk_ids, float* topk_weight, void* workspace, size_t workspace_bytes,
                               const uint32_t* next_w, const void* next_alpha, int next_alpha_dtype,
                               const float* next_rms, float next_eps, int64_t next_rows, void* next_out,
-                              void* stream) {
+                              const void* prefetch, int64_t prefetch_bytes, void* stream) {
   if (!o_w) return fail(MA_EVALUE, "moe_fused_o: no O weights");
   return moe_fused_impl(x, nullptr, norm_weight, norm_dtype, eps, nullptr, gate_weight, router_bias, n_experts,
                         hidden, inter, top_k, up_gate, up_gate_alpha, down, down_alpha, alpha_dtype, y, topk_ids,
                         topk_weight, workspace, workspace_bytes, next_w, next_alpha, next_alpha_dtype, next_rms,
-                        next_eps, next_rows, next_out, stream, attn, o_w, o_alpha);
+                        next_eps, next_rows, next_out, stream, attn, o_w, o_alpha, prefetch, prefetch_bytes);
 }
 
 extern "C" int ma_moe_fused_form(int64_t n_experts, int64_t hidden, int64_t inter, int64_t top_k) {

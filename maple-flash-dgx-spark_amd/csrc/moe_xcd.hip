@@ -43,6 +43,7 @@
 // the workspace error word is set and the kernel finishes with wrong values
 // instead of hanging (and if the workgroups were not spread over the XCDs as
 // assumed, a slot's h would be missing and its waits would time out).
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -51,6 +52,9 @@
 namespace ma {
 
 constexpr int kXcdWgs = 32;  // workgroups per XCD
+// Prefetch: 16-byte units per prefetching lane (7 waves x 32 workgroups of
+// an XCD x 2 = 28,672 units = 448 KB, more than a router of 64 x 2048 bf16)
+constexpr int kPfPerLane = 2;
 
 // Shapes: H = 16 * KWH * LPRH with LPRH = 32 (one up/gate row pair per
 // SwiGLU pass), I = 16 * KWI * LPRI, US SwiGLU outputs and UD down passes
@@ -67,7 +71,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     uint32_t* __restrict__ ws, const uint32_t* __restrict__ nx_w, const void* __restrict__ nx_alpha,
     const float* __restrict__ nx_rms, float nx_eps, int nx_rows,
     uint16_t* __restrict__ nx_out, const uint16_t* __restrict__ attn, const uint32_t* __restrict__ o_w,
-    const void* __restrict__ o_alpha) {
+    const void* __restrict__ o_alpha, const uint4* __restrict__ pf, int pf_units) {
   constexpr int TK = kXcds;  // one slot per XCD
   constexpr int W = 8;
   constexpr int LPRH = 32;
@@ -341,16 +345,6 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     load_words_v<KWH>(ug + row * NWH + klh * KWH, wu[u]);
     au[u] = ld_t<ADT>(ug_alpha, row);
   }
-  const int kld = lane % LPRI, subd = lane / LPRI;
-  const int r0 = (lw * W + wv) * RPW;
-  uint32_t wd[UD][KWI];
-  float ad[UD];
-#pragma unroll
-  for (int u = 0; u < UD; ++u) {
-    const int64_t r = ex * H + r0 + u * RPID + subd;
-    load_words_v<KWI>(dn + r * NWI + kld * KWI, wd[u]);
-    ad[u] = ld_t<ADT>(dn_alpha, r);
-  }
   // Next projection (optional): this workgroup's rows, as in k_moe_fused.
   constexpr int NXP = 1;
   const int nx_rq = nx_w ? (nx_rows + G - 1) / G : 0;
@@ -405,6 +399,31 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     if (lane < US) st_l2_32(&xh[o0 + lane], (tag16 << 16) | f32_to_bf16(swiglu_act(up_t, gate_t)));
   }
   if (wv == 0) MA_XSTAMP(5);  // this wave's h outputs published
+  const int kld = lane % LPRI, subd = lane / LPRI;
+  const int r0 = (lw * W + wv) * RPW;
+  uint32_t wd[UD][KWI];
+  float ad[UD];
+#pragma unroll
+  for (int u = 0; u < UD; ++u) {
+    const int64_t r = ex * H + r0 + u * RPID + subd;
+    load_words_v<KWI>(dn + r * NWI + kld * KWI, wd[u]);
+    ad[u] = ld_t<ADT>(dn_alpha, r);
+  }
+  // Prefetch (optional): waves 1..7 pull pf_units 16-byte units (the next
+  // layer's router rows, say) into this XCD's L2 and the Infinity Cache
+  // while they would otherwise wait for h; every XCD reads all of it (each
+  // has its own L2).  The values are only held (consumed at the end), so
+  // the loads are off every wait of the layer's own data except the last.
+  uint4 pfv[kPfPerLane];
+  constexpr int kPfLanes = kXcdWgs * (W - 1) * 64;  // lanes of an XCD that prefetch
+  const int pfl = (lw * (W - 1) + wv - 1) * 64 + lane;
+#pragma unroll
+  for (int k = 0; k < kPfPerLane; ++k) {
+    const int u = pfl + k * kPfLanes;
+    pfv[k] = make_uint4(0u, 0u, 0u, 0u);
+    if (pf && wv > 0 && u < pf_units) pfv[k] = pf[u];
+  }
+  MA_ISSUE_FENCE();
 
   // ---- 4. h of slot xcd from the XCD's region: thread t < NWI polls the 16
   // values of h word t until all carry this call's tag, then builds its x'
@@ -529,6 +548,10 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     timed_out = next_projection<KWH, LPRH, W, NXP, true>(y, nx_rms, nx_eps, nx_rows, nx_rq, nx_out, nxw, nxa, ws,
                                                          0u, G, wg, tid, lane, wv, t0, yx, tag) ||
                 timed_out;
+  if (pf && wv > 0) {  // hold the prefetched lines until they have arrived
+#pragma unroll
+    for (int k = 0; k < kPfPerLane; ++k) asm volatile("" ::"v"(pfv[k].x));
+  }
   if (wv == 0) MA_XSTAMP(11);  // end
   if (__ballot(timed_out) && lane == 0) st_coh32(&ws[2], 1u);
   if (tid == 0) st_coh32(calls, tag);
@@ -591,7 +614,8 @@ int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, in
                    const uint32_t* down, const void* down_alpha, int alpha_dtype, void* y, int32_t* topk_ids,
                    float* topk_weight, void* workspace, const uint32_t* next_w, const void* next_alpha,
                    const float* next_rms, float next_eps, int64_t next_rows, void* next_out, const void* attn,
-                   const uint32_t* o_w, const void* o_alpha, hipStream_t st) {
+                   const uint32_t* o_w, const void* o_alpha, const void* prefetch, int64_t prefetch_bytes,
+                   hipStream_t st) {
   (void)hidden;
   const void* kern = alpha_dtype == MA_F32 ? xcd_kernel_t<MA_F32>(inter) : xcd_kernel_t<MA_BF16>(inter);
   int64_t capacity = 0;
@@ -605,7 +629,12 @@ int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, in
       static_cast<int>(n_experts), up_gate, up_gate_alpha, down, down_alpha, static_cast<uint16_t*>(y), \
       topk_ids, topk_weight, static_cast<uint32_t*>(workspace), next_w, next_alpha, next_rms, next_eps, \
       static_cast<int>(next_rows), static_cast<uint16_t*>(next_out), static_cast<const uint16_t*>(attn), o_w, \
-      o_alpha
+      o_alpha, static_cast<const uint4*>(prefetch), pf_units
+  // the prefetch is a hint: whole 16-byte units, at most what the lanes cover
+  const int64_t pf_max = static_cast<int64_t>(kPfPerLane) * kXcdWgs * 7 * 64;
+  const int pf_units = prefetch ? static_cast<int>(std::min<int64_t>(prefetch_bytes / 16, pf_max)) : 0;
+  if (prefetch && (reinterpret_cast<uintptr_t>(prefetch) & 15))
+    return fail(MA_EVALUE, "moe_fused: the prefetch range must be 16-byte aligned");
   const dim3 grid(kXcds * kXcdWgs), block(512);
   if (alpha_dtype == MA_F32) {
     if (inter == 768)

@@ -180,8 +180,9 @@ class KVCache:
 class SyntheticDecoder:
     def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 4096 + 128,
                  fused_moe: bool = True, fused_o: bool = False, combine_next: bool = True,
-                 o_in_moe: bool = False):
+                 o_in_moe: bool = False, prefetch_router: bool = True):
         self.cfg = cfg
+        self.prefetch_router = prefetch_router
         self.fused_moe = fused_moe
         self.combine_next = combine_next
         self.fused_o = fused_o
@@ -208,13 +209,14 @@ class SyntheticDecoder:
     def from_weights(cls, cfg: DecoderConfig, device, layers: list, embed: tuple, lm_head: tuple,
                      final_norm: torch.Tensor, max_len: int = 4096 + 128, fused_moe: bool = True,
                      fused_o: bool = False, combine_next: bool = True,
-                     o_in_moe: bool = False) -> "SyntheticDecoder":
+                     o_in_moe: bool = False, prefetch_router: bool = True) -> "SyntheticDecoder":
         """A decoder over given weights (``checkpoint.load_decoder``) instead of
         the seeded synthetic ones."""
         self = cls.__new__(cls)
         self.cfg = cfg
         self.fused_moe, self.fused_o, self.combine_next = fused_moe, fused_o, combine_next
         self.o_in_moe = o_in_moe
+        self.prefetch_router = prefetch_router
         self.device = torch.device(device)
         self.max_len = max_len
         self.layers = list(layers)
@@ -286,9 +288,13 @@ class SyntheticDecoder:
             if fuse_next and i + 1 < c.layers and self.layers[i + 1].qkv_alpha.dtype == L.moe.up_gate_alpha.dtype:
                 n = self.layers[i + 1]
                 nl = (n.qkv, n.qkv_alpha, n.input_ln, c.eps)
+            # the next MoE layer's router rows are read ahead into the caches
+            # while this launch waits for h (routing-independent bytes)
+            pf = self.layers[i + 1].moe.gate_weight if self.prefetch_router and i + 1 < c.layers else None
             out = moe_fused(hidden, L.moe, c.top_k, add=o, norm_weight=L.post_ln, eps=c.eps,
                             next_linear=nl,
-                            o_linear=None if o is not None else (attn.reshape(1, -1), L.o, L.o_alpha))
+                            o_linear=None if o is not None else (attn.reshape(1, -1), L.o, L.o_alpha),
+                            prefetch=pf)
             y, ids = out[0], out[1]
             if nl is not None:
                 next_qkv = out[3]

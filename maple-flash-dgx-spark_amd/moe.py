@@ -89,7 +89,8 @@ def moe_fused_timed_out(device: torch.device | int = 0) -> bool:
 
 def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tensor | None = None,
               *, add: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None,
-              eps: float = 1e-6, next_linear: tuple | None = None, o_linear: tuple | None = None):
+              eps: float = 1e-6, next_linear: tuple | None = None, o_linear: tuple | None = None,
+              prefetch: torch.Tensor | None = None):
     """One token through the whole MoE layer in one launch.
 
     Plain: ``y = x_res + sum_j w_j down_j(swiglu_j(x))`` with ``x_res =
@@ -108,6 +109,10 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
     alpha)`` itself (the attention's output projection, the same bits as the
     separate GEMV; alpha of the experts' row_alpha dtype); needs the XCD-split
     form (``fused_form(layer, top_k) == 1``).
+
+    ``prefetch``: a contiguous device tensor (16-byte aligned) that the launch
+    reads ahead into the caches for a later kernel -- the next MoE layer's
+    router weight, say (routing-independent bytes); no effect on the results.
     """
     hidden = x.shape[-1]
     xf = x.reshape(1, hidden).contiguous()
@@ -124,6 +129,11 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
         o_a = o_a.contiguous()
     if (ad is not None or o_linear is not None) and norm_weight is None:
         raise ValueError("moe_fused: add needs norm_weight")
+    pf_bytes = 0
+    if prefetch is not None:
+        if not prefetch.is_contiguous() or prefetch.device != x.device:
+            raise ValueError("moe_fused: prefetch must be a contiguous tensor on x's device")
+        pf_bytes = prefetch.numel() * prefetch.element_size()
     res = (None if residual is None or ad is not None or o_linear is not None
            else residual.reshape(1, hidden).contiguous())
     nbytes = int(_lib.load().ma_moe_fused_workspace_bytes(layer.n_experts, hidden, layer.inter, top_k))
@@ -164,7 +174,7 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
             _lib.ptr(layer.down_alpha), alpha_dt, _lib.ptr(y), _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(ws),
             ws.numel(), _lib.ptr(nx_w), _lib.ptr(nx_a),
             _lib.dtype_code(nx_a, "row_alpha") if nx_a is not None else 0, _lib.ptr(nx_r),
-            float(nx_eps), nx_rows, _lib.ptr(nx_out), _lib.stream_of(x),
+            float(nx_eps), nx_rows, _lib.ptr(nx_out), _lib.ptr(prefetch), pf_bytes, _lib.stream_of(x),
         )
         return (y, ids, wts, nx_out) if next_linear is not None else (y, ids, wts)
     _lib.call(
@@ -176,7 +186,7 @@ def moe_fused(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
         _lib.ptr(layer.down_alpha), alpha_dt, _lib.ptr(y), _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(ws),
         ws.numel(), _lib.ptr(nx_w), _lib.ptr(nx_a),
         _lib.dtype_code(nx_a, "row_alpha") if nx_a is not None else 0, _lib.ptr(nx_r),
-        float(nx_eps), nx_rows, _lib.ptr(nx_out), _lib.stream_of(x),
+        float(nx_eps), nx_rows, _lib.ptr(nx_out), _lib.ptr(prefetch), pf_bytes, _lib.stream_of(x),
     )
     if next_linear is not None:
         return y, ids, wts, nx_out
@@ -326,11 +336,12 @@ def grouped_supported(layer: MoELayer, x: torch.Tensor) -> bool:
 
 
 def moe_block(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tensor | None = None,
-              *, plan: str = "auto"):
+              *, plan: str = "auto", prefetch: torch.Tensor | None = None):
     """One MoE layer on ``x [..., H]``; returns ``(y, ids, weights)``.
 
     ``plan``: "auto" (``choose_plan``), or "per_slot" / "grouped" / "fused"
-    to force one."""
+    to force one.  ``prefetch``: bytes the one-launch plan reads ahead into
+    the caches (``moe_fused``); the other plans ignore it."""
     hidden = x.shape[-1]
     xf = x.reshape(-1, hidden)
     if plan == "auto":
@@ -338,7 +349,7 @@ def moe_block(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
         plan = choose_plan(tokens, tokens == 1 and fused_supported(layer, top_k, xf),
                            grouped_supported(layer, xf))
     if plan == "fused":
-        y, ids, wts = moe_fused(xf, layer, top_k, residual)
+        y, ids, wts = moe_fused(xf, layer, top_k, residual, prefetch=prefetch)
         return y.reshape(x.shape), ids, wts
     ids, wts = router_topk(xf, layer.gate_weight, top_k, bias=layer.router_bias)
     res = None if residual is None else residual.reshape(-1, hidden)

@@ -374,3 +374,20 @@ def test_first_call_inside_graph_capture(dev):
                          timeout=300)
     assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-3000:]
     assert "FORM 1" in res.stdout, res.stdout[-2000:]
+
+
+def test_prefetch_is_only_a_hint(dev, layers):
+    """Reading the next layer's router ahead (prefetch) leaves every output
+    bit unchanged, in both forms' launcher; a misaligned range is refused."""
+    for step in range(3):
+        L, nxt = layers[step % 3], layers[(step + 1) % 3]
+        x = synthetic.randn_bf16((1, 2048), 800 + step, dev)
+        a = moe_fused(x, L, 8)
+        b = moe_fused(x, L, 8, prefetch=nxt.gate_weight)
+        c = moe_fused(x, L, 8, prefetch=nxt.up_gate_packed.view(torch.int32)[0, :4096])  # a partial range
+        torch.cuda.synchronize()
+        for u, v, w in zip(a, b, c):
+            assert torch.equal(u, v) and torch.equal(u, w)
+    with pytest.raises(ValueError, match="aligned"):
+        moe_fused(x, layers[0], 8, prefetch=layers[1].gate_weight.reshape(-1)[1:])
+    assert not moe_fused_timed_out(dev)
