@@ -422,10 +422,20 @@ int ma_moe_fused_o(const void* x, const void* attn, const uint32_t* o_w, const v
  * normal library, which writes none. */
 int ma_moe_phase_stamps(size_t* offset, int* words_per_workgroup, int* workgroups);
 
-/* *out = 1 if any ma_moe_fused call on this workspace timed out waiting
+/* *out = 1 if any ma_moe_fused call on this workspace timed out waiting,
+ * 2 if the XCD-split form found its workgroups not spread over the XCDs as
+ * it assumes (every XCD running 32 of them with distinct numbers i / 8: the
+ * call is aborted at once, its outputs invalid; turn the form off with
+ * ma_xcd_forms_disable), 0 otherwise, since the workspace was zeroed
  * (synchronises the stream).  No reference counterpart: the reference has no
  * cross-workgroup wait. */
 int ma_moe_fused_timed_out(const void* workspace, int* out, void* stream);
+
+/* Turn the XCD-split forms (ma_moe_fused's XCD split, the XCD-local decode
+ * attention) off (disable != 0) or on again for device `device`: later calls
+ * run the one-barrier / cross-XCD forms (same results to float32 rounding).
+ * No reference counterpart. */
+int ma_xcd_forms_disable(int device, int disable);
 
 /*
  * Decode (q_len = 1) QK RMSNorm + partial RoPE + KV write.  qkv bf16

@@ -68,6 +68,7 @@ _SIGNATURES = {
     "ma_moe_fused_resident": [_L, _L, _L, _L, _PL, _PL],
     "ma_moe_fused_form": [_L, _L, _L, _L],
     "ma_moe_phase_stamps": [_P, _P, _P],
+    "ma_xcd_forms_disable": [_I, _I],
     "ma_moe_route_workspace_bytes": [_L, _L],
     "ma_moe_route": [_P, _P, _L, _L, _P, _I, _F, _P, _P, _L, _I, _P, _P, _P, _P, _P, _P, _P, _P,
                      _P, _P, _P, _Z, _P],

@@ -776,11 +776,32 @@ __global__ __launch_bounds__(128) void k_gp_prep(const uint16_t* __restrict__ x,
   if (tid == 0) xc[t] = red[0] + red[1];
 }
 
-// Tile of workgroup L: the row tiles of a pair tile on one XCD.
-__device__ __forceinline__ void gp_tile(int n_rtiles, int& mtile, int& rtile) {
+// Tile of workgroup L (workgroups go to the 8 XCDs round-robin: L on XCD
+// L % 8, the XCD's slot L / 8).  The M pair tiles (experts in order, each
+// expert's tiles consecutive) are cut into 8 contiguous ranges of ceil(M / 8),
+// one per XCD, and an XCD's slots walk its range pair tile by pair tile, the
+// row tiles of a pair tile together: so an expert's pair tiles run on one
+// XCD (two at a range boundary) and read its codes through one L2, and the
+// row tiles of a pair tile share its x'.  M is counted from the dispatch
+// offsets (the grid is sized for the most tiles T k / 128 + E).  Returns
+// false for the workgroups past the XCD's range.
+__device__ __forceinline__ bool gp_tile(const int32_t* __restrict__ offsets, int n_exp, int n_rtiles, int& mtile,
+                                        int& rtile) {
+  const int lane = threadIdx.x & 63;
+  int m = 0;  // pair tiles of every expert
+  for (int base = 0; base < n_exp; base += 64) {
+    const int ee = base + lane;
+    m += ee < n_exp ? (offsets[ee + 1] - offsets[ee] + gp::kTok - 1) / gp::kTok : 0;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m += __shfl_xor(m, off, 64);
+  m = __builtin_amdgcn_readfirstlane(m);
   const int L = blockIdx.x, xcd = L % gp::kXcds, slot = L / gp::kXcds;
-  mtile = (slot / n_rtiles) * gp::kXcds + xcd;
+  const int per = (m + gp::kXcds - 1) / gp::kXcds;
+  const int local = slot / n_rtiles;
+  mtile = xcd * per + local;
   rtile = slot % n_rtiles;
+  return local < per && mtile < m;
 }
 
 // One K step of a wave: 4 row blocks x 4 pair blocks x 4 substeps of
@@ -923,7 +944,7 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
   __shared__ uint4 dsoff[kThreads];
   const int n_rtiles = static_cast<int>((n_half + kRows / 2 - 1) / (kRows / 2));
   int mtile, rtile;
-  gp_tile(n_rtiles, mtile, rtile);
+  if (!gp_tile(offsets, n_exp, n_rtiles, mtile, rtile)) return;
   int e, pos0, np;
   if (!decode_tile(offsets, n_exp, mtile, kTok, e, pos0, np)) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -1035,7 +1056,7 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
   __shared__ uint4 dsoff[kThreads];
   const int n_rtiles = static_cast<int>((n_out + kRows - 1) / kRows);
   int mtile, rtile;
-  gp_tile(n_rtiles, mtile, rtile);
+  if (!gp_tile(offsets, n_exp, n_rtiles, mtile, rtile)) return;
   int e, pos0, np;
   if (!decode_tile(offsets, n_exp, mtile, kTok, e, pos0, np)) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;

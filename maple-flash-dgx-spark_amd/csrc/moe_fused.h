@@ -36,6 +36,11 @@ namespace ma {
 //                      workgroup 16 words, word i the 100 MHz real-time
 //                      counter when the workgroup reached phase i, word 15
 //                      its XCD (unused otherwise)
+//   [400 KB, 401 KB)   XCD kernel: the layout check, one word per (XCD,
+//                      workgroup number on it), written with the call's tag
+//                      (XCD x's 32 words touched only by XCD x)
+//   line 0, word 4     XCD kernel: 1 once a call found the workgroups not
+//                      spread over the XCDs as the kernel assumes (sticky)
 constexpr int kSubB = 1, kTopB = kSubB + kBarGroups, kFlags = kTopB + 1;
 constexpr int kSubC = kFlags + kBarGroups, kTopC = kSubC + kBarGroups;
 constexpr size_t kLogitOff = 16384;
@@ -46,7 +51,9 @@ constexpr size_t kXYOff = kXPartOff + 8 * 2048 * 8, kXYRegion = 8192;
 constexpr size_t kXOOff = kXYOff + 8 * kXYRegion;
 constexpr size_t kXStampOff = kXOOff + 8 * kXYRegion;
 constexpr int kXStampWords = 16;
-constexpr size_t kXWsBytes = kXStampOff + 256 * kXStampWords * 4;
+constexpr size_t kXPresentOff = kXStampOff + 256 * kXStampWords * 4;
+constexpr size_t kXWsBytes = kXPresentOff + 256 * 4;
+constexpr int kXLayoutWord = 4;
 static_assert(kTopC < static_cast<int>(kLogitOff / 256), "workspace lines");
 static_assert(kLogitOff + 256 * kLogitStride * 8 <= kMoeWsHeader, "workspace logits");
 static_assert(kMoeWsHeader + 8 * 768 * 2 <= kXEpochOff, "grid kernel h");
@@ -79,7 +86,8 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
                                                 uint16_t* __restrict__ nx_out, const uint32_t (&nxw)[NXP][KWH],
                                                 const float (&nxa)[NXP], uint32_t* ws, uint32_t f_old, int G,
                                                 int wg, int tid, int lane, int wv, uint64_t t0,
-                                                const uint64_t* yx = nullptr, uint32_t ytag = 0) {
+                                                const uint64_t* yx = nullptr, uint32_t ytag = 0,
+                                                uint64_t wait_bound = kGridSpin) {
   constexpr int NWH = KWH * LPRH;
   constexpr int NTH = 64 * W;
   constexpr int RPIH = 64 / LPRH;
@@ -124,7 +132,7 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
           for (int i = 0; i < 4; ++i) bad |= (q[i].y ^ ytag) | (q[i].w ^ ytag);
           if (__all(bad == 0) || timed_out) break;
           __builtin_amdgcn_s_sleep(1);
-          timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+          timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > wait_bound;
         }
         // u[m]: values 2 m and 2 m + 1 of the word, as in memory
         const uint32_t u[8] = {q[0].x, q[0].z, q[1].x, q[1].z, q[2].x, q[2].z, q[3].x, q[3].z};

@@ -697,15 +697,16 @@ extern "C" int ma_moe_fused_form(int64_t n_experts, int64_t hidden, int64_t inte
 }
 
 extern "C" int ma_moe_fused_timed_out(const void* workspace, int* out, void* stream) {
-  // Copies the error word (1 if a wait timed out since the workspace was
-  // zeroed) to host memory ``out``; synchronises the stream.
+  // Copies the error words to host memory: *out = 2 if the XCD-split form's
+  // layout check aborted a call, else 1 if a wait timed out, else 0 (since
+  // the workspace was zeroed); synchronises the stream.
   if (!workspace || !out) return fail(MA_EVALUE, "moe_fused_timed_out: null pointer");
-  uint32_t v = 0;
+  uint32_t v[3] = {0, 0, 0};  // words 2 (timeout), 3 (unused), 4 (layout)
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (hipMemcpyAsync(&v, static_cast<const char*>(workspace) + 8, 4, hipMemcpyDeviceToHost, st) !=
+  if (hipMemcpyAsync(v, static_cast<const char*>(workspace) + 8, sizeof(v), hipMemcpyDeviceToHost, st) !=
           hipSuccess ||
       hipStreamSynchronize(st) != hipSuccess)
     return fail(MA_ERUNTIME, "moe_fused_timed_out: copy failed");
-  *out = static_cast<int>(v);
+  *out = v[2] ? 2 : (v[0] ? 1 : 0);
   return MA_OK;
 }

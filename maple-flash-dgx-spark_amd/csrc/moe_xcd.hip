@@ -39,10 +39,22 @@
 // Tags: each workgroup keeps its own count of calls on the workspace (written
 // only by itself at the end of a call); every call runs every workgroup, so
 // all counts agree and this call's tag is the count + 1.  Nothing needs
-// clearing between calls.  Every wait is bounded (about 0.2 s); on timeout
-// the workspace error word is set and the kernel finishes with wrong values
-// instead of hanging (and if the workgroups were not spread over the XCDs as
-// assumed, a slot's h would be missing and its waits would time out).
+// clearing between calls.  Every wait is bounded (200 us after the launch's
+// start, below); on timeout the workspace error word is set and the kernel
+// finishes with wrong values instead of hanging.
+// Layout check: the kernel is right exactly when every XCD runs 32 of the
+// workgroups with distinct numbers i / 8, i.e. (by pigeonhole) when each of
+// the 256 (XCD, number) slots gets one workgroup.  Each workgroup stores the
+// call's tag into its slot once its expert weight loads are issued: a plain
+// store into its XCD's L2 (a device-coherent one at entry, acknowledged from
+// memory, held the wave's first loads up by 0.15 us per layer: on this GPU a
+// wait for a load also waits for every older store).  The waits are bounded
+// at 200 us from the launch's start (below); a workgroup that ran out reads
+// its own XCD's 32 slots at the end.  If the layout is wrong, some XCD
+// misses a number, and the workgroups there that waited for that number's
+// data find its slot empty: the sticky layout word is set for the host,
+// which then turns the XCD-split forms off on the device
+// (ma_xcd_forms_disable).  A healthy call pays one store for it.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -52,6 +64,12 @@
 namespace ma {
 
 constexpr int kXcdWgs = 32;  // workgroups per XCD
+// Every wait of this kernel ends 200 us (of the 100 MHz counter) after the
+// launch's start at the latest -- a hundred times the longest hand-off of a
+// healthy call -- and once one has run out the later ones are skipped, so a
+// call whose workgroups cannot meet ends within about 200 us, flagged.
+// (MAPLE_AMD_WAIT_BOUND_US sets another bound, for tests.)
+constexpr uint64_t kXWaitTicks = 20000;
 // Prefetch: 16-byte units per prefetching lane (7 waves x 32 workgroups of
 // an XCD x 2 = 28,672 units = 448 KB, more than a router of 64 x 2048 bf16)
 constexpr int kPfPerLane = 2;
@@ -71,7 +89,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     uint32_t* __restrict__ ws, const uint32_t* __restrict__ nx_w, const void* __restrict__ nx_alpha,
     const float* __restrict__ nx_rms, float nx_eps, int nx_rows,
     uint16_t* __restrict__ nx_out, const uint16_t* __restrict__ attn, const uint32_t* __restrict__ o_w,
-    const void* __restrict__ o_alpha, const uint4* __restrict__ pf, int pf_units) {
+    const void* __restrict__ o_alpha, const uint4* __restrict__ pf, int pf_units, uint64_t wait_bound) {
   constexpr int TK = kXcds;  // one slot per XCD
   constexpr int W = 8;
   constexpr int LPRH = 32;
@@ -115,6 +133,9 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   const uint32_t tag16 = tag & 0xffffu;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   bool timed_out = false;
+  // the layout check: this call's tag into the slot of (this XCD, this
+  // workgroup's number on it), one device-coherent store, nothing waited for
+  uint32_t* const present = reinterpret_cast<uint32_t*>(wsb + kXPresentOff);
 #ifdef MA_PHASE_STAMPS
   uint32_t* const stamps = reinterpret_cast<uint32_t*>(wsb + kXStampOff) + kXStampWords * wg;
   if (wv == 0) {
@@ -209,7 +230,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
           for (int i = 0; i < 4; ++i) bad |= (q[i].y ^ tag) | (q[i].w ^ tag);
           if (__all(bad == 0) || timed_out) break;
           __builtin_amdgcn_s_sleep(1);
-          timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+          timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > wait_bound;
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -307,7 +328,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       }
       if (__all(have) || timed_out) break;
       __builtin_amdgcn_s_sleep(1);
-      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > wait_bound;
     }
     MA_XSTAMP(2);  // every logit of the XCD seen
     if (lane < n_exp) key = float_order_key(lg);
@@ -362,6 +383,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   }
   MA_ISSUE_FENCE();
   if (wv == 0) MA_XSTAMP(4);  // weight loads issued
+  if (tid == 0) st_l2_32(present + xcd * kXcdWgs + (lw & (kXcdWgs - 1)), tag);
 
   // routing weights while the loads are in flight (wave 0): the softmax over
   // all E logits with the max-subtracted exp, then p / (sum of the selected p
@@ -442,7 +464,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
                ((q[k].w >> 16) ^ tag16);
       if (__all(bad == 0) || timed_out) break;
       __builtin_amdgcn_s_sleep(1);
-      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > wait_bound;
     }
     if (wv == 0) MA_XSTAMP(6);  // h word 0 .. 15 seen (thread 0)
     float hv[16];
@@ -487,7 +509,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       rb = (ro & 1) ? (static_cast<uint32_t>(q) >> 16) : (static_cast<uint32_t>(q) & 0xffffu);
       if (__all(ok) || timed_out) break;
       __builtin_amdgcn_s_sleep(1);
-      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > wait_bound;
     }
   }
 
@@ -507,7 +529,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       pv = __uint_as_float(static_cast<uint32_t>(q));
       if (__all(ok) || timed_out) break;
       __builtin_amdgcn_s_sleep(1);
-      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > wait_bound;
     }
     if (wv == 0) MA_XSTAMP(9);  // the slots' values of this workgroup's rows seen
     s_pv[wv][lane] = pv;
@@ -532,7 +554,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       pv = __uint_as_float(static_cast<uint32_t>(q));
       if (__all(ok) || timed_out) break;
       __builtin_amdgcn_s_sleep(1);
-      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > kGridSpin;
+      timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > wait_bound;
     }
     MA_XSTAMP(9);
     float v = addp ? bf16_to_f32(f32_to_bf16(__uint_as_float(ra << 16) + __uint_as_float(rb << 16)))
@@ -546,14 +568,29 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   // ---- 7. next projection (optional), from the XCD's copy of y
   if (nx_w)
     timed_out = next_projection<KWH, LPRH, W, NXP, true>(y, nx_rms, nx_eps, nx_rows, nx_rq, nx_out, nxw, nxa, ws,
-                                                         0u, G, wg, tid, lane, wv, t0, yx, tag) ||
+                                                         0u, G, wg, tid, lane, wv, t0, yx, tag, wait_bound) ||
                 timed_out;
   if (pf && wv > 0) {  // hold the prefetched lines until they have arrived
 #pragma unroll
     for (int k = 0; k < kPfPerLane; ++k) asm volatile("" ::"v"(pfv[k].x));
   }
   if (wv == 0) MA_XSTAMP(11);  // end
-  if (__ballot(timed_out) && lane == 0) st_coh32(&ws[2], 1u);
+  if (__ballot(timed_out)) {
+    if (lane == 0) st_coh32(&ws[2], 1u);
+    // the layout check: a slot of this XCD still without this call's tag
+    // after 10 us more means no workgroup with that number ran here
+    // (another XCD ran two of one)
+    if (wv == 0) {
+      const uint32_t* const slot = present + xcd * kXcdWgs + (lane & (kXcdWgs - 1));
+      bool empty = __any(ld_coh32(slot) != tag);
+      const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+      while (empty && __builtin_amdgcn_s_memrealtime() - t1 < 1000) {
+        __builtin_amdgcn_s_sleep(8);
+        empty = __any(ld_coh32(slot) != tag);
+      }
+      if (empty && lane == 0) st_coh32(&ws[kXLayoutWord], 1u);
+    }
+  }
   if (tid == 0) st_coh32(calls, tag);
 }
 
@@ -629,12 +666,15 @@ int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, in
       static_cast<int>(n_experts), up_gate, up_gate_alpha, down, down_alpha, static_cast<uint16_t*>(y), \
       topk_ids, topk_weight, static_cast<uint32_t*>(workspace), next_w, next_alpha, next_rms, next_eps, \
       static_cast<int>(next_rows), static_cast<uint16_t*>(next_out), static_cast<const uint16_t*>(attn), o_w, \
-      o_alpha, static_cast<const uint4*>(prefetch), pf_units
+      o_alpha, static_cast<const uint4*>(prefetch), pf_units, wait_bound
   // the prefetch is a hint: whole 16-byte units, at most what the lanes cover
   const int64_t pf_max = static_cast<int64_t>(kPfPerLane) * kXcdWgs * 7 * 64;
   const int pf_units = prefetch ? static_cast<int>(std::min<int64_t>(prefetch_bytes / 16, pf_max)) : 0;
   if (prefetch && (reinterpret_cast<uintptr_t>(prefetch) & 15))
     return fail(MA_EVALUE, "moe_fused: the prefetch range must be 16-byte aligned");
+  // the waits' bound (MAPLE_AMD_WAIT_BOUND_US, for tests)
+  uint64_t wait_bound = kXWaitTicks;
+  if (const char* e = getenv("MAPLE_AMD_WAIT_BOUND_US")) wait_bound = static_cast<uint64_t>(atoll(e)) * 100;
   const dim3 grid(kXcds * kXcdWgs), block(512);
   if (alpha_dtype == MA_F32) {
     if (inter == 768)

@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "common.h"
@@ -23,12 +24,18 @@ __global__ __launch_bounds__(512) void k_xcd_probe(uint32_t* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = static_cast<uint32_t>(xcc_id());
 }
 
+// Per device: 1 once the host has turned the XCD-split forms off
+// (ma_xcd_forms_disable), after one of them found its workgroups not spread
+// as probed.
+static std::atomic<int> g_xcd_off[64];
+
 int xcd_round_robin(hipStream_t st, bool* ok) {
   static std::mutex mu;
   static int known[64];  // 0 unknown, 1 yes, 2 no
   *ok = false;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(MA_ERUNTIME, "no current HIP device");
+  if (g_xcd_off[dev].load(std::memory_order_relaxed)) return MA_OK;
   std::lock_guard<std::mutex> lock(mu);
   if (!known[dev]) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -55,6 +62,19 @@ int xcd_round_robin(hipStream_t st, bool* ok) {
   *ok = known[dev] == 1;
   return MA_OK;
 }
+
+}  // namespace ma
+
+// Turn the XCD-split forms (one-launch MoE layer, XCD-local decode attention)
+// off (disable != 0) or back on for a device; later calls take the
+// one-barrier / cross-XCD forms.  For the host's reaction to the layout check.
+extern "C" int ma_xcd_forms_disable(int device, int disable) {
+  if (device < 0 || device >= 64) return ma::fail(MA_EVALUE, "xcd_forms_disable: device %d", device);
+  ma::g_xcd_off[device].store(disable ? 1 : 0, std::memory_order_relaxed);
+  return MA_OK;
+}
+
+namespace ma {
 
 static thread_local char g_err[512] = "";
 

@@ -80,6 +80,27 @@ def fused_form(layer: MoELayer, top_k: int) -> int:
     return int(_lib.load().ma_moe_fused_form(layer.n_experts, layer.hidden, layer.inter, top_k))
 
 
+LAYOUT_WORD = 4  # uint32 word of the one-launch workspace set by the XCD form's layout check
+
+
+def _layout_check(workspaces, idx: int):
+    """check_timeouts hook: if the XCD-split form found its workgroups not
+    spread over the XCDs as it assumes (and aborted the call), turn the
+    XCD-split forms off on the device so that later calls take the
+    one-barrier / cross-XCD forms."""
+    if not workspaces:
+        return None
+    words = torch.stack([ws.view(torch.int32)[LAYOUT_WORD] for ws in workspaces]).cpu()
+    if not bool((words != 0).any()):
+        return None
+    _lib.call("ma_xcd_forms_disable", idx, 1)
+    return (f"the XCD-split MoE launch found its workgroups not spread over the XCDs of device {idx} "
+            "as probed; the XCD-split forms are now off on that device")
+
+
+workspace.on_timeout("moe_fused", _layout_check)
+
+
 def moe_fused_timed_out(device: torch.device | int = 0) -> bool:
     """True if a one-launch MoE call on ``device`` timed out waiting for another
     workgroup since its workspace was zeroed (the kernel records it instead of

@@ -29,9 +29,13 @@ overlap on one GPU, even on different streams: their grids could then not all
 fit, and the waits would run out (wrong values, reported by the timeout
 check).  Issue them from one stream per device, or order the streams.
 
-Every wait in those kernels is bounded (about 0.2 s); a wait that runs out
+Every wait in those kernels is bounded (about 0.2 s; in the XCD-split
+one-launch MoE layer 200 us after the launch's start); a wait that runs out
 sets the workspace's timeout word and the kernel finishes with wrong values
-instead of hanging.  ``check_timeouts`` reads every timeout word of a device
+instead of hanging.  The XCD-split layer also checks, in a call that ran out,
+whether its workgroups were spread over the XCDs as it assumes; if not, the
+timeout check turns the XCD-split forms off on that device (the hook the
+MoE module registers with ``on_timeout``).  ``check_timeouts`` reads every timeout word of a device
 in one copy (a host synchronisation) and raises ``RuntimeError`` if any is
 set, after zeroing the workspaces again so that later calls start clean.
 The decode loop (``generate.py``) calls it where it already synchronises.
@@ -50,6 +54,11 @@ TIMEOUT_WORD = {
     "moe_route": 64,  # ma_moe_route
     "attention": 2,   # ma_decode_attn_fused / ma_decode_gqa_attn (sync area, line 0)
 }
+
+# kind -> fn(workspaces of that kind on the device, device index) -> note or
+# None: run by check_timeouts on a timed-out kind before the re-zeroing
+# (the MoE layer's checks its layout word there)
+_ON_TIMEOUT: dict = {}
 
 _POOL: dict[tuple, torch.Tensor] = {}
 # (key, tensor) of workspaces replaced by larger ones; kept until the process ends
@@ -115,9 +124,22 @@ def check_timeouts(device=None) -> None:
     kinds = timed_out_kinds(device)
     if kinds:
         idx = _device_index(device if device is not None else torch.cuda.current_device())
+        notes = []
+        for kind in kinds:
+            hook = _ON_TIMEOUT.get(kind)
+            if hook is not None:
+                note = hook([ws for k, ws in _all(idx) if k == kind], idx)
+                if note:
+                    notes.append(note)
         for _, ws in _all(idx):
             ws.zero_()
         raise RuntimeError(
             "a cross-workgroup wait timed out in " + ", ".join(kinds)
             + "; the results of the calls since the last check are invalid "
-            "(workspaces have been zeroed again)")
+            "(workspaces have been zeroed again)" + "".join("; " + n for n in notes))
+
+
+def on_timeout(kind: str, fn) -> None:
+    """Register ``fn(workspaces, device_index) -> note | None``, run by
+    ``check_timeouts`` when ``kind`` timed out, before the re-zeroing."""
+    _ON_TIMEOUT[kind] = fn

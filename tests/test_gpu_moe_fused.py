@@ -391,3 +391,42 @@ def test_prefetch_is_only_a_hint(dev, layers):
     with pytest.raises(ValueError, match="aligned"):
         moe_fused(x, layers[0], 8, prefetch=layers[1].gate_weight.reshape(-1)[1:])
     assert not moe_fused_timed_out(dev)
+
+
+def test_bounded_waits_end_the_call_and_spare_the_layout_word(dev, layers, monkeypatch):
+    """The XCD form's waits end at their bound (200 us after the launch's
+    start; here 0, MAPLE_AMD_WAIT_BOUND_US, so that every wait that has to
+    wait at all runs out): the call returns at once with its error word set,
+    and, every workgroup having taken its slot, without the layout word; the
+    timeout check zeroes the workspace again, keeps the XCD forms on, and the
+    next call is right."""
+    import time
+
+    from maple_amd import workspace
+    from maple_amd.moe import LAYOUT_WORD, fused_form
+
+    L = layers[0]
+    if fused_form(L, 8) != 1:
+        pytest.skip("the XCD-split form does not run on this device")
+    x = synthetic.randn_bf16((1, 2048), 900, dev)
+    y0 = moe_fused(x, L, 8)
+    torch.cuda.synchronize()
+    key = ("moe_fused", dev.index or 0, torch.cuda.current_stream(dev).cuda_stream, 2048, L.inter, 8)
+    ws = workspace._POOL[key].view(torch.int32)
+    monkeypatch.setenv("MAPLE_AMD_WAIT_BOUND_US", "0")
+    t0 = time.perf_counter()
+    moe_fused(x, L, 8)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    monkeypatch.delenv("MAPLE_AMD_WAIT_BOUND_US")
+    assert elapsed < 0.05
+    assert int(ws[workspace.TIMEOUT_WORD["moe_fused"]].item()) == 1 and int(ws[LAYOUT_WORD].item()) == 0
+    with pytest.raises(RuntimeError, match="moe_fused") as ei:
+        workspace.check_timeouts(dev)
+    assert "XCD-split forms are now off" not in str(ei.value)
+    assert fused_form(L, 8) == 1
+    y1 = moe_fused(x, L, 8)
+    torch.cuda.synchronize()
+    for a, b in zip(y0, y1):
+        assert torch.equal(a, b)
+    assert not moe_fused_timed_out(dev)

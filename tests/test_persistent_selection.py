@@ -145,3 +145,40 @@ def test_grown_workspace_is_retired_not_freed(monkeypatch):
         workspace.get("router", 0, n)
     cur = workspace._POOL[("router", 0, 7)].numel()
     assert sum(t.numel() for _, t in workspace._RETIRED) < cur
+
+
+class _DisableRecorder:
+    """Stands in for the library: records ma_xcd_forms_disable calls."""
+
+    def __init__(self, real):
+        self.real, self.calls = real, []
+
+    def __getattr__(self, name):
+        return getattr(self.real, name)
+
+    def ma_xcd_forms_disable(self, device, disable):
+        self.calls.append((device, disable))
+        return 0
+
+
+@pytest.mark.parametrize("layout_bad", [False, True])
+def test_layout_check_turns_the_xcd_forms_off(monkeypatch, layout_bad):
+    """A timed-out one-launch workspace whose layout word is set (the XCD
+    form found two workgroups with one number on an XCD and aborted the
+    call) makes check_timeouts turn the XCD-split forms off on that device
+    and say so; a plain timeout leaves them on."""
+    stub = _DisableRecorder(moe._lib.load())
+    monkeypatch.setattr(moe._lib, "load", lambda: stub)
+    a = torch.zeros(4096, dtype=torch.uint8)
+    a.view(torch.int32)[workspace.TIMEOUT_WORD["moe_fused"]] = 1
+    if layout_bad:
+        a.view(torch.int32)[moe.LAYOUT_WORD] = 1
+    monkeypatch.setattr(workspace, "_POOL", {("moe_fused", 0, 1, 2048): a})
+    monkeypatch.setattr(workspace, "_RETIRED", [])
+    monkeypatch.setattr(workspace, "_ATTENTION", {})
+    monkeypatch.setattr(workspace, "_device_index", lambda d: 0)
+    with pytest.raises(RuntimeError, match="XCD-split forms are now off" if layout_bad else "moe_fused") as ei:
+        workspace.check_timeouts(0)
+    assert stub.calls == ([(0, 1)] if layout_bad else [])
+    assert layout_bad or "XCD-split" not in str(ei.value)
+    assert int(a.count_nonzero()) == 0  # zeroed again
