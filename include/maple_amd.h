@@ -168,6 +168,26 @@ int ma_ternary_expert_down_sum(const void* x, int x_dtype, int64_t ldx,
                                void* y, int64_t ldy, void* stream);
 
 /*
+ * The MoE block's down projection and top-k combine in one launch, with the
+ * block's rounding: out_j = alpha_e (.) (T_e h[t, j]) rounded to x_dtype per
+ * slot (what ternary_expert_gemv stores), then y[t] = sum_j w[t, j] * out_j
+ * in float32 in slot order, + residual[t] last, stored in x_dtype (what
+ * moe_reduce_add computes).  Same arguments as ma_ternary_expert_down_sum.
+ * Replaces the pair ternary_expert_gemv + moe_reduce_add of
+ * MapleSparseMoeBlock.__call__ (src/maple_run/model.py:470-473;
+ * kernels/ternary_expert.py:125-234, kernels/fused_norm.py:164-202), two
+ * launches there.
+ */
+int ma_ternary_expert_down_combine(const void* x, int x_dtype, int64_t ldx,
+                                   const uint32_t* packed, int64_t n_experts, int64_t n_out,
+                                   int64_t nwords, int packed_kn,
+                                   const void* row_alpha, int alpha_dtype,
+                                   const void* ids, int ids_is_int64, const float* topk_weight,
+                                   const void* residual, int residual_dtype,
+                                   int64_t tokens, int64_t top_k,
+                                   void* y, int64_t ldy, void* stream);
+
+/*
  * y[t, n] = sum_j w[t, j] * expert_out[t, j, n] (+ residual[t, n]), float32
  * accumulate, stored in expert_out's dtype.
  * Replaces moe_reduce_add, src/maple_run/kernels/fused_norm.py:164-202.

@@ -41,6 +41,8 @@ _SIGNATURES = {
     "ma_ternary_expert_swiglu": [_P, _I, _L, _L, _L, _P, _L, _L, _L, _I, _P, _I, _P, _I, _P, _L, _P],
     "ma_ternary_expert_down_sum": [_P, _I, _L, _P, _L, _L, _L, _I, _P, _I, _P, _I, _P, _P, _I,
                                    _L, _L, _P, _L, _P],
+    "ma_ternary_expert_down_combine": [_P, _I, _L, _P, _L, _L, _L, _I, _P, _I, _P, _I, _P, _P, _I,
+                                       _L, _L, _P, _L, _P],
     "ma_moe_reduce_add": [_P, _I, _L, _L, _L, _P, _P, _I, _P, _P],
     "ma_rms_norm": [_P, _I, _L, _L, _P, _I, _F, _P, _P],
     "ma_add_rms_norm": [_P, _P, _I, _L, _L, _P, _I, _F, _P, _P, _P],

@@ -123,7 +123,13 @@ __global__ __launch_bounds__(64) void k_egemv_fast(
 // ---------------------------------------------------------------------------
 constexpr int kDownWaves = 8;
 
-template <int KW, int LPR, int TK, int U, int ADT>
+// ROUND (the MoE block's composition, ternary_expert_gemv then moe_reduce_add,
+// model.py:470-473): each slot's output alpha * (T h) is rounded to bf16
+// (with k_egemv_fast's arithmetic), then weighted and summed in slot order
+// with k_moe_reduce's fused multiply-adds, the residual last
+// (fused_norm.py:83-96) -- the two launches' bits; otherwise
+// ternary_expert_down_sum's float32 sum.
+template <int KW, int LPR, int TK, int U, int ADT, bool ROUND>
 __global__ __launch_bounds__(64 * kDownWaves) void k_down_sum_fast(
     const uint16_t* __restrict__ x, int64_t ldx,
     const uint32_t* __restrict__ w, int64_t n_out,
@@ -134,6 +140,7 @@ __global__ __launch_bounds__(64 * kDownWaves) void k_down_sum_fast(
   constexpr int RPI = 64 / LPR;
   constexpr int SPW = TK >= kDownWaves ? TK / kDownWaves : 1;  // slots per wave
   constexpr int RPB = RPI * U;                                  // rows per workgroup
+  static_assert(!ROUND || SPW == 1, "per-slot rounding: one slot per wave");
   __shared__ float part[kDownWaves][RPB];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -170,18 +177,32 @@ __global__ __launch_bounds__(64 * kDownWaves) void k_down_sum_fast(
   for (int q = 0; q < SPW; ++q) {
     xs[q].finish();
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc[u] += slice_dot<KW>(wd[q][u], xs[q], kc) * (wj[q] * a[q][u]);
+    for (int u = 0; u < U; ++u) {
+      if constexpr (ROUND)
+        acc[u] += slice_dot<KW>(wd[q][u], xs[q], kc) * a[q][u];
+      else
+        acc[u] += slice_dot<KW>(wd[q][u], xs[q], kc) * (wj[q] * a[q][u]);
+    }
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const float v = group_sum<LPR>(acc[u]);
+    float v = group_sum<LPR>(acc[u]);
+    if constexpr (ROUND) v = bf16_to_f32(f32_to_bf16(v));  // the slot's output, as stored
     if (kl == 0) part[wv][u * RPI + sub] = v;
   }
   __syncthreads();
   if (threadIdx.x < RPB && ro < n_out) {
-    float v = resv;
+    float v;
+    if constexpr (ROUND) {
+      v = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < kDownWaves; ++ww) v += part[ww][threadIdx.x];
+      for (int j = 0; j < (TK < kDownWaves ? TK : kDownWaves); ++j) v = fmaf(wts[t * TK + j], part[j][threadIdx.x], v);
+      v += resv;
+    } else {
+      v = resv;
+#pragma unroll
+      for (int ww = 0; ww < kDownWaves; ++ww) v += part[ww][threadIdx.x];
+    }
     y[t * ldy + ro] = f32_to_bf16(v);
   }
 }
@@ -235,7 +256,7 @@ __global__ __launch_bounds__(256) void k_down_sum_generic(
     const uint32_t* __restrict__ w, int64_t n_out, int64_t nwords, int kn,
     const void* __restrict__ alpha, int a_dt, const void* __restrict__ ids, int ids64,
     int64_t n_exp, const float* __restrict__ wts, const void* __restrict__ res, int res_dt, int64_t topk,
-    void* __restrict__ y, int64_t ldy) {
+    void* __restrict__ y, int64_t ldy, int round_slots) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= n_out) return;
@@ -245,7 +266,11 @@ __global__ __launch_bounds__(256) void k_down_sum_generic(
     const int64_t s = t * topk + j;
     const int64_t e = expert_id(ids, ids64, s, n_exp);
     const float v = row_dot_generic(x, x_dt, s * ldx, w, e, row, n_out, nwords, kn, lane);
-    acc += wts[s] * (v * ld_f(alpha, a_dt, e * n_out + row));
+    float eo = v * ld_f(alpha, a_dt, e * n_out + row);
+    // round_slots: each slot's output in the activation dtype first (the block's composition)
+    if (round_slots) eo = x_dt == MA_BF16 ? bf16_to_f32(f32_to_bf16(eo))
+                          : x_dt == MA_F16 ? static_cast<float>(static_cast<_Float16>(eo)) : eo;
+    acc += wts[s] * eo;
   }
   if (lane == 0) {
     if (res) acc += ld_f(res, res_dt, t * n_out + row);
@@ -357,14 +382,11 @@ extern "C" int ma_ternary_expert_gemv(const void* x, int x_dtype, int64_t ldx, i
   return check_launch("ternary_expert_gemv");
 }
 
-extern "C" int ma_ternary_expert_down_sum(const void* x, int x_dtype, int64_t ldx,
-                                          const uint32_t* packed, int64_t n_experts,
-                                          int64_t n_out, int64_t nwords, int packed_kn,
-                                          const void* row_alpha, int alpha_dtype,
-                                          const void* ids, int ids_is_int64,
-                                          const float* topk_weight, const void* residual,
-                                          int residual_dtype, int64_t tokens, int64_t top_k,
-                                          void* y, int64_t ldy, void* stream) {
+template <bool ROUND>
+static int down_sum_impl(const void* x, int x_dtype, int64_t ldx, const uint32_t* packed, int64_t n_experts,
+                         int64_t n_out, int64_t nwords, int packed_kn, const void* row_alpha, int alpha_dtype,
+                         const void* ids, int ids_is_int64, const float* topk_weight, const void* residual,
+                         int residual_dtype, int64_t tokens, int64_t top_k, void* y, int64_t ldy, void* stream) {
   if (tokens < 0 || top_k < 1 || n_out < 0 || nwords < 1 || n_experts < 1)
     return fail(MA_EVALUE, "ternary_expert_down_sum: bad sizes");
   if (tokens == 0 || n_out == 0) return MA_OK;
@@ -380,11 +402,11 @@ extern "C" int ma_ternary_expert_down_sum(const void* x, int x_dtype, int64_t ld
     const auto* ib = static_cast<const int32_t*>(ids);                                         \
     auto* yb = static_cast<uint16_t*>(y);                                                      \
     if (alpha_dtype == MA_BF16)                                                                \
-      hipLaunchKernelGGL((k_down_sum_fast<K, L, TK, U, MA_BF16>), grid, dim3(64 * kDownWaves), 0, s, xb, ldx, \
+      hipLaunchKernelGGL((k_down_sum_fast<K, L, TK, U, MA_BF16, ROUND>), grid, dim3(64 * kDownWaves), 0, s, xb, ldx, \
                          packed, n_out, row_alpha, ib, n_experts, topk_weight, residual,       \
                          residual_dtype, yb, ldy);                                             \
     else                                                                                       \
-      hipLaunchKernelGGL((k_down_sum_fast<K, L, TK, U, MA_F32>), grid, dim3(64 * kDownWaves), 0, s, xb, ldx, \
+      hipLaunchKernelGGL((k_down_sum_fast<K, L, TK, U, MA_F32, ROUND>), grid, dim3(64 * kDownWaves), 0, s, xb, ldx, \
                          packed, n_out, row_alpha, ib, n_experts, topk_weight, residual,       \
                          residual_dtype, yb, ldy);                                             \
     return check_launch("ternary_expert_down_sum");                                           \
@@ -397,6 +419,35 @@ extern "C" int ma_ternary_expert_down_sum(const void* x, int x_dtype, int64_t ld
   dim3 grid(static_cast<unsigned>(cdiv(n_out, 4)), static_cast<unsigned>(tokens));
   hipLaunchKernelGGL(k_down_sum_generic, grid, dim3(256), 0, s, x, x_dtype, ldx, packed, n_out,
                      nwords, packed_kn, row_alpha, alpha_dtype, ids, ids_is_int64, n_experts, topk_weight,
-                     residual, residual_dtype, top_k, y, ldy);
+                     residual, residual_dtype, top_k, y, ldy, ROUND ? 1 : 0);
   return check_launch("ternary_expert_down_sum");
+}
+
+extern "C" int ma_ternary_expert_down_sum(const void* x, int x_dtype, int64_t ldx,
+                                          const uint32_t* packed, int64_t n_experts,
+                                          int64_t n_out, int64_t nwords, int packed_kn,
+                                          const void* row_alpha, int alpha_dtype,
+                                          const void* ids, int ids_is_int64,
+                                          const float* topk_weight, const void* residual,
+                                          int residual_dtype, int64_t tokens, int64_t top_k,
+                                          void* y, int64_t ldy, void* stream) {
+  return down_sum_impl<false>(x, x_dtype, ldx, packed, n_experts, n_out, nwords, packed_kn, row_alpha,
+                              alpha_dtype, ids, ids_is_int64, topk_weight, residual, residual_dtype, tokens,
+                              top_k, y, ldy, stream);
+}
+
+// The MoE block's down projection and combine (ternary_expert_gemv, then
+// moe_reduce_add) in one launch: each slot's output rounded to the
+// activation dtype before the float32 weighted sum, the residual last.
+extern "C" int ma_ternary_expert_down_combine(const void* x, int x_dtype, int64_t ldx,
+                                              const uint32_t* packed, int64_t n_experts,
+                                              int64_t n_out, int64_t nwords, int packed_kn,
+                                              const void* row_alpha, int alpha_dtype,
+                                              const void* ids, int ids_is_int64,
+                                              const float* topk_weight, const void* residual,
+                                              int residual_dtype, int64_t tokens, int64_t top_k,
+                                              void* y, int64_t ldy, void* stream) {
+  return down_sum_impl<true>(x, x_dtype, ldx, packed, n_experts, n_out, nwords, packed_kn, row_alpha,
+                             alpha_dtype, ids, ids_is_int64, topk_weight, residual, residual_dtype, tokens,
+                             top_k, y, ldy, stream);
 }

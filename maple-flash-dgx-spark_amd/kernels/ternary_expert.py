@@ -150,11 +150,18 @@ def ternary_expert_down_sum(
     residual: torch.Tensor | None = None,
     *,
     packed_kn: bool = False,
+    round_slots: bool = False,
 ) -> torch.Tensor:
     """Down-proj GEMV, weighted sum over top-k, optional residual add. One launch.
 
     ``x`` and ``expert_ids`` / ``topk_weight`` share leading dims ``[..., topk]``.
     Returns ``[..., N]`` (top-k reduced).
+
+    ``round_slots`` (not in the reference's signature): the MoE block's
+    composition instead -- each slot's output rounded to ``x.dtype`` before
+    the float32 weighted sum, the residual added last, i.e.
+    ``moe_reduce_add(ternary_expert_gemv(...), topk_weight, residual)``
+    (``model.py:470-473``) in one launch (``ma_ternary_expert_down_combine``).
     """
     if packed_weight.ndim != 3 or packed_weight.dtype != torch.uint32:
         raise ValueError("packed_weight must be uint32 [E, N, K/16] or [E, K/16, N].")
@@ -183,7 +190,7 @@ def ternary_expert_down_sum(
     pw = packed_weight.contiguous()
     alpha = row_alpha.contiguous()
     _lib.call(
-        "ma_ternary_expert_down_sum",
+        "ma_ternary_expert_down_combine" if round_slots else "ma_ternary_expert_down_sum",
         _lib.ptr(x_mat), _lib.dtype_code(x_mat, "x"), x_mat.stride(0) if x_mat.shape[0] else k_in,
         _lib.ptr(pw), n_exp, n_out, nwords, int(bool(packed_kn)),
         _lib.ptr(alpha), _lib.dtype_code(alpha, "row_alpha"), _lib.ptr(ids), ids64,

@@ -13,10 +13,10 @@ device):
   match the reference (bf16 h, bf16 per-slot output, float32 combine).
 * other decode (``tokens < GROUPED_MIN_TOKENS``, ``plan="per_slot"``):
   per-slot kernels, as the reference does -- fused SwiGLU, then the down
-  projection and the combine in one launch (``ternary_expert_down_sum``).
-  That skips the reference's bf16 rounding of each slot's down output before
-  the combine (``model.py:470-473``); the result stays within bf16 tolerance
-  of it.
+  projection and the combine in one launch
+  (``ternary_expert_down_sum(..., round_slots=True)``), with the reference's
+  rounding points: each slot's down output rounded to bf16 before the
+  float32 combine, the residual added last (``model.py:470-473``).
 * batched decode / prefill: dispatch the (token, slot) pairs into per-expert
   lists and run grouped MFMA GEMMs (``ma_moe_grouped``), so each selected
   expert's weights are read once per tile of its tokens instead of once per
@@ -378,7 +378,8 @@ def moe_block(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
         y = moe_grouped(xf, layer, ids, wts, res)
     else:
         h = ternary_expert_swiglu(xf, layer.up_gate_packed, layer.up_gate_alpha, ids)
-        y = ternary_expert_down_sum(h, layer.down_packed, layer.down_alpha, ids, wts, residual=res)
+        y = ternary_expert_down_sum(h, layer.down_packed, layer.down_alpha, ids, wts, residual=res,
+                                    round_slots=True)
     return y.reshape(x.shape), ids, wts
 
 

@@ -507,3 +507,32 @@ def test_greedy_argmax_all_negative_short_rows(dev, n, dtype):
     x = (-1.0 - torch.rand(4, n, generator=g, device=dev)).to(dtype)
     got = greedy_argmax(x)
     torch.testing.assert_close(got, torch.argmax(x.float(), dim=-1), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("tokens,top_k,dtype", [(1, 8, torch.bfloat16), (2, 8, torch.bfloat16),
+                                                (3, 8, torch.bfloat16), (5, 4, torch.bfloat16),
+                                                (3, 2, torch.float32)])
+def test_down_combine_is_the_blocks_two_launches(dev, tokens, top_k, dtype):
+    """ternary_expert_down_sum(..., round_slots=True) (ma_ternary_expert_down_combine,
+    what the per-slot MoE plan runs) gives the bits of the reference block's
+    two launches, ternary_expert_gemv then moe_reduce_add (model.py:470-473):
+    each slot's output rounded to x's dtype, the float32 combine in slot
+    order, the residual last; the plain down_sum keeps its float32 sum (and
+    differs); float32 x takes the generic kernel."""
+    from maple_amd.kernels import moe_reduce_add, ternary_expert_down_sum, ternary_expert_gemv
+
+    e, n_out, inter = 16, 2048, 768
+    w = synthetic.ternary_packed((e, n_out, inter), 31, dev)
+    alpha = synthetic.uniform_bf16((e, n_out), 0.01, 0.05, 32, dev)
+    h = synthetic.randn_bf16((tokens, top_k, inter), 33, dev).to(dtype)
+    g = torch.Generator(device=dev).manual_seed(34)
+    ids = torch.stack([torch.randperm(e, generator=g, device=dev)[:top_k] for _ in range(tokens)]).to(torch.int32)
+    wts = torch.rand(tokens, top_k, device=dev, generator=g)
+    wts = wts / wts.sum(-1, keepdim=True)
+    res = synthetic.randn_bf16((tokens, n_out), 35, dev).to(dtype)
+    y = ternary_expert_down_sum(h, w, alpha, ids, wts, residual=res, round_slots=True)
+    ref = moe_reduce_add(ternary_expert_gemv(h, w, alpha, ids), wts, residual=res)
+    plain = ternary_expert_down_sum(h, w, alpha, ids, wts, residual=res)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref)
+    assert_bf16_close(np_f(plain), np_f(ref), rtol=2 ** -7, atol_frac=2e-3, what="plain vs rounded")
