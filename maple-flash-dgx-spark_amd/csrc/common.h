@@ -62,6 +62,22 @@ __device__ __forceinline__ float ld_t(const void* p, int64_t i) {
   else return static_cast<const float*>(p)[i];
 }
 
+// Raw bits of element i of a row-scale array, converted by from_raw<DT>
+// where the value is used.  Converted next to the load inside a branch, the
+// value makes the wave wait for that load there -- and, memory counters
+// completing in issue order, for every load issued before it.
+template <int DT>
+__device__ __forceinline__ uint32_t ld_raw(const void* p, int64_t i) {
+  if constexpr (DT == MA_F32) return static_cast<const uint32_t*>(p)[i];
+  else return static_cast<const uint16_t*>(p)[i];
+}
+template <int DT>
+__device__ __forceinline__ float from_raw(uint32_t u) {
+  if constexpr (DT == MA_BF16) return bf16_to_f32(static_cast<uint16_t>(u));
+  else if constexpr (DT == MA_F16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u)));
+  else return __uint_as_float(u);
+}
+
 __device__ __forceinline__ float ld_f(const void* p, int dt, int64_t i) {
   switch (dt) {
     case MA_BF16: return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);

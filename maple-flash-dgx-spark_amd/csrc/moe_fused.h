@@ -178,6 +178,8 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
     }
   }
   __syncthreads();
+  // A wave with no rows of this workgroup is done (nothing below waits for it).
+  if (wv * RPIH >= nx_rq) return timed_out;
   // This lane's slice, in the standalone GEMV's order: sum of squares of
   // the raw values, then the pairs' correction term.
   uint32_t xh[KWH][8], xl[KWH][8];

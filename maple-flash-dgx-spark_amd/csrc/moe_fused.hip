@@ -343,14 +343,14 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
   constexpr int NXP = W == 4 ? 2 : 1;
   const int nx_rq = nx_w ? (nx_rows + G - 1) / G : 0;
   uint32_t nxw[NXP][KWH];
-  float nxa[NXP];
+  uint32_t nxa_raw[NXP] = {};  // converted where used (ld_raw)
   if (nx_w) {
 #pragma unroll
     for (int p = 0; p < NXP; ++p) {
       int r = wg * nx_rq + p * W * RPIH + wv * RPIH + subh;
       r = r < nx_rows ? r : nx_rows - 1;
       load_words_v<KWH>(nx_w + static_cast<int64_t>(r) * NWH + klh * KWH, nxw[p]);
-      nxa[p] = ld_t<ADT>(nx_alpha, r);
+      nxa_raw[p] = ld_raw<ADT>(nx_alpha, r);
     }
   }
   MA_ISSUE_FENCE();
@@ -493,6 +493,13 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
   }
 
   // ---- 5. next projection (optional), once every workgroup's rows of y are out
+  float nxa[NXP];
+#pragma unroll
+  for (int p = 0; p < NXP; ++p) {
+    uint32_t u = nxa_raw[p];
+    asm volatile("" : "+v"(u));  // keeps the conversion here, not next to the load
+    nxa[p] = from_raw<ADT>(u);
+  }
   if (nx_w)
     timed_out = next_projection<KWH, LPRH, W, NXP>(y, nx_rms, nx_eps, nx_rows, nx_rq, nx_out, nxw, nxa, ws,
                                                    f0 + 1u, G, wg, tid, lane, wv, t0) ||

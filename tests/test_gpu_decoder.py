@@ -174,6 +174,38 @@ def test_fused_attention_o_projection_equals_gemv(dev, seqlen, heads):
 
 
 @pytest.mark.parametrize("heads", HEADS[:2])
+@pytest.mark.parametrize("batch,window", [(1, None), (4, None), (3, 300)])
+def test_attention_ignores_cache_rows_past_the_sequence(dev, batch, window, heads):
+    """Cache positions past a row's new one hold NaN in one call and zeros in
+    the other: the outputs and the written K/V are the same bits (no load
+    reaches past the sequence, or a value read there reaches the output)."""
+    nq, nkv, d, rot = heads
+    max_len = 1000
+    seqlen = torch.tensor([999, 0, 130, 640][:batch], device=dev)
+    qkv = synthetic.randn_bf16((batch, (nq + 2 * nkv) * d), 61, dev)
+    kc = synthetic.randn_bf16((batch, nkv, max_len, d), 62, dev)
+    vc = synthetic.randn_bf16((batch, nkv, max_len, d), 63, dev)
+    past = torch.arange(max_len, device=dev)[None, :] > seqlen[:, None]  # [B, max_len]
+    m = past[:, None, :, None].expand_as(kc)
+    w = torch.ones(d, device=dev)
+    cos, sin = (torch.from_numpy(t).to(dev) for t in od.rope_tables(max_len, rot, 1e4))
+    kw = dict(num_heads=nq, num_kv_heads=nkv, head_dim=d, rotary_dim=rot, eps=1e-6, scale=d ** -0.5,
+              window=window)
+    outs, caches = [], []
+    for fill in (float("nan"), 0.0):
+        k2, v2 = kc.masked_fill(m, fill), vc.masked_fill(m, fill)
+        outs.append(decode_attention(qkv, w, w, cos, sin, k2, v2, seqlen,
+                                     gqa_workspace(batch, nkv, max_len, dev, d), **kw))
+        caches.append((k2, v2))
+    torch.cuda.synchronize()
+    assert not torch.isnan(outs[0]).any()
+    assert torch.equal(outs[0], outs[1])
+    live = ~m
+    for a, b in zip(caches[0], caches[1]):
+        assert torch.equal(a[live], b[live])
+
+
+@pytest.mark.parametrize("heads", HEADS[:2])
 @pytest.mark.parametrize("batch,window", [(1, None), (3, 300), (9, None), (32, None)])
 def test_attention_xcd_form_equals_grid_form(dev, monkeypatch, batch, window, heads):
     """The XCD-local attention form (every split of a (row, KV head) on one
