@@ -39,6 +39,7 @@ configurations the same way (bounded samples, each stated).
     python bench.py --counters-pass moe_bs1|prefill|decode32   # for rocprofv3 --pmc
     python bench.py --decode-batch 32 # only the full decoder at one batch size
     python bench.py --timeline        # the one-launch MoE layer's phase stamps
+    python bench.py --timeline-decoder  # the same with the add + norm and the next QKV projection
     python bench.py --gemv | --preview # config 1 alone | Maple-Preview shapes alone
 """
 
@@ -553,16 +554,24 @@ def counters_pass(dev, kind: str, n_layers: int) -> int:
 
 PHASES = ["start", "router logit out", "logits seen", "ranked", "weight loads issued", "h published",
           "h seen", "h staged", "down values out", "down values seen", "y out", "end"]
+# with the add + RMSNorm in front and the next layer's QKV projection behind
+NEXT_PHASES = ["next: y seen", "next: x' staged", "next: rows out"]
 
 
-def timeline(dev, n_layers: int, reps: int) -> int:
+def timeline(dev, n_layers: int, reps: int, decoder_form: bool = False) -> int:
     """Per-phase timeline of the one-launch MoE layer: the library's stamped
     variant (libmaple_amd_stamps.so, ma_moe_phase_stamps) runs ``n_layers``
     chained cold layers in one graph; after each replay the stamps of the
     chain's last layer are read from the workspace.  Prints one JSON line:
     per phase the median / p90 / max over workgroups and replays of the time
     since the launch's first workgroup started (us), and the stamped build's
-    period per layer (the stamps' own stores and waits lengthen it)."""
+    period per layer (the stamps' own stores and waits lengthen it).
+
+    ``decoder_form``: each layer as the bs1 decoder runs it -- the
+    attention's projected output added to x and RMS-normed in front (a fixed
+    bf16 vector, float32 norm weights), and the next layer's RMS-folded QKV
+    projection (2560 x 2048 ternary rows, bf16 row scales) behind, from each
+    XCD's own copy of y."""
     import ctypes
 
     import numpy as np
@@ -582,11 +591,25 @@ def timeline(dev, n_layers: int, reps: int) -> int:
         log("timeline: the XCD-split form does not run on this device")
         return 1
     x = synthetic.randn_bf16((1, HIDDEN), 12345, dev)
+    phases = PHASES + (NEXT_PHASES if decoder_form else [])
+    if decoder_form:
+        from maple_amd.moe import moe_fused
+
+        o = synthetic.randn_bf16((1, HIDDEN), 54321, dev)
+        norms = [(torch.rand(HIDDEN, generator=torch.Generator().manual_seed(i)) + 0.5).to(dev)
+                 for i in range(n_layers)]
+        qkv = [synthetic.ternary_linear(2560, HIDDEN, 1000 + i, dev) for i in range(n_layers)]
 
     def chain():
         h = x
         for i, layer in enumerate(layers):
-            h, _, _ = moe_block(h, layer, TOPK, plan="fused", prefetch=layers[(i + 1) % n_layers].gate_weight)
+            nxt = (i + 1) % n_layers
+            if decoder_form:
+                h = moe_fused(h, layer, TOPK, add=o, norm_weight=norms[i], eps=1e-6,
+                              next_linear=(qkv[nxt][0], qkv[nxt][1], norms[nxt], 1e-6),
+                              prefetch=layers[nxt].gate_weight)[0]
+            else:
+                h, _, _ = moe_block(h, layer, TOPK, plan="fused", prefetch=layers[nxt].gate_weight)
 
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
@@ -613,15 +636,16 @@ def timeline(dev, n_layers: int, reps: int) -> int:
     workspace.check_timeouts(dev)
     d = np.stack(rows) & 0xFFFFFFFF  # [reps, workgroups, words], 32-bit counter values
     t0 = d[:, :, 0].min(axis=1, keepdims=True)
-    rel = ((d[:, :, :len(PHASES)] - t0[:, :, None]) & 0xFFFFFFFF) * 0.01  # 100 MHz ticks -> us
+    rel = ((d[:, :, :len(phases)] - t0[:, :, None]) & 0xFFFFFFFF) * 0.01  # 100 MHz ticks -> us
     out = {}
     router_wgs = np.arange(ng) < 64  # workgroups 0..7 of each XCD (i / 8 < 8)
-    for i, name in enumerate(PHASES):
+    for i, name in enumerate(phases):
         v = rel[:, router_wgs, i] if i == 1 else rel[:, :, i]
         out[name] = {"median": round(float(np.median(v)), 2), "p90": round(float(np.percentile(v, 90)), 2),
                      "max": round(float(v.max()), 2)}
     xcds = sorted(set(int(v) for v in d[0, :, 15]))
     print(json.dumps({"timeline": "k_moe_xcd phase stamps, us from the launch's first workgroup",
+                      "form": "decoder (add + norm, next QKV projection)" if decoder_form else "plain",
                       "layers_in_chain": n_layers, "replays": reps, "xcds_seen": xcds,
                       "stamped_us_per_layer": round(elapsed / reps / n_layers * 1e6, 3), "phases": out}),
           flush=True)
@@ -649,6 +673,8 @@ def main() -> int:
                     help="only the decoder at Maple-Preview shapes (bs1 sampled / greedy, bs32)")
     ap.add_argument("--timeline", action="store_true",
                     help="only the one-launch MoE layer's per-phase timeline (stamped library)")
+    ap.add_argument("--timeline-decoder", action="store_true",
+                    help="the same in the decoder's form (add + norm in front, next QKV projection behind)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: there is no multi-GPU path "
@@ -669,8 +695,8 @@ def main() -> int:
     L = args.layers
     if args.counters_pass:
         return counters_pass(dev, args.counters_pass, L)
-    if args.timeline:
-        return timeline(dev, L, max(args.steps, 10))
+    if args.timeline or args.timeline_decoder:
+        return timeline(dev, L, max(args.steps, 10), decoder_form=args.timeline_decoder)
     if args.gemv:
         print(json.dumps({"gemv_1536x2048_bs1": gemv_config1(dev, max(args.steps, 3))}), flush=True)
         return 0

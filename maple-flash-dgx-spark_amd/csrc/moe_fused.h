@@ -69,6 +69,15 @@ static_assert(2048 / 2 * 8 <= kXYRegion, "XCD y region");
 #else
 #define MA_XSTAMP(i) do {} while (0)
 #endif
+// The same from a function given the stamp row (null: none), lane 0 of wave 0.
+#ifdef MA_PHASE_STAMPS
+#define MA_XSTAMP_AT(row, i)                                                           \
+  do {                                                                                \
+    if ((row) && tid == 0) (row)[i] = static_cast<uint32_t>(__builtin_amdgcn_s_memrealtime()); \
+  } while (0)
+#else
+#define MA_XSTAMP_AT(row, i) do {} while (0)
+#endif
 
 // Next projection, run by every workgroup of a one-launch layer once its rows
 // of y are out: nx_out = ternary_gemv(y, nx_w, nx_alpha, rms_weight = nx_rms)
@@ -87,7 +96,7 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
                                                 const float (&nxa)[NXP], uint32_t* ws, uint32_t f_old, int G,
                                                 int wg, int tid, int lane, int wv, uint64_t t0,
                                                 const uint64_t* yx = nullptr, uint32_t ytag = 0,
-                                                uint64_t wait_bound = kGridSpin) {
+                                                uint64_t wait_bound = kGridSpin, uint32_t* stamps = nullptr) {
   constexpr int NWH = KWH * LPRH;
   constexpr int NTH = 64 * W;
   constexpr int RPIH = 64 / LPRH;
@@ -177,7 +186,9 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
       }
     }
   }
+  MA_XSTAMP_AT(stamps, 12);  // this thread's part of y seen
   __syncthreads();
+  MA_XSTAMP_AT(stamps, 13);  // y and its x' pairs staged
   // A wave with no rows of this workgroup is done (nothing below waits for it).
   if (wv * RPIH >= nx_rq) return timed_out;
   // This lane's slice, in the standalone GEMV's order: sum of squares of
@@ -224,6 +235,7 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
     const int r = wg * nx_rq + rl;
     if (klh == 0 && rl < nx_rq && r < nx_rows) nx_out[r] = f32_to_bf16(d);
   }
+  MA_XSTAMP_AT(stamps, 14);  // projection rows out
   return timed_out;
 }
 

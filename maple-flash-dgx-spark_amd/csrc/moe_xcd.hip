@@ -77,8 +77,9 @@ constexpr int kPfPerLane = 2;
 // Shapes: H = 16 * KWH * LPRH with LPRH = 32 (one up/gate row pair per
 // SwiGLU pass), I = 16 * KWI * LPRI, US SwiGLU outputs and UD down passes
 // (64 / LPRI rows each) per wave, 8 waves per workgroup, E <= 64 experts,
-// top-8; ADT the row scales' dtype.
-template <int KWH, int US, int KWI, int LPRI, int UD, int ADT>
+// top-8; ADT the row scales' dtype; NX: the instance launched with a next
+// projection (nx_w set).
+template <int KWH, int US, int KWI, int LPRI, int UD, int ADT, bool NX>
 __global__ __launch_bounds__(512) void k_moe_xcd(
     const uint16_t* __restrict__ xa, const uint16_t* __restrict__ xb,
     const void* __restrict__ norm_w, int norm_dt, float eps, const uint16_t* __restrict__ residual,
@@ -366,12 +367,17 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     load_words_v<KWH>(ug + row * NWH + klh * KWH, wu[u]);
     au[u] = ld_t<ADT>(ug_alpha, row);
   }
-  // Next projection (optional): this workgroup's rows, as in k_moe_fused.
+  // Next projection (nx_w): this workgroup's rows, as in k_moe_fused.  In
+  // the instance built for it (NX) the loads are not behind a branch: past a
+  // branch holding loads, a wait for the loads issued before it also waits
+  // for these (the counts of the two paths merge).  (The instance without
+  // keeps the run-time branches: the same code without them measured 0.09 us
+  // slower per layer.)
   constexpr int NXP = 1;
   const int nx_rq = nx_w ? (nx_rows + G - 1) / G : 0;
   uint32_t nxw[NXP][KWH];
   uint32_t nxa_raw[NXP] = {};  // converted where used (ld_raw)
-  if (nx_w) {
+  if (NX || nx_w) {
     const int subh = lane / LPRH;
 #pragma unroll
     for (int p = 0; p < NXP; ++p) {
@@ -519,7 +525,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   // over through its L2, two values per tagged word; each XCD stores an
   // eighth of y.  Otherwise workgroup wg finishes rows wg * FR .. + FR:
   // lane l of wave 0 polls slot l / FR's value of row wg * FR + l % FR.
-  if (nx_w) {
+  if (NX || nx_w) {
     static_assert(H == 64 * kXcdWgs, "64 rows of y per workgroup of an XCD");
     const int row = 64 * lw + lane;
     float pv = 0.f;
@@ -566,17 +572,20 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   }
 
   // ---- 7. next projection (optional), from the XCD's copy of y
-  float nxa[NXP];
+  if (NX || nx_w) {
+    float nxa[NXP];
 #pragma unroll
-  for (int p = 0; p < NXP; ++p) {
-    uint32_t u = nxa_raw[p];
-    asm volatile("" : "+v"(u));  // keeps the conversion here, not next to the load
-    nxa[p] = from_raw<ADT>(u);
-  }
-  if (nx_w)
+    for (int p = 0; p < NXP; ++p) nxa[p] = from_raw<ADT>(nxa_raw[p]);
     timed_out = next_projection<KWH, LPRH, W, NXP, true>(y, nx_rms, nx_eps, nx_rows, nx_rq, nx_out, nxw, nxa, ws,
-                                                         0u, G, wg, tid, lane, wv, t0, yx, tag, wait_bound) ||
+                                                         0u, G, wg, tid, lane, wv, t0, yx, tag, wait_bound,
+#ifdef MA_PHASE_STAMPS
+                                                         stamps
+#else
+                                                         nullptr
+#endif
+                                                         ) ||
                 timed_out;
+  }
   if (pf && wv > 0) {  // hold the prefetched lines until they have arrived
 #pragma unroll
     for (int k = 0; k < kPfPerLane; ++k) asm volatile("" ::"v"(pfv[k].x));
@@ -601,12 +610,31 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   if (tid == 0) st_coh32(calls, tag);
 }
 
+// The instances in a fixed order in the code object: the forms without the
+// next projection first (the kernel's timing moved by ~0.7 % with its
+// position in the code object alone).
+#define MA_XCD_INST(US, KWI, ADT, NX)                                                                      \
+  template __global__ void k_moe_xcd<4, US, KWI, 16, 2, ADT, NX>(                                         \
+      const uint16_t*, const uint16_t*, const void*, int, float, const uint16_t*, const uint16_t*,       \
+      const float*, int, const uint32_t*, const void*, const uint32_t*, const void*, uint16_t*, int32_t*, \
+      float*, uint32_t*, const uint32_t*, const void*, const float*, float, int, uint16_t*,              \
+      const uint16_t*, const uint32_t*, const void*, const uint4*, int, uint64_t);
+MA_XCD_INST(3, 3, MA_F32, false)
+MA_XCD_INST(2, 2, MA_F32, false)
+MA_XCD_INST(3, 3, MA_BF16, false)
+MA_XCD_INST(2, 2, MA_BF16, false)
+MA_XCD_INST(3, 3, MA_F32, true)
+MA_XCD_INST(2, 2, MA_F32, true)
+MA_XCD_INST(3, 3, MA_BF16, true)
+MA_XCD_INST(2, 2, MA_BF16, true)
+#undef MA_XCD_INST
+
 namespace {
 
-template <int ADT>
+template <int ADT, bool NX>
 const void* xcd_kernel_t(int64_t inter) {
-  return inter == 768 ? reinterpret_cast<const void*>(&k_moe_xcd<4, 3, 3, 16, 2, ADT>)
-                      : reinterpret_cast<const void*>(&k_moe_xcd<4, 2, 2, 16, 2, ADT>);
+  return inter == 768 ? reinterpret_cast<const void*>(&k_moe_xcd<4, 3, 3, 16, 2, ADT, NX>)
+                      : reinterpret_cast<const void*>(&k_moe_xcd<4, 2, 2, 16, 2, ADT, NX>);
 }
 
 }  // namespace
@@ -646,8 +674,8 @@ bool moe_xcd_supported(int64_t n_experts, int64_t hidden, int64_t inter, int64_t
       cus != kXcds * kXcdWgs)
     return false;
   int64_t capacity = 0;  // every workgroup resident (the grid form is used otherwise)
-  if (resident_capacity(xcd_kernel_t<MA_BF16>(inter), 512, &capacity) != MA_OK || capacity < kXcds * kXcdWgs)
-    return false;
+  for (const void* k : {xcd_kernel_t<MA_BF16, false>(inter), xcd_kernel_t<MA_BF16, true>(inter)})
+    if (resident_capacity(k, 512, &capacity) != MA_OK || capacity < kXcds * kXcdWgs) return false;
   bool ok = false;
   return xcd_round_robin(st, &ok) == MA_OK && ok;
 }
@@ -661,7 +689,9 @@ int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, in
                    const uint32_t* o_w, const void* o_alpha, const void* prefetch, int64_t prefetch_bytes,
                    hipStream_t st) {
   (void)hidden;
-  const void* kern = alpha_dtype == MA_F32 ? xcd_kernel_t<MA_F32>(inter) : xcd_kernel_t<MA_BF16>(inter);
+  const bool nx = next_w != nullptr;
+  const void* kern = alpha_dtype == MA_F32 ? (nx ? xcd_kernel_t<MA_F32, true>(inter) : xcd_kernel_t<MA_F32, false>(inter))
+                                           : (nx ? xcd_kernel_t<MA_BF16, true>(inter) : xcd_kernel_t<MA_BF16, false>(inter));
   int64_t capacity = 0;
   if (int rc = resident_capacity(kern, 512, &capacity)) return rc;
   if (capacity < kXcds * kXcdWgs)
@@ -683,17 +713,25 @@ int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, in
   uint64_t wait_bound = kXWaitTicks;
   if (const char* e = getenv("MAPLE_AMD_WAIT_BOUND_US")) wait_bound = static_cast<uint64_t>(atoll(e)) * 100;
   const dim3 grid(kXcds * kXcdWgs), block(512);
+#define MA_XCD_LAUNCH(ADT, NX)                                                                 \
+  do {                                                                                        \
+    if (inter == 768)                                                                         \
+      hipLaunchKernelGGL((k_moe_xcd<4, 3, 3, 16, 2, ADT, NX>), grid, block, 0, st, MA_XCD_ARGS); \
+    else                                                                                      \
+      hipLaunchKernelGGL((k_moe_xcd<4, 2, 2, 16, 2, ADT, NX>), grid, block, 0, st, MA_XCD_ARGS); \
+  } while (0)
   if (alpha_dtype == MA_F32) {
-    if (inter == 768)
-      hipLaunchKernelGGL((k_moe_xcd<4, 3, 3, 16, 2, MA_F32>), grid, block, 0, st, MA_XCD_ARGS);
+    if (nx)
+      MA_XCD_LAUNCH(MA_F32, true);
     else
-      hipLaunchKernelGGL((k_moe_xcd<4, 2, 2, 16, 2, MA_F32>), grid, block, 0, st, MA_XCD_ARGS);
+      MA_XCD_LAUNCH(MA_F32, false);
   } else {
-    if (inter == 768)
-      hipLaunchKernelGGL((k_moe_xcd<4, 3, 3, 16, 2, MA_BF16>), grid, block, 0, st, MA_XCD_ARGS);
+    if (nx)
+      MA_XCD_LAUNCH(MA_BF16, true);
     else
-      hipLaunchKernelGGL((k_moe_xcd<4, 2, 2, 16, 2, MA_BF16>), grid, block, 0, st, MA_XCD_ARGS);
+      MA_XCD_LAUNCH(MA_BF16, false);
   }
+#undef MA_XCD_LAUNCH
 #undef MA_XCD_ARGS
   return check_launch("moe_fused");
 }
