@@ -104,9 +104,10 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
   // carries) for every word of y, laid out so that the LPRH lanes sharing a
   // row read consecutive entries: word w = LPRH-lane l's KWH-th word i sits at
   // column i * LPRH + l
-  __shared__ __align__(16) uint4 ys4[KWH * 2][LPRH];  // 8 bf16 of y per entry
   __shared__ __align__(16) uint32_t pxh[8][NWH], pxl[8][NWH];
-  __shared__ __align__(16) float prr[8][NWH];
+  // per word w and half h: the sum of squares of its raw values 8 h .. + 8,
+  // and its pairs 4 h .. + 4's part of the correction term
+  __shared__ float sq[2][NWH], cq[2][NWH];
   const int klh = lane % LPRH, subh = lane / LPRH;
 
   bool timed_out = false;
@@ -164,9 +165,15 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
       if (t < NWH * 2) {
         const int w = t >> 1, j0 = 4 * (t & 1);
         const int col = (w % KWH) * LPRH + w / KWH;
-        ys4[(w % KWH) * 2 + (t & 1)][w / KWH] =
-            make_uint4(static_cast<uint32_t>(y0[k]), static_cast<uint32_t>(y0[k] >> 32),
-                       static_cast<uint32_t>(y1[k]), static_cast<uint32_t>(y1[k] >> 32));
+        const uint32_t raw[4] = {static_cast<uint32_t>(y0[k]), static_cast<uint32_t>(y0[k] >> 32),
+                                 static_cast<uint32_t>(y1[k]), static_cast<uint32_t>(y1[k] >> 32)};
+        float s2 = 0.f, ch = 0.f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const float v0 = __uint_as_float(raw[m] << 16), v1 = __uint_as_float(raw[m] & 0xffff0000u);
+          s2 += v0 * v0;
+          s2 += v1 * v1;
+        }
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int j = j0 + jj;
@@ -181,41 +188,52 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
           const float r1 = split_hi_lo(f * xb2, hb, lb);
           pxh[j][col] = static_cast<uint32_t>(ha) | (static_cast<uint32_t>(hb) << 16);
           pxl[j][col] = static_cast<uint32_t>(la) | (static_cast<uint32_t>(lb) << 16);
-          prr[j][col] = r0 + r1;
+          ch += ((f + 1.0f) / f) * (r0 + r1);
         }
+        sq[t & 1][w] = s2;
+        cq[t & 1][w] = ch;
       }
     }
   }
   MA_XSTAMP_AT(stamps, 12);  // this thread's part of y seen
   __syncthreads();
-  MA_XSTAMP_AT(stamps, 13);  // y and its x' pairs staged
+  // Per K slice (the KWH words of LPRH-lane l, as the standalone GEMV splits
+  // a row), once for all rows, by wave 0, in the standalone GEMV's order:
+  // the slice's correction term, and the RMS scale from the sum of squares,
+  // each word's two halves added, then the words in order; the sum of
+  // squares reduced over the slices as the standalone GEMV's lanes reduce
+  // it, and kept per lane (the reduction's association differs between
+  // lanes, so lane l's scale may differ from lane 0's in the last bit).
+  __shared__ float s_corr[LPRH], s_rstd[LPRH];
+  if (wv == 0) {
+    const int l = lane % LPRH;
+    float c = 0.f, ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < KWH; ++i) {
+      const int w = l * KWH + i;
+      ss += sq[0][w] + sq[1][w];
+      c += cq[0][w] + cq[1][w];
+    }
+    ss = group_sum<LPRH>(ss);
+    if (lane < LPRH) {
+      s_corr[lane] = c;
+      s_rstd[lane] = rsqrtf(ss / static_cast<float>(NWH * 16) + nx_eps);
+    }
+  }
+  __syncthreads();
+  MA_XSTAMP_AT(stamps, 13);  // y, its x' pairs and the slices' terms staged
   // A wave with no rows of this workgroup is done (nothing below waits for it).
   if (wv * RPIH >= nx_rq) return timed_out;
-  // This lane's slice, in the standalone GEMV's order: sum of squares of
-  // the raw values, then the pairs' correction term.
   uint32_t xh[KWH][8], xl[KWH][8];
-  float c = 0.f, ss = 0.f;
 #pragma unroll
   for (int i = 0; i < KWH; ++i) {
-    const uint4 a0 = ys4[i * 2][klh];
-    const uint4 a1 = ys4[i * 2 + 1][klh];
-    const uint32_t u[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const float v0 = __uint_as_float(u[q] << 16), v1 = __uint_as_float(u[q] & 0xffff0000u);
-      ss += v0 * v0;
-      ss += v1 * v1;
-    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       xh[i][j] = pxh[j][i * LPRH + klh];
       xl[i][j] = pxl[j][i * LPRH + klh];
-      const float f = pair_scale(j);
-      c += ((f + 1.0f) / f) * prr[j][i * LPRH + klh];
     }
   }
-  ss = group_sum<LPRH>(ss);
-  const float rstd = rsqrtf(ss / static_cast<float>(NWH * 16) + nx_eps);
+  const float c = s_corr[klh], rstd = s_rstd[klh];
   const ExpandConsts kc;
 #pragma unroll
   for (int p = 0; p < NXP; ++p) {

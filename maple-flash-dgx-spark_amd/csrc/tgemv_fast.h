@@ -122,9 +122,14 @@ __global__ __launch_bounds__(64) void k_tgemv_fast(
         xs[2 * q + 1] = valid ? __uint_as_float(u[q] & 0xffff0000u) : 0.f;
       }
       if constexpr (RMS) {
+        // per word: the sums over its halves (values 0..7 and 8..15; pairs
+        // 0..3 and 4..7) each in order, then added, then the words in order
+        // -- an order the fused next projection reproduces from per-half
+        // partial sums
+        float s2[2] = {0.f, 0.f}, ch[2] = {0.f, 0.f};
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
-          ss += xs[q] * xs[q];
+          s2[q >> 3] += xs[q] * xs[q];
           xs[q] *= rmsv[i][q];
         }
 #pragma unroll
@@ -135,8 +140,10 @@ __global__ __launch_bounds__(64) void k_tgemv_fast(
           const float rb2 = split_hi_lo(f * xs[j + 8], hb, lb);
           xh[bt][i][j] = static_cast<uint32_t>(ha) | (static_cast<uint32_t>(hb) << 16);
           xl[bt][i][j] = static_cast<uint32_t>(la) | (static_cast<uint32_t>(lb) << 16);
-          c += ((f + 1.0f) / f) * (ra + rb2);
+          ch[j >> 2] += ((f + 1.0f) / f) * (ra + rb2);
         }
+        ss += s2[0] + s2[1];
+        c += ch[0] + ch[1];
       } else {
         c += prep_word_pairs(xs, xh[bt][i]);
       }
