@@ -79,6 +79,28 @@ static_assert(2048 / 2 * 8 <= kXYRegion, "XCD y region");
 #define MA_XSTAMP_AT(row, i) do {} while (0)
 #endif
 
+// The RMS weights a thread of the next projection's x' build multiplies in:
+// thread t < 2 NWH takes values j0 .. j0 + 3 and j0 + 8 .. j0 + 11 of word
+// t / 2 (j0 = 4 (t & 1)); PIT passes of NTH threads.
+template <int PIT>
+struct NxRms {
+  uint64_t wa[PIT][2], wb[PIT][2];
+};
+template <int NWH, int NTH, int PIT = (NWH * 2 + NTH - 1) / NTH>
+__device__ __forceinline__ NxRms<PIT> load_nx_rms(const float* __restrict__ nx_rms, int tid) {
+  NxRms<PIT> r;
+#pragma unroll
+  for (int k = 0; k < PIT; ++k) {
+    const int t = tid + NTH * k < NWH * 2 ? tid + NTH * k : NWH * 2 - 1;
+    const int w = t >> 1, j0 = 4 * (t & 1);
+    r.wa[k][0] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0)[0];
+    r.wa[k][1] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0)[1];
+    r.wb[k][0] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0 + 8)[0];
+    r.wb[k][1] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0 + 8)[1];
+  }
+  return r;
+}
+
 // Next projection, run by every workgroup of a one-launch layer once its rows
 // of y are out: nx_out = ternary_gemv(y, nx_w, nx_alpha, rms_weight = nx_rms)
 // -- reference kernels/ternary_gemv.py:110-146 -- with the standalone fast
@@ -96,7 +118,9 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
                                                 const float (&nxa)[NXP], uint32_t* ws, uint32_t f_old, int G,
                                                 int wg, int tid, int lane, int wv, uint64_t t0,
                                                 const uint64_t* yx = nullptr, uint32_t ytag = 0,
-                                                uint64_t wait_bound = kGridSpin, uint32_t* stamps = nullptr) {
+                                                uint64_t wait_bound = kGridSpin, uint32_t* stamps = nullptr,
+                                                const NxRms<(KWH * LPRH * 2 + 64 * W - 1) / (64 * W)>* rms_pre =
+                                                    nullptr) {
   constexpr int NWH = KWH * LPRH;
   constexpr int NTH = 64 * W;
   constexpr int RPIH = 64 / LPRH;
@@ -121,25 +145,27 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
      // word t / 2 (j0 = 4 (t & 1)), each from values j and j + 8 of the word
      // times their RMS weights
     constexpr int PIT = (NWH * 2 + NTH - 1) / NTH;
-    uint64_t y0[PIT], y1[PIT], ya[PIT], yb[PIT], wa[PIT][2], wb[PIT][2];
+    uint64_t y0[PIT], y1[PIT], ya[PIT], yb[PIT];
+    // the RMS weights: loaded by the caller ahead of time (rms_pre), or here
+    // (issued before the reads of y, so a wait for y also waits for them)
+    const NxRms<PIT> rw = rms_pre ? *rms_pre : load_nx_rms<NWH, NTH>(nx_rms, tid);
 #pragma unroll
     for (int k = 0; k < PIT; ++k) {
-      const int t = tid + NTH * k < NWH * 2 ? tid + NTH * k : NWH * 2 - 1;
+      const bool live = tid + NTH * k < NWH * 2;  // threads past the last word build nothing
+      const int t = live ? tid + NTH * k : NWH * 2 - 1;
       const int w = t >> 1, j0 = 4 * (t & 1);
-      wa[k][0] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0)[0];
-      wa[k][1] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0)[1];
-      wb[k][0] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0 + 8)[0];
-      wb[k][1] = reinterpret_cast<const uint64_t*>(nx_rms + w * 16 + j0 + 8)[1];
       if constexpr (XY) {  // the 16 values of word w: tagged words 8 w .. 8 w + 7
         const CoherentBuf yq(yx, NWH * 8 * 8);
-        uint4 q[4];
+        uint4 q[4] = {};
         for (;;) {
           MA_POLL_RELOAD();
-#pragma unroll
-          for (int i = 0; i < 4; ++i) q[i] = yq.ld4u(static_cast<uint32_t>((8 * w + 2 * i) * 8));
           uint32_t bad = 0;
+          if (live) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) bad |= (q[i].y ^ ytag) | (q[i].w ^ ytag);
+            for (int i = 0; i < 4; ++i) q[i] = yq.ld4u(static_cast<uint32_t>((8 * w + 2 * i) * 8));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bad |= (q[i].y ^ ytag) | (q[i].w ^ ytag);
+          }
           if (__all(bad == 0) || timed_out) break;
           __builtin_amdgcn_s_sleep(1);
           timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > wait_bound;
@@ -179,8 +205,8 @@ __device__ __forceinline__ bool next_projection(const uint16_t* __restrict__ y, 
           const int j = j0 + jj;
           const uint32_t ua = static_cast<uint32_t>(ya[k] >> (16 * jj)) & 0xffffu;
           const uint32_t ub = static_cast<uint32_t>(yb[k] >> (16 * jj)) & 0xffffu;
-          const float ra_w = __uint_as_float(static_cast<uint32_t>(wa[k][jj >> 1] >> (32 * (jj & 1))));
-          const float rb_w = __uint_as_float(static_cast<uint32_t>(wb[k][jj >> 1] >> (32 * (jj & 1))));
+          const float ra_w = __uint_as_float(static_cast<uint32_t>(rw.wa[k][jj >> 1] >> (32 * (jj & 1))));
+          const float rb_w = __uint_as_float(static_cast<uint32_t>(rw.wb[k][jj >> 1] >> (32 * (jj & 1))));
           const float xa = __uint_as_float(ua << 16) * ra_w, xb2 = __uint_as_float(ub << 16) * rb_w;
           const float f = pair_scale(j);
           uint16_t ha, la, hb, lb;

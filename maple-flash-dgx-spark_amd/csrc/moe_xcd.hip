@@ -377,6 +377,10 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   const int nx_rq = nx_w ? (nx_rows + G - 1) / G : 0;
   uint32_t nxw[NXP][KWH];
   uint32_t nxa_raw[NXP] = {};  // converted where used (ld_raw)
+  // and its RMS weights (NX), loaded now: loaded after y, they would hold up
+  // the reads of y (memory counters complete in issue order)
+  NxRms<(NWH * 2 + 64 * W - 1) / (64 * W)> nxr{};
+  if constexpr (NX) nxr = load_nx_rms<NWH, 64 * W>(nx_rms, tid);
   if (NX || nx_w) {
     const int subh = lane / LPRH;
 #pragma unroll
@@ -579,11 +583,11 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     timed_out = next_projection<KWH, LPRH, W, NXP, true>(y, nx_rms, nx_eps, nx_rows, nx_rq, nx_out, nxw, nxa, ws,
                                                          0u, G, wg, tid, lane, wv, t0, yx, tag, wait_bound,
 #ifdef MA_PHASE_STAMPS
-                                                         stamps
+                                                         stamps,
 #else
-                                                         nullptr
+                                                         nullptr,
 #endif
-                                                         ) ||
+                                                         NX ? &nxr : nullptr) ||
                 timed_out;
   }
   if (pf && wv > 0) {  // hold the prefetched lines until they have arrived
