@@ -565,6 +565,18 @@ int ma_argmax_rows(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t 
                    int64_t* out, void* stream);
 
 /*
+ * The same choice, each row read by many workgroups (chunks of 1280 16-byte
+ * vectors; the last one to finish reduces the row's partials): for rows of
+ * 16-byte aligned bf16 / float32 logits up to 64 chunks long; other rows take
+ * ma_argmax_rows.  workspace: ma_argmax_workspace_bytes(rows) bytes, 256-byte
+ * aligned, zero-filled once (every call leaves it zero); calls sharing one
+ * must not overlap.  Same replaced call as ma_argmax_rows.
+ */
+size_t ma_argmax_workspace_bytes(int64_t rows);
+int ma_argmax_rows_ws(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t ldx,
+                      int64_t* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * GEMV over the rows of selected clusters: packed [n_clusters, cluster_size,
  * nwords] (the head's rows grouped by cluster), scales / biases [n_clusters,
  * cluster_size, groups] (bf16 or float32, one dtype), cluster_ids int32

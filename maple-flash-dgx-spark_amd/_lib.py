@@ -75,6 +75,8 @@ _SIGNATURES = {
     "ma_moe_route": [_P, _P, _L, _L, _P, _I, _F, _P, _P, _L, _I, _P, _P, _P, _P, _P, _P, _P, _P,
                      _P, _P, _P, _Z, _P],
     "ma_argmax_rows": [_P, _I, _L, _L, _L, _P, _P],
+    "ma_argmax_workspace_bytes": [_L],
+    "ma_argmax_rows_ws": [_P, _I, _L, _L, _L, _P, _P, _Z, _P],
     "ma_ternarize": [_P, _I, _L, _L, _F, _P, _P, _P],
     "ma_ternary_gemv_combine_ws": [_P, _P, _P, _L, _P, _P, _L, _P, _L, _L, _P, _I, _P, _I, _F, _P, _L,
                                    _P, _Z, _P],
@@ -92,7 +94,7 @@ _SIGNATURES = {
 }
 _RESTYPES = {"ma_last_error": ctypes.c_char_p, "ma_router_workspace_bytes": _Z,
              "ma_ternary_gemv_workspace_bytes": _Z,
-             "ma_grouped_workspace_bytes": _Z, "ma_gqa_workspace_bytes": _Z,
+             "ma_grouped_workspace_bytes": _Z, "ma_gqa_workspace_bytes": _Z, "ma_argmax_workspace_bytes": _Z,
              "ma_moe_fused_workspace_bytes": _Z, "ma_moe_route_workspace_bytes": _Z,
              "ma_moe_grouped_noalloc_max_bytes": _Z, "ma_sampler_workspace_bytes": _Z,
              "ma_flash_head_workspace_bytes": _Z, "ma_rtn4_gemv_workspace_bytes": _Z}

@@ -8,6 +8,7 @@
 // 16-byte aligned take a scalar loop).  NaN logits are
 // not expected (the reference's output would be its own NaN handling).
 #include "common.h"
+#include "grid_sync.h"
 
 namespace ma {
 
@@ -117,13 +118,141 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_rows(const void* __re
     float v = lane < kArgmaxThreads / 64 ? sv[lane] : -INFINITY;
     int64_t i = lane < kArgmaxThreads / 64 ? si[lane] : n;
     wave_argmax(v, i);
-    if (lane == 0) out[row] = i < n ? i : 0;
+    if (lane == 0) out[row] = i < n && v != -INFINITY ? i : 0;  // every value -inf: index 0, as torch
+  }
+}
+
+// Split form (ma_argmax_rows_ws): kSplitChunk-vector chunks of a row, one
+// 256-thread workgroup each (every load of a chunk in flight at once), so a
+// row is read by many CUs instead of one.  Each workgroup stores its chunk's
+// (value, index) -- the larger value, the lower index on ties, as above --
+// with the device-coherent policy, then takes a ticket on the row's counter;
+// the workgroup that takes the last one reduces the row's partials in chunk
+// order, writes out[row] and clears the counter (the workspace starts and
+// ends every call zero; calls on one workspace must not overlap).  The last
+// chunk also takes the elements past the last whole vector.
+constexpr int kSplitThreads = 256, kSplitU = 5, kSplitChunk = kSplitThreads * kSplitU;
+constexpr int kSplitMaxChunks = 64;  // per row (rows of up to 64 x 1280 vectors)
+constexpr size_t kSplitRowBytes = 256 + kSplitMaxChunks * 16;  // counter line + partials
+
+template <int DT>
+__global__ __launch_bounds__(kSplitThreads) void k_argmax_split(const void* __restrict__ x, int64_t n,
+                                                                int64_t ldx, int64_t* __restrict__ out,
+                                                                uint8_t* __restrict__ ws) {
+  __shared__ float sv[kSplitThreads / 64];
+  __shared__ int64_t si[kSplitThreads / 64];
+  __shared__ int last;
+  constexpr int PER = DT == MA_BF16 ? 8 : 4;
+  const int64_t row = blockIdx.y;
+  const int g = blockIdx.x, G = gridDim.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t nvec = n / PER;
+  const uint4* p = reinterpret_cast<const uint4*>(static_cast<const char*>(x) +
+                                                  row * ldx * (DT == MA_BF16 ? 2 : 4));
+  constexpr uint32_t kNegInf4 = DT == MA_BF16 ? 0xff80ff80u : 0xff800000u;
+  const int64_t c0 = static_cast<int64_t>(g) * kSplitChunk;
+  uint4 q[kSplitU];
+#pragma unroll
+  for (int u = 0; u < kSplitU; ++u) {
+    const int64_t vi = c0 + tid + kSplitThreads * u;
+    q[u] = vi < nvec ? p[vi] : make_uint4(kNegInf4, kNegInf4, kNegInf4, kNegInf4);
+  }
+  float best = -INFINITY;
+  int64_t bv = -1;
+#pragma unroll
+  for (int u = 0; u < kSplitU; ++u) {
+    const int64_t vi = c0 + tid + kSplitThreads * u;
+    const float m = vec_max<DT>(q[u]);
+    if (m > best && vi < nvec) {
+      best = m;
+      bv = vi;
+    }
+  }
+  int64_t bi = n;
+  if (bv >= 0) {  // the lowest index of the winning vector holding the maximum
+    float f[PER];
+    vec_unpack<DT>(p[bv], f);
+    int e = PER - 1;
+#pragma unroll
+    for (int k = PER - 1; k >= 0; --k)
+      if (f[k] == best) e = k;
+    bi = bv * PER + e;
+  }
+  if (g == G - 1) {
+    for (int64_t k = nvec * PER + tid; k < n; k += kSplitThreads) {
+      const float f = DT == MA_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(x)[row * ldx + k])
+                                    : static_cast<const float*>(x)[row * ldx + k];
+      take_better(best, bi, f, k);
+    }
+  }
+  wave_argmax(best, bi);
+  if (lane == 0) {
+    sv[wv] = best;
+    si[wv] = bi;
+  }
+  __syncthreads();
+  uint8_t* const rw = ws + row * kSplitRowBytes;
+  uint32_t* const counter = reinterpret_cast<uint32_t*>(rw);
+  uint64_t* const part = reinterpret_cast<uint64_t*>(rw + 256);  // [chunk] (index, value bits)
+  if (tid == 0) {
+    float v = sv[0];
+    int64_t i = si[0];
+    for (int w = 1; w < kSplitThreads / 64; ++w) take_better(v, i, sv[w], si[w]);
+    st_coh64(&part[2 * g], static_cast<uint64_t>(i));
+    st_coh64(&part[2 * g + 1], __float_as_uint(v));
+    __builtin_amdgcn_s_waitcnt(0);  // the partial has completed before the ticket
+    last = atomicAdd(counter, 1u) == static_cast<uint32_t>(G - 1);
+  }
+  __syncthreads();
+  if (!last || wv != 0) return;
+  float v = -INFINITY;
+  int64_t i = n;
+  for (int c = lane; c < G; c += 64) {  // lane order within a chunk round, then the exchanges
+    const float vc = __uint_as_float(static_cast<uint32_t>(ld_coh64(&part[2 * c + 1])));
+    const int64_t ic = static_cast<int64_t>(ld_coh64(&part[2 * c]));
+    take_better(v, i, vc, ic);
+  }
+  wave_argmax(v, i);
+  if (lane == 0) {
+    out[row] = i < n && v != -INFINITY ? i : 0;  // every value -inf: index 0, as torch
+    st_coh32(counter, 0u);
   }
 }
 
 }  // namespace ma
 
 using namespace ma;
+
+extern "C" size_t ma_argmax_workspace_bytes(int64_t rows) {
+  return rows > 0 ? static_cast<size_t>(rows) * kSplitRowBytes : 0;
+}
+
+extern "C" int ma_argmax_rows_ws(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t ldx,
+                                 int64_t* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (rows < 0 || n < 1 || ldx < n) return fail(MA_EVALUE, "argmax_rows_ws: bad sizes");
+  if (x_dtype != MA_BF16 && x_dtype != MA_F32)
+    return fail(MA_ETYPE, "argmax_rows_ws: dtype %d unsupported", x_dtype);
+  if (rows == 0) return MA_OK;
+  const int per = x_dtype == MA_BF16 ? 8 : 4;
+  const int vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % per == 0;
+  const int64_t chunks = cdiv(n / per, kSplitChunk);
+  // rows the split form does not take (not 16-byte aligned, or too long):
+  // the one-workgroup form
+  if (!vec || chunks < 1 || chunks > kSplitMaxChunks) return ma_argmax_rows(x, x_dtype, rows, n, ldx, out, stream);
+  if (!workspace || workspace_bytes < ma_argmax_workspace_bytes(rows) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 255))
+    return fail(MA_EVALUE, "argmax_rows_ws: workspace must be %zu bytes, 256-byte aligned",
+                ma_argmax_workspace_bytes(rows));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(rows));
+  if (x_dtype == MA_BF16)
+    hipLaunchKernelGGL(k_argmax_split<MA_BF16>, grid, dim3(kSplitThreads), 0, s, x, n, ldx, out,
+                       static_cast<uint8_t*>(workspace));
+  else
+    hipLaunchKernelGGL(k_argmax_split<MA_F32>, grid, dim3(kSplitThreads), 0, s, x, n, ldx, out,
+                       static_cast<uint8_t*>(workspace));
+  return check_launch("argmax_rows_ws");
+}
 
 extern "C" int ma_argmax_rows(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t ldx,
                               int64_t* out, void* stream) {

@@ -495,6 +495,44 @@ def test_greedy_argmax_ties_within_and_across_vectors(dev, dtype):
     assert got.tolist()[:3] == [8 * per + 1, 7 * per + per - 1, 17 * per + 2]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_greedy_argmax_split_rows_equal_one_workgroup_form(dev, dtype):
+    """greedy_argmax reads each row in chunks of 1280 vectors, one
+    workgroup each, the last to finish reducing the partials: ties across
+    chunks go to the lower index, the maximum may sit on a chunk's last
+    element or in the elements past the last whole vector (a row of 151939
+    values at stride 151944), and three calls in a row on one workspace give
+    the one-workgroup ma_argmax_rows's ids and torch.argmax's."""
+    from maple_amd import _lib
+    from maple_amd.kernels import greedy_argmax
+
+    per = 8 if dtype == torch.bfloat16 else 4
+    chunk = 1280 * per
+    n, ld = 151939, 151944
+    g = torch.Generator(device=dev).manual_seed(5)
+    base = torch.randn(6, ld, generator=g, device=dev).to(dtype)
+    x = base[:, :n]
+    x[0, 5 * chunk + 7] = 9.0
+    x[0, 2 * chunk + 100] = 9.0  # an earlier chunk, same value
+    x[1, 3 * chunk - 1] = 9.0  # the last element of chunk 2
+    x[2, n - 2] = 9.0  # past the last whole vector
+    x[3] = -float("inf")
+    x[4, 0] = 9.0
+    x[4, n - 1] = 9.0
+    want = torch.argmax(x.float(), dim=-1)
+    one = torch.empty(6, dtype=torch.int64, device=dev)
+    _lib.call("ma_argmax_rows", _lib.ptr(x), _lib.dtype_code(x, "logits"), 6, n, x.stride(0), _lib.ptr(one),
+              _lib.stream_of(x))
+    for _ in range(3):
+        got = greedy_argmax(x)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want) and torch.equal(got, one)
+    assert got.tolist()[:5] == [2 * chunk + 100, 3 * chunk - 1, n - 2, 0, 0]
+    # a row stride that is not a whole number of vectors takes the one-workgroup form
+    y = torch.randn(2, 1001 * per + 1, generator=g, device=dev).to(dtype)[:, :1001 * per - 3]
+    assert torch.equal(greedy_argmax(y), torch.argmax(y.float(), dim=-1))
+
+
 @pytest.mark.parametrize("n", [1024, 4096, 20000])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_greedy_argmax_all_negative_short_rows(dev, n, dtype):
