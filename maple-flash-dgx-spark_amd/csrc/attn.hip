@@ -71,6 +71,28 @@ __device__ __forceinline__ float2 rope_coeffs(const RopeSrc& r, int64_t b, int64
                      bf16_to_f32(f32_to_bf16(ld_f(r.sin, r.dt, row * r.ld + dd))));
 }
 
+// rope_coeffs in two steps for the attention's prologue: the raw words,
+// loaded whether or not RoPE is on (from ``safe``, any readable 4-byte
+// aligned address, when it is off), then their conversion -- the same
+// values, with the loads issued together and no wait until the use.
+struct RopeWords {
+  AnyWord c, s;
+};
+__device__ __forceinline__ RopeWords rope_words(const RopeSrc& r, int64_t b, int64_t pos, int e,
+                                                const void* safe) {
+  const bool on = r.use_rope && r.rot > 0;
+  const int d = (threadIdx.x & 63) + 64 * e;
+  const int64_t row = r.n_pos > 0 ? (pos < r.n_pos ? pos : r.n_pos - 1) : b;
+  const int64_t i = on ? row * r.ld + (d < r.rot ? d : 0) : 0;
+  const int dt = on ? r.dt : MA_F32;
+  return {ld_any_word(on ? r.cos : safe, dt, i), ld_any_word(on ? r.sin : safe, dt, i)};
+}
+__device__ __forceinline__ float2 rope_of_words(const RopeSrc& r, const RopeWords& w) {
+  if (!r.use_rope || r.rot <= 0) return make_float2(1.f, 0.f);
+  return make_float2(bf16_to_f32(f32_to_bf16(any_word_f(w.c, r.dt))),
+                     bf16_to_f32(f32_to_bf16(any_word_f(w.s, r.dt))));
+}
+
 // RMSNorm of one head held wave-wide (lane owns dims lane + 64 e), then
 // rotate-half RoPE on the first ``rot`` dims with the lane's coefficients.
 template <int E>
@@ -105,6 +127,19 @@ __device__ __forceinline__ void norm_rope_lane(float (&y)[E], const float (&x)[E
       if (d < r.rot) y[e] = d < half ? y[e] * cs[e].x - other[e] * cs[e].y : y[e] * cs[e].x + other[e] * cs[e].y;
     }
   }
+}
+
+// Two wave-uniform 8-byte values read with scalar loads issued back to back
+// and one wait for both.
+__device__ __forceinline__ void ld_scalar_pair(const int64_t* a, const int64_t* b, int64_t& va,
+                                               int64_t& vb) {
+  asm volatile(
+      "s_load_dwordx2 %0, %2, 0x0\n\t"
+      "s_load_dwordx2 %1, %3, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(va), "=&s"(vb)
+      : "s"(a), "s"(b)
+      : "memory");
 }
 
 __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
@@ -211,15 +246,17 @@ __device__ __forceinline__ uint32_t sel32(bool c, uint32_t a, uint32_t b) { retu
 // dispatch order, so they are resident together when S workgroups fit on one
 // XCD.
 template <bool FUSED, int HD, bool XL>
+// (The arguments the prologue's first loads need come first: the first 14
+// dwords arrive preloaded in SGPRs, the rest are read from memory.)
 __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
-    const uint16_t* __restrict__ src, int64_t ldq, const void* __restrict__ qn_w,
-    const void* __restrict__ kn_w, int w_dt, RopeSrc rope, float eps,
-    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, int64_t cache_rows,
-    int64_t max_len, const int64_t* __restrict__ seqlen, const int64_t* __restrict__ row_map,
-    int nq, int nkv, int64_t window, float scale, int max_splits, uint32_t* __restrict__ sync,
+    const int64_t* __restrict__ seqlen, const int64_t* __restrict__ row_map,
+    const uint16_t* __restrict__ src, int64_t ldq, int nq, int nkv, int n_rows, int xl_splits,
+    int64_t max_len, const void* __restrict__ qn_w, const void* __restrict__ kn_w, int w_dt,
+    RopeSrc rope, float eps, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+    int64_t cache_rows, int64_t window, float scale, int max_splits, uint32_t* __restrict__ sync,
     float* __restrict__ part_acc, float* __restrict__ part_ml, uint16_t* __restrict__ out,
     const uint32_t* __restrict__ o_w, const void* __restrict__ o_alpha, int o_alpha_dt, int o_rows,
-    uint16_t* __restrict__ o_out, int n_rows, int xl_splits) {
+    uint16_t* __restrict__ o_out) {
   constexpr int E = HD / 64;   // dims per lane in the wave-wide head layouts
   constexpr int KS = HD / 32;  // 32-dim slices of K per score MFMA chain
   constexpr int NB = HD / 16;  // 16-dim output blocks of P.V
@@ -230,6 +267,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   __shared__ float wm[4][kMaxGroup], wl[4][kMaxGroup];
   __shared__ float hm[kMaxGroup], hl[kMaxGroup];
   __shared__ __align__(16) uint4 os4[kOWords * 2][32];  // O projection input
+  // The arguments past the preloaded ones that the prologue needs, read at
+  // once with one wait: left to itself the compiler read each where first
+  // used, a wait each (six dependent scalar round trips before the first
+  // K/V load).
+  asm volatile("" ::"s"(qn_w), "s"(kn_w), "s"(w_dt), "s"(rope.cos), "s"(rope.sin), "s"(rope.dt),
+               "s"(rope.ld), "s"(rope.n_pos), "s"(rope.rot), "s"(rope.use_rope), "s"(eps),
+               "s"(k_cache), "s"(v_cache), "s"(cache_rows), "s"(window), "s"(sync), "s"(o_w),
+               "s"(o_rows), "s"(max_splits));
   // (split, KV head, row) of this workgroup; the grid's split count; its
   // index and size for the O projection's barrier
   int sp, kvh, S, wgl, n_wg;
@@ -257,11 +302,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g = lane >> 4;
   const int group = nq / nkv;
-  // This pair's barrier words; the generation is read before this split can
-  // arrive, so it is the value the last arriver will advance.
+  // This pair's barrier words.
   uint32_t* const arrive = sync + kSyncLine * (1 + 2 * (b * nkv + kvh));
   uint32_t* const gen = arrive + kSyncLine;
-  const uint32_t g0 = wv == 0 ? __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   // O projection in the same launch (batch 1): a barrier over every workgroup
   // of the launch on the sync area's last 33 lines, then each workgroup
@@ -285,17 +328,63 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       ow_a[p] = ld_f(o_alpha, o_alpha_dt, r);
     }
   };
-  const int64_t pos = clamp64(seqlen[b], 0, max_len - 1);
+  auto attend = [&]() {
+  // The prologue's position-independent loads go out first, before the
+  // position is read: q's heads (fused: also the new K/V row's elements and
+  // the norm weights), as raw values from in-bounds addresses (heads past
+  // the group read head 0 and are dropped), converted only once the
+  // position-dependent loads (the RoPE rows, the first K/V chunk) are out
+  // too.  A load under a condition or a dtype switch would get a wait of its
+  // own right behind it: a chain of round trips before q is ready.
+  uint16_t xq[kMaxGroup / 4][E];                  // fused: head wv + 4 i, dims lane + 64 e
+  uint16_t xkv[E];                                // fused: the new K (wave 0) or V (wave 1) row
+  AnyWord wqr[E], wkr[E];                         // fused: the norm weights
+  uint16_t xqf[kMaxGroup * HD / kAttnThreads];    // not fused: q element tid + kAttnThreads k
+  if constexpr (FUSED) {
+    const uint16_t* row = src + b * ldq;
+#pragma unroll
+    for (int i = 0; i < kMaxGroup / 4; ++i) {
+      const int hh = wv + 4 * i, hc = hh < group ? hh : 0;
+#pragma unroll
+      for (int e = 0; e < E; ++e) xq[i][e] = row[(kvh * group + hc) * HD + lane + 64 * e];
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      xkv[e] = row[(nq + kvh + (wv == 1 ? nkv : 0)) * HD + lane + 64 * e];
+      wqr[e] = ld_any_word(qn_w, w_dt, lane + 64 * e);
+      wkr[e] = ld_any_word(kn_w, w_dt, lane + 64 * e);
+    }
+  } else {
+    const uint16_t* qsrc = src + (b * nq + kvh * group) * HD;
+#pragma unroll
+    for (int k = 0; k < kMaxGroup * HD / kAttnThreads; ++k) {
+      const int i = tid + kAttnThreads * k;
+      xqf[k] = qsrc[i / HD < group ? i : i % HD];
+    }
+  }
+  MA_ISSUE_FENCE();
+  // the cache row and the position: two scalar loads issued together, then
+  // one wait (the row map's from a valid address either way; left to the
+  // compiler, the second load went out only after the first had returned)
+  int64_t rmv, slv;
+  ld_scalar_pair(row_map ? row_map + b : seqlen + b, seqlen + b, rmv, slv);
+  // The pair's generation, read before this split can arrive (so it is the
+  // value the last arriver will advance) and after the prologue's loads are
+  // out; by every wave, though wave 0 alone uses it (under a wave condition
+  // the load got its wait right behind it).
+  const uint32_t g0 = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int64_t pos = clamp64(slv, 0, max_len - 1);
+  const int64_t crow = row_map ? clamp64(rmv, 0, cache_rows - 1) : b;
   const int64_t kv_len = pos + 1;
   const int64_t start = (window > 0 && kv_len > window) ? kv_len - window : 0;
   const int n_chunks = static_cast<int>(cdiv(kv_len - start, kSplit));
-  const int cps = static_cast<int>(cdiv(n_chunks, S));  // chunks per split
-  const int n_spl = static_cast<int>(cdiv(n_chunks, cps));
+  // (32-bit divisions: the 64-bit ones are long scalar sequences on the
+  // path to the first K/V load)
+  const int cps = static_cast<int>((static_cast<uint32_t>(n_chunks) + S - 1) / static_cast<uint32_t>(S));
+  const int n_spl = static_cast<int>((static_cast<uint32_t>(n_chunks) + cps - 1) / static_cast<uint32_t>(cps));
   const float scale2 = scale * 1.44269504088896341f;  // log2(e): maxima and sums in base 2
-  auto attend = [&]() {
   const int c_beg = sp * cps;
   const int c_end = c_beg + cps < n_chunks ? c_beg + cps : n_chunks;
-  const int64_t crow = row_map ? clamp64(row_map[b], 0, cache_rows - 1) : b;
   const int64_t base = (crow * nkv + kvh) * max_len;
   const bool owns_pos = FUSED && sp == n_spl - 1;
 
@@ -328,36 +417,31 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     // Every load of the prologue is issued before any of them is used, and
     // before the first chunk's (memory counters complete in issue order, so
     // q would otherwise wait for the K/V chunk).
-    const uint16_t* row = src + b * ldq;
-    uint16_t xq[kMaxGroup / 4][E];
+    RopeWords rw[E];
 #pragma unroll
-    for (int i = 0; i < kMaxGroup / 4; ++i) {
-      const int hh = wv + 4 * i;
-#pragma unroll
-      for (int e = 0; e < E; ++e)
-        xq[i][e] = hh < group ? row[(kvh * group + hh) * HD + lane + 64 * e] : uint16_t(0);
-    }
-    uint16_t xkv[E];
+    for (int e = 0; e < E; ++e) rw[e] = rope_words(rope, b, pos, e, qn_w);  // qn_w: read above
+    load_chunk(c_beg, kf, vr);
     float wq[E], wk[E];
     float2 cs[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      xkv[e] = owns_pos && wv < 2 ? row[(nq + kvh + (wv ? nkv : 0)) * HD + lane + 64 * e] : uint16_t(0);
-      wq[e] = ld_f(qn_w, w_dt, lane + 64 * e);
-      wk[e] = ld_f(kn_w, w_dt, lane + 64 * e);
-      cs[e] = rope_coeffs(rope, b, pos, e);
+      wq[e] = any_word_f(wqr[e], w_dt);
+      wk[e] = any_word_f(wkr[e], w_dt);
+      cs[e] = rope_of_words(rope, rw[e]);
     }
-    load_chunk(c_beg, kf, vr);
 #pragma unroll
     for (int i = 0; i < kMaxGroup / 4; ++i) {
       const int hh = wv + 4 * i;
-      if (hh < kMaxGroup) {
+      if (hh < group) {  // (rows past the group only need zeros)
         float xf[E], yf[E];
 #pragma unroll
         for (int e = 0; e < E; ++e) xf[e] = bf16_to_f32(xq[i][e]);
         norm_rope_lane<E>(yf, xf, wq, cs, rope, eps);
 #pragma unroll
-        for (int e = 0; e < E; ++e) qs[hh][lane + 64 * e] = hh < group ? f32_to_bf16(yf[e]) : uint16_t(0);
+        for (int e = 0; e < E; ++e) qs[hh][lane + 64 * e] = f32_to_bf16(yf[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) qs[hh][lane + 64 * e] = uint16_t(0);
       }
     }
     if (owns_pos && wv < 2) {
@@ -376,21 +460,21 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
       for (int e = 0; e < E; ++e) kvnew[wv][lane + 64 * e] = new_kv[e];
     }
   } else {
-    const uint16_t* qsrc = src + (b * nq + kvh * group) * HD;
-    uint16_t xq[kMaxGroup * HD / kAttnThreads];
-#pragma unroll
-    for (int k = 0; k < kMaxGroup * HD / kAttnThreads; ++k) {
-      const int i = tid + kAttnThreads * k;
-      xq[k] = i / HD < group ? qsrc[i] : uint16_t(0);
-    }
     load_chunk(c_beg, kf, vr);
 #pragma unroll
     for (int k = 0; k < kMaxGroup * HD / kAttnThreads; ++k) {
       const int i = tid + kAttnThreads * k;
-      qs[i / HD][i % HD] = xq[k];
+      qs[i / HD][i % HD] = i / HD < group ? xqf[k] : uint16_t(0);
     }
   }
   __syncthreads();
+  // Splits past the last chunk ran the prologue too (its loads stay in one
+  // block with their uses, so the compiler does not sink them behind the
+  // position's wait), and stop here.
+  if (sp >= n_spl) {
+    if (o_w) o_prefetch();
+    return;
+  }
   uint4 qf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const uint4*>(&qs[r16][8 * g + 32 * ks]);
@@ -681,7 +765,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_decode_attn(
     }
   }
   };
-  if (active && sp < n_spl)
+  if (active)
     attend();
   else if (o_w)
     o_prefetch();
@@ -927,11 +1011,11 @@ static int launch_attn(bool fused, const void* src, int64_t ldq, const void* qn_
       return fail(MA_ETYPE, "%s: O projection alpha dtype %d", what, o_alpha_dt);
   }
 #define MA_ATTN_ARGS                                                                            \
-  static_cast<const uint16_t*>(src), ldq, qn_w, kn_w, w_dt, rope, eps,                          \
-      static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), cache_rows, max_len,    \
-      seqlen, row_map, nq, nkv, window, scale, static_cast<int>(max_splits), sync, acc, ml,   \
-      static_cast<uint16_t*>(out), o_w, o_alpha, o_alpha_dt, static_cast<int>(o_rows),         \
-      static_cast<uint16_t*>(o_out), static_cast<int>(batch), static_cast<int>(grid_splits)
+  seqlen, row_map, static_cast<const uint16_t*>(src), ldq, nq, nkv, static_cast<int>(batch),   \
+      static_cast<int>(grid_splits), max_len, qn_w, kn_w, w_dt, rope, eps,                      \
+      static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), cache_rows, window,     \
+      scale, static_cast<int>(max_splits), sync, acc, ml, static_cast<uint16_t*>(out), o_w,     \
+      o_alpha, o_alpha_dt, static_cast<int>(o_rows), static_cast<uint16_t*>(o_out)
 #define MA_ATTN_LAUNCH(F, H)                                                                      \
   do {                                                                                          \
     if (xl)                                                                                     \

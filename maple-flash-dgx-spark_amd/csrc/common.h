@@ -78,6 +78,30 @@ __device__ __forceinline__ float from_raw(uint32_t u) {
   else return __uint_as_float(u);
 }
 
+// Element i of a float32, bf16 or f16 array whose dtype is known only at run
+// time, read as the aligned 32-bit word that holds it: one unconditional
+// load with no dtype branch around it (a 16-bit element's neighbour comes
+// along; an aligned word never crosses a page, so it is as safe to read as
+// the element).  any_word_f() converts it where the value is used.  With
+// ld_f the load sits in a dtype branch and its conversion, with the wait for
+// it, right behind it, so a run of such loads costs a round trip each.
+struct AnyWord {
+  uint32_t w;
+  uint32_t sh;  // 16 for an element in the upper half of the word, else 0
+};
+__device__ __forceinline__ AnyWord ld_any_word(const void* p, int dt, int64_t i) {
+  // pointer arithmetic (not an integer round trip) keeps the global address
+  // space known, so this is a global load rather than a flat one
+  const char* const e = static_cast<const char*>(p) + i * (dt == MA_F32 ? 4 : 2);
+  const uint32_t mis = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(e)) & 3u;
+  return {*reinterpret_cast<const uint32_t*>(e - mis), mis * 8u};
+}
+__device__ __forceinline__ float any_word_f(AnyWord v, int dt) {
+  const uint32_t h = (v.w >> v.sh) & 0xffffu;
+  const float f16 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+  return dt == MA_F32 ? __uint_as_float(v.w) : (dt == MA_BF16 ? __uint_as_float(h << 16) : f16);
+}
+
 __device__ __forceinline__ float ld_f(const void* p, int dt, int64_t i) {
   switch (dt) {
     case MA_BF16: return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
