@@ -73,6 +73,7 @@ constexpr uint64_t kXWaitTicks = 20000;
 // Prefetch: 16-byte units per prefetching lane (7 waves x 32 workgroups of
 // an XCD x 2 = 28,672 units = 448 KB, more than a router of 64 x 2048 bf16)
 constexpr int kPfPerLane = 2;
+constexpr int kXHasO = 0x100;  // k_moe_xcd's mode: the O projection in front
 
 // Shapes: H = 16 * KWH * LPRH with LPRH = 32 (one up/gate row pair per
 // SwiGLU pass), I = 16 * KWI * LPRI, US SwiGLU outputs and UD down passes
@@ -80,14 +81,18 @@ constexpr int kPfPerLane = 2;
 // top-8; ADT the row scales' dtype; NX: the instance launched with a next
 // projection (nx_w set).
 template <int KWH, int US, int KWI, int LPRI, int UD, int ADT, bool NX>
+//
+// The arguments the first loads need come first (the first 14 dwords arrive
+// preloaded in SGPRs); mode = the norm weights' dtype | kXHasO with the O
+// projection in front.
 __global__ __launch_bounds__(512) void k_moe_xcd(
-    const uint16_t* __restrict__ xa, const uint16_t* __restrict__ xb,
-    const void* __restrict__ norm_w, int norm_dt, float eps, const uint16_t* __restrict__ residual,
-    const uint16_t* __restrict__ gate_w, const float* __restrict__ bias, int n_exp,
+    const uint16_t* __restrict__ xa, uint32_t* __restrict__ ws, const uint16_t* __restrict__ gate_w,
+    const uint16_t* __restrict__ residual, const uint16_t* __restrict__ xb, const void* __restrict__ norm_w,
+    int n_exp, int mode, float eps, const float* __restrict__ bias,
     const uint32_t* __restrict__ ug, const void* __restrict__ ug_alpha,
     const uint32_t* __restrict__ dn, const void* __restrict__ dn_alpha,
     uint16_t* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ wts_out,
-    uint32_t* __restrict__ ws, const uint32_t* __restrict__ nx_w, const void* __restrict__ nx_alpha,
+    const uint32_t* __restrict__ nx_w, const void* __restrict__ nx_alpha,
     const float* __restrict__ nx_rms, float nx_eps, int nx_rows,
     uint16_t* __restrict__ nx_out, const uint16_t* __restrict__ attn, const uint32_t* __restrict__ o_w,
     const void* __restrict__ o_alpha, const uint4* __restrict__ pf, int pf_units, uint64_t wait_bound) {
@@ -130,8 +135,10 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   uint64_t* const part = reinterpret_cast<uint64_t*>(wsb + kXPartOff);
   uint64_t* const yx = reinterpret_cast<uint64_t*>(wsb + kXYOff + xcd * kXYRegion);
   uint64_t* const ox = reinterpret_cast<uint64_t*>(wsb + kXOOff + xcd * kXYRegion);
-  const uint32_t tag = ld_coh32(calls) + 1u;
-  const uint32_t tag16 = tag & 0xffffu;
+  // This call's tag is the count + 1, formed where it is first needed (after
+  // x is staged): formed here, it made every wave wait for this load before
+  // requesting x.
+  uint32_t tag_raw = ld_coh32(calls);
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   bool timed_out = false;
   // the layout check: this call's tag into the slot of (this XCD, this
@@ -148,12 +155,14 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   // The residual of the y rows this workgroup finishes (wave 0): rows
   // 64 lw + lane with a next projection (every XCD combines all of y), else
   // rows wg * FR + lane, lanes < FR.
-  const int ro = nx_w ? 64 * lw + lane : wg * FR + (lane < FR ? lane : 0);
-  const bool addp = xb || o_w;  // x + (add or the O projection), then RMSNorm
+  const int ro = NX ? 64 * lw + lane : wg * FR + (lane < FR ? lane : 0);
+  const int norm_dt = mode & 0xff;
+  const bool has_o = (mode & kXHasO) != 0;
+  const bool addp = xb || has_o;  // x + (add or the O projection), then RMSNorm
   const uint16_t* const res_a = addp ? xa : (residual ? residual : xa);
   const uint16_t* const res_b = xb ? xb : xa;
   const uint32_t ra = res_a[ro];
-  uint32_t rb = o_w ? 0u : res_b[ro];  // with the O projection: from the XCD's copy of o, below
+  uint32_t rb = has_o ? 0u : res_b[ro];  // with the O projection: from the XCD's copy of o, below
 
   // ---- 1. x (optionally add + RMSNorm) staged once per workgroup: thread
   // t < NWH takes word t, in bf16 (for the router waves) and as x' pairs (for
@@ -170,6 +179,34 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       gr[i][1] = gp[1];
     }
   }
+  // x, its addend and the norm weights requested now, ahead of everything
+  // that needs an argument read from memory (the word of x of thread t <
+  // NWH; the addend and the weights only with an add in front, the weights
+  // from an address that their dtype selects, not from a dtype branch)
+  static_assert(NWH <= 512, "one word of x per thread");
+  const int wc = tid < NWH ? tid : NWH - 1;
+  const uint4 xa0 = reinterpret_cast<const uint4*>(xa + wc * 16)[0];
+  const uint4 xa1 = reinterpret_cast<const uint4*>(xa + wc * 16)[1];
+  uint4 xb0 = make_uint4(0u, 0u, 0u, 0u), xb1 = xb0, nw0 = xb0, nw1 = xb0, nw2 = xb0, nw3 = xb0;
+  const bool nf32 = norm_dt == MA_F32;
+  if (xb) {
+    xb0 = reinterpret_cast<const uint4*>(xb + wc * 16)[0];
+    xb1 = reinterpret_cast<const uint4*>(xb + wc * 16)[1];
+  }
+  if (addp) {  // f32: 4 x 16 bytes per word of x; bf16: 2 x 16 (loaded twice)
+    const uint4* const np = reinterpret_cast<const uint4*>(static_cast<const char*>(norm_w) + wc * (nf32 ? 64 : 32));
+    nw0 = np[0];
+    nw1 = np[1];
+    nw2 = np[nf32 ? 2 : 0];
+    nw3 = np[nf32 ? 3 : 1];
+  }
+  // The other arguments the layer reads before its expert loads, read at
+  // once with one wait (left to itself, the compiler read each where first
+  // used, a wait each).
+  asm volatile("" ::"s"(eps), "s"(bias), "s"(ug), "s"(ug_alpha), "s"(dn), "s"(dn_alpha), "s"(nx_w),
+               "s"(pf), "s"(pf_units), "s"(wait_bound)
+               : "memory");
+
   // ---- 0. the O projection (optional): o = ternary_gemv(attn, o_w, o_alpha)
   // with the standalone fast GEMV's per-lane arithmetic (so the same bits);
   // every XCD computes all of o (wave w of workgroup j: rows 64 j + 8 w ..
@@ -177,7 +214,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
   // bf16 values per tagged word, as y below.
   __shared__ __align__(16) uint32_t os[NWH][8];
   __shared__ float oc[NWH];
-  if (o_w) {
+  if (has_o) {
     const int okl = lane % LPRH, osub = lane / LPRH;
     constexpr int OP = 64 / (W * RPIH);  // passes of RPIH rows per wave
     uint32_t wo[OP][KWH];
@@ -199,17 +236,13 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
       const uint32_t bits = f32_to_bf16(d);
       const uint32_t odd = __shfl(bits, LPRH, 64);  // row r + 1, held by lane LPRH
       const int r = 64 * lw + (64 / W) * wv + RPIH * p;
-      if (lane == 0) st_l2_64(&ox[r >> 1], (static_cast<uint64_t>(tag) << 32) | bits | (odd << 16));
+      if (lane == 0) st_l2_64(&ox[r >> 1], (static_cast<uint64_t>(tag_raw + 1u) << 32) | bits | (odd << 16));
     }
   }
   {
-    static_assert(NWH <= 512, "one word of x per thread");
-    const int wc = tid < NWH ? tid : NWH - 1;
     float v[16];
     {
-      const uint4 a0 = reinterpret_cast<const uint4*>(xa + wc * 16)[0];
-      const uint4 a1 = reinterpret_cast<const uint4*>(xa + wc * 16)[1];
-      const uint32_t u[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      const uint32_t u[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         v[2 * q] = __uint_as_float(u[q] << 16);
@@ -219,7 +252,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     if (addp) {
       float nw[16];
       uint32_t ub[8];
-      if (o_w) {  // word wc of o: tagged words 8 wc .. + 8 of the XCD's copy
+      if (has_o) {  // word wc of o: tagged words 8 wc .. + 8 of the XCD's copy
         const CoherentBuf oq(ox, NWH * 8 * 8);
         uint4 q[4];
         for (;;) {
@@ -228,7 +261,7 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
           for (int i = 0; i < 4; ++i) q[i] = oq.ld4u(static_cast<uint32_t>((8 * wc + 2 * i) * 8));
           uint32_t bad = 0;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) bad |= (q[i].y ^ tag) | (q[i].w ^ tag);
+          for (int i = 0; i < 4; ++i) bad |= (q[i].y ^ (tag_raw + 1u)) | (q[i].w ^ (tag_raw + 1u));
           if (__all(bad == 0) || timed_out) break;
           __builtin_amdgcn_s_sleep(1);
           timed_out = (__builtin_amdgcn_s_memrealtime() - t0) > wait_bound;
@@ -239,30 +272,16 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
           ub[2 * i + 1] = q[i].z;
         }
       } else {
-        const uint4 b0 = reinterpret_cast<const uint4*>(xb + wc * 16)[0];
-        const uint4 b1 = reinterpret_cast<const uint4*>(xb + wc * 16)[1];
-        ub[0] = b0.x, ub[1] = b0.y, ub[2] = b0.z, ub[3] = b0.w;
-        ub[4] = b1.x, ub[5] = b1.y, ub[6] = b1.z, ub[7] = b1.w;
+        ub[0] = xb0.x, ub[1] = xb0.y, ub[2] = xb0.z, ub[3] = xb0.w;
+        ub[4] = xb1.x, ub[5] = xb1.y, ub[6] = xb1.z, ub[7] = xb1.w;
       }
-      if (norm_dt == MA_F32) {
-        const float4* np = reinterpret_cast<const float4*>(static_cast<const float*>(norm_w) + wc * 16);
+      {
+        const uint32_t un[16] = {nw0.x, nw0.y, nw0.z, nw0.w, nw1.x, nw1.y, nw1.z, nw1.w,
+                                 nw2.x, nw2.y, nw2.z, nw2.w, nw3.x, nw3.y, nw3.z, nw3.w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 f = np[q];
-          nw[4 * q] = f.x;
-          nw[4 * q + 1] = f.y;
-          nw[4 * q + 2] = f.z;
-          nw[4 * q + 3] = f.w;
-        }
-      } else {
-        const uint4* np = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(norm_w) + wc * 16);
-        const uint4 n0 = np[0], n1 = np[1];
-        const uint32_t un[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          nw[2 * q] = __uint_as_float(un[q] << 16);
-          nw[2 * q + 1] = __uint_as_float(un[q] & 0xffff0000u);
-        }
+        for (int q = 0; q < 16; ++q)
+          nw[q] = nf32 ? __uint_as_float(un[q])
+                       : (q & 1 ? __uint_as_float(un[q >> 1] & 0xffff0000u) : __uint_as_float(un[q >> 1] << 16));
       }
       float ss = 0.f;
 #pragma unroll
@@ -295,6 +314,9 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     }
   }
   __syncthreads();
+  asm volatile("" : "+v"(tag_raw));  // (keeps the + 1 below from moving up)
+  const uint32_t tag = tag_raw + 1u;
+  const uint32_t tag16 = tag & 0xffffu;
   if (router_wave) {
     float dot = 0.f;
 #pragma unroll
@@ -619,9 +641,9 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
 // position in the code object alone).
 #define MA_XCD_INST(US, KWI, ADT, NX)                                                                      \
   template __global__ void k_moe_xcd<4, US, KWI, 16, 2, ADT, NX>(                                         \
-      const uint16_t*, const uint16_t*, const void*, int, float, const uint16_t*, const uint16_t*,       \
-      const float*, int, const uint32_t*, const void*, const uint32_t*, const void*, uint16_t*, int32_t*, \
-      float*, uint32_t*, const uint32_t*, const void*, const float*, float, int, uint16_t*,              \
+      const uint16_t*, uint32_t*, const uint16_t*, const uint16_t*, const uint16_t*, const void*, int, int, \
+      float, const float*, const uint32_t*, const void*, const uint32_t*, const void*, uint16_t*, int32_t*, \
+      float*, const uint32_t*, const void*, const float*, float, int, uint16_t*,                         \
       const uint16_t*, const uint32_t*, const void*, const uint4*, int, uint64_t);
 MA_XCD_INST(3, 3, MA_F32, false)
 MA_XCD_INST(2, 2, MA_F32, false)
@@ -702,10 +724,11 @@ int moe_xcd_launch(const void* x, const void* x_add, const void* norm_weight, in
     return fail(MA_ERUNTIME, "moe_fused: its %d workgroups wait on each other but the device holds %lld at once",
                 kXcds * kXcdWgs, static_cast<long long>(capacity));
 #define MA_XCD_ARGS                                                                                      \
-  static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(x_add), norm_weight, norm_dtype, eps,   \
-      static_cast<const uint16_t*>(residual), static_cast<const uint16_t*>(gate_weight), router_bias,    \
-      static_cast<int>(n_experts), up_gate, up_gate_alpha, down, down_alpha, static_cast<uint16_t*>(y), \
-      topk_ids, topk_weight, static_cast<uint32_t*>(workspace), next_w, next_alpha, next_rms, next_eps, \
+  static_cast<const uint16_t*>(x), static_cast<uint32_t*>(workspace),                                 \
+      static_cast<const uint16_t*>(gate_weight), static_cast<const uint16_t*>(residual),               \
+      static_cast<const uint16_t*>(x_add), norm_weight, static_cast<int>(n_experts),                   \
+      (norm_dtype & 0xff) | (o_w ? kXHasO : 0), eps, router_bias, up_gate, up_gate_alpha, down,        \
+      down_alpha, static_cast<uint16_t*>(y), topk_ids, topk_weight, next_w, next_alpha, next_rms, next_eps, \
       static_cast<int>(next_rows), static_cast<uint16_t*>(next_out), static_cast<const uint16_t*>(attn), o_w, \
       o_alpha, static_cast<const uint4*>(prefetch), pf_units, wait_bound
   // the prefetch is a hint: whole 16-byte units, at most what the lanes cover
