@@ -435,6 +435,21 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     }
   }
 
+  // This wave's down rows, requested once its SwiGLU rows are in and before
+  // their products (requested with them, they held up the SwiGLU rows;
+  // after the outputs are published, they arrived ~0.5 us later).
+  asm volatile("" ::"v"(au[US - 1]));  // (in-order counters: every SwiGLU row is in)
+  const int kld = lane % LPRI, subd = lane / LPRI;
+  const int r0 = (lw * W + wv) * RPW;
+  uint32_t wd[UD][KWI];
+  float ad[UD];
+#pragma unroll
+  for (int u = 0; u < UD; ++u) {
+    const int64_t r = ex * H + r0 + u * RPID + subd;
+    load_words_v<KWI>(dn + r * NWI + kld * KWI, wd[u]);
+    ad[u] = ld_t<ADT>(dn_alpha, r);
+  }
+
   // SwiGLU outputs o0 .. o0 + US of slot xcd, published in the XCD's region
   {
     XSlice<KWH> xsl;
@@ -453,16 +468,6 @@ __global__ __launch_bounds__(512) void k_moe_xcd(
     if (lane < US) st_l2_32(&xh[o0 + lane], (tag16 << 16) | f32_to_bf16(swiglu_act(up_t, gate_t)));
   }
   if (wv == 0) MA_XSTAMP(5);  // this wave's h outputs published
-  const int kld = lane % LPRI, subd = lane / LPRI;
-  const int r0 = (lw * W + wv) * RPW;
-  uint32_t wd[UD][KWI];
-  float ad[UD];
-#pragma unroll
-  for (int u = 0; u < UD; ++u) {
-    const int64_t r = ex * H + r0 + u * RPID + subd;
-    load_words_v<KWI>(dn + r * NWI + kld * KWI, wd[u]);
-    ad[u] = ld_t<ADT>(dn_alpha, r);
-  }
   // Prefetch (optional): waves 1..7 pull pf_units 16-byte units (the next
   // layer's router rows, say) into this XCD's L2 and the Infinity Cache
   // while they would otherwise wait for h; every XCD reads all of it (each
