@@ -26,6 +26,7 @@ half the head (rotary_dim 32, theta 1e4), full attention (no window).
 
 from __future__ import annotations
 
+import dataclasses
 from dataclasses import dataclass, field
 
 import torch
@@ -204,6 +205,7 @@ class SyntheticDecoder:
         self.final_norm = ones(c.hidden)
         self.cos, self.sin = rope_tables(max_len, c.rotary_dim, c.rope_theta, dev)
         self.flash_head = None
+        self._pack_read_ahead()
 
     @classmethod
     def from_weights(cls, cfg: DecoderConfig, device, layers: list, embed: tuple, lm_head: tuple,
@@ -223,7 +225,33 @@ class SyntheticDecoder:
         self.embed, self.lm_head, self.final_norm = embed, lm_head, final_norm
         self.cos, self.sin = rope_tables(max_len, cfg.rotary_dim, cfg.rope_theta, self.device)
         self.flash_head = None
+        self._pack_read_ahead()
         return self
+
+    def _pack_read_ahead(self) -> None:
+        """Lay out each layer's post-attention norm weights, QK-norm weights
+        and router rows in one buffer (in that order, 256-byte aligned; the
+        layer's tensors become views of it), which the previous layer's
+        one-launch MoE kernel reads ahead into every XCD's L2 while it waits
+        on its own hand-offs: bytes that are read at the start of the layer's
+        launches and would otherwise come cold from HBM (the small ones first,
+        so that a router larger than the read-ahead still leaves them in)."""
+        self.read_ahead = []
+        for i, L in enumerate(self.layers):
+            parts = [L.post_ln, L.q_norm, L.k_norm, L.moe.gate_weight]
+            offs, n = [], 0
+            for t in parts:
+                offs.append(n)
+                n += -(-t.numel() * t.element_size() // 256) * 256
+            buf = torch.empty(n, dtype=torch.uint8, device=L.post_ln.device)
+            views = []
+            for t, o in zip(parts, offs):
+                v = buf[o:o + t.numel() * t.element_size()].view(t.dtype).view(t.shape)
+                v.copy_(t)
+                views.append(v)
+            moe = dataclasses.replace(L.moe, gate_weight=views[3])
+            self.layers[i] = dataclasses.replace(L, post_ln=views[0], q_norm=views[1], k_norm=views[2], moe=moe)
+            self.read_ahead.append(buf)
 
     def make_cache(self, batch: int, prefill_len: int, seed: int = 0) -> KVCache:
         """Cache rows filled with seeded N(0, 1) bf16 K/V for ``prefill_len``
@@ -288,9 +316,9 @@ class SyntheticDecoder:
             if fuse_next and i + 1 < c.layers and self.layers[i + 1].qkv_alpha.dtype == L.moe.up_gate_alpha.dtype:
                 n = self.layers[i + 1]
                 nl = (n.qkv, n.qkv_alpha, n.input_ln, c.eps)
-            # the next MoE layer's router rows are read ahead into the caches
-            # while this launch waits for h (routing-independent bytes)
-            pf = self.layers[i + 1].moe.gate_weight if self.prefetch_router and i + 1 < c.layers else None
+            # the next layer's norm weights and router rows are read ahead
+            # into the caches while this launch waits for h
+            pf = self.read_ahead[i + 1] if self.prefetch_router and i + 1 < c.layers else None
             out = moe_fused(hidden, L.moe, c.top_k, add=o, norm_weight=L.post_ln, eps=c.eps,
                             next_linear=nl,
                             o_linear=None if o is not None else (attn.reshape(1, -1), L.o, L.o_alpha),
