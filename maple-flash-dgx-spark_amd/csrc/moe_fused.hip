@@ -52,13 +52,13 @@ __device__ __forceinline__ int slot_expert(uint32_t rank, int s, const int32_t* 
 // dtype switch among the weight loads delayed their issue by 4 us).
 template <int KWH, int LPRH, int US, int KWI, int LPRI, int UD, int TK, int PER, int W, int ADT>
 __global__ __launch_bounds__(64 * W) void k_moe_fused(
-    const uint16_t* __restrict__ xa, const uint16_t* __restrict__ xb,
-    const void* __restrict__ norm_w, int norm_dt, float eps, const uint16_t* __restrict__ residual,
-    const uint16_t* __restrict__ gate_w, const float* __restrict__ bias, int n_exp,
+    const uint16_t* __restrict__ xa, uint32_t* __restrict__ ws, const uint16_t* __restrict__ gate_w,
+    const uint16_t* __restrict__ residual, const uint16_t* __restrict__ xb, const void* __restrict__ norm_w,
+    int n_exp, int norm_dt, float eps, const float* __restrict__ bias,
     const uint32_t* __restrict__ ug, const void* __restrict__ ug_alpha,
     const uint32_t* __restrict__ dn, const void* __restrict__ dn_alpha,
     uint16_t* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ wts_out,
-    uint32_t* __restrict__ ws, const uint32_t* __restrict__ nx_w, const void* __restrict__ nx_alpha,
+    const uint32_t* __restrict__ nx_w, const void* __restrict__ nx_alpha,
     const float* __restrict__ nx_rms, float nx_eps, int nx_rows,
     uint16_t* __restrict__ nx_out) {
   constexpr int NWH = KWH * LPRH, H = 16 * NWH;
@@ -92,8 +92,9 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
   // Calls made on this workspace so far (the h barrier moves the flags to f0
   // + 1 only once every workgroup has arrived, so every workgroup reads f0);
   // this call's logits carry the tag f0 + 1.
-  const uint32_t f0 = ld_coh32(&flags[kLine * (wg % kBarGroups)]);
-  const uint64_t tag = static_cast<uint64_t>(f0 + 1u) << 32;
+  // (f0 is first used once x is staged: used here, every wave waited for
+  // this load before requesting x)
+  uint32_t f0 = ld_coh32(&flags[kLine * (wg % kBarGroups)]);
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   bool timed_out = false;
   const bool router_wg = wg < n_exp;  // workgroup e < E computes router logit e
@@ -106,6 +107,7 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
   const uint16_t* const res_b = xb ? xb : xa;
   const uint32_t ra = res_a[roc], rb = res_b[roc];
 
+  uint64_t tag = 0;  // this call's: (f0 + 1) << 32, formed below
   // ---- 1. x (optionally add + RMSNorm) staged as x' pairs; workgroup e also
   // takes the dot product with router row e (loaded alongside x)
   float dot = 0.f;
@@ -115,52 +117,60 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
     float v[WPT][16], nw[WPT][16];
     uint4 gr[WPT][2];
     float ss = 0.f;
+    // Every load first, as raw words (the norm weights from an address their
+    // dtype selects, not from a dtype branch), then the arithmetic: a load
+    // converted inside a branch gets its wait right behind it.
+    const bool nf32 = norm_dt == MA_F32;
+    uint4 xr[WPT][2], br[WPT][2], nr[WPT][4];
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
       const int w = tid + NTH * i;
       const int wc = w < NWH ? w : NWH - 1;
-      if (xb) {  // the norm weights, loaded with x
-        if (norm_dt == MA_F32) {
-          const float4* np = reinterpret_cast<const float4*>(static_cast<const float*>(norm_w) + wc * 16);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float4 f = np[q];
-            nw[i][4 * q] = f.x;
-            nw[i][4 * q + 1] = f.y;
-            nw[i][4 * q + 2] = f.z;
-            nw[i][4 * q + 3] = f.w;
-          }
-        } else {
-          const uint4* np = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(norm_w) + wc * 16);
-          const uint4 n0 = np[0], n1 = np[1];
-          const uint32_t u[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            nw[i][2 * q] = __uint_as_float(u[q] << 16);
-            nw[i][2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
-          }
-        }
-      }
+      xr[i][0] = reinterpret_cast<const uint4*>(xa + wc * 16)[0];
+      xr[i][1] = reinterpret_cast<const uint4*>(xa + wc * 16)[1];
       const uint4* gp = reinterpret_cast<const uint4*>(gate_w + static_cast<int64_t>(router_wg ? wg : 0) * H + wc * 16);
       gr[i][0] = gp[0];
       gr[i][1] = gp[1];
-      const uint4 a0 = reinterpret_cast<const uint4*>(xa + wc * 16)[0];
-      const uint4 a1 = reinterpret_cast<const uint4*>(xa + wc * 16)[1];
-      const uint32_t u[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      br[i][0] = br[i][1] = make_uint4(0u, 0u, 0u, 0u);
+      nr[i][0] = nr[i][1] = nr[i][2] = nr[i][3] = br[i][0];
+      if (xb) {  // the addend and the norm weights (f32: 4 x 16 bytes per word; bf16: 2 x 16, loaded twice)
+        br[i][0] = reinterpret_cast<const uint4*>(xb + wc * 16)[0];
+        br[i][1] = reinterpret_cast<const uint4*>(xb + wc * 16)[1];
+        const uint4* np = reinterpret_cast<const uint4*>(static_cast<const char*>(norm_w) + wc * (nf32 ? 64 : 32));
+        nr[i][0] = np[0];
+        nr[i][1] = np[1];
+        nr[i][2] = np[nf32 ? 2 : 0];
+        nr[i][3] = np[nf32 ? 3 : 1];
+      }
+    }
+    // the other arguments read before the expert loads, at once
+    asm volatile("" ::"s"(eps), "s"(bias), "s"(ug), "s"(ug_alpha), "s"(dn), "s"(dn_alpha), "s"(nx_w)
+                 : "memory");
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+      const int w = tid + NTH * i;
+      const uint32_t u[8] = {xr[i][0].x, xr[i][0].y, xr[i][0].z, xr[i][0].w,
+                             xr[i][1].x, xr[i][1].y, xr[i][1].z, xr[i][1].w};
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         v[i][2 * q] = __uint_as_float(u[q] << 16);
         v[i][2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
       }
       if (xb) {
-        const uint4 b0 = reinterpret_cast<const uint4*>(xb + wc * 16)[0];
-        const uint4 b1 = reinterpret_cast<const uint4*>(xb + wc * 16)[1];
-        const uint32_t ub[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        const uint32_t ub[8] = {br[i][0].x, br[i][0].y, br[i][0].z, br[i][0].w,
+                                br[i][1].x, br[i][1].y, br[i][1].z, br[i][1].w};
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           v[i][2 * q] += __uint_as_float(ub[q] << 16);
           v[i][2 * q + 1] += __uint_as_float(ub[q] & 0xffff0000u);
         }
+        const uint32_t un[16] = {nr[i][0].x, nr[i][0].y, nr[i][0].z, nr[i][0].w, nr[i][1].x, nr[i][1].y,
+                                 nr[i][1].z, nr[i][1].w, nr[i][2].x, nr[i][2].y, nr[i][2].z, nr[i][2].w,
+                                 nr[i][3].x, nr[i][3].y, nr[i][3].z, nr[i][3].w};
+#pragma unroll
+        for (int q = 0; q < 16; ++q)
+          nw[i][q] = nf32 ? __uint_as_float(un[q])
+                          : (q & 1 ? __uint_as_float(un[q >> 1] & 0xffff0000u) : __uint_as_float(un[q >> 1] << 16));
       }
       if (w < NWH) {
 #pragma unroll
@@ -197,6 +207,8 @@ __global__ __launch_bounds__(64 * W) void k_moe_fused(
       if (lane == 0) red2[wv] = s;
     }
     __syncthreads();
+    asm volatile("" : "+v"(f0));  // (keeps f0's uses from moving up)
+    tag = static_cast<uint64_t>(f0 + 1u) << 32;
     if (router_wg && tid == 0) {
       float l = red2[0];
 #pragma unroll
@@ -632,11 +644,11 @@ static int moe_fused_impl(const void* x, const void* x_add, const void* norm_wei
   if (o_w)
     return fail(MA_EVALUE, "moe_fused_o: the O projection in the launch needs the XCD-split form (ma_moe_fused_form)");
 #define MA_FUSED_ARGS                                                                            \
-  static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(x_add), norm_weight, norm_dtype, \
-      eps, static_cast<const uint16_t*>(residual), static_cast<const uint16_t*>(gate_weight),    \
-      router_bias, static_cast<int>(n_experts), up_gate,                                         \
-      up_gate_alpha, down, down_alpha,                                                           \
-      static_cast<uint16_t*>(y), topk_ids, topk_weight, static_cast<uint32_t*>(workspace),       \
+  static_cast<const uint16_t*>(x), static_cast<uint32_t*>(workspace),                           \
+      static_cast<const uint16_t*>(gate_weight), static_cast<const uint16_t*>(residual),         \
+      static_cast<const uint16_t*>(x_add), norm_weight, static_cast<int>(n_experts), norm_dtype, \
+      eps, router_bias, up_gate, up_gate_alpha, down, down_alpha,                                \
+      static_cast<uint16_t*>(y), topk_ids, topk_weight,                                          \
       next_w, next_alpha, next_rms, next_eps, static_cast<int>(next_rows),                        \
       static_cast<uint16_t*>(next_out)
   const dim3 grid(s->grid), block(64 * s->waves);
