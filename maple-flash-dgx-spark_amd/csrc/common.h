@@ -347,6 +347,24 @@ __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 
 
 // A grouped MoE combine run in front of a kernel that reads its output rows
 // (k_xprep): y[t] = sum_j wts[t, j] * slot_out[inverse[t, j]] + res[t].
+// The (row, weight) pairs of token t's k <= 8 slots, in every lane: lane j
+// (mod 8) loads slot j's pair (slots past k re-read the last one), then each
+// pair is read off its lane -- two loads in flight at once, where 2k uniform
+// loads, each under a slot condition, were issued one after the other with a
+// wait for each.
+__device__ __forceinline__ void slot_pairs8(const int32_t* __restrict__ inverse, const float* __restrict__ wts,
+                                            int64_t t, int k, int64_t (&row)[8], float (&w)[8]) {
+  const int lj = static_cast<int>(threadIdx.x) & 7;
+  const int j = lj < k ? lj : k - 1;
+  const int32_t r = inverse[t * k + j];
+  const float ww = wts[t * k + j];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    row[s] = __builtin_amdgcn_readlane(r, s);
+    w[s] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ww), s));
+  }
+}
+
 struct CombineIn {
   const uint16_t* slot_out;  // bf16 [pairs, K * 16] (null: read x)
   const int32_t* inverse;    // [batch, topk] row of each (token, slot) in slot_out

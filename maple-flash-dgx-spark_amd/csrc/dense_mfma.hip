@@ -87,16 +87,13 @@ __global__ __launch_bounds__(128) void k_xprep(const uint16_t* __restrict__ x, i
   const int tid = threadIdx.x;
   const bool valid = t < batch;
   float c = 0.f, ss = 0.f;
-  // the combine's (row, weight) pairs of this token (scalar loads)
+  // (the combine's arguments read at once: left to itself the compiler read
+  // them in two dependent rounds)
+  asm volatile("" ::"s"(cb.slot_out), "s"(cb.inverse), "s"(cb.wts), "s"(cb.topk), "s"(cb.res), "s"(cb.x_out));
+  // the combine's (row, weight) pairs of this token
   int64_t crow[8];
   float cw[8];
-  if (cb.slot_out && valid) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      crow[j] = j < cb.topk ? cb.inverse[t * cb.topk + j] : 0;
-      cw[j] = j < cb.topk ? cb.wts[t * cb.topk + j] : 0.f;
-    }
-  }
+  if (cb.slot_out && valid) slot_pairs8(cb.inverse, cb.wts, t, cb.topk, crow, cw);
   for (int64_t wd = tid; wd < nwords; wd += 128) {
     float v[16];
     if (valid && cb.slot_out) {

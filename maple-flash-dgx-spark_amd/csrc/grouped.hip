@@ -670,18 +670,14 @@ __global__ __launch_bounds__(256) void k_combine8(const uint16_t* __restrict__ o
                                                   uint16_t* __restrict__ y) {
   const int64_t t = blockIdx.y;
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
-  int64_t row[K];
-  float wj[K];
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    row[j] = j < topk ? inverse[t * topk + j] : 0;
-    wj[j] = j < topk ? wts[t * topk + j] : 0.f;
-  }
+  static_assert(K == 8, "slot pairs");
+  int64_t row[8];
+  float wj[8];
+  slot_pairs8(inverse, wts, t, topk, row, wj);
   if (i >= n) return;
   uint4 v[K], r = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-  for (int j = 0; j < K; ++j)
-    if (j < topk) v[j] = *reinterpret_cast<const uint4*>(out + row[j] * n + i);
+  for (int j = 0; j < K; ++j) v[j] = *reinterpret_cast<const uint4*>(out + row[j] * n + i);
   if (res) r = *reinterpret_cast<const uint4*>(res + t * n + i);
   float a[8];
 #pragma unroll
