@@ -180,13 +180,25 @@ __global__ __launch_bounds__(256) void k_rtn4_embed(
   const int64_t n_groups = nwords * 8 / group;
   for (int64_t wi = threadIdx.x; wi < nwords; wi += 256) {
     const uint32_t word = w[id * nwords + wi];
+    if (group % 8 == 0) {
+      // one group per word: its scale and bias read once, as raw words from a
+      // dtype-selected address (no dtype branch: a load converted in one
+      // waits right there, and this loop issued sixteen such loads a word)
+      const int64_t gi = id * n_groups + wi * 8 / group;
+      const AnyWord sw = ld_any_word(scales, s_dt, gi), bw = ld_any_word(biases, b_dt, gi);
+      const float s = any_word_f(sw, s_dt), bb = any_word_f(bw, b_dt);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t k = wi * 8 + j;
-      const int64_t g = k / group;
-      const float s = ld_f(scales, s_dt, id * n_groups + g);
-      const float bb = ld_f(biases, b_dt, id * n_groups + g);
-      out[i * nwords * 8 + k] = static_cast<float>((word >> (4 * j)) & 15u) * s + bb;
+      for (int j = 0; j < 8; ++j)
+        out[i * nwords * 8 + wi * 8 + j] = static_cast<float>((word >> (4 * j)) & 15u) * s + bb;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t k = wi * 8 + j;
+        const int64_t g = k / group;
+        const float s = ld_f(scales, s_dt, id * n_groups + g);
+        const float bb = ld_f(biases, b_dt, id * n_groups + g);
+        out[i * nwords * 8 + k] = static_cast<float>((word >> (4 * j)) & 15u) * s + bb;
+      }
     }
   }
 }
