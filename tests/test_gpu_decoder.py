@@ -143,6 +143,39 @@ def test_fused_attention_equals_two_step(dev, window, heads):
         assert_bf16_close(np_f(out[b, :, 0]), o, atol_frac=ATTN_ATOL, what=f"row {b}")
 
 
+@pytest.mark.parametrize("heads", HEADS)
+@pytest.mark.parametrize("wdt,tdt", [(torch.float16, torch.bfloat16), (torch.float32, torch.float16),
+                                     (torch.bfloat16, torch.bfloat16)])
+def test_fused_attention_weight_and_table_dtypes(dev, heads, wdt, tdt):
+    """The fused launch reads its norm weights and RoPE rows as the aligned
+    32-bit words that hold them, whatever their dtype: the same bits as the
+    two-step path (which reads each element in its dtype) for f16, f32 and
+    bf16 norm weights with bf16 and f16 tables, with RoPE and without."""
+    nq, nkv, d, rot = heads
+    max_len = 600
+    seqlen = torch.tensor([5, 128, 433], device=dev)
+    qkv = synthetic.randn_bf16((3, (nq + 2 * nkv) * d), 31, dev)
+    kc = synthetic.randn_bf16((3, nkv, max_len, d), 32, dev)
+    vc = synthetic.randn_bf16((3, nkv, max_len, d), 33, dev)
+    qw = (torch.rand(d, device=dev) + 0.5).to(wdt)
+    kw = (torch.rand(d, device=dev) + 0.5).to(wdt)
+    cos, sin = od.rope_tables(max_len, rot, 1e4)
+    cos_t, sin_t = torch.from_numpy(cos).to(dev).to(tdt), torch.from_numpy(sin).to(dev).to(tdt)
+    for use_rope in (True, False):
+        kc1, vc1, kc2, vc2 = kc.clone(), vc.clone(), kc.clone(), vc.clone()
+        q = apply_qkv_decode(qkv, qw, kw, cos_t[seqlen], sin_t[seqlen],
+                             kc1, vc1, seqlen, num_heads=nq, num_kv_heads=nkv, head_dim=d,
+                             rotary_dim=rot, use_rope=use_rope, use_qk_norm=True, eps=1e-6)
+        ref = decode_gqa_attn(q, kc1, vc1, seqlen, scale=d ** -0.5, window=None)
+        ws = gqa_workspace(3, nkv, max_len, dev, d)
+        out = decode_attention(qkv, qw, kw, cos_t, sin_t, kc2, vc2, seqlen, ws, num_heads=nq,
+                               num_kv_heads=nkv, head_dim=d, rotary_dim=rot, use_rope=use_rope, eps=1e-6,
+                               scale=d ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"use_rope={use_rope}"
+        assert torch.equal(kc2, kc1) and torch.equal(vc2, vc1), f"use_rope={use_rope}"
+
+
 @pytest.mark.parametrize("heads", HEADS[:2])
 @pytest.mark.parametrize("seqlen", [0, 130, 2000, 4100])
 def test_fused_attention_o_projection_equals_gemv(dev, seqlen, heads):
