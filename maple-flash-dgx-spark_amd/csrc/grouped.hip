@@ -853,6 +853,8 @@ __device__ __forceinline__ GpDma gp_dma_sources(const uint32_t* base, int64_t ld
 typedef __attribute__((address_space(3))) void* lds_void_t;
 // s_waitcnt immediate (gfx9 encoding): vmcnt(4), expcnt and lgkmcnt left open.
 constexpr int kVmcnt4 = 0x4 | (0x7 << 4) | (0xF << 8);
+// vmcnt(4) and lgkmcnt(0), expcnt left open.
+constexpr int kVmcnt4Lgkm0 = 0x4 | (0x7 << 4);
 
 // The copies of the step at K word k0 into the LDS buffer xsb (in flight
 // until the issuing wave's vector memory counter drains).
@@ -866,12 +868,15 @@ __device__ __forceinline__ void gp_dma(const GpDma& d, int64_t k0, uint32_t* xsb
                                      (lds_void_t)(xsb + 4 * (64 * wv + gp::kThreads * i)), 16, 0, 0);
 }
 
-// One step of the K loop: issue the next step's x' copies into ``nxt`` (if
-// there is a next step) and its weights into wn, then this step's MFMAs on
-// ``cur``, then wait for the copies and meet at the barrier.
+// One step of the K loop: take this step's weights out of w, issue the next
+// step's x' copies into ``nxt`` (if there is a next step) and its weights
+// into w, then this step's MFMAs on ``cur``, then wait for the copies and
+// meet at the barrier.  The weights move to their own registers at the top,
+// after the wait that covers their loads: a copy at the end of the step
+// would have to wait for the loads just issued, in the middle of the step.
 __device__ __forceinline__ void gp_kstep(const uint32_t* rp, const int64_t (&moff)[4], int64_t k0, int64_t nwk,
                                          const GpDma& d, const uint32_t* cur, uint32_t* nxt,
-                                         uint2 (&wq)[4], int g, int r16, int col0, f32x4_t (&acc)[4][4],
+                                         uint2 (&w)[4], int g, int r16, int col0, f32x4_t (&acc)[4][4],
                                          const ExpandConsts& kc) {
   using namespace gp;
   const int64_t kn = k0 + kWords < nwk ? k0 + kWords : k0;
@@ -880,20 +885,30 @@ __device__ __forceinline__ void gp_kstep(const uint32_t* rp, const int64_t (&mof
   // flight during the MFMAs.
   __builtin_amdgcn_s_waitcnt(0);
   MA_ISSUE_FENCE();
+  uint2 wq[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) wq[mb] = w[mb];
+  MA_ISSUE_FENCE();
   if (k0 + kWords < nwk) gp_dma(d, kn, nxt);
   MA_ISSUE_FENCE();  // the copies are issued before the weights
-  uint2 wn[4];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) wn[mb] = *reinterpret_cast<const uint2*>(rp + moff[mb] + kn);
+  for (int mb = 0; mb < 4; ++mb) w[mb] = *reinterpret_cast<const uint2*>(rp + moff[mb] + kn);
   MA_ISSUE_FENCE();  // the next step's loads go out before this step's MFMAs
   gp_step(wq, cur, g, r16, col0, acc, kc);
   // This wave's copies have landed: at most the 4 weight loads issued after
   // them are outstanding (vector memory completes in issue order); those
   // are waited for where the next step uses them.
-  __builtin_amdgcn_s_waitcnt(kVmcnt4);
-  __syncthreads();  // the next buffer is in; this one is free to refill
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) wq[mb] = wn[mb];
+  __builtin_amdgcn_s_waitcnt(kVmcnt4Lgkm0);
+  // The next buffer is in and this one is free to refill once every wave is
+  // here.  A plain barrier: __syncthreads' fence would also wait for the
+  // weight loads just issued (it drains every outstanding write to LDS, and
+  // the LDS DMA counts in the same counter as those loads).
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  // Register copies the loop needs between steps stay here, after the
+  // barrier, where the next step's first wait covers their loads.
+  MA_ISSUE_FENCE();
 }
 
 // The K loop shared by both stages: acc += W x x', the lane's weight row of
