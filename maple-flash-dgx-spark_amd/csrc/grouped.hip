@@ -1230,7 +1230,13 @@ static int grouped_launch(const void* x, int64_t ldx, const uint32_t* x_pairs, c
 #undef MA_GROUPED_KS
   } else {
     // prefill: the tokens' x' pairs once (or those of ma_moe_route), then
-    // tiles of 128 pairs x 256 weight rows
+    // tiles of 128 pairs x 256 weight rows.  The tiles' copy sources are
+    // 32-bit uint32 offsets into x' and h.
+    if (static_cast<uint64_t>(tokens) * hidden / 2 >= (uint64_t{1} << 32) ||
+        static_cast<uint64_t>(n_pairs) * inter / 2 >= (uint64_t{1} << 32))
+      return fail(MA_EVALUE, "moe_grouped: %lld tokens x hidden %lld (or their pairs x intermediate %lld) "
+                  "exceed the 16 GiB the batched kernels address; split the batch",
+                  (long long)tokens, (long long)hidden, (long long)inter);
     char* p = reinterpret_cast<char*>(out) + align256(static_cast<size_t>(n_pairs) * hidden * 2);
     const uint32_t* xpp = x_pairs;
     const float* xcc = x_corr;

@@ -7,6 +7,8 @@ entry points.
 from __future__ import annotations
 
 import ctypes
+
+import torch
 import re
 from pathlib import Path
 
@@ -59,6 +61,14 @@ def test_size_errors_map_without_a_gpu():
         _lib.call("ma_moe_dispatch", None, 0, 8, 0, None, None, None, None, None)
     with pytest.raises(ValueError, match="groups"):
         _lib.call("ma_rtn4_gemv", None, 1, 1, 96, None, 4, 12, 0, None, 1, None, 1, 64, None, 4, None)
+    # 2^22 tokens x hidden 2048: x' holds 2^32 uint32 words, past the batched
+    # kernels' 32-bit copy offsets (rejected before any launch; the pointers
+    # are never dereferenced)
+    fake = 0x10000
+    with pytest.raises(ValueError, match="split the batch"):
+        _lib.call("ma_moe_grouped", fake, 2048, None, None, 1 << 22, 8, fake, fake, fake, fake,
+                  _lib.dtype_code(torch.empty(0, dtype=torch.bfloat16), "a"), 64, 2048, 768, fake, fake,
+                  fake, fake, None, 0, None, 0, fake, fake, 1 << 62, None)
 
 
 def test_stamped_variant_exports_the_same_symbols_and_its_stamps_fit():
