@@ -214,13 +214,18 @@ __device__ __forceinline__ float prep_word_pairs(const float xs[16], uint32_t xp
 
 // SwiGLU of the reference's expert MLP (kernels/ternary_expert.py:314-318):
 // clamp(up, -7, 7) * g * sigmoid(g) with g = min(gate, 7), in that order;
-// sigmoid(g) = 1 / (1 + exp(-g)) with the hardware reciprocal (v_rcp_f32,
-// 1 ulp; the reference's Triton sigmoid divides approximately too).
+// sigmoid(g) = 1 / (1 + exp(-g)), exp(-g) as 2^(-g log2 e) on the hardware
+// exponential (v_exp_f32) and the division as the hardware reciprocal
+// (v_rcp_f32), each about 1 ulp -- the reference's Triton sigmoid also takes
+// its exp as an approximate base-2 exponential and divides approximately.
+// (-g log2 e > -10.1 here, so no result is denormal; a very negative gate
+// gives exp = +inf and an output of 0.)
 constexpr float kMlpClamp = 7.0f;
+constexpr float kLog2e = 1.4426950408889634f;
 __device__ __forceinline__ float swiglu_act(float up, float gate) {
   up = fminf(fmaxf(up, -kMlpClamp), kMlpClamp);
   gate = fminf(gate, kMlpClamp);
-  return (up * gate) * __builtin_amdgcn_rcpf(1.0f + expf(-gate));
+  return (up * gate) * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gate * kLog2e));
 }
 
 // ---------------------------------------------------------------------------

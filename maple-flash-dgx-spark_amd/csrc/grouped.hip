@@ -1021,9 +1021,10 @@ __global__ __launch_bounds__(gp::kThreads) __attribute__((amdgpu_waves_per_eu(4,
         const uint16_t hb = f32_to_bf16(swiglu_act(up, gt));
         const float hv = bf16_to_f32(hb);
         hst[col * kHRow + hoff] = static_cast<uint16_t>(bf16_bits_exact(hv * f));  // exact: power-of-two scale
-        if (col < np) {
-          if (h) h[static_cast<int64_t>(pid[col]) * ldh + o0 + 16 * mb + 4 * g + r] = hb;
-          hcl[nb] += (f + 1.0f) * hv;
+        // (+0.0 for the pad columns: hcl starts at +0.0, so no sum changes)
+        hcl[nb] += col < np ? (f + 1.0f) * hv : 0.0f;
+        if (h) {
+          if (col < np) h[static_cast<int64_t>(pid[col]) * ldh + o0 + 16 * mb + 4 * g + r] = hb;
         }
       }
     }
