@@ -95,6 +95,27 @@ def test_moe_grouped_zipf_vs_oracle(dev, layer, tokens):
     assert_bf16_close(np_f(y), ref, atol_frac=2.0 ** -7, what=f"y T={tokens}")
 
 
+@pytest.mark.parametrize("hidden,n_exp,inter,k,tokens", [(3072, 8, 1024, 4, 96), (1024, 16, 512, 2, 200)])
+def test_moe_grouped_prefill_form_other_shapes(dev, hidden, n_exp, inter, k, tokens):
+    """The prefill-form grouped kernels (more than 16 pairs per expert: x'
+    copied into LDS a K step ahead, 128-pair x 256-row tiles) at hidden sizes
+    and expert widths other than the synthetic layer's (K loops of 24 / 8 /
+    64 / 4 steps): h and y against the oracle on the kernel's own routing, and
+    the same bits on a second run."""
+    L = synthetic.make_moe_layer(hidden, n_exp, inter, seed=11, device=dev)
+    assert tokens * k > 16 * n_exp  # the prefill form
+    x = synthetic.randn_bf16((tokens, hidden), 500 + hidden, dev)
+    ids, wts = router_topk(x, L.gate_weight, k)
+    y, h = moe_grouped(x, L, ids, wts, return_h=True)
+    torch.cuda.synchronize()
+    idn, wn = ids.cpu().numpy(), wts.cpu().numpy()
+    ref, href = ok.moe_experts(np_f(x), idn, wn, *_oracle_inputs(L))
+    assert_bf16_close(np_f(h), href, what=f"h H={hidden} I={inter}")
+    assert_bf16_close(np_f(y), ref, atol_frac=2.0 ** -7, what=f"y H={hidden} I={inter}")
+    y2, h2 = moe_grouped(x, L, ids, wts, return_h=True)
+    assert torch.equal(y2, y) and torch.equal(h2, h)
+
+
 @pytest.mark.parametrize("tokens", [8, 32, 128])
 def test_moe_layer_routed_pairs_vs_oracle(dev, layer, tokens):
     """The decoder's batched MoE half: one routing launch that also writes xn
