@@ -115,12 +115,14 @@ __global__ __launch_bounds__(256) void k_router_logits(
 
 // The logits of prefill-sized batches as a GEMM on v_mfma_f32_16x16x32_bf16
 // (A = 16 tokens, B = 16 experts, both straight from memory): a workgroup
-// takes 16 tokens x 64 experts, its 8 waves each a K range of K / 8, walked
+// takes 16 tokens x 32 experts (at 2048 tokens and 64 experts, 256
+// workgroups: one per CU; with 64 experts each, half the CUs idled and the
+// launch took 11.6 against 7.9 us), its 8 waves each a K range of K / 8, walked
 // in steps of kRgStep 32-wide k-slices whose operands are all loaded before
 // the step's MFMAs; the waves' partial tiles are then added through LDS in
 // wave order (the same bits on every run).  bf16 x bf16 products are exact;
 // the sums are float32 (in another order than the dot-product kernel's).
-constexpr int kRgWaves = 8, kRgExperts = 64, kRgStep = 4;
+constexpr int kRgWaves = 8, kRgExperts = 32, kRgStep = 4;
 
 __global__ __launch_bounds__(64 * kRgWaves) void k_router_gemm(
     const uint16_t* __restrict__ x, int64_t ldx, int64_t tokens, const uint16_t* __restrict__ w,
@@ -133,26 +135,27 @@ __global__ __launch_bounds__(64 * kRgWaves) void k_router_gemm(
   const int64_t e0 = static_cast<int64_t>(blockIdx.y) * kRgExperts;
   const int64_t t = t0 + r16 < tokens ? t0 + r16 : tokens - 1;
   const uint16_t* const xr = x + t * ldx + 8 * g;
-  const uint16_t* wr[4];
+  constexpr int NBE = kRgExperts / 16;  // 16-expert blocks per workgroup
+  const uint16_t* wr[NBE];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) wr[nb] = w + (e0 + 16 * nb + r16) * k_in + 8 * g;
+  for (int nb = 0; nb < NBE; ++nb) wr[nb] = w + (e0 + 16 * nb + r16) * k_in + 8 * g;
   const int64_t kw = k_in / kRgWaves;
-  f32x4d_t acc[4];
+  f32x4d_t acc[NBE];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) acc[nb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+  for (int nb = 0; nb < NBE; ++nb) acc[nb] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
   for (int64_t k0 = wv * kw; k0 < (wv + 1) * kw; k0 += 32 * kRgStep) {
-    u32x4v_t a[kRgStep], b[kRgStep][4];
+    u32x4v_t a[kRgStep], b[kRgStep][NBE];
 #pragma unroll
     for (int s = 0; s < kRgStep; ++s) {
       a[s] = *reinterpret_cast<const u32x4v_t*>(xr + k0 + 32 * s);
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) b[s][nb] = *reinterpret_cast<const u32x4v_t*>(wr[nb] + k0 + 32 * s);
+      for (int nb = 0; nb < NBE; ++nb) b[s][nb] = *reinterpret_cast<const u32x4v_t*>(wr[nb] + k0 + 32 * s);
     }
     mfma_block_begin();
 #pragma unroll
     for (int s = 0; s < kRgStep; ++s)
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) mfma_acc(acc[nb], a[s], b[s][nb]);
+      for (int nb = 0; nb < NBE; ++nb) mfma_acc(acc[nb], a[s], b[s][nb]);
     mfma_block_end();
     keep_b(a, acc);
 #pragma unroll
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(64 * kRgWaves) void k_router_gemm(
   }
   // lane (r16, g) holds tokens 4 g .. 4 g + 3 of expert 16 nb + r16
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
+  for (int nb = 0; nb < NBE; ++nb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) part[wv][4 * g + i][16 * nb + r16] = acc[nb][i];
   __syncthreads();
