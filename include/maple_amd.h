@@ -113,6 +113,20 @@ int ma_router_topk(const void* x, int x_dtype, int64_t tokens, int64_t ldx,
                    const float* bias, int top_k,
                    int32_t* ids, float* weights,
                    void* workspace, size_t workspace_bytes, void* stream);
+/*
+ * ma_router_topk that also writes x in the form the grouped expert GEMMs
+ * read (x_pairs uint32 [tokens, k_in / 2], 16-byte aligned; x_corr float32
+ * [tokens]: each token's correction sum), from the same per-token launch as
+ * the top-k; ma_moe_grouped given them skips its own x' launch and returns
+ * the same bits.  x bfloat16, k_in a multiple of 16, rows 16-byte aligned.
+ * No reference counterpart: a fused form of router_topk and the first step
+ * of the grouped experts, for prefill-sized batches.
+ */
+int ma_router_topk_pairs(const void* x, int x_dtype, int64_t tokens, int64_t ldx,
+                         const void* gate_weight, int w_dtype, int64_t n_experts, int64_t k_in,
+                         const float* bias, int top_k,
+                         int32_t* ids, float* weights, uint32_t* x_pairs, float* x_corr,
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Dispatch of (token, slot) pairs p = token * top_k + slot to experts:

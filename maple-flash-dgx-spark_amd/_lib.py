@@ -36,6 +36,7 @@ _SIGNATURES = {
     "ma_ternary_gemv_ws": [_P, _I, _L, _L, _P, _L, _L, _I, _P, _I, _P, _I, _F, _P, _L, _P, _Z, _P],
     "ma_router_workspace_bytes": [_L, _L],
     "ma_router_topk": [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _P, _P, _P, _Z, _P],
+    "ma_router_topk_pairs": [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _P, _P, _P, _P, _P, _Z, _P],
     "ma_moe_dispatch": [_P, _I, _L, _I, _P, _P, _P, _P, _P],
     "ma_ternary_expert_gemv": [_P, _I, _L, _L, _P, _L, _L, _L, _I, _P, _I, _P, _I, _L, _P, _L, _P],
     "ma_ternary_expert_swiglu": [_P, _I, _L, _L, _L, _P, _L, _L, _L, _I, _P, _I, _P, _I, _P, _L, _P],

@@ -212,6 +212,19 @@ __device__ __forceinline__ float prep_word_pairs(const float xs[16], uint32_t xp
   return c;
 }
 
+// Convert 16 bf16 activations (two uint4) into 8 x' pair dwords; returns
+// sum (f + 1) x over them.
+__device__ __forceinline__ float x16_to_pairs(uint4 a, uint4 b, uint32_t pr[8]) {
+  const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  float v[16];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    v[2 * q] = __uint_as_float(u[q] << 16);
+    v[2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
+  }
+  return prep_word_pairs(v, pr);
+}
+
 // SwiGLU of the reference's expert MLP (kernels/ternary_expert.py:314-318):
 // clamp(up, -7, 7) * g * sigmoid(g) with g = min(gate, 7), in that order;
 // sigmoid(g) = 1 / (1 + exp(-g)), exp(-g) as 2^(-g log2 e) on the hardware

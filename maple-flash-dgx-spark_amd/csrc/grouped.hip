@@ -80,19 +80,6 @@ __device__ __forceinline__ bool decode_tile(const int32_t* __restrict__ offsets,
   return false;
 }
 
-// Convert 16 bf16 activations (two uint4) into 8 x' pair dwords; returns
-// sum (f + 1) x over them.
-__device__ __forceinline__ float x16_to_pairs(uint4 a, uint4 b, uint32_t pr[8]) {
-  const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  float v[16];
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    v[2 * q] = __uint_as_float(u[q] << 16);
-    v[2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
-  }
-  return prep_word_pairs(v, pr);
-}
-
 // sum (f + 1)/f * (lo + hi) over 8 x' pair dwords (recovers sum (f + 1) x).
 __device__ __forceinline__ float pairs_cst(const uint32_t pr[8]) {
   float c = 0.f;

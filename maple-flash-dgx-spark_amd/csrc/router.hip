@@ -189,10 +189,19 @@ static bool gemm_ok(int x_dtype, int w_dtype, int64_t tokens, int64_t n_exp, int
 }
 
 template <int PER>
+// Top-k of token t's logits.  With xp set, the same wave also writes token
+// t's x' pairs (the grouped experts' B operands: xp [T, nwords * 8]) and its
+// correction xc[t] = sum (f + 1) x, with the arithmetic and summation order
+// of the grouped GEMMs' own x' launch (whose two waves' words lane and
+// lane + 64, every 128th, are this lane's two sums), so the experts give the
+// same bits either way and that launch is not needed.
 __global__ __launch_bounds__(64) void k_router_topk(const float* __restrict__ logits,
                                                     int64_t n_exp, int top_k,
                                                     int32_t* __restrict__ ids,
-                                                    float* __restrict__ wts) {
+                                                    float* __restrict__ wts,
+                                                    const uint16_t* __restrict__ x, int64_t ldx,
+                                                    int64_t nwords, uint32_t* __restrict__ xp,
+                                                    float* __restrict__ xc) {
   const int lane = threadIdx.x;
   const int64_t t = blockIdx.x;
   float p[PER];
@@ -200,6 +209,25 @@ __global__ __launch_bounds__(64) void k_router_topk(const float* __restrict__ lo
   for (int i = 0; i < PER; ++i) {
     const int64_t e = lane + 64 * i;
     p[i] = e < n_exp ? logits[t * n_exp + e] : -INFINITY;
+  }
+  if (xp) {  // the same in every lane
+    float c[2] = {0.f, 0.f};
+    for (int64_t w0 = 0; w0 < nwords; w0 += 128) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t wd = w0 + lane + 64 * h;
+        if (wd < nwords) {
+          const uint4* src = reinterpret_cast<const uint4*>(x + t * ldx + wd * 16);
+          uint32_t pr[8];
+          c[h] += x16_to_pairs(src[0], src[1], pr);
+          uint4* dst = reinterpret_cast<uint4*>(xp + (t * nwords + wd) * 8);
+          dst[0] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+          dst[1] = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+        }
+      }
+    }
+    const float c0 = group_sum<64>(c[0]), c1 = group_sum<64>(c[1]);
+    if (lane == 0) xc[t] = c0 + c1;
   }
   softmax_topk<PER>(p, n_exp, top_k, ids + t * top_k, wts + t * top_k);
 }
@@ -224,11 +252,14 @@ extern "C" size_t ma_router_workspace_bytes(int64_t tokens, int64_t n_experts) {
   return fused + t * e * sizeof(float);
 }
 
-extern "C" int ma_router_topk(const void* x, int x_dtype, int64_t tokens, int64_t ldx,
-                              const void* gate_weight, int w_dtype, int64_t n_experts,
-                              int64_t k_in, const float* bias, int top_k, int32_t* ids,
-                              float* weights, void* workspace, size_t workspace_bytes,
-                              void* stream) {
+// router_topk, and with x_pairs / x_corr set also the grouped experts' x'
+// pairs of x (then always through the logits and the per-token top-k
+// launch, which writes them).
+static int router_topk_impl(const void* x, int x_dtype, int64_t tokens, int64_t ldx,
+                            const void* gate_weight, int w_dtype, int64_t n_experts,
+                            int64_t k_in, const float* bias, int top_k, int32_t* ids,
+                            float* weights, uint32_t* x_pairs, float* x_corr, void* workspace,
+                            size_t workspace_bytes, void* stream) {
   if (tokens < 0 || n_experts < 1 || k_in < 1)
     return fail(MA_EVALUE, "router_topk: bad sizes");
   if (top_k < 1 || top_k > n_experts || top_k > 64)
@@ -240,7 +271,7 @@ extern "C" int ma_router_topk(const void* x, int x_dtype, int64_t tokens, int64_
   if (!workspace || workspace_bytes < ma_router_workspace_bytes(tokens, n_experts))
     return fail(MA_EVALUE, "router_topk: workspace too small");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (fused_ok(x_dtype, w_dtype, tokens, n_experts, k_in, ldx, x, gate_weight)) {
+  if (!x_pairs && fused_ok(x_dtype, w_dtype, tokens, n_experts, k_in, ldx, x, gate_weight)) {
     dim3 grid(static_cast<unsigned>(n_experts), static_cast<unsigned>(tokens));
     const auto* xb = static_cast<const uint16_t*>(x);
     const auto* wb = static_cast<const uint16_t*>(gate_weight);
@@ -268,12 +299,38 @@ extern "C" int ma_router_topk(const void* x, int x_dtype, int64_t tokens, int64_
                        n_experts, k_in, bias, logits, fast);
   }
   const dim3 gt(static_cast<unsigned>(tokens));
+  const auto* xb = static_cast<const uint16_t*>(x);
+  const int64_t nwords = k_in / 16;
   if (n_experts <= 64)
-    hipLaunchKernelGGL(k_router_topk<1>, gt, dim3(64), 0, s, logits, n_experts, top_k, ids, weights);
+    hipLaunchKernelGGL(k_router_topk<1>, gt, dim3(64), 0, s, logits, n_experts, top_k, ids, weights, xb, ldx,
+                       nwords, x_pairs, x_corr);
   else if (n_experts <= 256)
-    hipLaunchKernelGGL(k_router_topk<4>, gt, dim3(64), 0, s, logits, n_experts, top_k, ids, weights);
+    hipLaunchKernelGGL(k_router_topk<4>, gt, dim3(64), 0, s, logits, n_experts, top_k, ids, weights, xb, ldx,
+                       nwords, x_pairs, x_corr);
   else
     hipLaunchKernelGGL(k_router_topk<kRouterMaxPerLane>, gt, dim3(64), 0, s, logits, n_experts,
-                       top_k, ids, weights);
+                       top_k, ids, weights, xb, ldx, nwords, x_pairs, x_corr);
   return check_launch("router_topk");
+}
+
+extern "C" int ma_router_topk(const void* x, int x_dtype, int64_t tokens, int64_t ldx,
+                              const void* gate_weight, int w_dtype, int64_t n_experts,
+                              int64_t k_in, const float* bias, int top_k, int32_t* ids,
+                              float* weights, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  return router_topk_impl(x, x_dtype, tokens, ldx, gate_weight, w_dtype, n_experts, k_in, bias, top_k, ids,
+                          weights, nullptr, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ma_router_topk_pairs(const void* x, int x_dtype, int64_t tokens, int64_t ldx,
+                                    const void* gate_weight, int w_dtype, int64_t n_experts,
+                                    int64_t k_in, const float* bias, int top_k, int32_t* ids,
+                                    float* weights, uint32_t* x_pairs, float* x_corr, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  if (x_dtype != MA_BF16 || k_in % 16 || ldx % 8 || !x_pairs || !x_corr ||
+      ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(x_pairs)) & 15u))
+    return fail(MA_EVALUE, "router_topk_pairs: x must be bfloat16 with 16-byte aligned rows, hidden a "
+                "multiple of 16, and x_pairs / x_corr given (x_pairs 16-byte aligned)");
+  return router_topk_impl(x, x_dtype, tokens, ldx, gate_weight, w_dtype, n_experts, k_in, bias, top_k, ids,
+                          weights, x_pairs, x_corr, workspace, workspace_bytes, stream);
 }

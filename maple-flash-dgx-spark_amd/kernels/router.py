@@ -25,11 +25,16 @@ def router_topk(
     top_k: int,
     *,
     bias: torch.Tensor | None = None,
-) -> tuple[torch.Tensor, torch.Tensor]:
+    pairs: bool = False,
+):
     """Router logits -> softmax -> top-k -> renormalized weights.
 
     Returns ``(topk_idx int32 [..., top_k], topk_weight float32 [..., top_k])``
-    in descending probability order, ties to the lowest expert index.
+    in descending probability order, ties to the lowest expert index.  With
+    ``pairs`` (bf16 ``x``, K a multiple of 16), a third item ``(x_pairs,
+    x_corr)``: ``x`` in the form the grouped experts read, written by the same
+    launch as the top-k (``moe_grouped(..., x_pairs=...)`` then skips its own
+    x' launch; same bits).
     """
     if not x.is_cuda or not gate_weight.is_cuda:
         raise RuntimeError("router_topk requires CUDA tensors.")
@@ -56,9 +61,21 @@ def router_topk(
     nbytes = int(_lib.load().ma_router_workspace_bytes(tokens, n_exp))
     # zero-filled once; the single-launch decode router leaves it zero again
     ws = workspace.get("router", x.device, nbytes, min_bytes=1 << 16)
+    ldx = x_mat.stride(0) if tokens else k_in
+    if pairs:
+        xp = torch.empty(tokens, k_in // 2, device=x.device, dtype=torch.uint32)
+        xc = torch.empty(tokens, device=x.device, dtype=torch.float32)
+        _lib.call(
+            "ma_router_topk_pairs",
+            _lib.ptr(x_mat), _lib.dtype_code(x_mat, "x"), tokens, ldx,
+            _lib.ptr(w), _lib.dtype_code(w, "gate_weight"), n_exp, k_in, _lib.ptr(b), int(top_k),
+            _lib.ptr(idx), _lib.ptr(wt), _lib.ptr(xp), _lib.ptr(xc), _lib.ptr(ws), ws.numel(),
+            _lib.stream_of(x),
+        )
+        return idx.reshape(*leading, top_k), wt.reshape(*leading, top_k), (xp, xc)
     _lib.call(
         "ma_router_topk",
-        _lib.ptr(x_mat), _lib.dtype_code(x_mat, "x"), tokens, x_mat.stride(0) if tokens else k_in,
+        _lib.ptr(x_mat), _lib.dtype_code(x_mat, "x"), tokens, ldx,
         _lib.ptr(w), _lib.dtype_code(w, "gate_weight"), n_exp, k_in, _lib.ptr(b), int(top_k),
         _lib.ptr(idx), _lib.ptr(wt), _lib.ptr(ws), ws.numel(), _lib.stream_of(x),
     )

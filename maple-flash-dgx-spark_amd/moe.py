@@ -298,7 +298,8 @@ def moe_grouped(x: torch.Tensor, layer: MoELayer, ids: torch.Tensor, wts: torch.
     """Dispatch + grouped MFMA SwiGLU/down + combine for ``x [T, H]`` (bf16).
 
     ``dispatch``: the lists for ``ids`` if already built (``moe_route``);
-    ``x_pairs``: ``(xn_pairs, xn_corr)`` of ``x`` from ``moe_route(pairs=True)``.
+    ``x_pairs``: ``(xn_pairs, xn_corr)`` of ``x`` from ``moe_route(pairs=True)``
+    or ``router_topk(..., pairs=True)``.
     Returns ``y [T, H]`` (bf16), and with ``return_h`` also ``h [T, k, I]``;
     with ``combine=False`` a ``PendingCombine`` in place of ``y``.
     """
@@ -372,8 +373,13 @@ def moe_block(x: torch.Tensor, layer: MoELayer, top_k: int, residual: torch.Tens
     if plan == "fused":
         y, ids, wts = moe_fused(xf, layer, top_k, residual, prefetch=prefetch)
         return y.reshape(x.shape), ids, wts
-    ids, wts = router_topk(xf, layer.gate_weight, top_k, bias=layer.router_bias)
     res = None if residual is None else residual.reshape(-1, hidden)
+    if plan == "grouped" and xf.shape[0] * top_k > 16 * layer.n_experts and hidden % 16 == 0:
+        # the grouped kernels' prefill form: the top-k launch also writes x'
+        ids, wts, xp = router_topk(xf, layer.gate_weight, top_k, bias=layer.router_bias, pairs=True)
+        y = moe_grouped(xf, layer, ids, wts, res, x_pairs=xp)
+        return y.reshape(x.shape), ids, wts
+    ids, wts = router_topk(xf, layer.gate_weight, top_k, bias=layer.router_bias)
     if plan == "grouped":
         y = moe_grouped(xf, layer, ids, wts, res)
     else:

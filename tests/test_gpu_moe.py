@@ -95,6 +95,31 @@ def test_moe_grouped_zipf_vs_oracle(dev, layer, tokens):
     assert_bf16_close(np_f(y), ref, atol_frac=2.0 ** -7, what=f"y T={tokens}")
 
 
+@pytest.mark.parametrize("tokens", [256, 2048])
+def test_router_pairs_equal_grouped_own_prep(dev, layer, tokens):
+    """router_topk(pairs=True) writes x' from its top-k launch; moe_block's
+    prefill path hands them to the grouped kernels: the same ids, weights, x'
+    and y bits as router_topk + moe_grouped building x' itself."""
+    L = synthetic.MoELayer(layer.gate_weight, layer.up_gate_packed, layer.up_gate_alpha,
+                           layer.down_packed, layer.down_alpha, zipf_bias(dev))
+    x = synthetic.randn_bf16((tokens, H), 700 + tokens, dev)
+    ids, wts = router_topk(x, L.gate_weight, K, bias=L.router_bias)
+    ids2, wts2, (xp, xc) = router_topk(x, L.gate_weight, K, bias=L.router_bias, pairs=True)
+    assert torch.equal(ids, ids2) and torch.equal(wts, wts2)
+    y_ref = moe_grouped(x, L, ids, wts)
+    y_pairs = moe_grouped(x, L, ids2, wts2, x_pairs=(xp, xc))
+    y_block, ids3, _ = moe_block(x, L, K, plan="grouped")
+    torch.cuda.synchronize()
+    assert torch.equal(y_pairs, y_ref) and torch.equal(y_block, y_ref) and torch.equal(ids3, ids)
+    # x' against the oracle's pair form (word w, pair j: (f_j x[16w+j], f_j x[16w+j+8]))
+    xf = np_f(x)[:4].reshape(4, -1, 2, 8)
+    f = np.where(np.arange(8) % 2 == 1, 4.0, 16.0).astype(np.float32)
+    lo, hi = (xf[:, :, 0, :] * f), (xf[:, :, 1, :] * f)
+    got = xp[:4].cpu().numpy().reshape(4, -1, 8)
+    np.testing.assert_array_equal(got & 0xFFFF, lo.astype(np.float32).view(np.uint32) >> 16)
+    np.testing.assert_array_equal(got >> 16, hi.astype(np.float32).view(np.uint32) >> 16)
+
+
 @pytest.mark.parametrize("hidden,n_exp,inter,k,tokens", [(3072, 8, 1024, 4, 96), (1024, 16, 512, 2, 200)])
 def test_moe_grouped_prefill_form_other_shapes(dev, hidden, n_exp, inter, k, tokens):
     """The prefill-form grouped kernels (more than 16 pairs per expert: x'
